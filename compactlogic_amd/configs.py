@@ -1,0 +1,98 @@
+"""Seeded synthetic workloads of the benchmark configurations.
+
+Networks are generated on the CPU with ``torch.Generator`` in a fixed draw order, then moved
+to the device, so every run (and the CPU baseline) sees identical parameters and inputs.
+
+  cfg1  LogicLayer 784->8000 x4, G=16, GroupSum(10, tau=10), batch 128, inputs Bernoulli(0.5)
+  cfg2  LogicLayer 784->12000 then 12000->12000 x5, G=16, GroupSum(10, 10), batch 1024,
+        inputs Bernoulli(0.3)
+  cfg4  the cfg2 network frozen to argmax gates (uniform opcode per neuron), 2^24 samples
+        bit-packed 64 per word
+
+Dense wiring of these configs: one input pair (a, b) per neuron, drawn uniformly and shared
+by its 16 slots; gate_sequence = arange(16); logits ~ N(0, 1).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from .layers import GroupSum, LogicLayer
+
+NET_SEED, INPUT_SEED, LABEL_SEED = 0, 1, 2
+
+
+@dataclass
+class DenseConfig:
+    name: str
+    in_dim: int
+    widths: list[int]
+    batch: int
+    p_one: float
+    k: int = 10
+    tau: float = 10.0
+    num_gates: int = 16
+    notes: str = ""
+
+    @property
+    def dims(self):
+        return list(zip([self.in_dim] + self.widths[:-1], self.widths))
+
+
+CONFIGS = {
+    "cfg1": DenseConfig("cfg1", 784, [8000] * 4, 128, 0.5),
+    "cfg2": DenseConfig("cfg2", 784, [12000] * 6, 1024, 0.3),
+}
+
+
+def _seeded_layer(in_dim: int, out_dim: int, gen: torch.Generator, num_gates: int) -> LogicLayer:
+    # Build without disturbing the global RNG, then overwrite the draws from `gen`.
+    with torch.random.fork_rng(devices=[]):
+        layer = LogicLayer(in_dim, out_dim, connections="original", num_gates=num_gates)
+    a = torch.randint(0, in_dim, (out_dim,), generator=gen)
+    b = torch.randint(0, in_dim, (out_dim,), generator=gen)
+    logits = torch.randn((out_dim, num_gates), generator=gen)
+    with torch.no_grad():
+        layer.weights.copy_(logits)
+        layer.indices.copy_(torch.stack((a, b)).unsqueeze(-1).expand(2, out_dim, num_gates))
+        layer.gate_sequence.copy_(
+            (torch.arange(num_gates, dtype=torch.int64) & 15).to(torch.uint8).expand(out_dim, num_gates))
+    layer.refresh_backward_index()
+    return layer
+
+
+def dense_network(cfg: DenseConfig, device="cuda", seed: int = NET_SEED) -> torch.nn.Sequential:
+    gen = torch.Generator().manual_seed(seed)
+    layers = [_seeded_layer(i, o, gen, cfg.num_gates) for i, o in cfg.dims]
+    model = torch.nn.Sequential(*layers, GroupSum(cfg.k, cfg.tau))
+    return model.to(device)
+
+
+def dense_inputs(cfg: DenseConfig, device="cuda", batch: int | None = None):
+    batch = cfg.batch if batch is None else batch
+    gx = torch.Generator().manual_seed(INPUT_SEED)
+    gl = torch.Generator().manual_seed(LABEL_SEED)
+    x = (torch.rand((batch, cfg.in_dim), generator=gx) < cfg.p_one).float()
+    labels = torch.randint(0, cfg.k, (batch,), generator=gl)
+    return x.to(device), labels.to(device)
+
+
+def freeze_uniform_gates(model: torch.nn.Sequential, seed: int = NET_SEED + 100) -> None:
+    """cfg4: fix every neuron to a uniformly drawn opcode (argmax slot = opcode, since
+    gate_sequence = arange(16))."""
+    gen = torch.Generator().manual_seed(seed)
+    for layer in model:
+        if isinstance(layer, LogicLayer):
+            slot = torch.randint(0, 16, (layer.out_dim,), generator=gen).to(torch.uint8)
+            layer.freeze()
+            layer.w.copy_(slot.to(layer.w.device))
+    model.eval()
+
+
+def packed_input_words(in_dim: int, words: int, device="cuda", seed: int = INPUT_SEED):
+    """[in_dim, words] int64 rows; word (f, w) = splitmix64(seed * 2^40 + f * words + w), i.e.
+    64 Bernoulli(0.5) samples per word."""
+    from . import difflogic_hip
+    out = torch.empty((in_dim, words), dtype=torch.int64, device=device)
+    return difflogic_hip.fill_splitmix64(out, seed << 40)

@@ -1,0 +1,183 @@
+// Shared host/device helpers for the gfx950 logic-layer kernels.
+//
+// Every extern "C" entry point returns a status code (CL_OK on success) and records a
+// message for the calling thread; nothing here ever calls exit().  Launches are
+// asynchronous on the stream the caller passes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/compactlogic_hip.h"
+
+namespace cl {
+
+// ---------------------------------------------------------------- error state
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define CL_REQUIRE(cond, code, ...)      \
+    do {                                 \
+        if (!(cond)) {                   \
+            ::cl::set_error(__VA_ARGS__); \
+            return (code);               \
+        }                                \
+    } while (0)
+
+#define CL_ARG(cond, ...) CL_REQUIRE(cond, CL_ERR_INVALID_ARGUMENT, __VA_ARGS__)
+
+// Check the launch that was just enqueued.
+int check_launch(const char* what);
+
+// Runs the statement block with scalar_t bound to the element type of `dtype`.
+#define CL_DTYPE_SWITCH(dtype, ...)                                                     \
+    do {                                                                                \
+        if ((dtype) == CL_DTYPE_F32) {                                                  \
+            using scalar_t = float;                                                     \
+            __VA_ARGS__                                                                 \
+        } else if ((dtype) == CL_DTYPE_F64) {                                           \
+            using scalar_t = double;                                                    \
+            __VA_ARGS__                                                                 \
+        } else {                                                                        \
+            ::cl::set_error("unsupported dtype code %d (expected CL_DTYPE_F32 or F64)", \
+                            int(dtype));                                                \
+            return CL_ERR_INVALID_ARGUMENT;                                             \
+        }                                                                               \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned(const void* p, size_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- gate algebra
+//
+// Opcode g in 0..15 stores its truth table in its four bits, MSB first over the input
+// combinations AB = 00, 01, 10, 11 (the table of compactlogic/cuda/utils.cuh:122-139):
+//     f(A, B) = (g >> (3 - (2A + B))) & 1.
+// The relaxed operator is the unique multilinear interpolation of that table,
+//     f(a, b) = c0 + c1*a + c2*b + c3*a*b,
+// with c0 = f00, c1 = f10 - f00, c2 = f01 - f00, c3 = f11 - f10 - f01 + f00.
+// Its partial derivatives are df/da = c1 + c3*b and df/db = c2 + c3*a.
+template <typename T>
+struct Coef4 {
+    T c0, c1, c2, c3;
+};
+
+template <typename T>
+__device__ __host__ __forceinline__ Coef4<T> gate_coef(int g) {
+    const int f00 = (g >> 3) & 1;
+    const int f01 = (g >> 2) & 1;
+    const int f10 = (g >> 1) & 1;
+    const int f11 = g & 1;
+    Coef4<T> c;
+    c.c0 = T(f00);
+    c.c1 = T(f10 - f00);
+    c.c2 = T(f01 - f00);
+    c.c3 = T(f11 - f10 - f01 + f00);
+    return c;
+}
+
+// Relaxed operator value, evaluated as c3*(a*b) + (c2*b + (c1*a + c0)).
+template <typename T>
+__device__ __forceinline__ T relaxed_op(const Coef4<T>& c, T a, T b) {
+    return fma(c.c3, a * b, fma(c.c2, b, fma(c.c1, a, c.c0)));
+}
+
+// Bitwise operator on packed words: each output bit selects the truth-table entry for its
+// (a, b) bit pair.  Branch-free: four minterm masks.
+template <typename W>
+__device__ __forceinline__ W bitwise_op(int g, W a, W b) {
+    const W m00 = W(0) - W((g >> 3) & 1);
+    const W m01 = W(0) - W((g >> 2) & 1);
+    const W m10 = W(0) - W((g >> 1) & 1);
+    const W m11 = W(0) - W(g & 1);
+    return (~a & ~b & m00) | (~a & b & m01) | (a & ~b & m10) | (a & b & m11);
+}
+
+// ---------------------------------------------------------------- wave helpers (wave64)
+constexpr int kWave = 64;
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Wave index inside the workgroup, as a scalar (uniform) value.
+__device__ __forceinline__ int wave_id() {
+    return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// ---------------------------------------------------------------- vector access
+template <typename T, int VEC>
+struct Vec;
+
+template <typename T>
+struct Vec<T, 1> {
+    T v[1];
+};
+template <typename T>
+struct Vec<T, 2> {
+    T v[2];
+};
+template <typename T>
+struct Vec<T, 4> {
+    T v[4];
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ Vec<T, VEC> vload(const T* p) {
+    Vec<T, VEC> r;
+    if constexpr (VEC == 4 && sizeof(T) == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(p);
+        r.v[0] = __builtin_bit_cast(T, t.x);
+        r.v[1] = __builtin_bit_cast(T, t.y);
+        r.v[2] = __builtin_bit_cast(T, t.z);
+        r.v[3] = __builtin_bit_cast(T, t.w);
+    } else if constexpr (VEC == 2 && sizeof(T) == 8) {
+        const double2 t = *reinterpret_cast<const double2*>(p);
+        r.v[0] = __builtin_bit_cast(T, t.x);
+        r.v[1] = __builtin_bit_cast(T, t.y);
+    } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) r.v[i] = p[i];
+    }
+    return r;
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void vstore(T* p, const Vec<T, VEC>& r) {
+    if constexpr (VEC == 4 && sizeof(T) == 4) {
+        float4 t;
+        t.x = __builtin_bit_cast(float, r.v[0]);
+        t.y = __builtin_bit_cast(float, r.v[1]);
+        t.z = __builtin_bit_cast(float, r.v[2]);
+        t.w = __builtin_bit_cast(float, r.v[3]);
+        *reinterpret_cast<float4*>(p) = t;
+    } else if constexpr (VEC == 2 && sizeof(T) == 8) {
+        double2 t;
+        t.x = __builtin_bit_cast(double, r.v[0]);
+        t.y = __builtin_bit_cast(double, r.v[1]);
+        *reinterpret_cast<double2*>(p) = t;
+    } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) p[i] = r.v[i];
+    }
+}
+
+// Widest vector of T that keeps 16-byte loads, when the row length and base allow it.
+template <typename T>
+constexpr int wide_vec() {
+    return 16 / int(sizeof(T));
+}
+
+}  // namespace cl

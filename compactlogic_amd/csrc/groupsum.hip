@@ -1,0 +1,216 @@
+// GroupSum forward / backward (compactlogic/compactlogic.py:450-468) for gfx950.
+//
+// The reference zero-pads the features to a multiple of k and sums k groups of
+// gs = ceil(F / k) consecutive features, then divides by tau.  Padding columns contribute
+// zero, so group c is simply features [c*gs, min((c+1)*gs, F)).
+//
+// A LogicLayer hands GroupSum a transposed view of its contiguous [F, batch] output, so the
+// kernels take element strides and have a fast variant for each unit-stride direction:
+//   batch-contiguous  (stride_batch == 1): lanes run along the batch, waves split the group
+//   feature-contiguous (stride_feature == 1): one wave reduces one contiguous group
+// and a plain strided variant for anything else.
+#include "common.h"
+
+#include <algorithm>
+
+namespace cl {
+namespace {
+
+constexpr int kSplitWaves = 8;  // waves splitting one group in the batch-contiguous kernel
+
+// ---- forward, batch-contiguous: block = (batch tile of 64*VEC samples, class c)
+template <typename T, int VEC>
+__global__ __launch_bounds__(kSplitWaves * 64) void k_gsum_fwd_bc(const T* __restrict__ x,
+                                                                  int64_t B, int64_t F,
+                                                                  int64_t sf, int64_t gsz,
+                                                                  int64_t k, T tau,
+                                                                  T* __restrict__ out) {
+    __shared__ T part[kSplitWaves][64 * VEC];
+    const int wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t c = blockIdx.y;
+    const int64_t n0 = int64_t(blockIdx.x) * 64 * VEC + int64_t(lane) * VEC;
+    const int64_t j0 = c * gsz;
+    const int64_t j1 = std::min<int64_t>(j0 + gsz, F);
+    Vec<T, VEC> s;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) s.v[i] = T(0);
+    if (n0 < B) {
+        for (int64_t j = j0 + wv; j < j1; j += kSplitWaves) {
+            const Vec<T, VEC> v = vload<T, VEC>(x + j * sf + n0);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) s.v[i] += v.v[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) part[wv][lane * VEC + i] = s.v[i];
+    __syncthreads();
+    // Fixed-order combine of the wave partials (deterministic).
+    for (int e = threadIdx.x; e < 64 * VEC; e += kSplitWaves * 64) {
+        const int64_t n = int64_t(blockIdx.x) * 64 * VEC + e;
+        if (n < B) {
+            T t = part[0][e];
+#pragma unroll
+            for (int w = 1; w < kSplitWaves; ++w) t += part[w][e];
+            out[n * k + c] = t / tau;
+        }
+    }
+}
+
+// ---- forward, feature-contiguous: one wave per (sample n, class c)
+template <typename T>
+__global__ __launch_bounds__(256) void k_gsum_fwd_fc(const T* __restrict__ x, int64_t B,
+                                                     int64_t F, int64_t sb, int64_t gsz,
+                                                     int64_t k, T tau, T* __restrict__ out) {
+    const int64_t item = int64_t(blockIdx.x) * 4 + wave_id();
+    if (item >= B * k) return;
+    const int64_t n = item / k, c = item % k;
+    const int64_t j0 = c * gsz;
+    const int64_t j1 = std::min<int64_t>(j0 + gsz, F);
+    const T* row = x + n * sb;
+    T s = 0;
+    for (int64_t j = j0 + lane_id(); j < j1; j += 64) s += row[j];
+    s = wave_sum(s);
+    if (lane_id() == 0) out[n * k + c] = s / tau;
+}
+
+// ---- forward, arbitrary strides: one thread per (n, c)
+template <typename T>
+__global__ __launch_bounds__(256) void k_gsum_fwd_generic(const T* __restrict__ x, int64_t B,
+                                                          int64_t F, int64_t sb, int64_t sf,
+                                                          int64_t gsz, int64_t k, T tau,
+                                                          T* __restrict__ out) {
+    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (item >= B * k) return;
+    const int64_t n = item / k, c = item % k;
+    const int64_t j0 = c * gsz;
+    const int64_t j1 = std::min<int64_t>(j0 + gsz, F);
+    T s = 0;
+    for (int64_t j = j0; j < j1; ++j) s += x[n * sb + j * sf];
+    out[n * k + c] = s / tau;
+}
+
+// ---- backward: grad_x[n, j] = g[n, j / gsz] / tau.  Elements are visited in memory order
+// of grad_x: `inner` is the unit-stride dimension (batch or feature).
+template <typename T, int VEC, bool BATCH_INNER>
+__global__ __launch_bounds__(256) void k_gsum_bwd(const T* __restrict__ g, int64_t B, int64_t F,
+                                                  int64_t so, int64_t gsz, int64_t k, T tau,
+                                                  T* __restrict__ gx) {
+    // Rows: features (BATCH_INNER) or samples; inner: samples or features.
+    const int64_t rows = BATCH_INNER ? F : B;
+    const int64_t inner = BATCH_INNER ? B : F;
+    const int64_t row = int64_t(blockIdx.x) * 4 + wave_id();
+    if (row >= rows) return;
+    const int64_t i0 = (int64_t(blockIdx.y) * 64 + lane_id()) * VEC;
+    if (i0 >= inner) return;
+    Vec<T, VEC> v;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+        const int64_t n = BATCH_INNER ? i0 + i : row;
+        const int64_t j = BATCH_INNER ? row : i0 + i;
+        v.v[i] = g[n * k + j / gsz] / tau;
+    }
+    vstore<T, VEC>(gx + row * so + i0, v);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_gsum_bwd_generic(const T* __restrict__ g, int64_t B,
+                                                          int64_t F, int64_t sb, int64_t sf,
+                                                          int64_t gsz, int64_t k, T tau,
+                                                          T* __restrict__ gx) {
+    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (item >= B * F) return;
+    const int64_t n = item / F, j = item % F;
+    gx[n * sb + j * sf] = g[n * k + j / gsz] / tau;
+}
+
+}  // namespace
+}  // namespace cl
+
+using namespace cl;
+
+extern "C" int cl_group_sum_forward(int dtype, const void* x, int64_t batch, int64_t features,
+                                    int64_t stride_batch, int64_t stride_feature, int64_t k,
+                                    double tau, void* out, void* stream) {
+    clear_error();
+    CL_ARG(batch >= 0 && features >= 0, "negative shape");
+    CL_ARG(k >= 1, "k must be >= 1, got %lld", (long long)k);
+    CL_ARG(stride_batch >= 0 && stride_feature >= 0, "negative strides are not supported");
+    if (batch == 0) return CL_OK;
+    CL_ARG(x && out, "null pointer argument");
+    const int64_t gsz = features == 0 ? 1 : ceil_div(features, k);
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        const T* xs = static_cast<const T*>(x);
+        T* os = static_cast<T*>(out);
+        const T t = T(tau);
+        constexpr int W = wide_vec<T>();
+        if (stride_batch == 1 && features > 0 && batch >= 64) {
+            const bool wide = batch % W == 0 && stride_feature % W == 0 && aligned(x, 16);
+            if (wide) {
+                const dim3 grid(unsigned(ceil_div(batch, 64 * W)), unsigned(k), 1);
+                k_gsum_fwd_bc<T, W><<<grid, kSplitWaves * 64, 0, s>>>(xs, batch, features,
+                                                                      stride_feature, gsz, k, t, os);
+            } else {
+                const dim3 grid(unsigned(ceil_div(batch, 64)), unsigned(k), 1);
+                k_gsum_fwd_bc<T, 1><<<grid, kSplitWaves * 64, 0, s>>>(xs, batch, features,
+                                                                      stride_feature, gsz, k, t, os);
+            }
+        } else if (stride_feature == 1) {
+            const dim3 grid(unsigned(ceil_div(batch * k, 4)), 1, 1);
+            k_gsum_fwd_fc<T><<<grid, 256, 0, s>>>(xs, batch, features, stride_batch, gsz, k, t, os);
+        } else {
+            const dim3 grid(unsigned(ceil_div(batch * k, 256)), 1, 1);
+            k_gsum_fwd_generic<T><<<grid, 256, 0, s>>>(xs, batch, features, stride_batch,
+                                                       stride_feature, gsz, k, t, os);
+        }
+    });
+    return check_launch("cl_group_sum_forward");
+}
+
+extern "C" int cl_group_sum_backward(int dtype, const void* grad_out, int64_t batch,
+                                     int64_t features, int64_t k, double tau, void* grad_x,
+                                     int64_t stride_batch, int64_t stride_feature, void* stream) {
+    clear_error();
+    CL_ARG(batch >= 0 && features >= 0, "negative shape");
+    CL_ARG(k >= 1, "k must be >= 1, got %lld", (long long)k);
+    CL_ARG(stride_batch >= 0 && stride_feature >= 0, "negative strides are not supported");
+    if (batch == 0 || features == 0) return CL_OK;
+    CL_ARG(grad_out && grad_x, "null pointer argument");
+    const int64_t gsz = ceil_div(features, k);
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        const T* gs = static_cast<const T*>(grad_out);
+        T* gxs = static_cast<T*>(grad_x);
+        const T t = T(tau);
+        constexpr int W = wide_vec<T>();
+        if (stride_batch == 1) {
+            const bool wide = batch % W == 0 && stride_feature % W == 0 && aligned(grad_x, 16);
+            const int vec = wide ? W : 1;
+            const dim3 grid(unsigned(ceil_div(features, 4)), unsigned(ceil_div(batch, 64 * vec)), 1);
+            if (wide)
+                k_gsum_bwd<T, W, true><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
+                                                           gsz, k, t, gxs);
+            else
+                k_gsum_bwd<T, 1, true><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
+                                                           gsz, k, t, gxs);
+        } else if (stride_feature == 1) {
+            const bool wide = features % W == 0 && stride_batch % W == 0 && aligned(grad_x, 16);
+            const int vec = wide ? W : 1;
+            const dim3 grid(unsigned(ceil_div(batch, 4)), unsigned(ceil_div(features, 64 * vec)), 1);
+            if (wide)
+                k_gsum_bwd<T, W, false><<<grid, 256, 0, s>>>(gs, batch, features, stride_batch,
+                                                            gsz, k, t, gxs);
+            else
+                k_gsum_bwd<T, 1, false><<<grid, 256, 0, s>>>(gs, batch, features, stride_batch,
+                                                            gsz, k, t, gxs);
+        } else {
+            const dim3 grid(unsigned(ceil_div(batch * features, 256)), 1, 1);
+            k_gsum_bwd_generic<T><<<grid, 256, 0, s>>>(gs, batch, features, stride_batch,
+                                                       stride_feature, gsz, k, t, gxs);
+        }
+    });
+    return check_launch("cl_group_sum_backward");
+}

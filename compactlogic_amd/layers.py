@@ -1,0 +1,477 @@
+"""LogicLayer / GroupSum / PackBitsTensor and their autograd Functions on gfx950.
+
+The constructors, buffers, forward dispatch and autograd signatures follow the reference
+modules in compactlogic/compactlogic.py (LogicLayer :10-444, GroupSum :450-468,
+LogicLayerCudaFunction :474-508) and the packed-bit API of the difflogic lineage
+(third_party/convlogic_source_code/src/difflogic/packbitstensor.py:11-43,
+difflogic.py:92-106,149-164,203-205).  Every numeric path runs on the HIP library; a tensor
+that is not on a HIP device is rejected, never computed on the CPU.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _capi
+from . import difflogic_hip as _dl
+from .plan import RunPlan, build_run_plan
+
+
+########################################################################################################################
+# Packed bits
+
+
+class PackBitsTensor:
+    """Bit-packed batch: `t` is [features, ceil(batch / bit_count)] integer words, bit i of word
+    w holds sample bit_count * w + i (packbitstensor.py:11-21)."""
+
+    def __init__(self, t: torch.Tensor, bit_count: int = 32):
+        assert len(t.shape) == 2, t.shape
+        self.bit_count = bit_count
+        if t.device.type != "cuda":
+            raise NotImplementedError(
+                f"PackBitsTensor only supports device tensors, but got {t.device}.")
+        t = t.T.contiguous()
+        self.t, self.pad_len = _dl.tensor_packbits_cuda(t, self.bit_count)
+
+    @classmethod
+    def from_packed(cls, words: torch.Tensor, pad_len: int = 0, bit_count: int | None = None):
+        """Wrap already packed rows [features, words] (no copy)."""
+        obj = cls.__new__(cls)
+        obj.t = words
+        obj.pad_len = int(pad_len)
+        obj.bit_count = bit_count or words.element_size() * 8
+        return obj
+
+    @property
+    def is_cuda(self) -> bool:
+        return self.t.is_cuda
+
+    @property
+    def device(self):
+        return self.t.device
+
+    @property
+    def num_samples(self) -> int:
+        return self.t.shape[1] * self.t.element_size() * 8 - self.pad_len
+
+    def group_sum(self, k):
+        return _dl.groupbitsum(self.t, self.pad_len, k)
+
+    def flatten(self, start_dim=0, end_dim=-1, **kwargs):
+        """Returns the PackBitsTensor itself (its feature axis is already flat)."""
+        return self
+
+    def _member_repr(self, member):
+        bits = self.bit_count
+        if len(member) <= 4:
+            return " ".join(np.binary_repr(int(v), width=bits)[::-1] for v in member)
+        head = " ".join(np.binary_repr(int(v), width=bits)[::-1] for v in member[:3])
+        return f"{head} ... {np.binary_repr(int(member[-1]), width=bits)[::-1]}"
+
+    def __repr__(self):
+        return "\n".join(self._member_repr(row.tolist()) for row in self.t.cpu())
+
+
+########################################################################################################################
+# Autograd functions
+
+
+class LogicLayerCudaFunction(torch.autograd.Function):
+    """Reference autograd bridge (compactlogic/compactlogic.py:474-508) over the drop-in
+    kernels: same inputs, same saved tensors, same (grad_x, grad_w) outputs."""
+
+    @staticmethod
+    def forward(ctx, x, a, b, w, gate_sequence, given_x_indices_of_y_start, given_x_indices_of_y,
+                given_x_indices_of_gate):
+        ctx.save_for_backward(x, a, b, w, gate_sequence, given_x_indices_of_y_start,
+                              given_x_indices_of_y, given_x_indices_of_gate)
+        return _dl.forward(x, a, b, w, gate_sequence)
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        (x, a, b, w, gate_sequence, given_x_indices_of_y_start, given_x_indices_of_y,
+         given_x_indices_of_gate) = ctx.saved_tensors
+        grad_y = grad_y.contiguous()
+        grad_w = grad_x = None
+        if ctx.needs_input_grad[0]:
+            grad_x = _dl.backward_x(x, a, b, w, gate_sequence, grad_y, given_x_indices_of_y_start,
+                                    given_x_indices_of_y, given_x_indices_of_gate)
+        if ctx.needs_input_grad[3]:
+            grad_w = _dl.backward_w(x, a, b, gate_sequence, grad_y)
+        return grad_x, None, None, grad_w, None, None, None, None
+
+
+class LogicLayerRunsFunction(torch.autograd.Function):
+    """Dense layer through the connection-run plan: same math as LogicLayerCudaFunction, with
+    shared-pair slots collapsed and both gradients produced by one inverse-index pass."""
+
+    @staticmethod
+    def forward(ctx, x, w, gate_sequence, plan: RunPlan):
+        _dl._check(x, "x")
+        if w.dtype != x.dtype:
+            raise RuntimeError("w must have the dtype of x")
+        if x.shape[0] != plan.in_dim:
+            raise RuntimeError(f"x has {x.shape[0]} rows, the layer expects {plan.in_dim}")
+        batch = x.shape[1]
+        y = torch.empty((plan.out_dim, batch), dtype=x.dtype, device=x.device)
+        w = w.contiguous()
+        with torch.cuda.device(x.device):
+            _capi.call("cl_dense_forward_runs", _dl.dtype_code(x), x.data_ptr(), w.data_ptr(),
+                       gate_sequence.data_ptr(), plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
+                       plan.run_gl.data_ptr(), y.data_ptr(), plan.in_dim, plan.out_dim,
+                       plan.num_runs, batch, plan.num_gates, _dl.stream_of(x))
+        ctx.save_for_backward(x, w, gate_sequence)
+        ctx.plan = plan
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        x, w, gate_sequence = ctx.saved_tensors
+        plan: RunPlan = ctx.plan
+        grad_y = grad_y.contiguous()
+        grad_x = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        grad_w = torch.empty_like(w) if ctx.needs_input_grad[1] else None
+        if grad_x is not None or grad_w is not None:
+            with torch.cuda.device(x.device):
+                _capi.call("cl_dense_backward_runs", _dl.dtype_code(x), x.data_ptr(),
+                           w.data_ptr(), gate_sequence.data_ptr(), grad_y.data_ptr(),
+                           plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
+                           plan.run_gl.data_ptr(), plan.run_y.data_ptr(),
+                           plan.inv_ptr.data_ptr(), plan.inv_entry.data_ptr(),
+                           _dl.ptr(grad_x), _dl.ptr(grad_w), plan.in_dim, plan.out_dim,
+                           plan.num_runs, x.shape[1], plan.num_gates, _dl.stream_of(x))
+        return grad_x, grad_w, None, None
+
+
+class GroupSumFunction(torch.autograd.Function):
+    """GroupSum (compactlogic/compactlogic.py:460-465) on the HIP kernels.  Reads the input
+    through its strides, so the transposed view a LogicLayer returns costs no copy, and
+    returns the input gradient in the same memory layout as the input."""
+
+    @staticmethod
+    def forward(ctx, x, k, tau):
+        if x.device.type != "cuda":
+            raise RuntimeError("GroupSum input must be a HIP device tensor")
+        if x.dim() != 2:
+            raise RuntimeError("GroupSum expects a 2-D [batch, features] input")
+        batch, feats = x.shape
+        sb, sf = x.stride()
+        if sb < 0 or sf < 0 or (batch > 1 and feats > 1 and (sb == 0 or sf == 0)):
+            x = x.contiguous()
+            sb, sf = x.stride()
+        out = torch.empty((batch, k), dtype=x.dtype, device=x.device)
+        with torch.cuda.device(x.device):
+            _capi.call("cl_group_sum_forward", _dl.dtype_code(x), x.data_ptr(), batch, feats,
+                       sb, sf, k, float(tau), out.data_ptr(), _dl.stream_of(x))
+        ctx.k, ctx.tau = k, tau
+        ctx.shape = (batch, feats)
+        ctx.batch_major = sb == 1 and sf != 1
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        grad_out = grad_out.contiguous()
+        batch, feats = ctx.shape
+        if ctx.batch_major:
+            grad_x = torch.empty((feats, batch), dtype=grad_out.dtype, device=grad_out.device).t()
+        else:
+            grad_x = torch.empty((batch, feats), dtype=grad_out.dtype, device=grad_out.device)
+        sb, sf = grad_x.stride()
+        with torch.cuda.device(grad_out.device):
+            _capi.call("cl_group_sum_backward", _dl.dtype_code(grad_out), grad_out.data_ptr(),
+                       batch, feats, ctx.k, float(ctx.tau), grad_x.data_ptr(), sb, sf,
+                       _dl.stream_of(grad_out))
+        return grad_x, None, None
+
+
+########################################################################################################################
+# Modules
+
+
+class LogicLayer(torch.nn.Module):
+    """Differentiable logic-gate layer (compactlogic/compactlogic.py:10-130).
+
+    Parameters
+    ----------
+    in_dim, out_dim : int
+    connections : {'random', 'original'}
+        'random' draws an independent input pair for every gate slot; 'original' draws one
+        pair per neuron shared by all its slots.
+    num_gates : int, default 16
+        Candidate gate slots per neuron (opcode of slot g defaults to g & 15).
+    residual_init : bool
+        Bias every neuron towards the pass-through gate (slot 3) instead of N(0, 1) logits.
+
+    Buffers: ``gate_sequence`` uint8 [out, G], ``indices`` int64 [2, out, G] and the inverse
+    index ``given_x_indices_of_y_start`` / ``given_x_indices_of_y`` /
+    ``given_x_indices_of_gate`` (state-dict compatible with the reference); ``w`` (uint8 argmax
+    slots) after ``freeze()``.  The connection-run plan used by the kernels is derived state
+    and is not saved.
+    """
+
+    def __init__(self, in_dim: int, out_dim: int, connections: str = 'random', num_gates=16,
+                 residual_init: bool = False):
+        super().__init__()
+        self.in_dim = in_dim
+        self.out_dim = out_dim
+        self.connections = connections
+        self.num_gates = num_gates
+        self.log_k = torch.log(torch.tensor(self.num_gates)).item()
+        self.init_weights(residual_init)
+        self.init_gate_sequence()
+        self.get_connections(device=self.weights.device)
+        self._plan = None
+        self._plan_key = None
+        self.refresh_backward_index()
+        self.num_neurons = out_dim
+        self.num_weights = out_dim
+        self.is_frozen = False
+
+    # -- forward ------------------------------------------------------------------------------------------------------
+
+    def forward(self, x):
+        if getattr(self, "is_frozen", False) or not self.training or isinstance(x, PackBitsTensor):
+            with torch.no_grad():
+                return self.forward_cuda_eval(x)
+        return self.forward_cuda(x)
+
+    def forward_cuda(self, x):
+        """Training forward: x [batch, in_dim] -> [batch, out_dim] (a transposed view of the
+        kernel's [out_dim, batch] output, as in the reference, :83-118)."""
+        assert x.ndim == 2, x.ndim
+        x = x.transpose(0, 1).contiguous()
+        assert x.shape[0] == self.in_dim, (x.shape, self.in_dim)
+        w = torch.nn.functional.softmax(self.weights, dim=-1).to(x.dtype)
+        plan = self.run_plan()
+        return LogicLayerRunsFunction.apply(x, w, self.gate_sequence, plan).transpose(0, 1)
+
+    @torch.no_grad()
+    def forward_cuda_eval(self, x):
+        """Discrete forward with the argmax slot per neuron (:120-130).  A PackBitsTensor is
+        evaluated bitwise and updated in place, as in difflogic.py:149-164."""
+        assert self.is_frozen or not self.training
+        w = getattr(self, "w", None)
+        if w is None:
+            w = self.weights.argmax(-1).to(dtype=torch.uint8, device=self.weights.device)
+        a, b = self.indices[0], self.indices[1]
+        if isinstance(x, PackBitsTensor):
+            assert x.t.shape[0] == self.in_dim, (x.t.shape, self.in_dim)
+            x.t = _dl.eval_packed(x.t, a, b, w, self.gate_sequence)
+            return x
+        x = x.transpose(0, 1).contiguous()
+        return _dl.eval(x, a, b, w, self.gate_sequence).transpose(0, 1)
+
+    def extra_repr(self):
+        return '{}, {}, {}'.format(self.in_dim, self.out_dim, 'train' if self.training else 'eval')
+
+    # -- parameters and wiring (same draws, in the same order, as the reference) ----------------------------------------
+
+    def init_weights(self, residual_init: bool = False):
+        """N(0, 1) logits, or the residual init: log(9 (G - 1)) on slot 3, zeros elsewhere
+        (:135-147)."""
+        rows = getattr(self, 'c_out', self.out_dim)
+        if residual_init:
+            logits = torch.zeros((rows, self.num_gates))
+            logits[:, 3] = float(np.log(9 * (self.num_gates - 1)))
+        else:
+            logits = torch.randn([rows, self.num_gates])
+        self.weights = torch.nn.parameter.Parameter(logits)
+
+    def init_gate_sequence(self):
+        """gate_sequence[row, g] = g & 15 (:149-158)."""
+        rows = self.c_out if hasattr(self, "c_out") else self.out_dim
+        seq = torch.arange(self.num_gates, device=self.weights.device, dtype=torch.int64) & 15
+        self.register_buffer('gate_sequence', seq.unsqueeze(0).repeat(rows, 1).to(torch.uint8))
+
+    def get_connections(self, device='cuda'):
+        """Input pairs per neuron and slot (:160-182).  'random' gives every slot column its
+        own pair of random permutations over 2*out_dim targets folded onto the inputs;
+        'original' draws one pair per neuron and repeats it over the slots."""
+        assert self.out_dim * 2 >= self.in_dim, (
+            'The number of neurons ({}) must not be smaller than half of the number of inputs '
+            '({}) because otherwise not all inputs could be used or considered.'.format(
+                self.out_dim, self.in_dim))
+        g = self.num_gates
+        if self.connections == 'random':
+            targets = torch.argsort(torch.rand(2 * self.out_dim, g, device=device), dim=0) % self.in_dim
+            relabel = torch.argsort(torch.rand(self.in_dim, g, device=device), dim=0)
+            pairs = torch.gather(relabel, 0, targets).view(2, self.out_dim, g)
+        elif self.connections == 'original':
+            flat = torch.randperm(2 * self.out_dim) % self.in_dim
+            flat = torch.randperm(self.in_dim)[flat]
+            pairs = flat.unsqueeze(-1).expand(*flat.shape, g).reshape(2, self.out_dim, g)
+        else:
+            raise NotImplementedError(f'self.connections: "{self.connections}" not implemented.')
+        self.register_buffer('indices', pairs.to(torch.int64).to(device).contiguous())
+
+    def _set_or_register_buffer(self, name: str, tensor: torch.Tensor) -> None:
+        if name in self._buffers:
+            self._buffers[name] = tensor
+        else:
+            self.register_buffer(name, tensor)
+
+    def refresh_backward_index(self, changed_rows: torch.Tensor | None = None) -> None:
+        """Rebuild the inverse index (:184-274): for every input, the (neuron, code) uses of
+        it, with code g for operand a of slot g and -(g+1) for operand b, grouped by input in
+        CSR form.  Rows are rebuilt in full (a stable sort, so the order inside a row is
+        canonical); an empty `changed_rows` leaves the index as it is, as in the reference."""
+        if not hasattr(self, "indices") or self.indices.ndim != 3:
+            return
+        if changed_rows is not None and "given_x_indices_of_y_start" in self._buffers:
+            if torch.as_tensor(changed_rows).numel() == 0:
+                return
+        dev = self.indices.device
+        _, out, g = self.indices.shape
+        rows = torch.arange(out, device=dev, dtype=torch.int64).unsqueeze(1).expand(out, g).reshape(-1)
+        slots = torch.arange(g, device=dev, dtype=torch.int64).unsqueeze(0).expand(out, g).reshape(-1)
+        inputs = torch.cat((self.indices[0].reshape(-1), self.indices[1].reshape(-1)))
+        ys = torch.cat((rows, rows))
+        codes = torch.cat((slots, -(slots + 1))).to(torch.int8)
+        order = torch.sort(inputs, stable=True).indices
+        counts = torch.bincount(inputs, minlength=self.in_dim)
+        starts = torch.zeros(self.in_dim + 1, dtype=torch.int64, device=dev)
+        starts[1:] = torch.cumsum(counts, 0)
+        self._set_or_register_buffer("given_x_indices_of_y_start", starts)
+        self._set_or_register_buffer("given_x_indices_of_y", ys[order])
+        self._set_or_register_buffer("given_x_indices_of_gate", codes[order])
+        self._plan = None
+
+    def run_plan(self) -> RunPlan:
+        """The connection-run plan for the current `indices`, rebuilt after any change."""
+        key = (self.indices.data_ptr(), self.indices._version, self.indices.device)
+        if self._plan is None or self._plan_key != key:
+            self._plan = build_run_plan(self.indices, self.in_dim)
+            self._plan_key = key
+        return self._plan
+
+    # -- rewiring, entropy, freezing ----------------------------------------------------------------------------------
+
+    @torch.no_grad()
+    def resample_connections(self, converged_rows, threshold_high: float = 0.95,
+                             threshold_low: float = 0.0, update_gate=True,
+                             keep_strong_weights=True):
+        """Re-draw logits, opcodes and wiring of the selected rows (:282-348): rows whose top
+        probability is below `threshold_low` are re-drawn in full; rows above
+        `threshold_high` keep their winning slot and re-draw the others."""
+        device = self.weights.device
+        num_rows = self.weights.shape[0]
+        assert len(converged_rows.shape) == 1
+        selected = torch.zeros(num_rows, device=device, dtype=torch.bool)
+        selected[converged_rows.detach().clone().to(device)] = True
+        probs = torch.nn.functional.softmax(self.weights, dim=-1)
+        row_max, row_argmax = probs.max(dim=1)
+        strong_mask = (row_max > threshold_high) & selected
+        weak_mask = (row_max < threshold_low) & selected
+        n_strong = int(strong_mask.sum().item())
+        n_weak = int(weak_mask.sum().item())
+        gate_pool = torch.arange(16, device=device, dtype=torch.uint8)
+        if n_weak:
+            self.weights[weak_mask] = torch.randn((n_weak, self.num_gates), device=device)
+            if update_gate:
+                pick = torch.randint(0, len(gate_pool), (n_weak, self.num_gates), device=device)
+                self.gate_sequence[weak_mask] = gate_pool[pick]
+            self.update_indices_weak(n_weak, weak_mask)
+        if n_strong:
+            refill = torch.zeros_like(self.weights, dtype=torch.bool, device=device)
+            refill[strong_mask] = True
+            strong_rows = strong_mask.nonzero(as_tuple=False).squeeze(-1)
+            keep = row_argmax[strong_rows]
+            refill[strong_rows, keep] = False
+            kept_p = row_max[strong_mask].clamp(min=1e-6, max=1 - 1e-6)
+            self.weights[strong_mask] = 0.0
+            if keep_strong_weights:
+                self.weights[strong_rows, keep] = torch.log(kept_p * (self.num_gates - 1) / (1 - kept_p))
+            else:
+                self.weights[strong_rows, keep] = float(np.log(9 * (self.num_gates - 1)))
+            n_fill = int(refill.sum().item())
+            if update_gate and n_fill > 0:
+                pick = torch.randint(0, len(gate_pool), (n_fill,), device=device)
+                self.gate_sequence[refill] = gate_pool[pick]
+            self.update_indices_strong(refill, n_fill)
+        if n_weak or n_strong:
+            changed = torch.nonzero(weak_mask | strong_mask, as_tuple=False).flatten()
+            self.refresh_backward_index(changed)
+        return weak_mask, strong_mask
+
+    @torch.no_grad()
+    def update_indices_weak(self, n_weak, weak_mask):
+        """New uniform input pairs for every slot of the weak rows (:350-359)."""
+        device = self.weights.device
+        self.indices[0][weak_mask] = torch.randint(0, self.in_dim, (n_weak, self.num_gates),
+                                                   device=device, dtype=torch.int64)
+        self.indices[1][weak_mask] = torch.randint(0, self.in_dim, (n_weak, self.num_gates),
+                                                   device=device, dtype=torch.int64)
+
+    @torch.no_grad()
+    def update_indices_strong(self, mask2d, num_to_fill):
+        """New uniform input pairs for the refilled slots of the strong rows (:361-368)."""
+        device = self.weights.device
+        self.indices[0][mask2d] = torch.randint(0, self.in_dim, (num_to_fill,), device=device,
+                                                dtype=torch.int64)
+        self.indices[1][mask2d] = torch.randint(0, self.in_dim, (num_to_fill,), device=device,
+                                                dtype=torch.int64)
+
+    @torch.no_grad()
+    def weights_entropy(self, dim: int = -1) -> torch.Tensor:
+        """Entropy of the gate distribution per row divided by log(G) (:370-385)."""
+        log_p = torch.log_softmax(self.weights, dim=dim)
+        return -(log_p.exp() * log_p).sum(dim=dim) / self.log_k
+
+    def freeze(self):
+        """Fix every neuron to its argmax slot (:387-394)."""
+        self.weights.requires_grad = False
+        self.register_buffer("w", self.weights.argmax(-1).to(dtype=torch.uint8,
+                                                              device=self.weights.device))
+        self.is_frozen = True
+
+    def unfreeze(self):
+        self.weights.requires_grad = True
+        self.is_frozen = False
+
+    @torch.no_grad()
+    def connected_neurons(self, y_flag: torch.Tensor, const_gates=None, trivial_gates_a=None,
+                          trivial_gates_b=None, device=None):
+        """Inputs feeding the active, non-trivial outputs (:400-444).  Returns (x_flag,
+        y_flag); y_flag is updated in place as in the reference."""
+        assert y_flag.shape == (self.out_dim,), \
+            f'y_flag shape mismatch: {y_flag.shape}, should be {self.out_dim}'
+        device = device if device is not None else y_flag.device
+        const_gates = torch.tensor([0, 15], device=device) if const_gates is None else const_gates
+        trivial_gates_a = torch.tensor([3, 12], device=device) if trivial_gates_a is None else trivial_gates_a
+        trivial_gates_b = torch.tensor([5, 10], device=device) if trivial_gates_b is None else trivial_gates_b
+        x_flag = torch.zeros(self.in_dim, dtype=torch.bool, device=device)
+        w = getattr(self, 'w', None)
+        w = (self.weights.argmax(-1) if w is None else w).to(torch.long)
+        pair = torch.gather(self.indices, 2, w.view(1, -1, 1).expand(2, -1, 1)).squeeze(-1)
+        g = torch.gather(self.gate_sequence, 1, w.unsqueeze(-1)).squeeze(-1)
+        is_const = torch.isin(g, const_gates.to(g.device))
+        only_a = torch.isin(g, trivial_gates_a.to(g.device))
+        only_b = torch.isin(g, trivial_gates_b.to(g.device))
+        uses_a = ~is_const & ~only_b
+        uses_b = ~is_const & ~only_a
+        y_flag[is_const] = False
+        used = torch.unique(torch.cat((pair[0][y_flag & uses_a], pair[1][y_flag & uses_b])))
+        x_flag[used] = True
+        y_flag[only_a | only_b] = False
+        return x_flag, y_flag
+
+
+class GroupSum(torch.nn.Module):
+    """k class scores from the summed outputs of k equal feature groups, divided by tau
+    (compactlogic/compactlogic.py:450-468).  A PackBitsTensor gives int32 per-class counts
+    (difflogic.py:203-205)."""
+
+    def __init__(self, k: int, tau: float = 1., device='cuda'):
+        super().__init__()
+        self.k = k
+        self.tau = tau
+        self.device = device
+
+    def forward(self, x):
+        if isinstance(x, PackBitsTensor):
+            return x.group_sum(self.k)
+        return GroupSumFunction.apply(x, self.k, self.tau)
+
+    def extra_repr(self):
+        return 'k={}, tau={}'.format(self.k, self.tau)

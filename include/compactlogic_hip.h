@@ -1,0 +1,172 @@
+/*
+ * compactlogic_hip.h -- C ABI of libcompactlogic_hip.so, the gfx950 (MI355X) kernels behind
+ * the LogicLayer / ConvLayer / GroupSum modules.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers (hipMalloc / torch CUDA tensors on ROCm) unless a
+ *     parameter says "host".  Buffers are dense, row-major and never mutated unless they are
+ *     outputs.  The caller allocates every output.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Every call only enqueues work on
+ *     that stream and returns; nothing synchronises the device.
+ *   - The return value is CL_OK (0) or one of the CL_ERR_* codes; cl_last_error() then
+ *     describes the failure for the calling thread.  No entry point exits the process.
+ *   - `dtype` selects the floating-point element type of the float buffers: CL_DTYPE_F32 or
+ *     CL_DTYPE_F64.
+ *   - Index buffers keep the reference's types: connection indices int64, gate opcodes
+ *     uint8, argmax slots uint8, backward-index starts / neuron ids int64, gate codes int8.
+ *   - Out-of-range indices never cause an out-of-bounds access: the affected outputs are
+ *     written as NaN (float paths) or all-zero words (packed paths).
+ *
+ * Reference interfaces replaced (paths relative to the eth-sri/CompactLogic tree):
+ *   difflogic_cuda  -- compactlogic/cuda/difflogic.cpp:60-105
+ *   convlogic_cuda  -- compactlogic/cuda/convlogic.cpp:49-110
+ *   GroupSum        -- compactlogic/compactlogic.py:450-468 (pure torch in the reference)
+ */
+#ifndef COMPACTLOGIC_HIP_H
+#define COMPACTLOGIC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CL_OK 0
+#define CL_ERR_INVALID_ARGUMENT 1 /* shapes, pointers or dtypes the kernels cannot take */
+#define CL_ERR_VALUE 2            /* a value error the reference raises as ValueError   */
+#define CL_ERR_HIP 3              /* the HIP runtime reported an error                   */
+
+#define CL_DTYPE_F32 0
+#define CL_DTYPE_F64 1
+
+/* ABI version of this header; bumped on any incompatible change. */
+int cl_abi_version(void);
+
+/* Message describing the last failed call on the calling thread ("" if none). */
+const char* cl_last_error(void);
+
+/* -------------------------------------------------------------------------------------------
+ * Dense LogicLayer, soft (training) path.  x: [in_dim, batch], y / grad_y: [out_dim, batch],
+ * a, b, w, gate_seq: [out_dim, num_gates].  w holds the softmax probabilities.
+ * ----------------------------------------------------------------------------------------- */
+
+/* difflogic_cuda.forward -- compactlogic/cuda/difflogic.cpp:61-66,
+ * compactlogic/cuda/difflogic_kernel.cu:197-236.
+ * y[o, n] = sum_g w[o, g] * op_{gate_seq[o, g]}(x[a[o, g], n], x[b[o, g], n]). */
+int cl_dense_forward(int dtype, const void* x, const int64_t* a, const int64_t* b, const void* w,
+                     const uint8_t* gate_seq, void* y, int64_t in_dim, int64_t out_dim,
+                     int64_t batch, int64_t num_gates, void* stream);
+
+/* difflogic_cuda.backward_w -- compactlogic/cuda/difflogic.cpp:67-71,
+ * compactlogic/cuda/difflogic_kernel.cu:239-282.
+ * grad_w[o, g] = sum_n grad_y[o, n] * op_{gate_seq[o, g]}(x[a[o, g], n], x[b[o, g], n]). */
+int cl_dense_backward_w(int dtype, const void* x, const int64_t* a, const int64_t* b,
+                        const uint8_t* gate_seq, const void* grad_y, void* grad_w, int64_t in_dim,
+                        int64_t out_dim, int64_t batch, int64_t num_gates, void* stream);
+
+/* difflogic_cuda.backward_x -- compactlogic/cuda/difflogic.cpp:72-77,
+ * compactlogic/cuda/difflogic_kernel.cu:285-333.  Deterministic gather through the
+ * reference's inverse index (compactlogic/compactlogic.py:184-274): row i of the index is
+ * entries start[i] .. start[i+1]-1 of (y_index, gate_code); gate_code g >= 0 means x_i is
+ * operand a of slot g of neuron y_index, -(g+1) means operand b.  num_entries is the length
+ * of y_index / gate_code. */
+int cl_dense_backward_x(int dtype, const void* x, const int64_t* a, const int64_t* b,
+                        const void* w, const uint8_t* gate_seq, const void* grad_y,
+                        const int64_t* start, const int64_t* y_index, const int8_t* gate_code,
+                        int64_t num_entries, void* grad_x, int64_t in_dim, int64_t out_dim,
+                        int64_t batch, int64_t num_gates, void* stream);
+
+/* difflogic_cuda.eval -- compactlogic/cuda/difflogic.cpp:78-83,
+ * compactlogic/cuda/difflogic_kernel.cu:341-411.  Discrete forward with the argmax slot
+ * w_slot[o] (a slot index, not an opcode): y[o, n] = op_s(x[a[o, s], n], x[b[o, s], n]) with
+ * s = w_slot[o] and op = gate_seq[o, s], evaluated with the relaxed formula. */
+int cl_dense_eval(int dtype, const void* x, const int64_t* a, const int64_t* b,
+                  const uint8_t* w_slot, const uint8_t* gate_seq, void* y, int64_t in_dim,
+                  int64_t out_dim, int64_t batch, int64_t num_gates, void* stream);
+
+/* -------------------------------------------------------------------------------------------
+ * Dense LogicLayer through a connection-run plan (no reference counterpart: the plan is
+ * derived from `indices` by the module and regenerated whenever the indices change).
+ *
+ * A run is a maximal range of consecutive slots [g0, g0+len) of one neuron whose slots share
+ * one input pair (a, b).  Because the relaxed operators are affine in each weight, a run
+ * collapses to four coefficients K = sum_{g in run} w[o,g] * (c0, c1, c2, c3)[gate_seq[o,g]],
+ * so each run costs two row gathers however many slots it spans.
+ *   run_ptr  int32 [out_dim + 1]   runs of neuron o are run_ptr[o] .. run_ptr[o+1]-1
+ *   run_ab   int32 [num_runs, 2]   input pair (a, b) of the run
+ *   run_gl   int32 [num_runs]      g0 | (len << 8)
+ *   run_y    int32 [num_runs]      neuron of the run
+ *   inv_ptr  int32 [in_dim + 1]    inverse index over inputs ...
+ *   inv_entry int32 [2 * num_runs] ... entries 2*r + side (side 0: operand a, 1: operand b)
+ * ----------------------------------------------------------------------------------------- */
+
+int cl_dense_forward_runs(int dtype, const void* x, const void* w, const uint8_t* gate_seq,
+                          const int32_t* run_ptr, const int32_t* run_ab, const int32_t* run_gl,
+                          void* y, int64_t in_dim, int64_t out_dim, int64_t num_runs,
+                          int64_t batch, int64_t num_gates, void* stream);
+
+/* Backward through the plan.  grad_x and/or grad_w may be NULL when not needed.  When both
+ * are requested the two are produced by one pass over the inverse index (the weight moments
+ * of each run are taken at its operand-a entry). */
+int cl_dense_backward_runs(int dtype, const void* x, const void* w, const uint8_t* gate_seq,
+                           const void* grad_y, const int32_t* run_ptr, const int32_t* run_ab,
+                           const int32_t* run_gl, const int32_t* run_y, const int32_t* inv_ptr,
+                           const int32_t* inv_entry, void* grad_x, void* grad_w, int64_t in_dim,
+                           int64_t out_dim, int64_t num_runs, int64_t batch, int64_t num_gates,
+                           void* stream);
+
+/* -------------------------------------------------------------------------------------------
+ * GroupSum -- compactlogic/compactlogic.py:450-468: out[n, c] = sum_{j in group c} x[n, j] / tau
+ * with the features zero-padded to a multiple of k; group c is columns
+ * [c*gs, min((c+1)*gs, features)), gs = ceil(features / k).  x is read through
+ * (stride_batch, stride_feature) element strides so the transposed view a LogicLayer returns
+ * is consumed without a copy.  out / grad_out: [batch, k] contiguous.
+ * ----------------------------------------------------------------------------------------- */
+int cl_group_sum_forward(int dtype, const void* x, int64_t batch, int64_t features,
+                         int64_t stride_batch, int64_t stride_feature, int64_t k, double tau,
+                         void* out, void* stream);
+
+/* grad_x[n, j] = grad_out[n, group(j)] / tau, written through (stride_batch, stride_feature). */
+int cl_group_sum_backward(int dtype, const void* grad_out, int64_t batch, int64_t features,
+                          int64_t k, double tau, void* grad_x, int64_t stride_batch,
+                          int64_t stride_feature, void* stream);
+
+/* -------------------------------------------------------------------------------------------
+ * Bit-packed discrete inference.  A packed row is a little-endian bit string: bit j of the
+ * row is sample j (word w of bit_count bits holds samples bit_count*w .. +bit_count-1, least
+ * significant bit first), as written by tensor_packbits_cuda
+ * (compactlogic/cuda/difflogic_kernel.cu:417-494).  row_bytes is the byte length of one row.
+ * ----------------------------------------------------------------------------------------- */
+
+/* difflogic_cuda.tensor_packbits_cuda -- compactlogic/cuda/difflogic.cpp:84-89,
+ * compactlogic/cuda/difflogic_kernel.cu:417-494.  t: bool (one byte, 0 or 1) [rows, n] ->
+ * packed [rows, ceil(n / bit_count)] words of bit_count in {8, 16, 32, 64}.  *pad_len (host)
+ * receives (bit_count - n % bit_count) % bit_count.  Padding bits are zero. */
+int cl_pack_bits(const uint8_t* t, int64_t rows, int64_t n, int32_t bit_count, void* packed,
+                 int64_t* pad_len, void* stream);
+
+/* Integer difflogic_cuda.eval on packed words
+ * (third_party/convlogic_source_code/src/difflogic/cuda/difflogic_kernel.cu:271-330) with
+ * compactlogic's slot semantics (compactlogic/compactlogic.py:120-130):
+ * y[o, :] = op(x[a[o, s], :], x[b[o, s], :]) bitwise, s = w_slot[o], op = gate_seq[o, s]. */
+int cl_dense_eval_packed(const void* x, const int64_t* a, const int64_t* b, const uint8_t* w_slot,
+                         const uint8_t* gate_seq, void* y, int64_t in_dim, int64_t out_dim,
+                         int64_t row_bytes, int64_t num_gates, void* stream);
+
+/* difflogic_cuda.groupbitsum -- compactlogic/cuda/difflogic.cpp:90-98,
+ * compactlogic/cuda/difflogic_kernel.cu:500-568.  counts[n, c] (int32, [N, k]) = number of
+ * set bits of sample n over the rows of group c (rows c*rows/k .. (c+1)*rows/k - 1), for
+ * n < N = row_bytes*8 - pad_len.  Returns CL_ERR_VALUE when rows % k != 0. */
+int cl_group_bit_sum(const void* packed, int64_t rows, int64_t row_bytes, int64_t pad_len,
+                     int64_t k, int32_t* counts, void* stream);
+
+/* Synthetic packed input for tests and benchmarks (no reference counterpart):
+ * out[i] = splitmix64(base + i) for i < count. */
+int cl_fill_splitmix64(uint64_t* out, int64_t count, uint64_t base, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COMPACTLOGIC_HIP_H */

@@ -1,0 +1,207 @@
+"""Dense LogicLayer kernels against the float64 CPU oracle.
+
+Tolerance (north star): fp32 results within rtol 1e-5 / atol 1e-6 of the float64 oracle; the
+upstream gradients are drawn at the scale of a mean-reduced loss (|gy| <= 1/batch) so batch
+reductions stay O(1).  fp64 results within rtol 1e-10 / atol 1e-12.
+"""
+import numpy as np
+import pytest
+import torch
+
+import compactlogic_amd as cl
+from compactlogic_amd import difflogic_hip as dl
+from oracle import logic_np as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: dict(rtol=1e-5, atol=1e-6), torch.float64: dict(rtol=1e-10, atol=1e-12)}
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+def make_layer(seed, in_dim, out_dim, g_n, batch, shared=False, binary_x=False):
+    rng = np.random.default_rng(seed)
+    if shared:
+        a = np.repeat(rng.integers(0, in_dim, out_dim)[:, None], g_n, 1)
+        b = np.repeat(rng.integers(0, in_dim, out_dim)[:, None], g_n, 1)
+    else:
+        a = rng.integers(0, in_dim, (out_dim, g_n))
+        b = rng.integers(0, in_dim, (out_dim, g_n))
+        # a few neurons with partially shared pairs, so runs of several lengths occur
+        for o in range(0, out_dim, 5):
+            a[o, : g_n // 2] = a[o, 0]
+            b[o, : g_n // 2] = b[o, 0]
+    gs = rng.integers(0, 16, (out_dim, g_n)).astype(np.uint8)
+    logits = rng.standard_normal((out_dim, g_n))
+    w = np.exp(logits) / np.exp(logits).sum(1, keepdims=True)
+    x = rng.integers(0, 2, (in_dim, batch)).astype(np.float64) if binary_x else rng.random((in_dim, batch))
+    gy = rng.uniform(-1, 1, (out_dim, batch)) / max(batch, 1)
+    return dict(x=x, a=a, b=b, gs=gs, w=w, gy=gy)
+
+
+def to_dev(L, device, dtype):
+    t = lambda v, dt: torch.as_tensor(v).to(device=device, dtype=dt).contiguous()
+    return dict(x=t(L["x"], dtype), a=t(L["a"], torch.int64), b=t(L["b"], torch.int64),
+                gs=t(L["gs"], torch.uint8), w=t(L["w"], dtype), gy=t(L["gy"], dtype))
+
+
+SHAPES = [
+    # in, out, G, batch, shared
+    (8, 64, 16, 1, False),
+    (23, 37, 4, 3, False),
+    (50, 40, 1, 64, False),
+    (100, 120, 16, 130, True),
+    (300, 256, 16, 1024, True),
+    (64, 80, 8, 2500, False),
+    (784, 500, 16, 128, True),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_dropin_kernels_match_oracle(device, dtype, shape):
+    in_dim, out_dim, g_n, batch, shared = shape
+    L = make_layer(hash(shape) % 1000, in_dim, out_dim, g_n, batch, shared)
+    D = to_dev(L, device, dtype)
+    y = dl.forward(D["x"], D["a"], D["b"], D["w"], D["gs"])
+    np.testing.assert_allclose(np_(y), O.dense_forward(L["x"], L["a"], L["b"], L["w"], L["gs"]),
+                               **TOL[dtype])
+    gw = dl.backward_w(D["x"], D["a"], D["b"], D["gs"], D["gy"])
+    np.testing.assert_allclose(np_(gw), O.dense_backward_w(L["x"], L["a"], L["b"], L["gs"], L["gy"]),
+                               **TOL[dtype])
+    start, yidx, code = O.backward_index(np.stack([L["a"], L["b"]]), in_dim)
+    gx = dl.backward_x(D["x"], D["a"], D["b"], D["w"], D["gs"], D["gy"],
+                       torch.as_tensor(start, device=device), torch.as_tensor(yidx, device=device),
+                       torch.as_tensor(code, device=device))
+    np.testing.assert_allclose(np_(gx), O.dense_backward_x_direct(L["x"], L["a"], L["b"], L["w"],
+                                                                 L["gs"], L["gy"]), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_run_plan_kernels_match_oracle(device, dtype, shape):
+    in_dim, out_dim, g_n, batch, shared = shape
+    L = make_layer(hash(shape) % 1000 + 1, in_dim, out_dim, g_n, batch, shared)
+    D = to_dev(L, device, dtype)
+    plan = cl.build_run_plan(torch.stack([D["a"], D["b"]]), in_dim)
+    x = D["x"].clone().requires_grad_(True)
+    w = D["w"].clone().requires_grad_(True)
+    y = cl.LogicLayerRunsFunction.apply(x, w, D["gs"], plan)
+    np.testing.assert_allclose(np_(y), O.dense_forward(L["x"], L["a"], L["b"], L["w"], L["gs"]),
+                               **TOL[dtype])
+    gx, gw = torch.autograd.grad(y, (x, w), D["gy"])
+    np.testing.assert_allclose(np_(gw), O.dense_backward_w(L["x"], L["a"], L["b"], L["gs"], L["gy"]),
+                               **TOL[dtype])
+    np.testing.assert_allclose(np_(gx), O.dense_backward_x_direct(L["x"], L["a"], L["b"], L["w"],
+                                                                 L["gs"], L["gy"]), **TOL[dtype])
+    # weight gradient alone (input needs no grad: the unfused per-neuron kernel)
+    w2 = D["w"].clone().requires_grad_(True)
+    y2 = cl.LogicLayerRunsFunction.apply(D["x"], w2, D["gs"], plan)
+    (gw2,) = torch.autograd.grad(y2, (w2,), D["gy"])
+    np.testing.assert_allclose(np_(gw2), np_(gw), **TOL[dtype])
+
+
+def test_eval_matches_truth_table(device):
+    L = make_layer(5, 40, 70, 6, 97, binary_x=True)
+    D = to_dev(L, device, torch.float32)
+    slot = np.random.default_rng(5).integers(0, 6, 70).astype(np.uint8)
+    y = dl.eval(D["x"], D["a"], D["b"], torch.as_tensor(slot, device=device), D["gs"])
+    assert np.array_equal(np_(y), O.dense_eval(L["x"], L["a"], L["b"], slot, L["gs"]))
+
+
+def test_all_gates_known_answer_through_module(device):
+    """third_party/convlogic_source_code/tests/difflogic/test_difflogic_forward.py:74-100 on
+    the module path: one-hot logits select gate g for rows 4g..4g+3."""
+    layer = cl.LogicLayer(8, 64, num_gates=16).to(device)
+    pairs = torch.tensor([[0, 1], [2, 3], [4, 5], [6, 7]], device=device).repeat(16, 1)
+    with torch.no_grad():
+        layer.indices.copy_(pairs.t().unsqueeze(-1).expand(2, 64, 16))
+        logits = torch.full((64, 16), float("-inf"), device=device)
+        for g in range(16):
+            logits[4 * g: 4 * g + 4, g] = 0.0
+        layer.weights.copy_(logits)
+    flat = [0.0, 0.0, 0.0, 1.0, 1.0, 0.0, 1.0, 1.0]
+    y = layer(torch.tensor([flat], device=device))
+    expected = [O.TRUTH[g, 2 * int(flat[p]) + int(flat[p + 1])] for g in range(16) for p in (0, 2, 4, 6)]
+    assert torch.equal(y.cpu(), torch.tensor([expected], dtype=torch.float32))
+    layer.eval()
+    assert torch.equal(layer(torch.tensor([flat], device=device)).cpu(),
+                       torch.tensor([expected], dtype=torch.float32))
+
+
+def test_module_paths_agree_and_are_deterministic(device):
+    torch.manual_seed(7)
+    layer = cl.LogicLayer(200, 300, num_gates=16).to(device)
+    x = torch.rand(96, 200, device=device, requires_grad=True)
+    gy = torch.randn(96, 300, device=device) / 96
+
+    def run_module():
+        layer.weights.grad = None
+        xx = x.detach().clone().requires_grad_(True)
+        y = layer(xx)
+        y.backward(gy)
+        return y.detach(), xx.grad, layer.weights.grad.clone()
+
+    def run_reference_function():
+        layer.weights.grad = None
+        xx = x.detach().clone().requires_grad_(True)
+        w = torch.softmax(layer.weights, -1)
+        y = cl.LogicLayerCudaFunction.apply(
+            xx.t().contiguous(), layer.indices[0], layer.indices[1], w, layer.gate_sequence,
+            layer.given_x_indices_of_y_start, layer.given_x_indices_of_y,
+            layer.given_x_indices_of_gate).t()
+        y.backward(gy)
+        return y.detach(), xx.grad, layer.weights.grad.clone()
+
+    r1, r2, r3 = run_module(), run_module(), run_reference_function()
+    for u, v in zip(r1, r2):
+        assert torch.equal(u, v), "module path is not bitwise deterministic"
+    for u, v in zip(r1, r3):
+        torch.testing.assert_close(u, v, rtol=1e-5, atol=1e-6)
+
+
+def test_gradcheck_fp64(device):
+    L = make_layer(11, 9, 7, 4, 5)
+    D = to_dev(L, device, torch.float64)
+    plan = cl.build_run_plan(torch.stack([D["a"], D["b"]]), 9)
+    x = D["x"].clone().requires_grad_(True)
+    w = D["w"].clone().requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda xx, ww: cl.LogicLayerRunsFunction.apply(xx, ww, D["gs"], plan),
+                                    (x, w), eps=1e-6, atol=1e-8)
+    start, yidx, code = (torch.as_tensor(v, device=device)
+                         for v in O.backward_index(np.stack([L["a"], L["b"]]), 9))
+    assert torch.autograd.gradcheck(
+        lambda xx, ww: cl.LogicLayerCudaFunction.apply(xx, D["a"], D["b"], ww, D["gs"], start, yidx, code),
+        (x, w), eps=1e-6, atol=1e-8)
+
+
+def test_invalid_indices_poison_instead_of_faulting(device):
+    L = make_layer(12, 10, 8, 4, 16)
+    D = to_dev(L, device, torch.float32)
+    a = D["a"].clone()
+    a[3, 1] = 10_000
+    y = dl.forward(D["x"], a, D["b"], D["w"], D["gs"])
+    assert torch.isnan(y[3]).all() and not torch.isnan(y[torch.arange(8) != 3]).any()
+
+
+def test_empty_batch_and_zero_width(device):
+    L = make_layer(13, 10, 6, 4, 0)
+    D = to_dev(L, device, torch.float32)
+    assert dl.forward(D["x"], D["a"], D["b"], D["w"], D["gs"]).shape == (6, 0)
+    gw = dl.backward_w(D["x"], D["a"], D["b"], D["gs"], D["gy"])
+    assert torch.equal(gw, torch.zeros_like(gw))
+
+
+def test_rewiring_keeps_training_path_consistent(device):
+    torch.manual_seed(8)
+    layer = cl.LogicLayer(30, 40).to(device)
+    with torch.no_grad():
+        layer.weights[:10] = 0.0
+    layer.resample_connections(torch.arange(10, device=device), threshold_low=0.5)
+    x = torch.rand(16, 30, device=device)
+    y = layer(x)
+    ref = O.dense_forward(np_(x).T, np_(layer.indices[0]), np_(layer.indices[1]),
+                          np_(torch.softmax(layer.weights, -1)), np_(layer.gate_sequence))
+    np.testing.assert_allclose(np_(y).T, ref, rtol=1e-5, atol=1e-6)
