@@ -540,7 +540,8 @@ extern "C" int cl_dense_backward_w(int dtype, const void* x, const int64_t* a, c
     clear_error();
     if (int rc = check_dims(in_dim, out_dim, batch, num_gates)) return rc;
     if (out_dim == 0) return CL_OK;
-    CL_ARG(x && a && b && gate_seq && grad_y && grad_w, "null pointer argument");
+    CL_ARG(a && b && gate_seq && grad_w, "null pointer argument");
+    CL_ARG(batch == 0 || (x && grad_y), "null pointer argument");
     CL_ARG(in_dim > 0 || batch == 0, "in_dim is 0 but out_dim > 0");
     CL_DTYPE_SWITCH(dtype, {
         const int vec = pick_vec<scalar_t>(batch, {x, grad_y});
@@ -625,9 +626,11 @@ extern "C" int cl_dense_backward_runs(int dtype, const void* x, const void* w,
     clear_error();
     if (int rc = check_dims(in_dim, out_dim, batch, num_gates)) return rc;
     CL_ARG(num_runs >= 0 && num_runs < (int64_t(1) << 30), "num_runs out of range");
-    CL_ARG(x && w && gate_seq && grad_y && run_ptr && run_ab && run_gl, "null pointer argument");
-    CL_ARG(aligned(run_ab, 8), "run_ab must be 8-byte aligned");
     if (!grad_x && !grad_w) return CL_OK;
+    if (out_dim == 0 && (in_dim == 0 || batch == 0 || !grad_x)) return CL_OK;
+    CL_ARG(w && gate_seq && run_ptr && run_ab && run_gl, "null pointer argument");
+    CL_ARG(batch == 0 || (x && grad_y), "null pointer argument");
+    CL_ARG(aligned(run_ab, 8), "run_ab must be 8-byte aligned");
     if (grad_x) CL_ARG(run_y && inv_ptr && inv_entry, "grad_x needs run_y, inv_ptr and inv_entry");
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
