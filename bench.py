@@ -142,6 +142,7 @@ def time_dense_kernels(model, x, reps, torch):
         plan = layer.run_plan()
         w = torch.softmax(layer.weights, -1).contiguous()
         y = torch.empty((plan.out_dim, batch), device=xt.device)
+        coef = torch.empty((plan.num_runs, 4), device=xt.device)
         gy = torch.randn_like(y) / batch
         gx = torch.empty_like(xt)
         gw = torch.empty_like(w)
@@ -149,9 +150,10 @@ def time_dense_kernels(model, x, reps, torch):
         fwd = lambda: _capi.call("cl_dense_forward_runs", 0, xt.data_ptr(), w.data_ptr(),
                                  layer.gate_sequence.data_ptr(), plan.run_ptr.data_ptr(),
                                  plan.run_ab.data_ptr(), plan.run_gl.data_ptr(), y.data_ptr(),
-                                 plan.in_dim, plan.out_dim, plan.num_runs, batch, plan.num_gates, s)
+                                 coef.data_ptr(), plan.in_dim, plan.out_dim, plan.num_runs, batch,
+                                 plan.num_gates, s)
         want_gx = li > 0
-        bwd = lambda: _capi.call("cl_dense_backward_runs", 0, xt.data_ptr(), w.data_ptr(),
+        bwd = lambda: _capi.call("cl_dense_backward_runs", 0, xt.data_ptr(), coef.data_ptr(),
                                  layer.gate_sequence.data_ptr(), gy.data_ptr(),
                                  plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
                                  plan.run_gl.data_ptr(), plan.run_y.data_ptr(),
@@ -166,12 +168,24 @@ def time_dense_kernels(model, x, reps, torch):
             kernel="k_dense_backward_runs" if want_gx else "k_dense_backward_w_runs", seconds=t_b,
             algorithmic_bytes=(2 * in_b + out_b) if want_gx else (in_b + out_b))
     # GroupSum over the last layer's [12000, batch] output
+    import ctypes
     ylast = torch.rand((layers[-1].out_dim, batch), device=x.device)
     head = torch.empty((batch, 10), device=x.device)
+    need = ctypes.c_int64(0)
+    _capi.call("cl_group_sum_workspace_size", 0, batch, ylast.shape[0], 1, batch, 10,
+               ctypes.byref(need))
+    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
     gsf = lambda: _capi.call("cl_group_sum_forward", 0, ylast.data_ptr(), batch, ylast.shape[0],
-                             1, batch, 10, 10.0, head.data_ptr(), stream.cuda_stream)
-    out["groupsum_forward"] = dict(kernel="k_gsum_fwd_bc", seconds=timed(gsf),
+                             1, batch, 10, 10.0, head.data_ptr(), ws.data_ptr(), need.value,
+                             stream.cuda_stream)
+    out["groupsum_forward"] = dict(kernel="k_gsum_partial+k_gsum_finish", seconds=timed(gsf),
                                    algorithmic_bytes=ylast.numel() * 4 + head.numel() * 4)
+    gx_head = torch.empty_like(ylast)
+    ghead = torch.randn_like(head)
+    gsb = lambda: _capi.call("cl_group_sum_backward", 0, ghead.data_ptr(), batch, ylast.shape[0],
+                             10, 10.0, gx_head.data_ptr(), 1, batch, stream.cuda_stream)
+    out["groupsum_backward"] = dict(kernel="k_gsum_bwd", seconds=timed(gsb),
+                                    algorithmic_bytes=gx_head.numel() * 4 + ghead.numel() * 4)
     for v in out.values():
         v["achieved_GBs"] = v["algorithmic_bytes"] / v["seconds"] / 1e9
     return out
@@ -293,6 +307,16 @@ def cpu_baseline_packed(torch):
                       f"single thread, {reps} timed passes"}
 
 
+def calibration_copy(torch, mib: int = 512):
+    """A plain device copy of known size (reads and writes `mib` MiB), run once so that a
+    counter profile of this command can scale FETCH_SIZE / WRITE_SIZE against it."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 # ---------------------------------------------------------------------------------- main
 
 def main():
@@ -310,6 +334,7 @@ def main():
     from compactlogic_amd import _capi
     _capi.load()
 
+    calibration_copy(torch)
     log(f"dense cfg2: mode={args.mode} warmup={args.warmup} steps={args.steps}")
     cfg, samples_s, dt, kernels, matches = bench_dense(args, torch)
     log(f"dense cfg2: {samples_s:,.0f} samples/s, {dt * 1e3:.3f} ms/step")

@@ -9,7 +9,9 @@ import ctypes
 import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libcompactlogic_hip.so"
+# COMPACTLOGIC_HIP_LIB selects another build of the same library (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("COMPACTLOGIC_HIP_LIB",
+                               Path(__file__).resolve().parent / "libcompactlogic_hip.so"))
 
 CL_OK = 0
 CL_ERR_INVALID_ARGUMENT = 1
@@ -36,10 +38,13 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_backward_x": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64,
                             _i64, _i64, _p],
     "cl_dense_eval": [_int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
-    "cl_dense_forward_runs": [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
+    "cl_dense_forward_runs": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                              _i64, _p],
+    "cl_dense_run_coefs": [_int, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_dense_backward_runs": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
                                _i64, _i64, _i64, _p],
-    "cl_group_sum_forward": [_int, _p, _i64, _i64, _i64, _i64, _i64, _f64, _p, _p],
+    "cl_group_sum_forward": [_int, _p, _i64, _i64, _i64, _i64, _i64, _f64, _p, _p, _i64, _p],
+    "cl_group_sum_workspace_size": [_int, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
     "cl_group_sum_backward": [_int, _p, _i64, _i64, _i64, _f64, _p, _i64, _i64, _p],
     "cl_pack_bits": [_p, _i64, _i64, _i32, _p, ctypes.POINTER(_i64), _p],
     "cl_dense_eval_packed": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],

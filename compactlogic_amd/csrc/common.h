@@ -110,6 +110,45 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+// DPP lane permutation of a 32- or 64-bit value (64-bit values move as two halves).
+template <int CTRL, typename T>
+__device__ __forceinline__ T dpp_move(T v) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(
+            T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const int lo = __builtin_amdgcn_update_dpp(0, int(uint32_t(u)), CTRL, 0xF, 0xF, false);
+        const int hi = __builtin_amdgcn_update_dpp(0, int(uint32_t(u >> 32)), CTRL, 0xF, 0xF, false);
+        return __builtin_bit_cast(T, (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T read_lane(T v, int lane) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = __builtin_amdgcn_readlane(int(uint32_t(u)), lane);
+        const uint32_t hi = __builtin_amdgcn_readlane(int(uint32_t(u >> 32)), lane);
+        return __builtin_bit_cast(T, (uint64_t(hi) << 32) | lo);
+    }
+}
+
+// Sum over all 64 lanes, returned as a wave-uniform (scalar) value.  Each 16-lane row is
+// reduced with DPP (quad swaps 1 and 2, then row rotations by 4 and 8, after which every
+// lane of a row holds the row total), and the four row totals are added in lane order, so
+// the result does not depend on scheduling.
+template <typename T>
+__device__ __forceinline__ T wave_total(T v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move<0x124>(v);  // row_ror:4
+    v += dpp_move<0x128>(v);  // row_ror:8
+    return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
+}
+
 // Wave index inside the workgroup, as a scalar (uniform) value.
 __device__ __forceinline__ int wave_id() {
     return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -57,6 +57,70 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_gsum_fwd_bc(const T* __res
     }
 }
 
+// ---- forward, batch-contiguous, split: block = (batch tile, class c, slice s of the
+// group).  Each block writes the partial sum of its slice; k_gsum_finish adds the slices in
+// slice order.  Used when a workspace is given, so that enough blocks fill the GPU.
+constexpr int kPartWaves = 4;
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kPartWaves * 64) void k_gsum_partial(const T* __restrict__ x,
+                                                                 int64_t B, int64_t F,
+                                                                 int64_t sf, int64_t gsz,
+                                                                 int64_t k, int64_t slice,
+                                                                 T* __restrict__ part) {
+    __shared__ T red[kPartWaves][64 * VEC];
+    const int wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t c = blockIdx.y, sidx = blockIdx.z;
+    const int64_t n0 = int64_t(blockIdx.x) * 64 * VEC + int64_t(lane) * VEC;
+    const int64_t g_end = std::min<int64_t>((c + 1) * gsz, F);
+    const int64_t j0 = c * gsz + sidx * slice;
+    const int64_t j1 = std::min<int64_t>(j0 + slice, g_end);
+    Vec<T, VEC> acc;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc.v[i] = T(0);
+    if (n0 < B) {
+        for (int64_t j = j0 + wv; j < j1; j += kPartWaves) {
+            const Vec<T, VEC> v = vload<T, VEC>(x + j * sf + n0);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc.v[i] += v.v[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) red[wv][lane * VEC + i] = acc.v[i];
+    __syncthreads();
+    T* dst = part + (sidx * k + c) * B;
+    for (int e = threadIdx.x; e < 64 * VEC; e += kPartWaves * 64) {
+        const int64_t n = int64_t(blockIdx.x) * 64 * VEC + e;
+        if (n < B) {
+            T t = red[0][e];
+#pragma unroll
+            for (int w = 1; w < kPartWaves; ++w) t += red[w][e];
+            dst[n] = t;
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_gsum_finish(const T* __restrict__ part, int64_t B,
+                                                     int64_t k, int64_t nslices, T tau,
+                                                     T* __restrict__ out) {
+    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;  // c * B + n
+    if (item >= B * k) return;
+    const int64_t c = item / B, n = item % B;
+    T t = 0;
+    for (int64_t s = 0; s < nslices; ++s) t += part[(s * k + c) * B + n];
+    out[n * k + c] = t / tau;
+}
+
+// Slices per group for the split forward (1 = no split).
+inline int64_t gsum_slices(int64_t B, int64_t F, int64_t k, int vec) {
+    const int64_t gsz = F == 0 ? 1 : ceil_div(F, k);
+    const int64_t tiles = ceil_div(B, 64 * vec);
+    const int64_t want = ceil_div(1024, tiles * k);
+    return std::max<int64_t>(1, std::min<int64_t>(want, ceil_div(gsz, 16)));
+}
+
 // ---- forward, feature-contiguous: one wave per (sample n, class c)
 template <typename T>
 __global__ __launch_bounds__(256) void k_gsum_fwd_fc(const T* __restrict__ x, int64_t B,
@@ -129,15 +193,41 @@ __global__ __launch_bounds__(256) void k_gsum_bwd_generic(const T* __restrict__ 
 
 using namespace cl;
 
+namespace {
+bool gsum_split_applies(int64_t batch, int64_t features, int64_t stride_batch) {
+    return stride_batch == 1 && features > 0 && batch >= 64;
+}
+}  // namespace
+
+extern "C" int cl_group_sum_workspace_size(int dtype, int64_t batch, int64_t features,
+                                           int64_t stride_batch, int64_t stride_feature,
+                                           int64_t k, int64_t* bytes) {
+    clear_error();
+    CL_ARG(bytes, "null pointer argument");
+    CL_ARG(batch >= 0 && features >= 0 && k >= 1, "bad shape");
+    *bytes = 0;
+    if (!gsum_split_applies(batch, features, stride_batch)) return CL_OK;
+    CL_DTYPE_SWITCH(dtype, {
+        constexpr int W = wide_vec<scalar_t>();
+        const bool wide = batch % W == 0 && stride_feature % W == 0;
+        const int64_t slices = gsum_slices(batch, features, k, wide ? W : 1);
+        *bytes = slices > 1 ? slices * k * batch * int64_t(sizeof(scalar_t)) : 0;
+    });
+    return CL_OK;
+}
+
 extern "C" int cl_group_sum_forward(int dtype, const void* x, int64_t batch, int64_t features,
                                     int64_t stride_batch, int64_t stride_feature, int64_t k,
-                                    double tau, void* out, void* stream) {
+                                    double tau, void* out, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
     clear_error();
     CL_ARG(batch >= 0 && features >= 0, "negative shape");
     CL_ARG(k >= 1, "k must be >= 1, got %lld", (long long)k);
     CL_ARG(stride_batch >= 0 && stride_feature >= 0, "negative strides are not supported");
+    CL_ARG(workspace_bytes >= 0, "negative workspace size");
     if (batch == 0) return CL_OK;
-    CL_ARG(x && out, "null pointer argument");
+    CL_ARG(out, "null pointer argument");
+    CL_ARG(features == 0 || x, "null pointer argument");
     const int64_t gsz = features == 0 ? 1 : ceil_div(features, k);
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
@@ -146,9 +236,25 @@ extern "C" int cl_group_sum_forward(int dtype, const void* x, int64_t batch, int
         T* os = static_cast<T*>(out);
         const T t = T(tau);
         constexpr int W = wide_vec<T>();
-        if (stride_batch == 1 && features > 0 && batch >= 64) {
+        if (gsum_split_applies(batch, features, stride_batch)) {
             const bool wide = batch % W == 0 && stride_feature % W == 0 && aligned(x, 16);
-            if (wide) {
+            const int vec = wide ? W : 1;
+            const int64_t slices = gsum_slices(batch, features, k, vec);
+            const int64_t need = slices * k * batch * int64_t(sizeof(T));
+            if (slices > 1 && workspace && workspace_bytes >= need) {
+                T* part = static_cast<T*>(workspace);
+                const int64_t slice = ceil_div(gsz, slices);
+                const dim3 grid(unsigned(ceil_div(batch, 64 * vec)), unsigned(k), unsigned(slices));
+                if (wide)
+                    k_gsum_partial<T, W><<<grid, kPartWaves * 64, 0, s>>>(
+                        xs, batch, features, stride_feature, gsz, k, slice, part);
+                else
+                    k_gsum_partial<T, 1><<<grid, kPartWaves * 64, 0, s>>>(
+                        xs, batch, features, stride_feature, gsz, k, slice, part);
+                if (int rc = check_launch("cl_group_sum_forward(partial)")) return rc;
+                k_gsum_finish<T><<<unsigned(ceil_div(batch * k, 256)), 256, 0, s>>>(
+                    part, batch, k, slices, t, os);
+            } else if (wide) {
                 const dim3 grid(unsigned(ceil_div(batch, 64 * W)), unsigned(k), 1);
                 k_gsum_fwd_bc<T, W><<<grid, kSplitWaves * 64, 0, s>>>(xs, batch, features,
                                                                       stride_feature, gsz, k, t, os);
@@ -157,7 +263,7 @@ extern "C" int cl_group_sum_forward(int dtype, const void* x, int64_t batch, int
                 k_gsum_fwd_bc<T, 1><<<grid, kSplitWaves * 64, 0, s>>>(xs, batch, features,
                                                                       stride_feature, gsz, k, t, os);
             }
-        } else if (stride_feature == 1) {
+        } else if (stride_feature == 1 || features <= 1) {
             const dim3 grid(unsigned(ceil_div(batch * k, 4)), 1, 1);
             k_gsum_fwd_fc<T><<<grid, 256, 0, s>>>(xs, batch, features, stride_batch, gsz, k, t, os);
         } else {

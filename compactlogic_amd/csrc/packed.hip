@@ -8,6 +8,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace cl {
 namespace {
@@ -143,6 +144,11 @@ struct SliceCounter {
     }
 };
 
+#ifndef CL_PACKED_UNROLL
+#define CL_PACKED_UNROLL 4
+#endif
+constexpr int kPackedUnroll = CL_PACKED_UNROLL;  // 16-byte vectors per lane in the layer kernel
+
 constexpr int kGbsThreads = 256;
 constexpr int kGbsMaxClasses = 16;  // classes per pass
 
@@ -153,7 +159,9 @@ __global__ __launch_bounds__(kGbsThreads) void k_group_bit_sum(const W* __restri
                                                                int cols, int kb,
                                                                int32_t* __restrict__ counts) {
     constexpr int kBits = int(sizeof(W)) * 8;
-    extern __shared__ int32_t lds[];  // [cols][kBits * kb + 1]
+    using CountT = typename std::conditional<NB <= 16, uint16_t, int32_t>::type;
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    CountT* lds = reinterpret_cast<CountT*>(lds_raw);  // [cols][kBits * kb + 1]
     const int row_stride = kBits * kb + 1;
     const int t = threadIdx.x;
     const int cls = t / cols, col = t % cols;
@@ -210,8 +218,8 @@ __global__ __launch_bounds__(kGbsThreads) void k_group_bit_sum(const W* __restri
         cnt.add(twos, 1);
         cnt.add(fours, 2);
         cnt.add(eights, 3);
-        int32_t* dst = lds + col * row_stride + cls;
-        for (int bit = 0; bit < kBits; ++bit) dst[bit * kb] = cnt.count(bit);
+        CountT* dst = lds + col * row_stride + cls;
+        for (int bit = 0; bit < kBits; ++bit) dst[bit * kb] = CountT(cnt.count(bit));
     }
     __syncthreads();
 
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(kGbsThreads) void k_group_bit_sum(const W* __restri
         const int64_t sample = s_base + sl;
         if (cl < kb_here && sample < n_valid) {
             const int64_t cc = sl / kBits, bit = sl % kBits;
-            counts[sample * k + c0 + cl] = lds[cc * row_stride + bit * kb + cl];
+            counts[sample * k + c0 + cl] = int32_t(lds[cc * row_stride + bit * kb + cl]);
         }
     }
 }
@@ -235,11 +243,12 @@ template <typename W, int NB>
 void launch_gbs(const W* x, int64_t words, int64_t gsz, int64_t k, int64_t n_valid,
                 int32_t* counts, hipStream_t s) {
     constexpr int kBits = int(sizeof(W)) * 8;
+    const size_t count_bytes = NB <= 16 ? 2 : 4;
     const int kb = int(std::min<int64_t>(k, kGbsMaxClasses));
     // Keep the LDS tile within 64 KiB (the default dynamic-LDS limit of a workgroup).
-    const int lds_cols = int(65536 / ((kBits * kb + 1) * sizeof(int32_t)));
+    const int lds_cols = int(65536 / ((kBits * kb + 1) * count_bytes));
     const int cols = std::min(kGbsThreads / kb, lds_cols);
-    const size_t lds = size_t(cols) * (kBits * kb + 1) * sizeof(int32_t);
+    const size_t lds = (size_t(cols) * (kBits * kb + 1) * count_bytes + 15) / 16 * 16;
     const dim3 grid(unsigned(ceil_div(words, cols)), unsigned(ceil_div(k, kb)), 1);
     k_group_bit_sum<W, NB><<<grid, kGbsThreads, lds, s>>>(x, words, gsz, k, n_valid, cols, kb,
                                                          counts);
@@ -310,7 +319,7 @@ extern "C" int cl_dense_eval_packed(const void* x, const int64_t* a, const int64
     const int G = int(num_gates);
     const unsigned gx = unsigned(ceil_div(out_dim, 4));
     if (row_bytes % 16 == 0 && aligned(x, 16) && aligned(y, 16)) {
-        constexpr int VEC = 2, U = 8;
+        constexpr int VEC = 2, U = kPackedUnroll;
         const int64_t words = row_bytes / 8;
         const dim3 grid(gx, unsigned(ceil_div(words, 64 * VEC * U)), 1);
         k_eval_packed<uint64_t, VEC, U><<<grid, 256, 0, s>>>(

@@ -9,6 +9,8 @@ that is not on a HIP device is rejected, never computed on the CPU.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -115,27 +117,29 @@ class LogicLayerRunsFunction(torch.autograd.Function):
             raise RuntimeError(f"x has {x.shape[0]} rows, the layer expects {plan.in_dim}")
         batch = x.shape[1]
         y = torch.empty((plan.out_dim, batch), dtype=x.dtype, device=x.device)
+        coef = torch.empty((plan.num_runs, 4), dtype=x.dtype, device=x.device)
         w = w.contiguous()
         with torch.cuda.device(x.device):
             _capi.call("cl_dense_forward_runs", _dl.dtype_code(x), x.data_ptr(), w.data_ptr(),
                        gate_sequence.data_ptr(), plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
-                       plan.run_gl.data_ptr(), y.data_ptr(), plan.in_dim, plan.out_dim,
-                       plan.num_runs, batch, plan.num_gates, _dl.stream_of(x))
-        ctx.save_for_backward(x, w, gate_sequence)
+                       plan.run_gl.data_ptr(), y.data_ptr(), coef.data_ptr(), plan.in_dim,
+                       plan.out_dim, plan.num_runs, batch, plan.num_gates, _dl.stream_of(x))
+        ctx.save_for_backward(x, coef, gate_sequence)
         ctx.plan = plan
         return y
 
     @staticmethod
     def backward(ctx, grad_y):
-        x, w, gate_sequence = ctx.saved_tensors
+        x, coef, gate_sequence = ctx.saved_tensors
         plan: RunPlan = ctx.plan
         grad_y = grad_y.contiguous()
         grad_x = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        grad_w = torch.empty_like(w) if ctx.needs_input_grad[1] else None
+        grad_w = (torch.empty((plan.out_dim, plan.num_gates), dtype=x.dtype, device=x.device)
+                  if ctx.needs_input_grad[1] else None)
         if grad_x is not None or grad_w is not None:
             with torch.cuda.device(x.device):
                 _capi.call("cl_dense_backward_runs", _dl.dtype_code(x), x.data_ptr(),
-                           w.data_ptr(), gate_sequence.data_ptr(), grad_y.data_ptr(),
+                           coef.data_ptr(), gate_sequence.data_ptr(), grad_y.data_ptr(),
                            plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
                            plan.run_gl.data_ptr(), plan.run_y.data_ptr(),
                            plan.inv_ptr.data_ptr(), plan.inv_entry.data_ptr(),
@@ -161,9 +165,14 @@ class GroupSumFunction(torch.autograd.Function):
             x = x.contiguous()
             sb, sf = x.stride()
         out = torch.empty((batch, k), dtype=x.dtype, device=x.device)
+        need = ctypes.c_int64(0)
+        _capi.call("cl_group_sum_workspace_size", _dl.dtype_code(x), batch, feats, sb, sf, k,
+                   ctypes.byref(need))
+        ws = torch.empty(need.value, dtype=torch.uint8, device=x.device) if need.value else None
         with torch.cuda.device(x.device):
             _capi.call("cl_group_sum_forward", _dl.dtype_code(x), x.data_ptr(), batch, feats,
-                       sb, sf, k, float(tau), out.data_ptr(), _dl.stream_of(x))
+                       sb, sf, k, float(tau), out.data_ptr(), _dl.ptr(ws), need.value,
+                       _dl.stream_of(x))
         ctx.k, ctx.tau = k, tau
         ctx.shape = (batch, feats)
         ctx.batch_major = sb == 1 and sf != 1

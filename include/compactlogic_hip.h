@@ -101,20 +101,29 @@ int cl_dense_eval(int dtype, const void* x, const int64_t* a, const int64_t* b,
  *   inv_entry int32 [2 * num_runs] ... entries 2*r + side (side 0: operand a, 1: operand b)
  * ----------------------------------------------------------------------------------------- */
 
+/* Forward through the plan.  When run_coef (T [num_runs, 4]) is not NULL the collapsed
+ * coefficients K of every run are also written there, for cl_dense_backward_runs. */
 int cl_dense_forward_runs(int dtype, const void* x, const void* w, const uint8_t* gate_seq,
                           const int32_t* run_ptr, const int32_t* run_ab, const int32_t* run_gl,
-                          void* y, int64_t in_dim, int64_t out_dim, int64_t num_runs,
-                          int64_t batch, int64_t num_gates, void* stream);
+                          void* y, void* run_coef, int64_t in_dim, int64_t out_dim,
+                          int64_t num_runs, int64_t batch, int64_t num_gates, void* stream);
 
-/* Backward through the plan.  grad_x and/or grad_w may be NULL when not needed.  When both
- * are requested the two are produced by one pass over the inverse index (the weight moments
- * of each run are taken at its operand-a entry). */
-int cl_dense_backward_runs(int dtype, const void* x, const void* w, const uint8_t* gate_seq,
-                           const void* grad_y, const int32_t* run_ptr, const int32_t* run_ab,
-                           const int32_t* run_gl, const int32_t* run_y, const int32_t* inv_ptr,
-                           const int32_t* inv_entry, void* grad_x, void* grad_w, int64_t in_dim,
-                           int64_t out_dim, int64_t num_runs, int64_t batch, int64_t num_gates,
-                           void* stream);
+/* The run coefficients K alone: run_coef[r] = sum_{g in run r} w[o, g] * (c0, c1, c2, c3). */
+int cl_dense_run_coefs(int dtype, const void* w, const uint8_t* gate_seq, const int32_t* run_ptr,
+                       const int32_t* run_gl, void* run_coef, int64_t out_dim, int64_t num_runs,
+                       int64_t num_gates, void* stream);
+
+/* Backward through the plan, from the run coefficients of the forward pass.  grad_x and/or
+ * grad_w may be NULL when not needed (run_coef, run_y and the inverse index are only read
+ * for grad_x).  When both are requested they come from one pass over the inverse index (the
+ * weight moments of each run are taken at its operand-a entry).  grad_w is the gradient with
+ * respect to w (the probabilities). */
+int cl_dense_backward_runs(int dtype, const void* x, const void* run_coef,
+                           const uint8_t* gate_seq, const void* grad_y, const int32_t* run_ptr,
+                           const int32_t* run_ab, const int32_t* run_gl, const int32_t* run_y,
+                           const int32_t* inv_ptr, const int32_t* inv_entry, void* grad_x,
+                           void* grad_w, int64_t in_dim, int64_t out_dim, int64_t num_runs,
+                           int64_t batch, int64_t num_gates, void* stream);
 
 /* -------------------------------------------------------------------------------------------
  * GroupSum -- compactlogic/compactlogic.py:450-468: out[n, c] = sum_{j in group c} x[n, j] / tau
@@ -125,7 +134,13 @@ int cl_dense_backward_runs(int dtype, const void* x, const void* w, const uint8_
  * ----------------------------------------------------------------------------------------- */
 int cl_group_sum_forward(int dtype, const void* x, int64_t batch, int64_t features,
                          int64_t stride_batch, int64_t stride_feature, int64_t k, double tau,
-                         void* out, void* stream);
+                         void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace (device bytes) that lets cl_group_sum_forward split every group over several
+ * workgroups; *bytes = 0 when the layout does not use one.  With a smaller or NULL workspace
+ * the forward still runs, with one workgroup per (batch tile, class). */
+int cl_group_sum_workspace_size(int dtype, int64_t batch, int64_t features, int64_t stride_batch,
+                                int64_t stride_feature, int64_t k, int64_t* bytes);
 
 /* grad_x[n, j] = grad_out[n, group(j)] / tau, written through (stride_batch, stride_feature). */
 int cl_group_sum_backward(int dtype, const void* grad_out, int64_t batch, int64_t features,
