@@ -41,6 +41,7 @@ def parse():
     p.add_argument("--no-packed", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--kernel-reps", type=int, default=20)
+    p.add_argument("--kernel-steps", type=int, default=5)
     return p.parse_args()
 
 
@@ -103,91 +104,38 @@ def bench_dense(args, torch):
     step()
     torch.cuda.synchronize()
     matches = all(torch.equal(p.grad, g) for p, g in zip(model.parameters(), grads_run))
-    kernels = time_dense_kernels(model, x, args.kernel_reps, torch)
+    kernels = time_dense_kernels(model, step, cfg.batch, args.kernel_steps, torch)
     return cfg, samples_s, dt, kernels, matches
 
 
-def time_dense_kernels(model, x, reps, torch):
-    """Average duration of each dense kernel at its cfg2 shape, timed with HIP events on the
-    current stream (the stream the kernels are launched on)."""
-    import compactlogic_amd as cl
-    from compactlogic_amd import _capi
-    from compactlogic_amd import difflogic_hip as dl
-    layers = [m for m in model if isinstance(m, cl.LogicLayer)]
-    acts, h = [], x
-    with torch.no_grad():
-        for layer in layers:
-            xt = h.t().contiguous()
-            acts.append(xt)
-            w = torch.softmax(layer.weights, -1)
-            h = cl.LogicLayerRunsFunction.apply(xt, w, layer.gate_sequence, layer.run_plan()).t()
-    batch = x.shape[0]
-    stream = torch.cuda.current_stream()
+# Algorithmic bytes per launch (activations read once + written once, fp32): forward reads x
+# and writes y; the fused backward reads x and grad_y and writes grad_x; the weight gradient
+# alone reads x and grad_y.  Parameters, indices and partial moments are not counted.
+def algorithmic_bytes(name: str, batch: int) -> int | None:
+    import re
+    m = re.match(r"(cl_[a-z_]+)\[(\d+)->(\d+)\]", name)
+    if not m:
+        return None
+    kind, i, o = m.group(1), int(m.group(2)), int(m.group(3))
+    x, y = 4 * i * batch, 4 * o * batch
+    return {"cl_dense_forward_tiled": x + y, "cl_dense_backward_tiled": 2 * x + y,
+            "cl_dense_weight_grad": x + y}.get(kind)
 
-    def timed(fn):
-        fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(reps):
-            fn()
-        end.record(stream)
-        end.synchronize()
-        return start.elapsed_time(end) / reps * 1e-3   # seconds per launch
 
+def time_dense_kernels(model, step, batch, nsteps, torch):
+    """Mean duration of every library call inside `nsteps` real (eager) training steps,
+    bracketed with HIP events on the stream each call uses."""
+    from compactlogic_amd import timing
+    with timing.record() as rec:
+        for _ in range(nsteps):
+            model.zero_grad(set_to_none=True)
+            step()
     out = {}
-    # a middle layer (12000 -> 12000) and the first layer (784 -> 12000)
-    for tag, li in (("L2", 1), ("L1", 0)):
-        layer, xt = layers[li], acts[li]
-        plan = layer.run_plan()
-        w = torch.softmax(layer.weights, -1).contiguous()
-        y = torch.empty((plan.out_dim, batch), device=xt.device)
-        coef = torch.empty((plan.num_runs, 4), device=xt.device)
-        gy = torch.randn_like(y) / batch
-        gx = torch.empty_like(xt)
-        gw = torch.empty_like(w)
-        s = stream.cuda_stream
-        fwd = lambda: _capi.call("cl_dense_forward_runs", 0, xt.data_ptr(), w.data_ptr(),
-                                 layer.gate_sequence.data_ptr(), plan.run_ptr.data_ptr(),
-                                 plan.run_ab.data_ptr(), plan.run_gl.data_ptr(), y.data_ptr(),
-                                 coef.data_ptr(), plan.in_dim, plan.out_dim, plan.num_runs, batch,
-                                 plan.num_gates, s)
-        want_gx = li > 0
-        bwd = lambda: _capi.call("cl_dense_backward_runs", 0, xt.data_ptr(), coef.data_ptr(),
-                                 layer.gate_sequence.data_ptr(), gy.data_ptr(),
-                                 plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
-                                 plan.run_gl.data_ptr(), plan.run_y.data_ptr(),
-                                 plan.inv_ptr.data_ptr(), plan.inv_entry.data_ptr(),
-                                 gx.data_ptr() if want_gx else None, gw.data_ptr(), plan.in_dim,
-                                 plan.out_dim, plan.num_runs, batch, plan.num_gates, s)
-        t_f, t_b = timed(fwd), timed(bwd)
-        in_b, out_b = plan.in_dim * batch * 4, plan.out_dim * batch * 4
-        out[f"{tag}_forward"] = dict(kernel="k_dense_forward_runs", seconds=t_f,
-                                     algorithmic_bytes=in_b + out_b)
-        out[f"{tag}_backward"] = dict(
-            kernel="k_dense_backward_runs" if want_gx else "k_dense_backward_w_runs", seconds=t_b,
-            algorithmic_bytes=(2 * in_b + out_b) if want_gx else (in_b + out_b))
-    # GroupSum over the last layer's [12000, batch] output
-    import ctypes
-    ylast = torch.rand((layers[-1].out_dim, batch), device=x.device)
-    head = torch.empty((batch, 10), device=x.device)
-    need = ctypes.c_int64(0)
-    _capi.call("cl_group_sum_workspace_size", 0, batch, ylast.shape[0], 1, batch, 10,
-               ctypes.byref(need))
-    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
-    gsf = lambda: _capi.call("cl_group_sum_forward", 0, ylast.data_ptr(), batch, ylast.shape[0],
-                             1, batch, 10, 10.0, head.data_ptr(), ws.data_ptr(), need.value,
-                             stream.cuda_stream)
-    out["groupsum_forward"] = dict(kernel="k_gsum_partial+k_gsum_finish", seconds=timed(gsf),
-                                   algorithmic_bytes=ylast.numel() * 4 + head.numel() * 4)
-    gx_head = torch.empty_like(ylast)
-    ghead = torch.randn_like(head)
-    gsb = lambda: _capi.call("cl_group_sum_backward", 0, ghead.data_ptr(), batch, ylast.shape[0],
-                             10, 10.0, gx_head.data_ptr(), 1, batch, stream.cuda_stream)
-    out["groupsum_backward"] = dict(kernel="k_gsum_bwd", seconds=timed(gsb),
-                                    algorithmic_bytes=gx_head.numel() * 4 + ghead.numel() * 4)
-    for v in out.values():
-        v["achieved_GBs"] = v["algorithmic_bytes"] / v["seconds"] / 1e9
+    for name, v in rec.summary().items():
+        sec = v["mean_ms"] * 1e-3
+        nbytes = algorithmic_bytes(name, batch)
+        out[name] = dict(seconds=sec, calls=v["calls"], algorithmic_bytes=nbytes,
+                         achieved_GBs=(nbytes / sec / 1e9) if nbytes else None)
     return out
 
 
@@ -338,13 +286,17 @@ def main():
     log(f"dense cfg2: mode={args.mode} warmup={args.warmup} steps={args.steps}")
     cfg, samples_s, dt, kernels, matches = bench_dense(args, torch)
     log(f"dense cfg2: {samples_s:,.0f} samples/s, {dt * 1e3:.3f} ms/step")
-    dom_name = max((k for k in kernels if k.startswith("L2")), key=lambda k: kernels[k]["seconds"])
+    # dominant kernel: the library call with the largest total time per step
+    dom_name = max((k for k in kernels if kernels[k]["algorithmic_bytes"]),
+                   key=lambda k: kernels[k]["seconds"] * kernels[k]["calls"])
     dom = kernels[dom_name]
     roofline = {"bound": "hbm", "achieved": round(dom["achieved_GBs"], 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(dom["achieved_GBs"] / HBM_PEAK_GBS, 4),
-                "traffic": None, "kernel": dom["kernel"],
+                "traffic": None, "kernel": dom_name,
                 "per_launch_ms": round(dom["seconds"] * 1e3, 4),
-                "algorithmic_bytes_per_launch": dom["algorithmic_bytes"]}
+                "algorithmic_bytes_per_launch": dom["algorithmic_bytes"],
+                "measured": f"HIP events around each launch inside {args.kernel_steps} eager "
+                            "training steps run right after the timed region"}
     step_bytes = CFG2_BYTES_PER_SAMPLE * cfg.batch
     result = {
         "metric": "train samples/s (fwd+bwd) & packed eval Gsamples/s; % of HBM peak",
@@ -365,7 +317,8 @@ def main():
         "step_hbm_frac": round(step_bytes / dt / 1e9 / HBM_PEAK_GBS, 4),
         "timed_path_matches_eager": matches,
         "roofline": roofline,
-        "kernels": {k: {"ms": round(v["seconds"] * 1e3, 4), "GB/s": round(v["achieved_GBs"], 1)}
+        "kernels": {k: {"ms": round(v["seconds"] * 1e3, 4), "calls_per_step": v["calls"] // args.kernel_steps,
+                        "GB/s": round(v["achieved_GBs"], 1) if v["achieved_GBs"] else None}
                     for k, v in kernels.items()},
     }
     if not args.no_cpu_baseline:

@@ -38,11 +38,14 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_backward_x": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64,
                             _i64, _i64, _p],
     "cl_dense_eval": [_int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
-    "cl_dense_forward_runs": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
-                              _i64, _p],
-    "cl_dense_run_coefs": [_int, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
-    "cl_dense_backward_runs": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
-                               _i64, _i64, _i64, _p],
+    "cl_dense_prep": [_int, _p, _int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "cl_dense_forward_tiled": [_int, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "cl_dense_weight_grad": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                             _p],
+    "cl_dense_tiled_chunks": [_int, _i64, _i64, _i64, ctypes.POINTER(_i64)],
+    "cl_dense_backward_tiled": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                                _i64, _i64, _p],
+    "cl_dense_backward_finalize": [_int, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_group_sum_forward": [_int, _p, _i64, _i64, _i64, _i64, _i64, _f64, _p, _p, _i64, _p],
     "cl_group_sum_workspace_size": [_int, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
     "cl_group_sum_backward": [_int, _p, _i64, _i64, _i64, _f64, _p, _i64, _i64, _p],

@@ -137,9 +137,9 @@ __device__ __forceinline__ T read_lane(T v, int lane) {
 }
 
 // Sum over all 64 lanes, returned as a wave-uniform (scalar) value.  Each 16-lane row is
-// reduced with DPP (quad swaps 1 and 2, then row rotations by 4 and 8, after which every
-// lane of a row holds the row total), and the four row totals are added in lane order, so
-// the result does not depend on scheduling.
+// reduced with DPP (quad swaps 1 and 2, then row rotations by 4 and 8; a full-row rotation
+// sum leaves the row total in every lane whatever the rotation direction), and the four row
+// totals are added in lane order, so the result does not depend on scheduling.
 template <typename T>
 __device__ __forceinline__ T wave_total(T v) {
     v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]

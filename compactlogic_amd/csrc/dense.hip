@@ -13,8 +13,9 @@
 // coefficient, so consecutive slots that share an input pair collapse into one set of four
 // coefficients (K = sum_g w_g * c[s_g]).  Each such run then costs two row gathers instead
 // of two per slot, and its weight gradient follows from four batch moments
-// (sum gy, sum gy*a, sum gy*b, sum gy*a*b).  The entry points over the reference's int64
-// indices detect runs on the fly; the *_runs entry points take them from a prebuilt plan.
+// (sum gy, sum gy*a, sum gy*b, sum gy*a*b).  These entry points take the reference's int64
+// indices and detect runs on the fly; the module's training path (dense_tiled.hip) takes
+// them from a prebuilt plan.
 #include "common.h"
 
 #include <algorithm>
@@ -50,16 +51,6 @@ __device__ __forceinline__ Coef4<T> run_coef(const T* __restrict__ wrow,
     k.c1 = wave_total(p1);
     k.c2 = wave_total(p2);
     k.c3 = wave_total(p3);
-    return k;
-}
-
-template <typename T>
-__device__ __forceinline__ Coef4<T> load_coef(const T* __restrict__ kc, int64_t r) {
-    Coef4<T> k;
-    k.c0 = kc[4 * r + 0];
-    k.c1 = kc[4 * r + 1];
-    k.c2 = kc[4 * r + 2];
-    k.c3 = kc[4 * r + 3];
     return k;
 }
 
@@ -138,79 +129,6 @@ __global__ __launch_bounds__(256) void k_dense_forward(const T* __restrict__ x,
     store_rows<T, VEC, U>(y + o * B, acc, b0, B, bad);
 }
 
-// Forward through a run plan.  The run coefficients are also written to `kc` (4 per run)
-// when it is given, for the backward pass to reuse.
-template <typename T, int VEC, int U>
-__global__ __launch_bounds__(256) void k_dense_forward_runs(
-    const T* __restrict__ x, const T* __restrict__ w, const uint8_t* __restrict__ gs,
-    const int32_t* __restrict__ run_ptr, const int2* __restrict__ run_ab,
-    const int32_t* __restrict__ run_gl, T* __restrict__ y, T* __restrict__ kc, int64_t in_dim,
-    int64_t out_dim, int64_t num_runs, int64_t B, int G) {
-    const int64_t o = int64_t(blockIdx.x) * kWaves + wave_id();
-    if (o >= out_dim) return;
-    const int64_t b0 = int64_t(blockIdx.y) * (kWave * VEC * U) + int64_t(lane_id()) * VEC;
-    const T* wrow = w + o * G;
-    const uint8_t* grow = gs + o * G;
-
-    Vec<T, VEC> acc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[u].v[i] = T(0);
-
-    bool bad = false;
-    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
-    if (r0 < 0 || r1 < r0 || r1 > num_runs) {
-        bad = true;
-        r1 = r0;
-    }
-    for (int64_t r = r0; r < r1; ++r) {
-        const int2 ab = run_ab[r];
-        const int gl = run_gl[r];
-        const int g0 = gl & 0xff, len = gl >> 8;
-        if (uint32_t(ab.x) >= uint64_t(in_dim) || uint32_t(ab.y) >= uint64_t(in_dim) ||
-            g0 + len > G) {
-            bad = true;
-            continue;
-        }
-        const Coef4<T> k = run_coef(wrow, grow, g0, len);
-        if (kc != nullptr && blockIdx.y == 0 && lane_id() == 0) {
-            kc[4 * r + 0] = k.c0;
-            kc[4 * r + 1] = k.c1;
-            kc[4 * r + 2] = k.c2;
-            kc[4 * r + 3] = k.c3;
-        }
-        accum_run<T, VEC, U>(acc, x + int64_t(ab.x) * B, x + int64_t(ab.y) * B, k, b0, B);
-    }
-    store_rows<T, VEC, U>(y + o * B, acc, b0, B, bad);
-}
-
-// Run coefficients only (for a backward pass without a preceding forward).
-template <typename T>
-__global__ __launch_bounds__(256) void k_dense_run_coefs(const T* __restrict__ w,
-                                                         const uint8_t* __restrict__ gs,
-                                                         const int32_t* __restrict__ run_ptr,
-                                                         const int32_t* __restrict__ run_gl,
-                                                         T* __restrict__ kc, int64_t out_dim,
-                                                         int64_t num_runs, int G) {
-    const int64_t o = int64_t(blockIdx.x) * kWaves + wave_id();
-    if (o >= out_dim) return;
-    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
-    if (r0 < 0 || r1 < r0 || r1 > num_runs) return;
-    for (int64_t r = r0; r < r1; ++r) {
-        const int gl = run_gl[r];
-        const int g0 = gl & 0xff, len = gl >> 8;
-        Coef4<T> k{qnan<T>(), qnan<T>(), qnan<T>(), qnan<T>()};
-        if (g0 + len <= G) k = run_coef(w + o * G, gs + o * G, g0, len);
-        if (lane_id() == 0) {
-            kc[4 * r + 0] = k.c0;
-            kc[4 * r + 1] = k.c1;
-            kc[4 * r + 2] = k.c2;
-            kc[4 * r + 3] = k.c3;
-        }
-    }
-}
-
 // ------------------------------------------------------------------------------------------
 // Batch moments of one run: S1 = sum gy, Sa = sum gy*a, Sb = sum gy*b, Sab = sum gy*a*b over
 // the whole batch, reduced across the wave (every lane returns the totals).
@@ -280,35 +198,6 @@ __global__ __launch_bounds__(256) void k_dense_backward_w(const T* __restrict__ 
     }
 }
 
-// Weight gradient through a run plan: one wave per neuron, whole batch.
-template <typename T, int VEC>
-__global__ __launch_bounds__(256) void k_dense_backward_w_runs(
-    const T* __restrict__ x, const uint8_t* __restrict__ gs, const T* __restrict__ gy,
-    const int32_t* __restrict__ run_ptr, const int2* __restrict__ run_ab,
-    const int32_t* __restrict__ run_gl, T* __restrict__ gw, int64_t in_dim, int64_t out_dim,
-    int64_t num_runs, int64_t B, int G) {
-    const int64_t o = int64_t(blockIdx.x) * kWaves + wave_id();
-    if (o >= out_dim) return;
-    const uint8_t* grow = gs + o * G;
-    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
-    if (r0 < 0 || r1 < r0 || r1 > num_runs) {
-        // Corrupt plan: poison the whole row.
-        for (int g = lane_id(); g < G; g += kWave) gw[o * G + g] = qnan<T>();
-        return;
-    }
-    for (int64_t r = r0; r < r1; ++r) {
-        const int2 ab = run_ab[r];
-        const int gl = run_gl[r];
-        const int g0 = gl & 0xff, len = gl >> 8;
-        if (g0 + len > G) continue;
-        const bool bad = uint32_t(ab.x) >= uint64_t(in_dim) || uint32_t(ab.y) >= uint64_t(in_dim);
-        Coef4<T> m{T(0), T(0), T(0), T(0)};
-        if (!bad)
-            m = run_moments<T, VEC>(gy + o * B, x + int64_t(ab.x) * B, x + int64_t(ab.y) * B, B);
-        write_run_grad_w<T>(gw + o * G, grow, g0, len, m, bad);
-    }
-}
-
 // ------------------------------------------------------------------------------------------
 // Input gradient through the reference's inverse index: one wave per input row i over a batch
 // chunk; every entry is one (neuron, slot, operand side) use of x_i.
@@ -371,171 +260,6 @@ __global__ __launch_bounds__(256) void k_dense_backward_x(
     store_rows<T, VEC, U>(gx + i * B, acc, b0, B, bad);
 }
 
-// Input gradient (and, with WANT_GW, the weight gradient) through the run plan's inverse
-// index, reading the run coefficients K written by the forward pass.
-//
-// WPR waves share one input row and split its batch (WPR = 1: four rows per workgroup).
-// With WANT_GW the workgroup covers the whole batch (gridDim.y == 1): the weight moments of
-// run r are reduced at its operand-a entry, which lives in exactly one row, so every weight
-// gradient is written exactly once and no atomics are needed.  With WPR > 1 the per-wave
-// partial moments meet in LDS and are added in wave order.
-constexpr int kPendingRuns = 16;
-
-template <typename T, int VEC, int U, int WPR, bool WANT_GX, bool WANT_GW>
-__global__ __launch_bounds__(256) void k_dense_backward_runs(
-    const T* __restrict__ x, const T* __restrict__ kc, const uint8_t* __restrict__ gs,
-    const T* __restrict__ gy, const int2* __restrict__ run_ab, const int32_t* __restrict__ run_gl,
-    const int32_t* __restrict__ run_y, const int32_t* __restrict__ inv_ptr,
-    const int32_t* __restrict__ inv_entry, T* __restrict__ gx, T* __restrict__ gw, int64_t in_dim,
-    int64_t out_dim, int64_t num_runs, int64_t B, int G) {
-    static_assert(kWaves % WPR == 0, "waves per row must divide the workgroup");
-    constexpr int kRowsPerBlock = kWaves / WPR;
-    constexpr bool kShared = WANT_GW && WPR > 1;
-    __shared__ T mom[kShared ? kPendingRuns : 1][WPR][4];
-    __shared__ int pend[kShared ? kPendingRuns : 1][2];
-
-    const int wave = wave_id();
-    const int part = wave % WPR;
-    const int64_t i = int64_t(blockIdx.x) * kRowsPerBlock + wave / WPR;
-    if (i >= in_dim) return;  // uniform across the workgroup when WPR == kWaves
-    // batch element of unroll step u: ((u * WPR + part) * 64 + lane) * VEC, within chunk y
-    const int64_t chunk0 = int64_t(blockIdx.y) * (int64_t(WPR) * kWave * VEC * U);
-    auto elem = [&](int u) -> int64_t {
-        return chunk0 + (int64_t(u) * WPR + part) * (kWave * VEC) + int64_t(lane_id()) * VEC;
-    };
-    const T* xi = x + i * B;
-
-    Vec<T, VEC> acc[U];
-    Vec<T, VEC> self[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-            acc[u].v[v] = T(0);
-            self[u].v[v] = T(0);
-        }
-        if (WANT_GW) {
-            const int64_t idx = elem(u);
-            if (idx < B) self[u] = vload<T, VEC>(xi + idx);
-        }
-    }
-
-    int npend = 0;
-    auto flush = [&](int n) {
-        for (int j = wave; j < n; j += kWaves) {
-            Coef4<T> m;
-            m.c0 = mom[j][0][0];
-            m.c1 = mom[j][0][1];
-            m.c2 = mom[j][0][2];
-            m.c3 = mom[j][0][3];
-            for (int q = 1; q < WPR; ++q) {
-                m.c0 += mom[j][q][0];
-                m.c1 += mom[j][q][1];
-                m.c2 += mom[j][q][2];
-                m.c3 += mom[j][q][3];
-            }
-            const int64_t yo = pend[j][0];
-            const int gl = pend[j][1];
-            write_run_grad_w<T>(gw + yo * G, gs + yo * G, gl & 0xff, gl >> 8, m, false);
-        }
-    };
-
-    bool bad = false;
-    int64_t e0 = inv_ptr[i], e1 = inv_ptr[i + 1];
-    if (e0 < 0 || e1 < e0 || e1 > 2 * num_runs) {
-        bad = true;
-        e1 = e0;
-    }
-    for (int64_t e = e0; e < e1; ++e) {
-        const int ent = inv_entry[e];
-        const int64_t r = ent >> 1;
-        const int side = ent & 1;
-        if (r >= num_runs || ent < 0) {
-            bad = true;
-            continue;
-        }
-        const int64_t yo = run_y[r];
-        const int2 ab = run_ab[r];
-        const int gl = run_gl[r];
-        const int64_t other = side ? ab.x : ab.y;
-        if (uint64_t(yo) >= uint64_t(out_dim) || uint64_t(other) >= uint64_t(in_dim) ||
-            (gl & 0xff) + (gl >> 8) > G) {
-            bad = true;
-            continue;
-        }
-        const Coef4<T> k = load_coef(kc, r);
-        const T kself = side ? k.c2 : k.c1;
-        const T* xo = x + other * B;
-        const T* gyr = gy + yo * B;
-        const bool moments = WANT_GW && side == 0;
-        T s1 = 0, sa = 0, sb = 0, sab = 0;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t idx = elem(u);
-            if (idx < B) {
-                const Vec<T, VEC> vo = vload<T, VEC>(xo + idx);
-                const Vec<T, VEC> vg = vload<T, VEC>(gyr + idx);
-#pragma unroll
-                for (int v = 0; v < VEC; ++v) {
-                    if (WANT_GX) acc[u].v[v] = fma(fma(k.c3, vo.v[v], kself), vg.v[v], acc[u].v[v]);
-                    if (moments) {
-                        const T ga = vg.v[v] * self[u].v[v];
-                        s1 += vg.v[v];
-                        sa += ga;
-                        sb = fma(vg.v[v], vo.v[v], sb);
-                        sab = fma(ga, vo.v[v], sab);
-                    }
-                }
-            }
-        }
-        if (moments) {
-            Coef4<T> m;
-            m.c0 = wave_total(s1);
-            m.c1 = wave_total(sa);
-            m.c2 = wave_total(sb);
-            m.c3 = wave_total(sab);
-            if constexpr (kShared) {
-                if (lane_id() == 0) {
-                    mom[npend][part][0] = m.c0;
-                    mom[npend][part][1] = m.c1;
-                    mom[npend][part][2] = m.c2;
-                    mom[npend][part][3] = m.c3;
-                    if (part == 0) {
-                        pend[npend][0] = int(yo);
-                        pend[npend][1] = gl;
-                    }
-                }
-                if (++npend == kPendingRuns) {
-                    __syncthreads();
-                    flush(npend);
-                    __syncthreads();
-                    npend = 0;
-                }
-            } else {
-                write_run_grad_w<T>(gw + yo * G, gs + yo * G, gl & 0xff, gl >> 8, m, false);
-            }
-        }
-    }
-    if constexpr (kShared) {
-        __syncthreads();
-        flush(npend);
-    }
-    if (WANT_GX) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t idx = elem(u);
-            if (idx < B) {
-                Vec<T, VEC> r = acc[u];
-                if (bad) {
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) r.v[v] = qnan<T>();
-                }
-                vstore<T, VEC>(gx + i * B + idx, r);
-            }
-        }
-    }
-}
-
 // Discrete forward with the argmax slot, relaxed formula (exact on {0, 1} inputs).
 template <typename T, int VEC, int U>
 __global__ __launch_bounds__(256) void k_dense_eval(const T* __restrict__ x,
@@ -581,15 +305,6 @@ int pick_vec(int64_t B, std::initializer_list<const void*> ptrs) {
 }
 
 constexpr int kChunkUnroll = 4;
-#ifndef CL_FWD_UNROLL
-#define CL_FWD_UNROLL 2
-#endif
-#ifndef CL_FUSED_WPR
-#define CL_FUSED_WPR 4
-#endif
-constexpr int kFwdUnroll = CL_FWD_UNROLL;      // 16-byte vectors per lane in the plan forward
-constexpr int kFusedWpr = CL_FUSED_WPR;        // waves sharing one row in the fused backward
-constexpr int kFusedMaxUnroll = 8;
 
 inline dim3 rows_grid(int64_t rows, int64_t B, int vec, int unroll) {
     const int64_t chunk = int64_t(kWave) * vec * unroll;
@@ -634,67 +349,6 @@ extern "C" int cl_dense_forward(int dtype, const void* x, const int64_t* a, cons
                 xs, a, b, ws, gate_seq, ys, in_dim, out_dim, batch, int(num_gates));
     });
     return check_launch("cl_dense_forward");
-}
-
-extern "C" int cl_dense_forward_runs(int dtype, const void* x, const void* w,
-                                     const uint8_t* gate_seq, const int32_t* run_ptr,
-                                     const int32_t* run_ab, const int32_t* run_gl, void* y,
-                                     void* run_coef, int64_t in_dim, int64_t out_dim,
-                                     int64_t num_runs, int64_t batch, int64_t num_gates,
-                                     void* stream) {
-    clear_error();
-    if (int rc = check_dims(in_dim, out_dim, batch, num_gates)) return rc;
-    if (out_dim == 0) return CL_OK;
-    CL_ARG(in_dim > 0, "in_dim is 0 but out_dim > 0");
-    CL_ARG(w && gate_seq && run_ptr && run_ab && run_gl, "null pointer argument");
-    CL_ARG(batch == 0 || (x && y), "null pointer argument");
-    CL_ARG(aligned(run_ab, 8), "run_ab must be 8-byte aligned");
-    const int64_t b_launch = std::max<int64_t>(batch, 1);  // batch 0 still fills run_coef
-    CL_DTYPE_SWITCH(dtype, {
-        using T = scalar_t;
-        constexpr int W = wide_vec<T>();
-        const int vec = pick_vec<T>(batch, {x, y});
-        auto* xs = static_cast<const T*>(x);
-        auto* ws = static_cast<const T*>(w);
-        auto* ys = static_cast<T*>(y);
-        auto* kc = static_cast<T*>(run_coef);
-        auto* ab = reinterpret_cast<const int2*>(run_ab);
-        hipStream_t s = as_stream(stream);
-        if (batch == 0) {
-            if (kc)
-                k_dense_run_coefs<T><<<dim3(unsigned(ceil_div(out_dim, kWaves))), 256, 0, s>>>(
-                    ws, gate_seq, run_ptr, run_gl, kc, out_dim, num_runs, int(num_gates));
-        } else if (vec == W) {
-            const dim3 grid = rows_grid(out_dim, b_launch, W, kFwdUnroll);
-            k_dense_forward_runs<T, W, kFwdUnroll><<<grid, 256, 0, s>>>(
-                xs, ws, gate_seq, run_ptr, ab, run_gl, ys, kc, in_dim, out_dim, num_runs, batch,
-                int(num_gates));
-        } else {
-            const dim3 grid = rows_grid(out_dim, b_launch, 1, kChunkUnroll);
-            k_dense_forward_runs<T, 1, kChunkUnroll><<<grid, 256, 0, s>>>(
-                xs, ws, gate_seq, run_ptr, ab, run_gl, ys, kc, in_dim, out_dim, num_runs, batch,
-                int(num_gates));
-        }
-    });
-    return check_launch("cl_dense_forward_runs");
-}
-
-extern "C" int cl_dense_run_coefs(int dtype, const void* w, const uint8_t* gate_seq,
-                                  const int32_t* run_ptr, const int32_t* run_gl, void* run_coef,
-                                  int64_t out_dim, int64_t num_runs, int64_t num_gates,
-                                  void* stream) {
-    clear_error();
-    CL_ARG(out_dim >= 0 && num_runs >= 0, "negative shape");
-    CL_ARG(num_gates >= 1 && num_gates <= 128, "num_gates must be in [1, 128]");
-    if (out_dim == 0) return CL_OK;
-    CL_ARG(w && gate_seq && run_ptr && run_gl && run_coef, "null pointer argument");
-    CL_DTYPE_SWITCH(dtype, {
-        k_dense_run_coefs<scalar_t><<<dim3(unsigned(ceil_div(out_dim, kWaves))), 256, 0,
-                                      as_stream(stream)>>>(
-            static_cast<const scalar_t*>(w), gate_seq, run_ptr, run_gl,
-            static_cast<scalar_t*>(run_coef), out_dim, num_runs, int(num_gates));
-    });
-    return check_launch("cl_dense_run_coefs");
 }
 
 extern "C" int cl_dense_backward_w(int dtype, const void* x, const int64_t* a, const int64_t* b,
@@ -755,108 +409,6 @@ extern "C" int cl_dense_backward_x(int dtype, const void* x, const int64_t* a, c
                 out_dim, batch, int(num_gates));
     });
     return check_launch("cl_dense_backward_x");
-}
-
-namespace cl {
-namespace {
-
-// The fused input + weight gradient kernel splits each row's batch over kFusedWpr waves and
-// covers up to kFusedMaxUnroll vectors per lane.
-template <typename T>
-constexpr int64_t fused_max_batch() {
-    return int64_t(kFusedWpr) * kWave * wide_vec<T>() * kFusedMaxUnroll;
-}
-
-template <typename T, int U>
-void launch_fused(const T* x, const T* kc, const uint8_t* gs, const T* gy, const int2* ab,
-                  const int32_t* gl, const int32_t* ry, const int32_t* ip, const int32_t* ie, T* gx,
-                  T* gw, int64_t in_dim, int64_t out_dim, int64_t R, int64_t B, int G,
-                  hipStream_t s) {
-    constexpr int W = wide_vec<T>();
-    const dim3 grid(unsigned(ceil_div(in_dim, kWaves / kFusedWpr)), 1, 1);
-    k_dense_backward_runs<T, W, U, kFusedWpr, true, true>
-        <<<grid, 256, 0, s>>>(x, kc, gs, gy, ab, gl, ry, ip, ie, gx, gw, in_dim, out_dim, R, B, G);
-}
-
-}  // namespace
-}  // namespace cl
-
-extern "C" int cl_dense_backward_runs(int dtype, const void* x, const void* run_coef,
-                                      const uint8_t* gate_seq, const void* grad_y,
-                                      const int32_t* run_ptr, const int32_t* run_ab,
-                                      const int32_t* run_gl, const int32_t* run_y,
-                                      const int32_t* inv_ptr, const int32_t* inv_entry,
-                                      void* grad_x, void* grad_w, int64_t in_dim, int64_t out_dim,
-                                      int64_t num_runs, int64_t batch, int64_t num_gates,
-                                      void* stream) {
-    clear_error();
-    if (int rc = check_dims(in_dim, out_dim, batch, num_gates)) return rc;
-    CL_ARG(num_runs >= 0 && num_runs < (int64_t(1) << 30), "num_runs out of range");
-    if (!grad_x && !grad_w) return CL_OK;
-    if (out_dim == 0 && (in_dim == 0 || batch == 0 || !grad_x)) return CL_OK;
-    CL_ARG(gate_seq && run_ptr && run_ab && run_gl, "null pointer argument");
-    CL_ARG(batch == 0 || (x && grad_y), "null pointer argument");
-    CL_ARG(aligned(run_ab, 8), "run_ab must be 8-byte aligned");
-    if (grad_x)
-        CL_ARG(run_coef && run_y && inv_ptr && inv_entry,
-               "grad_x needs run_coef, run_y, inv_ptr and inv_entry");
-    hipStream_t s = as_stream(stream);
-    CL_DTYPE_SWITCH(dtype, {
-        using T = scalar_t;
-        auto* xs = static_cast<const T*>(x);
-        auto* kc = static_cast<const T*>(run_coef);
-        auto* gys = static_cast<const T*>(grad_y);
-        auto* gxs = static_cast<T*>(grad_x);
-        auto* gws = static_cast<T*>(grad_w);
-        auto* ab = reinterpret_cast<const int2*>(run_ab);
-        const int G = int(num_gates);
-        const int vec = pick_vec<T>(batch, {x, grad_y, grad_x});
-        constexpr int W = wide_vec<T>();
-        const bool fuse = grad_x && grad_w && vec == W && batch > 0 &&
-                          batch <= fused_max_batch<T>() && in_dim > 0;
-        if (fuse) {
-            const int64_t per_unroll = int64_t(kFusedWpr) * kWave * W;
-            const int64_t U = ceil_div(batch, per_unroll);
-            if (U <= 1)
-                launch_fused<T, 1>(xs, kc, gate_seq, gys, ab, run_gl, run_y, inv_ptr, inv_entry,
-                                   gxs, gws, in_dim, out_dim, num_runs, batch, G, s);
-            else if (U <= 2)
-                launch_fused<T, 2>(xs, kc, gate_seq, gys, ab, run_gl, run_y, inv_ptr, inv_entry,
-                                   gxs, gws, in_dim, out_dim, num_runs, batch, G, s);
-            else if (U <= 4)
-                launch_fused<T, 4>(xs, kc, gate_seq, gys, ab, run_gl, run_y, inv_ptr, inv_entry,
-                                   gxs, gws, in_dim, out_dim, num_runs, batch, G, s);
-            else
-                launch_fused<T, kFusedMaxUnroll>(xs, kc, gate_seq, gys, ab, run_gl, run_y,
-                                                 inv_ptr, inv_entry, gxs, gws, in_dim, out_dim,
-                                                 num_runs, batch, G, s);
-        } else {
-            if (grad_x && in_dim > 0 && batch > 0) {
-                const dim3 grid = rows_grid(in_dim, batch, vec, kChunkUnroll);
-                if (vec == W)
-                    k_dense_backward_runs<T, W, kChunkUnroll, 1, true, false><<<grid, 256, 0, s>>>(
-                        xs, kc, gate_seq, gys, ab, run_gl, run_y, inv_ptr, inv_entry, gxs, nullptr,
-                        in_dim, out_dim, num_runs, batch, G);
-                else
-                    k_dense_backward_runs<T, 1, kChunkUnroll, 1, true, false><<<grid, 256, 0, s>>>(
-                        xs, kc, gate_seq, gys, ab, run_gl, run_y, inv_ptr, inv_entry, gxs, nullptr,
-                        in_dim, out_dim, num_runs, batch, G);
-                if (int rc = check_launch("cl_dense_backward_runs(grad_x)")) return rc;
-            }
-            if (grad_w && out_dim > 0) {
-                const int vw = pick_vec<T>(batch, {x, grad_y});
-                const dim3 grid(unsigned(ceil_div(out_dim, kWaves)), 1, 1);
-                const int64_t ind = std::max<int64_t>(in_dim, 1);
-                if (vw == W)
-                    k_dense_backward_w_runs<T, W><<<grid, 256, 0, s>>>(
-                        xs, gate_seq, gys, run_ptr, ab, run_gl, gws, ind, out_dim, num_runs, batch, G);
-                else
-                    k_dense_backward_w_runs<T, 1><<<grid, 256, 0, s>>>(
-                        xs, gate_seq, gys, run_ptr, ab, run_gl, gws, ind, out_dim, num_runs, batch, G);
-            }
-        }
-    });
-    return check_launch("cl_dense_backward_runs");
 }
 
 extern "C" int cl_dense_eval(int dtype, const void* x, const int64_t* a, const int64_t* b,

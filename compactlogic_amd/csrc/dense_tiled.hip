@@ -1,0 +1,914 @@
+// Dense LogicLayer training path for gfx950: batch-chunk tiles pinned to XCDs.
+//
+// Why tiles: every activation row is gathered by about two consumers (the neurons wired to
+// it), so a gather kernel that streams whole rows reads each row twice from beyond the L2.
+// Here the batch is cut into chunks of CS samples (one LPN-lane group of 16-byte vectors per
+// row), and all work on chunk c runs on one XCD: workgroups are dispatched round-robin over
+// the 8 XCDs of an MI355X, so workgroup w runs on XCD w % 8, and chunk c is given only to
+// workgroups w with w % 8 == c % 8.  The chunk's band of the activation matrix (rows x CS
+// samples, 1.5-3 MB at 12000 rows) then stays in that XCD's 4 MB L2 and the second gather of
+// a row hits L2.  Outputs are written with non-temporal stores so they do not evict the band.
+//
+// Per layer and training step:
+//   k_prep        logits -> softmax probabilities and the collapsed coefficients K of every
+//                 run (K = sum over the run's slots of p_g * (c0, c1, c2, c3)[gate_g])
+//   k_fwd_tiled   y[o, chunk] = sum over runs of K0 + K1 a + K2 b + K3 a b
+//   k_bwd_tiled   grad_x[i, chunk] through the inverse index, and per-chunk batch moments
+//                 (sum gy, gy a, gy b, gy a b) of every run at its operand-a entry
+//   k_moments     the same moments per neuron when no input gradient is needed
+//   k_finalize    moments summed over chunks in chunk order -> gradient per slot -> softmax
+//                 backward (optional) -> gradient of the logits
+// Every reduction has a fixed order, so results are bitwise reproducible.
+#include "common.h"
+
+#include <algorithm>
+#include <initializer_list>
+#include <type_traits>
+
+namespace cl {
+namespace {
+
+constexpr int kXcds = 8;  // MI355X: 8 XCDs of 32 CUs
+
+template <typename T, int N>
+struct VT {
+    typedef T type __attribute__((ext_vector_type(N)));
+};
+template <typename T>
+struct VT<T, 1> {
+    typedef T type;
+};
+
+template <typename V>
+__device__ __forceinline__ V vld(const void* p) {
+    return *reinterpret_cast<const V*>(p);
+}
+
+#ifndef CL_STREAM_STORES
+#define CL_STREAM_STORES 0
+#endif
+
+// Store of an output row segment.  Regular (write-back) stores measure faster inside a
+// training step than non-temporal ones: the next kernel reads these rows right away and then
+// finds them in the Infinity Cache.
+template <typename V>
+__device__ __forceinline__ void vst_stream(void* p, V v) {
+#if CL_STREAM_STORES
+    __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
+#else
+    *reinterpret_cast<V*>(p) = v;
+#endif
+}
+
+template <typename T, int N>
+__device__ __forceinline__ T hsum(typename VT<T, N>::type v) {
+    if constexpr (N == 1) {
+        return v;
+    } else if constexpr (N == 2) {
+        return v[0] + v[1];
+    } else {
+        return (v[0] + v[1]) + (v[2] + v[3]);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T nan_of() {
+    return T(__builtin_nan(""));
+}
+
+// Sum over each group of LPN consecutive lanes (LPN in {4, 8, 16}); the total is valid at the
+// group's first lane (for LPN = 16 at every lane of the group).  DPP stays inside a 16-lane
+// row, and the group leader only ever reads lanes of its own group: row_ror:n delivers to
+// lane l the value of lane (l - n) mod 16, so row_ror:12 brings lane l + 4 to lane l.
+template <int LPN, typename T>
+__device__ __forceinline__ T group_sum(T v) {
+    v += dpp_move<0xB1>(v);                           // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);                           // quad_perm [2,3,0,1]
+    if constexpr (LPN >= 8) v += dpp_move<0x12C>(v);  // row_ror:12 (lane l + 4)
+    if constexpr (LPN >= 16) v += dpp_move<0x128>(v); // row_ror:8
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T row16_max(T v) {
+    v = fmax(v, dpp_move<0xB1>(v));
+    v = fmax(v, dpp_move<0x4E>(v));
+    v = fmax(v, dpp_move<0x124>(v));
+    v = fmax(v, dpp_move<0x128>(v));
+    return v;
+}
+
+// Workgroup -> (chunk, tile).  With at least kXcds chunks, chunk c is handled only by the
+// workgroups w with w % kXcds == c % kXcds, all tiles of chunk c before those of chunk
+// c + kXcds.  With fewer chunks the tiles of each chunk are spread over all XCDs.
+struct TileMap {
+    int64_t nchunks;
+    int64_t ntiles;
+};
+
+__host__ __device__ __forceinline__ int64_t tile_grid(const TileMap& m) {
+    if (m.nchunks >= kXcds) return kXcds * ((m.nchunks + kXcds - 1) / kXcds) * m.ntiles;
+    return m.nchunks * m.ntiles;
+}
+
+__device__ __forceinline__ bool map_tile(const TileMap& m, int64_t w, int64_t& c, int64_t& t) {
+    if (m.nchunks >= kXcds) {
+        const int64_t x = w % kXcds, j = w / kXcds;
+        c = x + kXcds * (j / m.ntiles);
+        t = j % m.ntiles;
+    } else {
+        c = w / m.ntiles;
+        t = w % m.ntiles;
+    }
+    return c < m.nchunks;
+}
+
+constexpr int kMaxSlotGroups = 8;  // G <= 128 = 8 groups of 16 slots
+
+// ------------------------------------------------------------------------------------------
+// k_prep: 16 lanes per neuron; lane l holds slots l, l+16, ...
+template <typename T>
+__global__ __launch_bounds__(256) void k_prep(const T* __restrict__ w, int softmax,
+                                              const uint8_t* __restrict__ gs,
+                                              const int32_t* __restrict__ run_ptr,
+                                              const int32_t* __restrict__ run_gl,
+                                              const int32_t* __restrict__ inv_pos,
+                                              T* __restrict__ probs, T* __restrict__ kc,
+                                              T* __restrict__ inv_coef, int64_t out_dim,
+                                              int64_t num_runs, int G) {
+    const int64_t o = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4);
+    const int l = threadIdx.x & 15;
+    if (o >= out_dim) return;  // uniform per 16-lane row
+    const int ng = (G + 15) >> 4;
+    T p[kMaxSlotGroups];
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) {
+        const int g = l + 16 * m;
+        p[m] = (m < ng && g < G) ? w[o * G + g] : T(0);
+    }
+    if (softmax) {
+        T mx = -T(__builtin_inf());
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m)
+            if (m < ng && l + 16 * m < G) mx = fmax(mx, p[m]);
+        mx = row16_max(mx);
+        T s = 0;
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const bool ok = m < ng && l + 16 * m < G;
+            p[m] = ok ? exp(p[m] - mx) : T(0);
+            s += p[m];
+        }
+        s = group_sum<16>(s);
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) p[m] = p[m] / s;
+    }
+    if (probs) {
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const int g = l + 16 * m;
+            if (m < ng && g < G) probs[o * G + g] = p[m];
+        }
+    }
+    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
+    if (r0 < 0 || r1 < r0 || r1 > num_runs) return;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int gl = run_gl[r];
+        const int g0 = gl & 0xff, g1 = g0 + (gl >> 8);
+        T k0 = 0, k1 = 0, k2 = 0, k3 = 0;
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const int g = l + 16 * m;
+            if (m < ng && g >= g0 && g < g1 && g < G) {
+                const Coef4<T> c = gate_coef<T>(gs[o * G + g]);
+                k0 = fma(p[m], c.c0, k0);
+                k1 = fma(p[m], c.c1, k1);
+                k2 = fma(p[m], c.c2, k2);
+                k3 = fma(p[m], c.c3, k3);
+            }
+        }
+        k0 = group_sum<16>(k0);
+        k1 = group_sum<16>(k1);
+        k2 = group_sum<16>(k2);
+        k3 = group_sum<16>(k3);
+        if (l == 0) {
+            if (g1 > G) k0 = k1 = k2 = k3 = nan_of<T>();
+            kc[4 * r + 0] = k0;
+            kc[4 * r + 1] = k1;
+            kc[4 * r + 2] = k2;
+            kc[4 * r + 3] = k3;
+            if (inv_coef) {
+                // (own-operand coefficient, c3) of the run's two inverse-index entries
+                const int64_t pa = inv_pos[2 * r], pb = inv_pos[2 * r + 1];
+                if (uint64_t(pa) < uint64_t(2 * num_runs)) {
+                    inv_coef[2 * pa + 0] = k1;
+                    inv_coef[2 * pa + 1] = k3;
+                }
+                if (uint64_t(pb) < uint64_t(2 * num_runs)) {
+                    inv_coef[2 * pb + 0] = k2;
+                    inv_coef[2 * pb + 1] = k3;
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// k_fwd_tiled: LPN lanes per neuron row segment, NPG neurons per lane group (256 / LPN * NPG
+// neurons per tile).  nab[o] = (a, b of the first run, first run, end run) is one load, after
+// which the coefficients and both gathers of every neuron of the group are issued together.
+// Neurons with several runs continue through run_ab for the others.
+template <typename T, int VEC, int LPN, int NPG>
+__global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
+                                                   const T* __restrict__ kc,
+                                                   const int4* __restrict__ nab,
+                                                   const int2* __restrict__ run_ab,
+                                                   T* __restrict__ y, int64_t in_dim,
+                                                   int64_t out_dim, int64_t num_runs, int64_t B,
+                                                   TileMap tm) {
+    using V = typename VT<T, VEC>::type;
+    using V4 = typename VT<T, 4>::type;
+    constexpr int GROUPS = 256 / LPN;
+    int64_t c, t;
+    if (!map_tile(tm, blockIdx.x, c, t)) return;
+    const int64_t obase = (t * GROUPS + threadIdx.x / LPN) * NPG;
+    const int64_t idx = c * (LPN * VEC) + int64_t(threadIdx.x % LPN) * VEC;
+    if (obase >= out_dim || idx >= B) return;
+    int4 rec[NPG];
+#pragma unroll
+    for (int j = 0; j < NPG; ++j)
+        rec[j] = obase + j < out_dim ? nab[obase + j] : make_int4(0, 0, 0, 0);
+    V4 k[NPG];
+    V va[NPG], vb[NPG];
+    bool ok[NPG];
+#pragma unroll
+    for (int j = 0; j < NPG; ++j) {
+        ok[j] = obase + j < out_dim && rec[j].z >= 0 && rec[j].z < rec[j].w &&
+                rec[j].w <= num_runs && uint32_t(rec[j].x) < uint64_t(in_dim) &&
+                uint32_t(rec[j].y) < uint64_t(in_dim);
+        if (ok[j]) {
+            k[j] = vld<V4>(kc + 4 * int64_t(rec[j].z));
+            va[j] = vld<V>(x + int64_t(rec[j].x) * B + idx);
+            vb[j] = vld<V>(x + int64_t(rec[j].y) * B + idx);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NPG; ++j) {
+        const int64_t o = obase + j;
+        if (o >= out_dim) break;
+        V acc = V(nan_of<T>());
+        if (ok[j]) {
+            acc = k[j][3] * (va[j] * vb[j]) + k[j][2] * vb[j] + k[j][1] * va[j] + k[j][0];
+            for (int64_t r = int64_t(rec[j].z) + 1; r < rec[j].w; ++r) {
+                const int2 ab = run_ab[r];
+                if (uint32_t(ab.x) >= uint64_t(in_dim) || uint32_t(ab.y) >= uint64_t(in_dim)) {
+                    acc = V(nan_of<T>());
+                    break;
+                }
+                const V4 kr = vld<V4>(kc + 4 * r);
+                const V a = vld<V>(x + int64_t(ab.x) * B + idx);
+                const V b = vld<V>(x + int64_t(ab.y) * B + idx);
+                acc += kr[3] * (a * b) + kr[2] * b + kr[1] * a + kr[0];
+            }
+        }
+        vst_stream<V>(y + o * B + idx, acc);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Softmax + run coefficients of neuron o held by a 16-lane row (lane l: slots l, l+16, ...).
+template <typename T>
+struct SlotProbs {
+    T p[kMaxSlotGroups];
+};
+
+template <typename T>
+__device__ __forceinline__ SlotProbs<T> slot_probs(const T* __restrict__ w, int softmax, int64_t o,
+                                                   int l, int G) {
+    const int ng = (G + 15) >> 4;
+    SlotProbs<T> sp;
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) {
+        const int g = l + 16 * m;
+        sp.p[m] = (m < ng && g < G) ? w[o * G + g] : T(0);
+    }
+    if (softmax) {
+        T mx = -T(__builtin_inf());
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m)
+            if (m < ng && l + 16 * m < G) mx = fmax(mx, sp.p[m]);
+        mx = row16_max(mx);
+        T s = 0;
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const bool ok = m < ng && l + 16 * m < G;
+            sp.p[m] = ok ? exp(sp.p[m] - mx) : T(0);
+            s += sp.p[m];
+        }
+        s = group_sum<16>(s);
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) sp.p[m] = sp.p[m] / s;
+    }
+    return sp;
+}
+
+// K of the run [g0, g1) from the row's probabilities; every lane of the row gets the result.
+template <typename T>
+__device__ __forceinline__ Coef4<T> row_run_coef(const SlotProbs<T>& sp,
+                                                 const uint8_t* __restrict__ grow, int l, int g0,
+                                                 int g1, int G) {
+    const int ng = (G + 15) >> 4;
+    T k0 = 0, k1 = 0, k2 = 0, k3 = 0;
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) {
+        const int g = l + 16 * m;
+        if (m < ng && g >= g0 && g < g1 && g < G) {
+            const Coef4<T> c = gate_coef<T>(grow[g]);
+            k0 = fma(sp.p[m], c.c0, k0);
+            k1 = fma(sp.p[m], c.c1, k1);
+            k2 = fma(sp.p[m], c.c2, k2);
+            k3 = fma(sp.p[m], c.c3, k3);
+        }
+    }
+    Coef4<T> k;
+    k.c0 = group_sum<16>(k0);
+    k.c1 = group_sum<16>(k1);
+    k.c2 = group_sum<16>(k2);
+    k.c3 = group_sum<16>(k3);
+    return k;
+}
+
+// k_wgrad_full: weight gradient per neuron over the whole batch (16 lanes per neuron), with
+// the softmax backward when `probs` is given.  Used when no input gradient is needed, so no
+// per-chunk moments or finalize pass are required.
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void k_wgrad_full(const T* __restrict__ x, const T* __restrict__ gy,
+                                                    const uint8_t* __restrict__ gs,
+                                                    const T* __restrict__ probs,
+                                                    const int32_t* __restrict__ run_ptr,
+                                                    const int2* __restrict__ run_ab,
+                                                    const int32_t* __restrict__ run_gl,
+                                                    T* __restrict__ grad_w, int64_t in_dim,
+                                                    int64_t out_dim, int64_t num_runs, int64_t B,
+                                                    int G) {
+    using V = typename VT<T, VEC>::type;
+    const int64_t o = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4);
+    if (o >= out_dim) return;  // uniform per 16-lane row
+    const int l = threadIdx.x & 15;
+    const int ng = (G + 15) >> 4;
+    T gp[kMaxSlotGroups];
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) gp[m] = T(0);
+    bool bad = false;
+    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
+    if (r0 < 0 || r1 < r0 || r1 > num_runs) {
+        bad = true;
+        r1 = r0;
+    }
+    const T* gyr = gy + o * B;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int2 ab = run_ab[r];
+        const int gl = run_gl[r];
+        const int g0 = gl & 0xff, g1 = g0 + (gl >> 8);
+        const bool ok = uint32_t(ab.x) < uint64_t(in_dim) && uint32_t(ab.y) < uint64_t(in_dim);
+        bad = bad || !ok;
+        T s1 = 0, sa = 0, sb = 0, sab = 0;
+        if (ok) {
+            const T* xa = x + int64_t(ab.x) * B;
+            const T* xb = x + int64_t(ab.y) * B;
+            for (int64_t idx = int64_t(l) * VEC; idx < B; idx += 16 * VEC) {
+                const V vg = vld<V>(gyr + idx);
+                const V va = vld<V>(xa + idx);
+                const V vb = vld<V>(xb + idx);
+                const V ga = vg * va;
+                s1 += hsum<T, VEC>(vg);
+                sa += hsum<T, VEC>(ga);
+                sb += hsum<T, VEC>(vg * vb);
+                sab += hsum<T, VEC>(ga * vb);
+            }
+        }
+        s1 = group_sum<16>(s1);
+        sa = group_sum<16>(sa);
+        sb = group_sum<16>(sb);
+        sab = group_sum<16>(sab);
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const int g = l + 16 * m;
+            if (m < ng && g >= g0 && g < g1 && g < G) {
+                const Coef4<T> cf = gate_coef<T>(gs[o * G + g]);
+                gp[m] = fma(cf.c3, sab, fma(cf.c2, sb, fma(cf.c1, sa, cf.c0 * s1)));
+            }
+        }
+    }
+    if (probs) {
+        T dot = 0;
+        T p[kMaxSlotGroups];
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const int g = l + 16 * m;
+            p[m] = (m < ng && g < G) ? probs[o * G + g] : T(0);
+            dot = fma(p[m], gp[m], dot);
+        }
+        dot = group_sum<16>(dot);
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) gp[m] = p[m] * (gp[m] - dot);
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) {
+        const int g = l + 16 * m;
+        if (m < ng && g < G) grad_w[o * G + g] = bad ? nan_of<T>() : gp[m];
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// k_bwd_tiled: LPN lanes per input-row segment; rows are taken in processing-slot order
+// (descending entry count, so the lane groups of a wave have equal work), and slot_rec[slot]
+// = (input row, first entry, end entry) is one load.  Entry e of the inverse index
+// carries a record (neuron, other input, run, side) and the coefficients (own-operand K, K3)
+// written by k_prep, so each entry costs one record load followed by the two row loads; the
+// next entry's record is fetched while the current one is processed.
+// part[(r * nchunks + c) * 4 + j] receives the chunk-c moments of run r (WANT_GW) at the
+// run's operand-a entry.
+template <typename T, int VEC, int LPN, bool WANT_GX, bool WANT_GW>
+__global__ __launch_bounds__(256) void k_bwd_tiled(
+    const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
+    const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef, T* __restrict__ gx,
+    T* __restrict__ part,
+    int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, TileMap tm) {
+    using V = typename VT<T, VEC>::type;
+    using V2 = typename VT<T, 2>::type;
+    using V4 = typename VT<T, 4>::type;
+    constexpr int NT = 256 / LPN;
+    int64_t c, t;
+    if (!map_tile(tm, blockIdx.x, c, t)) return;
+    const int64_t slot = t * NT + threadIdx.x / LPN;
+    if (slot >= in_dim) return;  // uniform per lane group
+    const int4 sr = slot_rec[slot];
+    const int64_t i = sr.x;
+    if (uint64_t(i) >= uint64_t(in_dim)) return;
+    const int64_t idx = c * (LPN * VEC) + int64_t(threadIdx.x % LPN) * VEC;
+    const bool col = idx < B;
+    const bool leader = (threadIdx.x % LPN) == 0;
+
+    V xi = V(T(0));
+    if (WANT_GW && col) xi = vld<V>(x + i * B + idx);
+    V acc = V(T(0));
+    bool bad = false;
+    int64_t e0 = sr.y, e1 = sr.z;
+    if (e0 < 0 || e1 < e0 || e1 > 2 * num_runs) {
+        bad = true;
+        e1 = e0;
+    }
+    int4 rec = make_int4(0, 0, 0, 0);
+    V2 kk = V2(T(0));
+    if (e0 < e1) {
+        rec = inv_rec[e0];
+        kk = vld<V2>(inv_coef + 2 * e0);
+    }
+    for (int64_t e = e0; e < e1; ++e) {
+        const int4 cur = rec;
+        const V2 ck = kk;
+        if (e + 1 < e1) {
+            rec = inv_rec[e + 1];
+            kk = vld<V2>(inv_coef + 2 * (e + 1));
+        }
+        const int64_t yo = cur.x, other = cur.y, r = cur.z;
+        const int side = cur.w;
+        if (uint64_t(yo) >= uint64_t(out_dim) || uint64_t(other) >= uint64_t(in_dim) ||
+            uint64_t(r) >= uint64_t(num_runs)) {
+            bad = true;
+            continue;
+        }
+        V vo = V(T(0)), vg = V(T(0));
+        if (col) {
+            vo = vld<V>(x + other * B + idx);
+            vg = vld<V>(gy + yo * B + idx);
+        }
+        if (WANT_GX) acc += (ck[0] + ck[1] * vo) * vg;
+        if (WANT_GW && side == 0) {
+            const V ga = vg * xi;
+            T s1 = hsum<T, VEC>(vg), sa = hsum<T, VEC>(ga);
+            T sb = hsum<T, VEC>(vg * vo), sab = hsum<T, VEC>(ga * vo);
+            s1 = group_sum<LPN>(s1);
+            sa = group_sum<LPN>(sa);
+            sb = group_sum<LPN>(sb);
+            sab = group_sum<LPN>(sab);
+            if (leader) {
+                V4 mv;
+                mv[0] = s1;
+                mv[1] = sa;
+                mv[2] = sb;
+                mv[3] = sab;
+                *reinterpret_cast<V4*>(part + (r * tm.nchunks + c) * 4) = mv;
+            }
+        }
+    }
+    if (WANT_GX && col) {
+        if (bad) acc = V(nan_of<T>());
+        vst_stream<V>(gx + i * B + idx, acc);
+    }
+}
+
+// k_moments: the per-chunk moments of every run, per neuron (used when grad_x is not needed).
+template <typename T, int VEC, int LPN>
+__global__ __launch_bounds__(256) void k_moments(const T* __restrict__ x, const T* __restrict__ gy,
+                                                 const int32_t* __restrict__ run_ptr,
+                                                 const int2* __restrict__ run_ab,
+                                                 T* __restrict__ part, int64_t in_dim,
+                                                 int64_t out_dim, int64_t num_runs, int64_t B,
+                                                 TileMap tm) {
+    using V = typename VT<T, VEC>::type;
+    using V4 = typename VT<T, 4>::type;
+    constexpr int NT = 256 / LPN;
+    int64_t c, t;
+    if (!map_tile(tm, blockIdx.x, c, t)) return;
+    const int64_t o = t * NT + threadIdx.x / LPN;
+    if (o >= out_dim) return;  // uniform per lane group
+    const int64_t idx = c * (LPN * VEC) + int64_t(threadIdx.x % LPN) * VEC;
+    const bool col = idx < B;
+    const bool leader = (threadIdx.x % LPN) == 0;
+    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
+    if (r0 < 0 || r1 < r0 || r1 > num_runs) return;
+    V vg = V(T(0));
+    if (col) vg = vld<V>(gy + o * B + idx);
+    const T s1 = group_sum<LPN>(hsum<T, VEC>(vg));
+    for (int64_t r = r0; r < r1; ++r) {
+        const int2 ab = run_ab[r];
+        V va = V(T(0)), vb = V(T(0));
+        const bool ok = uint32_t(ab.x) < uint64_t(in_dim) && uint32_t(ab.y) < uint64_t(in_dim);
+        if (col && ok) {
+            va = vld<V>(x + int64_t(ab.x) * B + idx);
+            vb = vld<V>(x + int64_t(ab.y) * B + idx);
+        }
+        const V ga = vg * va;
+        const T sa = group_sum<LPN>(hsum<T, VEC>(ga));
+        const T sb = group_sum<LPN>(hsum<T, VEC>(vg * vb));
+        const T sab = group_sum<LPN>(hsum<T, VEC>(ga * vb));
+        if (leader) {
+            V4 mv;
+            mv[0] = ok ? s1 : nan_of<T>();
+            mv[1] = sa;
+            mv[2] = sb;
+            mv[3] = sab;
+            *reinterpret_cast<V4*>(part + (r * tm.nchunks + c) * 4) = mv;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// k_finalize: 16 lanes per neuron.  Moments of each run are summed over the chunks (lane l
+// takes chunks l, l+16, ..., then a fixed lane tree), expanded to the run's slots, and, when
+// `probs` is given, passed through the softmax backward: dL/dlogit_g = p_g (dL/dp_g - sum_h
+// p_h dL/dp_h).
+template <typename T>
+__global__ __launch_bounds__(256) void k_finalize(const T* __restrict__ part, int64_t nchunks,
+                                                  const uint8_t* __restrict__ gs,
+                                                  const T* __restrict__ probs,
+                                                  const int32_t* __restrict__ run_ptr,
+                                                  const int32_t* __restrict__ run_gl,
+                                                  T* __restrict__ grad_w, int64_t out_dim,
+                                                  int64_t num_runs, int G) {
+    const int64_t o = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4);
+    const int l = threadIdx.x & 15;
+    if (o >= out_dim) return;  // uniform per 16-lane row
+    const int ng = (G + 15) >> 4;
+    T gp[kMaxSlotGroups];
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) gp[m] = T(0);
+    bool bad = false;
+    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
+    if (r0 < 0 || r1 < r0 || r1 > num_runs) {
+        bad = true;
+        r1 = r0;
+    }
+    for (int64_t r = r0; r < r1; ++r) {
+        const int gl = run_gl[r];
+        const int g0 = gl & 0xff, g1 = g0 + (gl >> 8);
+        T m0 = 0, m1 = 0, m2 = 0, m3 = 0;
+        const T* pr = part + r * nchunks * 4;
+        for (int64_t cc = l; cc < nchunks; cc += 16) {
+            m0 += pr[cc * 4 + 0];
+            m1 += pr[cc * 4 + 1];
+            m2 += pr[cc * 4 + 2];
+            m3 += pr[cc * 4 + 3];
+        }
+        m0 = group_sum<16>(m0);
+        m1 = group_sum<16>(m1);
+        m2 = group_sum<16>(m2);
+        m3 = group_sum<16>(m3);
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const int g = l + 16 * m;
+            if (m < ng && g >= g0 && g < g1 && g < G) {
+                const Coef4<T> cf = gate_coef<T>(gs[o * G + g]);
+                gp[m] = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
+            }
+        }
+    }
+    if (probs) {
+        T dot = 0;
+        T p[kMaxSlotGroups];
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) {
+            const int g = l + 16 * m;
+            p[m] = (m < ng && g < G) ? probs[o * G + g] : T(0);
+            dot = fma(p[m], gp[m], dot);
+        }
+        dot = group_sum<16>(dot);
+#pragma unroll
+        for (int m = 0; m < kMaxSlotGroups; ++m) gp[m] = p[m] * (gp[m] - dot);
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) {
+        const int g = l + 16 * m;
+        if (m < ng && g < G) grad_w[o * G + g] = bad ? nan_of<T>() : gp[m];
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_zero(T* __restrict__ p, int64_t n) {
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+        p[i] = T(0);
+}
+
+// ------------------------------------------------------------------------------------------
+// Host-side tiling choice.
+
+struct Tiling {
+    int vec;   // elements per 16-byte access (1 when the batch does not allow vectors)
+    int lpn;   // lanes per row segment
+    int64_t chunk;
+    TileMap map;
+};
+
+// Narrowest lane group first that still leaves every XCD a chunk; bands of at most
+// `lpn_max` lanes keep a chunk's activation band within one XCD's L2.
+template <typename T>
+Tiling choose_tiling(int64_t B, int64_t rows, bool vec_ok, int lpn_max, int rows_per_group = 1) {
+    Tiling tl;
+    tl.vec = vec_ok ? wide_vec<T>() : 1;
+    tl.lpn = lpn_max;
+    while (tl.lpn > 4 && ceil_div(B, int64_t(tl.lpn) * tl.vec) < kXcds) tl.lpn >>= 1;
+    tl.chunk = int64_t(tl.lpn) * tl.vec;
+    tl.map.nchunks = ceil_div(B, tl.chunk);
+    tl.map.ntiles = ceil_div(rows, int64_t(256 / tl.lpn) * rows_per_group);
+    return tl;
+}
+
+}  // namespace
+}  // namespace cl
+
+using namespace cl;
+
+#ifndef CL_FWD_LPN
+#define CL_FWD_LPN 16
+#endif
+#ifndef CL_BWD_LPN
+#define CL_BWD_LPN 16
+#endif
+#ifndef CL_FWD_NPG
+#define CL_FWD_NPG 2
+#endif
+
+namespace {
+
+// The tiling (and with it the chunk count of the moments buffer) depends on the batch alone:
+// 16-byte vectors whenever batch % (16 / sizeof(T)) == 0, which then requires 16-byte aligned
+// row buffers.
+template <typename T>
+bool vec_ok(int64_t B) {
+    return B % wide_vec<T>() == 0;
+}
+
+bool all_aligned(std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs)
+        if (p && !aligned(p, 16)) return false;
+    return true;
+}
+
+int check_plan_dims(int64_t in_dim, int64_t out_dim, int64_t B, int64_t G, int64_t R) {
+    CL_ARG(in_dim >= 0 && out_dim >= 0 && B >= 0, "negative dimension");
+    CL_ARG(G >= 1 && G <= 128, "num_gates must be in [1, 128], got %lld", (long long)G);
+    CL_ARG(R >= 0 && R < (int64_t(1) << 30), "num_runs out of range");
+    CL_ARG(in_dim < (int64_t(1) << 31) && out_dim < (int64_t(1) << 31), "too many rows");
+    return CL_OK;
+}
+
+}  // namespace
+
+namespace {
+
+// Calls f(std::integral_constant<int, VEC>, std::integral_constant<int, LPN>) for the
+// tiling's vector width and lane-group size.
+template <typename T, typename F>
+void with_tiling(const Tiling& tl, F&& f) {
+    constexpr int W = wide_vec<T>();
+    using I = std::integral_constant<int, 1>;
+    using IW = std::integral_constant<int, W>;
+    using L4 = std::integral_constant<int, 4>;
+    using L8 = std::integral_constant<int, 8>;
+    using L16 = std::integral_constant<int, 16>;
+    if (tl.vec == W) {
+        if (tl.lpn == 16) f(IW{}, L16{});
+        else if (tl.lpn == 8) f(IW{}, L8{});
+        else f(IW{}, L4{});
+    } else {
+        if (tl.lpn == 16) f(I{}, L16{});
+        else if (tl.lpn == 8) f(I{}, L8{});
+        else f(I{}, L4{});
+    }
+}
+
+}  // namespace
+
+extern "C" int cl_dense_prep(int dtype, const void* w, int softmax, const uint8_t* gate_seq,
+                             const int32_t* run_ptr, const int32_t* run_gl,
+                             const int32_t* inv_pos, void* probs, void* run_coef,
+                             void* inv_coef, int64_t out_dim, int64_t num_runs,
+                             int64_t num_gates, void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(1, out_dim, 0, num_gates, num_runs)) return rc;
+    if (out_dim == 0) return CL_OK;
+    CL_ARG(w && gate_seq && run_ptr && run_gl && run_coef, "null pointer argument");
+    CL_ARG(!inv_coef || inv_pos, "inv_coef needs inv_pos");
+    CL_DTYPE_SWITCH(dtype, {
+        k_prep<scalar_t><<<unsigned(ceil_div(out_dim, 16)), 256, 0, as_stream(stream)>>>(
+            static_cast<const scalar_t*>(w), softmax, gate_seq, run_ptr, run_gl, inv_pos,
+            static_cast<scalar_t*>(probs), static_cast<scalar_t*>(run_coef),
+            static_cast<scalar_t*>(inv_coef), out_dim, num_runs, int(num_gates));
+    });
+    return check_launch("cl_dense_prep");
+}
+
+extern "C" int cl_dense_forward_tiled(int dtype, const void* x, const void* run_coef,
+                                      const int32_t* nab, const int32_t* run_ab, void* y,
+                                      int64_t in_dim, int64_t out_dim, int64_t num_runs,
+                                      int64_t batch, void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(in_dim, out_dim, batch, 1, num_runs)) return rc;
+    if (out_dim == 0 || batch == 0) return CL_OK;
+    CL_ARG(in_dim > 0, "in_dim is 0 but out_dim > 0");
+    CL_ARG(x && run_coef && nab && run_ab && y, "null pointer argument");
+    CL_ARG(aligned(run_ab, 8) && aligned(nab, 16) && aligned(run_coef, 16),
+           "run_ab / nab / run_coef misaligned");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        CL_ARG(!vec_ok<T>(batch) || all_aligned({x, y}), "x and y must be 16-byte aligned");
+        const Tiling tl = choose_tiling<T>(batch, out_dim, vec_ok<T>(batch), CL_FWD_LPN, CL_FWD_NPG);
+        const unsigned grid = unsigned(tile_grid(tl.map));
+        auto* xs = static_cast<const T*>(x);
+        auto* kc = static_cast<const T*>(run_coef);
+        auto* nb = reinterpret_cast<const int4*>(nab);
+        auto* ab = reinterpret_cast<const int2*>(run_ab);
+        auto* ys = static_cast<T*>(y);
+        with_tiling<T>(tl, [&](auto vc, auto lc) {
+            k_fwd_tiled<T, decltype(vc)::value, decltype(lc)::value, CL_FWD_NPG>
+                <<<grid, 256, 0, s>>>(xs, kc, nb, ab, ys, in_dim, out_dim, num_runs, batch, tl.map);
+        });
+    });
+    return check_launch("cl_dense_forward_tiled");
+}
+
+extern "C" int cl_dense_weight_grad(int dtype, const void* x, const void* grad_y,
+                                    const uint8_t* gate_seq, const void* probs,
+                                    const int32_t* run_ptr, const int32_t* run_ab,
+                                    const int32_t* run_gl, void* grad_w, int64_t in_dim,
+                                    int64_t out_dim, int64_t num_runs, int64_t batch,
+                                    int64_t num_gates, void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(in_dim, out_dim, batch, num_gates, num_runs)) return rc;
+    if (out_dim == 0) return CL_OK;
+    CL_ARG(gate_seq && run_ptr && run_ab && run_gl && grad_w, "null pointer argument");
+    CL_ARG(batch == 0 || (x && grad_y), "null pointer argument");
+    CL_ARG(aligned(run_ab, 8), "run_ab misaligned");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        constexpr int W = wide_vec<T>();
+        const bool v = vec_ok<T>(batch);
+        CL_ARG(!v || all_aligned({x, grad_y}), "x and grad_y must be 16-byte aligned");
+        const unsigned grid = unsigned(ceil_div(out_dim, 16));
+        auto* xs = static_cast<const T*>(x);
+        auto* gys = static_cast<const T*>(grad_y);
+        auto* pr = static_cast<const T*>(probs);
+        auto* ab = reinterpret_cast<const int2*>(run_ab);
+        auto* gw = static_cast<T*>(grad_w);
+        if (v)
+            k_wgrad_full<T, W><<<grid, 256, 0, s>>>(xs, gys, gate_seq, pr, run_ptr, ab, run_gl, gw,
+                                                   std::max<int64_t>(in_dim, 1), out_dim, num_runs,
+                                                   batch, int(num_gates));
+        else
+            k_wgrad_full<T, 1><<<grid, 256, 0, s>>>(xs, gys, gate_seq, pr, run_ptr, ab, run_gl, gw,
+                                                   std::max<int64_t>(in_dim, 1), out_dim, num_runs,
+                                                   batch, int(num_gates));
+    });
+    return check_launch("cl_dense_weight_grad");
+}
+
+extern "C" int cl_dense_tiled_chunks(int dtype, int64_t batch, int64_t in_dim, int64_t out_dim,
+                                     int64_t* nchunks) {
+    clear_error();
+    CL_ARG(nchunks && batch >= 0, "bad argument");
+    // Chunks of the backward tiling: they depend on the batch (and dtype) only.
+    (void)in_dim;
+    (void)out_dim;
+    CL_DTYPE_SWITCH(dtype, {
+        const int64_t b = std::max<int64_t>(batch, 1);
+        *nchunks = choose_tiling<scalar_t>(b, 1, vec_ok<scalar_t>(b), CL_BWD_LPN).map.nchunks;
+    });
+    return CL_OK;
+}
+
+extern "C" int cl_dense_backward_tiled(int dtype, const void* x, const void* grad_y,
+                                       const int32_t* run_ptr, const int32_t* run_ab,
+                                       const int32_t* slot_rec, const int32_t* inv_rec,
+                                       const void* inv_coef, void* grad_x, void* moments,
+                                       int64_t nchunks,
+                                       int64_t in_dim, int64_t out_dim, int64_t num_runs,
+                                       int64_t batch, void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(in_dim, out_dim, batch, 1, num_runs)) return rc;
+    if (!grad_x && !moments) return CL_OK;
+    if (batch == 0) {
+        // Empty batch: all moments are zero (a fill kernel, so the call stays graph-safe).
+        CL_ARG(!moments || nchunks >= 1, "nchunks must be >= 1");
+        if (moments && num_runs > 0) {
+            const int64_t n = num_runs * nchunks * 4;
+            CL_DTYPE_SWITCH(dtype, {
+                k_zero<scalar_t><<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65535)), 256, 0,
+                                   as_stream(stream)>>>(static_cast<scalar_t*>(moments), n);
+            });
+        }
+        return check_launch("cl_dense_backward_tiled(zero)");
+    }
+    CL_ARG(x && grad_y, "null pointer argument");
+    if (grad_x)
+        CL_ARG(slot_rec && inv_rec && inv_coef && aligned(slot_rec, 16) && aligned(inv_rec, 16) &&
+                   aligned(inv_coef, 8),
+               "grad_x needs slot_rec, inv_rec (16-byte aligned) and inv_coef");
+    if (moments) CL_ARG(aligned(moments, 16), "moments must be 16-byte aligned");
+    if (moments && !grad_x)
+        CL_ARG(run_ptr && run_ab && aligned(run_ab, 8), "moments need run_ptr and run_ab");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        const bool v = vec_ok<T>(batch);
+        CL_ARG(!v || all_aligned({x, grad_y, grad_x}), "row buffers must be 16-byte aligned");
+        auto* xs = static_cast<const T*>(x);
+        auto* gys = static_cast<const T*>(grad_y);
+        auto* ab = reinterpret_cast<const int2*>(run_ab);
+        auto* rec = reinterpret_cast<const int4*>(inv_rec);
+        auto* srec = reinterpret_cast<const int4*>(slot_rec);
+        auto* ic = static_cast<const T*>(inv_coef);
+        auto* gxs = static_cast<T*>(grad_x);
+        auto* mom = static_cast<T*>(moments);
+        if (grad_x && in_dim > 0) {
+            const Tiling tl = choose_tiling<T>(batch, in_dim, v, CL_BWD_LPN);
+            const unsigned grid = unsigned(tile_grid(tl.map));
+            if (moments) {
+                CL_ARG(nchunks == tl.map.nchunks, "moments buffer must use the backward chunk count");
+                with_tiling<T>(tl, [&](auto vc, auto lc) {
+                    k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, true, true>
+                        <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gxs, mom,
+                                              in_dim, out_dim, num_runs, batch, tl.map);
+                });
+            } else {
+                with_tiling<T>(tl, [&](auto vc, auto lc) {
+                    k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, true, false>
+                        <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gxs, mom,
+                                              in_dim, out_dim, num_runs, batch, tl.map);
+                });
+            }
+        } else if (moments && out_dim > 0) {
+            const Tiling tl = choose_tiling<T>(batch, out_dim, v, CL_BWD_LPN);
+            CL_ARG(nchunks == tl.map.nchunks, "moments buffer must use the backward chunk count");
+            const unsigned grid = unsigned(tile_grid(tl.map));
+            with_tiling<T>(tl, [&](auto vc, auto lc) {
+                k_moments<T, decltype(vc)::value, decltype(lc)::value><<<grid, 256, 0, s>>>(
+                    xs, gys, run_ptr, ab, mom, in_dim, out_dim, num_runs, batch, tl.map);
+            });
+        }
+    });
+    return check_launch("cl_dense_backward_tiled");
+}
+
+extern "C" int cl_dense_backward_finalize(int dtype, const void* moments, int64_t nchunks,
+                                          const uint8_t* gate_seq, const void* probs,
+                                          const int32_t* run_ptr, const int32_t* run_gl,
+                                          void* grad_w, int64_t out_dim, int64_t num_runs,
+                                          int64_t num_gates, void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(1, out_dim, 0, num_gates, num_runs)) return rc;
+    if (out_dim == 0) return CL_OK;
+    CL_ARG(nchunks >= 1, "nchunks must be >= 1");
+    CL_ARG(gate_seq && run_ptr && run_gl && grad_w, "null pointer argument");
+    CL_ARG(num_runs == 0 || moments, "null moments");
+    CL_DTYPE_SWITCH(dtype, {
+        k_finalize<scalar_t><<<unsigned(ceil_div(out_dim, 16)), 256, 0, as_stream(stream)>>>(
+            static_cast<const scalar_t*>(moments), nchunks, gate_seq,
+            static_cast<const scalar_t*>(probs), run_ptr, run_gl,
+            static_cast<scalar_t*>(grad_w), out_dim, num_runs, int(num_gates));
+    });
+    return check_launch("cl_dense_backward_finalize");
+}

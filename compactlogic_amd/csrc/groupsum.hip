@@ -177,6 +177,38 @@ __global__ __launch_bounds__(256) void k_gsum_bwd(const T* __restrict__ g, int64
     vstore<T, VEC>(gx + row * so + i0, v);
 }
 
+// ---- backward, batch-contiguous grad_x ([F, batch] in memory): block = (batch tile, class
+// c, slice of the group's rows).  Each lane computes its g[n, c] / tau once and streams it
+// down the rows of its slice with non-temporal stores.
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void k_gsum_bwd_rows(const T* __restrict__ g, int64_t B,
+                                                       int64_t F, int64_t sf, int64_t gsz,
+                                                       int64_t k, int64_t slice, T tau,
+                                                       T* __restrict__ gx) {
+    const int64_t n0 = (int64_t(blockIdx.x) * 64 + (threadIdx.x & 63)) * VEC;
+    if (n0 >= B) return;
+    const int64_t c = blockIdx.y;
+    const int64_t j0 = c * gsz + int64_t(blockIdx.z) * slice;
+    const int64_t j1 = std::min<int64_t>(std::min<int64_t>(j0 + slice, (c + 1) * gsz), F);
+    Vec<T, VEC> v;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v.v[i] = g[(n0 + i) * k + c] / tau;
+    for (int64_t j = j0 + (threadIdx.x >> 6); j < j1; j += 4) {
+        T* dst = gx + j * sf + n0;
+        if constexpr (VEC == 4 && sizeof(T) == 4) {
+            typedef float F4 __attribute__((ext_vector_type(4)));
+            F4 t = {v.v[0], v.v[1], v.v[2], v.v[3]};
+            __builtin_nontemporal_store(t, reinterpret_cast<F4*>(dst));
+        } else if constexpr (VEC == 2 && sizeof(T) == 8) {
+            typedef double D2 __attribute__((ext_vector_type(2)));
+            D2 t = {v.v[0], v.v[1]};
+            __builtin_nontemporal_store(t, reinterpret_cast<D2*>(dst));
+        } else {
+            vstore<T, VEC>(dst, v);
+        }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_gsum_bwd_generic(const T* __restrict__ g, int64_t B,
                                                           int64_t F, int64_t sb, int64_t sf,
@@ -295,13 +327,15 @@ extern "C" int cl_group_sum_backward(int dtype, const void* grad_out, int64_t ba
         if (stride_batch == 1) {
             const bool wide = batch % W == 0 && stride_feature % W == 0 && aligned(grad_x, 16);
             const int vec = wide ? W : 1;
-            const dim3 grid(unsigned(ceil_div(features, 4)), unsigned(ceil_div(batch, 64 * vec)), 1);
+            const int64_t slice = std::max<int64_t>(std::min<int64_t>(gsz, 32), ceil_div(gsz, 65535));
+            const dim3 grid(unsigned(ceil_div(batch, 64 * vec)), unsigned(k),
+                            unsigned(ceil_div(gsz, slice)));
             if (wide)
-                k_gsum_bwd<T, W, true><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
-                                                           gsz, k, t, gxs);
+                k_gsum_bwd_rows<T, W><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
+                                                          gsz, k, slice, t, gxs);
             else
-                k_gsum_bwd<T, 1, true><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
-                                                           gsz, k, t, gxs);
+                k_gsum_bwd_rows<T, 1><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
+                                                          gsz, k, slice, t, gxs);
         } else if (stride_feature == 1) {
             const bool wide = features % W == 0 && stride_batch % W == 0 && aligned(grad_x, 16);
             const int vec = wide ? W : 1;

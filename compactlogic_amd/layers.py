@@ -16,6 +16,7 @@ import torch
 
 from . import _capi
 from . import difflogic_hip as _dl
+from . import timing
 from .plan import RunPlan, build_run_plan
 
 
@@ -104,48 +105,90 @@ class LogicLayerCudaFunction(torch.autograd.Function):
         return grad_x, None, None, grad_w, None, None, None, None
 
 
+def _chunks(x: torch.Tensor, in_dim: int, out_dim: int) -> int:
+    n = ctypes.c_int64(0)
+    _capi.call("cl_dense_tiled_chunks", _dl.dtype_code(x), x.shape[1], in_dim, out_dim,
+               ctypes.byref(n))
+    return n.value
+
+
 class LogicLayerRunsFunction(torch.autograd.Function):
-    """Dense layer through the connection-run plan: same math as LogicLayerCudaFunction, with
-    shared-pair slots collapsed and both gradients produced by one inverse-index pass."""
+    """Dense layer through the connection-run plan (same math as LogicLayerCudaFunction).
+
+    ``w`` holds logits when ``softmax`` is true (the softmax and its backward run inside the
+    HIP kernels and the gradient returned is that of the logits), else probabilities.  Slots
+    sharing an input pair are collapsed, the batch is tiled in XCD-pinned chunks, and both
+    gradients come from one pass over the inverse index plus a per-neuron finalize (a single
+    whole-batch pass when the input needs no gradient)."""
 
     @staticmethod
-    def forward(ctx, x, w, gate_sequence, plan: RunPlan):
+    def forward(ctx, x, w, gate_sequence, plan: RunPlan, softmax: bool = False):
         _dl._check(x, "x")
         if w.dtype != x.dtype:
             raise RuntimeError("w must have the dtype of x")
         if x.shape[0] != plan.in_dim:
             raise RuntimeError(f"x has {x.shape[0]} rows, the layer expects {plan.in_dim}")
         batch = x.shape[1]
-        y = torch.empty((plan.out_dim, batch), dtype=x.dtype, device=x.device)
-        coef = torch.empty((plan.num_runs, 4), dtype=x.dtype, device=x.device)
         w = w.contiguous()
-        with torch.cuda.device(x.device):
-            _capi.call("cl_dense_forward_runs", _dl.dtype_code(x), x.data_ptr(), w.data_ptr(),
-                       gate_sequence.data_ptr(), plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
-                       plan.run_gl.data_ptr(), y.data_ptr(), coef.data_ptr(), plan.in_dim,
-                       plan.out_dim, plan.num_runs, batch, plan.num_gates, _dl.stream_of(x))
-        ctx.save_for_backward(x, coef, gate_sequence)
+        dev = x.device
+        code = _dl.dtype_code(x)
+        probs = torch.empty_like(w) if softmax else None
+        coef = torch.empty((plan.num_runs, 4), dtype=x.dtype, device=dev)
+        inv_coef = torch.empty((2 * plan.num_runs, 2), dtype=x.dtype, device=dev)
+        y = torch.empty((plan.out_dim, batch), dtype=x.dtype, device=dev)
+        stream = _dl.stream_of(x)
+        with torch.cuda.device(dev):
+            timing.timed(f"cl_dense_prep[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                "cl_dense_prep", code, w.data_ptr(), int(softmax), gate_sequence.data_ptr(),
+                plan.run_ptr.data_ptr(), plan.run_gl.data_ptr(), plan.inv_pos.data_ptr(),
+                _dl.ptr(probs), coef.data_ptr(), inv_coef.data_ptr(), plan.out_dim,
+                plan.num_runs, plan.num_gates, stream))
+            timing.timed(f"cl_dense_forward_tiled[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                "cl_dense_forward_tiled", code, x.data_ptr(), coef.data_ptr(), plan.nab.data_ptr(),
+                plan.run_ab.data_ptr(), y.data_ptr(), plan.in_dim, plan.out_dim, plan.num_runs,
+                batch, stream))
+        ctx.save_for_backward(x, inv_coef, gate_sequence, probs)
         ctx.plan = plan
         return y
 
     @staticmethod
     def backward(ctx, grad_y):
-        x, coef, gate_sequence = ctx.saved_tensors
+        x, inv_coef, gate_sequence, probs = ctx.saved_tensors
         plan: RunPlan = ctx.plan
         grad_y = grad_y.contiguous()
-        grad_x = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        grad_x = torch.empty_like(x) if need_x else None
         grad_w = (torch.empty((plan.out_dim, plan.num_gates), dtype=x.dtype, device=x.device)
-                  if ctx.needs_input_grad[1] else None)
-        if grad_x is not None or grad_w is not None:
-            with torch.cuda.device(x.device):
-                _capi.call("cl_dense_backward_runs", _dl.dtype_code(x), x.data_ptr(),
-                           coef.data_ptr(), gate_sequence.data_ptr(), grad_y.data_ptr(),
-                           plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(),
-                           plan.run_gl.data_ptr(), plan.run_y.data_ptr(),
-                           plan.inv_ptr.data_ptr(), plan.inv_entry.data_ptr(),
-                           _dl.ptr(grad_x), _dl.ptr(grad_w), plan.in_dim, plan.out_dim,
-                           plan.num_runs, x.shape[1], plan.num_gates, _dl.stream_of(x))
-        return grad_x, grad_w, None, None
+                  if need_w else None)
+        code = _dl.dtype_code(x)
+        stream = _dl.stream_of(x)
+        batch = x.shape[1]
+        with torch.cuda.device(x.device):
+            if need_x:
+                moments, nchunks = None, 1
+                if need_w:
+                    nchunks = _chunks(x, plan.in_dim, plan.out_dim)
+                    moments = torch.empty((plan.num_runs, nchunks, 4), dtype=x.dtype,
+                                          device=x.device)
+                timing.timed(f"cl_dense_backward_tiled[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                    "cl_dense_backward_tiled", code, x.data_ptr(), grad_y.data_ptr(),
+                    plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(), plan.slot_rec.data_ptr(),
+                    plan.inv_rec.data_ptr(), inv_coef.data_ptr(), grad_x.data_ptr(),
+                    _dl.ptr(moments), nchunks, plan.in_dim, plan.out_dim, plan.num_runs, batch,
+                    stream))
+                if need_w:
+                    timing.timed(f"cl_dense_backward_finalize[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                        "cl_dense_backward_finalize", code, moments.data_ptr(), nchunks,
+                        gate_sequence.data_ptr(), _dl.ptr(probs), plan.run_ptr.data_ptr(),
+                        plan.run_gl.data_ptr(), grad_w.data_ptr(), plan.out_dim, plan.num_runs,
+                        plan.num_gates, stream))
+            elif need_w:
+                timing.timed(f"cl_dense_weight_grad[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                    "cl_dense_weight_grad", code, x.data_ptr(), grad_y.data_ptr(),
+                    gate_sequence.data_ptr(), _dl.ptr(probs), plan.run_ptr.data_ptr(),
+                    plan.run_ab.data_ptr(), plan.run_gl.data_ptr(), grad_w.data_ptr(),
+                    plan.in_dim, plan.out_dim, plan.num_runs, batch, plan.num_gates, stream))
+        return grad_x, grad_w, None, None, None
 
 
 class GroupSumFunction(torch.autograd.Function):
@@ -170,9 +213,9 @@ class GroupSumFunction(torch.autograd.Function):
                    ctypes.byref(need))
         ws = torch.empty(need.value, dtype=torch.uint8, device=x.device) if need.value else None
         with torch.cuda.device(x.device):
-            _capi.call("cl_group_sum_forward", _dl.dtype_code(x), x.data_ptr(), batch, feats,
-                       sb, sf, k, float(tau), out.data_ptr(), _dl.ptr(ws), need.value,
-                       _dl.stream_of(x))
+            timing.timed("cl_group_sum_forward", lambda: _capi.call(
+                "cl_group_sum_forward", _dl.dtype_code(x), x.data_ptr(), batch, feats, sb, sf, k,
+                float(tau), out.data_ptr(), _dl.ptr(ws), need.value, _dl.stream_of(x)))
         ctx.k, ctx.tau = k, tau
         ctx.shape = (batch, feats)
         ctx.batch_major = sb == 1 and sf != 1
@@ -188,9 +231,9 @@ class GroupSumFunction(torch.autograd.Function):
             grad_x = torch.empty((batch, feats), dtype=grad_out.dtype, device=grad_out.device)
         sb, sf = grad_x.stride()
         with torch.cuda.device(grad_out.device):
-            _capi.call("cl_group_sum_backward", _dl.dtype_code(grad_out), grad_out.data_ptr(),
-                       batch, feats, ctx.k, float(ctx.tau), grad_x.data_ptr(), sb, sf,
-                       _dl.stream_of(grad_out))
+            timing.timed("cl_group_sum_backward", lambda: _capi.call(
+                "cl_group_sum_backward", _dl.dtype_code(grad_out), grad_out.data_ptr(), batch,
+                feats, ctx.k, float(ctx.tau), grad_x.data_ptr(), sb, sf, _dl.stream_of(grad_out)))
         return grad_x, None, None
 
 
@@ -251,9 +294,14 @@ class LogicLayer(torch.nn.Module):
         assert x.ndim == 2, x.ndim
         x = x.transpose(0, 1).contiguous()
         assert x.shape[0] == self.in_dim, (x.shape, self.in_dim)
-        w = torch.nn.functional.softmax(self.weights, dim=-1).to(x.dtype)
         plan = self.run_plan()
-        return LogicLayerRunsFunction.apply(x, w, self.gate_sequence, plan).transpose(0, 1)
+        if self.weights.dtype == x.dtype:
+            # softmax(weights) and its backward run inside the kernels
+            y = LogicLayerRunsFunction.apply(x, self.weights, self.gate_sequence, plan, True)
+        else:
+            w = torch.nn.functional.softmax(self.weights, dim=-1).to(x.dtype)
+            y = LogicLayerRunsFunction.apply(x, w, self.gate_sequence, plan, False)
+        return y.transpose(0, 1)
 
     @torch.no_grad()
     def forward_cuda_eval(self, x):

@@ -8,7 +8,13 @@ with per-slot random wiring most slots are runs of length one.
 
 The plan also carries the inverse index over inputs that the input-gradient kernel walks:
 row i lists the (run, operand side) uses of input i, encoded as 2 * run + side.  Entries
-within a row are in ascending (side, run) order, so the result is deterministic.
+within a row are in ascending (side, run) order, so the result is deterministic.  Each entry
+also has a ready record (neuron, other input, run, side) so the kernel needs no second
+lookup, `inv_pos` maps a run side to its entry (where the per-step coefficients are written),
+and `row_order` lists the inputs by descending entry count so that rows processed side by
+side have equal work.  `nab` and `slot_rec` hold, per neuron and per processing slot, what a
+kernel needs before its first gather (first run's pair and run range; input row and entry
+range), so each is one load away.
 """
 from __future__ import annotations
 
@@ -28,6 +34,11 @@ class RunPlan:
     run_y: torch.Tensor      # int32 [R]
     inv_ptr: torch.Tensor    # int32 [in_dim + 1]
     inv_entry: torch.Tensor  # int32 [2R]
+    inv_rec: torch.Tensor    # int32 [2R, 4]  (neuron, other input, run, side) per entry
+    inv_pos: torch.Tensor    # int32 [2R]     entry position of run side 2r + s
+    row_order: torch.Tensor  # int32 [in_dim] inputs by descending entry count (stable)
+    nab: torch.Tensor        # int32 [out_dim, 4] (a, b of the first run, run_ptr[o], run_ptr[o+1])
+    slot_rec: torch.Tensor   # int32 [in_dim, 4]  (input, first entry, end entry, 0) in row_order
 
     @property
     def num_runs(self) -> int:
@@ -77,6 +88,21 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
     inv_ptr = torch.zeros(in_dim + 1, dtype=torch.int64, device=dev)
     inv_ptr[1:] = torch.cumsum(inv_counts, 0)
     i32 = torch.int32
+    inv_entry = entry[order]
+    ent_run = torch.div(inv_entry, 2, rounding_mode="floor")
+    ent_side = inv_entry - 2 * ent_run
+    ent_other = torch.where(ent_side == 0, rb[ent_run], ra[ent_run])
+    inv_rec = torch.stack((run_y[ent_run], ent_other, ent_run, ent_side), dim=1)
+    inv_pos = torch.empty_like(inv_entry)
+    inv_pos[inv_entry] = torch.arange(inv_entry.numel(), dtype=torch.int64, device=dev)
+    row_order = torch.sort(inv_counts, descending=True, stable=True).indices
+    first = run_ptr[:-1].clamp(max=max(r - 1, 0))
+    has = run_ptr[1:] > run_ptr[:-1]
+    nab = torch.stack((torch.where(has, ra[first] if r else first, 0),
+                       torch.where(has, rb[first] if r else first, 0),
+                       run_ptr[:-1], run_ptr[1:]), dim=1)
+    slot_rec = torch.stack((row_order, inv_ptr[row_order], inv_ptr[row_order + 1],
+                            torch.zeros_like(row_order)), dim=1)
     return RunPlan(
         in_dim=int(in_dim), out_dim=int(out_dim), num_gates=int(g),
         run_ptr=run_ptr.to(i32).contiguous(),
@@ -84,5 +110,10 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
         run_gl=run_gl.to(i32).contiguous(),
         run_y=run_y.to(i32).contiguous(),
         inv_ptr=inv_ptr.to(i32).contiguous(),
-        inv_entry=entry[order].to(i32).contiguous(),
+        inv_entry=inv_entry.to(i32).contiguous(),
+        inv_rec=inv_rec.to(i32).contiguous(),
+        inv_pos=inv_pos.to(i32).contiguous(),
+        row_order=row_order.to(i32).contiguous(),
+        nab=nab.to(i32).contiguous(),
+        slot_rec=slot_rec.to(i32).contiguous(),
     )

@@ -86,44 +86,78 @@ int cl_dense_eval(int dtype, const void* x, const int64_t* a, const int64_t* b,
                   int64_t out_dim, int64_t batch, int64_t num_gates, void* stream);
 
 /* -------------------------------------------------------------------------------------------
- * Dense LogicLayer through a connection-run plan (no reference counterpart: the plan is
- * derived from `indices` by the module and regenerated whenever the indices change).
+ * Dense LogicLayer training path through a connection-run plan (no reference counterpart:
+ * the plan is derived from `indices` by the module and regenerated whenever they change).
  *
  * A run is a maximal range of consecutive slots [g0, g0+len) of one neuron whose slots share
- * one input pair (a, b).  Because the relaxed operators are affine in each weight, a run
- * collapses to four coefficients K = sum_{g in run} w[o,g] * (c0, c1, c2, c3)[gate_seq[o,g]],
- * so each run costs two row gathers however many slots it spans.
- *   run_ptr  int32 [out_dim + 1]   runs of neuron o are run_ptr[o] .. run_ptr[o+1]-1
- *   run_ab   int32 [num_runs, 2]   input pair (a, b) of the run
- *   run_gl   int32 [num_runs]      g0 | (len << 8)
- *   run_y    int32 [num_runs]      neuron of the run
- *   inv_ptr  int32 [in_dim + 1]    inverse index over inputs ...
- *   inv_entry int32 [2 * num_runs] ... entries 2*r + side (side 0: operand a, 1: operand b)
+ * one input pair (a, b).  The relaxed operators are affine in the gate weights, so a run
+ * collapses to four coefficients K = sum_{g in run} p[o,g] * (c0, c1, c2, c3)[gate_seq[o,g]]
+ * and costs two row gathers however many slots it spans.
+ *   run_ptr   int32 [out_dim + 1]   runs of neuron o are run_ptr[o] .. run_ptr[o+1]-1
+ *   run_ab    int32 [num_runs, 2]   input pair (a, b) of the run
+ *   run_gl    int32 [num_runs]      g0 | (len << 8)
+ *   run_y     int32 [num_runs]      neuron of the run
+ *   inv_ptr   int32 [in_dim + 1]    inverse index over inputs ...
+ *   inv_entry int32 [2 * num_runs]  ... entries 2*r + side (side 0: operand a, 1: operand b)
+ *   inv_rec   int32 [2R, 4]         per entry: neuron, other input, run, side
+ *   inv_pos   int32 [2R]            entry position of run side 2r + side
+ *   nab       int32 [out_dim, 4]    a, b of the first run, run_ptr[o], run_ptr[o+1]
+ *   slot_rec  int32 [in_dim, 4]     input row, first entry, end entry, 0 -- by descending
+ *                                   entry count
+ *   run_coef  T [num_runs, 4]       K of every run
+ *
+ * The batch is processed in chunks pinned to XCDs (see dense_tiled.hip); when
+ * batch % (16 / sizeof(T)) == 0 the row buffers must be 16-byte aligned.
  * ----------------------------------------------------------------------------------------- */
 
-/* Forward through the plan.  When run_coef (T [num_runs, 4]) is not NULL the collapsed
- * coefficients K of every run are also written there, for cl_dense_backward_runs. */
-int cl_dense_forward_runs(int dtype, const void* x, const void* w, const uint8_t* gate_seq,
-                          const int32_t* run_ptr, const int32_t* run_ab, const int32_t* run_gl,
-                          void* y, void* run_coef, int64_t in_dim, int64_t out_dim,
-                          int64_t num_runs, int64_t batch, int64_t num_gates, void* stream);
+/* Probabilities (softmax of w over the slots when `softmax` is non-zero, else w itself;
+ * written to `probs` when not NULL) and the run coefficients K (run_coef, 16-byte aligned).
+ * With inv_coef (T [2 * num_runs, 2], may be NULL) the coefficients of every inverse-index
+ * entry are also written at inv_pos[2r + side]: (K1, K3) for side 0, (K2, K3) for side 1. */
+int cl_dense_prep(int dtype, const void* w, int softmax, const uint8_t* gate_seq,
+                  const int32_t* run_ptr, const int32_t* run_gl, const int32_t* inv_pos,
+                  void* probs, void* run_coef, void* inv_coef, int64_t out_dim,
+                  int64_t num_runs, int64_t num_gates, void* stream);
 
-/* The run coefficients K alone: run_coef[r] = sum_{g in run r} w[o, g] * (c0, c1, c2, c3). */
-int cl_dense_run_coefs(int dtype, const void* w, const uint8_t* gate_seq, const int32_t* run_ptr,
-                       const int32_t* run_gl, void* run_coef, int64_t out_dim, int64_t num_runs,
-                       int64_t num_gates, void* stream);
+/* y[o, n] = sum over the runs of o of K0 + K1 x[a, n] + K2 x[b, n] + K3 x[a, n] x[b, n], with
+ * nab[o] = (a, b of o's first run, run_ptr[o], run_ptr[o+1]) (int32 [out_dim, 4], 16-byte
+ * aligned) and run_ab for the further runs of a neuron. */
+int cl_dense_forward_tiled(int dtype, const void* x, const void* run_coef, const int32_t* nab,
+                           const int32_t* run_ab, void* y, int64_t in_dim, int64_t out_dim,
+                           int64_t num_runs, int64_t batch, void* stream);
 
-/* Backward through the plan, from the run coefficients of the forward pass.  grad_x and/or
- * grad_w may be NULL when not needed (run_coef, run_y and the inverse index are only read
- * for grad_x).  When both are requested they come from one pass over the inverse index (the
- * weight moments of each run are taken at its operand-a entry).  grad_w is the gradient with
- * respect to w (the probabilities). */
-int cl_dense_backward_runs(int dtype, const void* x, const void* run_coef,
-                           const uint8_t* gate_seq, const void* grad_y, const int32_t* run_ptr,
-                           const int32_t* run_ab, const int32_t* run_gl, const int32_t* run_y,
-                           const int32_t* inv_ptr, const int32_t* inv_entry, void* grad_x,
-                           void* grad_w, int64_t in_dim, int64_t out_dim, int64_t num_runs,
-                           int64_t batch, int64_t num_gates, void* stream);
+/* Weight gradient of every slot straight from the whole batch (no chunked moments), with the
+ * softmax backward when probs is not NULL: for layers whose input needs no gradient. */
+int cl_dense_weight_grad(int dtype, const void* x, const void* grad_y, const uint8_t* gate_seq,
+                         const void* probs, const int32_t* run_ptr, const int32_t* run_ab,
+                         const int32_t* run_gl, void* grad_w, int64_t in_dim, int64_t out_dim,
+                         int64_t num_runs, int64_t batch, int64_t num_gates, void* stream);
+
+/* Number of batch chunks of the backward tiling (the middle dimension of `moments`). */
+int cl_dense_tiled_chunks(int dtype, int64_t batch, int64_t in_dim, int64_t out_dim,
+                          int64_t* nchunks);
+
+/* Backward through the plan.  grad_x (may be NULL) receives the input gradient, walking the
+ * inverse index slot by slot: slot_rec[s] = (input row, first entry, end entry, 0) (int32
+ * [in_dim, 4]) in descending order of entry count, entry records inv_rec[e] = (neuron, other
+ * input, run, side) (int32 [2 * num_runs, 4]) and the entry coefficients inv_coef of
+ * cl_dense_prep (all 16-byte aligned).  moments (T [num_runs, nchunks, 4], may be NULL)
+ * receives the per-chunk batch moments (sum gy, gy a, gy b, gy a b) of every run: at its
+ * operand-a entry when grad_x is computed in the same pass, else per neuron from run_ptr /
+ * run_ab. */
+int cl_dense_backward_tiled(int dtype, const void* x, const void* grad_y, const int32_t* run_ptr,
+                            const int32_t* run_ab, const int32_t* slot_rec,
+                            const int32_t* inv_rec, const void* inv_coef, void* grad_x,
+                            void* moments, int64_t nchunks, int64_t in_dim, int64_t out_dim,
+                            int64_t num_runs, int64_t batch, void* stream);
+
+/* Weight gradient from the moments: grad_w[o, g] = (c0, c1, c2, c3)[gate_seq[o,g]] . (moments
+ * of g's run summed over the chunks in chunk order); with `probs` (not NULL) followed by the
+ * softmax backward, giving the gradient of the logits. */
+int cl_dense_backward_finalize(int dtype, const void* moments, int64_t nchunks,
+                               const uint8_t* gate_seq, const void* probs, const int32_t* run_ptr,
+                               const int32_t* run_gl, void* grad_w, int64_t out_dim,
+                               int64_t num_runs, int64_t num_gates, void* stream);
 
 /* -------------------------------------------------------------------------------------------
  * GroupSum -- compactlogic/compactlogic.py:450-468: out[n, c] = sum_{j in group c} x[n, j] / tau

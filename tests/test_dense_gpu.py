@@ -56,6 +56,8 @@ SHAPES = [
     (300, 256, 16, 1024, True),
     (64, 80, 8, 2500, False),
     (784, 500, 16, 128, True),
+    (40, 30, 128, 40, False),
+    (1000, 600, 16, 4096, True),
 ]
 
 
@@ -101,6 +103,28 @@ def test_run_plan_kernels_match_oracle(device, dtype, shape):
     y2 = cl.LogicLayerRunsFunction.apply(D["x"], w2, D["gs"], plan)
     (gw2,) = torch.autograd.grad(y2, (w2,), D["gy"])
     np.testing.assert_allclose(np_(gw2), np_(gw), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_run_plan_softmax_path_matches_oracle(device, dtype, shape):
+    """Logits in, softmax inside the kernels: forward and the gradient of the logits."""
+    in_dim, out_dim, g_n, batch, shared = shape
+    L = make_layer(hash(shape) % 1000 + 2, in_dim, out_dim, g_n, batch, shared)
+    D = to_dev(L, device, dtype)
+    logits = np.log(L["w"]) + np.random.default_rng(3).standard_normal((out_dim, 1))
+    lt = torch.as_tensor(logits, dtype=dtype, device=device).requires_grad_(True)
+    plan = cl.build_run_plan(torch.stack([D["a"], D["b"]]), in_dim)
+    x = D["x"].clone().requires_grad_(True)
+    y = cl.LogicLayerRunsFunction.apply(x, lt, D["gs"], plan, True)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    np.testing.assert_allclose(np_(y), O.dense_forward(L["x"], L["a"], L["b"], p, L["gs"]), **TOL[dtype])
+    gx, gl = torch.autograd.grad(y, (x, lt), D["gy"])
+    gp = O.dense_backward_w(L["x"], L["a"], L["b"], L["gs"], L["gy"])
+    np.testing.assert_allclose(np_(gl), p * (gp - (p * gp).sum(1, keepdims=True)), **TOL[dtype])
+    np.testing.assert_allclose(np_(gx), O.dense_backward_x_direct(L["x"], L["a"], L["b"], p,
+                                                                 L["gs"], L["gy"]), **TOL[dtype])
 
 
 def test_eval_matches_truth_table(device):
