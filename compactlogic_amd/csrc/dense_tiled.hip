@@ -421,15 +421,15 @@ __global__ __launch_bounds__(256) void k_wgrad_full(const T* __restrict__ x, con
 }
 
 // ------------------------------------------------------------------------------------------
-// k_bwd_tiled: LPN lanes per input-row segment; rows are taken in processing-slot order
-// (descending entry count, so the lane groups of a wave have equal work), and slot_rec[slot]
-// = (input row, first entry, end entry) is one load.  Entry e of the inverse index
-// carries a record (neuron, other input, run, side) and the coefficients (own-operand K, K3)
-// written by k_prep, so each entry costs one record load followed by the two row loads; the
-// next entry's record is fetched while the current one is processed.
+// k_bwd_tiled: LPN lanes per input-row segment, NPG rows per lane group.  Rows are taken in
+// processing-slot order (descending entry count, so the rows of a group and the groups of a
+// wave have nearly equal work), and slot_rec[slot] = (input row, first entry, end entry) is
+// one load.  Entry e of the inverse index carries a record (neuron, other input, run, side)
+// and the coefficients (own-operand K, K3) written by k_prep; the records of the group's NPG
+// rows for the next step are fetched while the current step's row loads are in flight.
 // part[(r * nchunks + c) * 4 + j] receives the chunk-c moments of run r (WANT_GW) at the
 // run's operand-a entry.
-template <typename T, int VEC, int LPN, bool WANT_GX, bool WANT_GW>
+template <typename T, int VEC, int LPN, int NPG, bool WANT_GX, bool WANT_GW>
 __global__ __launch_bounds__(256) void k_bwd_tiled(
     const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
     const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef, T* __restrict__ gx,
@@ -438,74 +438,111 @@ __global__ __launch_bounds__(256) void k_bwd_tiled(
     using V = typename VT<T, VEC>::type;
     using V2 = typename VT<T, 2>::type;
     using V4 = typename VT<T, 4>::type;
-    constexpr int NT = 256 / LPN;
+    constexpr int GROUPS = 256 / LPN;
     int64_t c, t;
     if (!map_tile(tm, blockIdx.x, c, t)) return;
-    const int64_t slot = t * NT + threadIdx.x / LPN;
-    if (slot >= in_dim) return;  // uniform per lane group
-    const int4 sr = slot_rec[slot];
-    const int64_t i = sr.x;
-    if (uint64_t(i) >= uint64_t(in_dim)) return;
+    const int64_t slot0 = (t * GROUPS + threadIdx.x / LPN) * NPG;
+    if (slot0 >= in_dim) return;  // uniform per lane group
     const int64_t idx = c * (LPN * VEC) + int64_t(threadIdx.x % LPN) * VEC;
     const bool col = idx < B;
     const bool leader = (threadIdx.x % LPN) == 0;
 
-    V xi = V(T(0));
-    if (WANT_GW && col) xi = vld<V>(x + i * B + idx);
-    V acc = V(T(0));
-    bool bad = false;
-    int64_t e0 = sr.y, e1 = sr.z;
-    if (e0 < 0 || e1 < e0 || e1 > 2 * num_runs) {
-        bad = true;
-        e1 = e0;
+    int64_t row[NPG], e0[NPG], deg[NPG];
+    bool live[NPG], bad[NPG];
+    int64_t maxdeg = 0;
+#pragma unroll
+    for (int j = 0; j < NPG; ++j) {
+        live[j] = slot0 + j < in_dim;
+        const int4 sr = live[j] ? slot_rec[slot0 + j] : make_int4(0, 0, 0, 0);
+        row[j] = sr.x;
+        e0[j] = sr.y;
+        deg[j] = int64_t(sr.z) - sr.y;
+        bad[j] = false;
+        if (live[j] && (uint64_t(row[j]) >= uint64_t(in_dim) || sr.y < 0 || deg[j] < 0 ||
+                        sr.z > 2 * num_runs)) {
+            live[j] = false;  // corrupt slot record: nothing is read or written for it
+            deg[j] = 0;
+        }
+        if (!live[j]) deg[j] = 0;
+        maxdeg = deg[j] > maxdeg ? deg[j] : maxdeg;
     }
-    int4 rec = make_int4(0, 0, 0, 0);
-    V2 kk = V2(T(0));
-    if (e0 < e1) {
-        rec = inv_rec[e0];
-        kk = vld<V2>(inv_coef + 2 * e0);
+    V xi[NPG], acc[NPG];
+#pragma unroll
+    for (int j = 0; j < NPG; ++j) {
+        acc[j] = V(T(0));
+        xi[j] = V(T(0));
+        if (WANT_GW && live[j] && col) xi[j] = vld<V>(x + row[j] * B + idx);
     }
-    for (int64_t e = e0; e < e1; ++e) {
-        const int4 cur = rec;
-        const V2 ck = kk;
-        if (e + 1 < e1) {
-            rec = inv_rec[e + 1];
-            kk = vld<V2>(inv_coef + 2 * (e + 1));
+    int4 rec[NPG];
+    V2 kk[NPG];
+#pragma unroll
+    for (int j = 0; j < NPG; ++j) {
+        rec[j] = make_int4(0, 0, 0, 0);
+        kk[j] = V2(T(0));
+        if (deg[j] > 0) {
+            rec[j] = inv_rec[e0[j]];
+            kk[j] = vld<V2>(inv_coef + 2 * e0[j]);
         }
-        const int64_t yo = cur.x, other = cur.y, r = cur.z;
-        const int side = cur.w;
-        if (uint64_t(yo) >= uint64_t(out_dim) || uint64_t(other) >= uint64_t(in_dim) ||
-            uint64_t(r) >= uint64_t(num_runs)) {
-            bad = true;
-            continue;
+    }
+    for (int64_t k = 0; k < maxdeg; ++k) {
+        int4 cur[NPG];
+        V2 ck[NPG];
+        V vo[NPG], vg[NPG];
+        bool use[NPG];
+#pragma unroll
+        for (int j = 0; j < NPG; ++j) {
+            cur[j] = rec[j];
+            ck[j] = kk[j];
+            if (k + 1 < deg[j]) {
+                rec[j] = inv_rec[e0[j] + k + 1];
+                kk[j] = vld<V2>(inv_coef + 2 * (e0[j] + k + 1));
+            }
+            use[j] = k < deg[j];
+            if (use[j] && (uint64_t(cur[j].x) >= uint64_t(out_dim) ||
+                           uint64_t(cur[j].y) >= uint64_t(in_dim) ||
+                           uint64_t(cur[j].z) >= uint64_t(num_runs))) {
+                bad[j] = true;
+                use[j] = false;
+            }
+            vo[j] = V(T(0));
+            vg[j] = V(T(0));
+            if (use[j] && col) {
+                vo[j] = vld<V>(x + int64_t(cur[j].y) * B + idx);
+                vg[j] = vld<V>(gy + int64_t(cur[j].x) * B + idx);
+            }
         }
-        V vo = V(T(0)), vg = V(T(0));
-        if (col) {
-            vo = vld<V>(x + other * B + idx);
-            vg = vld<V>(gy + yo * B + idx);
-        }
-        if (WANT_GX) acc += (ck[0] + ck[1] * vo) * vg;
-        if (WANT_GW && side == 0) {
-            const V ga = vg * xi;
-            T s1 = hsum<T, VEC>(vg), sa = hsum<T, VEC>(ga);
-            T sb = hsum<T, VEC>(vg * vo), sab = hsum<T, VEC>(ga * vo);
-            s1 = group_sum<LPN>(s1);
-            sa = group_sum<LPN>(sa);
-            sb = group_sum<LPN>(sb);
-            sab = group_sum<LPN>(sab);
-            if (leader) {
-                V4 mv;
-                mv[0] = s1;
-                mv[1] = sa;
-                mv[2] = sb;
-                mv[3] = sab;
-                *reinterpret_cast<V4*>(part + (r * tm.nchunks + c) * 4) = mv;
+#pragma unroll
+        for (int j = 0; j < NPG; ++j) {
+            if (!use[j]) continue;
+            const int side = cur[j].w;
+            if (WANT_GX) acc[j] += (ck[j][0] + ck[j][1] * vo[j]) * vg[j];
+            if (WANT_GW && side == 0) {
+                const V ga = vg[j] * xi[j];
+                T s1 = hsum<T, VEC>(vg[j]), sa = hsum<T, VEC>(ga);
+                T sb = hsum<T, VEC>(vg[j] * vo[j]), sab = hsum<T, VEC>(ga * vo[j]);
+                s1 = group_sum<LPN>(s1);
+                sa = group_sum<LPN>(sa);
+                sb = group_sum<LPN>(sb);
+                sab = group_sum<LPN>(sab);
+                if (leader) {
+                    V4 mv;
+                    mv[0] = s1;
+                    mv[1] = sa;
+                    mv[2] = sb;
+                    mv[3] = sab;
+                    *reinterpret_cast<V4*>(part + (int64_t(cur[j].z) * tm.nchunks + c) * 4) = mv;
+                }
             }
         }
     }
     if (WANT_GX && col) {
-        if (bad) acc = V(nan_of<T>());
-        vst_stream<V>(gx + i * B + idx, acc);
+#pragma unroll
+        for (int j = 0; j < NPG; ++j) {
+            if (!live[j]) continue;
+            V r = acc[j];
+            if (bad[j]) r = V(nan_of<T>());
+            vst_stream<V>(gx + row[j] * B + idx, r);
+        }
     }
 }
 
@@ -668,6 +705,9 @@ using namespace cl;
 #endif
 #ifndef CL_FWD_NPG
 #define CL_FWD_NPG 2
+#endif
+#ifndef CL_BWD_NPG
+#define CL_BWD_NPG 1
 #endif
 
 namespace {
@@ -864,18 +904,18 @@ extern "C" int cl_dense_backward_tiled(int dtype, const void* x, const void* gra
         auto* gxs = static_cast<T*>(grad_x);
         auto* mom = static_cast<T*>(moments);
         if (grad_x && in_dim > 0) {
-            const Tiling tl = choose_tiling<T>(batch, in_dim, v, CL_BWD_LPN);
+            const Tiling tl = choose_tiling<T>(batch, in_dim, v, CL_BWD_LPN, CL_BWD_NPG);
             const unsigned grid = unsigned(tile_grid(tl.map));
             if (moments) {
                 CL_ARG(nchunks == tl.map.nchunks, "moments buffer must use the backward chunk count");
                 with_tiling<T>(tl, [&](auto vc, auto lc) {
-                    k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, true, true>
+                    k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, CL_BWD_NPG, true, true>
                         <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gxs, mom,
                                               in_dim, out_dim, num_runs, batch, tl.map);
                 });
             } else {
                 with_tiling<T>(tl, [&](auto vc, auto lc) {
-                    k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, true, false>
+                    k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, CL_BWD_NPG, true, false>
                         <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gxs, mom,
                                               in_dim, out_dim, num_runs, batch, tl.map);
                 });
