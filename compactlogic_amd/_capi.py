@@ -46,6 +46,12 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_backward_tiled": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
                                 _i64, _i64, _p],
     "cl_dense_backward_finalize": [_int, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "cl_conv_forward": [_int, _p, _p, _p, _p, _p, _p, _p] + [_i64] * 9 + [_p],
+    "cl_conv_eval": [_int, _p, _p, _p, _p, _p, _p, _p] + [_i64] * 9 + [_p],
+    "cl_conv_backward_w": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64] + [_i64] * 9 + [_p],
+    "cl_conv_backward_w_workspace": [_int] + [_i64] * 9 + [ctypes.POINTER(_i64)],
+    "cl_conv_backward_x": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p] + [_i64] * 9 + [_p],
+    "cl_eval_packed_indexed": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_group_sum_forward": [_int, _p, _i64, _i64, _i64, _i64, _i64, _f64, _p, _p, _i64, _p],
     "cl_group_sum_workspace_size": [_int, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
     "cl_group_sum_backward": [_int, _p, _i64, _i64, _i64, _f64, _p, _i64, _i64, _p],

@@ -6,11 +6,18 @@ to the device, so every run (and the CPU baseline) sees identical parameters and
   cfg1  LogicLayer 784->8000 x4, G=16, GroupSum(10, tau=10), batch 128, inputs Bernoulli(0.5)
   cfg2  LogicLayer 784->12000 then 12000->12000 x5, G=16, GroupSum(10, 10), batch 1024,
         inputs Bernoulli(0.3)
+  cfg3  ConvLayer((9,32,32), pad 1, c_out 256, ks 3, stride 2) -> ConvLayer((256,16,16), pad 0,
+        c_out 512, ks 3, stride 2) -> flatten 25088 -> LogicLayer 16000 x2, G=16,
+        GroupSum(10, tau=30), batch 256, inputs Bernoulli(0.5)
   cfg4  the cfg2 network frozen to argmax gates (uniform opcode per neuron), 2^24 samples
         bit-packed 64 per word
+  cfg5  the cfg3 network with G=4, each row's gate_sequence 4 distinct seeded opcodes, frozen
+        to the argmax of N(0, 1) logits; 2^20 samples bit-packed 64 per word
 
 Dense wiring of these configs: one input pair (a, b) per neuron, drawn uniformly and shared
-by its 16 slots; gate_sequence = arange(16); logits ~ N(0, 1).
+by its slots; gate_sequence = arange(G) & 15 unless stated; logits ~ N(0, 1).  Conv layers
+draw their taps with ConvLayer's own sampler (num_chn = 1: channel c mod c_in, offsets
+uniform in [0, ks) minus the padding, coinciding operands re-drawn) under a seeded global RNG.
 """
 from __future__ import annotations
 
@@ -18,7 +25,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-from .layers import GroupSum, LogicLayer
+from .layers import ConvLayer, GroupSum, LogicLayer
 
 NET_SEED, INPUT_SEED, LABEL_SEED = 0, 1, 2
 
@@ -46,6 +53,27 @@ CONFIGS = {
 }
 
 
+@dataclass
+class ConvConfig:
+    name: str
+    in_shape: tuple
+    convs: list          # (c_out, ks, stride, padding) per ConvLayer
+    widths: list         # dense LogicLayers after the flatten
+    batch: int
+    p_one: float = 0.5
+    k: int = 10
+    tau: float = 30.0
+    num_gates: int = 16
+    gate_subset: bool = False   # per-row gate_sequence = num_gates distinct seeded opcodes
+
+
+CONV_CONFIGS = {
+    "cfg3": ConvConfig("cfg3", (9, 32, 32), [(256, 3, 2, 1), (512, 3, 2, 0)], [16000, 16000], 256),
+    "cfg5": ConvConfig("cfg5", (9, 32, 32), [(256, 3, 2, 1), (512, 3, 2, 0)], [16000, 16000], 256,
+                       num_gates=4, gate_subset=True),
+}
+
+
 def _seeded_layer(in_dim: int, out_dim: int, gen: torch.Generator, num_gates: int) -> LogicLayer:
     # Build without disturbing the global RNG, then overwrite the draws from `gen`.
     with torch.random.fork_rng(devices=[]):
@@ -67,6 +95,58 @@ def dense_network(cfg: DenseConfig, device="cuda", seed: int = NET_SEED) -> torc
     layers = [_seeded_layer(i, o, gen, cfg.num_gates) for i, o in cfg.dims]
     model = torch.nn.Sequential(*layers, GroupSum(cfg.k, cfg.tau))
     return model.to(device)
+
+
+def _gate_subsets(rows: int, num_gates: int, gen: torch.Generator) -> torch.Tensor:
+    """rows x num_gates distinct opcodes per row: the first num_gates of a seeded permutation
+    of 0..15 (the resampler's gate pool, compactlogic/compactlogic.py:315-321)."""
+    return torch.argsort(torch.rand((rows, 16), generator=gen), dim=1)[:, :num_gates].to(torch.uint8)
+
+
+def conv_network(cfg: ConvConfig, device="cuda", seed: int = NET_SEED) -> torch.nn.Sequential:
+    gen = torch.Generator().manual_seed(seed)
+    layers = []
+    shape = cfg.in_shape
+    for c_out, ks, stride, pad in cfg.convs:
+        layer_seed = int(torch.randint(0, 2**31 - 1, (1,), generator=gen))
+        with torch.random.fork_rng(devices=[]):
+            torch.manual_seed(layer_seed)
+            layer = ConvLayer(shape, padding=pad, c_out=c_out, ks=ks, stride=stride, num_chn=1,
+                              num_gates=cfg.num_gates)
+        with torch.no_grad():
+            layer.weights.copy_(torch.randn((c_out, cfg.num_gates), generator=gen))
+            if cfg.gate_subset:
+                layer.gate_sequence.copy_(_gate_subsets(c_out, cfg.num_gates, gen))
+        layers.append(layer)
+        shape = layer.out_shape
+    layers.append(torch.nn.Flatten())
+    in_dim = int(shape[0] * shape[1] * shape[2])
+    for out_dim in cfg.widths:
+        layer = _seeded_layer(in_dim, out_dim, gen, cfg.num_gates)
+        if cfg.gate_subset:
+            with torch.no_grad():
+                layer.gate_sequence.copy_(_gate_subsets(out_dim, cfg.num_gates, gen))
+        layers.append(layer)
+        in_dim = out_dim
+    model = torch.nn.Sequential(*layers, GroupSum(cfg.k, cfg.tau))
+    return model.to(device)
+
+
+def conv_inputs(cfg: ConvConfig, device="cuda", batch: int | None = None):
+    batch = cfg.batch if batch is None else batch
+    gx = torch.Generator().manual_seed(INPUT_SEED)
+    gl = torch.Generator().manual_seed(LABEL_SEED)
+    x = (torch.rand((batch,) + tuple(cfg.in_shape), generator=gx) < cfg.p_one).float()
+    labels = torch.randint(0, cfg.k, (batch,), generator=gl)
+    return x.to(device), labels.to(device)
+
+
+def freeze_argmax(model: torch.nn.Sequential) -> None:
+    """cfg5: fix every layer to the argmax slot of its logits."""
+    for layer in model:
+        if isinstance(layer, LogicLayer):
+            layer.freeze()
+    model.eval()
 
 
 def dense_inputs(cfg: DenseConfig, device="cuda", batch: int | None = None):

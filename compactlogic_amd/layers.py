@@ -15,6 +15,7 @@ import numpy as np
 import torch
 
 from . import _capi
+from . import convlogic_hip as _cl
 from . import difflogic_hip as _dl
 from . import timing
 from .plan import RunPlan, build_run_plan
@@ -511,6 +512,297 @@ class LogicLayer(torch.nn.Module):
         used = torch.unique(torch.cat((pair[0][y_flag & uses_a], pair[1][y_flag & uses_b])))
         x_flag[used] = True
         y_flag[only_a | only_b] = False
+        return x_flag, y_flag
+
+
+class ConvLayerCudaFunction(torch.autograd.Function):
+    """Autograd bridge for the conv kernels, argument list as in
+    compactlogic/compactlogic.py:838-867: (x, offsets_ch, offsets_h, offsets_w, w,
+    gate_sequence, stride, pad, ks) with ``w`` the gate probabilities."""
+
+    @staticmethod
+    def forward(ctx, x, offsets_ch, offsets_h, offsets_w, w, gate_sequence, stride, pad, ks):
+        y = timing.timed(_conv_name("cl_conv_forward", x, w), lambda: _cl.forward(
+            x, offsets_ch, offsets_h, offsets_w, w, gate_sequence, stride, pad, ks))
+        ctx.save_for_backward(x, offsets_ch, offsets_h, offsets_w, w, gate_sequence)
+        ctx.stride = stride
+        ctx.pad = pad
+        ctx.index = (_cl.inverse_index(offsets_ch, offsets_h, offsets_w, x.shape[1], stride)
+                     if ctx.needs_input_grad[0] else None)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        x, offsets_ch, offsets_h, offsets_w, w, gate_sequence = ctx.saved_tensors
+        grad_y = grad_y.contiguous()
+        grad_x = grad_w = None
+        if ctx.needs_input_grad[0]:
+            grad_x = timing.timed(_conv_name("cl_conv_backward_x", x, w), lambda: _cl.backward_x(
+                x, offsets_ch, offsets_h, offsets_w, w, gate_sequence, grad_y, ctx.stride, ctx.pad,
+                ctx.index))
+        if ctx.needs_input_grad[4]:
+            grad_w = timing.timed(_conv_name("cl_conv_backward_w", x, w), lambda: _cl.backward_w(
+                x, offsets_ch, offsets_h, offsets_w, gate_sequence, grad_y, ctx.stride))
+        return grad_x, None, None, None, grad_w, None, None, None, None
+
+
+class ConvLayerSoftmaxFunction(torch.autograd.Function):
+    """ConvLayerCudaFunction with the softmax over the gate logits folded in: the forward
+    computes the probabilities once, and the weight-gradient kernel applies the softmax
+    backward in its final reduction, returning the gradient of the logits."""
+
+    @staticmethod
+    def forward(ctx, x, offsets_ch, offsets_h, offsets_w, logits, gate_sequence, stride, pad, ks):
+        probs = torch.softmax(logits, dim=-1).contiguous()
+        y = timing.timed(_conv_name("cl_conv_forward", x, probs), lambda: _cl.forward(
+            x, offsets_ch, offsets_h, offsets_w, probs, gate_sequence, stride, pad, ks))
+        ctx.save_for_backward(x, offsets_ch, offsets_h, offsets_w, probs, gate_sequence)
+        ctx.stride = stride
+        ctx.pad = pad
+        ctx.index = (_cl.inverse_index(offsets_ch, offsets_h, offsets_w, x.shape[1], stride)
+                     if ctx.needs_input_grad[0] else None)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        x, offsets_ch, offsets_h, offsets_w, probs, gate_sequence = ctx.saved_tensors
+        grad_y = grad_y.contiguous()
+        grad_x = grad_w = None
+        if ctx.needs_input_grad[0]:
+            grad_x = timing.timed(_conv_name("cl_conv_backward_x", x, probs), lambda: _cl.backward_x(
+                x, offsets_ch, offsets_h, offsets_w, probs, gate_sequence, grad_y, ctx.stride,
+                ctx.pad, ctx.index))
+        if ctx.needs_input_grad[4]:
+            grad_w = timing.timed(_conv_name("cl_conv_backward_w", x, probs), lambda: _cl.backward_w(
+                x, offsets_ch, offsets_h, offsets_w, gate_sequence, grad_y, ctx.stride, probs))
+        return grad_x, None, None, None, grad_w, None, None, None, None
+
+
+def _conv_name(entry: str, x: torch.Tensor, w: torch.Tensor) -> str:
+    return f"{entry}[{x.shape[1]}x{x.shape[2]}x{x.shape[3]}->{w.shape[0]}]"
+
+
+class ConvLayer(LogicLayer):
+    """Convolutional logic layer (compactlogic/compactlogic.py:514-835).
+
+    ``in_shape`` = (c_in, h, w) of the unpadded input; every output channel has ``num_gates``
+    candidate slots, each reading two taps (channel, dh, dw) of the receptive field of size
+    ``ks``; taps outside the input plane read 0.  ``num_chn`` selects the channel sampling:
+    0 uniform, 1 channel c mod c_in for output channel c, > 1 groups of ``num_chn`` input
+    channels.  Buffers ``offsets_ch`` int32, ``offsets_h`` / ``offsets_w`` int8, all
+    [2, c_out, G], hold the spatial offsets already shifted by ``-padding``; ``in_dim`` counts
+    the padded plane and ``out_dim`` = c_out * h_out * w_out, as in the reference.
+    """
+
+    def __init__(self, in_shape, padding: int, c_out: int, ks: int, stride: int,
+                 num_chn: int = 1, **kwargs):
+        self.padding = padding
+        self.c_in = in_shape[0]
+        self.h_in = in_shape[1] + 2 * padding
+        self.w_in = in_shape[2] + 2 * padding
+        self.in_dim = int(np.prod((self.c_in, self.h_in, self.w_in)))
+        self.in_shape = tuple(in_shape)
+        self.c_out = c_out
+        self.ks = ks
+        self.stride = stride
+        self.h_out = (self.h_in - self.ks) // self.stride + 1
+        self.w_out = (self.w_in - self.ks) // self.stride + 1
+        self.out_shape = (self.c_out, self.h_out, self.w_out)
+        self.out_dim = int(np.prod(self.out_shape))
+        self.chn_grp = num_chn if num_chn <= 1 else (self.c_in // num_chn)
+        super().__init__(self.in_dim, self.out_dim, **kwargs)
+        self._packed_key = None
+        self._packed_tables = None
+
+    def forward_cuda(self, x):
+        """x [N, c_in, h, w] -> [N, c_out, h_out, w_out] (:598-626)."""
+        assert tuple(x.shape[1:]) == self.in_shape, f'input shape mismatch {x.shape}, {self.in_shape}'
+        assert x.ndim == 4, x.ndim
+        x = x.contiguous()
+        if self.weights.dtype == x.dtype and self.num_gates <= 64:
+            return ConvLayerSoftmaxFunction.apply(
+                x, self.offsets_ch, self.offsets_h, self.offsets_w, self.weights,
+                self.gate_sequence, self.stride, self.padding, self.ks)
+        w = torch.nn.functional.softmax(self.weights, dim=-1).to(x.dtype)
+        return ConvLayerCudaFunction.apply(
+            x, self.offsets_ch, self.offsets_h, self.offsets_w, w, self.gate_sequence,
+            self.stride, self.padding, self.ks)
+
+    @torch.no_grad()
+    def forward_cuda_eval(self, x):
+        """Discrete conv with the argmax slot per output channel (:628-640).  A
+        PackBitsTensor (rows = the c_in * h * w input features in NCHW order) is evaluated
+        bitwise and updated in place; its rows become the c_out * h_out * w_out outputs."""
+        assert self.is_frozen or not self.training
+        w = getattr(self, "w", None)
+        if w is None:
+            w = self.weights.argmax(-1).to(dtype=torch.uint8, device=self.weights.device)
+        if isinstance(x, PackBitsTensor):
+            ia, ib, gate = self.packed_tables(w)
+            assert x.t.shape[0] == int(np.prod(self.in_shape)), (x.t.shape, self.in_shape)
+            x.t = timing.timed(f"cl_eval_packed_indexed[{x.t.shape[0]}->{ia.numel()}]",
+                               lambda: _cl.eval_packed_indexed(x.t, ia, ib, gate))
+            return x
+        return _cl.eval(x.contiguous(), self.offsets_ch, self.offsets_h, self.offsets_w, w,
+                        self.gate_sequence, self.stride, self.padding, self.ks)
+
+    @torch.no_grad()
+    def packed_tables(self, w: torch.Tensor):
+        """(ia, ib, gate) per output feature (c, oy, ox) for the winner slots ``w``: the
+        flattened NCHW input feature of each tap, -1 outside the plane (compiler/extract.py:
+        101-174), and the opcode.  Cached until the offsets, opcodes or winners change."""
+        key = (w.data_ptr(), w._version, self.offsets_ch._version, self.offsets_h._version,
+               self.offsets_w._version, self.gate_sequence._version, w.device)
+        if self._packed_key == key:
+            return self._packed_tables
+        dev = w.device
+        c_in, h, wd = self.in_shape
+        rows = torch.arange(self.c_out, device=dev)
+        slot = w.to(torch.long)
+        oy = torch.arange(self.h_out, device=dev).view(1, -1, 1) * self.stride
+        ox = torch.arange(self.w_out, device=dev).view(1, 1, -1) * self.stride
+        tables = []
+        for side in (0, 1):
+            ch = self.offsets_ch[side, rows, slot].to(torch.long).view(-1, 1, 1)
+            iy = oy + self.offsets_h[side, rows, slot].to(torch.long).view(-1, 1, 1)
+            ix = ox + self.offsets_w[side, rows, slot].to(torch.long).view(-1, 1, 1)
+            inside = (iy >= 0) & (iy < h) & (ix >= 0) & (ix < wd)
+            feat = (ch * h + iy) * wd + ix
+            tables.append(torch.where(inside, feat, torch.full_like(feat, -1))
+                          .reshape(-1).to(torch.int32).contiguous())
+        gate = (self.gate_sequence[rows, slot].view(-1, 1)
+                .expand(self.c_out, self.h_out * self.w_out).reshape(-1).contiguous())
+        self._packed_tables = (tables[0], tables[1], gate)
+        self._packed_key = key
+        return self._packed_tables
+
+    def get_connections(self, device='cuda'):
+        """Sample the two taps of every slot (:642-699), in the reference's draw order."""
+        shape = (2, self.c_out, self.num_gates)
+        if self.chn_grp > 1:
+            assert self.chn_grp <= self.c_in and self.chn_grp <= self.c_out
+            offsets_h = torch.randint(0, self.ks, size=shape, device=device, dtype=torch.int8)
+            offsets_w = torch.randint(0, self.ks, size=shape, device=device, dtype=torch.int8)
+            per_group = self.c_in // self.chn_grp
+            sizes = torch.full((self.chn_grp,), per_group, device=device)
+            sizes[:self.c_in % self.chn_grp] += 1
+            starts = torch.cat([torch.zeros(1, device=device), sizes.cumsum(0)]).to(torch.int32)
+            channels = torch.arange(self.c_in, device=device, dtype=torch.int32)
+            out_per_group = self.c_out // self.chn_grp
+            group_of = torch.clamp(torch.arange(self.c_out, device=device, dtype=torch.int32)
+                                   // out_per_group, 0, self.chn_grp - 1)
+            offsets_ch = torch.empty(shape, device=device, dtype=torch.int32)
+            for gid in range(self.chn_grp):
+                members = channels[starts[gid]:starts[gid + 1]]
+                rows = (group_of == gid).nonzero(as_tuple=True)[0]
+                if rows.numel() > 0:
+                    k = members.numel()
+                    offsets_ch[0, rows] = members[torch.randint(0, k, (rows.numel(), self.num_gates), device=device)]
+                    offsets_ch[1, rows] = members[torch.randint(0, k, (rows.numel(), self.num_gates), device=device)]
+        elif self.chn_grp == 1:
+            assert self.ks > 1
+            offsets_ch = torch.arange(0, self.c_out, device=device, dtype=torch.int32) % self.c_in
+            offsets_ch = offsets_ch.unsqueeze(-1).expand(2, -1, self.num_gates)
+            offsets_h = torch.randint(0, self.ks, size=shape, device=device, dtype=torch.int8)
+            offsets_w = torch.randint(0, self.ks, size=shape, device=device, dtype=torch.int8)
+        else:
+            offsets_ch = torch.randint(0, self.c_in, size=shape, device=device, dtype=torch.int32)
+            offsets_h = torch.randint(0, self.ks, size=shape, device=device, dtype=torch.int8)
+            offsets_w = torch.randint(0, self.ks, size=shape, device=device, dtype=torch.int8)
+        offsets_ch, offsets_h, offsets_w = self.resolve_conflicts(
+            offsets_ch, offsets_h, offsets_w, self.ks, self.c_in)
+        offsets_h -= self.padding
+        offsets_w -= self.padding
+        self.register_buffer("offsets_ch", offsets_ch.contiguous().to(device))
+        self.register_buffer("offsets_h", offsets_h.contiguous().to(device))
+        self.register_buffer("offsets_w", offsets_w.contiguous().to(device))
+
+    @staticmethod
+    def resolve_conflicts(offsets_ch, offsets_h, offsets_w, ks, c_in):
+        """Re-draw operand b of every slot whose two taps coincide until none do (:700-743):
+        its spatial offsets when ks > 1, its channel when ks == 1."""
+        def clash():
+            return ((offsets_ch[0] == offsets_ch[1]) & (offsets_h[0] == offsets_h[1])
+                    & (offsets_w[0] == offsets_w[1]))
+        conflict = clash()
+        while conflict.any():
+            num = conflict.sum()
+            if ks > 1:
+                offsets_h[1][conflict] = torch.randint(0, ks, size=(num,), device=offsets_h.device,
+                                                       dtype=torch.int8)
+                offsets_w[1][conflict] = torch.randint(0, ks, size=(num,), device=offsets_w.device,
+                                                       dtype=torch.int8)
+            elif ks == 1:
+                offsets_ch[1][conflict] = torch.randint(0, c_in, size=(num,), device=offsets_ch.device,
+                                                        dtype=torch.int32)
+            conflict = clash()
+        return offsets_ch, offsets_h, offsets_w
+
+    @torch.no_grad()
+    def update_indices_weak(self, n_weak, weak_mask):
+        """New taps for every slot of the weak rows (:745-764): channels when ks == 1, else
+        spatial offsets (shifted by -padding)."""
+        device = self.weights.device
+        size = (n_weak, self.num_gates)
+        if self.ks == 1:
+            self.offsets_ch[0][weak_mask] = torch.randint(0, self.c_in, size=size, device=device, dtype=torch.int32)
+            self.offsets_ch[1][weak_mask] = torch.randint(0, self.c_in, size=size, device=device, dtype=torch.int32)
+        else:
+            for t in (self.offsets_h[0], self.offsets_h[1], self.offsets_w[0], self.offsets_w[1]):
+                t[weak_mask] = torch.randint(0, self.ks, size=size, device=device,
+                                             dtype=torch.int8) - self.padding
+
+    @torch.no_grad()
+    def update_indices_strong(self, mask2d, num_to_fill):
+        """New taps for the refilled slots of the strong rows (:766-778)."""
+        device = self.weights.device
+        if self.ks == 1:
+            self.offsets_ch[0][mask2d] = torch.randint(0, self.c_in, size=(num_to_fill,), device=device, dtype=torch.int32)
+            self.offsets_ch[1][mask2d] = torch.randint(0, self.c_in, size=(num_to_fill,), device=device, dtype=torch.int32)
+        else:
+            for t in (self.offsets_h[0], self.offsets_h[1], self.offsets_w[0], self.offsets_w[1]):
+                t[mask2d] = torch.randint(0, self.ks, size=(num_to_fill,), device=device,
+                                          dtype=torch.int8) - self.padding
+
+    def extra_repr(self):
+        return 'in_shape={}, out_shape={}, pad={}, kernel_size={}, stride={}, num_chn={}, {}'.format(
+            self.in_shape, self.out_shape, self.padding, self.ks, self.stride,
+            self.chn_grp if self.chn_grp <= 1 else (self.c_in // self.chn_grp),
+            'train' if self.training else 'eval')
+
+    @torch.no_grad()
+    def connected_neurons(self, y_flag: torch.Tensor, const_gates=None, trivial_gates=None,
+                          device=None):
+        """Input pixels feeding the active, non-trivial outputs (:793-835).  Returns (x_flag
+        [c_in, h, w], y_flag [c_out, h_out, w_out]); y_flag is updated in place."""
+        assert tuple(y_flag.shape) == self.out_shape, \
+            f'y_flag shape mismatch: {y_flag.shape}, should be {self.out_shape}'
+        device = device if device is not None else y_flag.device
+        const_gates = torch.tensor([0, 15], device=device) if const_gates is None else const_gates
+        trivial_gates = (torch.tensor([3, 5, 10, 12], device=device) if trivial_gates is None
+                         else trivial_gates)
+        x_flag = torch.zeros(self.in_shape, dtype=torch.bool, device=device)
+        w = getattr(self, 'w', None)
+        w = (self.weights.argmax(-1) if w is None else w).to(torch.long)
+        idx = w.view(1, -1, 1).expand(2, -1, 1)
+        och = torch.gather(self.offsets_ch, 2, idx).squeeze(-1).to(torch.long)
+        oh = torch.gather(self.offsets_h, 2, idx).squeeze(-1).to(torch.long)
+        ow = torch.gather(self.offsets_w, 2, idx).squeeze(-1).to(torch.long)
+        g = torch.gather(self.gate_sequence, 1, w.unsqueeze(-1)).squeeze(-1)
+        is_const = torch.isin(g, const_gates.to(g.device))
+        is_trivial = torch.isin(g, trivial_gates.to(g.device))
+        y_flag[is_const] = False
+        uses = (~is_const & (g != 5) & (g != 10), ~is_const & (g != 3) & (g != 12))
+        c, oy, ox = torch.nonzero(y_flag, as_tuple=True)
+        _, h, wd = self.in_shape
+        for side in (0, 1):
+            keep = uses[side][c]
+            cc, yy, xx = c[keep], oy[keep], ox[keep]
+            iy = yy * self.stride + oh[side][cc]
+            ix = xx * self.stride + ow[side][cc]
+            inside = (iy >= 0) & (iy < h) & (ix >= 0) & (ix < wd)
+            x_flag[och[side][cc][inside], iy[inside], ix[inside]] = True
+        y_flag[is_trivial] = False
         return x_flag, y_flag
 
 

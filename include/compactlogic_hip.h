@@ -160,6 +160,70 @@ int cl_dense_backward_finalize(int dtype, const void* moments, int64_t nchunks,
                                int64_t num_runs, int64_t num_gates, void* stream);
 
 /* -------------------------------------------------------------------------------------------
+ * ConvLayer.  x / grad_x: [N, Cin, H, W] (unpadded), y / grad_y: [N, Cout, Ho, Wo] with
+ * Ho = (H + 2 pad - ks) / stride + 1 (Wo likewise); offsets_ch int32, offsets_h / offsets_w
+ * int8, all [2, Cout, G] with the spatial offsets already shifted by -pad; w, gate_seq
+ * [Cout, G].  Tap (side, c, g) of output (oy, ox) is x[n, ch, oy*stride + dh, ox*stride + dw],
+ * zero outside the input plane.  The backward passes take (h_out, w_out) from grad_y, as the
+ * reference binding does, so they need neither pad nor ks.
+ * ----------------------------------------------------------------------------------------- */
+
+/* convlogic_cuda.forward -- compactlogic/cuda/convlogic.cpp:50-63,
+ * compactlogic/cuda/convlogic_kernel.cu:87-188.
+ * y[n, c, oy, ox] = sum_g w[c, g] * op_{gate_seq[c, g]}(tap0, tap1). */
+int cl_conv_forward(int dtype, const void* x, const int32_t* offsets_ch, const int8_t* offsets_h,
+                    const int8_t* offsets_w, const void* w, const uint8_t* gate_seq, void* y,
+                    int64_t N, int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+                    int64_t num_gates, int64_t stride, int64_t pad, int64_t ks, void* stream);
+
+/* convlogic_cuda.backward_w -- compactlogic/cuda/convlogic.cpp:81-94,
+ * compactlogic/cuda/convlogic_kernel.cu:295-430.  grad_w[c, g] = sum over n, oy, ox of
+ * grad_y * op_g(tap0, tap1), reduced deterministically through `workspace` (size from
+ * cl_conv_backward_w_workspace).  With probs (not NULL, num_gates <= 64) the result is passed
+ * through the softmax backward (gradient of the logits). */
+int cl_conv_backward_w(int dtype, const void* x, const int32_t* offsets_ch,
+                       const int8_t* offsets_h, const int8_t* offsets_w, const uint8_t* gate_seq,
+                       const void* grad_y, const void* probs, void* grad_w, void* workspace,
+                       int64_t workspace_bytes, int64_t N, int64_t Cin, int64_t H, int64_t W,
+                       int64_t Cout, int64_t num_gates, int64_t stride, int64_t h_out,
+                       int64_t w_out, void* stream);
+
+/* Workspace bytes cl_conv_backward_w needs for these shapes. */
+int cl_conv_backward_w_workspace(int dtype, int64_t N, int64_t Cin, int64_t H, int64_t W,
+                                 int64_t Cout, int64_t num_gates, int64_t stride, int64_t h_out,
+                                 int64_t w_out, int64_t* bytes);
+
+/* convlogic_cuda.backward_x -- compactlogic/cuda/convlogic.cpp:65-79,
+ * compactlogic/cuda/convlogic_kernel.cu:190-293, as a deterministic gather (the reference
+ * scatters with float atomics).  The inverse index lists, for every bucket
+ * k = ch * stride^2 + (dh mod stride) * stride + (dw mod stride), the taps 2 * (c * G + g) +
+ * side whose channel is ch and whose offsets have that phase: entries inv_ent[inv_ptr[k] ..
+ * inv_ptr[k+1]-1], inv_ptr int32 [Cin * stride^2 + 1]. */
+int cl_conv_backward_x(int dtype, const void* x, const int32_t* offsets_ch,
+                       const int8_t* offsets_h, const int8_t* offsets_w, const void* w,
+                       const uint8_t* gate_seq, const void* grad_y, const int32_t* inv_ptr,
+                       const int32_t* inv_ent, void* grad_x, int64_t N, int64_t Cin, int64_t H,
+                       int64_t W, int64_t Cout, int64_t num_gates, int64_t stride,
+                       int64_t h_out, int64_t w_out, void* stream);
+
+/* convlogic_cuda.eval -- compactlogic/cuda/convlogic.cpp:96-109,
+ * compactlogic/cuda/convlogic_kernel.cu:433-530: the argmax slot w_slot[c] only. */
+int cl_conv_eval(int dtype, const void* x, const int32_t* offsets_ch, const int8_t* offsets_h,
+                 const int8_t* offsets_w, const uint8_t* w_slot, const uint8_t* gate_seq,
+                 void* y, int64_t N, int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+                 int64_t num_gates, int64_t stride, int64_t pad, int64_t ks, void* stream);
+
+/* Packed layer from resolved index tables (no reference counterpart; the packed form of a
+ * frozen ConvLayer, whose output feature (c, oy, ox) in NCHW order reads input features
+ * (ch * H + y) * W + x, compiler/extract.py:101-102):
+ * y[o, :] = op_{gate[o]}(x[ia[o], :], x[ib[o], :]); a negative index reads zeros (a tap
+ * outside the input plane).  Any row_bytes; 16-byte rows at 16-byte aligned bases stream as
+ * 16-byte vectors. */
+int cl_eval_packed_indexed(const void* x, const int32_t* ia, const int32_t* ib,
+                           const uint8_t* gate, void* y, int64_t in_dim, int64_t out_dim,
+                           int64_t row_bytes, void* stream);
+
+/* -------------------------------------------------------------------------------------------
  * GroupSum -- compactlogic/compactlogic.py:450-468: out[n, c] = sum_{j in group c} x[n, j] / tau
  * with the features zero-padded to a multiple of k; group c is columns
  * [c*gs, min((c+1)*gs, features)), gs = ceil(features / k).  x is read through

@@ -88,6 +88,33 @@ def resolve_slots(indices: np.ndarray, gate_sequence: np.ndarray, w_slot: np.nda
     return indices[0][o, s], indices[1][o, s], np.asarray(gate_sequence)[o, s]
 
 
+def resolve_conv_slots(offsets_ch, offsets_h, offsets_w, gate_sequence, w_slot, in_shape, stride,
+                       out_hw):
+    """(ia, ib, g) per output feature (c, oy, ox) of a frozen ConvLayer, following the loop of
+    compiler/extract.py:130-174: the winner slot s = w_slot[c] reads input feature
+    (ch * h + y) * w + x (NCHW, :101-102) at y = oy * stride + dh, x = ox * stride + dw, and a
+    tap outside the input plane is the constant 0 (index -1 here)."""
+    _, h, w = in_shape
+    h_out, w_out = out_hw
+    c_out = len(w_slot)
+    ia = np.empty(c_out * h_out * w_out, dtype=np.int64)
+    ib = np.empty_like(ia)
+    g = np.empty(len(ia), dtype=np.uint8)
+    for c in range(c_out):
+        s = int(w_slot[c])
+        taps = [(int(offsets_ch[side][c][s]), int(offsets_h[side][c][s]),
+                 int(offsets_w[side][c][s])) for side in (0, 1)]
+        for oy in range(h_out):
+            for ox in range(w_out):
+                o = (c * h_out + oy) * w_out + ox
+                for side, dst in ((0, ia), (1, ib)):
+                    ch, dh, dw = taps[side]
+                    y, x = oy * stride + dh, ox * stride + dw
+                    dst[o] = (ch * h + y) * w + x if (0 <= y < h and 0 <= x < w) else -1
+                g[o] = int(gate_sequence[c][s])
+    return ia, ib, g
+
+
 def group_bit_sum(packed: np.ndarray, pad_len: int, k: int) -> np.ndarray:
     """uint rows [rows, *] -> int32 [N, k]; raises ValueError when rows % k != 0."""
     packed = np.ascontiguousarray(packed).view(np.uint8)

@@ -160,3 +160,107 @@ def test_config_network_is_deterministic():
         if isinstance(l1, cl.LogicLayer):
             assert torch.equal(l1.weights, l2.weights) and torch.equal(l1.indices, l2.indices)
             assert l1.run_plan().num_runs == l1.out_dim
+
+
+# ------------------------------------------------------------------------------ ConvLayer
+
+@pytest.mark.parametrize("num_chn,ks,pad", [(0, 3, 1), (1, 3, 1), (3, 3, 0), (0, 1, 0)])
+def test_conv_layer_buffers_and_sampler(num_chn, ks, pad):
+    torch.manual_seed(num_chn * 7 + ks)
+    layer = cl.ConvLayer((9, 10, 12), padding=pad, c_out=18, ks=ks, stride=2, num_chn=num_chn,
+                         num_gates=16)
+    sd = layer.state_dict()
+    assert set(sd) == {"weights", "gate_sequence", "offsets_ch", "offsets_h", "offsets_w"}
+    assert sd["weights"].shape == (18, 16)
+    assert sd["offsets_ch"].dtype == torch.int32 and sd["offsets_h"].dtype == torch.int8
+    for k in ("offsets_ch", "offsets_h", "offsets_w"):
+        assert sd[k].shape == (2, 18, 16) and sd[k].is_contiguous()
+    h_out = (10 + 2 * pad - ks) // 2 + 1
+    w_out = (12 + 2 * pad - ks) // 2 + 1
+    assert layer.out_shape == (18, h_out, w_out)
+    assert layer.in_dim == 9 * (10 + 2 * pad) * (12 + 2 * pad)   # padded plane, as the reference
+    assert layer.out_dim == 18 * h_out * w_out
+    och, oh, ow = layer.offsets_ch, layer.offsets_h, layer.offsets_w
+    assert int(oh.min()) >= -pad and int(oh.max()) < ks - pad
+    assert int(ow.min()) >= -pad and int(ow.max()) < ks - pad
+    assert int(och.min()) >= 0 and int(och.max()) < 9
+    same = (och[0] == och[1]) & (oh[0] == oh[1]) & (ow[0] == ow[1])
+    assert not bool(same.any())                                    # resolve_conflicts
+    if num_chn == 1:
+        expect = (torch.arange(18) % 9).to(torch.int32)
+        assert torch.equal(och[0][:, 0], expect) and torch.equal(och[1][:, 5], expect)
+    if num_chn == 3:                                              # 3 groups of 3 channels
+        group = torch.clamp(torch.arange(18) // 6, 0, 2)
+        assert torch.equal(och[0] // 3, group.view(-1, 1).expand(18, 16).to(torch.int32))
+    assert "num_chn={}".format(num_chn) in layer.extra_repr()
+
+
+def test_conv_packed_tables_match_oracle():
+    from oracle import packed as P
+    torch.manual_seed(3)
+    layer = cl.ConvLayer((3, 7, 9), padding=1, c_out=5, ks=3, stride=2, num_chn=0, num_gates=4)
+    layer.freeze()
+    ia, ib, g = layer.packed_tables(layer.w)
+    ra, rb, rg = P.resolve_conv_slots(layer.offsets_ch.numpy(), layer.offsets_h.numpy(),
+                                      layer.offsets_w.numpy(), layer.gate_sequence.numpy(),
+                                      layer.w.numpy(), layer.in_shape, 2, layer.out_shape[1:])
+    assert np.array_equal(ia.numpy(), ra) and np.array_equal(ib.numpy(), rb)
+    assert np.array_equal(g.numpy(), rg)
+    # cached until the winners change
+    assert layer.packed_tables(layer.w)[0] is ia
+    layer.w.fill_(1)
+    assert layer.packed_tables(layer.w)[0] is not ia
+
+
+def test_conv_layer_rewiring_keeps_ranges():
+    torch.manual_seed(4)
+    layer = cl.ConvLayer((4, 8, 8), padding=1, c_out=6, ks=3, stride=1, num_chn=0, num_gates=8)
+    before = layer.offsets_h.clone()
+    weak, strong = layer.resample_connections(torch.arange(6), threshold_high=2.0, threshold_low=1.0)
+    assert bool(weak.all()) and not bool(strong.any())
+    assert not torch.equal(before, layer.offsets_h)
+    assert int(layer.offsets_h.min()) >= -1 and int(layer.offsets_h.max()) <= 1
+
+
+def test_conv_forward_rejects_host_tensors():
+    layer = cl.ConvLayer((3, 6, 6), padding=1, c_out=4, ks=3, stride=1, num_chn=0)
+    with pytest.raises(RuntimeError):
+        layer(torch.rand(2, 3, 6, 6))
+
+
+def test_conv_config_network_shapes():
+    model = configs.conv_network(configs.CONV_CONFIGS["cfg5"], device="cpu")
+    assert model[0].out_shape == (256, 16, 16) and model[1].out_shape == (512, 7, 7)
+    assert model[3].in_dim == 25088 and model[4].out_dim == 16000
+    gs = model[0].gate_sequence
+    assert gs.shape == (256, 4)
+    assert all(len(set(r.tolist())) == 4 for r in gs)          # distinct opcodes per row
+
+
+def test_conv_inverse_index_cache_follows_tensors():
+    """The cached inverse index is reused only for the same live, unmodified offsets: a new
+    tensor at a recycled address, or an in-place change, rebuilds it (CPU torch ops)."""
+    import gc
+    from compactlogic_amd import convlogic_hip as cv
+    g = torch.Generator().manual_seed(0)
+    och = torch.randint(0, 3, (2, 4, 5), generator=g, dtype=torch.int32)
+    oh = torch.randint(-1, 2, (2, 4, 5), generator=g).to(torch.int8)
+    ow = torch.randint(-1, 2, (2, 4, 5), generator=g).to(torch.int8)
+    first = cv.inverse_index(och, oh, ow, 3, 2)
+    assert cv.inverse_index(och, oh, ow, 3, 2) is first
+    oh[1, 2, 3] = 1 - int(oh[1, 2, 3])
+    second = cv.inverse_index(och, oh, ow, 3, 2)
+    assert second is not first
+    del och
+    gc.collect()
+    och2 = torch.zeros((2, 4, 5), dtype=torch.int32)
+    third = cv.inverse_index(och2, oh, ow, 3, 2)
+    assert third is not second
+    # bucket contents: every tap once, in the bucket of its channel and stride phase
+    inv_ptr, inv_ent = third
+    assert int(inv_ptr[-1]) == 40 and sorted(inv_ent.tolist()) == list(range(40))
+    for k in range(3 * 4):
+        for e in inv_ent[int(inv_ptr[k]):int(inv_ptr[k + 1])].tolist():
+            side, slot = e & 1, e >> 1
+            c, gg = divmod(slot, 5)
+            assert int(och2[side, c, gg]) * 4 + (int(oh[side, c, gg]) % 2) * 2 + int(ow[side, c, gg]) % 2 == k

@@ -227,6 +227,29 @@ def test_conv_oracle_against_loops(stride, pad, ks):
                                atol=0)
 
 
+@pytest.mark.parametrize("stride,pad,ks", [(2, 1, 3), (2, 0, 3), (1, 1, 3)])
+def test_conv_slot_tables_match_float_discrete_conv(stride, pad, ks):
+    """The packed conv tables, evaluated bitwise on 64 samples per word, give the same bits
+    as the float discrete conv (itself pinned against scalar loops above)."""
+    rng = np.random.default_rng(40 + stride * 10 + pad)
+    n_, c_in, h, wd, c_out, g_n = 130, 3, 7, 6, 5, 4
+    och = rng.integers(0, c_in, (2, c_out, g_n)).astype(np.int32)
+    oh = (rng.integers(0, ks, (2, c_out, g_n)) - pad).astype(np.int8)
+    ow = (rng.integers(0, ks, (2, c_out, g_n)) - pad).astype(np.int8)
+    gs = rng.integers(0, 16, (c_out, g_n)).astype(np.uint8)
+    slot = rng.integers(0, g_n, c_out)
+    xb = rng.integers(0, 2, (n_, c_in, h, wd)).astype(np.float64)
+    y = O.conv_eval(xb, och, oh, ow, slot, gs, stride, pad, ks)
+    h_out, w_out = y.shape[2:]
+    ia, ib, g = P.resolve_conv_slots(och, oh, ow, gs, slot, (c_in, h, wd), stride, (h_out, w_out))
+    assert ia.min() >= -1 and ia.max() < c_in * h * wd
+    feats = xb.reshape(n_, -1).T.astype(bool)            # [features, samples]
+    packed, pad_len = P.pack_bits(feats, 64)
+    out = P.eval_layer(packed.view(np.uint64), ia, ib, g)
+    bits = np.unpackbits(out.view(np.uint8), axis=1, bitorder="little")[:, :n_]
+    np.testing.assert_array_equal(bits.T.reshape(y.shape), y.astype(np.uint8))
+
+
 # ------------------------------------------------------------------------------ packed
 
 def test_splitmix64_published_sequence():
