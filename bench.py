@@ -10,9 +10,13 @@ Also reported on the same JSON line:
   roofline      the dominant kernel's algorithmic bytes per launch / its average duration,
                 timed live with HIP events on the stream it runs on
   cpu_baseline  the pure-PyTorch CPU step (oracle/torch_cpu.py) on a bounded sample
+  conv_train    cfg3: conv 9x32x32 -> 256x16x16 -> 512x7x7, flatten, 2 x 16000 dense,
+                GroupSum(10, tau 30), batch 256, fp32 fwd + CE + bwd, same measurements
   packed        cfg4: the cfg2 network frozen to argmax gates, 2^24 bit-packed samples,
                 layer-by-layer bitwise evaluation + popcount GroupSum, with its own roofline
                 and CPU (C oracle) baseline
+  packed_conv   cfg5: the cfg3 network with 4 candidate gates per row, frozen, 2^20
+                bit-packed samples
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10]
 """
@@ -27,7 +31,9 @@ import time
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 CFG2_BYTES_PER_SAMPLE = 1_398_352
+CFG3_BYTES_PER_SAMPLE = 2_462_288
 CFG4_BYTES_PER_SAMPLE = 18_138
+CFG5_BYTES_PER_SAMPLE = 31_848
 
 
 def parse():
@@ -42,6 +48,10 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--kernel-reps", type=int, default=20)
     p.add_argument("--kernel-steps", type=int, default=5)
+    p.add_argument("--no-conv", action="store_true")
+    p.add_argument("--conv-steps", type=int, default=50)
+    p.add_argument("--conv-warmup", type=int, default=5)
+    p.add_argument("--conv-packed-log2-samples", type=int, default=20)
     return p.parse_args()
 
 
@@ -60,19 +70,15 @@ def dense_step_fn(model, x, labels, torch):
     return step
 
 
-def bench_dense(args, torch):
+def bench_train(model, x, labels, steps, warmup, mode, kernel_steps, torch):
+    """Time `steps` training steps (forward, cross-entropy, backward into every layer's logits)
+    after `warmup`; returns (samples/s, s/step, per-kernel timings, timed == eager)."""
     import compactlogic_amd as cl
-    from compactlogic_amd import configs
-    cfg = configs.CONFIGS["cfg2"]
-    dev = torch.device("cuda:0")
-    model = configs.dense_network(cfg, device=dev)
-    x, labels = configs.dense_inputs(cfg, device=dev)
     for m in model:
-        if isinstance(m, cl.LogicLayer):
+        if isinstance(m, cl.LogicLayer) and not isinstance(m, cl.ConvLayer):
             m.run_plan()
     step = dense_step_fn(model, x, labels, torch)
-
-    if args.mode == "graph":
+    if mode == "graph":
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -89,40 +95,81 @@ def bench_dense(args, torch):
         def run():
             model.zero_grad(set_to_none=True)
             step()
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         run()
     torch.cuda.synchronize()
     grads_run = [p.grad.clone() for p in model.parameters()]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         run()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
-    samples_s = cfg.batch / dt
+    dt = (time.perf_counter() - t0) / steps
+    batch = x.shape[0]
     # The timed path must compute what an eager step computes (bitwise: no atomics).
     model.zero_grad(set_to_none=True)
     step()
     torch.cuda.synchronize()
     matches = all(torch.equal(p.grad, g) for p, g in zip(model.parameters(), grads_run))
-    kernels = time_dense_kernels(model, step, cfg.batch, args.kernel_steps, torch)
+    kernels = time_train_kernels(model, step, batch, kernel_steps, torch)
+    return batch / dt, dt, kernels, matches
+
+
+def bench_dense(args, torch):
+    from compactlogic_amd import configs
+    cfg = configs.CONFIGS["cfg2"]
+    dev = torch.device("cuda:0")
+    model = configs.dense_network(cfg, device=dev)
+    x, labels = configs.dense_inputs(cfg, device=dev)
+    samples_s, dt, kernels, matches = bench_train(model, x, labels, args.steps, args.warmup,
+                                                  args.mode, args.kernel_steps, torch)
+    del model
+    torch.cuda.empty_cache()
     return cfg, samples_s, dt, kernels, matches
 
 
-# Algorithmic bytes per launch (activations read once + written once, fp32): forward reads x
-# and writes y; the fused backward reads x and grad_y and writes grad_x; the weight gradient
-# alone reads x and grad_y.  Parameters, indices and partial moments are not counted.
-def algorithmic_bytes(name: str, batch: int) -> int | None:
-    import re
-    m = re.match(r"(cl_[a-z_]+)\[(\d+)->(\d+)\]", name)
-    if not m:
-        return None
-    kind, i, o = m.group(1), int(m.group(2)), int(m.group(3))
-    x, y = 4 * i * batch, 4 * o * batch
-    return {"cl_dense_forward_tiled": x + y, "cl_dense_backward_tiled": 2 * x + y,
-            "cl_dense_weight_grad": x + y}.get(kind)
+# Algorithmic bytes per launch (activations read once + written once, fp32): a forward reads
+# its input and writes its output; the dense fused backward and the conv input gradient read
+# the input and grad_y and write grad_x; a weight gradient alone reads the input and grad_y.
+# Parameters, indices and partial sums are not counted.
+def train_kernel_bytes(model, batch: int) -> dict:
+    import compactlogic_amd as cl
+    out = {}
+    for m in model:
+        if isinstance(m, cl.ConvLayer):
+            c, h, w = m.in_shape
+            tag = f"[{c}x{h}x{w}->{m.c_out}]"
+            xb = 4 * batch * c * h * w
+            yb = 4 * batch * m.c_out * m.h_out * m.w_out
+            out.update({"cl_conv_forward" + tag: xb + yb, "cl_conv_backward_x" + tag: 2 * xb + yb,
+                        "cl_conv_backward_w" + tag: xb + yb})
+        elif isinstance(m, cl.LogicLayer):
+            tag = f"[{m.in_dim}->{m.out_dim}]"
+            xb, yb = 4 * batch * m.in_dim, 4 * batch * m.out_dim
+            out.update({"cl_dense_forward_tiled" + tag: xb + yb,
+                        "cl_dense_backward_tiled" + tag: 2 * xb + yb,
+                        "cl_dense_weight_grad" + tag: xb + yb})
+    return out
 
 
-def time_dense_kernels(model, step, batch, nsteps, torch):
+def packed_kernel_bytes(model, words: int, k: int) -> dict:
+    """Packed eval: read the input rows once, write the output rows once (8 bytes per word);
+    GroupSum reads the last rows and writes int32 counts [samples, k]."""
+    import compactlogic_amd as cl
+    out = {}
+    rows = None
+    for m in model:
+        if isinstance(m, cl.ConvLayer):
+            fin = m.in_shape[0] * m.in_shape[1] * m.in_shape[2]
+            out[f"cl_eval_packed_indexed[{fin}->{m.out_dim}]"] = (fin + m.out_dim) * words * 8
+            rows = m.out_dim
+        elif isinstance(m, cl.LogicLayer):
+            out[f"cl_dense_eval_packed[{m.in_dim}->{m.out_dim}]"] = (m.in_dim + m.out_dim) * words * 8
+            rows = m.out_dim
+    out[f"cl_group_bit_sum[{rows}]"] = rows * words * 8 + words * 64 * k * 4
+    return out
+
+
+def time_train_kernels(model, step, batch, nsteps, torch):
     """Mean duration of every library call inside `nsteps` real (eager) training steps,
     bracketed with HIP events on the stream each call uses."""
     from compactlogic_amd import timing
@@ -130,25 +177,54 @@ def time_dense_kernels(model, step, batch, nsteps, torch):
         for _ in range(nsteps):
             model.zero_grad(set_to_none=True)
             step()
+    return kernel_table(rec.summary(), train_kernel_bytes(model, batch))
+
+
+def kernel_table(summary: dict, nbytes_of: dict) -> dict:
     out = {}
-    for name, v in rec.summary().items():
+    for name, v in summary.items():
         sec = v["mean_ms"] * 1e-3
-        nbytes = algorithmic_bytes(name, batch)
+        nbytes = nbytes_of.get(name)
         out[name] = dict(seconds=sec, calls=v["calls"], algorithmic_bytes=nbytes,
                          achieved_GBs=(nbytes / sec / 1e9) if nbytes else None)
     return out
 
 
-def cpu_baseline_dense(torch):
+def roofline_of(kernels: dict, how: str) -> dict:
+    """The dominant kernel (largest total time per step among those with a byte count)."""
+    name = max((k for k in kernels if kernels[k]["algorithmic_bytes"]),
+               key=lambda k: kernels[k]["seconds"] * kernels[k]["calls"])
+    d = kernels[name]
+    return {"bound": "hbm", "achieved": round(d["achieved_GBs"], 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(d["achieved_GBs"] / HBM_PEAK_GBS, 4),
+            "traffic": None, "kernel": name, "per_launch_ms": round(d["seconds"] * 1e3, 4),
+            "algorithmic_bytes_per_launch": d["algorithmic_bytes"], "measured": how}
+
+
+def kernels_json(kernels: dict, steps: int) -> dict:
+    return {k: {"ms": round(v["seconds"] * 1e3, 4), "calls_per_step": v["calls"] // steps,
+                "GB/s": round(v["achieved_GBs"], 1) if v["achieved_GBs"] else None}
+            for k, v in kernels.items()}
+
+
+def cpu_baseline_train(torch, which: str):
     from compactlogic_amd import configs
     from oracle.torch_cpu import CpuDenseNet
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    cfg = configs.CONFIGS["cfg2"]
-    batch, warm, steps = 256, 1, 3
-    model = configs.dense_network(cfg, device="cpu")
+    if which == "cfg2":
+        cfg = configs.CONFIGS["cfg2"]
+        batch, warm, steps = 256, 1, 3
+        model = configs.dense_network(cfg, device="cpu")
+        x, labels = configs.dense_inputs(cfg, device="cpu", batch=batch)
+        what = "cfg2 network (6x12000, G=16, fp32)"
+    else:
+        cfg = configs.CONV_CONFIGS["cfg3"]
+        batch, warm, steps = 64, 1, 3
+        model = configs.conv_network(cfg, device="cpu")
+        x, labels = configs.conv_inputs(cfg, device="cpu", batch=batch)
+        what = "cfg3 network (2 conv + 2x16000 dense, G=16, fp32)"
     net = CpuDenseNet.from_model(model)
-    x, labels = configs.dense_inputs(cfg, device="cpu", batch=batch)
     for _ in range(warm):
         net.train_step(x, labels)
     t0 = time.perf_counter()
@@ -156,24 +232,48 @@ def cpu_baseline_dense(torch):
         net.train_step(x, labels)
     dt = (time.perf_counter() - t0) / steps
     return {"value": batch / dt, "unit": "samples/s", "cores": threads, "kind": "port",
-            "sample": f"cfg2 network (6x12000, G=16, fp32) fwd+bwd in torch CPU autograd "
-                      f"(bin_op_s formulation) at batch {batch} of 1024, {warm} warm-up + "
-                      f"{steps} timed steps; host {platform.processor() or platform.machine()}, "
+            "sample": f"{what} fwd+bwd in torch CPU autograd (oracle/torch_cpu.py) at batch "
+                      f"{batch} of {cfg.batch}, {warm} warm-up + {steps} timed steps; host "
+                      f"{platform.processor() or platform.machine()}, "
                       f"os.cpu_count()={os.cpu_count()}"}
 
 
-# ---------------------------------------------------------------------------------- packed cfg4
-
-def bench_packed(args, torch):
-    import compactlogic_amd as cl
+def bench_conv(args, torch):
     from compactlogic_amd import configs
-    cfg = configs.CONFIGS["cfg2"]
+    cfg = configs.CONV_CONFIGS["cfg3"]
     dev = torch.device("cuda:0")
-    model = configs.dense_network(cfg, device=dev)
-    configs.freeze_uniform_gates(model)
-    n = 1 << args.packed_log2_samples
+    model = configs.conv_network(cfg, device=dev)
+    x, labels = configs.conv_inputs(cfg, device=dev)
+    samples_s, dt, kernels, matches = bench_train(model, x, labels, args.conv_steps,
+                                                  args.conv_warmup, args.mode, args.kernel_steps,
+                                                  torch)
+    out = {
+        "workload": "cfg3: ConvLayer 9x32x32 -> 256x16x16 (ks 3, stride 2, pad 1) -> 512x7x7 "
+                    "(ks 3, stride 2, pad 0), flatten, LogicLayer 25088->16000->16000, "
+                    "GroupSum(10, tau=30), G=16, batch 256, fp32 fwd+CE+bwd",
+        "value": round(samples_s, 1), "unit": "samples/s", "steps": args.conv_steps,
+        "warmup": args.conv_warmup, "ms_per_step": round(dt * 1e3, 4),
+        "step_hbm_frac": round(CFG3_BYTES_PER_SAMPLE * samples_s / 1e9 / HBM_PEAK_GBS, 4),
+        "timed_path_matches_eager": matches,
+        "roofline": roofline_of(kernels, f"HIP events around each launch inside "
+                                         f"{args.kernel_steps} eager training steps"),
+        "kernels": kernels_json(kernels, args.kernel_steps),
+    }
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------------- packed cfg4 / cfg5
+
+def bench_packed_net(model, in_features: int, log2n: int, passes: int, k: int, torch):
+    """Whole packed passes over 2^log2n resident samples (min over `passes`), then one more
+    pass with every library call bracketed by HIP events."""
+    import compactlogic_amd as cl
+    from compactlogic_amd import configs, timing
+    n = 1 << log2n
     words = n // 64
-    xw = configs.packed_input_words(cfg.in_dim, words, device=dev)
+    xw = configs.packed_input_words(in_features, words, device=torch.device("cuda:0"))
 
     def one_pass():
         return model(cl.PackBitsTensor.from_packed(xw))
@@ -181,7 +281,7 @@ def bench_packed(args, torch):
     counts = one_pass()
     torch.cuda.synchronize()
     times = []
-    for _ in range(args.packed_passes):
+    for _ in range(passes):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         counts = one_pass()
@@ -189,61 +289,53 @@ def bench_packed(args, torch):
         times.append(time.perf_counter() - t0)
     dt = min(times)
     checksum = int(counts.to(torch.int64).sum().item())
-    kern = time_packed_kernels(model, xw, args.kernel_reps, torch)
-    return dict(n=n, seconds=dt, samples_s=n / dt, checksum=checksum, kernels=kern)
+    with timing.record() as rec:
+        one_pass()
+    kernels = kernel_table(rec.summary(), packed_kernel_bytes(model, words, k))
+    del xw, counts
+    torch.cuda.empty_cache()
+    return dict(n=n, seconds=dt, samples_s=n / dt, checksum=checksum, kernels=kernels)
 
 
-def time_packed_kernels(model, xw, reps, torch):
-    import compactlogic_amd as cl
-    from compactlogic_amd import _capi
-    layers = [m for m in model if isinstance(m, cl.LogicLayer)]
-    stream = torch.cuda.current_stream()
-    words = xw.shape[1]
-    layer = layers[1]
-    xin = torch.empty((layer.in_dim, words), dtype=torch.int64, device=xw.device)
-    from compactlogic_amd import difflogic_hip as dl
-    dl.fill_splitmix64(xin, 77)
-    y = torch.empty((layer.out_dim, words), dtype=torch.int64, device=xw.device)
-    counts = torch.empty((words * 64, 10), dtype=torch.int32, device=xw.device)
-    s = stream.cuda_stream
-    ev = lambda: _capi.call("cl_dense_eval_packed", xin.data_ptr(), layer.indices[0].data_ptr(),
-                            layer.indices[1].data_ptr(), layer.w.data_ptr(),
-                            layer.gate_sequence.data_ptr(), y.data_ptr(), layer.in_dim,
-                            layer.out_dim, words * 8, layer.num_gates, s)
-    gb = lambda: _capi.call("cl_group_bit_sum", y.data_ptr(), layer.out_dim, words * 8, 0, 10,
-                            counts.data_ptr(), s)
-    out = {}
-    for name, fn, kname, nbytes in (
-            ("layer_12000", ev, "k_eval_packed", (layer.in_dim + layer.out_dim) * words * 8),
-            ("groupbitsum", gb, "k_group_bit_sum", layer.out_dim * words * 8 + counts.numel() * 4)):
-        fn()
-        torch.cuda.synchronize()
-        r = max(1, reps // 4)
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(r):
-            fn()
-        end.record(stream)
-        end.synchronize()
-        sec = start.elapsed_time(end) / r * 1e-3
-        out[name] = dict(kernel=kname, seconds=sec, algorithmic_bytes=nbytes,
-                         achieved_GBs=nbytes / sec / 1e9)
-    return out
+def packed_json(pk: dict, workload: str, bytes_per_sample: int) -> dict:
+    return {
+        "workload": workload,
+        "value": round(pk["samples_s"] / 1e9, 4), "unit": "Gsamples/s",
+        "ms_per_pass": round(pk["seconds"] * 1e3, 3),
+        "hbm_frac": round(bytes_per_sample * pk["samples_s"] / 1e9 / HBM_PEAK_GBS, 4),
+        "counts_checksum": pk["checksum"],
+        "roofline": roofline_of(pk["kernels"], "HIP events around each launch inside one "
+                                               "extra whole pass"),
+        "kernels": kernels_json(pk["kernels"], 1),
+    }
 
 
-def cpu_baseline_packed(torch):
+def cpu_baseline_packed(torch, which: str):
     import numpy as np
     import compactlogic_amd as cl
     from compactlogic_amd import configs
     from oracle import packed as P
-    cfg = configs.CONFIGS["cfg2"]
-    model = configs.dense_network(cfg, device="cpu")
-    configs.freeze_uniform_gates(model)
-    layers = [P.resolve_slots(m.indices.numpy(), m.gate_sequence.numpy(), m.w.numpy())
-              for m in model if isinstance(m, cl.LogicLayer)]
-    n = 1 << 16
+    if which == "cfg4":
+        cfg = configs.CONFIGS["cfg2"]
+        model = configs.dense_network(cfg, device="cpu")
+        configs.freeze_uniform_gates(model)
+        in_features, log2n = cfg.in_dim, 16
+    else:
+        cfg = configs.CONV_CONFIGS["cfg5"]
+        model = configs.conv_network(cfg, device="cpu")
+        configs.freeze_argmax(model)
+        in_features, log2n = cfg.in_shape[0] * cfg.in_shape[1] * cfg.in_shape[2], 15
+    layers = []
+    for m in model:
+        if isinstance(m, cl.ConvLayer):
+            layers.append(P.resolve_conv_slots(m.offsets_ch.numpy(), m.offsets_h.numpy(),
+                                               m.offsets_w.numpy(), m.gate_sequence.numpy(),
+                                               m.w.numpy(), m.in_shape, m.stride, m.out_shape[1:]))
+        elif isinstance(m, cl.LogicLayer):
+            layers.append(P.resolve_slots(m.indices.numpy(), m.gate_sequence.numpy(), m.w.numpy()))
+    n = 1 << log2n
     words = n // 64
-    xw = np.stack([P.fill_splitmix64(words, (1 << 40) + f * words) for f in range(cfg.in_dim)])
+    xw = np.stack([P.fill_splitmix64(words, (1 << 40) + f * words) for f in range(in_features)])
     P.network_counts(xw, layers, cfg.k)           # warm
     t0 = time.perf_counter()
     reps = 3
@@ -251,7 +343,7 @@ def cpu_baseline_packed(torch):
         P.network_counts(xw, layers, cfg.k)
     dt = (time.perf_counter() - t0) / reps
     return {"value": n / dt / 1e9, "unit": "Gsamples/s", "cores": 1, "kind": "port",
-            "sample": f"cfg4 network on 2^16 samples (of 2^24), C oracle oracle/packed_ref.c, "
+            "sample": f"{which} network on 2^{log2n} samples, C oracle oracle/packed_ref.c, "
                       f"single thread, {reps} timed passes"}
 
 
@@ -279,24 +371,13 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
-    from compactlogic_amd import _capi
+    from compactlogic_amd import _capi, configs
     _capi.load()
 
     calibration_copy(torch)
     log(f"dense cfg2: mode={args.mode} warmup={args.warmup} steps={args.steps}")
     cfg, samples_s, dt, kernels, matches = bench_dense(args, torch)
     log(f"dense cfg2: {samples_s:,.0f} samples/s, {dt * 1e3:.3f} ms/step")
-    # dominant kernel: the library call with the largest total time per step
-    dom_name = max((k for k in kernels if kernels[k]["algorithmic_bytes"]),
-                   key=lambda k: kernels[k]["seconds"] * kernels[k]["calls"])
-    dom = kernels[dom_name]
-    roofline = {"bound": "hbm", "achieved": round(dom["achieved_GBs"], 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(dom["achieved_GBs"] / HBM_PEAK_GBS, 4),
-                "traffic": None, "kernel": dom_name,
-                "per_launch_ms": round(dom["seconds"] * 1e3, 4),
-                "algorithmic_bytes_per_launch": dom["algorithmic_bytes"],
-                "measured": f"HIP events around each launch inside {args.kernel_steps} eager "
-                            "training steps run right after the timed region"}
     step_bytes = CFG2_BYTES_PER_SAMPLE * cfg.batch
     result = {
         "metric": "train samples/s (fwd+bwd) & packed eval Gsamples/s; % of HBM peak",
@@ -316,38 +397,55 @@ def main():
                    "global_batch": cfg.batch, "mode": args.mode, "parallelism": "none (1 GPU)"},
         "step_hbm_frac": round(step_bytes / dt / 1e9 / HBM_PEAK_GBS, 4),
         "timed_path_matches_eager": matches,
-        "roofline": roofline,
-        "kernels": {k: {"ms": round(v["seconds"] * 1e3, 4), "calls_per_step": v["calls"] // args.kernel_steps,
-                        "GB/s": round(v["achieved_GBs"], 1) if v["achieved_GBs"] else None}
-                    for k, v in kernels.items()},
+        "roofline": roofline_of(kernels, f"HIP events around each launch inside "
+                                         f"{args.kernel_steps} eager training steps run right "
+                                         "after the timed region"),
+        "kernels": kernels_json(kernels, args.kernel_steps),
     }
     if not args.no_cpu_baseline:
-        log("cpu baseline (dense)")
-        result["cpu_baseline"] = cpu_baseline_dense(torch)
+        log("cpu baseline (cfg2)")
+        result["cpu_baseline"] = cpu_baseline_train(torch, "cfg2")
+    if not args.no_conv:
+        log(f"conv cfg3: warmup={args.conv_warmup} steps={args.conv_steps}")
+        conv = bench_conv(args, torch)
+        log(f"conv cfg3: {conv['value']:,.0f} samples/s, {conv['ms_per_step']:.3f} ms/step")
+        if not args.no_cpu_baseline:
+            log("cpu baseline (cfg3)")
+            conv["cpu_baseline"] = cpu_baseline_train(torch, "cfg3")
+        result["conv_train"] = conv
     if not args.no_packed:
         log(f"packed cfg4: 2^{args.packed_log2_samples} samples x {args.packed_passes} passes")
-        pk = bench_packed(args, torch)
-        pk_dom = pk["kernels"]["layer_12000"]
-        packed = {
-            "workload": f"cfg4: cfg2 network frozen to argmax gates, 2^{args.packed_log2_samples} "
-                        "samples bit-packed 64 per word, 6 bitwise layers + popcount GroupSum",
-            "value": round(pk["samples_s"] / 1e9, 4), "unit": "Gsamples/s",
-            "ms_per_pass": round(pk["seconds"] * 1e3, 3),
-            "hbm_frac": round(CFG4_BYTES_PER_SAMPLE * pk["samples_s"] / 1e9 / HBM_PEAK_GBS, 4),
-            "counts_checksum": pk["checksum"],
-            "roofline": {"bound": "hbm", "achieved": round(pk_dom["achieved_GBs"], 1),
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(pk_dom["achieved_GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": pk_dom["kernel"], "per_launch_ms": round(pk_dom["seconds"] * 1e3, 3),
-                         "algorithmic_bytes_per_launch": pk_dom["algorithmic_bytes"]},
-            "kernels": {k: {"ms": round(v["seconds"] * 1e3, 3), "GB/s": round(v["achieved_GBs"], 1)}
-                        for k, v in pk["kernels"].items()},
-        }
+        c2 = configs.CONFIGS["cfg2"]
+        model = configs.dense_network(c2, device=torch.device("cuda:0"))
+        configs.freeze_uniform_gates(model)
+        pk = bench_packed_net(model, c2.in_dim, args.packed_log2_samples, args.packed_passes,
+                              c2.k, torch)
+        del model
+        packed = packed_json(pk, f"cfg4: cfg2 network frozen to argmax gates, "
+                                 f"2^{args.packed_log2_samples} samples bit-packed 64 per word, "
+                                 "6 bitwise layers + popcount GroupSum", CFG4_BYTES_PER_SAMPLE)
         log(f"packed cfg4: {packed['value']} Gsamples/s")
         if not args.no_cpu_baseline:
-            log("cpu baseline (packed)")
-            packed["cpu_baseline"] = cpu_baseline_packed(torch)
+            log("cpu baseline (cfg4)")
+            packed["cpu_baseline"] = cpu_baseline_packed(torch, "cfg4")
         result["packed"] = packed
+        if not args.no_conv:
+            log(f"packed cfg5: 2^{args.conv_packed_log2_samples} samples")
+            c5 = configs.CONV_CONFIGS["cfg5"]
+            model = configs.conv_network(c5, device=torch.device("cuda:0"))
+            configs.freeze_argmax(model)
+            pk = bench_packed_net(model, c5.in_shape[0] * c5.in_shape[1] * c5.in_shape[2],
+                                  args.conv_packed_log2_samples, args.packed_passes, c5.k, torch)
+            del model
+            pc = packed_json(pk, f"cfg5: cfg3 network with 4 candidate gates per row, frozen "
+                                 f"to argmax, 2^{args.conv_packed_log2_samples} samples bit-packed "
+                                 "64 per word, 2 packed conv + 2 dense layers + popcount GroupSum",
+                             CFG5_BYTES_PER_SAMPLE)
+            log(f"packed cfg5: {pc['value']} Gsamples/s")
+            if not args.no_cpu_baseline:
+                log("cpu baseline (cfg5)")
+                pc["cpu_baseline"] = cpu_baseline_packed(torch, "cfg5")
+            result["packed_conv"] = pc
     print(json.dumps(result), flush=True)
 
 

@@ -60,7 +60,8 @@ class PackBitsTensor:
         return self.t.shape[1] * self.t.element_size() * 8 - self.pad_len
 
     def group_sum(self, k):
-        return _dl.groupbitsum(self.t, self.pad_len, k)
+        return timing.timed(f"cl_group_bit_sum[{self.t.shape[0]}]",
+                            lambda: _dl.groupbitsum(self.t, self.pad_len, k))
 
     def flatten(self, start_dim=0, end_dim=-1, **kwargs):
         """Returns the PackBitsTensor itself (its feature axis is already flat)."""
@@ -315,7 +316,8 @@ class LogicLayer(torch.nn.Module):
         a, b = self.indices[0], self.indices[1]
         if isinstance(x, PackBitsTensor):
             assert x.t.shape[0] == self.in_dim, (x.t.shape, self.in_dim)
-            x.t = _dl.eval_packed(x.t, a, b, w, self.gate_sequence)
+            x.t = timing.timed(f"cl_dense_eval_packed[{self.in_dim}->{self.out_dim}]",
+                               lambda: _dl.eval_packed(x.t, a, b, w, self.gate_sequence))
             return x
         x = x.transpose(0, 1).contiguous()
         return _dl.eval(x, a, b, w, self.gate_sequence).transpose(0, 1)

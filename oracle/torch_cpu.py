@@ -64,6 +64,42 @@ def layer_forward(x: torch.Tensor, indices: torch.Tensor, gate_sequence: torch.T
     return y
 
 
+def conv_forward(x: torch.Tensor, och: torch.Tensor, oh: torch.Tensor, ow: torch.Tensor,
+                 gate_sequence: torch.Tensor, logits: torch.Tensor, stride: int,
+                 out_hw: tuple[int, int]) -> torch.Tensor:
+    """x [N, C, H, W] -> [N, Cout, Ho, Wo] for one soft ConvLayer: slot (c, g) reads the taps
+    x[n, ch, oy*stride + dh, ox*stride + dw] (0 outside the plane) of both operands, as in
+    compactlogic/cuda/convlogic_kernel.cu:98-137, and the slots are mixed with softmax(logits).
+    Each opcode's relaxed gate is applied through its four polynomial coefficients, read off
+    _GATES at the corners of the unit square."""
+    probs = torch.softmax(logits, dim=-1)
+    n, _, h, w = x.shape
+    ho, wo = out_hw
+    lo = max(0, -int(min(oh.min(), ow.min())))
+    hi_h = max(0, (ho - 1) * stride + int(oh.max()) - (h - 1))
+    hi_w = max(0, (wo - 1) * stride + int(ow.max()) - (w - 1))
+    xp = torch.nn.functional.pad(x, (lo, hi_w, lo, hi_h))
+    oy = (torch.arange(ho) * stride).view(1, 1, ho, 1)
+    ox = (torch.arange(wo) * stride).view(1, 1, 1, wo)
+    taps = []
+    for side in (0, 1):
+        ch = och[side].long().unsqueeze(-1).unsqueeze(-1)                 # [Cout, G, 1, 1]
+        iy = oy + oh[side].long().unsqueeze(-1).unsqueeze(-1) + lo
+        ix = ox + ow[side].long().unsqueeze(-1).unsqueeze(-1) + lo
+        taps.append(xp[:, ch, iy, ix])                                     # [N, Cout, G, Ho, Wo]
+    a, b = taps
+    one, zero = torch.ones(()), torch.zeros(())
+    corners = torch.tensor([[float(gate(zero, zero)), float(gate(one, zero)),
+                             float(gate(zero, one)), float(gate(one, one))] for gate in _GATES],
+                           dtype=x.dtype)                                  # f00, f10, f01, f11
+    coef = torch.stack((corners[:, 0], corners[:, 1] - corners[:, 0], corners[:, 2] - corners[:, 0],
+                        corners[:, 3] - corners[:, 1] - corners[:, 2] + corners[:, 0]), dim=1)
+    c = coef[gate_sequence.long()]                                         # [Cout, G, 4]
+    c = [c[..., i].unsqueeze(-1).unsqueeze(-1) for i in range(4)]
+    op = c[0] + c[1] * a + c[2] * b + c[3] * (a * b)
+    return (op * probs.unsqueeze(-1).unsqueeze(-1)).sum(2)
+
+
 def group_sum(x: torch.Tensor, k: int, tau: float) -> torch.Tensor:
     if x.shape[-1] % k:
         x = torch.cat([x, torch.zeros((x.shape[0], k - x.shape[1] % k), dtype=x.dtype)], dim=1)
@@ -71,32 +107,57 @@ def group_sum(x: torch.Tensor, k: int, tau: float) -> torch.Tensor:
 
 
 class CpuDenseNet:
-    """CPU copy of a dense network: per layer (indices, gate_sequence, logits leaf)."""
+    """CPU copy of a network of soft layers: ('dense', indices, gate_sequence, logits),
+    ('conv', offsets_ch, offsets_h, offsets_w, gate_sequence, logits, stride, out_hw) and
+    ('flatten',) stages, then GroupSum; the logits are leaves that receive gradients."""
 
     def __init__(self, layers, k: int, tau: float, dtype=torch.float32):
-        self.layers = [(ind.cpu(), gs.cpu(), lg.detach().cpu().to(dtype).clone().requires_grad_(True))
-                       for ind, gs, lg in layers]
+        self.layers = []
+        for spec in layers:
+            if len(spec) == 3:                      # (indices, gate_sequence, logits)
+                spec = ("dense",) + tuple(spec)
+            if spec[0] == "flatten":
+                self.layers.append(spec)
+                continue
+            *bufs, lg = spec[1:-2] if spec[0] == "conv" else spec[1:]
+            leaf = lg.detach().cpu().to(dtype).clone().requires_grad_(True)
+            tail = tuple(spec[-2:]) if spec[0] == "conv" else ()
+            self.layers.append((spec[0],) + tuple(b.cpu() for b in bufs) + (leaf,) + tail)
         self.k, self.tau, self.dtype = k, tau, dtype
 
     @classmethod
     def from_model(cls, model, dtype=torch.float32):
         from_layers, k, tau = [], None, None
         for m in model:
-            if hasattr(m, "indices"):
-                from_layers.append((m.indices, m.gate_sequence, m.weights))
+            if hasattr(m, "offsets_ch"):
+                from_layers.append(("conv", m.offsets_ch, m.offsets_h, m.offsets_w,
+                                    m.gate_sequence, m.weights, m.stride, tuple(m.out_shape[1:])))
+            elif hasattr(m, "indices"):
+                from_layers.append(("dense", m.indices, m.gate_sequence, m.weights))
+            elif isinstance(m, torch.nn.Flatten):
+                from_layers.append(("flatten",))
             elif hasattr(m, "k"):
                 k, tau = m.k, m.tau
         return cls(from_layers, k, tau, dtype)
 
+    def leaves(self):
+        return [spec[-3] if spec[0] == "conv" else spec[-1]
+                for spec in self.layers if spec[0] != "flatten"]
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         h = x.cpu().to(self.dtype)
-        for ind, gs, lg in self.layers:
-            h = layer_forward(h, ind, gs, lg)
+        for spec in self.layers:
+            if spec[0] == "dense":
+                h = layer_forward(h, *spec[1:])
+            elif spec[0] == "conv":
+                h = conv_forward(h, *spec[1:])
+            else:
+                h = h.flatten(1)
         return group_sum(h, self.k, self.tau)
 
     def train_step(self, x: torch.Tensor, labels: torch.Tensor) -> float:
-        for _, _, lg in self.layers:
+        for lg in self.leaves():
             lg.grad = None
         loss = torch.nn.functional.cross_entropy(self.forward(x), labels.cpu())
         loss.backward()
-        return float(loss)
+        return float(loss.detach())

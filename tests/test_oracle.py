@@ -340,3 +340,30 @@ def test_torch_cpu_step_matches_oracle():
         p = torch.softmax(lg, -1).numpy()
         h = O.dense_forward(h, ind[0].numpy(), ind[1].numpy(), p, gs.numpy())
     np.testing.assert_allclose(out, O.group_sum(h.T, 4, 2.0), atol=1e-12)
+
+
+@pytest.mark.parametrize("stride,pad", [(2, 1), (1, 0), (2, 0)])
+def test_torch_cpu_conv_matches_oracle(stride, pad):
+    """The CPU baseline's conv layer (gather formulation, autograd backward) against the
+    loop-pinned float64 conv oracle, forward and both gradients."""
+    rng = np.random.default_rng(20 + stride + pad)
+    n_, c_in, h, wd, c_out, g_n, ks = 3, 4, 7, 8, 5, 6, 3
+    och = torch.as_tensor(rng.integers(0, c_in, (2, c_out, g_n)).astype(np.int32))
+    oh = torch.as_tensor((rng.integers(0, ks, (2, c_out, g_n)) - pad).astype(np.int8))
+    ow = torch.as_tensor((rng.integers(0, ks, (2, c_out, g_n)) - pad).astype(np.int8))
+    gs = torch.as_tensor(rng.integers(0, 16, (c_out, g_n)).astype(np.uint8))
+    logits = torch.randn(c_out, g_n, dtype=torch.float64, requires_grad=True)
+    x = torch.as_tensor(rng.random((n_, c_in, h, wd)), dtype=torch.float64).requires_grad_(True)
+    hw = O.conv_out_hw(h, wd, pad, ks, stride)
+    y = TC.conv_forward(x, och, oh, ow, gs, logits, stride, hw)
+    p = torch.softmax(logits, -1).detach().numpy()
+    args = (och.numpy(), oh.numpy(), ow.numpy())
+    np.testing.assert_allclose(y.detach().numpy(),
+                               O.conv_forward(x.detach().numpy(), *args, p, gs.numpy(), stride, pad, ks),
+                               atol=1e-12)
+    gy = rng.standard_normal(y.shape)
+    y.backward(torch.as_tensor(gy))
+    rgx, rgw = O.conv_backward(x.detach().numpy(), *args, p, gs.numpy(), gy, stride, pad)
+    np.testing.assert_allclose(x.grad.numpy(), rgx, atol=1e-12)
+    np.testing.assert_allclose(logits.grad.numpy(), p * (rgw - (p * rgw).sum(1, keepdims=True)),
+                               atol=1e-12)
