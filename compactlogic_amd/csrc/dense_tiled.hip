@@ -7,7 +7,7 @@
 // the 8 XCDs of an MI355X, so workgroup w runs on XCD w % 8, and chunk c is given only to
 // workgroups w with w % 8 == c % 8.  The chunk's band of the activation matrix (rows x CS
 // samples, 1.5-3 MB at 12000 rows) then stays in that XCD's 4 MB L2 and the second gather of
-// a row hits L2.  Outputs are written with non-temporal stores so they do not evict the band.
+// a row hits L2.  Outputs use ordinary write-back stores (see vst_stream).
 //
 // Per layer and training step:
 //   k_prep        logits -> softmax probabilities and the collapsed coefficients K of every

@@ -120,6 +120,38 @@ def backward_x(x, a, b, w, gate_seq, grad_y, given_x_indices_of_y_start, given_x
     return grad_x
 
 
+def inverse_index(a, b, in_dim: int):
+    """The inverse connection index of compactlogic/compactlogic.py:184-274 for pairs a, b
+    [out, G] (int64): per input i, entries start[i] .. start[i+1]-1 of (neuron, code) with
+    code g when i is operand a of slot g, -(g+1) when it is operand b.  Built on the tensors'
+    device; the order inside a row is ascending by (side, neuron, slot) (a stable sort)."""
+    dev = a.device
+    out, g = a.shape
+    rows = torch.arange(out, device=dev, dtype=torch.int64).unsqueeze(1).expand(out, g).reshape(-1)
+    slots = torch.arange(g, device=dev, dtype=torch.int64).unsqueeze(0).expand(out, g).reshape(-1)
+    inputs = torch.cat((a.reshape(-1), b.reshape(-1))).to(torch.int64)
+    ys = torch.cat((rows, rows))
+    codes = torch.cat((slots, -(slots + 1))).to(torch.int8)
+    order = torch.sort(inputs, stable=True).indices
+    counts = torch.bincount(inputs, minlength=in_dim)
+    starts = torch.zeros(in_dim + 1, dtype=torch.int64, device=dev)
+    starts[1:] = torch.cumsum(counts, 0)
+    return starts, ys[order].contiguous(), codes[order].contiguous()
+
+
+def backward_x_atomicAdd(x, a, b, w, gate_seq, grad_y):  # noqa: N802 - reference name
+    """difflogic_cuda.backward_x_atomicAdd (compactlogic/cuda/difflogic.cpp:99-104,
+    difflogic_kernel.cu:613-653): the same input gradient without a caller-supplied index.
+    The reference scatters with float atomics; here the index is built on the device and the
+    gradient gathered through it, so the result is deterministic."""
+    for t, n in ((x, "x"), (a, "a"), (b, "b"), (w, "w"), (gate_seq, "gate_seq"), (grad_y, "grad_y")):
+        _check(t, n)
+    _check_dtype(a, torch.int64, "a")
+    _check_dtype(b, torch.int64, "b")
+    start, ys, codes = inverse_index(a, b, x.shape[0])
+    return backward_x(x, a, b, w, gate_seq, grad_y, start, ys, codes)
+
+
 def eval(x, a, b, w, gate_seq):  # noqa: A001 - mirrors difflogic_cuda.eval
     """Discrete forward with argmax slots w (uint8 slot ids) (difflogic_kernel.cu:341-411)."""
     for t, n in ((x, "x"), (a, "a"), (b, "b"), (w, "w"), (gate_seq, "gate_seq")):

@@ -381,20 +381,10 @@ class LogicLayer(torch.nn.Module):
         if changed_rows is not None and "given_x_indices_of_y_start" in self._buffers:
             if torch.as_tensor(changed_rows).numel() == 0:
                 return
-        dev = self.indices.device
-        _, out, g = self.indices.shape
-        rows = torch.arange(out, device=dev, dtype=torch.int64).unsqueeze(1).expand(out, g).reshape(-1)
-        slots = torch.arange(g, device=dev, dtype=torch.int64).unsqueeze(0).expand(out, g).reshape(-1)
-        inputs = torch.cat((self.indices[0].reshape(-1), self.indices[1].reshape(-1)))
-        ys = torch.cat((rows, rows))
-        codes = torch.cat((slots, -(slots + 1))).to(torch.int8)
-        order = torch.sort(inputs, stable=True).indices
-        counts = torch.bincount(inputs, minlength=self.in_dim)
-        starts = torch.zeros(self.in_dim + 1, dtype=torch.int64, device=dev)
-        starts[1:] = torch.cumsum(counts, 0)
+        starts, ys, codes = _dl.inverse_index(self.indices[0], self.indices[1], self.in_dim)
         self._set_or_register_buffer("given_x_indices_of_y_start", starts)
-        self._set_or_register_buffer("given_x_indices_of_y", ys[order])
-        self._set_or_register_buffer("given_x_indices_of_gate", codes[order])
+        self._set_or_register_buffer("given_x_indices_of_y", ys)
+        self._set_or_register_buffer("given_x_indices_of_gate", codes)
         self._plan = None
 
     def run_plan(self) -> RunPlan:

@@ -79,6 +79,9 @@ def test_dropin_kernels_match_oracle(device, dtype, shape):
                        torch.as_tensor(code, device=device))
     np.testing.assert_allclose(np_(gx), O.dense_backward_x_direct(L["x"], L["a"], L["b"], L["w"],
                                                                  L["gs"], L["gy"]), **TOL[dtype])
+    # the index-free variant builds its own index and gathers through it
+    gx2 = dl.backward_x_atomicAdd(D["x"], D["a"], D["b"], D["w"], D["gs"], D["gy"])
+    np.testing.assert_allclose(np_(gx2), np_(gx), **TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
