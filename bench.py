@@ -190,6 +190,18 @@ def kernel_table(summary: dict, nbytes_of: dict) -> dict:
     return out
 
 
+def measured_traffic() -> dict:
+    """HBM-side bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) of the dominant kernels,
+    from the committed counter profile; a kernel that is not listed reports null."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "traffic_per_launch.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["bytes"]
+    except (OSError, ValueError, KeyError):
+        return {}
+
+
 def roofline_of(kernels: dict, how: str) -> dict:
     """The dominant kernel (largest total time per step among those with a byte count)."""
     name = max((k for k in kernels if kernels[k]["algorithmic_bytes"]),
@@ -197,8 +209,11 @@ def roofline_of(kernels: dict, how: str) -> dict:
     d = kernels[name]
     return {"bound": "hbm", "achieved": round(d["achieved_GBs"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(d["achieved_GBs"] / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel": name, "per_launch_ms": round(d["seconds"] * 1e3, 4),
-            "algorithmic_bytes_per_launch": d["algorithmic_bytes"], "measured": how}
+            "traffic": measured_traffic().get(name), "kernel": name,
+            "per_launch_ms": round(d["seconds"] * 1e3, 4),
+            "algorithmic_bytes_per_launch": d["algorithmic_bytes"], "measured": how,
+            "traffic_source": "profiles/traffic_per_launch.json (rocprofv3 --pmc FETCH_SIZE / "
+                              "WRITE_SIZE of this command, calibrated by a 512 MiB copy)"}
 
 
 def kernels_json(kernels: dict, steps: int) -> dict:
