@@ -141,7 +141,10 @@ def train_kernel_bytes(model, batch: int) -> dict:
             xb = 4 * batch * c * h * w
             yb = 4 * batch * m.c_out * m.h_out * m.w_out
             out.update({"cl_conv_forward" + tag: xb + yb, "cl_conv_backward_x" + tag: 2 * xb + yb,
-                        "cl_conv_backward_w" + tag: xb + yb})
+                        "cl_conv_backward_w" + tag: xb + yb,
+                        "cl_conv_window_forward" + tag: xb + yb,
+                        "cl_conv_window_backward_x" + tag: 2 * xb + yb,
+                        "cl_conv_window_moments" + tag: xb + yb})
         elif isinstance(m, cl.LogicLayer):
             tag = f"[{m.in_dim}->{m.out_dim}]"
             xb, yb = 4 * batch * m.in_dim, 4 * batch * m.out_dim

@@ -6,13 +6,14 @@ ConvLayerCudaFunction, plus the packed-bit inference API (PackBitsTensor).  All 
 ``python -m compactlogic_amd.build``.
 """
 from . import convlogic_hip, difflogic_hip
-from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction, GroupSum,
-                     GroupSumFunction, LogicLayer, LogicLayerCudaFunction,
-                     LogicLayerRunsFunction, PackBitsTensor)
+from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction,
+                     ConvLayerWindowFunction, GroupSum, GroupSumFunction, LogicLayer,
+                     LogicLayerCudaFunction, LogicLayerRunsFunction, PackBitsTensor)
 from .plan import RunPlan, build_run_plan
 
 __all__ = [
     "LogicLayer", "GroupSum", "LogicLayerCudaFunction", "LogicLayerRunsFunction",
     "GroupSumFunction", "PackBitsTensor", "RunPlan", "build_run_plan", "difflogic_hip",
-    "ConvLayer", "ConvLayerCudaFunction", "ConvLayerSoftmaxFunction", "convlogic_hip",
+    "ConvLayer", "ConvLayerCudaFunction", "ConvLayerSoftmaxFunction", "ConvLayerWindowFunction",
+    "convlogic_hip",
 ]

@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import weakref
+from dataclasses import dataclass
 
 import torch
 
@@ -121,6 +122,73 @@ def inverse_index(offsets_ch, offsets_h, offsets_w, c_in, stride):
     _INDEX_CACHE.update(live)
     _INDEX_CACHE[key] = (tuple(weakref.ref(t) for t in (offsets_ch, offsets_h, offsets_w)), state, out)
     return out
+
+
+@dataclass
+class WindowPlan:
+    """Tables of the window path (every output channel reads one input channel; all taps in a
+    kw x kw window at offset (oy0, ox0) of the output position times the stride)."""
+    kw: int
+    oy0: int
+    ox0: int
+    width: int                # coefficients per channel
+    max_group: int            # most output channels reading one input channel
+    slot_win: torch.Tensor    # int32 [Cout, G]: window index of operand a | of operand b << 8
+    grp_ptr: torch.Tensor     # int32 [Cin + 1]
+    chan_order: torch.Tensor  # int32 [Cout]
+
+
+_WINDOW_CACHE: dict = {}
+
+
+def window_plan(offsets_ch, offsets_h, offsets_w, c_in: int):
+    """The WindowPlan of these offsets, or None when some output channel reads more than one
+    input channel or the taps span more than a 3 x 3 window.  Cached like inverse_index (the
+    eligibility test reads a few scalars back from the device once per offsets version)."""
+    key = (id(offsets_ch), id(offsets_h), id(offsets_w), int(c_in))
+    state = tuple((t.data_ptr(), t._version) for t in (offsets_ch, offsets_h, offsets_w))
+    hit = _WINDOW_CACHE.get(key)
+    if hit is not None:
+        refs, hit_state, out = hit
+        if all(r() is t for r, t in zip(refs, (offsets_ch, offsets_h, offsets_w))) and hit_state == state:
+            return out
+    out = _build_window_plan(offsets_ch, offsets_h, offsets_w, int(c_in))
+    live = {k: v for k, v in _WINDOW_CACHE.items() if all(r() is not None for r in v[0])}
+    _WINDOW_CACHE.clear()
+    _WINDOW_CACHE.update(live)
+    _WINDOW_CACHE[key] = (tuple(weakref.ref(t) for t in (offsets_ch, offsets_h, offsets_w)), state, out)
+    return out
+
+
+def _build_window_plan(offsets_ch, offsets_h, offsets_w, c_in: int):
+    _, cout, g = offsets_ch.shape
+    if cout == 0 or g > 64:
+        return None
+    dev = offsets_ch.device
+    ch = offsets_ch.to(torch.int64)
+    first = ch[0, :, :1]
+    stats = torch.stack((
+        (ch != first.unsqueeze(0)).any().to(torch.int64),
+        ((first < 0) | (first >= c_in)).any().to(torch.int64),
+        offsets_h.min().to(torch.int64), offsets_h.max().to(torch.int64),
+        offsets_w.min().to(torch.int64), offsets_w.max().to(torch.int64))).tolist()
+    mixed, out_of_range, hmin, hmax, wmin, wmax = stats
+    kw = max(hmax - hmin, wmax - wmin) + 1
+    if mixed or out_of_range or kw > 3:
+        return None
+    win = (offsets_h.to(torch.int64) - hmin) * kw + (offsets_w.to(torch.int64) - wmin)
+    slot_win = (win[0] | (win[1] << 8)).to(torch.int32).contiguous()
+    chan = first.squeeze(1)
+    chan_order = torch.sort(chan, stable=True).indices
+    counts = torch.bincount(chan, minlength=c_in)
+    grp_ptr = torch.zeros(c_in + 1, dtype=torch.int64, device=dev)
+    grp_ptr[1:] = torch.cumsum(counts, 0)
+    width = ctypes.c_int64(0)
+    _capi.call("cl_conv_window_coef_width", kw, ctypes.byref(width))
+    return WindowPlan(kw=int(kw), oy0=int(hmin), ox0=int(wmin), width=width.value,
+                      max_group=int(counts.max()), slot_win=slot_win,
+                      grp_ptr=grp_ptr.to(torch.int32).contiguous(),
+                      chan_order=chan_order.to(torch.int32).contiguous())
 
 
 def backward_x(x, offsets_ch, offsets_h, offsets_w, w, gate_seq, grad_y, stride, pad, index=None):

@@ -1,0 +1,501 @@
+// Window path of the ConvLayer for gfx950: layers whose output channels each read a single
+// input channel (ConvLayer's default num_chn = 1 wiring, compactlogic/compactlogic.py:678-683).
+//
+// Every slot of output channel c then reads two taps of the same input plane inside one
+// KW x KW window anchored at (oy*s + oy0, ox*s + ox0), KW <= 3.  With the window values
+// v_0 .. v_{P-1} (P = KW^2, zero outside the plane) the relaxed layer is a quadratic form
+//     y = K + sum_k alpha_k v_k + sum_{k <= l} beta_kl v_k v_l
+// whose coefficients collapse all G slots (slot g with taps (a, b) adds p_g * c0 to K,
+// p_g * c1 to alpha_a, p_g * c2 to alpha_b and p_g * c3 to beta_{min(a,b) max(a,b)}).  So:
+//   k_win_prep      softmax of the logits and the coefficients of every channel, summed in
+//                   slot order (one wave per channel, lane j owns coefficient j)
+//   k_win_fwd       one thread per output position of one (sample, input channel): loads the
+//                   window once, evaluates every output channel reading that input channel
+//   k_win_bwd_x     one workgroup per (sample, input channel): per position the derivative
+//                   of sum_c gy_c y_c with respect to each window value, accumulated into an
+//                   LDS copy of the input plane one window position at a time (positions map
+//                   to distinct pixels for a fixed window index, so no two threads collide and
+//                   the summation order is fixed)
+//   k_win_moments   per (input channel, pair of output channels, sample chunk): the moments
+//                   sum gy, sum gy v_k, sum gy v_k v_l over the chunk, reduced in a fixed order
+//   k_win_finalize  moments summed over chunks in order -> gradient of every slot -> softmax
+//                   backward -> gradient of the logits
+// The coefficient block of a channel is [K, alpha_0 .. alpha_{P-1}, beta_00, beta_01, ...,
+// beta_{P-1,P-1}] (upper triangle by rows), padded to a multiple of 4.
+#include "common.h"
+
+#include <algorithm>
+
+namespace cl {
+namespace {
+
+template <int KW>
+struct Win {
+    static constexpr int P = KW * KW;
+    static constexpr int NP = P * (P + 1) / 2;
+    static constexpr int CW = (1 + P + NP + 3) & ~3;
+};
+
+// Index of beta_kl (k <= l) inside the coefficient block.
+__host__ __device__ constexpr int beta_at(int P, int k, int l) {
+    return 1 + P + k * P - k * (k - 1) / 2 + (l - k);
+}
+
+int coef_width(int kw) {
+    switch (kw) {
+        case 1: return Win<1>::CW;
+        case 2: return Win<2>::CW;
+        case 3: return Win<3>::CW;
+        default: return 0;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+template <typename T, int KW>
+__global__ __launch_bounds__(256) void k_win_prep(const T* __restrict__ w, int softmax,
+                                                  const uint8_t* __restrict__ gs,
+                                                  const int32_t* __restrict__ slot_win,
+                                                  T* __restrict__ probs, T* __restrict__ coef,
+                                                  int64_t Cout, int G) {
+    constexpr int P = Win<KW>::P, CW = Win<KW>::CW;
+    const int64_t c = int64_t(blockIdx.x) * 4 + wave_id();
+    if (c >= Cout) return;  // uniform per wave
+    const int l = lane_id();
+    T p = l < G ? w[c * G + l] : T(0);
+    if (softmax) {
+        T m = l < G ? p : -__builtin_inf();
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = std::max(m, __shfl_xor(m, off, kWave));
+        const T e = l < G ? T(exp(p - m)) : T(0);
+        p = e / wave_total(e);
+    }
+    if (probs && l < G) probs[c * G + l] = p;
+    T acc = 0;
+    for (int g = 0; g < G; ++g) {
+        const T pg = read_lane(p, g);
+        const Coef4<T> cf = gate_coef<T>(gs[c * G + g]);
+        const int rec = slot_win[c * G + g];
+        const int ka = rec & 0xff, kb = (rec >> 8) & 0xff;
+        const int lo = std::min(ka, kb), hi = std::max(ka, kb);
+        T add = 0;
+        if (l == 0) add += pg * cf.c0;
+        if (l == 1 + ka) add += pg * cf.c1;
+        if (l == 1 + kb) add += pg * cf.c2;
+        if (l == beta_at(P, lo, hi)) add += pg * cf.c3;
+        acc += add;
+    }
+    if (l < CW) coef[c * CW + l] = acc;
+}
+
+// Window values of the thread's output position; zero outside the plane or past the end.
+template <typename T, int KW>
+__device__ __forceinline__ void load_window(T (&v)[KW * KW], const T* __restrict__ plane, int H,
+                                            int W, int by, int bx, bool active) {
+#pragma unroll
+    for (int kh = 0; kh < KW; ++kh) {
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw) {
+            const int yy = by + kh, xx = bx + kw;
+            const bool ok = active && unsigned(yy) < unsigned(H) && unsigned(xx) < unsigned(W);
+            v[kh * KW + kw] = ok ? plane[yy * W + xx] : T(0);
+        }
+    }
+}
+
+struct WinDims {
+    int64_t N, Cin, Cout;
+    int H, W, Ho, Wo, stride, oy0, ox0;
+};
+
+// ------------------------------------------------------------------------------------------
+// Block = BS threads over the output positions of sample n and input channel ch
+// (blockIdx.x = (n * Cin + ch) * pchunks + chunk).
+template <typename T, int KW>
+__global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const T* __restrict__ coef,
+                                                 const int32_t* __restrict__ grp_ptr,
+                                                 const int32_t* __restrict__ chan_order,
+                                                 T* __restrict__ y, int pchunks, WinDims d) {
+    constexpr int P = Win<KW>::P, CW = Win<KW>::CW;
+    const int64_t blk = blockIdx.x;
+    const int chunk = int(blk % pchunks);
+    const int64_t nc = blk / pchunks;
+    const int64_t ch = nc % d.Cin, n = nc / d.Cin;
+    const int hw = d.Ho * d.Wo;
+    const int pos = chunk * int(blockDim.x) + int(threadIdx.x);
+    const int c0 = grp_ptr[ch], c1 = grp_ptr[ch + 1];
+    if (c0 == c1 || pos >= hw) return;
+    const int oy = pos / d.Wo, ox = pos - oy * d.Wo;
+    T v[P];
+    load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(d.H) * d.W, d.H, d.W,
+                       oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
+    T* yn = y + n * d.Cout * hw + pos;
+    for (int i = c0; i < c1; ++i) {
+        const int c = chan_order[i];
+        const T* cf = coef + int64_t(c) * CW;
+        T acc = cf[0];
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            T t = cf[1 + k];
+#pragma unroll
+            for (int l = k; l < P; ++l) t = fma(cf[beta_at(P, k, l)], v[l], t);
+            acc = fma(v[k], t, acc);
+        }
+        yn[int64_t(c) * hw] = acc;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Block (sample n, input channel ch): BS >= Ho * Wo threads, one per output position; the
+// input-gradient plane of (n, ch) is built in LDS and written out whole.
+template <typename T, int KW>
+__global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
+                                                    const T* __restrict__ gy,
+                                                    const T* __restrict__ coef,
+                                                    const int32_t* __restrict__ grp_ptr,
+                                                    const int32_t* __restrict__ chan_order,
+                                                    T* __restrict__ gx, WinDims d) {
+    constexpr int P = Win<KW>::P, NP = Win<KW>::NP, CW = Win<KW>::CW;
+    extern __shared__ __align__(16) unsigned char smem[];
+    T* plane = reinterpret_cast<T*>(smem);
+    const int64_t ch = blockIdx.x % d.Cin, n = blockIdx.x / d.Cin;
+    const int hw = d.Ho * d.Wo, HW = d.H * d.W;
+    const int pos = threadIdx.x;
+    const bool active = pos < hw;
+    const int oy = active ? pos / d.Wo : 0, ox = active ? pos - oy * d.Wo : 0;
+    const int by = oy * d.stride + d.oy0, bx = ox * d.stride + d.ox0;
+    const T* xplane = x + (n * d.Cin + ch) * int64_t(HW);
+    T v[P];
+    load_window<T, KW>(v, xplane, d.H, d.W, by, bx, active);
+    // A_k = sum_c gy_c alpha_kc, B_kl = sum_c gy_c beta_klc over the channels reading ch
+    T A[P], B[NP];
+#pragma unroll
+    for (int k = 0; k < P; ++k) A[k] = 0;
+#pragma unroll
+    for (int q = 0; q < NP; ++q) B[q] = 0;
+    const int c0 = grp_ptr[ch], c1 = grp_ptr[ch + 1];
+    const T* gyn = gy + n * d.Cout * hw + pos;
+    for (int i = c0; i < c1; ++i) {
+        const int c = chan_order[i];
+        const T g = active ? gyn[int64_t(c) * hw] : T(0);
+        const T* cf = coef + int64_t(c) * CW;
+#pragma unroll
+        for (int k = 0; k < P; ++k) A[k] = fma(g, cf[1 + k], A[k]);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) B[q] = fma(g, cf[1 + P + q], B[q]);
+    }
+    for (int i = threadIdx.x; i < HW; i += blockDim.x) plane[i] = T(0);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        // d(sum_c gy_c y_c)/dv_k = A_k + sum_{l != k} B_{kl} v_l + 2 B_kk v_k
+        T dk = A[k];
+#pragma unroll
+        for (int l = 0; l < P; ++l) {
+            const int q = (l < k ? beta_at(P, l, k) : beta_at(P, k, l)) - 1 - P;
+            dk = fma(l == k ? T(2) * B[q] : B[q], v[l], dk);
+        }
+        const int yy = by + k / KW, xx = bx + k % KW;
+        if (active && unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W))
+            plane[yy * d.W + xx] += dk;
+        __syncthreads();
+    }
+    T* gplane = gx + (n * d.Cin + ch) * int64_t(HW);
+    for (int i = threadIdx.x; i < HW; i += blockDim.x) gplane[i] = plane[i];
+}
+
+// ------------------------------------------------------------------------------------------
+// Moments: block (ch, sub-block sb of CB channels, sample chunk q), BS threads over the
+// output positions (several passes when Ho * Wo > BS).  part[q, c, j] for j < CW.
+template <typename T, int KW, int CB>
+__global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
+                                                     const T* __restrict__ gy,
+                                                     const int32_t* __restrict__ grp_ptr,
+                                                     const int32_t* __restrict__ chan_order,
+                                                     T* __restrict__ part, int nsub, int nq,
+                                                     WinDims d) {
+    constexpr int P = Win<KW>::P, NM = 1 + P + Win<KW>::NP, CW = Win<KW>::CW;
+    __shared__ T red[4][CB * NM];
+    const int q = blockIdx.y;
+    const int64_t ch = blockIdx.x / nsub;
+    const int sb = blockIdx.x % nsub;
+    const int g0 = grp_ptr[ch] + sb * CB, g1 = std::min(grp_ptr[ch + 1], g0 + CB);
+    if (g0 >= g1) return;  // uniform per block
+    int cs[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) cs[j] = g0 + j < g1 ? chan_order[g0 + j] : -1;
+    const int hw = d.Ho * d.Wo, HW = d.H * d.W;
+    const int64_t n0 = q * d.N / nq, n1 = (q + 1) * d.N / nq;
+    T S[CB][NM];
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) S[j][m] = 0;
+    for (int p0 = 0; p0 < hw; p0 += blockDim.x) {
+        const int pos = p0 + threadIdx.x;
+        const bool active = pos < hw;
+        const int oy = active ? pos / d.Wo : 0, ox = active ? pos - oy * d.Wo : 0;
+        const int by = oy * d.stride + d.oy0, bx = ox * d.stride + d.ox0;
+        for (int64_t n = n0; n < n1; ++n) {
+            T v[P];
+            load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(HW), d.H, d.W, by, bx, active);
+            const T* gyn = gy + n * d.Cout * hw + pos;
+#pragma unroll
+            for (int j = 0; j < CB; ++j) {
+                const T g = (active && cs[j] >= 0) ? gyn[int64_t(cs[j]) * hw] : T(0);
+                S[j][0] += g;
+#pragma unroll
+                for (int k = 0; k < P; ++k) {
+                    const T gv = g * v[k];
+                    S[j][1 + k] += gv;
+#pragma unroll
+                    for (int l = k; l < P; ++l) S[j][beta_at(P, k, l)] = fma(gv, v[l], S[j][beta_at(P, k, l)]);
+                }
+            }
+        }
+    }
+    const int wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const T t = wave_total(S[j][m]);
+            if ((threadIdx.x & 63) == 0) red[wv][j * NM + m] = t;
+        }
+    __syncthreads();
+    const int nw = int(blockDim.x) >> 6;
+    for (int i = threadIdx.x; i < CB * CW; i += blockDim.x) {
+        const int j = i / CW, m = i % CW;
+        if (cs[j] < 0) continue;
+        T t = 0;
+        if (m < NM)
+            for (int w2 = 0; w2 < nw; ++w2) t += red[w2][j * NM + m];
+        part[(int64_t(q) * d.Cout + cs[j]) * CW + m] = t;
+    }
+}
+
+// One wave per channel: moments summed over the chunks in order (lane j: moment j), then
+// slot g (lane g) takes c0 S0 + c1 S_a + c2 S_b + c3 S_ab; with probs the softmax backward.
+template <typename T, int KW>
+__global__ __launch_bounds__(256) void k_win_finalize(const T* __restrict__ part, int nq,
+                                                      const uint8_t* __restrict__ gs,
+                                                      const int32_t* __restrict__ slot_win,
+                                                      const T* __restrict__ probs,
+                                                      T* __restrict__ grad_w, int64_t Cout,
+                                                      int G) {
+    constexpr int P = Win<KW>::P, CW = Win<KW>::CW;
+    const int64_t c = int64_t(blockIdx.x) * 4 + wave_id();
+    if (c >= Cout) return;  // uniform per wave
+    const int l = lane_id();
+    T s = 0;
+    if (l < CW)
+        for (int q = 0; q < nq; ++q) s += part[(int64_t(q) * Cout + c) * CW + l];
+    T gw = 0;
+    int ia = 0, ib = 0, iab = 0;
+    Coef4<T> cf = gate_coef<T>(0);
+    if (l < G) {
+        const int rec = slot_win[c * G + l];
+        const int ka = rec & 0xff, kb = (rec >> 8) & 0xff;
+        ia = 1 + ka;
+        ib = 1 + kb;
+        iab = beta_at(P, std::min(ka, kb), std::max(ka, kb));
+        cf = gate_coef<T>(gs[c * G + l]);
+    }
+    const T s0 = read_lane(s, 0);
+    const T sa = __shfl(s, ia, kWave), sb = __shfl(s, ib, kWave), sab = __shfl(s, iab, kWave);
+    if (l < G) gw = fma(cf.c3, sab, fma(cf.c2, sb, fma(cf.c1, sa, cf.c0 * s0)));
+    if (probs) {
+        const T p = l < G ? probs[c * G + l] : T(0);
+        const T dot = wave_total(p * gw);
+        gw = p * (gw - dot);
+    }
+    if (l < G) grad_w[c * G + l] = gw;
+}
+
+int win_dims(WinDims& d, int64_t N, int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+             int64_t stride, int64_t h_out, int64_t w_out, int64_t oy0, int64_t ox0, int64_t kw) {
+    CL_ARG(N >= 0 && Cin >= 1 && Cout >= 0 && H >= 1 && W >= 1, "bad shape");
+    CL_ARG(h_out >= 1 && w_out >= 1 && stride >= 1, "bad output plane or stride");
+    CL_ARG(kw >= 1 && kw <= 3, "window width must be 1, 2 or 3");
+    CL_ARG(H * W < (int64_t(1) << 24) && h_out * w_out < (int64_t(1) << 24),
+           "planes too large for the window path");
+    CL_ARG(oy0 > -128 && oy0 < 128 && ox0 > -128 && ox0 < 128, "bad window origin");
+    d = WinDims{N, Cin, Cout, int(H), int(W), int(h_out), int(w_out), int(stride), int(oy0),
+                int(ox0)};
+    return CL_OK;
+}
+
+template <typename F>
+int with_kw(int64_t kw, F&& f) {
+    switch (kw) {
+        case 1: return f(std::integral_constant<int, 1>());
+        case 2: return f(std::integral_constant<int, 2>());
+        case 3: return f(std::integral_constant<int, 3>());
+        default: set_error("window width must be 1, 2 or 3"); return CL_ERR_INVALID_ARGUMENT;
+    }
+}
+
+int block_for(int64_t hw, int cap) {
+    int64_t b = ceil_div(hw, 64) * 64;
+    return int(std::min<int64_t>(b, cap));
+}
+
+constexpr int kWinCB = 2;  // output channels per moments block
+
+}  // namespace
+}  // namespace cl
+
+using namespace cl;
+
+extern "C" int cl_conv_window_coef_width(int64_t kw, int64_t* width) {
+    clear_error();
+    CL_ARG(width, "null pointer argument");
+    const int w = coef_width(int(kw));
+    CL_ARG(w > 0, "window width must be 1, 2 or 3");
+    *width = w;
+    return CL_OK;
+}
+
+extern "C" int cl_conv_window_prep(int dtype, const void* w, int softmax, const uint8_t* gate_seq,
+                                   const int32_t* slot_win, void* probs, void* coef,
+                                   int64_t Cout, int64_t num_gates, int64_t kw, void* stream) {
+    clear_error();
+    CL_ARG(Cout >= 0 && num_gates >= 1 && num_gates <= 64, "num_gates must be in [1, 64]");
+    if (Cout == 0) return CL_OK;
+    CL_ARG(w && gate_seq && slot_win && coef, "null pointer argument");
+    const unsigned blocks = unsigned(ceil_div(Cout, 4));
+    CL_DTYPE_SWITCH(dtype, {
+        int rc = with_kw(kw, [&](auto K) {
+            k_win_prep<scalar_t, decltype(K)::value><<<blocks, 256, 0, as_stream(stream)>>>(
+                static_cast<const scalar_t*>(w), softmax, gate_seq, slot_win,
+                static_cast<scalar_t*>(probs), static_cast<scalar_t*>(coef), Cout,
+                int(num_gates));
+            return CL_OK;
+        });
+        if (rc) return rc;
+    });
+    return check_launch("cl_conv_window_prep");
+}
+
+extern "C" int cl_conv_window_forward(int dtype, const void* x, const void* coef,
+                                      const int32_t* grp_ptr, const int32_t* chan_order, void* y,
+                                      int64_t N, int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+                                      int64_t stride, int64_t h_out, int64_t w_out, int64_t oy0,
+                                      int64_t ox0, int64_t kw, void* stream) {
+    clear_error();
+    WinDims d;
+    if (int rc = win_dims(d, N, Cin, H, W, Cout, stride, h_out, w_out, oy0, ox0, kw)) return rc;
+    if (N == 0 || Cout == 0) return CL_OK;
+    CL_ARG(x && coef && grp_ptr && chan_order && y, "null pointer argument");
+    const int hw = d.Ho * d.Wo;
+    const int bs = block_for(hw, 256);
+    const int64_t pchunks = ceil_div(hw, bs);
+    const int64_t blocks = N * Cin * pchunks;
+    CL_ARG(blocks < (int64_t(1) << 32), "conv layer too large for one launch");
+    CL_DTYPE_SWITCH(dtype, {
+        int rc = with_kw(kw, [&](auto K) {
+            k_win_fwd<scalar_t, decltype(K)::value><<<unsigned(blocks), bs, 0, as_stream(stream)>>>(
+                static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(coef), grp_ptr,
+                chan_order, static_cast<scalar_t*>(y), int(pchunks), d);
+            return CL_OK;
+        });
+        if (rc) return rc;
+    });
+    return check_launch("cl_conv_window_forward");
+}
+
+extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* grad_y,
+                                         const void* coef, const int32_t* grp_ptr,
+                                         const int32_t* chan_order, void* grad_x, int64_t N,
+                                         int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+                                         int64_t stride, int64_t h_out, int64_t w_out,
+                                         int64_t oy0, int64_t ox0, int64_t kw, void* stream) {
+    clear_error();
+    WinDims d;
+    if (int rc = win_dims(d, N, Cin, H, W, Cout, stride, h_out, w_out, oy0, ox0, kw)) return rc;
+    if (N == 0) return CL_OK;
+    CL_ARG(x && grad_y && coef && grp_ptr && chan_order && grad_x, "null pointer argument");
+    const int64_t hw = h_out * w_out;
+    CL_ARG(hw <= 1024, "the window input gradient needs h_out * w_out <= 1024");
+    const size_t tsize = dtype == CL_DTYPE_F64 ? 8 : 4;
+    const size_t lds = size_t(H * W) * tsize;
+    CL_ARG(lds <= 65536, "the window input gradient needs the input plane in 64 KiB of LDS");
+    const int bs = block_for(hw, 1024);
+    const int64_t blocks = N * Cin;
+    CL_ARG(blocks < (int64_t(1) << 32), "conv layer too large for one launch");
+    CL_DTYPE_SWITCH(dtype, {
+        int rc = with_kw(kw, [&](auto K) {
+            k_win_bwd_x<scalar_t, decltype(K)::value>
+                <<<unsigned(blocks), bs, lds, as_stream(stream)>>>(
+                    static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(grad_y),
+                    static_cast<const scalar_t*>(coef), grp_ptr, chan_order,
+                    static_cast<scalar_t*>(grad_x), d);
+            return CL_OK;
+        });
+        if (rc) return rc;
+    });
+    return check_launch("cl_conv_window_backward_x");
+}
+
+extern "C" int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t* nq) {
+    clear_error();
+    CL_ARG(nq && N >= 0 && Cin >= 1 && max_group >= 0, "bad argument");
+    // about 1024 blocks, but at least 32 samples per chunk so that the closing reduction of
+    // a block stays small against its accumulation loop
+    const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
+    const int64_t want = ceil_div(1024, Cin * nsub);
+    *nq = std::max<int64_t>(1, std::min<int64_t>(want, N / 32));
+    return CL_OK;
+}
+
+extern "C" int cl_conv_window_moments(int dtype, const void* x, const void* grad_y,
+                                      const int32_t* grp_ptr, const int32_t* chan_order,
+                                      void* moments, int64_t nq, int64_t max_group, int64_t N,
+                                      int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+                                      int64_t stride, int64_t h_out, int64_t w_out, int64_t oy0,
+                                      int64_t ox0, int64_t kw, void* stream) {
+    clear_error();
+    WinDims d;
+    if (int rc = win_dims(d, N, Cin, H, W, Cout, stride, h_out, w_out, oy0, ox0, kw)) return rc;
+    if (Cout == 0) return CL_OK;
+    CL_ARG(grp_ptr && chan_order && moments, "null pointer argument");
+    CL_ARG(N == 0 || (x && grad_y), "null pointer argument");
+    CL_ARG(nq >= 1 && nq < 65536 && max_group >= 0, "bad chunk count");
+    const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
+    const int64_t bx = Cin * nsub;
+    CL_ARG(bx < (int64_t(1) << 31), "conv layer too large for one launch");
+    const int bs = block_for(h_out * w_out, 256);
+    const dim3 grid(unsigned(bx), unsigned(nq), 1);
+    CL_DTYPE_SWITCH(dtype, {
+        int rc = with_kw(kw, [&](auto K) {
+            k_win_moments<scalar_t, decltype(K)::value, kWinCB><<<grid, bs, 0, as_stream(stream)>>>(
+                static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(grad_y), grp_ptr,
+                chan_order, static_cast<scalar_t*>(moments), int(nsub), int(nq), d);
+            return CL_OK;
+        });
+        if (rc) return rc;
+    });
+    return check_launch("cl_conv_window_moments");
+}
+
+extern "C" int cl_conv_window_finalize(int dtype, const void* moments, int64_t nq,
+                                       const uint8_t* gate_seq, const int32_t* slot_win,
+                                       const void* probs, void* grad_w, int64_t Cout,
+                                       int64_t num_gates, int64_t kw, void* stream) {
+    clear_error();
+    CL_ARG(Cout >= 0 && num_gates >= 1 && num_gates <= 64, "num_gates must be in [1, 64]");
+    if (Cout == 0) return CL_OK;
+    CL_ARG(moments && gate_seq && slot_win && grad_w, "null pointer argument");
+    CL_ARG(nq >= 1, "bad chunk count");
+    const unsigned blocks = unsigned(ceil_div(Cout, 4));
+    CL_DTYPE_SWITCH(dtype, {
+        int rc = with_kw(kw, [&](auto K) {
+            k_win_finalize<scalar_t, decltype(K)::value><<<blocks, 256, 0, as_stream(stream)>>>(
+                static_cast<const scalar_t*>(moments), int(nq), gate_seq, slot_win,
+                static_cast<const scalar_t*>(probs), static_cast<scalar_t*>(grad_w), Cout,
+                int(num_gates));
+            return CL_OK;
+        });
+        if (rc) return rc;
+    });
+    return check_launch("cl_conv_window_finalize");
+}

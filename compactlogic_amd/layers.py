@@ -570,6 +570,81 @@ class ConvLayerSoftmaxFunction(torch.autograd.Function):
         return grad_x, None, None, None, grad_w, None, None, None, None
 
 
+class ConvLayerWindowFunction(torch.autograd.Function):
+    """ConvLayer training step through the window path (every output channel reads one input
+    channel): the softmax and the collapse of all slots into per-channel window coefficients
+    run in one prep kernel; the forward evaluates every output channel of an input channel
+    from one load of each window; the backward gives the input gradient per (sample, input
+    channel) plane and the gradient of the logits from per-chunk window moments."""
+
+    @staticmethod
+    def forward(ctx, x, logits, gate_sequence, plan, stride: int, out_hw: tuple):
+        for t, nm in ((x, "x"), (gate_sequence, "gate_sequence"), (plan.slot_win, "slot_win")):
+            _dl._check(t, nm)
+        _dl._same_device(x, logits, gate_sequence, plan.slot_win, plan.grp_ptr, plan.chan_order)
+        if logits.dtype != x.dtype:
+            raise RuntimeError("logits must have the dtype of x")
+        n, cin, h, w = x.shape
+        cout, g = logits.shape
+        if (plan.grp_ptr.numel() != cin + 1 or plan.chan_order.numel() != cout
+                or tuple(plan.slot_win.shape) != (cout, g)
+                or tuple(gate_sequence.shape) != (cout, g)):
+            raise RuntimeError("window plan, gate_sequence and logits do not match the input")
+        ho, wo = out_hw
+        code = _dl.dtype_code(x)
+        stream = _dl.stream_of(x)
+        logits = logits.contiguous()
+        probs = torch.empty_like(logits)
+        coef = torch.empty((cout, plan.width), dtype=x.dtype, device=x.device)
+        y = torch.empty((n, cout, ho, wo), dtype=x.dtype, device=x.device)
+        tag = f"[{cin}x{h}x{w}->{cout}]"
+        geo = (stride, ho, wo, plan.oy0, plan.ox0, plan.kw)
+        with torch.cuda.device(x.device):
+            timing.timed("cl_conv_window_prep" + tag, lambda: _capi.call(
+                "cl_conv_window_prep", code, logits.data_ptr(), 1, gate_sequence.data_ptr(),
+                plan.slot_win.data_ptr(), probs.data_ptr(), coef.data_ptr(), cout, g, plan.kw,
+                stream))
+            timing.timed("cl_conv_window_forward" + tag, lambda: _capi.call(
+                "cl_conv_window_forward", code, x.data_ptr(), coef.data_ptr(),
+                plan.grp_ptr.data_ptr(), plan.chan_order.data_ptr(), y.data_ptr(), n, cin, h, w,
+                cout, *geo, stream))
+        ctx.save_for_backward(x, coef, probs, gate_sequence)
+        ctx.plan, ctx.geo, ctx.tag = plan, geo, tag
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        x, coef, probs, gate_sequence = ctx.saved_tensors
+        plan, geo, tag = ctx.plan, ctx.geo, ctx.tag
+        grad_y = grad_y.contiguous()
+        n, cin, h, w = x.shape
+        cout, g = probs.shape
+        code = _dl.dtype_code(x)
+        stream = _dl.stream_of(x)
+        grad_x = grad_w = None
+        with torch.cuda.device(x.device):
+            if ctx.needs_input_grad[0]:
+                grad_x = torch.empty_like(x)
+                timing.timed("cl_conv_window_backward_x" + tag, lambda: _capi.call(
+                    "cl_conv_window_backward_x", code, x.data_ptr(), grad_y.data_ptr(),
+                    coef.data_ptr(), plan.grp_ptr.data_ptr(), plan.chan_order.data_ptr(),
+                    grad_x.data_ptr(), n, cin, h, w, cout, *geo, stream))
+            if ctx.needs_input_grad[1]:
+                nq = ctypes.c_int64(0)
+                _capi.call("cl_conv_window_chunks", n, cin, plan.max_group, ctypes.byref(nq))
+                moments = torch.empty((nq.value, cout, plan.width), dtype=x.dtype, device=x.device)
+                grad_w = torch.empty_like(probs)
+                timing.timed("cl_conv_window_moments" + tag, lambda: _capi.call(
+                    "cl_conv_window_moments", code, x.data_ptr(), grad_y.data_ptr(),
+                    plan.grp_ptr.data_ptr(), plan.chan_order.data_ptr(), moments.data_ptr(),
+                    nq.value, plan.max_group, n, cin, h, w, cout, *geo, stream))
+                timing.timed("cl_conv_window_finalize" + tag, lambda: _capi.call(
+                    "cl_conv_window_finalize", code, moments.data_ptr(), nq.value,
+                    gate_sequence.data_ptr(), plan.slot_win.data_ptr(), probs.data_ptr(),
+                    grad_w.data_ptr(), cout, g, plan.kw, stream))
+        return grad_x, grad_w, None, None, None, None
+
+
 def _conv_name(entry: str, x: torch.Tensor, w: torch.Tensor) -> str:
     return f"{entry}[{x.shape[1]}x{x.shape[2]}x{x.shape[3]}->{w.shape[0]}]"
 
@@ -612,6 +687,10 @@ class ConvLayer(LogicLayer):
         assert x.ndim == 4, x.ndim
         x = x.contiguous()
         if self.weights.dtype == x.dtype and self.num_gates <= 64:
+            plan = self.window_plan(x)
+            if plan is not None:
+                return ConvLayerWindowFunction.apply(x, self.weights, self.gate_sequence, plan,
+                                                     self.stride, (self.h_out, self.w_out))
             return ConvLayerSoftmaxFunction.apply(
                 x, self.offsets_ch, self.offsets_h, self.offsets_w, self.weights,
                 self.gate_sequence, self.stride, self.padding, self.ks)
@@ -619,6 +698,15 @@ class ConvLayer(LogicLayer):
         return ConvLayerCudaFunction.apply(
             x, self.offsets_ch, self.offsets_h, self.offsets_w, w, self.gate_sequence,
             self.stride, self.padding, self.ks)
+
+    def window_plan(self, x: torch.Tensor):
+        """The window-path tables when this layer qualifies (each output channel reads one
+        input channel, taps within 3 x 3, at most 1024 output positions and an input plane of
+        at most 64 KiB), else None."""
+        c_in, h, w = self.in_shape
+        if self.h_out * self.w_out > 1024 or h * w * x.element_size() > 65536:
+            return None
+        return _cl.window_plan(self.offsets_ch, self.offsets_h, self.offsets_w, c_in)
 
     @torch.no_grad()
     def forward_cuda_eval(self, x):

@@ -213,6 +213,60 @@ int cl_conv_eval(int dtype, const void* x, const int32_t* offsets_ch, const int8
                  void* y, int64_t N, int64_t Cin, int64_t H, int64_t W, int64_t Cout,
                  int64_t num_gates, int64_t stride, int64_t pad, int64_t ks, void* stream);
 
+/* -------------------------------------------------------------------------------------------
+ * ConvLayer window path (no reference counterpart: the module's training path for layers in
+ * which every output channel reads a single input channel, ConvLayer's default num_chn = 1
+ * wiring, compactlogic/compactlogic.py:678-683).  Every slot's two taps then lie in one
+ * kw x kw window (kw <= 3) at (oy*stride + oy0, ox*stride + ox0) of that channel's plane, and
+ * the layer is the quadratic form y = K + sum_k alpha_k v_k + sum_{k<=l} beta_kl v_k v_l of
+ * the window values.  Derived tables (built by the module from the offsets):
+ *   slot_win   int32 [Cout, G]      window index of operand a | (of operand b) << 8
+ *   grp_ptr    int32 [Cin + 1]      output channels reading input channel ch are
+ *   chan_order int32 [Cout]         chan_order[grp_ptr[ch] .. grp_ptr[ch+1]-1]
+ *   coef       T [Cout, width]      [K, alpha_0.., beta_00, beta_01, .., beta_PP] per channel
+ *   moments    T [nq, Cout, width]  sum gy, sum gy v_k, sum gy v_k v_l per sample chunk
+ * ----------------------------------------------------------------------------------------- */
+
+/* Coefficients per channel for window width kw (2, 12 or 56 for kw = 1, 2, 3). */
+int cl_conv_window_coef_width(int64_t kw, int64_t* width);
+
+/* Softmax of w over the slots (softmax != 0; else w holds probabilities), written to probs
+ * when not NULL, and the coefficients of every channel summed in slot order.  G <= 64. */
+int cl_conv_window_prep(int dtype, const void* w, int softmax, const uint8_t* gate_seq,
+                        const int32_t* slot_win, void* probs, void* coef, int64_t Cout,
+                        int64_t num_gates, int64_t kw, void* stream);
+
+/* y[N, Cout, h_out, w_out] from x[N, Cin, H, W] and the coefficients. */
+int cl_conv_window_forward(int dtype, const void* x, const void* coef, const int32_t* grp_ptr,
+                           const int32_t* chan_order, void* y, int64_t N, int64_t Cin, int64_t H,
+                           int64_t W, int64_t Cout, int64_t stride, int64_t h_out, int64_t w_out,
+                           int64_t oy0, int64_t ox0, int64_t kw, void* stream);
+
+/* grad_x[N, Cin, H, W] (every element written).  h_out * w_out <= 1024 and the H x W plane
+ * must fit in 64 KiB. */
+int cl_conv_window_backward_x(int dtype, const void* x, const void* grad_y, const void* coef,
+                              const int32_t* grp_ptr, const int32_t* chan_order, void* grad_x,
+                              int64_t N, int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+                              int64_t stride, int64_t h_out, int64_t w_out, int64_t oy0,
+                              int64_t ox0, int64_t kw, void* stream);
+
+/* Number of sample chunks nq of the moments (max_group = largest group of output channels
+ * reading one input channel). */
+int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t* nq);
+
+/* Per-chunk moments of every channel (moments T [nq, Cout, width]). */
+int cl_conv_window_moments(int dtype, const void* x, const void* grad_y, const int32_t* grp_ptr,
+                           const int32_t* chan_order, void* moments, int64_t nq,
+                           int64_t max_group, int64_t N, int64_t Cin, int64_t H, int64_t W,
+                           int64_t Cout, int64_t stride, int64_t h_out, int64_t w_out,
+                           int64_t oy0, int64_t ox0, int64_t kw, void* stream);
+
+/* grad_w[Cout, G] from the moments summed over the chunks in order; with probs (not NULL)
+ * followed by the softmax backward (the gradient of the logits). */
+int cl_conv_window_finalize(int dtype, const void* moments, int64_t nq, const uint8_t* gate_seq,
+                            const int32_t* slot_win, const void* probs, void* grad_w,
+                            int64_t Cout, int64_t num_gates, int64_t kw, void* stream);
+
 /* Packed layer from resolved index tables (no reference counterpart; the packed form of a
  * frozen ConvLayer, whose output feature (c, oy, ox) in NCHW order reads input features
  * (ch * H + y) * W + x, compiler/extract.py:101-102):

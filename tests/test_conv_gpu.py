@@ -174,7 +174,7 @@ def test_conv_layer_module_autograd(device, num_chn):
                                         layer.gate_sequence, 2, 1, 3)
     y2.backward(gy)
     np.testing.assert_allclose(np_(w.grad), rgw, rtol=1e-5, atol=1e-6)
-    assert torch.equal(x2.grad, x.grad)
+    np.testing.assert_allclose(np_(x2.grad), rgx, **TOL[torch.float32])
 
 
 def test_conv_layer_gradcheck_fp64(device):
@@ -335,3 +335,100 @@ def test_cfg3_layers_vs_oracle(device):
         rgl = p * (rgw - (p * rgw).sum(1, keepdims=True))
         np.testing.assert_allclose(np_(layer.weights.grad), rgl, rtol=1e-5, atol=1e-6)
         h = y.detach()
+
+
+# ------------------------------------------------------------------------------ window path
+
+def _layer_vs_oracle(layer, x, gy, dtype):
+    """Run layer fwd + bwd on x with upstream gy; compare y, grad_x and the logits gradient
+    with the float64 oracle."""
+    xg = x.detach().clone().requires_grad_(True)
+    y = layer(xg)
+    y.backward(gy)
+    logits = np_(layer.weights).astype(np.float64)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    args = (np_(layer.offsets_ch), np_(layer.offsets_h), np_(layer.offsets_w))
+    xs = np_(x).astype(np.float64)
+    gs = np_(layer.gate_sequence)
+    ref = O.conv_forward(xs, *args, p, gs, layer.stride, layer.padding, layer.ks)
+    np.testing.assert_allclose(np_(y), ref, **TOL[dtype])
+    rgx, rgw = O.conv_backward(xs, *args, p, gs, np_(gy).astype(np.float64), layer.stride,
+                               layer.padding)
+    np.testing.assert_allclose(np_(xg.grad), rgx, **TOL[dtype])
+    rgl = p * (rgw - (p * rgw).sum(1, keepdims=True))
+    np.testing.assert_allclose(np_(layer.weights.grad), rgl, **TOL[dtype])
+    layer.weights.grad = None
+
+
+WINDOW_SHAPES = [
+    # c_in, h, w, c_out, G, ks, stride, pad, n
+    (9, 32, 32, 20, 16, 3, 2, 1, 5),     # cfg3 conv1 geometry
+    (16, 16, 16, 32, 16, 3, 2, 0, 4),    # cfg3 conv2 geometry
+    (3, 9, 7, 7, 4, 2, 1, 0, 3),         # 2 x 2 windows, non-square
+    (4, 11, 13, 9, 64, 3, 3, 1, 2),      # stride 3, 64 slots
+    (5, 6, 6, 5, 1, 3, 1, 2, 70),        # one slot, wide padding, several sample chunks
+    (2, 40, 24, 3, 8, 3, 1, 1, 2),       # 960 output positions in one block
+]
+
+
+@pytest.mark.parametrize("shape", WINDOW_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_window_path_matches_oracle(device, shape, dtype):
+    c_in, h, wd, c_out, g_n, ks, stride, pad, n = shape
+    torch.manual_seed(sum(shape))
+    layer = cl.ConvLayer((c_in, h, wd), padding=pad, c_out=c_out, ks=ks, stride=stride,
+                         num_chn=1, num_gates=g_n).to(device).to(dtype)
+    x = torch.rand((n, c_in, h, wd), device=device, dtype=dtype)
+    plan = layer.window_plan(x)
+    assert plan is not None and plan.kw == ks
+    y_shape = (n,) + layer.out_shape
+    gy = torch.empty(y_shape, device=device, dtype=dtype).uniform_(-1, 1) / n
+    _layer_vs_oracle(layer, x, gy, dtype)
+
+
+def test_window_path_self_pairs_and_rewiring(device):
+    """Slots whose two operands are the same tap (reachable through rewiring, which does not
+    re-resolve conflicts) give square terms; in-place offset changes rebuild the plan."""
+    torch.manual_seed(8)
+    layer = cl.ConvLayer((4, 10, 10), padding=1, c_out=8, ks=3, stride=2, num_chn=1,
+                         num_gates=16).to(device)
+    x = torch.rand((6, 4, 10, 10), device=device)
+    first = layer.window_plan(x)
+    with torch.no_grad():
+        layer.offsets_h[1, :, ::3] = layer.offsets_h[0, :, ::3]
+        layer.offsets_w[1, :, ::3] = layer.offsets_w[0, :, ::3]
+    second = layer.window_plan(x)
+    assert second is not None and second is not first
+    gy = torch.randn((6,) + layer.out_shape, device=device) / 6
+    _layer_vs_oracle(layer, x, gy, torch.float32)
+    layer.resample_connections(torch.arange(8, device=device), threshold_high=2.0, threshold_low=1.0)
+    assert layer.window_plan(x) is not second
+    _layer_vs_oracle(layer, x, gy, torch.float32)
+
+
+def test_window_path_not_taken_for_mixed_channels(device):
+    torch.manual_seed(1)
+    layer = cl.ConvLayer((4, 8, 8), padding=1, c_out=6, ks=3, stride=1, num_chn=0,
+                         num_gates=8).to(device)
+    assert layer.window_plan(torch.rand(1, 4, 8, 8, device=device)) is None
+
+
+def test_window_path_deterministic_and_input_only(device):
+    torch.manual_seed(3)
+    layer = cl.ConvLayer((8, 16, 16), padding=1, c_out=24, ks=3, stride=2, num_chn=1,
+                         num_gates=16).to(device)
+    x = torch.rand((40, 8, 16, 16), device=device, requires_grad=True)
+    grads = []
+    for _ in range(2):
+        x.grad = None
+        layer.weights.grad = None
+        layer(x).square().sum().backward()
+        grads.append((x.grad.clone(), layer.weights.grad.clone()))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    # logits frozen: only the input gradient is produced
+    layer.weights.requires_grad_(False)
+    x.grad = None
+    layer(x).square().sum().backward()
+    assert torch.equal(x.grad, grads[0][0])
+    layer.weights.requires_grad_(True)
