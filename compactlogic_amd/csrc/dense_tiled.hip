@@ -48,6 +48,20 @@ __device__ __forceinline__ V vld(const void* p) {
 #define CL_STREAM_STORES 0
 #endif
 
+// Lane accesses of the forward / backward tiled kernels are this many 16-byte vectors wide
+// (two for the backward: twice the bytes per gather for the same index records).
+#ifndef CL_FWD_VEC_MULT
+#define CL_FWD_VEC_MULT 1
+#endif
+#ifndef CL_BWD_VEC_MULT
+#define CL_BWD_VEC_MULT 2
+#endif
+
+// Inverse-index entries a backward lane group handles per step (loads kept in flight).
+#ifndef CL_BWD_UNROLL
+#define CL_BWD_UNROLL 1
+#endif
+
 // Store of an output row segment.  Regular (write-back) stores measure faster inside a
 // training step than non-temporal ones: the next kernel reads these rows right away and then
 // finds them in the Infinity Cache.
@@ -66,8 +80,10 @@ __device__ __forceinline__ T hsum(typename VT<T, N>::type v) {
         return v;
     } else if constexpr (N == 2) {
         return v[0] + v[1];
-    } else {
+    } else if constexpr (N == 4) {
         return (v[0] + v[1]) + (v[2] + v[3]);
+    } else {
+        return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
     }
 }
 
@@ -121,6 +137,21 @@ __device__ __forceinline__ bool map_tile(const TileMap& m, int64_t w, int64_t& c
         t = w % m.ntiles;
     }
     return c < m.nchunks;
+}
+
+#ifndef CL_TILE_ITERS
+#define CL_TILE_ITERS 1
+#endif
+
+// Virtual tile `it` of workgroup w: the same XCD (w % kXcds), consecutive along that XCD.
+__device__ __forceinline__ int64_t virtual_tile(int64_t w, int it) {
+    return ((w / kXcds) * CL_TILE_ITERS + it) * kXcds + w % kXcds;
+}
+
+// Grid of a kernel whose workgroups each take CL_TILE_ITERS virtual tiles.
+inline int64_t iter_grid(const TileMap& m) {
+    const int64_t v = tile_grid(m);
+    return kXcds * ceil_div(v, int64_t(kXcds) * CL_TILE_ITERS);
 }
 
 constexpr int kMaxSlotGroups = 8;  // G <= 128 = 8 groups of 16 slots
@@ -219,18 +250,14 @@ __global__ __launch_bounds__(256) void k_prep(const T* __restrict__ w, int softm
 // which the coefficients and both gathers of every neuron of the group are issued together.
 // Neurons with several runs continue through run_ab for the others.
 template <typename T, int VEC, int LPN, int NPG>
-__global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
-                                                   const T* __restrict__ kc,
-                                                   const int4* __restrict__ nab,
-                                                   const int2* __restrict__ run_ab,
-                                                   T* __restrict__ y, int64_t in_dim,
-                                                   int64_t out_dim, int64_t num_runs, int64_t B,
-                                                   TileMap tm) {
+__device__ __forceinline__ void fwd_tile(const T* __restrict__ x, const T* __restrict__ kc,
+                                         const int4* __restrict__ nab,
+                                         const int2* __restrict__ run_ab, T* __restrict__ y,
+                                         int64_t in_dim, int64_t out_dim, int64_t num_runs,
+                                         int64_t B, int64_t c, int64_t t) {
     using V = typename VT<T, VEC>::type;
     using V4 = typename VT<T, 4>::type;
     constexpr int GROUPS = 256 / LPN;
-    int64_t c, t;
-    if (!map_tile(tm, blockIdx.x, c, t)) return;
     const int64_t obase = (t * GROUPS + threadIdx.x / LPN) * NPG;
     const int64_t idx = c * (LPN * VEC) + int64_t(threadIdx.x % LPN) * VEC;
     if (obase >= out_dim || idx >= B) return;
@@ -272,6 +299,23 @@ __global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
             }
         }
         vst_stream<V>(y + o * B + idx, acc);
+    }
+}
+
+// Workgroup w handles CL_TILE_ITERS consecutive virtual tiles of its XCD (w % 8), so fewer,
+// longer-lived workgroups cover the grid.
+template <typename T, int VEC, int LPN, int NPG>
+__global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
+                                                   const T* __restrict__ kc,
+                                                   const int4* __restrict__ nab,
+                                                   const int2* __restrict__ run_ab,
+                                                   T* __restrict__ y, int64_t in_dim,
+                                                   int64_t out_dim, int64_t num_runs, int64_t B,
+                                                   TileMap tm) {
+    for (int it = 0; it < CL_TILE_ITERS; ++it) {
+        int64_t c, t;
+        if (map_tile(tm, virtual_tile(blockIdx.x, it), c, t))
+            fwd_tile<T, VEC, LPN, NPG>(x, kc, nab, run_ab, y, in_dim, out_dim, num_runs, B, c, t);
     }
 }
 
@@ -430,17 +474,16 @@ __global__ __launch_bounds__(256) void k_wgrad_full(const T* __restrict__ x, con
 // part[(r * nchunks + c) * 4 + j] receives the chunk-c moments of run r (WANT_GW) at the
 // run's operand-a entry.
 template <typename T, int VEC, int LPN, int NPG, bool WANT_GX, bool WANT_GW>
-__global__ __launch_bounds__(256) void k_bwd_tiled(
+__device__ __forceinline__ void bwd_tile(
     const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
     const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef, T* __restrict__ gx,
     T* __restrict__ part,
-    int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, TileMap tm) {
+    int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, const TileMap& tm, int64_t c,
+    int64_t t) {
     using V = typename VT<T, VEC>::type;
     using V2 = typename VT<T, 2>::type;
     using V4 = typename VT<T, 4>::type;
     constexpr int GROUPS = 256 / LPN;
-    int64_t c, t;
-    if (!map_tile(tm, blockIdx.x, c, t)) return;
     const int64_t slot0 = (t * GROUPS + threadIdx.x / LPN) * NPG;
     if (slot0 >= in_dim) return;  // uniform per lane group
     const int64_t idx = c * (LPN * VEC) + int64_t(threadIdx.x % LPN) * VEC;
@@ -473,67 +516,77 @@ __global__ __launch_bounds__(256) void k_bwd_tiled(
         xi[j] = V(T(0));
         if (WANT_GW && live[j] && col) xi[j] = vld<V>(x + row[j] * B + idx);
     }
-    int4 rec[NPG];
-    V2 kk[NPG];
+    // Entries are taken U at a time: the records of the next U entries are fetched while
+    // the gathers of the current U are in flight, so each lane group keeps 2U row segments
+    // in flight.  The accumulation order is still the entry order.
+    constexpr int U = CL_BWD_UNROLL;
+    int4 rec[NPG][U];
+    V2 kk[NPG][U];
 #pragma unroll
-    for (int j = 0; j < NPG; ++j) {
-        rec[j] = make_int4(0, 0, 0, 0);
-        kk[j] = V2(T(0));
-        if (deg[j] > 0) {
-            rec[j] = inv_rec[e0[j]];
-            kk[j] = vld<V2>(inv_coef + 2 * e0[j]);
-        }
-    }
-    for (int64_t k = 0; k < maxdeg; ++k) {
-        int4 cur[NPG];
-        V2 ck[NPG];
-        V vo[NPG], vg[NPG];
-        bool use[NPG];
+    for (int j = 0; j < NPG; ++j)
 #pragma unroll
-        for (int j = 0; j < NPG; ++j) {
-            cur[j] = rec[j];
-            ck[j] = kk[j];
-            if (k + 1 < deg[j]) {
-                rec[j] = inv_rec[e0[j] + k + 1];
-                kk[j] = vld<V2>(inv_coef + 2 * (e0[j] + k + 1));
-            }
-            use[j] = k < deg[j];
-            if (use[j] && (uint64_t(cur[j].x) >= uint64_t(out_dim) ||
-                           uint64_t(cur[j].y) >= uint64_t(in_dim) ||
-                           uint64_t(cur[j].z) >= uint64_t(num_runs))) {
-                bad[j] = true;
-                use[j] = false;
-            }
-            vo[j] = V(T(0));
-            vg[j] = V(T(0));
-            if (use[j] && col) {
-                vo[j] = vld<V>(x + int64_t(cur[j].y) * B + idx);
-                vg[j] = vld<V>(gy + int64_t(cur[j].x) * B + idx);
+        for (int u = 0; u < U; ++u) {
+            rec[j][u] = make_int4(0, 0, 0, 0);
+            kk[j][u] = V2(T(0));
+            if (u < deg[j]) {
+                rec[j][u] = inv_rec[e0[j] + u];
+                kk[j][u] = vld<V2>(inv_coef + 2 * (e0[j] + u));
             }
         }
+    for (int64_t k = 0; k < maxdeg; k += U) {
+        int4 cur[NPG][U];
+        V2 ck[NPG][U];
+        V vo[NPG][U], vg[NPG][U];
+        bool use[NPG][U];
 #pragma unroll
-        for (int j = 0; j < NPG; ++j) {
-            if (!use[j]) continue;
-            const int side = cur[j].w;
-            if (WANT_GX) acc[j] += (ck[j][0] + ck[j][1] * vo[j]) * vg[j];
-            if (WANT_GW && side == 0) {
-                const V ga = vg[j] * xi[j];
-                T s1 = hsum<T, VEC>(vg[j]), sa = hsum<T, VEC>(ga);
-                T sb = hsum<T, VEC>(vg[j] * vo[j]), sab = hsum<T, VEC>(ga * vo[j]);
-                s1 = group_sum<LPN>(s1);
-                sa = group_sum<LPN>(sa);
-                sb = group_sum<LPN>(sb);
-                sab = group_sum<LPN>(sab);
-                if (leader) {
-                    V4 mv;
-                    mv[0] = s1;
-                    mv[1] = sa;
-                    mv[2] = sb;
-                    mv[3] = sab;
-                    *reinterpret_cast<V4*>(part + (int64_t(cur[j].z) * tm.nchunks + c) * 4) = mv;
+        for (int j = 0; j < NPG; ++j)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                cur[j][u] = rec[j][u];
+                ck[j][u] = kk[j][u];
+                if (k + U + u < deg[j]) {
+                    rec[j][u] = inv_rec[e0[j] + k + U + u];
+                    kk[j][u] = vld<V2>(inv_coef + 2 * (e0[j] + k + U + u));
+                }
+                use[j][u] = k + u < deg[j];
+                if (use[j][u] && (uint64_t(cur[j][u].x) >= uint64_t(out_dim) ||
+                                  uint64_t(cur[j][u].y) >= uint64_t(in_dim) ||
+                                  uint64_t(cur[j][u].z) >= uint64_t(num_runs))) {
+                    bad[j] = true;
+                    use[j][u] = false;
+                }
+                vo[j][u] = V(T(0));
+                vg[j][u] = V(T(0));
+                if (use[j][u] && col) {
+                    vo[j][u] = vld<V>(x + int64_t(cur[j][u].y) * B + idx);
+                    vg[j][u] = vld<V>(gy + int64_t(cur[j][u].x) * B + idx);
                 }
             }
-        }
+#pragma unroll
+        for (int j = 0; j < NPG; ++j)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (!use[j][u]) continue;
+                const int side = cur[j][u].w;
+                if (WANT_GX) acc[j] += (ck[j][u][0] + ck[j][u][1] * vo[j][u]) * vg[j][u];
+                if (WANT_GW && side == 0) {
+                    const V ga = vg[j][u] * xi[j];
+                    T s1 = hsum<T, VEC>(vg[j][u]), sa = hsum<T, VEC>(ga);
+                    T sb = hsum<T, VEC>(vg[j][u] * vo[j][u]), sab = hsum<T, VEC>(ga * vo[j][u]);
+                    s1 = group_sum<LPN>(s1);
+                    sa = group_sum<LPN>(sa);
+                    sb = group_sum<LPN>(sb);
+                    sab = group_sum<LPN>(sab);
+                    if (leader) {
+                        V4 mv;
+                        mv[0] = s1;
+                        mv[1] = sa;
+                        mv[2] = sb;
+                        mv[3] = sab;
+                        *reinterpret_cast<V4*>(part + (int64_t(cur[j][u].z) * tm.nchunks + c) * 4) = mv;
+                    }
+                }
+            }
     }
     if (WANT_GX && col) {
 #pragma unroll
@@ -543,6 +596,21 @@ __global__ __launch_bounds__(256) void k_bwd_tiled(
             if (bad[j]) r = V(nan_of<T>());
             vst_stream<V>(gx + row[j] * B + idx, r);
         }
+    }
+}
+
+template <typename T, int VEC, int LPN, int NPG, bool WANT_GX, bool WANT_GW>
+__global__ __launch_bounds__(256) void k_bwd_tiled(
+    const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
+    const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef, T* __restrict__ gx,
+    T* __restrict__ part,
+    int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, TileMap tm) {
+    for (int it = 0; it < CL_TILE_ITERS; ++it) {
+        int64_t c, t;
+        if (map_tile(tm, virtual_tile(blockIdx.x, it), c, t))
+            bwd_tile<T, VEC, LPN, NPG, WANT_GX, WANT_GW>(x, gy, slot_rec, inv_rec, inv_coef, gx,
+                                                         part, in_dim, out_dim, num_runs, B, tm,
+                                                         c, t);
     }
 }
 
@@ -680,10 +748,12 @@ struct Tiling {
 
 // Narrowest lane group first that still leaves every XCD a chunk; bands of at most
 // `lpn_max` lanes keep a chunk's activation band within one XCD's L2.
+// Lane vector width: `mult` 16-byte vectors when the batch allows it, else one, else scalars.
 template <typename T>
-Tiling choose_tiling(int64_t B, int64_t rows, bool vec_ok, int lpn_max, int rows_per_group = 1) {
+Tiling choose_tiling(int64_t B, int64_t rows, int mult, int lpn_max, int rows_per_group = 1) {
     Tiling tl;
-    tl.vec = vec_ok ? wide_vec<T>() : 1;
+    constexpr int W = wide_vec<T>();
+    tl.vec = B % (W * mult) == 0 ? W * mult : (B % W == 0 ? W : 1);
     tl.lpn = lpn_max;
     while (tl.lpn > 4 && ceil_div(B, int64_t(tl.lpn) * tl.vec) < kXcds) tl.lpn >>= 1;
     tl.chunk = int64_t(tl.lpn) * tl.vec;
@@ -740,23 +810,23 @@ namespace {
 
 // Calls f(std::integral_constant<int, VEC>, std::integral_constant<int, LPN>) for the
 // tiling's vector width and lane-group size.
-template <typename T, typename F>
+template <typename T, int MULT, typename F>
 void with_tiling(const Tiling& tl, F&& f) {
     constexpr int W = wide_vec<T>();
     using I = std::integral_constant<int, 1>;
     using IW = std::integral_constant<int, W>;
+    using IM = std::integral_constant<int, W * MULT>;
     using L4 = std::integral_constant<int, 4>;
     using L8 = std::integral_constant<int, 8>;
     using L16 = std::integral_constant<int, 16>;
-    if (tl.vec == W) {
-        if (tl.lpn == 16) f(IW{}, L16{});
-        else if (tl.lpn == 8) f(IW{}, L8{});
-        else f(IW{}, L4{});
-    } else {
-        if (tl.lpn == 16) f(I{}, L16{});
-        else if (tl.lpn == 8) f(I{}, L8{});
-        else f(I{}, L4{});
-    }
+    auto by_lanes = [&](auto vc) {
+        if (tl.lpn == 16) f(vc, L16{});
+        else if (tl.lpn == 8) f(vc, L8{});
+        else f(vc, L4{});
+    };
+    if (MULT > 1 && tl.vec == W * MULT) by_lanes(IM{});
+    else if (tl.vec == W) by_lanes(IW{});
+    else by_lanes(I{});
 }
 
 }  // namespace
@@ -795,14 +865,14 @@ extern "C" int cl_dense_forward_tiled(int dtype, const void* x, const void* run_
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
         CL_ARG(!vec_ok<T>(batch) || all_aligned({x, y}), "x and y must be 16-byte aligned");
-        const Tiling tl = choose_tiling<T>(batch, out_dim, vec_ok<T>(batch), CL_FWD_LPN, CL_FWD_NPG);
-        const unsigned grid = unsigned(tile_grid(tl.map));
+        const Tiling tl = choose_tiling<T>(batch, out_dim, CL_FWD_VEC_MULT, CL_FWD_LPN, CL_FWD_NPG);
+        const unsigned grid = unsigned(iter_grid(tl.map));
         auto* xs = static_cast<const T*>(x);
         auto* kc = static_cast<const T*>(run_coef);
         auto* nb = reinterpret_cast<const int4*>(nab);
         auto* ab = reinterpret_cast<const int2*>(run_ab);
         auto* ys = static_cast<T*>(y);
-        with_tiling<T>(tl, [&](auto vc, auto lc) {
+        with_tiling<T, CL_FWD_VEC_MULT>(tl, [&](auto vc, auto lc) {
             k_fwd_tiled<T, decltype(vc)::value, decltype(lc)::value, CL_FWD_NPG>
                 <<<grid, 256, 0, s>>>(xs, kc, nb, ab, ys, in_dim, out_dim, num_runs, batch, tl.map);
         });
@@ -855,7 +925,7 @@ extern "C" int cl_dense_tiled_chunks(int dtype, int64_t batch, int64_t in_dim, i
     (void)out_dim;
     CL_DTYPE_SWITCH(dtype, {
         const int64_t b = std::max<int64_t>(batch, 1);
-        *nchunks = choose_tiling<scalar_t>(b, 1, vec_ok<scalar_t>(b), CL_BWD_LPN).map.nchunks;
+        *nchunks = choose_tiling<scalar_t>(b, 1, CL_BWD_VEC_MULT, CL_BWD_LPN).map.nchunks;
     });
     return CL_OK;
 }
@@ -904,27 +974,27 @@ extern "C" int cl_dense_backward_tiled(int dtype, const void* x, const void* gra
         auto* gxs = static_cast<T*>(grad_x);
         auto* mom = static_cast<T*>(moments);
         if (grad_x && in_dim > 0) {
-            const Tiling tl = choose_tiling<T>(batch, in_dim, v, CL_BWD_LPN, CL_BWD_NPG);
-            const unsigned grid = unsigned(tile_grid(tl.map));
+            const Tiling tl = choose_tiling<T>(batch, in_dim, CL_BWD_VEC_MULT, CL_BWD_LPN, CL_BWD_NPG);
+            const unsigned grid = unsigned(iter_grid(tl.map));
             if (moments) {
                 CL_ARG(nchunks == tl.map.nchunks, "moments buffer must use the backward chunk count");
-                with_tiling<T>(tl, [&](auto vc, auto lc) {
+                with_tiling<T, CL_BWD_VEC_MULT>(tl, [&](auto vc, auto lc) {
                     k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, CL_BWD_NPG, true, true>
                         <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gxs, mom,
                                               in_dim, out_dim, num_runs, batch, tl.map);
                 });
             } else {
-                with_tiling<T>(tl, [&](auto vc, auto lc) {
+                with_tiling<T, CL_BWD_VEC_MULT>(tl, [&](auto vc, auto lc) {
                     k_bwd_tiled<T, decltype(vc)::value, decltype(lc)::value, CL_BWD_NPG, true, false>
                         <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gxs, mom,
                                               in_dim, out_dim, num_runs, batch, tl.map);
                 });
             }
         } else if (moments && out_dim > 0) {
-            const Tiling tl = choose_tiling<T>(batch, out_dim, v, CL_BWD_LPN);
+            const Tiling tl = choose_tiling<T>(batch, out_dim, CL_BWD_VEC_MULT, CL_BWD_LPN);
             CL_ARG(nchunks == tl.map.nchunks, "moments buffer must use the backward chunk count");
             const unsigned grid = unsigned(tile_grid(tl.map));
-            with_tiling<T>(tl, [&](auto vc, auto lc) {
+            with_tiling<T, CL_BWD_VEC_MULT>(tl, [&](auto vc, auto lc) {
                 k_moments<T, decltype(vc)::value, decltype(lc)::value><<<grid, 256, 0, s>>>(
                     xs, gys, run_ptr, ab, mom, in_dim, out_dim, num_runs, batch, tl.map);
             });

@@ -11,8 +11,8 @@ row i lists the (run, operand side) uses of input i, encoded as 2 * run + side. 
 within a row are in ascending (side, run) order, so the result is deterministic.  Each entry
 also has a ready record (neuron, other input, run, side) so the kernel needs no second
 lookup, `inv_pos` maps a run side to its entry (where the per-step coefficients are written),
-and `row_order` lists the inputs by descending entry count so that rows processed side by
-side have equal work.  `nab` and `slot_rec` hold, per neuron and per processing slot, what a
+and `row_order` is the processing order of the inputs (breadth-first over the run graph for
+cache reuse, degree-sorted in blocks so that rows processed side by side have equal work).  `nab` and `slot_rec` hold, per neuron and per processing slot, what a
 kernel needs before its first gather (first run's pair and run range; input row and entry
 range), so each is one load away.
 """
@@ -20,6 +20,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 
@@ -36,13 +37,60 @@ class RunPlan:
     inv_entry: torch.Tensor  # int32 [2R]
     inv_rec: torch.Tensor    # int32 [2R, 4]  (neuron, other input, run, side) per entry
     inv_pos: torch.Tensor    # int32 [2R]     entry position of run side 2r + s
-    row_order: torch.Tensor  # int32 [in_dim] inputs by descending entry count (stable)
+    row_order: torch.Tensor  # int32 [in_dim] processing order of the inputs (locality_order)
     nab: torch.Tensor        # int32 [out_dim, 4] (a, b of the first run, run_ptr[o], run_ptr[o+1])
     slot_rec: torch.Tensor   # int32 [in_dim, 4]  (input, first entry, end entry, 0) in row_order
 
     @property
     def num_runs(self) -> int:
         return int(self.run_gl.numel())
+
+
+def locality_order(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor, in_dim: int,
+                   block: int = 256) -> torch.Tensor:
+    """Processing order of the inputs for the input-gradient pass: breadth-first over the
+    graph whose edges are the runs (a, b), then sorted by descending degree inside blocks of
+    `block` consecutive inputs.  Both uses of a run (its rows a and b) and of an input (as a
+    row and as the other operand of its neighbours' entries) then fall close together in
+    time, so the second read of a row segment hits the L2; the block sort keeps the inputs
+    processed side by side of equal work.  Inputs of degree 0 come last.  Deterministic:
+    searches start from the highest-degree unvisited input (lowest index on ties)."""
+    dev = ra.device
+    a = ra.cpu().numpy().astype(np.int64)
+    b = rb.cpu().numpy().astype(np.int64)
+    deg = degree.cpu().numpy().astype(np.int64)
+    src = np.concatenate((a, b))
+    dst = np.concatenate((b, a))
+    order = np.argsort(src, kind="stable")
+    nbr = dst[order]
+    ptr = np.zeros(in_dim + 1, dtype=np.int64)
+    np.cumsum(np.bincount(src, minlength=in_dim), out=ptr[1:])
+    seen = deg == 0
+    out = []
+    for start in np.argsort(-deg, kind="stable"):
+        if seen[start]:
+            continue
+        seen[start] = True
+        frontier = np.array([start], dtype=np.int64)
+        while frontier.size:
+            out.append(frontier)
+            cnt = ptr[frontier + 1] - ptr[frontier]
+            tot = int(cnt.sum())
+            if tot == 0:
+                break
+            first = np.repeat(ptr[frontier], cnt)
+            offs = np.arange(tot) - np.repeat(np.cumsum(cnt) - cnt, cnt)
+            cand = nbr[first + offs]
+            cand = cand[~seen[cand]]
+            _, keep = np.unique(cand, return_index=True)
+            frontier = cand[np.sort(keep)]
+            seen[frontier] = True
+    out.append(np.nonzero(deg == 0)[0])
+    visit = np.concatenate(out) if out else np.zeros(0, dtype=np.int64)
+    for s0 in range(0, visit.size, block):
+        seg = visit[s0:s0 + block]
+        visit[s0:s0 + block] = seg[np.argsort(-deg[seg], kind="stable")]
+    return torch.as_tensor(visit, dtype=torch.int64, device=dev)
 
 
 def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
@@ -95,7 +143,7 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
     inv_rec = torch.stack((run_y[ent_run], ent_other, ent_run, ent_side), dim=1)
     inv_pos = torch.empty_like(inv_entry)
     inv_pos[inv_entry] = torch.arange(inv_entry.numel(), dtype=torch.int64, device=dev)
-    row_order = torch.sort(inv_counts, descending=True, stable=True).indices
+    row_order = locality_order(ra, rb, inv_counts, in_dim)
     first = run_ptr[:-1].clamp(max=max(r - 1, 0))
     has = run_ptr[1:] > run_ptr[:-1]
     nab = torch.stack((torch.where(has, ra[first] if r else first, 0),

@@ -264,3 +264,26 @@ def test_conv_inverse_index_cache_follows_tensors():
             side, slot = e & 1, e >> 1
             c, gg = divmod(slot, 5)
             assert int(och2[side, c, gg]) * 4 + (int(oh[side, c, gg]) % 2) * 2 + int(ow[side, c, gg]) % 2 == k
+
+
+def test_run_plan_processing_order():
+    """row_order is a permutation of the inputs, degree-sorted inside blocks of 256, with
+    every input of degree 0 last; slot_rec follows it."""
+    from compactlogic_amd.plan import build_run_plan
+    g = torch.Generator().manual_seed(11)
+    in_dim, out_dim = 3000, 1600
+    pair = torch.randint(0, in_dim, (2, out_dim, 1), generator=g).expand(2, out_dim, 16)
+    plan = build_run_plan(pair.contiguous(), in_dim)
+    order = plan.row_order.long()
+    assert sorted(order.tolist()) == list(range(in_dim))
+    deg = (plan.inv_ptr[1:] - plan.inv_ptr[:-1]).long()
+    d = deg[order]
+    for s0 in range(0, in_dim, 256):
+        seg = d[s0:s0 + 256]
+        assert bool((seg[:-1] >= seg[1:]).all())
+    nz = int((deg > 0).sum())
+    assert bool((d[nz:] == 0).all())
+    rec = plan.slot_rec.long()
+    assert torch.equal(rec[:, 0], order)
+    assert torch.equal(rec[:, 1], plan.inv_ptr.long()[order])
+    assert torch.equal(rec[:, 2], plan.inv_ptr.long()[order + 1])
