@@ -321,16 +321,18 @@ __global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
 
 // ------------------------------------------------------------------------------------------
 // Softmax + run coefficients of neuron o held by a 16-lane row (lane l: slots l, l+16, ...).
-template <typename T>
+template <typename T, int NG = kMaxSlotGroups>
 struct SlotProbs {
-    T p[kMaxSlotGroups];
+    T p[NG];
 };
 
-template <typename T>
-__device__ __forceinline__ SlotProbs<T> slot_probs(const T* __restrict__ w, int softmax, int64_t o,
-                                                   int l, int G) {
+// NG: slot groups of 16 held per lane (a compile-time bound on (G + 15) / 16).
+template <typename T, int NG = kMaxSlotGroups>
+__device__ __forceinline__ SlotProbs<T, NG> slot_probs(const T* __restrict__ w, int softmax,
+                                                       int64_t o, int l, int G) {
+    constexpr int kMaxSlotGroups = NG;
     const int ng = (G + 15) >> 4;
-    SlotProbs<T> sp;
+    SlotProbs<T, NG> sp;
 #pragma unroll
     for (int m = 0; m < kMaxSlotGroups; ++m) {
         const int g = l + 16 * m;
@@ -357,10 +359,11 @@ __device__ __forceinline__ SlotProbs<T> slot_probs(const T* __restrict__ w, int 
 }
 
 // K of the run [g0, g1) from the row's probabilities; every lane of the row gets the result.
-template <typename T>
-__device__ __forceinline__ Coef4<T> row_run_coef(const SlotProbs<T>& sp,
+template <typename T, int NG = kMaxSlotGroups>
+__device__ __forceinline__ Coef4<T> row_run_coef(const SlotProbs<T, NG>& sp,
                                                  const uint8_t* __restrict__ grow, int l, int g0,
                                                  int g1, int G) {
+    constexpr int kMaxSlotGroups = NG;
     const int ng = (G + 15) >> 4;
     T k0 = 0, k1 = 0, k2 = 0, k3 = 0;
 #pragma unroll

@@ -135,10 +135,10 @@ class LogicLayerRunsFunction(torch.autograd.Function):
         dev = x.device
         code = _dl.dtype_code(x)
         probs = torch.empty_like(w) if softmax else None
-        coef = torch.empty((plan.num_runs, 4), dtype=x.dtype, device=dev)
         inv_coef = torch.empty((2 * plan.num_runs, 2), dtype=x.dtype, device=dev)
         y = torch.empty((plan.out_dim, batch), dtype=x.dtype, device=dev)
         stream = _dl.stream_of(x)
+        coef = torch.empty((plan.num_runs, 4), dtype=x.dtype, device=dev)
         with torch.cuda.device(dev):
             timing.timed(f"cl_dense_prep[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
                 "cl_dense_prep", code, w.data_ptr(), int(softmax), gate_sequence.data_ptr(),

@@ -47,7 +47,7 @@ class RunPlan:
 
 
 def locality_order(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor, in_dim: int,
-                   block: int = 256) -> torch.Tensor:
+                   block: int = 1024) -> torch.Tensor:
     """Processing order of the inputs for the input-gradient pass: breadth-first over the
     graph whose edges are the runs (a, b), then sorted by descending degree inside blocks of
     `block` consecutive inputs.  Both uses of a run (its rows a and b) and of an input (as a

@@ -267,7 +267,7 @@ def test_conv_inverse_index_cache_follows_tensors():
 
 
 def test_run_plan_processing_order():
-    """row_order is a permutation of the inputs, degree-sorted inside blocks of 256, with
+    """row_order is a permutation of the inputs, degree-sorted inside blocks of 1024, with
     every input of degree 0 last; slot_rec follows it."""
     from compactlogic_amd.plan import build_run_plan
     g = torch.Generator().manual_seed(11)
@@ -278,8 +278,8 @@ def test_run_plan_processing_order():
     assert sorted(order.tolist()) == list(range(in_dim))
     deg = (plan.inv_ptr[1:] - plan.inv_ptr[:-1]).long()
     d = deg[order]
-    for s0 in range(0, in_dim, 256):
-        seg = d[s0:s0 + 256]
+    for s0 in range(0, in_dim, 1024):
+        seg = d[s0:s0 + 1024]
         assert bool((seg[:-1] >= seg[1:]).all())
     nz = int((deg > 0).sum())
     assert bool((d[nz:] == 0).all())
