@@ -56,7 +56,7 @@ SIGNATURES: dict[str, list] = {
     "cl_conv_window_prep": [_int, _p, _int, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_conv_window_forward": [_int, _p, _p, _p, _p, _p] + [_i64] * 11 + [_p],
     "cl_conv_window_backward_x": [_int, _p, _p, _p, _p, _p, _p] + [_i64] * 11 + [_p],
-    "cl_conv_window_chunks": [_i64, _i64, _i64, ctypes.POINTER(_i64)],
+    "cl_conv_window_chunks": [_i64, _i64, _i64, _i64, ctypes.POINTER(_i64)],
     "cl_conv_window_moments": [_int, _p, _p, _p, _p, _p, _i64, _i64] + [_i64] * 11 + [_p],
     "cl_conv_window_finalize": [_int, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_group_sum_forward": [_int, _p, _i64, _i64, _i64, _i64, _i64, _f64, _p, _p, _i64, _p],

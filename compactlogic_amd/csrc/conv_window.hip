@@ -129,6 +129,7 @@ __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const 
     load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(d.H) * d.W, d.H, d.W,
                        oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
     T* yn = y + n * d.Cout * hw + pos;
+#pragma unroll 2
     for (int i = c0; i < c1; ++i) {
         const int c = chan_order[i];
         const T* cf = coef + int64_t(c) * CW;
@@ -204,8 +205,10 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
 }
 
 // ------------------------------------------------------------------------------------------
-// Moments: block (ch, sub-block sb of CB channels, sample chunk q), BS threads over the
-// output positions (several passes when Ho * Wo > BS).  part[q, c, j] for j < CW.
+// Moments: block (ch, sub-block sb of CB channels, sample chunk q) of 256 threads; the
+// threads stride over the chunk's (sample, position) elements.  part[q, c, j] for j < CW.
+// The closing reduction adds quads with DPP, then the 16 quad sums of each of the 4 waves in
+// a fixed order through LDS.
 template <typename T, int KW, int CB>
 __global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
                                                      const T* __restrict__ gy,
@@ -214,7 +217,8 @@ __global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
                                                      T* __restrict__ part, int nsub, int nq,
                                                      WinDims d) {
     constexpr int P = Win<KW>::P, NM = 1 + P + Win<KW>::NP, CW = Win<KW>::CW;
-    __shared__ T red[4][CB * NM];
+    constexpr int BS = 256;
+    __shared__ T red[BS / 4][CB * NM];
     const int q = blockIdx.y;
     const int64_t ch = blockIdx.x / nsub;
     const int sb = blockIdx.x % nsub;
@@ -225,50 +229,65 @@ __global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
     for (int j = 0; j < CB; ++j) cs[j] = g0 + j < g1 ? chan_order[g0 + j] : -1;
     const int hw = d.Ho * d.Wo, HW = d.H * d.W;
     const int64_t n0 = q * d.N / nq, n1 = (q + 1) * d.N / nq;
+    const int64_t cnt = (n1 - n0) * hw;
     T S[CB][NM];
 #pragma unroll
     for (int j = 0; j < CB; ++j)
 #pragma unroll
         for (int m = 0; m < NM; ++m) S[j][m] = 0;
-    for (int p0 = 0; p0 < hw; p0 += blockDim.x) {
-        const int pos = p0 + threadIdx.x;
-        const bool active = pos < hw;
-        const int oy = active ? pos / d.Wo : 0, ox = active ? pos - oy * d.Wo : 0;
-        const int by = oy * d.stride + d.oy0, bx = ox * d.stride + d.ox0;
-        for (int64_t n = n0; n < n1; ++n) {
-            T v[P];
-            load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(HW), d.H, d.W, by, bx, active);
-            const T* gyn = gy + n * d.Cout * hw + pos;
+    // element e = (n - n0) * hw + oy * Wo + ox, advanced by BS per step without a division
+    const int dn = BS / hw, dp = BS % hw;
+    const int dy = dp / d.Wo, dx = dp % d.Wo;
+    int64_t n = n0 + threadIdx.x / hw;
+    const int pos0 = threadIdx.x % hw;
+    int oy = pos0 / d.Wo, ox = pos0 % d.Wo;
+    for (int64_t e = threadIdx.x; e < cnt; e += BS) {
+        const int pos = oy * d.Wo + ox;
+        T v[P];
+        load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(HW), d.H, d.W,
+                           oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
+        const T* gyn = gy + n * d.Cout * hw + pos;
+        n += dn;
+        oy += dy;
+        ox += dx;
+        if (ox >= d.Wo) {
+            ox -= d.Wo;
+            ++oy;
+        }
+        if (oy >= d.Ho) {
+            oy -= d.Ho;
+            ++n;
+        }
 #pragma unroll
-            for (int j = 0; j < CB; ++j) {
-                const T g = (active && cs[j] >= 0) ? gyn[int64_t(cs[j]) * hw] : T(0);
-                S[j][0] += g;
+        for (int j = 0; j < CB; ++j) {
+            const T g = cs[j] >= 0 ? gyn[int64_t(cs[j]) * hw] : T(0);
+            S[j][0] += g;
 #pragma unroll
-                for (int k = 0; k < P; ++k) {
-                    const T gv = g * v[k];
-                    S[j][1 + k] += gv;
+            for (int k = 0; k < P; ++k) {
+                const T gv = g * v[k];
+                S[j][1 + k] += gv;
 #pragma unroll
-                    for (int l = k; l < P; ++l) S[j][beta_at(P, k, l)] = fma(gv, v[l], S[j][beta_at(P, k, l)]);
-                }
+                for (int l = k; l < P; ++l) S[j][beta_at(P, k, l)] = fma(gv, v[l], S[j][beta_at(P, k, l)]);
             }
         }
     }
-    const int wv = threadIdx.x >> 6;
+    const bool quad_lead = (threadIdx.x & 3) == 0;
 #pragma unroll
     for (int j = 0; j < CB; ++j)
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            const T t = wave_total(S[j][m]);
-            if ((threadIdx.x & 63) == 0) red[wv][j * NM + m] = t;
+            T t = S[j][m];
+            t += dpp_move<0xB1>(t);  // quad_perm [1,0,3,2]
+            t += dpp_move<0x4E>(t);  // quad_perm [2,3,0,1]
+            if (quad_lead) red[threadIdx.x >> 2][j * NM + m] = t;
         }
     __syncthreads();
-    const int nw = int(blockDim.x) >> 6;
-    for (int i = threadIdx.x; i < CB * CW; i += blockDim.x) {
+    for (int i = threadIdx.x; i < CB * CW; i += BS) {
         const int j = i / CW, m = i % CW;
         if (cs[j] < 0) continue;
         T t = 0;
         if (m < NM)
-            for (int w2 = 0; w2 < nw; ++w2) t += red[w2][j * NM + m];
+            for (int r = 0; r < BS / 4; ++r) t += red[r][j * NM + m];
         part[(int64_t(q) * d.Cout + cs[j]) * CW + m] = t;
     }
 }
@@ -339,7 +358,10 @@ int block_for(int64_t hw, int cap) {
     return int(std::min<int64_t>(b, cap));
 }
 
-constexpr int kWinCB = 2;  // output channels per moments block
+#ifndef CL_WIN_CB
+#define CL_WIN_CB 2
+#endif
+constexpr int kWinCB = CL_WIN_CB;  // output channels per moments block
 
 }  // namespace
 }  // namespace cl
@@ -436,14 +458,16 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
     return check_launch("cl_conv_window_backward_x");
 }
 
-extern "C" int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t* nq) {
+extern "C" int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t hw,
+                                     int64_t* nq) {
     clear_error();
-    CL_ARG(nq && N >= 0 && Cin >= 1 && max_group >= 0, "bad argument");
-    // about 1024 blocks, but at least 32 samples per chunk so that the closing reduction of
-    // a block stays small against its accumulation loop
+    CL_ARG(nq && N >= 0 && Cin >= 1 && max_group >= 0 && hw >= 1, "bad argument");
+    // about 1536 blocks (two rounds of resident blocks), but at least 8 (sample, position)
+    // elements per thread so that the closing reduction stays small against the loop
     const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
-    const int64_t want = ceil_div(1024, Cin * nsub);
-    *nq = std::max<int64_t>(1, std::min<int64_t>(want, N / 32));
+    const int64_t want = ceil_div(1536, Cin * nsub);
+    const int64_t most = N * hw / (256 * 8);
+    *nq = std::max<int64_t>(1, std::min<int64_t>(std::min(want, most), std::max<int64_t>(N, 1)));
     return CL_OK;
 }
 
@@ -463,7 +487,7 @@ extern "C" int cl_conv_window_moments(int dtype, const void* x, const void* grad
     const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
     const int64_t bx = Cin * nsub;
     CL_ARG(bx < (int64_t(1) << 31), "conv layer too large for one launch");
-    const int bs = block_for(h_out * w_out, 256);
+    const int bs = 256;
     const dim3 grid(unsigned(bx), unsigned(nq), 1);
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {

@@ -631,7 +631,8 @@ class ConvLayerWindowFunction(torch.autograd.Function):
                     grad_x.data_ptr(), n, cin, h, w, cout, *geo, stream))
             if ctx.needs_input_grad[1]:
                 nq = ctypes.c_int64(0)
-                _capi.call("cl_conv_window_chunks", n, cin, plan.max_group, ctypes.byref(nq))
+                _capi.call("cl_conv_window_chunks", n, cin, plan.max_group, geo[1] * geo[2],
+                           ctypes.byref(nq))
                 moments = torch.empty((nq.value, cout, plan.width), dtype=x.dtype, device=x.device)
                 grad_w = torch.empty_like(probs)
                 timing.timed("cl_conv_window_moments" + tag, lambda: _capi.call(

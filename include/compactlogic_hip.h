@@ -251,8 +251,8 @@ int cl_conv_window_backward_x(int dtype, const void* x, const void* grad_y, cons
                               int64_t ox0, int64_t kw, void* stream);
 
 /* Number of sample chunks nq of the moments (max_group = largest group of output channels
- * reading one input channel). */
-int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t* nq);
+ * reading one input channel, hw = h_out * w_out). */
+int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t hw, int64_t* nq);
 
 /* Per-chunk moments of every channel (moments T [nq, Cout, width]). */
 int cl_conv_window_moments(int dtype, const void* x, const void* grad_y, const int32_t* grp_ptr,
