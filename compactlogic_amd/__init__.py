@@ -10,10 +10,13 @@ from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction,
                      ConvLayerWindowFunction, GroupSum, GroupSumFunction, LogicLayer,
                      LogicLayerCudaFunction, LogicLayerRunsFunction, PackBitsTensor)
 from .plan import RunPlan, build_run_plan
+from .schedules import (EntropyRowResampler, FixedSequentialEntropyFreezer,
+                        SequentialEntropyFreezer)
 
 __all__ = [
     "LogicLayer", "GroupSum", "LogicLayerCudaFunction", "LogicLayerRunsFunction",
     "GroupSumFunction", "PackBitsTensor", "RunPlan", "build_run_plan", "difflogic_hip",
     "ConvLayer", "ConvLayerCudaFunction", "ConvLayerSoftmaxFunction", "ConvLayerWindowFunction",
-    "convlogic_hip",
+    "convlogic_hip", "SequentialEntropyFreezer", "FixedSequentialEntropyFreezer",
+    "EntropyRowResampler",
 ]
