@@ -315,6 +315,40 @@ def bench_packed_net(model, in_features: int, log2n: int, passes: int, k: int, t
     return dict(n=n, seconds=dt, samples_s=n / dt, checksum=checksum, kernels=kernels)
 
 
+def bench_packed_fused(model, in_features: int, log2n: int, passes: int, checksum: int, torch):
+    """The same network through PackedNetwork (all layers and the popcount GroupSum in one
+    launch, activations in LDS).  Compulsory HBM bytes of the fused pass: the packed input and
+    the int32 counts."""
+    import compactlogic_amd as cl
+    from compactlogic_amd import configs
+    n = 1 << log2n
+    xw = configs.packed_input_words(in_features, n // 64, device=torch.device("cuda:0"))
+    net = cl.PackedNetwork(model)
+    x = cl.PackBitsTensor.from_packed(xw)
+    counts = net(x)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(passes):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        counts = net(x)
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) * 1e-3)
+    dt = min(times)
+    same = int(counts.to(torch.int64).sum().item()) == checksum
+    fused_bytes = in_features // 8 + 4 * model[-1].k
+    del xw, counts
+    torch.cuda.empty_cache()
+    return {"workload": "the same network and inputs through PackedNetwork: one launch, "
+                        "32-sample columns held in LDS through all layers",
+            "value": round(n / dt / 1e9, 4), "unit": "Gsamples/s", "ms_per_pass": round(dt * 1e3, 3),
+            "counts_match_layerwise": same,
+            "fused_compulsory_bytes_per_sample": fused_bytes,
+            "hbm_frac_of_fused_bytes": round(fused_bytes * n / dt / 1e9 / HBM_PEAK_GBS, 4),
+            "speedup_vs_layerwise": None}
+
+
 def packed_json(pk: dict, workload: str, bytes_per_sample: int) -> dict:
     return {
         "workload": workload,
@@ -438,11 +472,16 @@ def main():
         configs.freeze_uniform_gates(model)
         pk = bench_packed_net(model, c2.in_dim, args.packed_log2_samples, args.packed_passes,
                               c2.k, torch)
+        fused = bench_packed_fused(model, c2.in_dim, args.packed_log2_samples,
+                                   args.packed_passes, pk["checksum"], torch)
         del model
         packed = packed_json(pk, f"cfg4: cfg2 network frozen to argmax gates, "
                                  f"2^{args.packed_log2_samples} samples bit-packed 64 per word, "
                                  "6 bitwise layers + popcount GroupSum", CFG4_BYTES_PER_SAMPLE)
-        log(f"packed cfg4: {packed['value']} Gsamples/s")
+        fused["speedup_vs_layerwise"] = round(fused["value"] / packed["value"], 2)
+        packed["fused"] = fused
+        log(f"packed cfg4: {packed['value']} Gsamples/s layer by layer, "
+            f"{fused['value']} Gsamples/s fused")
         if not args.no_cpu_baseline:
             log("cpu baseline (cfg4)")
             packed["cpu_baseline"] = cpu_baseline_packed(torch, "cfg4")

@@ -9,6 +9,7 @@ from . import convlogic_hip, difflogic_hip
 from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction,
                      ConvLayerWindowFunction, GroupSum, GroupSumFunction, LogicLayer,
                      LogicLayerCudaFunction, LogicLayerRunsFunction, PackBitsTensor)
+from .packed_net import PackedNetwork
 from .plan import RunPlan, build_run_plan
 from .schedules import (EntropyRowResampler, FixedSequentialEntropyFreezer,
                         SequentialEntropyFreezer)
@@ -18,5 +19,5 @@ __all__ = [
     "GroupSumFunction", "PackBitsTensor", "RunPlan", "build_run_plan", "difflogic_hip",
     "ConvLayer", "ConvLayerCudaFunction", "ConvLayerSoftmaxFunction", "ConvLayerWindowFunction",
     "convlogic_hip", "SequentialEntropyFreezer", "FixedSequentialEntropyFreezer",
-    "EntropyRowResampler",
+    "EntropyRowResampler", "PackedNetwork",
 ]

@@ -66,6 +66,8 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_eval_packed": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "cl_group_bit_sum": [_p, _i64, _i64, _i64, _i64, _p, _p],
     "cl_fill_splitmix64": [_p, _i64, _u64, _p],
+    "cl_packed_network_limits": [ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
+    "cl_packed_network": [_p, _i64, _i64, _p, ctypes.POINTER(_i64), _i64, _i64, _p, _p],
 }
 
 _lib = None

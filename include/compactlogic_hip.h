@@ -332,6 +332,24 @@ int cl_group_bit_sum(const void* packed, int64_t rows, int64_t row_bytes, int64_
  * out[i] = splitmix64(base + i) for i < count. */
 int cl_fill_splitmix64(uint64_t* out, int64_t count, uint64_t base, void* stream);
 
+/* -------------------------------------------------------------------------------------------
+ * Whole-network packed inference (no reference counterpart: the cross-module fusion of the
+ * layer-by-layer packed path, for callers that evaluate a frozen dense network end to end).
+ * One launch evaluates num_layers packed layers and the popcount GroupSum for every 32-sample
+ * column of x (rows[0] packed rows of row_bytes bytes, bit j = sample j), keeping the
+ * activations in LDS.  tables: for layer l, rows[l+1] entries (uint64) of
+ * 4*a | (4*b) << 20 | opcode << 40 with a, b < rows[l], concatenated over the layers.
+ * counts: int32 [nsamples, k], k dividing rows[num_layers] (else CL_ERR_VALUE).
+ * rows_host is a host array of num_layers + 1 widths, each at most the limit below.
+ * ----------------------------------------------------------------------------------------- */
+
+/* Largest layer count and layer width the fused pass accepts. */
+int cl_packed_network_limits(int64_t* max_layers, int64_t* max_rows);
+
+int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamples, const uint64_t* tables,
+                      const int64_t* rows_host, int64_t num_layers, int64_t k, int32_t* counts,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif
