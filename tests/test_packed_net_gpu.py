@@ -41,6 +41,7 @@ def oracle_counts(model, words_np, n):
     ([(17, 33), (33, 40)], 5, 2, 96),
     ([(64, 2000), (2000, 1000)], 8, 16, 4096),
     ([(12, 20)] + [(20, 20)] * 14 + [(20, 30)], 3, 8, 130),
+    ([(64, 17000), (17000, 8500)], 10, 4, 200),     # wider than the register-table variant
 ])
 def test_packed_network_matches_oracle_and_layerwise(device, dims, k, g_n, n):
     model = frozen_net(dims, k, g_n, sum(d[1] for d in dims), device)
