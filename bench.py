@@ -149,8 +149,12 @@ def train_kernel_bytes(model, batch: int) -> dict:
             tag = f"[{m.in_dim}->{m.out_dim}]"
             xb, yb = 4 * batch * m.in_dim, 4 * batch * m.out_dim
             out.update({"cl_dense_forward_tiled" + tag: xb + yb,
+                        "cl_dense_forward_fused" + tag: xb + yb,
                         "cl_dense_backward_tiled" + tag: 2 * xb + yb,
                         "cl_dense_weight_grad" + tag: xb + yb})
+            # layout change of a [batch, in_dim] input and of its gradient: read + write
+            out[f"cl_transpose[{batch}x{m.in_dim}]"] = 2 * xb
+            out[f"cl_transpose[{m.in_dim}x{batch}]"] = 2 * xb
     return out
 
 

@@ -40,6 +40,11 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_eval": [_int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "cl_dense_prep": [_int, _p, _int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_dense_forward_tiled": [_int, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "cl_dense_backward_part": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p,
+                               _i64, _i64, _i64, _i64, _i64, _p],
+    "cl_transpose": [_int, _p, _p, _i64, _i64, _p],
+    "cl_dense_forward_fused": [_int, _p, _p, _int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                               _i64, _i64, _p],
     "cl_dense_weight_grad": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                              _p],
     "cl_dense_tiled_chunks": [_int, _i64, _i64, _i64, ctypes.POINTER(_i64)],

@@ -56,6 +56,9 @@ __device__ __forceinline__ V vld(const void* p) {
 #ifndef CL_BWD_VEC_MULT
 #define CL_BWD_VEC_MULT 2
 #endif
+#ifndef CL_FUSED_VEC_MULT
+#define CL_FUSED_VEC_MULT 1
+#endif
 
 // Inverse-index entries a backward lane group handles per step (loads kept in flight).
 #ifndef CL_BWD_UNROLL
@@ -127,6 +130,10 @@ __host__ __device__ __forceinline__ int64_t tile_grid(const TileMap& m) {
     return m.nchunks * m.ntiles;
 }
 
+#ifndef CL_TILE_ROTATE
+#define CL_TILE_ROTATE 0
+#endif
+
 __device__ __forceinline__ bool map_tile(const TileMap& m, int64_t w, int64_t& c, int64_t& t) {
     if (m.nchunks >= kXcds) {
         const int64_t x = w % kXcds, j = w / kXcds;
@@ -136,6 +143,12 @@ __device__ __forceinline__ bool map_tile(const TileMap& m, int64_t w, int64_t& c
         c = w / m.ntiles;
         t = w % m.ntiles;
     }
+#if CL_TILE_ROTATE
+    // Chunk c starts its tile sweep at a different row band, so the XCDs working on different
+    // chunks at the same moment read different rows.
+    t += (c % kXcds) * m.ntiles / kXcds;
+    if (t >= m.ntiles) t -= m.ntiles;
+#endif
     return c < m.nchunks;
 }
 
@@ -316,6 +329,187 @@ __global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
         int64_t c, t;
         if (map_tile(tm, virtual_tile(blockIdx.x, it), c, t))
             fwd_tile<T, VEC, LPN, NPG>(x, kc, nab, run_ab, y, in_dim, out_dim, num_runs, B, c, t);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Butterfly reductions over each group of LPN consecutive lanes (LPN in {4, 8, 16}) that
+// leave the result in every lane of the group: quad permutes, then the mirror inside each
+// half row (lane i <-> 7 - i), then the mirror inside the row (i <-> 15 - i).  Each step adds
+// two partial sums of the same set of lanes, so all lanes end with bitwise the same value.
+template <int LPN, typename T>
+__device__ __forceinline__ T group_allsum(T v) {
+    v += dpp_move<0xB1>(v);                            // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);                            // quad_perm [2,3,0,1]
+    if constexpr (LPN >= 8) v += dpp_move<0x141>(v);   // row_half_mirror
+    if constexpr (LPN >= 16) v += dpp_move<0x140>(v);  // row_mirror
+    return v;
+}
+
+template <int LPN, typename T>
+__device__ __forceinline__ T group_allmax(T v) {
+    v = fmax(v, dpp_move<0xB1>(v));
+    v = fmax(v, dpp_move<0x4E>(v));
+    if constexpr (LPN >= 8) v = fmax(v, dpp_move<0x141>(v));
+    if constexpr (LPN >= 16) v = fmax(v, dpp_move<0x140>(v));
+    return v;
+}
+
+// exp and 1/s of the fused forward's softmax.  fp32 uses the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32: about 1 ulp each, and one of each per slot in place of the
+// range-reduced exp and the IEEE divide); the softmax of 16 slots stays within 1e-6 relative.
+#ifndef CL_FUSED_FAST
+#define CL_FUSED_FAST 1
+#endif
+
+template <typename T>
+__device__ __forceinline__ T fused_exp(T v) {
+    if constexpr (CL_FUSED_FAST && sizeof(T) == 4)
+        return __builtin_amdgcn_exp2f(v * 1.44269504088896340736f);
+    else
+        return exp(v);
+}
+
+template <typename T>
+__device__ __forceinline__ T fused_rcp(T v) {
+    if constexpr (CL_FUSED_FAST && sizeof(T) == 4)
+        return __builtin_amdgcn_rcpf(v);
+    else
+        return T(1) / v;
+}
+
+// k_fwd_fused: k_prep and k_fwd_tiled in one pass for layers whose neurons are single runs of
+// at most 16 slots.  Lane l of a neuron's LPN-lane group holds slots l, l + LPN, ... (16 / LPN
+// of them); the logits are loaded together with the row gathers, so the softmax and the
+// collapse to K run while the gathers are in flight.  All lanes of a group stay active until
+// the last reduction (DPP reads its neighbours), partial-chunk lanes only skip their row
+// accesses.  The tile's writer chunk (t mod nchunks) stores probs and the inverse-index
+// coefficients that the backward pass reads.
+template <typename T, int VEC, int LPN, int NPG>
+__device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T* __restrict__ w,
+                                               int softmax, const uint8_t* __restrict__ gs,
+                                               const int4* __restrict__ nab,
+                                               const int32_t* __restrict__ inv_pos,
+                                               T* __restrict__ probs, T* __restrict__ inv_coef,
+                                               T* __restrict__ y, int64_t in_dim, int64_t out_dim,
+                                               int64_t num_runs, int64_t B, int G,
+                                               const TileMap& tm, int64_t c, int64_t t) {
+    using V = typename VT<T, VEC>::type;
+    constexpr int GROUPS = 256 / LPN;
+    constexpr int SPL = 16 / LPN;
+    const int64_t obase = (t * GROUPS + threadIdx.x / LPN) * NPG;
+    if (obase >= out_dim) return;  // uniform per lane group
+    const int l = threadIdx.x % LPN;
+    const int64_t idx = c * (LPN * VEC) + int64_t(l) * VEC;
+    const bool col = idx < B;
+    const bool writer = c == t % tm.nchunks;
+    int4 rec[NPG];
+#pragma unroll
+    for (int j = 0; j < NPG; ++j)
+        rec[j] = obase + j < out_dim ? nab[obase + j] : make_int4(0, 0, 0, 0);
+    T p[NPG][SPL];
+    int code[NPG][SPL];
+#pragma unroll
+    for (int j = 0; j < NPG; ++j)
+#pragma unroll
+        for (int m = 0; m < SPL; ++m) {
+            const int g = l + LPN * m;
+            const bool v = obase + j < out_dim && g < G;
+            p[j][m] = v ? w[(obase + j) * G + g] : -T(__builtin_inf());
+            code[j][m] = v ? gs[(obase + j) * G + g] : 0;
+        }
+    V va[NPG], vb[NPG];
+    bool ok[NPG];
+#pragma unroll
+    for (int j = 0; j < NPG; ++j) {
+        ok[j] = obase + j < out_dim && rec[j].z >= 0 && rec[j].w == rec[j].z + 1 &&
+                rec[j].w <= num_runs && uint32_t(rec[j].x) < uint64_t(in_dim) &&
+                uint32_t(rec[j].y) < uint64_t(in_dim);
+        va[j] = V(T(0));
+        vb[j] = V(T(0));
+        if (ok[j] && col) {
+            va[j] = vld<V>(x + int64_t(rec[j].x) * B + idx);
+            vb[j] = vld<V>(x + int64_t(rec[j].y) * B + idx);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NPG; ++j) {
+        const int64_t o = obase + j;
+        if (softmax) {
+            T mx = p[j][0];
+#pragma unroll
+            for (int m = 1; m < SPL; ++m) mx = fmax(mx, p[j][m]);
+            mx = group_allmax<LPN>(mx);
+            T s = 0;
+#pragma unroll
+            for (int m = 0; m < SPL; ++m) {
+                p[j][m] = l + LPN * m < G ? fused_exp(p[j][m] - mx) : T(0);
+                s += p[j][m];
+            }
+            s = group_allsum<LPN>(s);
+            const T inv = fused_rcp(s);
+#pragma unroll
+            for (int m = 0; m < SPL; ++m) p[j][m] = p[j][m] * inv;
+        } else {
+#pragma unroll
+            for (int m = 0; m < SPL; ++m)
+                if (l + LPN * m >= G) p[j][m] = T(0);
+        }
+        T k0 = 0, k1 = 0, k2 = 0, k3 = 0;
+#pragma unroll
+        for (int m = 0; m < SPL; ++m) {
+            const Coef4<T> cf = gate_coef<T>(code[j][m]);
+            k0 = fma(p[j][m], cf.c0, k0);
+            k1 = fma(p[j][m], cf.c1, k1);
+            k2 = fma(p[j][m], cf.c2, k2);
+            k3 = fma(p[j][m], cf.c3, k3);
+        }
+        k0 = group_allsum<LPN>(k0);
+        k1 = group_allsum<LPN>(k1);
+        k2 = group_allsum<LPN>(k2);
+        k3 = group_allsum<LPN>(k3);
+        if (o >= out_dim) break;
+        if (writer) {
+            if (probs) {
+#pragma unroll
+                for (int m = 0; m < SPL; ++m)
+                    if (l + LPN * m < G) probs[o * G + l + LPN * m] = p[j][m];
+            }
+            if (inv_coef && ok[j] && l == 0) {
+                const int64_t r = rec[j].z;
+                const int64_t pa = inv_pos[2 * r], pb = inv_pos[2 * r + 1];
+                if (uint64_t(pa) < uint64_t(2 * num_runs)) {
+                    inv_coef[2 * pa + 0] = k1;
+                    inv_coef[2 * pa + 1] = k3;
+                }
+                if (uint64_t(pb) < uint64_t(2 * num_runs)) {
+                    inv_coef[2 * pb + 0] = k2;
+                    inv_coef[2 * pb + 1] = k3;
+                }
+            }
+        }
+        if (col) {
+            V acc = V(nan_of<T>());
+            if (ok[j]) acc = k3 * (va[j] * vb[j]) + k2 * vb[j] + k1 * va[j] + k0;
+            vst_stream<V>(y + o * B + idx, acc);
+        }
+    }
+}
+
+template <typename T, int VEC, int LPN, int NPG>
+__global__ __launch_bounds__(256) void k_fwd_fused(const T* __restrict__ x, const T* __restrict__ w,
+                                                   int softmax, const uint8_t* __restrict__ gs,
+                                                   const int4* __restrict__ nab,
+                                                   const int32_t* __restrict__ inv_pos,
+                                                   T* __restrict__ probs, T* __restrict__ inv_coef,
+                                                   T* __restrict__ y, int64_t in_dim,
+                                                   int64_t out_dim, int64_t num_runs, int64_t B,
+                                                   int G, TileMap tm) {
+    for (int it = 0; it < CL_TILE_ITERS; ++it) {
+        int64_t c, t;
+        if (map_tile(tm, virtual_tile(blockIdx.x, it), c, t))
+            fwd_fused_tile<T, VEC, LPN, NPG>(x, w, softmax, gs, nab, inv_pos, probs, inv_coef, y,
+                                             in_dim, out_dim, num_runs, B, G, tm, c, t);
     }
 }
 
@@ -617,6 +811,174 @@ __global__ __launch_bounds__(256) void k_bwd_tiled(
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// k_bwd_part: the input gradient and per-chunk moments through tiles of kPartRows consecutive
+// processing slots.  A workgroup takes TPW = 16 / LPN tiles of one batch chunk; lane group g
+// owns slot row g % 16 of tile g / 16.
+//   1. Every lane group loads its own row segment x_i and leaves a copy in LDS.
+//   2. Internal runs of each tile (both inputs in the tile; listed by tile_ptr / tile_run /
+//      tile_loc) are spread over the tile's lane groups: grad_y of the run's neuron is read
+//      once, both inputs come from LDS, and the two contributions gy (K1 + K3 b) and
+//      gy (K2 + K3 a) go to the LDS slots of the run's two entries, the chunk moments to
+//      `part`.
+//   3. Each owner adds its row's entries in entry order: an internal entry's contribution from
+//      its LDS slot, an external one from the row gathers of bwd_tile.
+// The sum of every row keeps the entry order, so results are bitwise reproducible.
+constexpr int kPartRows = 16;
+constexpr int kPartMaxSlots = 64;
+
+template <typename T, int VEC, int LPN, bool WANT_GX, bool WANT_GW>
+__global__ __launch_bounds__(256) void k_bwd_part(
+    const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
+    const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef,
+    const int32_t* __restrict__ inv_slot, const int32_t* __restrict__ tile_ptr,
+    const int4* __restrict__ tile_run, const int32_t* __restrict__ tile_loc,
+    int64_t num_internal, T* __restrict__ gx, T* __restrict__ part, int64_t in_dim,
+    int64_t out_dim, int64_t num_runs, int64_t B, int slots, TileMap tm) {
+    using V = typename VT<T, VEC>::type;
+    using V2 = typename VT<T, 2>::type;
+    using V4 = typename VT<T, 4>::type;
+    constexpr int CH = LPN * VEC;              // samples per chunk
+    constexpr int TPW = 16 / LPN;              // tiles per workgroup
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    T* xs = reinterpret_cast<T*>(smem_raw);    // [TPW][kPartRows][CH]
+    T* cs = xs + TPW * kPartRows * CH;         // [TPW][slots][CH]
+    int64_t c, t;
+    if (!map_tile(tm, blockIdx.x, c, t)) return;  // uniform per workgroup
+    const int g = threadIdx.x / LPN, l = threadIdx.x % LPN;
+    const int tl = g / kPartRows, rg = g % kPartRows;
+    const int64_t tile = t * TPW + tl;
+    const int64_t slot = tile * kPartRows + rg;
+    const int64_t idx = c * CH + int64_t(l) * VEC;
+    const bool col = idx < B;
+    const bool leader = l == 0;
+    T* xs_t = xs + tl * kPartRows * CH;
+    T* cs_t = cs + int64_t(tl) * slots * CH;
+
+    // 1. own row
+    bool live = slot < in_dim;
+    const int4 sr = live ? slot_rec[slot] : make_int4(0, 0, 0, 0);
+    const int64_t row = sr.x, e0 = sr.y;
+    int64_t deg = int64_t(sr.z) - sr.y;
+    if (live && (uint64_t(row) >= uint64_t(in_dim) || sr.y < 0 || deg < 0 || sr.z > 2 * num_runs))
+        live = false;  // corrupt slot record: nothing is read or written for it
+    if (!live) deg = 0;
+    V xi = V(T(0));
+    if (live && col) xi = vld<V>(x + row * B + idx);
+    *reinterpret_cast<V*>(xs_t + rg * CH + l * VEC) = xi;
+    __syncthreads();
+
+    // 2. internal runs of the tile
+    const int64_t ntiles = (in_dim + kPartRows - 1) / kPartRows;
+    if (tile < ntiles) {
+        const int64_t ip0 = tile_ptr[tile], ip1 = tile_ptr[tile + 1];
+        const bool ok_range = ip0 >= 0 && ip1 >= ip0 && ip1 <= num_internal &&
+                              ip1 - ip0 <= slots / 2;
+        for (int64_t k = ok_range ? ip0 + rg : ip1; k < ip1; k += kPartRows) {
+            const int4 tr = tile_run[k];
+            const int loc = tile_loc[k];
+            const int al = loc & 0xff, bl = (loc >> 8) & 0xff;
+            const int sa = (loc >> 16) & 0xff, sb = (loc >> 24) & 0xff;
+            if (uint64_t(tr.x) >= uint64_t(out_dim) || uint64_t(tr.y) >= uint64_t(num_runs) ||
+                uint64_t(tr.z) >= uint64_t(2 * num_runs) ||
+                uint64_t(tr.w) >= uint64_t(2 * num_runs) || al >= kPartRows || bl >= kPartRows ||
+                sa >= slots || sb >= slots)
+                continue;  // corrupt record: skipped, nothing is read or written for it
+            V vg = V(T(0));
+            if (col) vg = vld<V>(gy + int64_t(tr.x) * B + idx);
+            const V2 ka = vld<V2>(inv_coef + 2 * int64_t(tr.z));
+            const V2 kb = vld<V2>(inv_coef + 2 * int64_t(tr.w));
+            const V va = *reinterpret_cast<const V*>(xs_t + al * CH + l * VEC);
+            const V vb = *reinterpret_cast<const V*>(xs_t + bl * CH + l * VEC);
+            if (WANT_GX) {
+                *reinterpret_cast<V*>(cs_t + sa * CH + l * VEC) = (ka[0] + ka[1] * vb) * vg;
+                *reinterpret_cast<V*>(cs_t + sb * CH + l * VEC) = (kb[0] + kb[1] * va) * vg;
+            }
+            if (WANT_GW) {
+                const V ga = vg * va;
+                T s1 = hsum<T, VEC>(vg), s2 = hsum<T, VEC>(ga);
+                T s3 = hsum<T, VEC>(vg * vb), s4 = hsum<T, VEC>(ga * vb);
+                s1 = group_sum<LPN>(s1);
+                s2 = group_sum<LPN>(s2);
+                s3 = group_sum<LPN>(s3);
+                s4 = group_sum<LPN>(s4);
+                if (leader) {
+                    V4 mv;
+                    mv[0] = s1;
+                    mv[1] = s2;
+                    mv[2] = s3;
+                    mv[3] = s4;
+                    *reinterpret_cast<V4*>(part + (int64_t(tr.y) * tm.nchunks + c) * 4) = mv;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. the row's entries in entry order
+    V acc = V(T(0));
+    bool bad = false;
+    int4 rec = make_int4(0, 0, 0, 0);
+    V2 kk = V2(T(0));
+    int sl = -1;
+    if (deg > 0) {
+        rec = inv_rec[e0];
+        kk = vld<V2>(inv_coef + 2 * e0);
+        sl = inv_slot[e0];
+    }
+    for (int64_t k = 0; k < deg; ++k) {
+        const int4 cur = rec;
+        const V2 ck = kk;
+        const int cs_slot = sl;
+        if (k + 1 < deg) {
+            rec = inv_rec[e0 + k + 1];
+            kk = vld<V2>(inv_coef + 2 * (e0 + k + 1));
+            sl = inv_slot[e0 + k + 1];
+        }
+        if (cs_slot >= 0) {
+            if (cs_slot >= slots) {
+                bad = true;
+                continue;
+            }
+            if (WANT_GX) acc += *reinterpret_cast<const V*>(cs_t + cs_slot * CH + l * VEC);
+            continue;
+        }
+        if (uint64_t(cur.x) >= uint64_t(out_dim) || uint64_t(cur.y) >= uint64_t(in_dim) ||
+            uint64_t(cur.z) >= uint64_t(num_runs)) {
+            bad = true;
+            continue;
+        }
+        V vo = V(T(0)), vg = V(T(0));
+        if (col) {
+            vo = vld<V>(x + int64_t(cur.y) * B + idx);
+            vg = vld<V>(gy + int64_t(cur.x) * B + idx);
+        }
+        if (WANT_GX) acc += (ck[0] + ck[1] * vo) * vg;
+        if (WANT_GW && cur.w == 0) {
+            const V ga = vg * xi;
+            T s1 = hsum<T, VEC>(vg), s2 = hsum<T, VEC>(ga);
+            T s3 = hsum<T, VEC>(vg * vo), s4 = hsum<T, VEC>(ga * vo);
+            s1 = group_sum<LPN>(s1);
+            s2 = group_sum<LPN>(s2);
+            s3 = group_sum<LPN>(s3);
+            s4 = group_sum<LPN>(s4);
+            if (leader) {
+                V4 mv;
+                mv[0] = s1;
+                mv[1] = s2;
+                mv[2] = s3;
+                mv[3] = s4;
+                *reinterpret_cast<V4*>(part + (int64_t(cur.z) * tm.nchunks + c) * 4) = mv;
+            }
+        }
+    }
+    if (WANT_GX && live && col) {
+        V r = acc;
+        if (bad) r = V(nan_of<T>());
+        vst_stream<V>(gx + row * B + idx, r);
+    }
+}
+
 // k_moments: the per-chunk moments of every run, per neuron (used when grad_x is not needed).
 template <typename T, int VEC, int LPN>
 __global__ __launch_bounds__(256) void k_moments(const T* __restrict__ x, const T* __restrict__ gy,
@@ -883,6 +1245,43 @@ extern "C" int cl_dense_forward_tiled(int dtype, const void* x, const void* run_
     return check_launch("cl_dense_forward_tiled");
 }
 
+extern "C" int cl_dense_forward_fused(int dtype, const void* x, const void* w, int softmax,
+                                      const uint8_t* gate_seq, const int32_t* nab,
+                                      const int32_t* inv_pos, void* probs, void* inv_coef,
+                                      void* y, int64_t in_dim, int64_t out_dim,
+                                      int64_t num_runs, int64_t batch, int64_t num_gates,
+                                      void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(in_dim, out_dim, batch, num_gates, num_runs)) return rc;
+    CL_ARG(num_gates <= 16, "the fused forward takes at most 16 slots, got %lld",
+           (long long)num_gates);
+    CL_ARG(batch >= 1, "the fused forward needs batch >= 1 (use cl_dense_prep)");
+    if (out_dim == 0) return CL_OK;
+    CL_ARG(in_dim > 0, "in_dim is 0 but out_dim > 0");
+    CL_ARG(x && w && gate_seq && nab && y, "null pointer argument");
+    CL_ARG(!inv_coef || inv_pos, "inv_coef needs inv_pos");
+    CL_ARG(aligned(nab, 16), "nab misaligned");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        CL_ARG(!vec_ok<T>(batch) || all_aligned({x, y}), "x and y must be 16-byte aligned");
+        const Tiling tl = choose_tiling<T>(batch, out_dim, CL_FUSED_VEC_MULT, CL_FWD_LPN, CL_FWD_NPG);
+        const unsigned grid = unsigned(iter_grid(tl.map));
+        auto* xs = static_cast<const T*>(x);
+        auto* ws = static_cast<const T*>(w);
+        auto* nb = reinterpret_cast<const int4*>(nab);
+        auto* pr = static_cast<T*>(probs);
+        auto* ic = static_cast<T*>(inv_coef);
+        auto* ys = static_cast<T*>(y);
+        with_tiling<T, CL_FUSED_VEC_MULT>(tl, [&](auto vc, auto lc) {
+            k_fwd_fused<T, decltype(vc)::value, decltype(lc)::value, CL_FWD_NPG>
+                <<<grid, 256, 0, s>>>(xs, ws, softmax, gate_seq, nb, inv_pos, pr, ic, ys, in_dim,
+                                      out_dim, num_runs, batch, int(num_gates), tl.map);
+        });
+    });
+    return check_launch("cl_dense_forward_fused");
+}
+
 extern "C" int cl_dense_weight_grad(int dtype, const void* x, const void* grad_y,
                                     const uint8_t* gate_seq, const void* probs,
                                     const int32_t* run_ptr, const int32_t* run_ab,
@@ -1004,6 +1403,65 @@ extern "C" int cl_dense_backward_tiled(int dtype, const void* x, const void* gra
         }
     });
     return check_launch("cl_dense_backward_tiled");
+}
+
+extern "C" int cl_dense_backward_part(int dtype, const void* x, const void* grad_y,
+                                      const int32_t* slot_rec, const int32_t* inv_rec,
+                                      const void* inv_coef, const int32_t* inv_slot,
+                                      const int32_t* tile_ptr, const int32_t* tile_run,
+                                      const int32_t* tile_loc, int64_t num_internal,
+                                      int64_t part_slots, void* grad_x,
+                                      void* moments, int64_t nchunks, int64_t in_dim,
+                                      int64_t out_dim, int64_t num_runs, int64_t batch,
+                                      void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(in_dim, out_dim, batch, 1, num_runs)) return rc;
+    CL_ARG(part_slots >= 2 && part_slots <= kPartMaxSlots && part_slots % 2 == 0,
+           "part_slots must be even and in [2, %d]", kPartMaxSlots);
+    CL_ARG(grad_x, "grad_x is required (use cl_dense_backward_tiled for moments alone)");
+    CL_ARG(num_internal >= 0 && (num_internal == 0 || (tile_run && tile_loc)),
+           "tile_run / tile_loc missing");
+    if (batch == 0 || in_dim == 0)
+        return cl_dense_backward_tiled(dtype, x, grad_y, nullptr, nullptr, slot_rec, inv_rec,
+                                       inv_coef, grad_x, moments, nchunks, in_dim, out_dim,
+                                       num_runs, batch, stream);
+    CL_ARG(x && grad_y && slot_rec && inv_rec && inv_coef && inv_slot && tile_ptr,
+           "null pointer argument");
+    CL_ARG(aligned(slot_rec, 16) && aligned(inv_rec, 16) && aligned(inv_coef, 8) &&
+               (!tile_run || aligned(tile_run, 16)),
+           "slot_rec / inv_rec / tile_run must be 16-byte aligned, inv_coef 8-byte aligned");
+    if (moments) CL_ARG(aligned(moments, 16), "moments must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        const bool v = vec_ok<T>(batch);
+        CL_ARG(!v || all_aligned({x, grad_y, grad_x}), "row buffers must be 16-byte aligned");
+        const Tiling tl = choose_tiling<T>(batch, in_dim, CL_BWD_VEC_MULT, CL_BWD_LPN, 1);
+        if (moments)
+            CL_ARG(nchunks == tl.map.nchunks, "moments buffer must use the backward chunk count");
+        const unsigned grid = unsigned(tile_grid(tl.map));
+        auto* xs = static_cast<const T*>(x);
+        auto* gys = static_cast<const T*>(grad_y);
+        auto* rec = reinterpret_cast<const int4*>(inv_rec);
+        auto* srec = reinterpret_cast<const int4*>(slot_rec);
+        auto* trun = reinterpret_cast<const int4*>(tile_run);
+        auto* ic = static_cast<const T*>(inv_coef);
+        auto* gxs = static_cast<T*>(grad_x);
+        auto* mom = static_cast<T*>(moments);
+        with_tiling<T, CL_BWD_VEC_MULT>(tl, [&](auto vc, auto lc) {
+            constexpr int VEC = decltype(vc)::value, LPN = decltype(lc)::value;
+            const size_t lds = size_t(16 / LPN) * (kPartRows + part_slots) * LPN * VEC * sizeof(T);
+            if (moments)
+                k_bwd_part<T, VEC, LPN, true, true><<<grid, 256, lds, s>>>(
+                    xs, gys, srec, rec, ic, inv_slot, tile_ptr, trun, tile_loc, num_internal, gxs, mom, in_dim,
+                    out_dim, num_runs, batch, int(part_slots), tl.map);
+            else
+                k_bwd_part<T, VEC, LPN, true, false><<<grid, 256, lds, s>>>(
+                    xs, gys, srec, rec, ic, inv_slot, tile_ptr, trun, tile_loc, num_internal, gxs, mom, in_dim,
+                    out_dim, num_runs, batch, int(part_slots), tl.map);
+        });
+    });
+    return check_launch("cl_dense_backward_part");
 }
 
 extern "C" int cl_dense_backward_finalize(int dtype, const void* moments, int64_t nchunks,

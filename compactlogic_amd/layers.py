@@ -18,7 +18,7 @@ from . import _capi
 from . import convlogic_hip as _cl
 from . import difflogic_hip as _dl
 from . import timing
-from .plan import RunPlan, build_run_plan
+from .plan import PART_SLOTS, RunPlan, build_run_plan
 
 
 ########################################################################################################################
@@ -121,7 +121,17 @@ class LogicLayerRunsFunction(torch.autograd.Function):
     HIP kernels and the gradient returned is that of the logits), else probabilities.  Slots
     sharing an input pair are collapsed, the batch is tiled in XCD-pinned chunks, and both
     gradients come from one pass over the inverse index plus a per-neuron finalize (a single
-    whole-batch pass when the input needs no gradient)."""
+    whole-batch pass when the input needs no gradient).  When every neuron is one run of at
+    most 16 slots, the softmax and the collapse happen inside the forward kernel
+    (cl_dense_forward_fused); `fused_forward = False` selects the separate prep launch.
+    `partitioned_backward = True` takes the input gradient through the plan's tiles
+    (cl_dense_backward_part: runs with both inputs in one tile read grad_y once and their
+    inputs from LDS).  It reads a third fewer row bytes but its barrier-separated phases keep
+    fewer loads in flight, and it measures slower than cl_dense_backward_tiled at cfg2, so it
+    is off by default."""
+
+    fused_forward = True
+    partitioned_backward = False
 
     @staticmethod
     def forward(ctx, x, w, gate_sequence, plan: RunPlan, softmax: bool = False):
@@ -138,6 +148,17 @@ class LogicLayerRunsFunction(torch.autograd.Function):
         inv_coef = torch.empty((2 * plan.num_runs, 2), dtype=x.dtype, device=dev)
         y = torch.empty((plan.out_dim, batch), dtype=x.dtype, device=dev)
         stream = _dl.stream_of(x)
+        if (LogicLayerRunsFunction.fused_forward and plan.single_run and plan.num_gates <= 16
+                and batch > 0):
+            with torch.cuda.device(dev):
+                timing.timed(f"cl_dense_forward_fused[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                    "cl_dense_forward_fused", code, x.data_ptr(), w.data_ptr(), int(softmax),
+                    gate_sequence.data_ptr(), plan.nab.data_ptr(), plan.inv_pos.data_ptr(),
+                    _dl.ptr(probs), inv_coef.data_ptr(), y.data_ptr(), plan.in_dim, plan.out_dim,
+                    plan.num_runs, batch, plan.num_gates, stream))
+            ctx.save_for_backward(x, inv_coef, gate_sequence, probs)
+            ctx.plan = plan
+            return y
         coef = torch.empty((plan.num_runs, 4), dtype=x.dtype, device=dev)
         with torch.cuda.device(dev):
             timing.timed(f"cl_dense_prep[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
@@ -172,12 +193,22 @@ class LogicLayerRunsFunction(torch.autograd.Function):
                     nchunks = _chunks(x, plan.in_dim, plan.out_dim)
                     moments = torch.empty((plan.num_runs, nchunks, 4), dtype=x.dtype,
                                           device=x.device)
-                timing.timed(f"cl_dense_backward_tiled[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
-                    "cl_dense_backward_tiled", code, x.data_ptr(), grad_y.data_ptr(),
-                    plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(), plan.slot_rec.data_ptr(),
-                    plan.inv_rec.data_ptr(), inv_coef.data_ptr(), grad_x.data_ptr(),
-                    _dl.ptr(moments), nchunks, plan.in_dim, plan.out_dim, plan.num_runs, batch,
-                    stream))
+                if LogicLayerRunsFunction.partitioned_backward and plan.tile_ptr is not None:
+                    timing.timed(f"cl_dense_backward_part[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                        "cl_dense_backward_part", code, x.data_ptr(), grad_y.data_ptr(),
+                        plan.slot_rec.data_ptr(), plan.inv_rec.data_ptr(), inv_coef.data_ptr(),
+                        plan.inv_slot.data_ptr(), plan.tile_ptr.data_ptr(),
+                        plan.tile_run.data_ptr(), plan.tile_loc.data_ptr(),
+                        plan.tile_loc.numel(), PART_SLOTS,
+                        grad_x.data_ptr(), _dl.ptr(moments), nchunks, plan.in_dim, plan.out_dim,
+                        plan.num_runs, batch, stream))
+                else:
+                    timing.timed(f"cl_dense_backward_tiled[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                        "cl_dense_backward_tiled", code, x.data_ptr(), grad_y.data_ptr(),
+                        plan.run_ptr.data_ptr(), plan.run_ab.data_ptr(), plan.slot_rec.data_ptr(),
+                        plan.inv_rec.data_ptr(), inv_coef.data_ptr(), grad_x.data_ptr(),
+                        _dl.ptr(moments), nchunks, plan.in_dim, plan.out_dim, plan.num_runs,
+                        batch, stream))
                 if need_w:
                     timing.timed(f"cl_dense_backward_finalize[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
                         "cl_dense_backward_finalize", code, moments.data_ptr(), nchunks,
@@ -191,6 +222,40 @@ class LogicLayerRunsFunction(torch.autograd.Function):
                     plan.run_ab.data_ptr(), plan.run_gl.data_ptr(), grad_w.data_ptr(),
                     plan.in_dim, plan.out_dim, plan.num_runs, batch, plan.num_gates, stream))
         return grad_x, grad_w, None, None, None
+
+
+def _transpose_rows(x: torch.Tensor) -> torch.Tensor:
+    """Contiguous [cols, rows] transpose of a contiguous 2-D device tensor [rows, cols]."""
+    out = torch.empty((x.shape[1], x.shape[0]), dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        timing.timed(f"cl_transpose[{x.shape[0]}x{x.shape[1]}]", lambda: _capi.call(
+            "cl_transpose", _dl.dtype_code(x), x.data_ptr(), out.data_ptr(), x.shape[0],
+            x.shape[1], _dl.stream_of(x)))
+    return out
+
+
+class TransposeFunction(torch.autograd.Function):
+    """x [batch, features] -> contiguous [features, batch] rows, and the gradient back, through
+    the HIP transpose kernel: the layout change of compactlogic/compactlogic.py:100-101."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return _transpose_rows(x.contiguous())
+
+    @staticmethod
+    def backward(ctx, grad):
+        return _transpose_rows(grad.contiguous())
+
+
+def to_rows(x: torch.Tensor) -> torch.Tensor:
+    """[batch, features] -> contiguous [features, batch]; a view when x already is the
+    transpose of a contiguous tensor (the output of a previous LogicLayer)."""
+    t = x.transpose(0, 1)
+    if t.is_contiguous():
+        return t
+    if x.device.type == "cuda" and x.dtype in (torch.float32, torch.float64):
+        return TransposeFunction.apply(x)
+    return t.contiguous()
 
 
 class GroupSumFunction(torch.autograd.Function):
@@ -294,7 +359,7 @@ class LogicLayer(torch.nn.Module):
         """Training forward: x [batch, in_dim] -> [batch, out_dim] (a transposed view of the
         kernel's [out_dim, batch] output, as in the reference, :83-118)."""
         assert x.ndim == 2, x.ndim
-        x = x.transpose(0, 1).contiguous()
+        x = to_rows(x)
         assert x.shape[0] == self.in_dim, (x.shape, self.in_dim)
         plan = self.run_plan()
         if self.weights.dtype == x.dtype:
@@ -319,8 +384,7 @@ class LogicLayer(torch.nn.Module):
             x.t = timing.timed(f"cl_dense_eval_packed[{self.in_dim}->{self.out_dim}]",
                                lambda: _dl.eval_packed(x.t, a, b, w, self.gate_sequence))
             return x
-        x = x.transpose(0, 1).contiguous()
-        return _dl.eval(x, a, b, w, self.gate_sequence).transpose(0, 1)
+        return _dl.eval(to_rows(x), a, b, w, self.gate_sequence).transpose(0, 1)
 
     def extra_repr(self):
         return '{}, {}, {}'.format(self.in_dim, self.out_dim, 'train' if self.training else 'eval')

@@ -102,8 +102,8 @@ int cl_dense_eval(int dtype, const void* x, const int64_t* a, const int64_t* b,
  *   inv_rec   int32 [2R, 4]         per entry: neuron, other input, run, side
  *   inv_pos   int32 [2R]            entry position of run side 2r + side
  *   nab       int32 [out_dim, 4]    a, b of the first run, run_ptr[o], run_ptr[o+1]
- *   slot_rec  int32 [in_dim, 4]     input row, first entry, end entry, 0 -- by descending
- *                                   entry count
+ *   slot_rec  int32 [in_dim, 4]     input row, first entry, end entry, 0 -- in the plan's
+ *                                   processing order (depth-first over the runs)
  *   run_coef  T [num_runs, 4]       K of every run
  *
  * The batch is processed in chunks pinned to XCDs (see dense_tiled.hip); when
@@ -126,6 +126,20 @@ int cl_dense_forward_tiled(int dtype, const void* x, const void* run_coef, const
                            const int32_t* run_ab, void* y, int64_t in_dim, int64_t out_dim,
                            int64_t num_runs, int64_t batch, void* stream);
 
+/* cl_dense_prep and cl_dense_forward_tiled in one launch, for layers whose neurons are one run
+ * each (nab[o].w == nab[o].z + 1, every slot of a neuron reads the same input pair) and at
+ * most 16 slots.  Every workgroup computes the probabilities and coefficients of its neurons
+ * in registers while its gathers are in flight; one batch chunk per tile writes `probs` and
+ * `inv_coef` (either may be NULL) as cl_dense_prep does.  batch must be >= 1 (use
+ * cl_dense_prep for an empty batch).  No single counterpart in the reference: it does the
+ * softmax of compactlogic/compactlogic.py:107 and the forward of
+ * compactlogic/cuda/difflogic_kernel.cu:38-78 together, for the module path. */
+int cl_dense_forward_fused(int dtype, const void* x, const void* w, int softmax,
+                           const uint8_t* gate_seq, const int32_t* nab, const int32_t* inv_pos,
+                           void* probs, void* inv_coef, void* y, int64_t in_dim,
+                           int64_t out_dim, int64_t num_runs, int64_t batch,
+                           int64_t num_gates, void* stream);
+
 /* Weight gradient of every slot straight from the whole batch (no chunked moments), with the
  * softmax backward when probs is not NULL: for layers whose input needs no gradient. */
 int cl_dense_weight_grad(int dtype, const void* x, const void* grad_y, const uint8_t* gate_seq,
@@ -139,7 +153,7 @@ int cl_dense_tiled_chunks(int dtype, int64_t batch, int64_t in_dim, int64_t out_
 
 /* Backward through the plan.  grad_x (may be NULL) receives the input gradient, walking the
  * inverse index slot by slot: slot_rec[s] = (input row, first entry, end entry, 0) (int32
- * [in_dim, 4]) in descending order of entry count, entry records inv_rec[e] = (neuron, other
+ * [in_dim, 4]) in the plan's processing order, entry records inv_rec[e] = (neuron, other
  * input, run, side) (int32 [2 * num_runs, 4]) and the entry coefficients inv_coef of
  * cl_dense_prep (all 16-byte aligned).  moments (T [num_runs, nchunks, 4], may be NULL)
  * receives the per-chunk batch moments (sum gy, gy a, gy b, gy a b) of every run: at its
@@ -150,6 +164,24 @@ int cl_dense_backward_tiled(int dtype, const void* x, const void* grad_y, const 
                             const int32_t* inv_rec, const void* inv_coef, void* grad_x,
                             void* moments, int64_t nchunks, int64_t in_dim, int64_t out_dim,
                             int64_t num_runs, int64_t batch, void* stream);
+
+/* cl_dense_backward_tiled (grad_x required) through tiles of 16 consecutive processing slots.
+ * A run whose two inputs are in the same tile is internal to it: tile_ptr[t] .. tile_ptr[t+1]-1
+ * (int32 [ceil(in_dim / 16) + 1]) index its records tile_run = (neuron, run, entry of operand
+ * a, entry of operand b) (int32 [N, 4], 16-byte aligned) and tile_loc = a's position in the
+ * tile | b's position << 8 | LDS slot of a's entry << 16 | slot of b's entry << 24 (int32
+ * [N], N = num_internal); inv_slot[e] (int32 [2 * num_runs]) is the LDS slot of entry e,
+ * -1 for the entries of the other runs.  At most part_slots / 2 internal runs per tile
+ * (part_slots even, 2..64).
+ * An internal run's grad_y row is read once and both its input rows come from the tile's
+ * copy in LDS; each row still adds its entries in entry order, so the result equals
+ * cl_dense_backward_tiled's to rounding and is bitwise reproducible. */
+int cl_dense_backward_part(int dtype, const void* x, const void* grad_y, const int32_t* slot_rec,
+                           const int32_t* inv_rec, const void* inv_coef, const int32_t* inv_slot,
+                           const int32_t* tile_ptr, const int32_t* tile_run,
+                           const int32_t* tile_loc, int64_t num_internal, int64_t part_slots,
+                           void* grad_x, void* moments, int64_t nchunks, int64_t in_dim,
+                           int64_t out_dim, int64_t num_runs, int64_t batch, void* stream);
 
 /* Weight gradient from the moments: grad_w[o, g] = (c0, c1, c2, c3)[gate_seq[o,g]] . (moments
  * of g's run summed over the chunks in chunk order); with `probs` (not NULL) followed by the
@@ -298,6 +330,14 @@ int cl_group_sum_workspace_size(int dtype, int64_t batch, int64_t features, int6
 int cl_group_sum_backward(int dtype, const void* grad_out, int64_t batch, int64_t features,
                           int64_t k, double tau, void* grad_x, int64_t stride_batch,
                           int64_t stride_feature, void* stream);
+
+/* -------------------------------------------------------------------------------------------
+ * Layout change: dst [cols, rows] = transpose of src [rows, cols] (both contiguous, not
+ * overlapping).  Replaces the torch transpose copy of compactlogic/compactlogic.py:100-101
+ * between a module's [batch, features] input and the kernels' [features, batch] rows.
+ * ----------------------------------------------------------------------------------------- */
+int cl_transpose(int dtype, const void* src, void* dst, int64_t rows, int64_t cols,
+                 void* stream);
 
 /* -------------------------------------------------------------------------------------------
  * Bit-packed discrete inference.  A packed row is a little-endian bit string: bit j of the

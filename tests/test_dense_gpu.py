@@ -58,6 +58,9 @@ SHAPES = [
     (784, 500, 16, 128, True),
     (40, 30, 128, 40, False),
     (1000, 600, 16, 4096, True),
+    # single-run neurons with 8- and 4-lane groups (the fused forward), a partial last chunk
+    (200, 150, 16, 256, True),
+    (60, 70, 5, 200, True),
 ]
 
 
@@ -232,3 +235,146 @@ def test_rewiring_keeps_training_path_consistent(device):
     ref = O.dense_forward(np_(x).T, np_(layer.indices[0]), np_(layer.indices[1]),
                           np_(torch.softmax(layer.weights, -1)), np_(layer.gate_sequence))
     np.testing.assert_allclose(np_(y).T, ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("batch", [1, 37, 200, 256, 1024])
+def test_fused_forward_matches_separate_prep(device, batch):
+    """cl_dense_forward_fused (softmax + collapse inside the forward) against cl_dense_prep +
+    cl_dense_forward_tiled: the same outputs, probabilities, inverse-index coefficients and
+    gradients, to rounding."""
+    torch.manual_seed(21)
+    layer = cl.LogicLayer(300, 260, num_gates=16, connections="original").to(device)
+    plan = layer.run_plan()
+    assert plan.single_run
+    x = torch.rand(batch, 300, device=device)
+    gy = torch.randn(batch, 260, device=device) / batch
+    outs = []
+    for fused in (True, False):
+        cl.LogicLayerRunsFunction.fused_forward = fused
+        try:
+            layer.weights.grad = None
+            xx = x.clone().requires_grad_(True)
+            y = layer(xx)
+            y.backward(gy)
+            outs.append((y.detach(), xx.grad, layer.weights.grad.clone()))
+        finally:
+            cl.LogicLayerRunsFunction.fused_forward = True
+    for u, v in zip(*outs):
+        torch.testing.assert_close(u, v, rtol=1e-6, atol=1e-7)
+    ref = O.dense_forward(np_(x).T.astype(np.float64), np_(layer.indices[0]), np_(layer.indices[1]),
+                          np_(torch.softmax(layer.weights.double(), -1)), np_(layer.gate_sequence))
+    np.testing.assert_allclose(np_(outs[0][0]).T, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_fused_forward_entry_point_checks(device):
+    import ctypes
+    from compactlogic_amd import _capi
+    L = make_layer(31, 20, 12, 16, 64, shared=True)
+    D = to_dev(L, device, torch.float32)
+    plan = cl.build_run_plan(torch.stack([D["a"], D["b"]]), 20)
+    probs = torch.empty_like(D["w"])
+    inv = torch.empty((2 * plan.num_runs, 2), device=device)
+    y = torch.empty((12, 64), device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = _capi.load()
+
+    def call(batch, gates):
+        return lib.cl_dense_forward_fused(0, D["x"].data_ptr(), D["w"].data_ptr(), 0,
+                                          D["gs"].data_ptr(), plan.nab.data_ptr(),
+                                          plan.inv_pos.data_ptr(), probs.data_ptr(),
+                                          inv.data_ptr(), y.data_ptr(), 20, 12, plan.num_runs,
+                                          batch, gates, stream)
+
+    assert call(64, 17) != 0 and b"16 slots" in lib.cl_last_error()
+    assert call(0, 16) != 0
+    assert call(64, 16) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(np_(y), O.dense_forward(L["x"], L["a"], L["b"], L["w"], L["gs"]),
+                               rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(np_(probs), L["w"].astype(np.float32))
+    # a neuron whose plan record claims two runs is poisoned, never mis-computed
+    nab = plan.nab.clone()
+    nab[3, 3] += 1
+    plan.nab, saved = nab, plan.nab
+    try:
+        assert call(64, 16) == 0
+    finally:
+        plan.nab = saved
+    torch.cuda.synchronize()
+    assert torch.isnan(y[3]).all() and not torch.isnan(y[torch.arange(12) != 3]).any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", [(1, 1), (3, 70), (130, 65), (64, 64), (1024, 784), (256, 25088)])
+def test_transpose_kernel_is_exact(device, dtype, shape):
+    x = torch.randn(shape, dtype=dtype, device=device)
+    t = cl.layers.TransposeFunction.apply(x)
+    assert t.is_contiguous() and torch.equal(t, x.t())
+    xg = x.clone().requires_grad_(True)
+    g = torch.randn(shape[1], shape[0], dtype=dtype, device=device)
+    cl.layers.TransposeFunction.apply(xg).backward(g)
+    assert torch.equal(xg.grad, g.t())
+
+
+def test_layer_input_layout_change_keeps_gradients(device):
+    """A LogicLayer fed a contiguous [batch, in] tensor (transposed by the HIP kernel) and one
+    fed the transpose of a contiguous [in, batch] tensor (a view, no kernel) agree bitwise."""
+    torch.manual_seed(23)
+    layer = cl.LogicLayer(130, 90, connections="original").to(device)
+    x = torch.rand(70, 130, device=device)
+    gy = torch.randn(70, 90, device=device)
+    grads = []
+    for xin in (x.clone(), x.t().contiguous().t()):
+        xin.requires_grad_(True)
+        layer.weights.grad = None
+        layer(xin).backward(gy)
+        grads.append((xin.grad.clone(), layer.weights.grad.clone()))
+    for u, v in zip(*grads):
+        assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", [(3000, 1600, 16, 1024), (20, 300, 4, 256), (500, 400, 8, 96),
+                                   (1200, 1000, 1, 37), (64, 64, 16, 2048)])
+def test_partitioned_backward_matches_untiled(device, dtype, shape):
+    """cl_dense_backward_part (internal runs through LDS) against cl_dense_backward_tiled:
+    the same input gradient and logits gradient to rounding, both against the oracle, and
+    bitwise reproducible.  Shapes cover full tiles (more internal runs than LDS slots),
+    self-pairs, multi-slot runs, 4- to 16-lane groups and a partial last chunk."""
+    in_dim, out_dim, g_n, batch = shape
+    g = torch.Generator().manual_seed(sum(shape))
+    idx = torch.randint(0, in_dim, (2, out_dim, g_n), generator=g)
+    idx[:, ::3] = idx[:, ::3, :1]
+    idx[1, ::7] = idx[0, ::7]
+    idx = idx.to(device)
+    plan = cl.build_run_plan(idx.contiguous(), in_dim)
+    assert int(plan.tile_ptr[-1]) > 0
+    logits = torch.randn(out_dim, g_n, generator=g).to(device=device, dtype=dtype)
+    gs = torch.randint(0, 16, (out_dim, g_n), generator=g).to(device=device, dtype=torch.uint8)
+    x0 = torch.rand(in_dim, batch, generator=g).to(device=device, dtype=dtype)
+    gy = (torch.rand(out_dim, batch, generator=g) - 0.5).to(device=device, dtype=dtype) / batch
+    outs = []
+    default = cl.LogicLayerRunsFunction.partitioned_backward
+    for part in (True, True, False):
+        cl.LogicLayerRunsFunction.partitioned_backward = part
+        try:
+            x = x0.clone().requires_grad_(True)
+            w = logits.clone().requires_grad_(True)
+            y = cl.LogicLayerRunsFunction.apply(x, w, gs, plan, True)
+            outs.append(torch.autograd.grad(y, (x, w), gy))
+        finally:
+            cl.LogicLayerRunsFunction.partitioned_backward = default
+    for u, v in zip(outs[0], outs[1]):
+        assert torch.equal(u, v), "partitioned backward is not bitwise deterministic"
+    tol = dict(rtol=1e-6, atol=1e-7) if dtype == torch.float32 else dict(rtol=1e-12, atol=1e-14)
+    for u, v in zip(outs[0], outs[2]):
+        torch.testing.assert_close(u, v, **tol)
+    a, b = idx[0].cpu().numpy(), idx[1].cpu().numpy()
+    p = torch.softmax(logits.double(), -1).cpu().numpy()
+    gyn = gy.double().cpu().numpy()
+    xn = x0.double().cpu().numpy()
+    gp = O.dense_backward_w(xn, a, b, gs.cpu().numpy(), gyn)
+    np.testing.assert_allclose(np_(outs[0][1]), p * (gp - (p * gp).sum(1, keepdims=True)),
+                               **TOL[dtype])
+    np.testing.assert_allclose(np_(outs[0][0]), O.dense_backward_x_direct(xn, a, b, p, gs.cpu().numpy(), gyn),
+                               **TOL[dtype])

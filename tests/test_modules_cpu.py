@@ -267,8 +267,9 @@ def test_conv_inverse_index_cache_follows_tensors():
 
 
 def test_run_plan_processing_order():
-    """row_order is a permutation of the inputs, degree-sorted inside blocks of 1024, with
-    every input of degree 0 last; slot_rec follows it."""
+    """row_order is a depth-first preorder of the run graph: a permutation of the inputs with
+    every input of degree 0 last, in which each input after the first of a search has an
+    earlier neighbour (depth-first: its parent); slot_rec follows it."""
     from compactlogic_amd.plan import build_run_plan
     g = torch.Generator().manual_seed(11)
     in_dim, out_dim = 3000, 1600
@@ -278,12 +279,77 @@ def test_run_plan_processing_order():
     assert sorted(order.tolist()) == list(range(in_dim))
     deg = (plan.inv_ptr[1:] - plan.inv_ptr[:-1]).long()
     d = deg[order]
-    for s0 in range(0, in_dim, 1024):
-        seg = d[s0:s0 + 1024]
-        assert bool((seg[:-1] >= seg[1:]).all())
     nz = int((deg > 0).sum())
-    assert bool((d[nz:] == 0).all())
+    assert bool((d[nz:] == 0).all()) and bool((d[:nz] > 0).all())
+    # depth-first: the input right after u is a neighbour of u, or the search backtracked to
+    # a neighbour of an earlier input, or a new search started (no visited neighbour at all)
+    ab = plan.run_ab.long()
+    nbrs = [set() for _ in range(in_dim)]
+    for x, y in ab.tolist():
+        nbrs[x].add(y)
+        nbrs[y].add(x)
+    seen = set()
+    starts = 0
+    for k, u in enumerate(order[:nz].tolist()):
+        if k and order[k - 1].item() in nbrs[u]:
+            pass
+        elif nbrs[u] & seen:
+            pass
+        else:
+            starts += 1
+            # a new search starts at an input of maximal degree among the unvisited ones
+            rest = [v for v in range(in_dim) if v not in seen and deg[v] > 0]
+            assert deg[u] == max(deg[v] for v in rest)
+        seen.add(u)
+    assert starts < nz // 4
     rec = plan.slot_rec.long()
     assert torch.equal(rec[:, 0], order)
     assert torch.equal(rec[:, 1], plan.inv_ptr.long()[order])
     assert torch.equal(rec[:, 2], plan.inv_ptr.long()[order + 1])
+
+
+@pytest.mark.parametrize("in_dim,out_dim,g_n,seed", [(3000, 1600, 16, 11), (20, 300, 4, 12),
+                                                     (64, 64, 1, 13), (1000, 900, 8, 14)])
+def test_run_plan_tiles(in_dim, out_dim, g_n, seed):
+    """The tiles of the partitioned input gradient: every internal run has both inputs in its
+    tile, at the recorded positions, with two distinct LDS slots that the entries' inv_slot
+    name; at most PART_SLOTS / 2 internal runs per tile, and a run left external only when its
+    tile is full; all other entries are external (-1)."""
+    from compactlogic_amd.plan import PART_ROWS, PART_SLOTS, build_run_plan
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(0, in_dim, (2, out_dim, g_n), generator=g)
+    idx[:, ::3] = idx[:, ::3, :1]                      # some multi-slot runs
+    idx[1, ::7] = idx[0, ::7]                          # self-pairs
+    plan = build_run_plan(idx.contiguous(), in_dim)
+    pos = torch.empty(in_dim, dtype=torch.long)
+    pos[plan.row_order.long()] = torch.arange(in_dim)
+    ab = plan.run_ab.long()
+    tile_of = pos // PART_ROWS
+    ptr = plan.tile_ptr.long()
+    assert ptr.numel() == (in_dim + PART_ROWS - 1) // PART_ROWS + 1 and int(ptr[0]) == 0
+    inv_slot = plan.inv_slot.long()
+    inv_pos = plan.inv_pos.long()
+    internal = set()
+    for t in range(ptr.numel() - 1):
+        k0, k1 = int(ptr[t]), int(ptr[t + 1])
+        assert 0 <= k1 - k0 <= PART_SLOTS // 2
+        runs = plan.tile_run[k0:k1].long()
+        locs = plan.tile_loc[k0:k1].long()
+        assert runs[:, 1].tolist() == sorted(runs[:, 1].tolist())
+        used = set()
+        for (o, r, pa, pb), loc in zip(runs.tolist(), locs.tolist()):
+            a, b = ab[r].tolist()
+            assert int(plan.run_y[r]) == o and tile_of[a] == t and tile_of[b] == t
+            al, bl, sa, sb = loc & 255, (loc >> 8) & 255, (loc >> 16) & 255, (loc >> 24) & 255
+            assert pos[a] == t * PART_ROWS + al and pos[b] == t * PART_ROWS + bl
+            assert pa == int(inv_pos[2 * r]) and pb == int(inv_pos[2 * r + 1])
+            assert sa != sb and sa < PART_SLOTS and sb < PART_SLOTS and not {sa, sb} & used
+            used |= {sa, sb}
+            assert int(inv_slot[pa]) == sa and int(inv_slot[pb]) == sb
+            internal.add(r)
+        if k1 - k0 < PART_SLOTS // 2:
+            same = [r for r in range(ab.shape[0]) if tile_of[ab[r, 0]] == t == tile_of[ab[r, 1]]]
+            assert set(same) <= internal
+    ext = [r for r in range(ab.shape[0]) if r not in internal]
+    for r in ext:
+        assert int(inv_slot[inv_pos[2 * r]]) == -1 and int(inv_slot[inv_pos[2 * r + 1]]) == -1
