@@ -151,6 +151,8 @@ def train_kernel_bytes(model, batch: int) -> dict:
             out.update({"cl_dense_forward_tiled" + tag: xb + yb,
                         "cl_dense_forward_fused" + tag: xb + yb,
                         "cl_dense_backward_tiled" + tag: 2 * xb + yb,
+                        "cl_dense_backward_rows" + tag: 2 * xb + yb,
+                        "cl_dense_backward_part" + tag: 2 * xb + yb,
                         "cl_dense_weight_grad" + tag: xb + yb})
             # layout change of a [batch, in_dim] input and of its gradient: read + write
             out[f"cl_transpose[{batch}x{m.in_dim}]"] = 2 * xb

@@ -42,6 +42,8 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_forward_tiled": [_int, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "cl_dense_backward_part": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p,
                                _i64, _i64, _i64, _i64, _i64, _p],
+    "cl_dense_backward_rows": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                               _i64, _i64, _p],
     "cl_transpose": [_int, _p, _p, _i64, _i64, _p],
     "cl_dense_forward_fused": [_int, _p, _p, _int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
                                _i64, _i64, _p],

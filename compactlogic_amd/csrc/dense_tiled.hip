@@ -979,6 +979,104 @@ __global__ __launch_bounds__(256) void k_bwd_part(
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// k_bwd_rows: one wave per input row over the whole batch (lane l holds samples
+// (u * 64 + l) * VEC .. +VEC-1, u < U), for batches of at most 64 * VEC * U samples.  Every
+// gather moves a whole 64 * VEC * U-sample row segment, and the moments of a run are complete
+// inside the wave that handles its operand-a entry, so for layers of single-run neurons that
+// wave also applies the finalize (moments -> slot gradients -> softmax backward) and writes
+// the neuron's logits gradient: no moments buffer and no finalize launch.  Workgroup w (four
+// rows) takes slot block (w % 8) * nblk + w / 8, so XCD w % 8 walks one contiguous stretch of
+// the processing order, whose rows share neighbours.
+template <typename T, int VEC, int U, bool WANT_GW>
+__global__ __launch_bounds__(256) void k_bwd_rows(
+    const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
+    const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef,
+    const uint8_t* __restrict__ gs, const T* __restrict__ probs,
+    const int32_t* __restrict__ run_ptr, T* __restrict__ grad_w, T* __restrict__ gx,
+    int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, int G, int64_t nblk) {
+    using V = typename VT<T, VEC>::type;
+    using V2 = typename VT<T, 2>::type;
+    const int lane = threadIdx.x & 63;
+    const int64_t w = blockIdx.x;
+    const int64_t slot = ((w % kXcds) * nblk + w / kXcds) * 4 + wave_id();
+    if (slot >= in_dim) return;  // uniform per wave
+    const int4 sr = slot_rec[slot];
+    const int64_t row = sr.x, e0 = sr.y;
+    int64_t deg = int64_t(sr.z) - sr.y;
+    if (uint64_t(row) >= uint64_t(in_dim) || sr.y < 0 || deg < 0 || sr.z > 2 * num_runs)
+        return;  // corrupt slot record: nothing is read or written for it
+    V xi[U], acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t idx = int64_t(u * 64 + lane) * VEC;
+        acc[u] = V(T(0));
+        xi[u] = V(T(0));
+        if (WANT_GW && idx < B) xi[u] = vld<V>(x + row * B + idx);
+    }
+    bool bad = false;
+    int4 rec = make_int4(0, 0, 0, 0);
+    V2 kk = V2(T(0));
+    if (deg > 0) {
+        rec = inv_rec[e0];
+        kk = vld<V2>(inv_coef + 2 * e0);
+    }
+    for (int64_t k = 0; k < deg; ++k) {
+        const int4 cur = rec;
+        const V2 ck = kk;
+        if (k + 1 < deg) {
+            rec = inv_rec[e0 + k + 1];
+            kk = vld<V2>(inv_coef + 2 * (e0 + k + 1));
+        }
+        if (uint64_t(cur.x) >= uint64_t(out_dim) || uint64_t(cur.y) >= uint64_t(in_dim) ||
+            uint64_t(cur.z) >= uint64_t(num_runs)) {
+            bad = true;
+            continue;
+        }
+        V vo[U], vg[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = int64_t(u * 64 + lane) * VEC;
+            vo[u] = V(T(0));
+            vg[u] = V(T(0));
+            if (idx < B) {
+                vo[u] = vld<V>(x + int64_t(cur.y) * B + idx);
+                vg[u] = vld<V>(gy + int64_t(cur.x) * B + idx);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] += (ck[0] + ck[1] * vo[u]) * vg[u];
+        if (WANT_GW && cur.w == 0) {
+            T s1 = 0, s2 = 0, s3 = 0, s4 = 0;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const V ga = vg[u] * xi[u];
+                s1 += hsum<T, VEC>(vg[u]);
+                s2 += hsum<T, VEC>(ga);
+                s3 += hsum<T, VEC>(vg[u] * vo[u]);
+                s4 += hsum<T, VEC>(ga * vo[u]);
+            }
+            const T m0 = wave_total(s1), m1 = wave_total(s2);
+            const T m2 = wave_total(s3), m3 = wave_total(s4);
+            const int64_t o = cur.x;
+            const bool single = run_ptr[o] == cur.z && run_ptr[o + 1] == cur.z + 1;
+            T gp = T(0), p = T(0);
+            if (lane < G) {
+                const Coef4<T> cf = gate_coef<T>(gs[o * G + lane]);
+                gp = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
+                if (probs) p = probs[o * G + lane];
+            }
+            if (probs) gp = p * (gp - wave_total(p * gp));
+            if (lane < G) grad_w[o * G + lane] = single ? gp : nan_of<T>();
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t idx = int64_t(u * 64 + lane) * VEC;
+        if (idx < B) vst_stream<V>(gx + row * B + idx, bad ? V(nan_of<T>()) : acc[u]);
+    }
+}
+
 // k_moments: the per-chunk moments of every run, per neuron (used when grad_x is not needed).
 template <typename T, int VEC, int LPN>
 __global__ __launch_bounds__(256) void k_moments(const T* __restrict__ x, const T* __restrict__ gy,
@@ -1462,6 +1560,63 @@ extern "C" int cl_dense_backward_part(int dtype, const void* x, const void* grad
         });
     });
     return check_launch("cl_dense_backward_part");
+}
+
+extern "C" int cl_dense_backward_rows(int dtype, const void* x, const void* grad_y,
+                                      const int32_t* slot_rec, const int32_t* inv_rec,
+                                      const void* inv_coef, const uint8_t* gate_seq,
+                                      const void* probs, const int32_t* run_ptr, void* grad_w,
+                                      void* grad_x, int64_t in_dim, int64_t out_dim,
+                                      int64_t num_runs, int64_t batch, int64_t num_gates,
+                                      void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(in_dim, out_dim, batch, num_gates, num_runs)) return rc;
+    CL_ARG(num_gates <= 64, "the row backward takes at most 64 slots, got %lld",
+           (long long)num_gates);
+    CL_ARG(grad_x, "grad_x is required");
+    if (in_dim == 0 || batch == 0) return CL_OK;
+    CL_ARG(x && grad_y && slot_rec && inv_rec && inv_coef, "null pointer argument");
+    CL_ARG(!grad_w || (gate_seq && run_ptr), "grad_w needs gate_seq and run_ptr");
+    CL_ARG(aligned(slot_rec, 16) && aligned(inv_rec, 16) && aligned(inv_coef, 8),
+           "slot_rec / inv_rec must be 16-byte aligned, inv_coef 8-byte aligned");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        constexpr int W = wide_vec<T>();
+        CL_ARG(batch % W == 0 && batch <= 64 * W * 8,
+               "the row backward needs batch %% %d == 0 and batch <= %d", W, 64 * W * 8);
+        CL_ARG(all_aligned({x, grad_y, grad_x}), "row buffers must be 16-byte aligned");
+        const int64_t nblk = ceil_div(ceil_div(in_dim, int64_t(4)), int64_t(kXcds));
+        CL_ARG(kXcds * nblk < (int64_t(1) << 31), "too many rows");
+        const unsigned grid = unsigned(kXcds * nblk);
+        auto go = [&](auto uc) {
+            constexpr int U = decltype(uc)::value;
+            auto* xs = static_cast<const T*>(x);
+            auto* gys = static_cast<const T*>(grad_y);
+            auto* srec = reinterpret_cast<const int4*>(slot_rec);
+            auto* rec = reinterpret_cast<const int4*>(inv_rec);
+            auto* ic = static_cast<const T*>(inv_coef);
+            auto* pr = static_cast<const T*>(probs);
+            auto* gw = static_cast<T*>(grad_w);
+            auto* gxs = static_cast<T*>(grad_x);
+            if (grad_w)
+                k_bwd_rows<T, W, U, true><<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq,
+                                                             pr, run_ptr, gw, gxs, in_dim,
+                                                             out_dim, num_runs, batch,
+                                                             int(num_gates), nblk);
+            else
+                k_bwd_rows<T, W, U, false><<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq,
+                                                              pr, run_ptr, gw, gxs, in_dim,
+                                                              out_dim, num_runs, batch,
+                                                              int(num_gates), nblk);
+        };
+        const int64_t per_u = 64 * W;
+        if (batch <= per_u) go(std::integral_constant<int, 1>{});
+        else if (batch <= 2 * per_u) go(std::integral_constant<int, 2>{});
+        else if (batch <= 4 * per_u) go(std::integral_constant<int, 4>{});
+        else go(std::integral_constant<int, 8>{});
+    });
+    return check_launch("cl_dense_backward_rows");
 }
 
 extern "C" int cl_dense_backward_finalize(int dtype, const void* moments, int64_t nchunks,

@@ -128,10 +128,13 @@ class LogicLayerRunsFunction(torch.autograd.Function):
     (cl_dense_backward_part: runs with both inputs in one tile read grad_y once and their
     inputs from LDS).  It reads a third fewer row bytes but its barrier-separated phases keep
     fewer loads in flight, and it measures slower than cl_dense_backward_tiled at cfg2, so it
-    is off by default."""
+    is off by default.  Layers of single-run neurons with batches of up to 2048 (fp32) take
+    both gradients from cl_dense_backward_rows (one wave per input row over the whole batch,
+    finalize inside); `row_backward = False` selects the chunked passes."""
 
     fused_forward = True
     partitioned_backward = False
+    row_backward = True
 
     @staticmethod
     def forward(ctx, x, w, gate_sequence, plan: RunPlan, softmax: bool = False):
@@ -187,7 +190,17 @@ class LogicLayerRunsFunction(torch.autograd.Function):
         stream = _dl.stream_of(x)
         batch = x.shape[1]
         with torch.cuda.device(x.device):
-            if need_x:
+            wide = 16 // x.element_size()
+            if (need_x and LogicLayerRunsFunction.row_backward and plan.single_run
+                    and plan.num_gates <= 64 and 0 < batch <= 64 * wide * 8
+                    and batch % wide == 0):
+                timing.timed(f"cl_dense_backward_rows[{plan.in_dim}->{plan.out_dim}]", lambda: _capi.call(
+                    "cl_dense_backward_rows", code, x.data_ptr(), grad_y.data_ptr(),
+                    plan.slot_rec.data_ptr(), plan.inv_rec.data_ptr(), inv_coef.data_ptr(),
+                    gate_sequence.data_ptr(), _dl.ptr(probs), plan.run_ptr.data_ptr(),
+                    _dl.ptr(grad_w), grad_x.data_ptr(), plan.in_dim, plan.out_dim,
+                    plan.num_runs, batch, plan.num_gates, stream))
+            elif need_x:
                 moments, nchunks = None, 1
                 if need_w:
                     nchunks = _chunks(x, plan.in_dim, plan.out_dim)

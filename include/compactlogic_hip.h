@@ -183,6 +183,20 @@ int cl_dense_backward_part(int dtype, const void* x, const void* grad_y, const i
                            void* grad_x, void* moments, int64_t nchunks, int64_t in_dim,
                            int64_t out_dim, int64_t num_runs, int64_t batch, void* stream);
 
+/* Input gradient (and, with grad_w, the logits gradient) with one wave per input row over the
+ * whole batch: batch % (16 / sizeof(T)) == 0 and batch <= 64 * 8 * (16 / sizeof(T)) (2048
+ * samples in fp32), at most 64 slots.  Rows, entries and coefficients as for
+ * cl_dense_backward_tiled.  The moments of a run are complete in the wave of its operand-a
+ * entry, which applies the finalize there (slot gradients from gate_seq, softmax backward
+ * when probs is not NULL) and writes grad_w[o, :] (T [out_dim, num_gates]); this requires
+ * every neuron to be a single run (run_ptr[o + 1] == run_ptr[o] + 1), and a neuron that is
+ * not gets NaN.  No moments buffer and no cl_dense_backward_finalize call. */
+int cl_dense_backward_rows(int dtype, const void* x, const void* grad_y, const int32_t* slot_rec,
+                           const int32_t* inv_rec, const void* inv_coef, const uint8_t* gate_seq,
+                           const void* probs, const int32_t* run_ptr, void* grad_w,
+                           void* grad_x, int64_t in_dim, int64_t out_dim, int64_t num_runs,
+                           int64_t batch, int64_t num_gates, void* stream);
+
 /* Weight gradient from the moments: grad_w[o, g] = (c0, c1, c2, c3)[gate_seq[o,g]] . (moments
  * of g's run summed over the chunks in chunk order); with `probs` (not NULL) followed by the
  * softmax backward, giving the gradient of the logits. */

@@ -378,3 +378,81 @@ def test_partitioned_backward_matches_untiled(device, dtype, shape):
                                **TOL[dtype])
     np.testing.assert_allclose(np_(outs[0][0]), O.dense_backward_x_direct(xn, a, b, p, gs.cpu().numpy(), gyn),
                                **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("batch,g_n,softmax", [(4, 16, True), (256, 16, True), (1024, 16, True),
+                                               (2048, 5, False), (100, 40, True), (1024, 1, False)])
+def test_row_backward_matches_chunked(device, dtype, batch, g_n, softmax):
+    """cl_dense_backward_rows (one wave per input row, finalize inside) against the chunked
+    backward + finalize: the same input and logits gradients to rounding, both against the
+    oracle, bitwise reproducible.  Batches above the row kernel's limit fall back."""
+    in_dim, out_dim = 700, 900
+    g = torch.Generator().manual_seed(batch + g_n)
+    pair = torch.randint(0, in_dim, (2, out_dim, 1), generator=g)
+    pair[1, ::9] = pair[0, ::9]                       # self-pairs
+    idx = pair.expand(2, out_dim, g_n).contiguous().to(device)
+    plan = cl.build_run_plan(idx, in_dim)
+    assert plan.single_run
+    w0 = torch.randn(out_dim, g_n, generator=g).to(device=device, dtype=dtype)
+    if not softmax:
+        w0 = torch.softmax(w0, -1)
+    gs = torch.randint(0, 16, (out_dim, g_n), generator=g).to(device=device, dtype=torch.uint8)
+    x0 = torch.rand(in_dim, batch, generator=g).to(device=device, dtype=dtype)
+    gy = (torch.rand(out_dim, batch, generator=g) - 0.5).to(device=device, dtype=dtype) / batch
+    outs = []
+    default = cl.LogicLayerRunsFunction.row_backward
+    for rows in (True, True, False):
+        cl.LogicLayerRunsFunction.row_backward = rows
+        try:
+            x = x0.clone().requires_grad_(True)
+            w = w0.clone().requires_grad_(True)
+            y = cl.LogicLayerRunsFunction.apply(x, w, gs, plan, softmax)
+            outs.append(torch.autograd.grad(y, (x, w), gy))
+        finally:
+            cl.LogicLayerRunsFunction.row_backward = default
+    for u, v in zip(outs[0], outs[1]):
+        assert torch.equal(u, v), "row backward is not bitwise deterministic"
+    tol = dict(rtol=1e-6, atol=1e-7) if dtype == torch.float32 else dict(rtol=1e-12, atol=1e-14)
+    for u, v in zip(outs[0], outs[2]):
+        torch.testing.assert_close(u, v, **tol)
+    a, b = idx[0].cpu().numpy(), idx[1].cpu().numpy()
+    p = (torch.softmax(w0.double(), -1) if softmax else w0.double()).cpu().numpy()
+    gyn, xn = gy.double().cpu().numpy(), x0.double().cpu().numpy()
+    gp = O.dense_backward_w(xn, a, b, gs.cpu().numpy(), gyn)
+    want_w = p * (gp - (p * gp).sum(1, keepdims=True)) if softmax else gp
+    np.testing.assert_allclose(np_(outs[0][1]), want_w, **TOL[dtype])
+    np.testing.assert_allclose(np_(outs[0][0]),
+                               O.dense_backward_x_direct(xn, a, b, p, gs.cpu().numpy(), gyn),
+                               **TOL[dtype])
+
+
+def test_row_backward_entry_point_checks(device):
+    """Limits are enforced, and a neuron that is not a single run gets NaN logits gradients
+    instead of a partial sum."""
+    from compactlogic_amd import _capi
+    lib = _capi.load()
+    L = make_layer(41, 30, 20, 4, 64)                  # per-slot wiring: multi-run neurons
+    D = to_dev(L, device, torch.float32)
+    plan = cl.build_run_plan(torch.stack([D["a"], D["b"]]), 30)
+    assert not plan.single_run
+    inv = torch.zeros((2 * plan.num_runs, 2), device=device)
+    gw = torch.zeros((20, 4), device=device)
+    gx = torch.empty((30, 64), device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(batch, gates=4, x=D["x"], gyv=D["gy"]):
+        return lib.cl_dense_backward_rows(0, x.data_ptr(), gyv.data_ptr(), plan.slot_rec.data_ptr(),
+                                          plan.inv_rec.data_ptr(), inv.data_ptr(),
+                                          D["gs"].data_ptr(), 0, plan.run_ptr.data_ptr(),
+                                          gw.data_ptr(), gx.data_ptr(), 30, 20, plan.num_runs,
+                                          batch, gates, stream)
+
+    assert call(64, gates=65) != 0
+    assert call(2052) != 0 and b"batch" in lib.cl_last_error()
+    assert call(62) != 0
+    assert call(64) == 0
+    torch.cuda.synchronize()
+    multi = (plan.run_ptr[1:] - plan.run_ptr[:-1]) != 1
+    assert bool(multi.any())
+    assert torch.isnan(gw[multi]).all() and not torch.isnan(gw[~multi]).any()
