@@ -35,6 +35,42 @@ __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ src, T*
     }
 }
 
+// fp32 with rows % 4 == cols % 4 == 0: 16-byte loads along the source rows (16 lanes per
+// 64-column row segment) and 16-byte stores along the destination rows, the four values of
+// a store gathered from four LDS rows.
+__global__ __launch_bounds__(256) void k_transpose_v4(const float4* __restrict__ src,
+                                                      float4* __restrict__ dst, int64_t rows,
+                                                      int64_t cols) {
+    __shared__ float tile[kTile][kTile + 1];
+    const int64_t r0 = int64_t(blockIdx.y) * kTile;
+    const int64_t c0 = int64_t(blockIdx.x) * kTile;
+    const int q = threadIdx.x & 15;   // 4-element column group
+    const int rr0 = threadIdx.x >> 4; // 0..15
+    const int64_t cols4 = cols / 4, rows4 = rows / 4;
+#pragma unroll
+    for (int i = 0; i < kTile / 16; ++i) {
+        const int rr = i * 16 + rr0;
+        const int64_t r = r0 + rr, c = c0 + 4 * q;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < rows && c < cols) v = src[r * cols4 + c / 4];
+        tile[rr][4 * q + 0] = v.x;
+        tile[rr][4 * q + 1] = v.y;
+        tile[rr][4 * q + 2] = v.z;
+        tile[rr][4 * q + 3] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kTile / 16; ++i) {
+        const int cc = i * 16 + rr0;
+        const int64_t c = c0 + cc, r = r0 + 4 * q;
+        if (c < cols && r < rows) {
+            const float4 v = make_float4(tile[4 * q + 0][cc], tile[4 * q + 1][cc],
+                                         tile[4 * q + 2][cc], tile[4 * q + 3][cc]);
+            dst[c * rows4 + r / 4] = v;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace cl
 
@@ -49,6 +85,12 @@ extern "C" int cl_transpose(int dtype, const void* src, void* dst, int64_t rows,
     CL_ARG(src != dst, "cl_transpose does not work in place");
     const int64_t gx = ceil_div(cols, int64_t(kTile)), gy = ceil_div(rows, int64_t(kTile));
     CL_ARG(gx < (int64_t(1) << 31) && gy < 65536, "matrix too large for one launch");
+    if (dtype == CL_DTYPE_F32 && rows % 4 == 0 && cols % 4 == 0 && aligned(src, 16) &&
+        aligned(dst, 16)) {
+        k_transpose_v4<<<dim3(unsigned(gx), unsigned(gy)), 256, 0, as_stream(stream)>>>(
+            static_cast<const float4*>(src), static_cast<float4*>(dst), rows, cols);
+        return check_launch("cl_transpose");
+    }
     CL_DTYPE_SWITCH(dtype, {
         k_transpose<scalar_t><<<dim3(unsigned(gx), unsigned(gy)), 256, 0, as_stream(stream)>>>(
             static_cast<const scalar_t*>(src), static_cast<scalar_t*>(dst), rows, cols);
