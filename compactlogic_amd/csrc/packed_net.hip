@@ -147,39 +147,117 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net(const uint32_t* __re
 // inputs, 16 bits each, and the opcode) in registers for the whole launch, so the gate
 // tables are read once per workgroup instead of once per column, and each workgroup walks a
 // range of columns, loading the next column's input words while it evaluates the current one.
-constexpr int kRegGateCap = 80;
+constexpr int kSlotCap = 80;  // gate slots per thread (registers)
 
-struct RegNet {
-    int total;                   // gate slots per thread over all layers
-    uint8_t layer_of[kRegGateCap];
-    uint8_t index_of[kRegGateCap];  // slot i of its layer: gate row tid + 1024 i
-};
+// Bit-sliced addition of the partner lane's number to this lane's: a += partner(a), W words
+// (word i holds bit i of 32 counts), the sum fitting in W bits.  Each word is fetched from
+// the partner inside the carry loop: all lanes fetch word i before any lane updates it, so
+// one temporary register suffices.
+template <int CTRL, int W>
+__device__ __forceinline__ void bs_add_dpp(uint32_t (&a)[W]) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+        const uint32_t x = a[i], y = dpp_move<CTRL>(x);
+        a[i] = x ^ y ^ c;
+        c = (x & y) | (c & (x | y));
+    }
+}
 
-template <int NB, int TG, int IPT>
-__global__ __launch_bounds__(kNetThreads) void k_packed_net_regs(
+template <int W>
+__device__ __forceinline__ void bs_add_xor(uint32_t (&a)[W], int d) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+        const uint32_t x = a[i], y = uint32_t(__shfl_xor(int(x), d, 64));
+        a[i] = x ^ y ^ c;
+        c = (x & y) | (c & (x | y));
+    }
+}
+
+// Class counts of one column, one wave per class: lane l adds rows l, l + 64, ... of the
+// class into (W - 6)-bit vertical counters, six butterfly steps of bit-sliced addition (DPP
+// inside each 16-lane row, then lane shuffles across rows) leave the class total of all 32
+// samples in every lane as W bit planes, and lane s < 32 reads off the count of sample s.
+// Requires gs <= 2^W - 64 (per-lane counts fit W - 6 bits, the total W bits).  Integer sums:
+// exact and independent of the order.
+template <int W>
+__device__ __forceinline__ void column_counts_wave(const uint32_t* last, const PackedNet& net,
+                                                   int64_t col, int64_t nsamples,
+                                                   int32_t* __restrict__ counts) {
+    constexpr int LW = W - 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gs = net.rows[net.num_layers] / net.k;
+    for (int c = wave; c < net.k; c += kNetThreads / 64) {  // uniform per wave
+        uint32_t a[W];
+#pragma unroll
+        for (int i = 0; i < W; ++i) a[i] = 0;
+#pragma unroll 1
+        for (int r = c * gs + lane; r < (c + 1) * gs; r += 64) {
+            // add one row's bits into the low LW words (per-lane counts stay below 2^LW)
+            uint32_t x = last[r];
+#pragma unroll
+            for (int i = 0; i < LW; ++i) {
+                const uint32_t carry = a[i] & x;
+                a[i] ^= x;
+                x = carry;
+            }
+        }
+        bs_add_dpp<0xB1>(a);   // quad_perm [1,0,3,2]
+        bs_add_dpp<0x4E>(a);   // quad_perm [2,3,0,1]
+        bs_add_dpp<0x124>(a);  // row_ror:4
+        bs_add_dpp<0x128>(a);  // row_ror:8
+        bs_add_xor<W>(a, 16);
+        bs_add_xor<W>(a, 32);
+        if (lane < 32) {
+            int32_t n = 0;
+#pragma unroll
+            for (int i = 0; i < W; ++i) n |= int32_t((a[i] >> lane) & 1u) << i;
+            const int64_t sample = col * 32 + lane;
+            if (sample < nsamples) counts[sample * net.k + c] = n;
+        }
+    }
+}
+
+// k_packed_net_slots: persistent workgroups (columns col, col + gridDim/8, ... on XCD
+// blockIdx % 8, a contiguous range of columns per XCD) with the gate tables in registers.
+// Every layer owns J slots of a thread: slot q = l * J + j is gate row tid + 1024 j of layer
+// l, so the layer of a slot, its output row and the LDS buffer it reads (l even: the first,
+// odd: the second) are compile-time constants.  A layer issues the 2J row reads of its gates
+// before computing them, then writes the J outputs, then meets the barrier.  Gate entry in a
+// register: byte offset of row a | that of row b << 16 (rows < 16384); opcodes as nibbles.
+// Slots past a layer's width hold entry 0: they read row 0 and write rows at or beyond the
+// width, which no later step reads (each buffer spans at least 1024 J words), so no slot
+// needs a branch.
+#ifndef CL_NET_BATCH
+#define CL_NET_BATCH 4
+#endif
+constexpr int kBatch = CL_NET_BATCH;  // gates whose row reads are in flight together
+
+template <int CW, int J, int IPT>
+__global__ __launch_bounds__(kNetThreads) void k_packed_net_slots(
     const uint32_t* __restrict__ x, int64_t cols, int64_t nsamples,
-    const uint64_t* __restrict__ tables, PackedNet net, RegNet rn,
-    int32_t* __restrict__ counts, int buf_words) {
+    const uint64_t* __restrict__ tables, PackedNet net, int32_t* __restrict__ counts,
+    int buf_words) {
+    constexpr int LMAX = kSlotCap / J < kNetMaxLayers ? kSlotCap / J : kNetMaxLayers;
+    constexpr int TG = LMAX * J;
     extern __shared__ __align__(16) uint32_t lds[];
     const int tid = threadIdx.x;
+    const int L = net.num_layers;
     uint32_t ent[TG];
     uint32_t ops[(TG + 7) / 8];
 #pragma unroll
     for (int i = 0; i < (TG + 7) / 8; ++i) ops[i] = 0;
-#pragma clang loop unroll(full)
+#pragma unroll
     for (int q = 0; q < TG; ++q) {
-        ent[q] = 0xffffffffu;  // no gate in this slot
-        if (q < rn.total) {
-            const int l = rn.layer_of[q];
-            const int o = tid + kNetThreads * int(rn.index_of[q]);
-            if (o < net.rows[l + 1]) {
-                const uint64_t e = tables[net.table_off[l] + o];
-                ent[q] = (uint32_t(e) & 0xffffu) | (__builtin_amdgcn_ubfe(uint32_t(e >> 20), 0, 16) << 16);
-                ops[q / 8] |= __builtin_amdgcn_ubfe(uint32_t(e >> 32), 8, 4) << (4 * (q % 8));
-            }
+        const int l = q / J, o = tid + kNetThreads * (q % J);
+        ent[q] = 0;  // no gate in this slot: reads row 0, writes past the layer's rows
+        if (l < L && o < net.rows[l + 1]) {
+            const uint64_t e = tables[net.table_off[l] + o];
+            ent[q] = (uint32_t(e) & 0xffffu) | (__builtin_amdgcn_ubfe(uint32_t(e >> 20), 0, 16) << 16);
+            ops[q / 8] |= __builtin_amdgcn_ubfe(uint32_t(e >> 32), 8, 4) << (4 * (q % 8));
         }
     }
-    // columns of this workgroup: XCD x = blockIdx % 8 walks a contiguous range of columns
     const int64_t per = (cols + 7) / 8;
     const int64_t nb8 = gridDim.x / 8;
     const int64_t c_first = (blockIdx.x % 8) * per + blockIdx.x / 8;
@@ -193,84 +271,50 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net_regs(
         }
     };
     fetch(c_first);
-    const int rows = net.rows[net.num_layers];
-    const int gs = rows / net.k;
-    const int S = net.slices;
-    const int pairs = 32 * net.k;
-    const int P = std::max(1, kNetThreads / pairs);
     for (int64_t col = c_first; col < c_end; col += nb8) {
-        uint32_t* buf0 = lds;
-        uint32_t* buf1 = lds + buf_words;
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const int r = tid + kNetThreads * j;
-            if (r < net.rows[0]) buf0[r] = in[j];
+            if (r < net.rows[0]) lds[r] = in[j];
         }
         fetch(col + nb8);
         __syncthreads();
-        int layer = 0;
-        const uint32_t* cur = buf0;
-        uint32_t* nxt = buf1;
-        // Opaque copy of the opcodes: keeps the compiler from hoisting the per-gate truth-table
-        // masks out of the column loop (they would need 4 registers per gate).
-        uint32_t opv[(TG + 7) / 8];
+        // The gate entries and opcode words are made opaque for every column: keeps the
+        // compiler from hoisting per-gate values derived from them (the two LDS addresses,
+        // the four truth-table masks) out of the column loop, which would need up to six more
+        // registers per gate.
 #pragma unroll
-        for (int i = 0; i < (TG + 7) / 8; ++i) {
-            opv[i] = ops[i];
-            asm volatile("" : "+v"(opv[i]));
-        }
-#pragma clang loop unroll(full)
-        for (int q = 0; q < TG; ++q) {
-            const bool slot = q < rn.total;        // uniform
-            if (slot && rn.layer_of[q] != layer) { // uniform: next layer
+        for (int i = 0; i < (TG + 7) / 8; ++i) asm volatile("" : "+v"(ops[i]));
+#pragma unroll
+        for (int q = 0; q < TG; ++q) asm volatile("" : "+v"(ent[q]));
+#pragma unroll
+        for (int l = 0; l < LMAX; ++l) {
+            if (l < L) {  // uniform
+                const unsigned char* cur =
+                    reinterpret_cast<const unsigned char*>(lds + (l & 1) * buf_words);
+                uint32_t* nxt = lds + ((l + 1) & 1) * buf_words;
+                // the row reads of kBatch gates are issued together, then the gates computed
+#pragma unroll
+                for (int j0 = 0; j0 < J; j0 += kBatch) {
+                    uint32_t va[kBatch], vb[kBatch];
+#pragma unroll
+                    for (int j = j0; j < j0 + kBatch && j < J; ++j) {
+                        const uint32_t e = ent[l * J + j];
+                        va[j - j0] = *reinterpret_cast<const uint32_t*>(cur + (e & 0xffffu));
+                        vb[j - j0] = *reinterpret_cast<const uint32_t*>(cur + (e >> 16));
+                    }
+#pragma unroll
+                    for (int j = j0; j < j0 + kBatch && j < J; ++j) {
+                        const int q = l * J + j;
+                        nxt[tid + kNetThreads * j] = gate_word(
+                            (ops[q / 8] >> (4 * (q % 8))) & 15u, va[j - j0], vb[j - j0]);
+                    }
+                }
                 __syncthreads();
-                layer = rn.layer_of[q];
-                const uint32_t* t = cur;
-                cur = nxt;
-                nxt = const_cast<uint32_t*>(t);
-            }
-            const uint32_t e = ent[q];
-            if (slot && e != 0xffffffffu) {
-                const unsigned char* src = reinterpret_cast<const unsigned char*>(cur);
-                const uint32_t a = *reinterpret_cast<const uint32_t*>(src + (e & 0xffffu));
-                const uint32_t b = *reinterpret_cast<const uint32_t*>(src + (e >> 16));
-                nxt[tid + kNetThreads * int(rn.index_of[q])] =
-                    gate_word((opv[q / 8] >> (4 * (q % 8))) & 15u, a, b);
             }
         }
-        __syncthreads();
-        // nxt now holds the last layer's rows; the other buffer takes the counters
-        const uint32_t* last = nxt;
-        uint32_t* vc = const_cast<uint32_t*>(cur);
-        int32_t* part = reinterpret_cast<int32_t*>(vc + net.k * S * NB);
-        if (tid < net.k * S) {
-            const int c = tid / S, j = tid % S;
-            uint32_t v[NB];
-#pragma unroll
-            for (int b = 0; b < NB; ++b) v[b] = 0;
-            for (int r = c * gs + j; r < (c + 1) * gs; r += S) add_vertical<NB>(v, last[r]);
-#pragma unroll
-            for (int b = 0; b < NB; ++b) vc[tid * NB + b] = v[b];
-        }
-        __syncthreads();
-        if (tid < pairs * P) {
-            const int i = tid % pairs, p = tid / pairs;
-            const int smp = i / net.k, c = i % net.k;
-            int32_t n = 0;
-            for (int j = p; j < S; j += P) {
-                const uint32_t* vv = vc + (c * S + j) * NB;
-#pragma unroll
-                for (int b = 0; b < NB; ++b) n += int32_t((vv[b] >> smp) & 1u) << b;
-            }
-            part[p * pairs + i] = n;
-        }
-        __syncthreads();
-        for (int i = tid; i < pairs; i += kNetThreads) {
-            int32_t n = 0;
-            for (int p = 0; p < P; ++p) n += part[p * pairs + i];
-            const int64_t sample = col * 32 + i / net.k;
-            if (sample < nsamples) counts[sample * net.k + i % net.k] = n;
-        }
+        // the last layer's rows are in buffer L % 2
+        column_counts_wave<CW>(lds + (L & 1) * buf_words, net, col, nsamples, counts);
         __syncthreads();  // the next column overwrites both buffers
     }
 }
@@ -330,8 +374,8 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
     const int pairs = 32 * int(k);
     const int P = std::max(1, kNetThreads / pairs);
     const int count_words = int(k) * S * NB + P * pairs;
-    const int buf_words = std::max(max_rows, count_words);
-    const size_t lds = size_t(2) * buf_words * 4;
+    int buf_words = std::max(max_rows, count_words);
+    size_t lds = size_t(2) * buf_words * 4;
     CL_ARG(lds <= 160 * 1024, "activations do not fit in LDS");
     const int64_t cols = row_bytes / 4;
     if (nsamples == 0 || cols == 0) return CL_OK;
@@ -340,24 +384,21 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
     const int64_t blocks = 8 * ceil_div(cols, 8);
     CL_ARG(blocks < (int64_t(1) << 31), "too many columns");
     int rc = CL_OK;
-    // persistent register-table variant when it applies
-    int total = 0;
-    RegNet rn{};
-    bool regs = max_rows <= 16383 && net.rows[0] <= 4 * kNetThreads;
-    for (int l = 0; regs && l < num_layers; ++l) {
-        const int n = int(ceil_div(net.rows[l + 1], kNetThreads));
-        if (total + n > kRegGateCap) {
-            regs = false;
+    // persistent slot-table variant when it applies: J slots of 1024 rows per layer
+    int J = int(ceil_div(int64_t(*std::max_element(net.rows + 1, net.rows + num_layers + 1)),
+                         int64_t(kNetThreads)));
+    for (int cand : {1, 2, 4, 8, 12, 16}) {
+        if (J <= cand) {
+            J = cand;
             break;
         }
-        for (int i = 0; i < n; ++i) {
-            rn.layer_of[total] = uint8_t(l);
-            rn.index_of[total] = uint8_t(i);
-            ++total;
-        }
     }
-    rn.total = total;
-    if (regs && !kNetDisableRegs) {
+    const bool slots = max_rows <= 16383 && net.rows[0] <= 4 * kNetThreads && J <= 16 &&
+                       num_layers <= std::min(kSlotCap / J, kNetMaxLayers);
+    if (slots && !kNetDisableRegs) {
+        // every slot writes: a buffer spans the J * 1024 rows a thread's slots can address
+        buf_words = std::max(buf_words, J * kNetThreads);
+        lds = size_t(2) * buf_words * 4;
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
@@ -366,9 +407,9 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
         }
         const int64_t want = std::max<int64_t>(8, (int64_t(cus) / 8) * 8);
         const int64_t pblocks = std::min<int64_t>(want, 8 * ceil_div(cols, 8));
-        auto go = [&](auto nb, auto tg, auto ipt) {
-            auto* kern = &k_packed_net_regs<decltype(nb)::value, decltype(tg)::value,
-                                            decltype(ipt)::value>;
+        auto go = [&](auto nb, auto jc, auto ipt) {
+            auto* kern = &k_packed_net_slots<decltype(nb)::value, decltype(jc)::value,
+                                             decltype(ipt)::value>;
             if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) !=
                 hipSuccess) {
@@ -377,23 +418,28 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
                 return;
             }
             kern<<<unsigned(pblocks), kNetThreads, lds, as_stream(stream)>>>(
-                static_cast<const uint32_t*>(x), cols, nsamples, tables, net, rn, counts,
-                buf_words);
+                static_cast<const uint32_t*>(x), cols, nsamples, tables, net, counts, buf_words);
         };
-        auto by_tg = [&](auto nb, auto ipt) {
-            if (total <= 16) go(nb, std::integral_constant<int, 16>(), ipt);
-            else if (total <= 32) go(nb, std::integral_constant<int, 32>(), ipt);
-            else if (total <= 48) go(nb, std::integral_constant<int, 48>(), ipt);
-            else if (total <= 64) go(nb, std::integral_constant<int, 64>(), ipt);
-            else go(nb, std::integral_constant<int, kRegGateCap>(), ipt);
+        auto by_j = [&](auto nb, auto ipt) {
+            using std::integral_constant;
+            switch (J) {
+                case 1: go(nb, integral_constant<int, 1>(), ipt); break;
+                case 2: go(nb, integral_constant<int, 2>(), ipt); break;
+                case 4: go(nb, integral_constant<int, 4>(), ipt); break;
+                case 8: go(nb, integral_constant<int, 8>(), ipt); break;
+                case 12: go(nb, integral_constant<int, 12>(), ipt); break;
+                default: go(nb, integral_constant<int, 16>(), ipt); break;
+            }
         };
         auto by_ipt = [&](auto nb) {
-            if (net.rows[0] <= kNetThreads) by_tg(nb, std::integral_constant<int, 1>());
-            else by_tg(nb, std::integral_constant<int, 4>());
+            if (net.rows[0] <= kNetThreads) by_j(nb, std::integral_constant<int, 1>());
+            else by_j(nb, std::integral_constant<int, 4>());
         };
-        if (NB == 4) by_ipt(std::integral_constant<int, 4>());
-        else if (NB == 8) by_ipt(std::integral_constant<int, 8>());
-        else by_ipt(std::integral_constant<int, kMaxCountBits>());
+        // count width: gs <= 2^CW - 64
+        if (gs <= 192) by_ipt(std::integral_constant<int, 8>());
+        else if (gs <= 960) by_ipt(std::integral_constant<int, 10>());
+        else if (gs <= 4032) by_ipt(std::integral_constant<int, 12>());
+        else by_ipt(std::integral_constant<int, 15>());
         if (rc) return rc;
         return check_launch("cl_packed_network");
     }

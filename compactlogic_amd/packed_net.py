@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _capi
@@ -24,16 +25,101 @@ def _limits():
     return nl.value, rows.value
 
 
+# LDS geometry of gfx950 as the fused kernel uses it: rows are 32-bit words, bank = word % 64,
+# and a read instruction is served 32 lanes at a time; the lanes of one half-wave read the
+# rows of 32 consecutive positions of the layer being computed.
+_LDS_BANKS = 64
+_HALF_WAVE = 32
+
+
+def bank_aware_positions(pos_a: np.ndarray, pos_b: np.ndarray, rows: int) -> np.ndarray:
+    """Positions (LDS words, a permutation of 0..rows-1) for the gates of one layer whose
+    inputs sit at words pos_a / pos_b of the previous layer, chosen so that the gates of each
+    block of 32 consecutive positions (one half-wave of the kernel's row reads) read their a
+    rows from 32 distinct banks and their b rows from 32 distinct banks.  The gate-to-position
+    assignment is free because the next layer addresses rows through the tables; a greedy
+    first fit (gates in a fixed order, blocks in order) colours the (bank a, bank b) multigraph
+    with blocks.  A gate that fits no block conflict-free goes to the open block with the
+    fewest clashes.  Deterministic."""
+    n = int(rows)
+    blocks = (n + _HALF_WAVE - 1) // _HALF_WAVE
+    cap = np.full(blocks, _HALF_WAVE, dtype=np.int64)
+    cap[-1] = n - (blocks - 1) * _HALF_WAVE
+    fill = np.zeros(blocks, dtype=np.int64)
+    used_a = np.zeros((_LDS_BANKS, blocks), dtype=bool)
+    used_b = np.zeros((_LDS_BANKS, blocks), dtype=bool)
+    ka = (np.asarray(pos_a) % _LDS_BANKS).astype(np.int64)
+    kb = (np.asarray(pos_b) % _LDS_BANKS).astype(np.int64)
+    pos = np.empty(n, dtype=np.int64)
+    open_ = np.ones(blocks, dtype=bool)
+    for o in range(n):
+        ok = open_ & ~used_a[ka[o]] & ~used_b[kb[o]]
+        blk = int(ok.argmax())
+        if not ok[blk]:
+            clash = used_a[ka[o]].astype(np.int64) + used_b[kb[o]]
+            clash[~open_] = 3
+            blk = int(clash.argmin())
+        used_a[ka[o], blk] = True
+        used_b[kb[o], blk] = True
+        pos[o] = blk * _HALF_WAVE + fill[blk]
+        fill[blk] += 1
+        if fill[blk] == cap[blk]:
+            open_[blk] = False
+    return pos
+
+
+def bank_aware_positions_grouped(pos_a: np.ndarray, pos_b: np.ndarray, rows: int,
+                                 group_size: int) -> np.ndarray:
+    """bank_aware_positions for the last layer, whose rows must stay in their class: gate o
+    (class o // group_size) is placed inside [class * group_size, (class + 1) * group_size),
+    in the first block overlapping that range that has a free position there and both banks
+    free (else the one with the fewest clashes).  Deterministic."""
+    n, gsz = int(rows), int(group_size)
+    blocks = (n + _HALF_WAVE - 1) // _HALF_WAVE
+    used_a = np.zeros((_LDS_BANKS, blocks), dtype=bool)
+    used_b = np.zeros((_LDS_BANKS, blocks), dtype=bool)
+    ka = (np.asarray(pos_a) % _LDS_BANKS).astype(np.int64)
+    kb = (np.asarray(pos_b) % _LDS_BANKS).astype(np.int64)
+    taken = np.zeros(n, dtype=bool)
+    pos = np.empty(n, dtype=np.int64)
+    for c in range(n // gsz):
+        lo, hi = c * gsz, (c + 1) * gsz
+        blks = np.arange(lo // _HALF_WAVE, (hi - 1) // _HALF_WAVE + 1)
+        # free positions of the class inside each of its blocks
+        first = np.maximum(blks * _HALF_WAVE, lo)
+        last = np.minimum(blks * _HALF_WAVE + _HALF_WAVE, hi)
+        room = last - first
+        for o in range(lo, hi):
+            open_ = room > 0
+            ok = open_ & ~used_a[ka[o], blks] & ~used_b[kb[o], blks]
+            i = int(ok.argmax())
+            if not ok[i]:
+                clash = used_a[ka[o], blks].astype(np.int64) + used_b[kb[o], blks]
+                clash[~open_] = 3
+                i = int(clash.argmin())
+            blk = int(blks[i])
+            used_a[ka[o], blk] = True
+            used_b[kb[o], blk] = True
+            p = int(first[i]) + int(np.argmin(taken[first[i]:last[i]]))
+            taken[p] = True
+            pos[o] = p
+            room[i] -= 1
+    return pos
+
+
 class PackedNetwork:
     """Fused packed evaluator of `model`: LogicLayers (frozen or in eval mode; each neuron uses
     its argmax slot `w`) followed by a GroupSum.  Call it with a PackBitsTensor of the first
     layer's input (or its [features, words] tensor) to get int32 class counts [samples, k].
 
     Widths are limited by LDS: every layer at most cl_packed_network_limits()'s row count.  The
-    gate tables are built once here; rebuild after changing the model.
+    gate tables are built once here; rebuild after changing the model.  With `bank_aware`
+    (default), each hidden layer's rows are laid out in LDS by bank_aware_positions, so that
+    the row reads of the kernel's half-waves hit distinct LDS banks; the counts do not depend
+    on the layout.
     """
 
-    def __init__(self, model):
+    def __init__(self, model, bank_aware: bool = True):
         mods = list(model)
         if not mods or not isinstance(mods[-1], GroupSum):
             raise ValueError("the network must end with a GroupSum")
@@ -56,7 +142,8 @@ class PackedNetwork:
                              "but it is not")
         entries = []
         with torch.no_grad():
-            for m in layers:
+            prev_pos = np.arange(self.rows[0], dtype=np.int64)   # input rows stay in place
+            for i, m in enumerate(layers):
                 w = getattr(m, "w", None)
                 if w is None:
                     w = m.weights.argmax(-1)
@@ -67,7 +154,18 @@ class PackedNetwork:
                 if int(a.min()) < 0 or int(a.max()) >= m.in_dim or int(b.min()) < 0 or \
                         int(b.max()) >= m.in_dim:
                     raise IndexError("connection indices out of range")
-                entries.append((a * 4) | ((b * 4) << 20) | (g << 40))
+                pa = prev_pos[a.cpu().numpy()]
+                pb = prev_pos[b.cpu().numpy()]
+                if not bank_aware:
+                    pos = np.arange(m.out_dim, dtype=np.int64)
+                elif i + 1 < len(layers):
+                    pos = bank_aware_positions(pa, pb, m.out_dim)
+                else:  # class groups stay contiguous
+                    pos = bank_aware_positions_grouped(pa, pb, m.out_dim, m.out_dim // self.k)
+                ent = np.empty(m.out_dim, dtype=np.int64)
+                ent[pos] = (pa * 4) | ((pb * 4) << 20) | (g.cpu().numpy() << 40)
+                entries.append(torch.as_tensor(ent, device=a.device))
+                prev_pos = pos
         self.tables = torch.cat(entries).contiguous()
         self.device = self.tables.device
         self._rows_host = (ctypes.c_int64 * len(self.rows))(*self.rows)

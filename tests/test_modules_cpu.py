@@ -353,3 +353,57 @@ def test_run_plan_tiles(in_dim, out_dim, g_n, seed):
     ext = [r for r in range(ab.shape[0]) if r not in internal]
     for r in ext:
         assert int(inv_slot[inv_pos[2 * r]]) == -1 and int(inv_slot[inv_pos[2 * r + 1]]) == -1
+
+
+@pytest.mark.parametrize("rows,seed", [(12000, 0), (1000, 1), (47, 2), (32, 3)])
+def test_bank_aware_positions(rows, seed):
+    """The fused packed layout is a permutation of the layer's rows whose blocks of 32
+    consecutive positions read their a rows and their b rows from distinct LDS banks (word %
+    64) far more often than the identity layout does."""
+    from compactlogic_amd.packed_net import bank_aware_positions
+    rng = np.random.default_rng(seed)
+    pa = rng.integers(0, 5 * rows, rows)
+    pb = rng.integers(0, 5 * rows, rows)
+    pb[::5] = pa[::5]
+    pos = bank_aware_positions(pa, pb, rows)
+    assert sorted(pos.tolist()) == list(range(rows))
+
+    def clashes(p):
+        n = 0
+        for blk in range(int(p.max()) // 32 + 1):
+            m = p // 32 == blk
+            for k in (pa[m] % 64, pb[m] % 64):
+                n += len(k) - len(set(k.tolist()))
+        return n
+
+    # few blocks leave the placement little choice; with many it removes nearly all clashes
+    assert clashes(pos) <= clashes(np.arange(rows))
+    if rows >= 1000:
+        assert clashes(np.arange(rows)) > 10 * max(1, clashes(pos))
+
+
+@pytest.mark.parametrize("rows,k", [(12000, 10), (1500, 10), (96, 3), (100, 4)])
+def test_bank_aware_positions_grouped(rows, k):
+    """The last layer's layout keeps every gate inside its class range, is a permutation, and
+    has fewer bank clashes than the identity layout."""
+    from compactlogic_amd.packed_net import bank_aware_positions_grouped
+    rng = np.random.default_rng(rows + k)
+    pa = rng.integers(0, 3 * rows, rows)
+    pb = rng.integers(0, 3 * rows, rows)
+    pos = bank_aware_positions_grouped(pa, pb, rows, rows // k)
+    assert sorted(pos.tolist()) == list(range(rows))
+    gs = rows // k
+    assert all(o // gs == p // gs for o, p in enumerate(pos.tolist()))
+
+    def clashes(p):
+        n = 0
+        for blk in range(int(p.max()) // 32 + 1):
+            m = p // 32 == blk
+            for kk in (pa[m] % 64, pb[m] % 64):
+                n += len(kk) - len(set(kk.tolist()))
+        return n
+
+    # a class spans few blocks, so the choice is narrower than for hidden layers
+    assert clashes(pos) <= clashes(np.arange(rows))
+    if rows >= 1000:
+        assert clashes(np.arange(rows)) > 3 * max(1, clashes(pos))

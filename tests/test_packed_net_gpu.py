@@ -85,3 +85,17 @@ def test_packed_network_word_widths_and_errors(device):
         cl.PackedNetwork(wide)                                          # too wide for LDS
     with pytest.raises(RuntimeError):
         cl.PackedNetwork(model)(torch.zeros((31, 4), dtype=torch.int64, device=device))
+
+
+def test_bank_aware_layout_gives_the_same_counts(device):
+    """The LDS layout of the hidden layers changes where rows live, never the counts."""
+    dims = [(300, 2000), (2000, 3000), (3000, 1500)]
+    model = frozen_net(dims, 10, 16, 5, device)
+    n = 2048
+    rng = np.random.default_rng(5)
+    bits = rng.integers(0, 2, (n, 300)).astype(bool)
+    x = cl.PackBitsTensor(torch.as_tensor(bits, device=device), 64)
+    a = cl.PackedNetwork(model)(x)
+    b = cl.PackedNetwork(model, bank_aware=False)(x)
+    assert torch.equal(a, b)
+    assert np.array_equal(np_(a), oracle_counts(model, np_(x.t).view(np.uint64), n))
