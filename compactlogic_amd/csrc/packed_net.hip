@@ -153,22 +153,23 @@ constexpr int kSlotCap = 80;  // gate slots per thread (registers)
 // (word i holds bit i of 32 counts), the sum fitting in W bits.  Each word is fetched from
 // the partner inside the carry loop: all lanes fetch word i before any lane updates it, so
 // one temporary register suffices.
-template <int CTRL, int W>
+// Only the low N words can be non-zero in either addend (N <= W).
+template <int CTRL, int N, int W>
 __device__ __forceinline__ void bs_add_dpp(uint32_t (&a)[W]) {
     uint32_t c = 0;
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
+    for (int i = 0; i < N; ++i) {
         const uint32_t x = a[i], y = dpp_move<CTRL>(x);
         a[i] = x ^ y ^ c;
         c = (x & y) | (c & (x | y));
     }
 }
 
-template <int W>
+template <int N, int W>
 __device__ __forceinline__ void bs_add_xor(uint32_t (&a)[W], int d) {
     uint32_t c = 0;
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
+    for (int i = 0; i < N; ++i) {
         const uint32_t x = a[i], y = uint32_t(__shfl_xor(int(x), d, 64));
         a[i] = x ^ y ^ c;
         c = (x & y) | (c & (x | y));
@@ -203,12 +204,14 @@ __device__ __forceinline__ void column_counts_wave(const uint32_t* last, const P
                 x = carry;
             }
         }
-        bs_add_dpp<0xB1>(a);   // quad_perm [1,0,3,2]
-        bs_add_dpp<0x4E>(a);   // quad_perm [2,3,0,1]
-        bs_add_dpp<0x124>(a);  // row_ror:4
-        bs_add_dpp<0x128>(a);  // row_ror:8
-        bs_add_xor<W>(a, 16);
-        bs_add_xor<W>(a, 32);
+        // after step k the sums have at most LW + k bits: each step carries one word further
+        constexpr auto n = [](int k) { return LW + k < W ? LW + k : W; };
+        bs_add_dpp<0xB1, n(1)>(a);   // quad_perm [1,0,3,2]
+        bs_add_dpp<0x4E, n(2)>(a);   // quad_perm [2,3,0,1]
+        bs_add_dpp<0x124, n(3)>(a);  // row_ror:4
+        bs_add_dpp<0x128, n(4)>(a);  // row_ror:8
+        bs_add_xor<n(5)>(a, 16);
+        bs_add_xor<n(6)>(a, 32);
         if (lane < 32) {
             int32_t n = 0;
 #pragma unroll
