@@ -58,7 +58,7 @@ SIGNATURES: dict[str, list] = {
     "cl_conv_backward_w": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64] + [_i64] * 9 + [_p],
     "cl_conv_backward_w_workspace": [_int] + [_i64] * 9 + [ctypes.POINTER(_i64)],
     "cl_conv_backward_x": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p] + [_i64] * 9 + [_p],
-    "cl_eval_packed_indexed": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "cl_eval_packed_indexed": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_conv_window_coef_width": [_i64, ctypes.POINTER(_i64)],
     "cl_conv_window_prep": [_int, _p, _int, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "cl_conv_window_forward": [_int, _p, _p, _p, _p, _p] + [_i64] * 11 + [_p],

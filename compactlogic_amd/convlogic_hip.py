@@ -236,13 +236,18 @@ def eval(x, offsets_ch, offsets_h, offsets_w, w, gate_seq, stride, pad, ks):  # 
     return y
 
 
-def eval_packed_indexed(x, ia, ib, gate):
-    """Packed layer from index tables (int32, -1 = zero row): y[o] = op(x[ia[o]], x[ib[o]])."""
+def eval_packed_indexed(x, ia, ib, gate, order=None):
+    """Packed layer from index tables (int32, -1 = zero row): y[o] = op(x[ia[o]], x[ib[o]]).
+    `order` (int32, a permutation of the output rows) is the order the rows are evaluated in."""
     for t, nm in ((x, "x"), (ia, "ia"), (ib, "ib"), (gate, "gate")):
         _check(t, nm)
     out_dim = ia.numel()
+    if order is not None:
+        _check(order, "order")
+        if order.dtype != torch.int32 or order.numel() != out_dim:
+            raise RuntimeError("order must be int32 with one entry per output row")
     y = torch.empty((out_dim, x.shape[1]), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_eval_packed_indexed", ptr(x), ptr(ia), ptr(ib), ptr(gate), ptr(y),
-                   x.shape[0], out_dim, x.shape[1] * x.element_size(), stream_of(x))
+        _capi.call("cl_eval_packed_indexed", ptr(x), ptr(ia), ptr(ib), ptr(gate), ptr(order),
+                   ptr(y), x.shape[0], out_dim, x.shape[1] * x.element_size(), stream_of(x))
     return y

@@ -244,10 +244,13 @@ __global__ __launch_bounds__(256) void k_eval_packed_idx(const V* __restrict__ x
                                                          const int32_t* __restrict__ ia,
                                                          const int32_t* __restrict__ ib,
                                                          const uint8_t* __restrict__ gate,
+                                                         const int32_t* __restrict__ order,
                                                          V* __restrict__ y, int64_t in_dim,
                                                          int64_t out_dim, int64_t elems) {
-    const int64_t o = int64_t(blockIdx.x) * 4 + wave_id();
-    if (o >= out_dim) return;
+    const int64_t i = int64_t(blockIdx.x) * 4 + wave_id();
+    if (i >= out_dim) return;
+    const int64_t o = order ? int64_t(order[i]) : i;
+    if (uint64_t(o) >= uint64_t(out_dim)) return;  // corrupt order entry: nothing is written
     const int64_t a = ia[o], b = ib[o];
     const int g = gate[o] & 15;
     const bool bad = a >= in_dim || b >= in_dim;
@@ -266,20 +269,21 @@ __global__ __launch_bounds__(256) void k_eval_packed_idx(const V* __restrict__ x
             if (!bad && b >= 0) vb = x[b * elems + e];
             V r = (~va & ~vb & m00) | (~va & vb & m01) | (va & ~vb & m10) | (va & vb & m11);
             if (bad) r = zero;
-            y[o * elems + e] = r;
+            // written once, read by the next layer only: bypass the caches
+            __builtin_nontemporal_store(r, y + o * elems + e);
         }
     }
 }
 
 template <typename V>
 int launch_eval_packed_idx(const void* x, const int32_t* ia, const int32_t* ib,
-                           const uint8_t* gate, void* y, int64_t in_dim, int64_t out_dim,
-                           int64_t row_bytes, hipStream_t s) {
+                           const uint8_t* gate, const int32_t* order, void* y, int64_t in_dim,
+                           int64_t out_dim, int64_t row_bytes, hipStream_t s) {
     constexpr int U = 4;
     const int64_t elems = row_bytes / int64_t(sizeof(V));
     CL_ARG(ceil_div(elems, 64 * U) < 65536, "packed rows too long for one launch");
     const dim3 grid(unsigned(ceil_div(out_dim, 4)), unsigned(ceil_div(elems, 64 * U)), 1);
-    k_eval_packed_idx<V, U><<<grid, 256, 0, s>>>(static_cast<const V*>(x), ia, ib, gate,
+    k_eval_packed_idx<V, U><<<grid, 256, 0, s>>>(static_cast<const V*>(x), ia, ib, gate, order,
                                                  static_cast<V*>(y), in_dim, out_dim, elems);
     return CL_OK;
 }
@@ -438,8 +442,9 @@ extern "C" int cl_conv_backward_x(int dtype, const void* x, const int32_t* offse
 }
 
 extern "C" int cl_eval_packed_indexed(const void* x, const int32_t* ia, const int32_t* ib,
-                                      const uint8_t* gate, void* y, int64_t in_dim,
-                                      int64_t out_dim, int64_t row_bytes, void* stream) {
+                                      const uint8_t* gate, const int32_t* order, void* y,
+                                      int64_t in_dim, int64_t out_dim, int64_t row_bytes,
+                                      void* stream) {
     clear_error();
     CL_ARG(in_dim >= 0 && out_dim >= 0 && row_bytes >= 0, "negative shape");
     if (out_dim == 0 || row_bytes == 0) return CL_OK;
@@ -449,13 +454,13 @@ extern "C" int cl_eval_packed_indexed(const void* x, const int32_t* ia, const in
     hipStream_t s = as_stream(stream);
     int rc;
     if (row_bytes % 16 == 0 && aligned(x, 16) && aligned(y, 16))
-        rc = launch_eval_packed_idx<U4>(x, ia, ib, gate, y, in_dim, out_dim, row_bytes, s);
+        rc = launch_eval_packed_idx<U4>(x, ia, ib, gate, order, y, in_dim, out_dim, row_bytes, s);
     else if (row_bytes % 8 == 0 && aligned(x, 8) && aligned(y, 8))
-        rc = launch_eval_packed_idx<uint64_t>(x, ia, ib, gate, y, in_dim, out_dim, row_bytes, s);
+        rc = launch_eval_packed_idx<uint64_t>(x, ia, ib, gate, order, y, in_dim, out_dim, row_bytes, s);
     else if (row_bytes % 4 == 0 && aligned(x, 4) && aligned(y, 4))
-        rc = launch_eval_packed_idx<uint32_t>(x, ia, ib, gate, y, in_dim, out_dim, row_bytes, s);
+        rc = launch_eval_packed_idx<uint32_t>(x, ia, ib, gate, order, y, in_dim, out_dim, row_bytes, s);
     else
-        rc = launch_eval_packed_idx<uint8_t>(x, ia, ib, gate, y, in_dim, out_dim, row_bytes, s);
+        rc = launch_eval_packed_idx<uint8_t>(x, ia, ib, gate, order, y, in_dim, out_dim, row_bytes, s);
     if (rc) return rc;
     return check_launch("cl_eval_packed_indexed");
 }

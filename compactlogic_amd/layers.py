@@ -758,6 +758,7 @@ class ConvLayer(LogicLayer):
         super().__init__(self.in_dim, self.out_dim, **kwargs)
         self._packed_key = None
         self._packed_tables = None
+        self._packed_order = None
 
     def forward_cuda(self, x):
         """x [N, c_in, h, w] -> [N, c_out, h_out, w_out] (:598-626)."""
@@ -797,9 +798,10 @@ class ConvLayer(LogicLayer):
             w = self.weights.argmax(-1).to(dtype=torch.uint8, device=self.weights.device)
         if isinstance(x, PackBitsTensor):
             ia, ib, gate = self.packed_tables(w)
+            order = self.packed_order(w)
             assert x.t.shape[0] == int(np.prod(self.in_shape)), (x.t.shape, self.in_shape)
             x.t = timing.timed(f"cl_eval_packed_indexed[{x.t.shape[0]}->{ia.numel()}]",
-                               lambda: _cl.eval_packed_indexed(x.t, ia, ib, gate))
+                               lambda: _cl.eval_packed_indexed(x.t, ia, ib, gate, order))
             return x
         return _cl.eval(x.contiguous(), self.offsets_ch, self.offsets_h, self.offsets_w, w,
                         self.gate_sequence, self.stride, self.padding, self.ks)
@@ -831,8 +833,27 @@ class ConvLayer(LogicLayer):
         gate = (self.gate_sequence[rows, slot].view(-1, 1)
                 .expand(self.c_out, self.h_out * self.w_out).reshape(-1).contiguous())
         self._packed_tables = (tables[0], tables[1], gate)
+        self._packed_order = None
         self._packed_key = key
         return self._packed_tables
+
+    def packed_order(self, w: torch.Tensor) -> torch.Tensor:
+        """Order in which the packed kernel evaluates the output features (int32): the output
+        channels sorted by the input channel of their winner slot's first tap, each channel's
+        positions in order.  The channels reading one input channel then run together, and
+        the rows of that channel they all gather stay cache resident.  Cached with the
+        tables."""
+        self.packed_tables(w)
+        if self._packed_order is None:
+            dev = w.device
+            rows = torch.arange(self.c_out, device=dev)
+            ch = self.offsets_ch[0, rows, w.to(torch.long)].to(torch.long)
+            chans = torch.sort(ch * self.c_out + rows).values % self.c_out
+            hw = self.h_out * self.w_out
+            pos = torch.arange(hw, device=dev)
+            self._packed_order = (chans.view(-1, 1) * hw + pos.view(1, -1)).reshape(-1) \
+                .to(torch.int32).contiguous()
+        return self._packed_order
 
     def get_connections(self, device='cuda'):
         """Sample the two taps of every slot (:642-699), in the reference's draw order."""

@@ -318,10 +318,12 @@ int cl_conv_window_finalize(int dtype, const void* moments, int64_t nq, const ui
  * (ch * H + y) * W + x, compiler/extract.py:101-102):
  * y[o, :] = op_{gate[o]}(x[ia[o], :], x[ib[o], :]); a negative index reads zeros (a tap
  * outside the input plane).  Any row_bytes; 16-byte rows at 16-byte aligned bases stream as
- * 16-byte vectors. */
+ * 16-byte vectors.  order (int32 [out_dim], may be NULL = identity) is the processing order:
+ * the i-th row evaluated is output row order[i], so rows that read the same input rows can
+ * be evaluated together; every output row must appear once. */
 int cl_eval_packed_indexed(const void* x, const int32_t* ia, const int32_t* ib,
-                           const uint8_t* gate, void* y, int64_t in_dim, int64_t out_dim,
-                           int64_t row_bytes, void* stream);
+                           const uint8_t* gate, const int32_t* order, void* y, int64_t in_dim,
+                           int64_t out_dim, int64_t row_bytes, void* stream);
 
 /* -------------------------------------------------------------------------------------------
  * GroupSum -- compactlogic/compactlogic.py:450-468: out[n, c] = sum_{j in group c} x[n, j] / tau

@@ -281,6 +281,12 @@ def test_eval_packed_indexed_widths(device, nbytes):
     xw = np.concatenate([xb, np.zeros((in_dim, pad), np.uint8)], 1).view(np.uint64)
     ref = P.eval_layer(xw, ia, ib, g).view(np.uint8)[:, :nbytes]
     np.testing.assert_array_equal(np_(y), ref)
+    # any processing order gives the same rows
+    order = torch.as_tensor(rng.permutation(out_dim).astype(np.int32), device=device)
+    y2 = cv.eval_packed_indexed(torch.as_tensor(xb, device=device), torch.as_tensor(ia, device=device),
+                                torch.as_tensor(ib, device=device), torch.as_tensor(g, device=device),
+                                order)
+    assert torch.equal(y, y2)
 
 
 def test_cfg5_network_slice_bit_exact(device):

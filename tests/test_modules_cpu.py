@@ -407,3 +407,18 @@ def test_bank_aware_positions_grouped(rows, k):
     assert clashes(pos) <= clashes(np.arange(rows))
     if rows >= 1000:
         assert clashes(np.arange(rows)) > 3 * max(1, clashes(pos))
+
+
+def test_conv_packed_order_groups_channels_by_input():
+    """The packed evaluation order is a permutation of the output features that visits the
+    output channels in order of the input channel their winner slot reads."""
+    torch.manual_seed(3)
+    layer = cl.ConvLayer((6, 8, 8), padding=1, c_out=20, ks=3, stride=2, num_chn=1)
+    layer.freeze()
+    order = layer.packed_order(layer.w).long()
+    hw = layer.h_out * layer.w_out
+    assert sorted(order.tolist()) == list(range(20 * hw))
+    chans = order.view(20, hw)[:, 0] // hw
+    assert torch.equal(order.view(20, hw) - (chans * hw).view(-1, 1), torch.arange(hw).expand(20, hw))
+    src = layer.offsets_ch[0, chans, layer.w.long()[chans]]
+    assert bool((src[1:] >= src[:-1]).all())
