@@ -458,6 +458,13 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
     return check_launch("cl_conv_window_backward_x");
 }
 
+#ifndef CL_WIN_BLOCKS
+#define CL_WIN_BLOCKS 1536
+#endif
+#ifndef CL_WIN_MIN_ITERS
+#define CL_WIN_MIN_ITERS 8
+#endif
+
 extern "C" int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t hw,
                                      int64_t* nq) {
     clear_error();
@@ -465,8 +472,8 @@ extern "C" int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, 
     // about 1536 blocks (two rounds of resident blocks), but at least 8 (sample, position)
     // elements per thread so that the closing reduction stays small against the loop
     const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
-    const int64_t want = ceil_div(1536, Cin * nsub);
-    const int64_t most = N * hw / (256 * 8);
+    const int64_t want = ceil_div(CL_WIN_BLOCKS, Cin * nsub);
+    const int64_t most = N * hw / (256 * CL_WIN_MIN_ITERS);
     *nq = std::max<int64_t>(1, std::min<int64_t>(std::min(want, most), std::max<int64_t>(N, 1)));
     return CL_OK;
 }

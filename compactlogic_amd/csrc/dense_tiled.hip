@@ -661,6 +661,79 @@ __global__ __launch_bounds__(256) void k_wgrad_full(const T* __restrict__ x, con
     }
 }
 
+// k_wgrad_rows: the same with one wave per neuron over the whole batch (lane l holds samples
+// (u * 64 + l) * VEC .. +VEC-1, u < U), for batches of at most 64 * VEC * U samples and at
+// most 64 slots (lane g owns slot g).  grad_y of the neuron is loaded once for all its runs;
+// each run's moments are wave totals, so no partial sums leave the wave.
+template <typename T, int VEC, int U>
+__global__ __launch_bounds__(256) void k_wgrad_rows(const T* __restrict__ x,
+                                                    const T* __restrict__ gy,
+                                                    const uint8_t* __restrict__ gs,
+                                                    const T* __restrict__ probs,
+                                                    const int32_t* __restrict__ run_ptr,
+                                                    const int2* __restrict__ run_ab,
+                                                    const int32_t* __restrict__ run_gl,
+                                                    T* __restrict__ grad_w, int64_t in_dim,
+                                                    int64_t out_dim, int64_t num_runs, int64_t B,
+                                                    int G) {
+    using V = typename VT<T, VEC>::type;
+    const int lane = threadIdx.x & 63;
+    const int64_t o = int64_t(blockIdx.x) * 4 + wave_id();
+    if (o >= out_dim) return;  // uniform per wave
+    // the run range first, so that the grad_y row and the first run's rows load together
+    bool bad = false;
+    int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
+    if (r0 < 0 || r1 < r0 || r1 > num_runs) {
+        bad = true;
+        r1 = r0;
+    }
+    V vg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t idx = int64_t(u * 64 + lane) * VEC;
+        vg[u] = idx < B ? vld<V>(gy + o * B + idx) : V(T(0));
+    }
+    T s1 = 0;
+    T gp = T(0), m0 = T(0);
+    for (int64_t r = r0; r < r1; ++r) {
+        const int2 ab = run_ab[r];
+        const int gl = run_gl[r];
+        const int g0 = gl & 0xff, g1 = g0 + (gl >> 8);
+        if (uint32_t(ab.x) >= uint64_t(in_dim) || uint32_t(ab.y) >= uint64_t(in_dim)) {
+            bad = true;
+            continue;
+        }
+        T s2 = 0, s3 = 0, s4 = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = int64_t(u * 64 + lane) * VEC;
+            if (idx < B) {
+                const V va = vld<V>(x + int64_t(ab.x) * B + idx);
+                const V vb = vld<V>(x + int64_t(ab.y) * B + idx);
+                const V ga = vg[u] * va;
+                s2 += hsum<T, VEC>(ga);
+                s3 += hsum<T, VEC>(vg[u] * vb);
+                s4 += hsum<T, VEC>(ga * vb);
+            }
+        }
+        if (r == r0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) s1 += hsum<T, VEC>(vg[u]);
+            m0 = wave_total(s1);
+        }
+        const T m1 = wave_total(s2), m2 = wave_total(s3), m3 = wave_total(s4);
+        if (lane >= g0 && lane < g1 && lane < G) {
+            const Coef4<T> cf = gate_coef<T>(gs[o * G + lane]);
+            gp = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
+        }
+    }
+    if (probs) {
+        const T p = lane < G ? probs[o * G + lane] : T(0);
+        gp = p * (gp - wave_total(p * gp));
+    }
+    if (lane < G) grad_w[o * G + lane] = bad ? nan_of<T>() : gp;
+}
+
 // ------------------------------------------------------------------------------------------
 // k_bwd_tiled: LPN lanes per input-row segment, NPG rows per lane group.  Rows are taken in
 // processing-slot order (descending entry count, so the rows of a group and the groups of a
@@ -1404,7 +1477,19 @@ extern "C" int cl_dense_weight_grad(int dtype, const void* x, const void* grad_y
         auto* pr = static_cast<const T*>(probs);
         auto* ab = reinterpret_cast<const int2*>(run_ab);
         auto* gw = static_cast<T*>(grad_w);
-        if (v)
+        if (v && num_gates <= 64 && batch <= 64 * W * 8) {
+            const unsigned wgrid = unsigned(ceil_div(out_dim, int64_t(4)));
+            auto go = [&](auto uc) {
+                k_wgrad_rows<T, W, decltype(uc)::value><<<wgrid, 256, 0, s>>>(
+                    xs, gys, gate_seq, pr, run_ptr, ab, run_gl, gw, std::max<int64_t>(in_dim, 1),
+                    out_dim, num_runs, batch, int(num_gates));
+            };
+            const int64_t per_u = 64 * W;
+            if (batch <= per_u) go(std::integral_constant<int, 1>{});
+            else if (batch <= 2 * per_u) go(std::integral_constant<int, 2>{});
+            else if (batch <= 4 * per_u) go(std::integral_constant<int, 4>{});
+            else go(std::integral_constant<int, 8>{});
+        } else if (v)
             k_wgrad_full<T, W><<<grid, 256, 0, s>>>(xs, gys, gate_seq, pr, run_ptr, ab, run_gl, gw,
                                                    std::max<int64_t>(in_dim, 1), out_dim, num_runs,
                                                    batch, int(num_gates));
