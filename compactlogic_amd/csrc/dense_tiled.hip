@@ -420,6 +420,7 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
         }
     V va[NPG], vb[NPG];
     bool ok[NPG];
+    int2 ipos[NPG];
 #pragma unroll
     for (int j = 0; j < NPG; ++j) {
         ok[j] = obase + j < out_dim && rec[j].z >= 0 && rec[j].w == rec[j].z + 1 &&
@@ -431,6 +432,10 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
             va[j] = vld<V>(x + int64_t(rec[j].x) * B + idx);
             vb[j] = vld<V>(x + int64_t(rec[j].y) * B + idx);
         }
+        // entry positions of the run's two sides, loaded with the rows by the writer chunk
+        ipos[j] = make_int2(-1, -1);
+        if (writer && inv_coef && ok[j] && l == 0)
+            ipos[j] = make_int2(inv_pos[2 * int64_t(rec[j].z)], inv_pos[2 * int64_t(rec[j].z) + 1]);
     }
 #pragma unroll
     for (int j = 0; j < NPG; ++j) {
@@ -476,8 +481,7 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
                     if (l + LPN * m < G) probs[o * G + l + LPN * m] = p[j][m];
             }
             if (inv_coef && ok[j] && l == 0) {
-                const int64_t r = rec[j].z;
-                const int64_t pa = inv_pos[2 * r], pb = inv_pos[2 * r + 1];
+                const int64_t pa = ipos[j].x, pb = ipos[j].y;
                 if (uint64_t(pa) < uint64_t(2 * num_runs)) {
                     inv_coef[2 * pa + 0] = k1;
                     inv_coef[2 * pa + 1] = k3;
@@ -693,6 +697,9 @@ __global__ __launch_bounds__(256) void k_wgrad_rows(const T* __restrict__ x,
         const int64_t idx = int64_t(u * 64 + lane) * VEC;
         vg[u] = idx < B ? vld<V>(gy + o * B + idx) : V(T(0));
     }
+    // the slot's opcode and probability are loaded with the rows, not after the moments
+    const int code = lane < G ? gs[o * G + lane] : 0;
+    const T p = (probs && lane < G) ? probs[o * G + lane] : T(0);
     T s1 = 0;
     T gp = T(0), m0 = T(0);
     for (int64_t r = r0; r < r1; ++r) {
@@ -723,14 +730,11 @@ __global__ __launch_bounds__(256) void k_wgrad_rows(const T* __restrict__ x,
         }
         const T m1 = wave_total(s2), m2 = wave_total(s3), m3 = wave_total(s4);
         if (lane >= g0 && lane < g1 && lane < G) {
-            const Coef4<T> cf = gate_coef<T>(gs[o * G + lane]);
+            const Coef4<T> cf = gate_coef<T>(code);
             gp = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
         }
     }
-    if (probs) {
-        const T p = lane < G ? probs[o * G + lane] : T(0);
-        gp = p * (gp - wave_total(p * gp));
-    }
+    if (probs) gp = p * (gp - wave_total(p * gp));
     if (lane < G) grad_w[o * G + lane] = bad ? nan_of<T>() : gp;
 }
 
@@ -1117,9 +1121,21 @@ __global__ __launch_bounds__(256) void k_bwd_rows(
                 vg[u] = vld<V>(gy + int64_t(cur.x) * B + idx);
             }
         }
+        // the finalize's per-neuron data is loaded with the rows, not after the moments
+        const bool fin = WANT_GW && cur.w == 0;
+        int rp0 = 0, rp1 = 0, code = 0;
+        T p = T(0);
+        if (fin) {
+            rp0 = run_ptr[cur.x];
+            rp1 = run_ptr[cur.x + 1];
+            if (lane < G) {
+                code = gs[int64_t(cur.x) * G + lane];
+                if (probs) p = probs[int64_t(cur.x) * G + lane];
+            }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) acc[u] += (ck[0] + ck[1] * vo[u]) * vg[u];
-        if (WANT_GW && cur.w == 0) {
+        if (fin) {
             T s1 = 0, s2 = 0, s3 = 0, s4 = 0;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -1132,12 +1148,11 @@ __global__ __launch_bounds__(256) void k_bwd_rows(
             const T m0 = wave_total(s1), m1 = wave_total(s2);
             const T m2 = wave_total(s3), m3 = wave_total(s4);
             const int64_t o = cur.x;
-            const bool single = run_ptr[o] == cur.z && run_ptr[o + 1] == cur.z + 1;
-            T gp = T(0), p = T(0);
+            const bool single = rp0 == cur.z && rp1 == cur.z + 1;
+            T gp = T(0);
             if (lane < G) {
-                const Coef4<T> cf = gate_coef<T>(gs[o * G + lane]);
+                const Coef4<T> cf = gate_coef<T>(code);
                 gp = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
-                if (probs) p = probs[o * G + lane];
             }
             if (probs) gp = p * (gp - wave_total(p * gp));
             if (lane < G) grad_w[o * G + lane] = single ? gp : nan_of<T>();
