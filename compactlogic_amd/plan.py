@@ -11,8 +11,9 @@ row i lists the (run, operand side) uses of input i, encoded as 2 * run + side. 
 within a row are in ascending (side, run) order, so the result is deterministic.  Each entry
 also has a ready record (neuron, other input, run, side) so the kernel needs no second
 lookup, `inv_pos` maps a run side to its entry (where the per-step coefficients are written),
-and `row_order` is the processing order of the inputs: depth-first over the graph whose
-edges are the runs, so that consecutive inputs are mostly joined by runs.  `nab` and
+and `row_order` is the processing order of the inputs: a depth-first preorder over the graph
+whose edges are the runs (small subtrees first), so that inputs joined by runs are mostly
+close together.  `nab` and
 `slot_rec` hold, per neuron and per processing slot, what a kernel needs before its first
 gather (first run's pair and run range; input row and entry range), so each is one load away.
 
@@ -63,15 +64,11 @@ class RunPlan:
         return int(self.run_gl.numel())
 
 
-def locality_order(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor,
-                   in_dim: int) -> torch.Tensor:
-    """Processing order of the inputs for the input-gradient pass: depth-first preorder over
-    the graph whose edges are the runs (a, b), inputs of degree 0 last.  A depth-first order
-    keeps the inputs joined by runs next to each other (a subtree occupies consecutive
-    positions), so most runs have both inputs in the same tile of consecutive inputs.
-    Deterministic: each search starts from the highest-degree unvisited input (lowest index
-    on ties) and follows the neighbours in entry order."""
-    dev = ra.device
+def dfs_forest(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor, in_dim: int):
+    """Depth-first spanning forest of the graph whose edges are the runs (a, b): returns
+    (roots, parent, children) as Python lists, parent[v] = -1 for a root and -2 for an input of
+    degree 0.  Each search starts from the highest-degree unvisited input (lowest index on
+    ties) and follows the neighbours in entry order; children are listed in discovery order."""
     a = ra.cpu().numpy().astype(np.int64)
     b = rb.cpu().numpy().astype(np.int64)
     deg = degree.cpu().numpy().astype(np.int64)
@@ -81,22 +78,65 @@ def locality_order(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor,
     ptr = np.zeros(in_dim + 1, dtype=np.int64)
     np.cumsum(np.bincount(src, minlength=in_dim), out=ptr[1:])
     ptr = ptr.tolist()
-    seen = (deg == 0).tolist()
-    out = []
-    for start in np.argsort(-deg, kind="stable").tolist():
-        if seen[start]:
+    parent = [-2] * in_dim
+    children = [[] for _ in range(in_dim)]
+    roots = []
+    for s in np.argsort(-deg, kind="stable").tolist():
+        if parent[s] != -2 or deg[s] == 0:
             continue
-        stack = [start]
+        parent[s] = -1
+        roots.append(s)
+        stack = [[s, ptr[s]]]
+        while stack:
+            top = stack[-1]
+            u, i = top
+            if i < ptr[u + 1]:
+                top[1] = i + 1
+                v = nbr[i]
+                if parent[v] == -2:
+                    parent[v] = u
+                    children[u].append(v)
+                    stack.append([v, ptr[v]])
+            else:
+                stack.pop()
+    return roots, parent, children
+
+
+def locality_order(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor,
+                   in_dim: int) -> torch.Tensor:
+    """Processing order of the inputs for the input-gradient pass: preorder of the depth-first
+    spanning forest of the run graph (dfs_forest), in which the children of every input are
+    visited in increasing order of their subtree sizes (equal sizes in discovery order);
+    inputs of degree 0 last.
+
+    A subtree occupies consecutive positions, so a run between a parent and its child spans
+    only the subtrees of the child's smaller siblings; visiting the small subtrees first keeps
+    that span short for every child, and with it the time between the two reads of the
+    run's grad_y row and of the shared input rows.  Deterministic."""
+    dev = ra.device
+    roots, parent, children = dfs_forest(ra, rb, degree, in_dim)
+    size = [1] * in_dim
+    # a parent is discovered before its children, so reversed discovery (preorder) order
+    # visits every child before its parent
+    pre = []
+    for r in roots:
+        stack = [r]
         while stack:
             u = stack.pop()
-            if seen[u]:
-                continue
-            seen[u] = True
+            pre.append(u)
+            stack.extend(children[u])
+    for u in reversed(pre):
+        if parent[u] >= 0:
+            size[parent[u]] += size[u]
+    out = []
+    for r in roots:
+        stack = [r]
+        while stack:
+            u = stack.pop()
             out.append(u)
-            # reversed, so that the first neighbour in entry order is visited first
-            for v in reversed(nbr[ptr[u]:ptr[u + 1]]):
-                if not seen[v]:
-                    stack.append(v)
+            ch = sorted(children[u], key=lambda v: size[v])   # stable: discovery order on ties
+            stack.extend(reversed(ch))
+    deg = degree.cpu().numpy()
     out.extend(np.nonzero(deg == 0)[0].tolist())
     return torch.as_tensor(np.asarray(out, dtype=np.int64), dtype=torch.int64, device=dev)
 

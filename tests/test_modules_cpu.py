@@ -267,10 +267,10 @@ def test_conv_inverse_index_cache_follows_tensors():
 
 
 def test_run_plan_processing_order():
-    """row_order is a depth-first preorder of the run graph: a permutation of the inputs with
-    every input of degree 0 last, in which each input after the first of a search has an
-    earlier neighbour (depth-first: its parent); slot_rec follows it."""
-    from compactlogic_amd.plan import build_run_plan
+    """row_order is the preorder of a depth-first spanning forest of the run graph with every
+    input's children visited smallest subtree first, inputs of degree 0 last; slot_rec
+    follows it."""
+    from compactlogic_amd.plan import build_run_plan, dfs_forest
     g = torch.Generator().manual_seed(11)
     in_dim, out_dim = 3000, 1600
     pair = torch.randint(0, in_dim, (2, out_dim, 1), generator=g).expand(2, out_dim, 16)
@@ -281,27 +281,45 @@ def test_run_plan_processing_order():
     d = deg[order]
     nz = int((deg > 0).sum())
     assert bool((d[nz:] == 0).all()) and bool((d[:nz] > 0).all())
-    # depth-first: the input right after u is a neighbour of u, or the search backtracked to
-    # a neighbour of an earlier input, or a new search started (no visited neighbour at all)
     ab = plan.run_ab.long()
+    roots, parent, children = dfs_forest(ab[:, 0], ab[:, 1], deg, in_dim)
     nbrs = [set() for _ in range(in_dim)]
     for x, y in ab.tolist():
         nbrs[x].add(y)
         nbrs[y].add(x)
-    seen = set()
-    starts = 0
-    for k, u in enumerate(order[:nz].tolist()):
-        if k and order[k - 1].item() in nbrs[u]:
-            pass
-        elif nbrs[u] & seen:
-            pass
-        else:
-            starts += 1
-            # a new search starts at an input of maximal degree among the unvisited ones
-            rest = [v for v in range(in_dim) if v not in seen and deg[v] > 0]
-            assert deg[u] == max(deg[v] for v in rest)
-        seen.add(u)
-    assert starts < nz // 4
+    # a spanning forest of the inputs of nonzero degree, each edge to a neighbour
+    assert sorted(v for v in range(in_dim) if parent[v] != -2) == sorted(
+        v for v in range(in_dim) if deg[v] > 0)
+    assert all(parent[v] in nbrs[v] for v in range(in_dim) if parent[v] >= 0)
+    assert [r for r in range(in_dim) if parent[r] == -1] == sorted(roots)
+    # depth-first: every run joins an input to one of its ancestors (no cross edges)
+    def ancestors(v):
+        out = set()
+        while parent[v] >= 0:
+            v = parent[v]
+            out.add(v)
+        return out
+    anc = [ancestors(v) if parent[v] != -2 else set() for v in range(in_dim)]
+    for x, y in ab.tolist():
+        assert x == y or x in anc[y] or y in anc[x]
+    # preorder with smallest subtrees first: the subtree of u is the block of size(u)
+    # positions starting at u, and its children's blocks follow in increasing size
+    pos = torch.empty(in_dim, dtype=torch.long)
+    pos[order] = torch.arange(in_dim)
+    size = [1] * in_dim
+    for v in sorted(range(in_dim), key=lambda v: -len(anc[v])):
+        if parent[v] >= 0:
+            size[parent[v]] += size[v]
+    for u in range(in_dim):
+        if parent[u] == -2:
+            continue
+        nxt = int(pos[u]) + 1
+        for c in sorted(children[u], key=lambda c: int(pos[c])):
+            assert int(pos[c]) == nxt
+            nxt += size[c]
+        sizes = [size[c] for c in sorted(children[u], key=lambda c: int(pos[c]))]
+        assert sizes == sorted(sizes)
+    assert len(roots) < nz // 4
     rec = plan.slot_rec.long()
     assert torch.equal(rec[:, 0], order)
     assert torch.equal(rec[:, 1], plan.inv_ptr.long()[order])
