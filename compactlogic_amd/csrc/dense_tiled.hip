@@ -135,13 +135,15 @@ __host__ __device__ __forceinline__ int64_t tile_grid(const TileMap& m) {
 #endif
 
 __device__ __forceinline__ bool map_tile(const TileMap& m, int64_t w, int64_t& c, int64_t& t) {
+    // grids stay below 2^32 workgroups and tile counts below 2^31: 32-bit divisions
+    const uint32_t nt = uint32_t(m.ntiles);
     if (m.nchunks >= kXcds) {
-        const int64_t x = w % kXcds, j = w / kXcds;
-        c = x + kXcds * (j / m.ntiles);
-        t = j % m.ntiles;
+        const uint32_t x = uint32_t(w) % kXcds, j = uint32_t(w) / kXcds;
+        c = x + kXcds * int64_t(j / nt);
+        t = j % nt;
     } else {
-        c = w / m.ntiles;
-        t = w % m.ntiles;
+        c = uint32_t(w) / nt;
+        t = uint32_t(w) % nt;
     }
 #if CL_TILE_ROTATE
     // Chunk c starts its tile sweep at a different row band, so the XCDs working on different
@@ -402,7 +404,7 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
     const int l = threadIdx.x % LPN;
     const int64_t idx = c * (LPN * VEC) + int64_t(l) * VEC;
     const bool col = idx < B;
-    const bool writer = c == t % tm.nchunks;
+    const bool writer = uint32_t(c) == uint32_t(t) % uint32_t(tm.nchunks);
     int4 rec[NPG];
 #pragma unroll
     for (int j = 0; j < NPG; ++j)
