@@ -13,11 +13,14 @@ from .packed_net import PackedNetwork
 from .plan import RunPlan, build_run_plan
 from .schedules import (EntropyRowResampler, FixedSequentialEntropyFreezer,
                         SequentialEntropyFreezer)
+from .treelogic import (ConvLogicFunction, ConvLogicLayer, FullConvLogicFunction,
+                        PoolLogicLayer, TreeLogicFunction, TreeLogicLayer)
 
 __all__ = [
     "LogicLayer", "GroupSum", "LogicLayerCudaFunction", "LogicLayerRunsFunction",
     "GroupSumFunction", "PackBitsTensor", "RunPlan", "build_run_plan", "difflogic_hip",
     "ConvLayer", "ConvLayerCudaFunction", "ConvLayerSoftmaxFunction", "ConvLayerWindowFunction",
     "convlogic_hip", "SequentialEntropyFreezer", "FixedSequentialEntropyFreezer",
-    "EntropyRowResampler", "PackedNetwork",
+    "EntropyRowResampler", "PackedNetwork", "ConvLogicLayer", "TreeLogicLayer", "PoolLogicLayer",
+    "ConvLogicFunction", "FullConvLogicFunction", "TreeLogicFunction",
 ]

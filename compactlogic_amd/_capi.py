@@ -45,6 +45,17 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_backward_rows": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
                                _i64, _i64, _p],
     "cl_transpose": [_int, _p, _p, _i64, _i64, _p],
+    "cl_tree_conv_forward": [_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int, _int,
+                             _int, _int, _int, _int, _p, _p, _p, _p, _p],
+    "cl_tree_conv_workspace": [_int, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int,
+                               _int, _int, _p],
+    "cl_tree_conv_backward": [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                              _int, _int, _int, _int, _int, _int, _int, _p, _p, _p, _i64, _p],
+    "cl_tree_level_forward": [_int, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
+    "cl_tree_level_workspace": [_int, _i64, _i64, _i64, _i64, _p],
+    "cl_tree_level_backward": [_int, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
+    "cl_tree_conv_eval_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _int, _int, _int, _int,
+                                 _int, _int, _int, _p, _p],
     "cl_dense_forward_fused": [_int, _p, _p, _int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
                                _i64, _i64, _p],
     "cl_dense_weight_grad": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,

@@ -1,0 +1,802 @@
+// Logic-tree convolution block (ConvLogic): third_party/convlogic_source_code/src/convlogic/
+// convlogic_layer.py:85-360 (ConvLogicLayer, forward_python_full :236-321), treelogic_layer.py:
+// 33-130 (TreeLogicLayer), cuda/full_convlogic_kernel.cu:10-701, cuda/convlogic_kernel.cu,
+// cuda/treelogic_kernel.cu.
+//
+// Per output channel c and conv position (oy, ox), eight taps selection[c][k] =
+// ch << 16 | row << 8 | col read x[n, ch, oy*sh + row - ph, ox*sw + col - pw] (0 outside the
+// image).  Nodes 0..3 are relaxed gates on the tap pairs (2q, 2q + 1).  The complete block adds
+// node 4 on the outputs of nodes (0, 1), node 5 on (2, 3), node 6 on (4, 5), and a 2x2 / stride 2
+// max pool in which the first maximum in row-major window order wins (strict >).
+//
+// Every node's 16 probabilities w_prob[c][q][:] collapse to the four coefficients of
+// K0 + K1 a + K2 b + K3 a b (the multilinear form of the gate mixture), so a node costs one
+// evaluation whatever the mixture.
+//
+// Backward (all deterministic, no float atomics in global memory):
+//   k_tree_nodes   per (sample, channel, pooled window): recompute the winner position's
+//                  taps and nodes, propagate grad_y to the four conv gates (stored for the input
+//                  gradient) and form the node moments (sum gy a b, gy a, gy b, gy); each
+//                  workgroup reduces its items in a fixed order into one partial per channel;
+//   k_tree_gather  per (sample, group of input channels): the input gradient accumulated in
+//                  LDS.  Each lane group walks the (channel, tap) uses of one input channel in
+//                  a fixed order; within one use the positions are distinct (a tap offset maps
+//                  positions one to one), so every LDS word receives its additions in a fixed
+//                  order and the result is bitwise reproducible;
+//   k_tree_finalize  partials summed in block order, moments -> gradient of every probability.
+#include "common.h"
+
+namespace cl {
+namespace {
+
+constexpr int kTaps = 8;
+constexpr int kMaxNodes = 7;
+
+template <typename T>
+__device__ __forceinline__ T quiet_nan() {
+    return T(__builtin_nan(""));
+}
+
+struct TreeDims {
+    int n, cin, h, w, cout, ho, wo, sh, sw, ph, pw;
+    int complete;
+    int P;  // items per (sample, channel): pooled windows (complete) or conv positions
+};
+
+// Decoded tap: channel, row and column offset relative to the output position (pad removed).
+struct TapOff {
+    int ch, dy, dx;
+};
+
+__device__ __forceinline__ TapOff decode_tap(int32_t s, int ph, int pw) {
+    TapOff t;
+    t.ch = (s >> 16) & 0xFFFF;
+    t.dy = ((s >> 8) & 0xFF) - ph;
+    t.dx = (s & 0xFF) - pw;
+    return t;
+}
+
+template <typename T>
+__device__ __forceinline__ T tap_value(const T* __restrict__ xn, const TreeDims& d, const TapOff& t,
+                                       int oy, int ox) {
+    const int iy = oy * d.sh + t.dy, ix = ox * d.sw + t.dx;
+    if (iy < 0 || iy >= d.h || ix < 0 || ix >= d.w || t.ch >= d.cin) return T(0);
+    return xn[(int64_t(t.ch) * d.h + iy) * d.w + ix];
+}
+
+template <typename T>
+__device__ __forceinline__ T node(const T* k, T a, T b) {
+    return fma(k[3], a * b, fma(k[2], b, fma(k[1], a, k[0])));
+}
+
+// Collapse w_prob[c][q][:] for q < nodes into sk[q][0..3]; taps of channel c into st.  Called by
+// the whole workgroup, followed by a barrier.
+template <typename T>
+__device__ __forceinline__ void load_channel(const T* __restrict__ w_prob,
+                                             const int32_t* __restrict__ sel, int c, int nodes,
+                                             const TreeDims& d, T (*sk)[4], TapOff* st,
+                                             int* bad) {
+    const int t = threadIdx.x;
+    if (t < nodes * 4) {
+        const int q = t >> 2, m = t & 3;
+        const T* p = w_prob + (int64_t(c) * nodes + q) * 16;
+        T acc = 0;
+        for (int g = 0; g < 16; ++g) {
+            const Coef4<T> cf = gate_coef<T>(g);
+            const T cm = m == 0 ? cf.c0 : m == 1 ? cf.c1 : m == 2 ? cf.c2 : cf.c3;
+            acc = fma(p[g], cm, acc);
+        }
+        sk[q][m] = acc;
+    }
+    if (t >= 32 && t < 32 + kTaps) {
+        const int k = t - 32;
+        st[k] = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
+        if (st[k].ch >= d.cin) *bad = 1;
+    }
+}
+
+// Node values at conv position (oy, ox): taps v, gates g (nodes 0..3), tree t (nodes 4, 5), r.
+template <typename T, bool COMPLETE>
+struct Eval {
+    T v[kTaps], g[4], t[2], r;
+};
+
+template <typename T, bool COMPLETE>
+__device__ __forceinline__ void eval_at(const T* __restrict__ xn, const TreeDims& d,
+                                        const TapOff* st, T (*sk)[4], int oy, int ox,
+                                        Eval<T, COMPLETE>& e) {
+#pragma unroll
+    for (int k = 0; k < kTaps; ++k) e.v[k] = tap_value(xn, d, st[k], oy, ox);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) e.g[q] = node(sk[q], e.v[2 * q], e.v[2 * q + 1]);
+    if constexpr (COMPLETE) {
+        e.t[0] = node(sk[4], e.g[0], e.g[1]);
+        e.t[1] = node(sk[5], e.g[2], e.g[3]);
+        e.r = node(sk[6], e.t[0], e.t[1]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward: one thread per (sample, pooled window) (complete) or (sample, conv position), the
+// workgroup's channel in blockIdx.y.
+template <typename T, bool COMPLETE>
+__global__ __launch_bounds__(256) void k_tree_fwd(const T* __restrict__ x, const T* __restrict__ w_prob,
+                                                  const int32_t* __restrict__ sel, TreeDims d,
+                                                  T* __restrict__ y, T* __restrict__ x2,
+                                                  T* __restrict__ x3, int32_t* __restrict__ idx) {
+    constexpr int NODES = COMPLETE ? 7 : 4;
+    __shared__ T sk[kMaxNodes][4];
+    __shared__ TapOff st[kTaps];
+    __shared__ int bad;
+    const int c = blockIdx.y;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    load_channel(w_prob, sel, c, NODES, d, sk, st, &bad);
+    __syncthreads();
+    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (item >= int64_t(d.n) * d.P) return;
+    const int n = int(item / d.P), p = int(item % d.P);
+    const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
+    const T nan = quiet_nan<T>();
+    const int64_t cell = int64_t(n) * d.cout + c;  // (n, c)
+    if constexpr (COMPLETE) {
+        const int wp = d.wo / 2;
+        const int py = p / wp, px = p % wp;
+        T best = -T(__builtin_inf());
+        int bidx = -1;
+#pragma unroll
+        for (int dy2 = 0; dy2 < 2; ++dy2)
+#pragma unroll
+            for (int dx2 = 0; dx2 < 2; ++dx2) {
+                const int oy = 2 * py + dy2, ox = 2 * px + dx2;
+                Eval<T, true> e;
+                eval_at<T, true>(xn, d, st, sk, oy, ox, e);
+                const int64_t pos = cell * d.ho * d.wo + int64_t(oy) * d.wo + ox;
+                if (x2) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) x2[pos * 4 + q] = bad ? nan : e.g[q];
+                }
+                if (x3) {
+                    x3[pos * 2 + 0] = bad ? nan : e.t[0];
+                    x3[pos * 2 + 1] = bad ? nan : e.t[1];
+                }
+                if (e.r > best) {
+                    best = e.r;
+                    bidx = oy * d.wo + ox;
+                }
+            }
+        y[cell * d.P + p] = bad ? nan : best;
+        if (idx) idx[cell * d.P + p] = bidx;
+    } else {
+        const int oy = p / d.wo, ox = p % d.wo;
+        Eval<T, false> e;
+        eval_at<T, false>(xn, d, st, sk, oy, ox, e);
+        const int64_t pos = cell * d.P + p;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? nan : e.g[q];
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward, node part: per item the upstream gradients of the four conv gates (gconv, complete
+// only; the conv-only block reads them from grad_y) and the node moments, reduced over the
+// workgroup's items into part[(c * nblk + blk) * NODES * 4 + q * 4 + m] with
+// m = (sum gy a b, sum gy a, sum gy b, sum gy).  The blk == 0 workgroup of each channel also
+// stores the collapsed coefficients kc[c][q][:] for the gather kernel.
+template <typename T, bool COMPLETE>
+__global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y, const T* __restrict__ x,
+                                                    const T* __restrict__ w_prob,
+                                                    const int32_t* __restrict__ sel,
+                                                    const int32_t* __restrict__ idx, TreeDims d,
+                                                    T* __restrict__ gconv, T* __restrict__ part,
+                                                    T* __restrict__ kc) {
+    constexpr int NODES = COMPLETE ? 7 : 4;
+    constexpr int NM = NODES * 4;
+    __shared__ T sk[kMaxNodes][4];
+    __shared__ TapOff st[kTaps];
+    __shared__ int bad;
+    __shared__ T red[4][NM];
+    const int c = blockIdx.y;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    load_channel(w_prob, sel, c, NODES, d, sk, st, &bad);
+    __syncthreads();
+    if (blockIdx.x == 0 && threadIdx.x < NM) kc[int64_t(c) * NM + threadIdx.x] = sk[threadIdx.x >> 2][threadIdx.x & 3];
+    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    T mom[NM];
+#pragma unroll
+    for (int i = 0; i < NM; ++i) mom[i] = T(0);
+    if (item < int64_t(d.n) * d.P) {
+        const int n = int(item / d.P), p = int(item % d.P);
+        const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
+        const int64_t cell = int64_t(n) * d.cout + c;
+        T gc[4];
+        Eval<T, COMPLETE> e;
+        bool live = true;
+        if constexpr (COMPLETE) {
+            const int win = idx[cell * d.P + p];
+            live = win >= 0 && win < d.ho * d.wo;
+            const int w0 = live ? win : 0;
+            eval_at<T, true>(xn, d, st, sk, w0 / d.wo, w0 % d.wo, e);
+            const T gy = live ? grad_y[cell * d.P + p] : T(0);
+            const T gt0 = gy * fma(sk[6][3], e.t[1], sk[6][1]);
+            const T gt1 = gy * fma(sk[6][3], e.t[0], sk[6][2]);
+            gc[0] = gt0 * fma(sk[4][3], e.g[1], sk[4][1]);
+            gc[1] = gt0 * fma(sk[4][3], e.g[0], sk[4][2]);
+            gc[2] = gt1 * fma(sk[5][3], e.g[3], sk[5][1]);
+            gc[3] = gt1 * fma(sk[5][3], e.g[2], sk[5][2]);
+            const T* gn = gc;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gn[q];
+            const T gts[2] = {gt0, gt1};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const T a = e.g[2 * j], b = e.g[2 * j + 1], g = gts[j];
+                mom[(4 + j) * 4 + 0] = g * a * b;
+                mom[(4 + j) * 4 + 1] = g * a;
+                mom[(4 + j) * 4 + 2] = g * b;
+                mom[(4 + j) * 4 + 3] = g;
+            }
+            mom[24] = gy * e.t[0] * e.t[1];
+            mom[25] = gy * e.t[0];
+            mom[26] = gy * e.t[1];
+            mom[27] = gy;
+        } else {
+            const int oy = p / d.wo, ox = p % d.wo;
+            eval_at<T, false>(xn, d, st, sk, oy, ox, e);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) gc[q] = grad_y[(cell * d.P + p) * 4 + q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const T a = e.v[2 * q], b = e.v[2 * q + 1], g = gc[q];
+            mom[q * 4 + 0] = g * a * b;
+            mom[q * 4 + 1] = g * a;
+            mom[q * 4 + 2] = g * b;
+            mom[q * 4 + 3] = g;
+        }
+    }
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+        const T s = wave_total(mom[i]);
+        if (lane == 0) red[wv][i] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < NM) {
+        const int i = threadIdx.x;
+        const T s = (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
+        part[(int64_t(c) * gridDim.x + blockIdx.x) * NM + i] = bad ? quiet_nan<T>() : s;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward, input gradient.  Workgroup (n, channel group); LDS holds the gradient of CG input
+// channels.  A lane group of PW lanes (PW = items per pass, a power of two <= 64) owns one input
+// channel at a time and walks its uses ent[ent_ptr[ch] ..) = c * 8 + k in order; lane pl of the
+// group handles items pl, pl + PW, ...  For use (c, k) at item p (conv position win, the pooled
+// window's winner when complete) the tap reads (iy, ix) = (oy*sh + dy_k, ox*sw + dx_k) and adds
+//   gconv[n, c, p, k/2] * (k even ? K1 + K3 x_partner : K2 + K3 x_partner)
+// of node k/2, x_partner being the other tap of the node at the same position.
+template <typename T, bool COMPLETE>
+__global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc, const T* __restrict__ x,
+                                                     const int32_t* __restrict__ sel,
+                                                     const int32_t* __restrict__ idx,
+                                                     const int32_t* __restrict__ ent_ptr,
+                                                     const int32_t* __restrict__ ent,
+                                                     const T* __restrict__ kc, TreeDims d, int cg,
+                                                     int pw_lanes, T* __restrict__ grad_x) {
+    constexpr int NODES = COMPLETE ? 7 : 4;
+    extern __shared__ unsigned char smem_raw[];
+    T* gx = reinterpret_cast<T*>(smem_raw);
+    const int n = blockIdx.x;
+    const int ch0 = blockIdx.y * cg;
+    const int nch = min(cg, d.cin - ch0);
+    const int hw = d.h * d.w;
+    for (int i = threadIdx.x; i < nch * hw; i += 256) gx[i] = T(0);
+    __syncthreads();
+    const T* xn = x + int64_t(n) * d.cin * hw;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int PW = pw_lanes;
+    const int groups_per_wave = 64 / PW;
+    const int sub = lane / PW, pl = lane % PW;
+    // channel slot handled by this lane group in pass `it`: wave-major so a wave's groups take
+    // consecutive channels
+    for (int base = 0; base < nch; base += 4 * groups_per_wave) {
+        const int chl = base + wv * groups_per_wave + sub;
+        const bool have = chl < nch;
+        const int ch = ch0 + chl;
+        const int e0 = have ? ent_ptr[ch] : 0, e1 = have ? ent_ptr[ch + 1] : 0;
+        // trip count uniform over the wave: the largest use count of its groups
+        int cnt = e1 - e0;
+        for (int off = 32; off > 0; off >>= 1) cnt = max(cnt, __shfl_xor(cnt, off, 64));
+        for (int j = 0; j < cnt; ++j) {
+            const bool on = j < e1 - e0;
+            const int u = on ? ent[e0 + j] : 0;
+            const int c = u >> 3, k = u & 7;
+            const TapOff tk = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
+            const TapOff tp = decode_tap(sel[c * kTaps + (k ^ 1)], d.ph, d.pw);
+            const T* kq = kc + (int64_t(c) * NODES + (k >> 1)) * 4;
+            const T kown = (k & 1) ? kq[2] : kq[1], k3 = kq[3];
+            const int64_t cell = int64_t(n) * d.cout + c;
+            for (int p = pl; on && p < d.P; p += PW) {
+                int win = p;
+                if constexpr (COMPLETE) win = idx[cell * d.P + p];
+                if (win < 0 || win >= d.ho * d.wo) continue;
+                const int oy = win / d.wo, ox = win % d.wo;
+                const int iy = oy * d.sh + tk.dy, ix = ox * d.sw + tk.dx;
+                if (iy < 0 || iy >= d.h || ix < 0 || ix >= d.w) continue;
+                const T xp = tap_value(xn, d, tp, oy, ox);
+                const T g = gsrc[(cell * d.P + p) * 4 + (k >> 1)];
+                atomicAdd(&gx[(ch - ch0) * hw + iy * d.w + ix], g * fma(k3, xp, kown));
+            }
+        }
+    }
+    __syncthreads();
+    T* dst = grad_x + (int64_t(n) * d.cin + ch0) * hw;
+    for (int i = threadIdx.x; i < nch * hw; i += 256) dst[i] = gx[i];
+}
+
+// grad_w[c][q][g] = c0(g) M3 + c1(g) M1 + c2(g) M2 + c3(g) M0 with M the node's moments summed
+// over the nblk partials in block order.  One thread per (c, q, g).
+template <typename T>
+__global__ __launch_bounds__(256) void k_tree_finalize(const T* __restrict__ part, int64_t cout,
+                                                       int nodes, int64_t nblk,
+                                                       T* __restrict__ grad_w) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= cout * nodes * 16) return;
+    const int g = int(i & 15);
+    const int64_t cq = i >> 4;
+    const int64_t c = cq / nodes, q = cq % nodes;
+    T m[4] = {0, 0, 0, 0};
+    for (int64_t b = 0; b < nblk; ++b) {
+        const T* src = part + ((c * nblk + b) * nodes + q) * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m[j] += src[j];
+    }
+    const Coef4<T> cf = gate_coef<T>(g);
+    grad_w[i] = fma(cf.c3, m[0], fma(cf.c2, m[2], fma(cf.c1, m[1], cf.c0 * m[3])));
+}
+
+// ------------------------------------------------------------------------------------------
+// One tree level (TreeLogicLayer): x[..., 2j], x[..., 2j + 1] -> y[..., j] with node j of the
+// element's channel.  x is [N, C, S, 2 * xo] (S = H * W), y [N, C, S, xo].
+template <typename T>
+__global__ __launch_bounds__(256) void k_level_fwd(const T* __restrict__ x, const T* __restrict__ w_prob,
+                                                   int64_t n, int64_t c_dim, int64_t s, int xo,
+                                                   T* __restrict__ y) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (n, c, s, j)
+    const int64_t total = n * c_dim * s * xo;
+    if (i >= total) return;
+    const int j = int(i % xo);
+    const int64_t c = (i / xo / s) % c_dim;
+    const T* p = w_prob + (c * xo + j) * 16;
+    T k[4] = {0, 0, 0, 0};
+    for (int g = 0; g < 16; ++g) {
+        const Coef4<T> cf = gate_coef<T>(g);
+        k[0] = fma(p[g], cf.c0, k[0]);
+        k[1] = fma(p[g], cf.c1, k[1]);
+        k[2] = fma(p[g], cf.c2, k[2]);
+        k[3] = fma(p[g], cf.c3, k[3]);
+    }
+    const int64_t base = (i / xo) * 2 * xo + 2 * j;
+    y[i] = node(k, x[base], x[base + 1]);
+}
+
+// Tree level backward: grad_x elementwise, node moments per workgroup (fixed order) into
+// part[(c * nblk + blk) * xo * 4 + j * 4 + m]; the workgroup's items all have channel
+// blockIdx.y (items are (n, s) pairs).
+template <typename T>
+__global__ __launch_bounds__(256) void k_level_bwd(const T* __restrict__ grad_y, const T* __restrict__ x,
+                                                   const T* __restrict__ w_prob, int64_t n,
+                                                   int64_t c_dim, int64_t s, int xo,
+                                                   T* __restrict__ grad_x, T* __restrict__ part) {
+    constexpr int kMaxOut = 4;
+    __shared__ T sk[kMaxOut][4];
+    __shared__ T red[4][kMaxOut * 4];
+    const int c = blockIdx.y;
+    if (threadIdx.x < xo * 4) {
+        const int j = threadIdx.x >> 2, m = threadIdx.x & 3;
+        const T* p = w_prob + (int64_t(c) * xo + j) * 16;
+        T acc = 0;
+        for (int g = 0; g < 16; ++g) {
+            const Coef4<T> cf = gate_coef<T>(g);
+            acc = fma(p[g], m == 0 ? cf.c0 : m == 1 ? cf.c1 : m == 2 ? cf.c2 : cf.c3, acc);
+        }
+        sk[j][m] = acc;
+    }
+    __syncthreads();
+    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    T mom[kMaxOut * 4];
+#pragma unroll
+    for (int i = 0; i < kMaxOut * 4; ++i) mom[i] = T(0);
+    if (item < n * s) {
+        const int64_t nn = item / s, ss = item % s;
+        const int64_t row = (nn * c_dim + c) * s + ss;
+#pragma unroll
+        for (int j = 0; j < kMaxOut; ++j) {
+            if (j >= xo) continue;
+            const T a = x[row * 2 * xo + 2 * j], b = x[row * 2 * xo + 2 * j + 1];
+            const T g = grad_y[row * xo + j];
+            if (grad_x) {
+                grad_x[row * 2 * xo + 2 * j] = g * fma(sk[j][3], b, sk[j][1]);
+                grad_x[row * 2 * xo + 2 * j + 1] = g * fma(sk[j][3], a, sk[j][2]);
+            }
+            mom[j * 4 + 0] = g * a * b;
+            mom[j * 4 + 1] = g * a;
+            mom[j * 4 + 2] = g * b;
+            mom[j * 4 + 3] = g;
+        }
+    }
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kMaxOut * 4; ++i) {
+        if (i >= xo * 4) continue;  // uniform
+        const T t = wave_total(mom[i]);
+        if (lane == 0) red[wv][i] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < xo * 4) {
+        const int i = threadIdx.x;
+        part[(int64_t(c) * gridDim.x + blockIdx.x) * xo * 4 + i] =
+            (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Packed discrete block: rows of 64-bit words, one row per (channel, y, x) of the NCHW input
+// (row = (ch * H + y) * W + x); output rows (c * Hp + py) * Wp + px (complete) or
+// ((c * Ho + oy) * Wo + ox) * 4 + q (conv gates only).  gates[c * nodes + q] is node q's opcode;
+// the pool of {0, 1} values is the OR of the window.
+__global__ __launch_bounds__(256) void k_tree_packed(const uint64_t* __restrict__ x, int64_t words,
+                                                     const uint8_t* __restrict__ gates,
+                                                     const int32_t* __restrict__ sel, TreeDims d,
+                                                     uint64_t* __restrict__ y) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t rows = int64_t(d.cout) * d.P;
+    if (i >= rows * words) return;
+    const int64_t r = i / words, w = i % words;
+    const int c = int(r / d.P), p = int(r % d.P);
+    const int nodes = d.complete ? 7 : 4;
+    int op[kMaxNodes];
+#pragma unroll
+    for (int q = 0; q < kMaxNodes; ++q) op[q] = q < nodes ? (gates[c * nodes + q] & 15) : 0;
+    TapOff t[kTaps];
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < kTaps; ++k) {
+        t[k] = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
+        bad |= t[k].ch >= d.cin;
+    }
+    auto word_at = [&](const TapOff& tk, int oy, int ox) -> uint64_t {
+        const int iy = oy * d.sh + tk.dy, ix = ox * d.sw + tk.dx;
+        if (iy < 0 || iy >= d.h || ix < 0 || ix >= d.w || tk.ch >= d.cin) return 0;
+        return x[((int64_t(tk.ch) * d.h + iy) * d.w + ix) * words + w];
+    };
+    if (d.complete) {
+        const int wp = d.wo / 2;
+        const int py = p / wp, px = p % wp;
+        uint64_t out = 0;
+#pragma unroll
+        for (int dy2 = 0; dy2 < 2; ++dy2)
+#pragma unroll
+            for (int dx2 = 0; dx2 < 2; ++dx2) {
+                const int oy = 2 * py + dy2, ox = 2 * px + dx2;
+                uint64_t g[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    g[q] = bitwise_op<uint64_t>(op[q], word_at(t[2 * q], oy, ox),
+                                                word_at(t[2 * q + 1], oy, ox));
+                const uint64_t t0 = bitwise_op<uint64_t>(op[4], g[0], g[1]);
+                const uint64_t t1 = bitwise_op<uint64_t>(op[5], g[2], g[3]);
+                out |= bitwise_op<uint64_t>(op[6], t0, t1);
+            }
+        y[i] = bad ? ~uint64_t(0) : out;
+    } else {
+        const int q = p & 3, pos = p >> 2;
+        const int oy = pos / d.wo, ox = pos % d.wo;
+        y[i] = bad ? ~uint64_t(0)
+                   : bitwise_op<uint64_t>(op[q], word_at(t[2 * q], oy, ox),
+                                          word_at(t[2 * q + 1], oy, ox));
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_zero(T* __restrict__ p, int64_t count) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < count) p[i] = T(0);
+}
+
+// Zero `count` elements with a kernel (not a memset node, so the call stays graph-safe).
+template <typename T>
+int zero_fill(void* p, int64_t count, hipStream_t s, const char* what) {
+    if (count <= 0 || !p) return CL_OK;
+    CL_ARG(ceil_div(count, 256) < (int64_t(1) << 31), "tensor too large");
+    k_zero<T><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(static_cast<T*>(p), count);
+    return check_launch(what);
+}
+
+int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t cout, int sh,
+              int sw, int ph, int pw, int kh, int kw, int complete) {
+    CL_ARG(n >= 0 && cin >= 1 && h >= 1 && w >= 1 && cout >= 0, "bad block shape");
+    CL_ARG(sh >= 1 && sw >= 1 && ph >= 0 && pw >= 0 && kh >= 1 && kw >= 1,
+           "bad stride / padding / kernel");
+    CL_ARG(cin <= 0xFFFF && h <= 4096 && w <= 4096 && kh <= 255 && kw <= 255 && ph <= 255 &&
+               pw <= 255,
+           "block dimensions beyond the selection encoding");
+    const int64_t ho = (h + 2 * ph - kh) / sh + 1, wo = (w + 2 * pw - kw) / sw + 1;
+    CL_ARG(h + 2 * ph >= kh && w + 2 * pw >= kw && ho > 0 && wo > 0,
+           "invalid output shape: H_out=%lld, W_out=%lld", (long long)ho, (long long)wo);
+    if (complete)
+        CL_ARG(ho % 2 == 0 && wo % 2 == 0,
+               "Output height and width after convolution must be divisible by 2 for 2x2 max "
+               "pooling, but got H_out=%lld, W_out=%lld",
+               (long long)ho, (long long)wo);
+    const int64_t P = complete ? (ho / 2) * (wo / 2) : ho * wo;
+    CL_ARG(n * cin * h * w < (int64_t(1) << 40) && cout * P < (int64_t(1) << 31) &&
+               n * P < (int64_t(1) << 40) && cout < 65536,
+           "block too large");
+    d.n = int(n);
+    d.cin = int(cin);
+    d.h = int(h);
+    d.w = int(w);
+    d.cout = int(cout);
+    d.ho = int(ho);
+    d.wo = int(wo);
+    d.sh = sh;
+    d.sw = sw;
+    d.ph = ph;
+    d.pw = pw;
+    d.complete = complete ? 1 : 0;
+    d.P = int(P);
+    return CL_OK;
+}
+
+// Items per lane-group pass of the gather kernel: the next power of two >= P, at most 64.
+int gather_lanes(int P) {
+    int pw = 1;
+    while (pw < P && pw < 64) pw <<= 1;
+    return pw;
+}
+
+constexpr int64_t kGatherLdsBytes = 64 * 1024;
+
+template <typename T>
+int64_t tree_workspace_bytes(const TreeDims& d) {
+    const int nodes = d.complete ? 7 : 4;
+    const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256);
+    int64_t b = 0;
+    if (d.complete) b += int64_t(d.n) * d.cout * d.P * 4 * sizeof(T);  // gconv
+    b = (b + 255) / 256 * 256;
+    b += int64_t(d.cout) * nblk * nodes * 4 * sizeof(T);  // partial moments
+    b = (b + 255) / 256 * 256;
+    b += int64_t(d.cout) * nodes * 4 * sizeof(T);  // collapsed coefficients
+    return b;
+}
+
+}  // namespace
+}  // namespace cl
+
+using namespace cl;
+
+extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob,
+                                    const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
+                                    int64_t w, int64_t c_out, int stride_h, int stride_w,
+                                    int pad_h, int pad_w, int kernel_h, int kernel_w,
+                                    int complete, void* y, void* x2, void* x3, int32_t* indices,
+                                    void* stream) {
+    clear_error();
+    TreeDims d;
+    if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
+                           kernel_w, complete))
+        return rc;
+    if (n == 0 || c_out == 0) return CL_OK;
+    CL_ARG(x && w_prob && selection && y, "null pointer argument");
+    const unsigned gx = unsigned(ceil_div(int64_t(d.n) * d.P, 256));
+    const dim3 grid(gx, unsigned(d.cout));
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        if (complete)
+            k_tree_fwd<T, true><<<grid, 256, 0, s>>>(
+                static_cast<const T*>(x), static_cast<const T*>(w_prob), selection, d,
+                static_cast<T*>(y), static_cast<T*>(x2), static_cast<T*>(x3), indices);
+        else
+            k_tree_fwd<T, false><<<grid, 256, 0, s>>>(
+                static_cast<const T*>(x), static_cast<const T*>(w_prob), selection, d,
+                static_cast<T*>(y), nullptr, nullptr, nullptr);
+    });
+    return check_launch("cl_tree_conv_forward");
+}
+
+extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,
+                                      int64_t c_out, int stride_h, int stride_w, int pad_h,
+                                      int pad_w, int kernel_h, int kernel_w, int complete,
+                                      int64_t* bytes) {
+    clear_error();
+    CL_ARG(bytes, "null pointer argument");
+    TreeDims d;
+    if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
+                           kernel_w, complete))
+        return rc;
+    CL_DTYPE_SWITCH(dtype, { *bytes = tree_workspace_bytes<scalar_t>(d); });
+    return CL_OK;
+}
+
+extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x,
+                                     const void* w_prob, const int32_t* selection,
+                                     const int32_t* indices, const int32_t* ent_ptr,
+                                     const int32_t* ent, int64_t n, int64_t c_in, int64_t h,
+                                     int64_t w, int64_t c_out, int stride_h, int stride_w,
+                                     int pad_h, int pad_w, int kernel_h, int kernel_w,
+                                     int complete, void* grad_x, void* grad_w, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+    clear_error();
+    TreeDims d;
+    if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
+                           kernel_w, complete))
+        return rc;
+    if (!grad_x && !grad_w) return CL_OK;
+    const int nodes = complete ? 7 : 4;
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        if (n == 0 || c_out == 0) {  // no items: zero gradients
+            if (grad_x)
+                if (int rc = zero_fill<T>(grad_x, n * c_in * h * w, s, "cl_tree_conv_backward"))
+                    return rc;
+            if (grad_w)
+                if (int rc = zero_fill<T>(grad_w, c_out * nodes * 16, s, "cl_tree_conv_backward"))
+                    return rc;
+            return CL_OK;
+        }
+        CL_ARG(grad_y && x && w_prob && selection, "null pointer argument");
+        CL_ARG(!complete || indices, "the complete block's backward needs the pooling indices");
+        CL_ARG(!grad_x || (ent_ptr && ent), "the input gradient needs the channel use index");
+        const int64_t need = tree_workspace_bytes<T>(d);
+        CL_ARG(workspace && workspace_bytes >= need,
+               "workspace of %lld bytes needed (see cl_tree_conv_workspace)", (long long)need);
+        CL_ARG(aligned(workspace, 256), "workspace must be 256-byte aligned");
+        const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256);
+        unsigned char* ws = static_cast<unsigned char*>(workspace);
+        T* gconv = nullptr;
+        int64_t off = 0;
+        if (complete) {
+            gconv = reinterpret_cast<T*>(ws);
+            off = int64_t(d.n) * d.cout * d.P * 4 * sizeof(T);
+        }
+        off = (off + 255) / 256 * 256;
+        T* part = reinterpret_cast<T*>(ws + off);
+        off += int64_t(d.cout) * nblk * nodes * 4 * sizeof(T);
+        off = (off + 255) / 256 * 256;
+        T* kc = reinterpret_cast<T*>(ws + off);
+        const dim3 grid(unsigned(nblk), unsigned(d.cout));
+        const T* gy = static_cast<const T*>(grad_y);
+        const T* xs = static_cast<const T*>(x);
+        const T* wp = static_cast<const T*>(w_prob);
+        if (complete)
+            k_tree_nodes<T, true><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gconv,
+                                                       part, kc);
+        else
+            k_tree_nodes<T, false><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gconv,
+                                                        part, kc);
+        if (int rc = check_launch("cl_tree_conv_backward(nodes)")) return rc;
+        if (grad_w) {
+            k_tree_finalize<T><<<unsigned(ceil_div(int64_t(d.cout) * nodes * 16, 256)), 256, 0, s>>>(
+                part, d.cout, nodes, nblk, static_cast<T*>(grad_w));
+            if (int rc = check_launch("cl_tree_conv_backward(finalize)")) return rc;
+        }
+        if (grad_x) {
+            const int64_t hw_bytes = int64_t(d.h) * d.w * int64_t(sizeof(T));
+            CL_ARG(hw_bytes <= kGatherLdsBytes,
+                   "input planes of more than %lld bytes are not supported by the input gradient",
+                   (long long)kGatherLdsBytes);
+            const int cg = int(std::min<int64_t>(d.cin, kGatherLdsBytes / hw_bytes));
+            const dim3 g2(unsigned(d.n), unsigned(ceil_div(d.cin, cg)));
+            const size_t lds = size_t(cg) * size_t(hw_bytes);
+            const T* src = complete ? gconv : gy;
+            if (complete)
+                k_tree_gather<T, true><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
+                                                            ent, kc, d, cg, gather_lanes(d.P),
+                                                            static_cast<T*>(grad_x));
+            else
+                k_tree_gather<T, false><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
+                                                             ent, kc, d, cg, gather_lanes(d.P),
+                                                             static_cast<T*>(grad_x));
+            if (int rc = check_launch("cl_tree_conv_backward(gather)")) return rc;
+        }
+    });
+    return CL_OK;
+}
+
+extern "C" int cl_tree_level_forward(int dtype, const void* x, const void* w_prob, int64_t n,
+                                     int64_t channels, int64_t positions, int64_t out_bits,
+                                     void* y, void* stream) {
+    clear_error();
+    CL_ARG(n >= 0 && channels >= 0 && positions >= 0, "negative shape");
+    CL_ARG(out_bits >= 1 && out_bits <= 4, "Xout > 4 is not supported");
+    const int64_t total = n * channels * positions * out_bits;
+    if (total == 0) return CL_OK;
+    CL_ARG(x && w_prob && y, "null pointer argument");
+    CL_ARG(ceil_div(total, 256) < (int64_t(1) << 31), "tensor too large");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        k_level_fwd<T><<<unsigned(ceil_div(total, 256)), 256, 0, s>>>(
+            static_cast<const T*>(x), static_cast<const T*>(w_prob), n, channels, positions,
+            int(out_bits), static_cast<T*>(y));
+    });
+    return check_launch("cl_tree_level_forward");
+}
+
+extern "C" int cl_tree_level_workspace(int dtype, int64_t n, int64_t channels, int64_t positions,
+                                       int64_t out_bits, int64_t* bytes) {
+    clear_error();
+    CL_ARG(bytes, "null pointer argument");
+    CL_ARG(n >= 0 && channels >= 0 && positions >= 0 && out_bits >= 1 && out_bits <= 4,
+           "bad shape");
+    const int64_t nblk = ceil_div(n * positions, 256);
+    CL_DTYPE_SWITCH(dtype, { *bytes = channels * nblk * out_bits * 4 * int64_t(sizeof(scalar_t)); });
+    return CL_OK;
+}
+
+extern "C" int cl_tree_level_backward(int dtype, const void* grad_y, const void* x,
+                                      const void* w_prob, int64_t n, int64_t channels,
+                                      int64_t positions, int64_t out_bits, void* grad_x,
+                                      void* grad_w, void* workspace, int64_t workspace_bytes,
+                                      void* stream) {
+    clear_error();
+    CL_ARG(n >= 0 && channels >= 0 && positions >= 0, "negative shape");
+    CL_ARG(out_bits >= 1 && out_bits <= 4, "Xout > 4 is not supported");
+    if (!grad_x && !grad_w) return CL_OK;
+    hipStream_t s = as_stream(stream);
+    const int64_t items = n * positions;
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        if (items == 0 || channels == 0) {  // no items: zero weight gradient
+            if (grad_w)
+                return zero_fill<T>(grad_w, channels * out_bits * 16, s, "cl_tree_level_backward");
+            return CL_OK;
+        }
+        CL_ARG(grad_y && x && w_prob, "null pointer argument");
+        const int64_t nblk = ceil_div(items, 256);
+        CL_ARG(nblk < (int64_t(1) << 31) && channels < 65536, "tensor too large");
+        const int64_t need = channels * nblk * out_bits * 4 * int64_t(sizeof(T));
+        CL_ARG(workspace && workspace_bytes >= need,
+               "workspace of %lld bytes needed (see cl_tree_level_workspace)", (long long)need);
+        T* part = static_cast<T*>(workspace);
+        k_level_bwd<T><<<dim3(unsigned(nblk), unsigned(channels)), 256, 0, s>>>(
+            static_cast<const T*>(grad_y), static_cast<const T*>(x), static_cast<const T*>(w_prob),
+            n, channels, positions, int(out_bits), static_cast<T*>(grad_x), part);
+        if (int rc = check_launch("cl_tree_level_backward")) return rc;
+        if (grad_w) {
+            k_tree_finalize<T><<<unsigned(ceil_div(channels * out_bits * 16, 256)), 256, 0, s>>>(
+                part, channels, int(out_bits), nblk, static_cast<T*>(grad_w));
+        }
+    });
+    return check_launch("cl_tree_level_backward");
+}
+
+extern "C" int cl_tree_conv_eval_packed(const void* x, int64_t row_bytes, const uint8_t* gates,
+                                        const int32_t* selection, int64_t c_in, int64_t h,
+                                        int64_t w, int64_t c_out, int stride_h, int stride_w,
+                                        int pad_h, int pad_w, int kernel_h, int kernel_w,
+                                        int complete, void* y, void* stream) {
+    clear_error();
+    TreeDims d;
+    if (int rc = tree_dims(d, 1, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
+                           kernel_w, complete))
+        return rc;
+    CL_ARG(row_bytes >= 0 && row_bytes % 8 == 0, "row_bytes must be a multiple of 8");
+    const int64_t words = row_bytes / 8;
+    const int64_t rows = int64_t(d.cout) * d.P * (complete ? 1 : 4);
+    if (words == 0 || rows == 0) return CL_OK;
+    CL_ARG(x && gates && selection && y, "null pointer argument");
+    CL_ARG(aligned(x, 8) && aligned(y, 8), "packed rows must be 8-byte aligned");
+    if (!complete) d.P *= 4;  // one output row per (position, gate)
+    const int64_t total = rows * words;
+    CL_ARG(ceil_div(total, 256) < (int64_t(1) << 31), "tensor too large");
+    k_tree_packed<<<unsigned(ceil_div(total, 256)), 256, 0, as_stream(stream)>>>(
+        static_cast<const uint64_t*>(x), words, gates, selection, d, static_cast<uint64_t*>(y));
+    return check_launch("cl_tree_conv_eval_packed");
+}

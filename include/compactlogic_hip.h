@@ -406,6 +406,77 @@ int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamples, const 
                       const int64_t* rows_host, int64_t num_layers, int64_t k, int32_t* counts,
                       void* stream);
 
+/* -------------------------------------------------------------------------------------------
+ * Logic-tree convolution block (third-party ConvLogic, convlogic_cuda extension,
+ * third_party/convlogic_source_code/src/convlogic/cuda/convlogic.cpp:31-43).
+ * x: [n, c_in, h, w] NCHW; w_prob: [c_out, nodes, 16] gate probabilities (nodes = 7 when
+ * complete, else 4); selection: int32 [c_out, 8], tap k = ch << 16 | row << 8 | col.  Tap k
+ * of channel c reads x[n, ch, oy*stride_h + row - pad_h, ox*stride_w + col - pad_w], zero
+ * outside the image; node q < 4 is the gate on taps (2q, 2q+1).  The complete block adds
+ * node 4 on nodes (0, 1), node 5 on (2, 3), node 6 on (4, 5) and a 2x2 stride-2 max pool in
+ * which the first maximum in row-major window order wins.
+ * ----------------------------------------------------------------------------------------- */
+
+/* Replaces full_convlogic_forward (complete; full_convlogic_kernel.cu:156-231) and
+ * convlogic_forward (conv gates only; convlogic_kernel.cu:67-107).  complete: y [n, c_out,
+ * h_out/2, w_out/2]; x2 [n, c_out, h_out, w_out, 4] and x3 [.., 2] (node outputs at every
+ * position) and indices int32 [n, c_out, (h_out/2)*(w_out/2)] (winner oy*w_out + ox) are each
+ * written when not NULL.  Not complete: y [n, c_out, h_out, w_out, 4].  A selection channel
+ * >= c_in makes the channel's outputs NaN. */
+int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob, const int32_t* selection,
+                         int64_t n, int64_t c_in, int64_t h, int64_t w, int64_t c_out,
+                         int stride_h, int stride_w, int pad_h, int pad_w, int kernel_h,
+                         int kernel_w, int complete, void* y, void* x2, void* x3,
+                         int32_t* indices, void* stream);
+
+/* Workspace bytes of cl_tree_conv_backward for this shape. */
+int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,
+                           int64_t c_out, int stride_h, int stride_w, int pad_h, int pad_w,
+                           int kernel_h, int kernel_w, int complete, int64_t* bytes);
+
+/* Replaces full_convlogic_backward_x + full_convlogic_backward_weight
+ * (full_convlogic_kernel.cu:332-430, :580-701) and convlogic_backward_x +
+ * convlogic_backward_weight (convlogic_kernel.cu:197-249, :321-360).  grad_y has the shape of
+ * the forward's y; indices are the forward's (complete only).  ent_ptr (int32 [c_in + 1]) and
+ * ent (int32 [8 * c_out], c * 8 + k) list the taps reading each input channel in ascending
+ * order (the input gradient's gather order).  grad_x [n, c_in, h, w] (may be NULL) is exact
+ * and reproducible: a sum over the taps in that order, no float atomics; it needs
+ * h * w * sizeof(element) <= 65536.  grad_w [c_out, nodes, 16] (may be NULL) is the gradient of
+ * the probabilities. */
+int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x, const void* w_prob,
+                          const int32_t* selection, const int32_t* indices,
+                          const int32_t* ent_ptr, const int32_t* ent, int64_t n, int64_t c_in,
+                          int64_t h, int64_t w, int64_t c_out, int stride_h, int stride_w,
+                          int pad_h, int pad_w, int kernel_h, int kernel_w, int complete,
+                          void* grad_x, void* grad_w, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/* One tree level (TreeLogicLayer).  Replaces treelogic_forward (treelogic_kernel.cu:46-86):
+ * x [n, channels, positions, 2*out_bits] -> y [n, channels, positions, out_bits], node j of the
+ * channel on inputs (2j, 2j+1); w_prob [channels, out_bits, 16]; out_bits <= 4. */
+int cl_tree_level_forward(int dtype, const void* x, const void* w_prob, int64_t n,
+                          int64_t channels, int64_t positions, int64_t out_bits, void* y,
+                          void* stream);
+
+int cl_tree_level_workspace(int dtype, int64_t n, int64_t channels, int64_t positions,
+                            int64_t out_bits, int64_t* bytes);
+
+/* Replaces treelogic_backward_x + treelogic_backward_weight (treelogic_kernel.cu:160-290);
+ * grad_x and grad_w may each be NULL. */
+int cl_tree_level_backward(int dtype, const void* grad_y, const void* x, const void* w_prob,
+                           int64_t n, int64_t channels, int64_t positions, int64_t out_bits,
+                           void* grad_x, void* grad_w, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
+/* Packed discrete block (the discrete reading of the block: argmax gates, pool = OR of the
+ * window; third_party/convlogic/extract.py:177-214, evaluate.py:117-122).  x: c_in*h*w packed
+ * rows of row_bytes bytes (row (ch*h + y)*w + x); gates: uint8 [c_out, nodes] opcodes.
+ * complete: y rows (c*h_p + py)*w_p + px; else ((c*h_out + oy)*w_out + ox)*4 + q. */
+int cl_tree_conv_eval_packed(const void* x, int64_t row_bytes, const uint8_t* gates,
+                             const int32_t* selection, int64_t c_in, int64_t h, int64_t w,
+                             int64_t c_out, int stride_h, int stride_w, int pad_h, int pad_w,
+                             int kernel_h, int kernel_w, int complete, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,249 @@
+"""Logic-tree conv block (ConvLogicLayer / TreeLogicLayer / PoolLogicLayer) on the HIP kernels
+against the float64 CPU oracle (oracle/tree_np.py) and the reference's own module tests
+(third_party/convlogic_source_code/tests/convlogic/test_full_convlogic_forward.py,
+test_full_convlogic_autograd.py, test_treelogic_forward.py)."""
+import numpy as np
+import pytest
+import torch
+
+import compactlogic_amd as cl
+from compactlogic_amd import treelogic as TL
+from oracle import tree_np as T
+
+pytestmark = pytest.mark.gpu
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+def make(seed, n, c_in, h, w, c_out, kernel=3, nodes=7, dtype=torch.float32, device="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.rand((n, c_in, h, w), generator=g, dtype=torch.float64)
+    w_prob = torch.softmax(torch.randn((c_out, nodes, 16), generator=g, dtype=torch.float64), -1)
+    ch = torch.randint(0, c_in, (c_out, 8), generator=g)
+    r = torch.randint(0, kernel, (c_out, 8), generator=g)
+    cc = torch.randint(0, kernel, (c_out, 8), generator=g)
+    sel = ((ch << 16) | (r << 8) | cc).to(torch.int32)
+    return x.to(device, dtype), w_prob.to(device, dtype), sel.to(device)
+
+
+def tol(dtype):
+    return dict(rtol=1e-5, atol=1e-6) if dtype == torch.float32 else dict(rtol=1e-10, atol=1e-12)
+
+
+SHAPES = [  # stride, pad, kernel, (n, c_in, h, w, c_out)
+    ((1, 1), (1, 1), (3, 3), (2, 3, 8, 8, 4)),
+    ((2, 2), (2, 2), (3, 3), (3, 3, 10, 10, 5)),
+    ((2, 2), (1, 1), (3, 3), (4, 9, 32, 32, 16)),     # conv1 of the tree reading of cfg3
+    ((2, 2), (1, 1), (3, 3), (3, 16, 8, 8, 32)),      # conv2 of the tree reading
+    ((1, 1), (0, 0), (2, 2), (2, 2, 5, 5, 3)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("stride,pad,kernel,shape", SHAPES)
+def test_complete_block_forward_matches_oracle(dtype, stride, pad, kernel, shape):
+    n, c_in, h, w, c_out = shape
+    x, w_prob, sel = make(1, n, c_in, h, w, c_out, kernel[0], dtype=dtype)
+    y, x2, x3, idx = TL.full_convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel)
+    ry, rx2, rx3, ridx = T.block_forward(np_(x), np_(w_prob), np_(sel), stride, pad, kernel)
+    np.testing.assert_allclose(np_(y), ry, **tol(dtype))
+    np.testing.assert_allclose(np_(x2), rx2, **tol(dtype))
+    np.testing.assert_allclose(np_(x3), rx3, **tol(dtype))
+    # fp32 rounding may flip a window's winner where two positions nearly tie
+    if dtype == torch.float64:
+        assert np.array_equal(np_(idx), ridx)
+    else:
+        assert (np_(idx) == ridx).mean() > 0.99
+    y2, a, b, idx2 = TL.full_convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel,
+                                               intermediate=False)
+    assert a is None and b is None
+    assert torch.equal(y2, y) and torch.equal(idx2, idx)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("stride,pad,kernel,shape", SHAPES)
+def test_conv_gates_forward_matches_oracle(dtype, stride, pad, kernel, shape):
+    n, c_in, h, w, c_out = shape
+    x, w_prob, sel = make(2, n, c_in, h, w, c_out, kernel[0], nodes=4, dtype=dtype)
+    y = TL.convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel)
+    ref = T.block_forward(np_(x), np_(w_prob), np_(sel), stride, pad, kernel, complete=False)
+    np.testing.assert_allclose(np_(y), ref, **tol(dtype))
+
+
+@pytest.mark.parametrize("complete", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("stride,pad,kernel,shape", SHAPES)
+def test_block_backward_matches_oracle_and_is_reproducible(complete, dtype, stride, pad, kernel,
+                                                           shape):
+    n, c_in, h, w, c_out = shape
+    nodes = 7 if complete else 4
+    x, w_prob, sel = make(3, n, c_in, h, w, c_out, kernel[0], nodes=nodes, dtype=dtype)
+    idx = None
+    if complete:
+        y, _, _, idx = TL.full_convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel,
+                                                 intermediate=False)
+    else:
+        y = TL.convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel)
+    g = torch.Generator().manual_seed(4)
+    gy = torch.randn(y.shape, generator=g, dtype=torch.float64).to(y.device, dtype)
+    gx, gw = TL.tree_conv_backward(gy, x, w_prob, sel, idx, *stride, *pad, *kernel, complete)
+    rgx, rgw = T.block_backward(np_(x), np_(w_prob), np_(sel), stride, pad, kernel, np_(gy),
+                                complete, idx=np_(idx) if complete else None)
+    scale = max(1.0, float(np.abs(rgw).max()))
+    np.testing.assert_allclose(np_(gx), rgx, **tol(dtype))
+    np.testing.assert_allclose(np_(gw) / scale, rgw / scale, **tol(dtype))
+    gx2, gw2 = TL.tree_conv_backward(gy, x, w_prob, sel, idx, *stride, *pad, *kernel, complete)
+    assert torch.equal(gx, gx2) and torch.equal(gw, gw2)
+    gx3, gw3 = TL.tree_conv_backward(gy, x, w_prob, sel, idx, *stride, *pad, *kernel, complete,
+                                     need_x=False)
+    assert gx3 is None and torch.equal(gw3, gw)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_tree_level_matches_oracle(dtype):
+    g = torch.Generator().manual_seed(5)
+    for xin in (2, 4, 8):
+        x = torch.rand((3, 5, 4, 6, xin), generator=g, dtype=torch.float64).cuda().to(dtype)
+        w_prob = torch.softmax(torch.randn((5, xin // 2, 16), generator=g, dtype=torch.float64),
+                               -1).cuda().to(dtype)
+        y = TL.treelogic_forward(x, w_prob)
+        np.testing.assert_allclose(np_(y), T.level_forward(np_(x), np_(w_prob)), **tol(dtype))
+        gy = torch.randn(y.shape, generator=g, dtype=torch.float64).cuda().to(dtype)
+        gx, gw = TL.treelogic_backward(gy, x, w_prob)
+        rgx, rgw = T.level_backward(np_(x), np_(w_prob), np_(gy))
+        np.testing.assert_allclose(np_(gx), rgx, **tol(dtype))
+        np.testing.assert_allclose(np_(gw), rgw, **tol(dtype))
+
+
+@pytest.mark.parametrize("complete", [True, False])
+def test_packed_block_matches_bit_oracle(complete):
+    rng = np.random.default_rng(6)
+    c_in, h, w, c_out, words = 9, 32, 32, 12, 5
+    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    nodes = 7 if complete else 4
+    xw = rng.integers(0, 2**63, (c_in * h * w, words), dtype=np.int64).view(np.uint64)
+    gates = rng.integers(0, 16, (c_out, nodes)).astype(np.uint8)
+    _, _, sel = make(7, 1, c_in, h, w, c_out, nodes=nodes)
+    out = TL.tree_conv_eval_packed(torch.as_tensor(xw.view(np.int64)).cuda(),
+                                   torch.as_tensor(gates).cuda(), sel, (c_in, h, w), stride, pad,
+                                   kernel, complete)
+    ref = T.block_bits(xw, gates, np_(sel), (c_in, h, w), stride, pad, kernel, complete)
+    assert np.array_equal(np_(out).view(np.uint64), ref)
+
+
+def test_module_packed_path_matches_float_eval():
+    torch.manual_seed(8)
+    layer = cl.ConvLogicLayer(3, 6, stride=2, padding=1, kernel=3, complete=True).cuda().eval()
+    n = 128
+    bits = (torch.rand((n, 3, 12, 12), device="cuda") < 0.5)
+    y_float = layer(bits.float())
+    xp = cl.PackBitsTensor(bits.reshape(n, -1), 64)
+    out = layer(xp)
+    got = torch.stack([((out.t >> j) & 1) for j in range(64)], 0)  # [64, rows, words]
+    got = got.permute(2, 0, 1).reshape(-1, out.t.shape[0])[:n]
+    assert torch.equal(got.float(), y_float.reshape(n, -1))
+
+
+# ---- module tests in the pattern of the reference's own
+@pytest.mark.parametrize("stride,pad", [(1, 1), (2, 2)])
+def test_output_shape(stride, pad):
+    h_in = w_in = 11 + pad
+    layer = cl.ConvLogicLayer(3, 2, stride=stride, padding=pad, kernel=3, complete=True).cuda().eval()
+    y = layer(torch.randn(2, 3, h_in, w_in, device="cuda"))
+    h_out = (h_in + 2 * pad - 3) // stride + 1
+    assert y.shape == (2, 2, h_out // 2, h_out // 2)
+
+
+def test_range_determinism_and_irregular_channels():
+    torch.manual_seed(0)
+    layer = cl.ConvLogicLayer(1, 1, complete=True).cuda().eval()
+    x = torch.rand(3, 1, 6, 6, device="cuda")
+    y1, y2 = layer(x), layer(x)
+    assert torch.equal(y1, y2) and bool(((y1 >= 0) & (y1 <= 1)).all())
+    assert not torch.isnan(cl.ConvLogicLayer(2, 2, complete=True).cuda().eval()(
+        torch.randn(4, 2, 6, 6, device="cuda"))).any()
+    y = cl.ConvLogicLayer(1, 5, complete=True).cuda().eval()(torch.randn(1, 1, 6, 6, device="cuda"))
+    assert y.shape[1] == 5 and y.shape[-1] == 3
+    y = cl.ConvLogicLayer(1, 1, kernel=2, padding=0, complete=True).cuda().eval()(
+        torch.randn(1, 1, 3, 3, device="cuda"))
+    assert y.shape == (1, 1, 1, 1)
+
+
+def test_identity_init():
+    layer = cl.ConvLogicLayer(2, 2, residual_init=True, complete=True).cuda().eval()
+    assert bool((layer.weights.argmax(-1) == 3).all())
+    x = (torch.rand(2, 2, 6, 6, device="cuda") < 0.5).float()
+    # every node passes its first input: the block is the max over the window of tap 0
+    y = layer(x)
+    ch, r, c = TL.unpack_selection(layer.selection[:, 0].long())
+    xp = torch.nn.functional.pad(x, (1, 1, 1, 1))
+    for o in range(2):
+        tap = xp[:, ch[o], r[o]:r[o] + 6, c[o]:c[o] + 6]
+        assert torch.equal(y[:, o], torch.nn.functional.max_pool2d(tap, 2, 2))
+
+
+@pytest.mark.parametrize("stride,pad", [(1, 1), (2, 2)])
+def test_split_layers_vs_complete(stride, pad):
+    torch.manual_seed(0)
+    full = cl.ConvLogicLayer(3, 2, stride=stride, padding=pad, kernel=3, complete=True,
+                             return_indices=True, return_intermediate=True).cuda()
+    conv = cl.ConvLogicLayer(3, 2, stride=stride, padding=pad, kernel=3, complete=False).cuda()
+    tree1 = cl.TreeLogicLayer(2, 4).cuda()
+    tree2 = cl.TreeLogicLayer(2, 2).cuda()
+    pool = cl.PoolLogicLayer(return_indices=True)
+    conv.selection = full.selection
+    with torch.no_grad():
+        conv.weights.copy_(full.weights[:, 0:4])
+        tree1.weights.copy_(full.weights[:, 4:6])
+        tree2.weights.copy_(full.weights[:, 6:7])
+    x = torch.randn(4, 3, 10, 10, device="cuda")
+    with torch.no_grad():
+        y_full, x1_full, x2_full, idx_full = full(x)
+        x1 = conv(x)
+        x2 = tree1(x1)
+        y, idx = pool(tree2(x2))
+    assert torch.equal(idx.flatten(start_dim=2).to(torch.int32), idx_full)
+    torch.testing.assert_close(x1, x1_full, atol=1e-6, rtol=0)
+    torch.testing.assert_close(x2, x2_full, atol=1e-6, rtol=0)
+    torch.testing.assert_close(y, y_full, atol=1e-6, rtol=0)
+
+
+def test_module_gradients_match_oracle():
+    """Training mode through the module: softmax of the logits (torch), the block's kernels,
+    and the gradients of the logits and the input against the oracle chained with the softmax
+    Jacobian."""
+    torch.manual_seed(9)
+    layer = cl.ConvLogicLayer(4, 6, stride=2, padding=1, kernel=3, complete=True).cuda().double()
+    x = torch.rand(3, 4, 12, 12, device="cuda", dtype=torch.float64, requires_grad=True)
+    y = layer(x)
+    gy = torch.randn_like(y)
+    y.backward(gy)
+    w_prob = torch.softmax(layer.weights.detach(), -1)
+    rgx, rgw = T.block_backward(np_(x), np_(w_prob), np_(layer.selection), (2, 2), (1, 1), (3, 3),
+                                np_(gy))
+    np.testing.assert_allclose(np_(x.grad), rgx, rtol=1e-10, atol=1e-12)
+    p = np_(w_prob)
+    rgl = p * (rgw - (rgw * p).sum(-1, keepdims=True))
+    np.testing.assert_allclose(np_(layer.weights.grad), rgl, rtol=1e-10, atol=1e-12)
+
+
+def test_tree_layer_module_and_errors():
+    layer = cl.TreeLogicLayer(3, 4).cuda()
+    x = torch.rand(2, 3, 4, 4, 4, device="cuda", requires_grad=True)
+    y = layer(x)
+    assert y.shape == (2, 3, 4, 4, 2)
+    y.sum().backward()
+    assert x.grad is not None and layer.weights.grad.shape == (3, 2, 16)
+    with pytest.raises(AssertionError):
+        layer(torch.rand(2, 3, 4, 4, 6, device="cuda"))
+    with pytest.raises(RuntimeError):
+        TL.full_convlogic_forward(torch.rand(1, 1, 5, 5, device="cuda"),
+                                  torch.rand(1, 7, 16, device="cuda"),
+                                  torch.zeros(1, 8, dtype=torch.int32, device="cuda"),
+                                  1, 1, 1, 1, 3, 3)            # H_out = 5 is odd
+    with pytest.raises(ValueError):
+        TL.channel_uses(torch.tensor([[5 << 16] * 8], dtype=torch.int32, device="cuda"), 3)
+    with pytest.raises(ValueError):
+        cl.ConvLogicLayer(2, 2, implementation="python")
