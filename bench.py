@@ -12,11 +12,15 @@ Also reported on the same JSON line:
   cpu_baseline  the pure-PyTorch CPU step (oracle/torch_cpu.py) on a bounded sample
   conv_train    cfg3: conv 9x32x32 -> 256x16x16 -> 512x7x7, flatten, 2 x 16000 dense,
                 GroupSum(10, tau 30), batch 256, fp32 fwd + CE + bwd, same measurements
+  conv_tree_train  the logic-tree reading of cfg3: two complete ConvLogicLayer blocks (8 taps,
+                4 -> 2 -> 1 gates, 2x2 max pool) -> 512x2x2, flatten, 2 x 16000 dense, same step
   packed        cfg4: the cfg2 network frozen to argmax gates, 2^24 bit-packed samples,
                 layer-by-layer bitwise evaluation + popcount GroupSum, with its own roofline
                 and CPU (C oracle) baseline
   packed_conv   cfg5: the cfg3 network with 4 candidate gates per row, frozen, 2^20
                 bit-packed samples
+  packed_conv_tree  the cfg3_tree network frozen to argmax gates (pool = OR), 2^20 bit-packed
+                samples
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10]
 """
@@ -32,6 +36,8 @@ import time
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 CFG2_BYTES_PER_SAMPLE = 1_398_352
 CFG3_BYTES_PER_SAMPLE = 2_462_288
+CFG3_TREE_BYTES_PER_SAMPLE = 1_018_448
+CFG5_TREE_BYTES_PER_SAMPLE = 13_800
 CFG4_BYTES_PER_SAMPLE = 18_138
 CFG5_BYTES_PER_SAMPLE = 31_848
 
@@ -134,8 +140,20 @@ def bench_dense(args, torch):
 def train_kernel_bytes(model, batch: int) -> dict:
     import compactlogic_amd as cl
     out = {}
+    first = True
     for m in model:
-        if isinstance(m, cl.ConvLayer):
+        if isinstance(m, cl.ConvLogicLayer):
+            # complete block: forward reads x, writes the pooled y; backward reads x and
+            # grad_y and writes grad_x (not for the first module, whose input needs no gradient)
+            c, h, w = m._last_shape
+            tag = f"[{c}x{h}x{w}->{m.out_channels}]"
+            xb = 4 * batch * c * h * w
+            ho = (h + 2 * m.padding[0] - m.kernel[0]) // m.stride[0] + 1
+            wo = (w + 2 * m.padding[1] - m.kernel[1]) // m.stride[1] + 1
+            yb = 4 * batch * m.out_channels * (ho // 2) * (wo // 2)
+            out.update({"cl_tree_conv_forward" + tag: xb + yb,
+                        "cl_tree_conv_backward" + tag: (xb + yb) if first else (2 * xb + yb)})
+        elif isinstance(m, cl.ConvLayer):
             c, h, w = m.in_shape
             tag = f"[{c}x{h}x{w}->{m.c_out}]"
             xb = 4 * batch * c * h * w
@@ -157,7 +175,14 @@ def train_kernel_bytes(model, batch: int) -> dict:
             # layout change of a [batch, in_dim] input and of its gradient: read + write
             out[f"cl_transpose[{batch}x{m.in_dim}]"] = 2 * xb
             out[f"cl_transpose[{m.in_dim}x{batch}]"] = 2 * xb
+        if not isinstance(m, torch_flatten_types()):
+            first = False
     return out
+
+
+def torch_flatten_types():
+    import torch
+    return (torch.nn.Flatten,)
 
 
 def packed_kernel_bytes(model, words: int, k: int) -> dict:
@@ -167,7 +192,14 @@ def packed_kernel_bytes(model, words: int, k: int) -> dict:
     out = {}
     rows = None
     for m in model:
-        if isinstance(m, cl.ConvLayer):
+        if isinstance(m, cl.ConvLogicLayer):
+            c, h, w = m._last_shape
+            ho = (h + 2 * m.padding[0] - m.kernel[0]) // m.stride[0] + 1
+            wo = (w + 2 * m.padding[1] - m.kernel[1]) // m.stride[1] + 1
+            fin, fout = c * h * w, m.out_channels * (ho // 2) * (wo // 2)
+            out[f"cl_tree_conv_eval_packed[{fin}->{fout}]"] = (fin + fout) * words * 8
+            rows = fout
+        elif isinstance(m, cl.ConvLayer):
             fin = m.in_shape[0] * m.in_shape[1] * m.in_shape[2]
             out[f"cl_eval_packed_indexed[{fin}->{m.out_dim}]"] = (fin + m.out_dim) * words * 8
             rows = m.out_dim
@@ -278,6 +310,47 @@ def bench_conv(args, torch):
         "value": round(samples_s, 1), "unit": "samples/s", "steps": args.conv_steps,
         "warmup": args.conv_warmup, "ms_per_step": round(dt * 1e3, 4),
         "step_hbm_frac": round(CFG3_BYTES_PER_SAMPLE * samples_s / 1e9 / HBM_PEAK_GBS, 4),
+        "timed_path_matches_eager": matches,
+        "roofline": roofline_of(kernels, f"HIP events around each launch inside "
+                                         f"{args.kernel_steps} eager training steps"),
+        "kernels": kernels_json(kernels, args.kernel_steps),
+    }
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
+def annotate_block_shapes(model, in_shape):
+    """Record each ConvLogicLayer's input shape (for the byte accounting)."""
+    shape = tuple(in_shape)
+    for m in model:
+        if hasattr(m, "complete"):
+            m._last_shape = shape
+            ho = (shape[1] + 2 * m.padding[0] - m.kernel[0]) // m.stride[0] + 1
+            wo = (shape[2] + 2 * m.padding[1] - m.kernel[1]) // m.stride[1] + 1
+            shape = (m.out_channels, ho // 2, wo // 2)
+
+
+def bench_tree(args, torch):
+    """The logic-tree reading of cfg3: two complete ConvLogicLayer blocks, the dense layers and
+    GroupSum, trained like cfg3."""
+    from compactlogic_amd import configs
+    cfg = configs.TREE_CONFIGS["cfg3_tree"]
+    dev = torch.device("cuda:0")
+    model = configs.tree_network(cfg, device=dev)
+    x, labels = configs.conv_inputs(cfg, device=dev)
+    annotate_block_shapes(model, cfg.in_shape)
+    samples_s, dt, kernels, matches = bench_train(model, x, labels, args.conv_steps,
+                                                  args.conv_warmup, args.mode, args.kernel_steps,
+                                                  torch)
+    out = {
+        "workload": "cfg3_tree: ConvLogicLayer(9->256, ks 3, stride 2, pad 1, complete: 8 taps, "
+                    "4->2->1 gates, 2x2 max pool) -> 256x8x8 -> ConvLogicLayer(256->512) -> "
+                    "512x2x2, flatten, LogicLayer 2048->16000->16000, GroupSum(10, tau=30), "
+                    "batch 256, fp32 fwd+CE+bwd",
+        "value": round(samples_s, 1), "unit": "samples/s", "steps": args.conv_steps,
+        "warmup": args.conv_warmup, "ms_per_step": round(dt * 1e3, 4),
+        "step_hbm_frac": round(CFG3_TREE_BYTES_PER_SAMPLE * samples_s / 1e9 / HBM_PEAK_GBS, 4),
         "timed_path_matches_eager": matches,
         "roofline": roofline_of(kernels, f"HIP events around each launch inside "
                                          f"{args.kernel_steps} eager training steps"),
@@ -471,6 +544,10 @@ def main():
             log("cpu baseline (cfg3)")
             conv["cpu_baseline"] = cpu_baseline_train(torch, "cfg3")
         result["conv_train"] = conv
+        log(f"tree conv cfg3_tree: warmup={args.conv_warmup} steps={args.conv_steps}")
+        tree = bench_tree(args, torch)
+        log(f"tree conv cfg3_tree: {tree['value']:,.0f} samples/s, {tree['ms_per_step']:.3f} ms/step")
+        result["conv_tree_train"] = tree
     if not args.no_packed:
         log(f"packed cfg4: 2^{args.packed_log2_samples} samples x {args.packed_passes} passes")
         c2 = configs.CONFIGS["cfg2"]
@@ -514,6 +591,20 @@ def main():
                 log("cpu baseline (cfg5)")
                 pc["cpu_baseline"] = cpu_baseline_packed(torch, "cfg5")
             result["packed_conv"] = pc
+            log(f"packed cfg3_tree: 2^{args.conv_packed_log2_samples} samples")
+            ct = configs.TREE_CONFIGS["cfg3_tree"]
+            model = configs.tree_network(ct, device=torch.device("cuda:0"))
+            configs.freeze_argmax(model)
+            annotate_block_shapes(model, ct.in_shape)
+            pk = bench_packed_net(model, ct.in_shape[0] * ct.in_shape[1] * ct.in_shape[2],
+                                  args.conv_packed_log2_samples, args.packed_passes, ct.k, torch)
+            del model
+            pt = packed_json(pk, f"cfg3_tree frozen to argmax gates (pool = OR), "
+                                 f"2^{args.conv_packed_log2_samples} samples bit-packed 64 per "
+                                 "word, 2 packed ConvLogic blocks + 2 dense layers + popcount "
+                                 "GroupSum", CFG5_TREE_BYTES_PER_SAMPLE)
+            log(f"packed cfg3_tree: {pt['value']} Gsamples/s")
+            result["packed_conv_tree"] = pt
     print(json.dumps(result), flush=True)
 
 

@@ -26,6 +26,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .layers import ConvLayer, GroupSum, LogicLayer
+from .treelogic import ConvLogicLayer
 
 NET_SEED, INPUT_SEED, LABEL_SEED = 0, 1, 2
 
@@ -127,6 +128,54 @@ def conv_network(cfg: ConvConfig, device="cuda", seed: int = NET_SEED) -> torch.
             with torch.no_grad():
                 layer.gate_sequence.copy_(_gate_subsets(out_dim, cfg.num_gates, gen))
         layers.append(layer)
+        in_dim = out_dim
+    model = torch.nn.Sequential(*layers, GroupSum(cfg.k, cfg.tau))
+    return model.to(device)
+
+
+@dataclass
+class TreeConfig:
+    """The logic-tree reading of cfg3: ConvLogicLayer blocks (8 taps, 4 -> 2 -> 1 gates, 2x2 max
+    pool) in place of ConvLayer, then the dense layers and GroupSum."""
+    name: str
+    in_shape: tuple
+    blocks: list         # (c_out, ks, stride, padding) per complete ConvLogicLayer
+    widths: list
+    batch: int
+    p_one: float = 0.5
+    k: int = 10
+    tau: float = 30.0
+    num_gates: int = 16
+    num_chn: int = 2     # the ConvLogicLayer default
+
+
+TREE_CONFIGS = {
+    "cfg3_tree": TreeConfig("cfg3_tree", (9, 32, 32), [(256, 3, 2, 1), (512, 3, 2, 1)],
+                            [16000, 16000], 256),
+}
+
+
+def tree_network(cfg: TreeConfig, device="cuda", seed: int = NET_SEED) -> torch.nn.Sequential:
+    """(9,32,32) -> (256,8,8) -> (512,2,2) = 2048 -> 16000 -> 16000 -> GroupSum for cfg3_tree.
+    Block logits ~ N(0, 1); taps drawn by ConvLogicLayer's own sampler under a seeded RNG."""
+    gen = torch.Generator().manual_seed(seed)
+    layers = []
+    c, h, w = cfg.in_shape
+    for c_out, ks, stride, pad in cfg.blocks:
+        layer_seed = int(torch.randint(0, 2**31 - 1, (1,), generator=gen))
+        with torch.random.fork_rng(devices=[]):
+            torch.manual_seed(layer_seed)
+            layer = ConvLogicLayer(c, c_out, stride=stride, padding=pad, kernel=ks, complete=True,
+                                   num_chn=cfg.num_chn)
+        with torch.no_grad():
+            layer.weights.copy_(torch.randn(layer.weights.shape, generator=gen))
+        layers.append(layer)
+        ho, wo = (h + 2 * pad - ks) // stride + 1, (w + 2 * pad - ks) // stride + 1
+        c, h, w = c_out, ho // 2, wo // 2
+    layers.append(torch.nn.Flatten())
+    in_dim = c * h * w
+    for out_dim in cfg.widths:
+        layers.append(_seeded_layer(in_dim, out_dim, gen, cfg.num_gates))
         in_dim = out_dim
     model = torch.nn.Sequential(*layers, GroupSum(cfg.k, cfg.tau))
     return model.to(device)

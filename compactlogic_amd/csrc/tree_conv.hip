@@ -448,14 +448,35 @@ __global__ __launch_bounds__(256) void k_level_bwd(const T* __restrict__ grad_y,
 // (row = (ch * H + y) * W + x); output rows (c * Hp + py) * Wp + px (complete) or
 // ((c * Ho + oy) * Wo + ox) * 4 + q (conv gates only).  gates[c * nodes + q] is node q's opcode;
 // the pool of {0, 1} values is the OR of the window.
+//
+// Every input pixel is read by many output rows (all taps of all output channels that name
+// its channel), so the words are cut into chunks of kPkChunk and a workgroup evaluates
+// kPkRows output rows over one chunk.  Chunk j runs only on XCD j % 8 (workgroup w runs on XCD
+// w % 8), all row blocks of a chunk before the next chunk of that XCD: the chunk's slice of
+// the input (rows x 256 B) stays in the XCD's L2 while every output row reads it.
+constexpr int kPkChunk = 32;                 // words per chunk (one 256-byte row segment)
+constexpr int kPkRows = 256 / kPkChunk;      // output rows per workgroup
+
 __global__ __launch_bounds__(256) void k_tree_packed(const uint64_t* __restrict__ x, int64_t words,
                                                      const uint8_t* __restrict__ gates,
                                                      const int32_t* __restrict__ sel, TreeDims d,
+                                                     int64_t nchunks, int64_t rblocks,
                                                      uint64_t* __restrict__ y) {
-    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    int64_t chunk, rb;
+    const int64_t wg = blockIdx.x;
+    if (nchunks >= 8) {
+        const int64_t xcd = wg % 8, j = wg / 8;
+        chunk = xcd + 8 * (j / rblocks);
+        rb = j % rblocks;
+    } else {
+        chunk = wg / rblocks;
+        rb = wg % rblocks;
+    }
+    if (chunk >= nchunks) return;  // uniform per workgroup
+    const int64_t r = rb * kPkRows + threadIdx.x / kPkChunk;
+    const int64_t w = chunk * kPkChunk + threadIdx.x % kPkChunk;
     const int64_t rows = int64_t(d.cout) * d.P;
-    if (i >= rows * words) return;
-    const int64_t r = i / words, w = i % words;
+    if (r >= rows || w >= words) return;
     const int c = int(r / d.P), p = int(r % d.P);
     const int nodes = d.complete ? 7 : 4;
     int op[kMaxNodes];
@@ -491,13 +512,14 @@ __global__ __launch_bounds__(256) void k_tree_packed(const uint64_t* __restrict_
                 const uint64_t t1 = bitwise_op<uint64_t>(op[5], g[2], g[3]);
                 out |= bitwise_op<uint64_t>(op[6], t0, t1);
             }
-        y[i] = bad ? ~uint64_t(0) : out;
+        __builtin_nontemporal_store(bad ? ~uint64_t(0) : out, &y[r * words + w]);
     } else {
         const int q = p & 3, pos = p >> 2;
         const int oy = pos / d.wo, ox = pos % d.wo;
-        y[i] = bad ? ~uint64_t(0)
-                   : bitwise_op<uint64_t>(op[q], word_at(t[2 * q], oy, ox),
-                                          word_at(t[2 * q + 1], oy, ox));
+        const uint64_t v = bad ? ~uint64_t(0)
+                               : bitwise_op<uint64_t>(op[q], word_at(t[2 * q], oy, ox),
+                                                      word_at(t[2 * q + 1], oy, ox));
+        __builtin_nontemporal_store(v, &y[r * words + w]);
     }
 }
 
@@ -794,9 +816,11 @@ extern "C" int cl_tree_conv_eval_packed(const void* x, int64_t row_bytes, const 
     CL_ARG(x && gates && selection && y, "null pointer argument");
     CL_ARG(aligned(x, 8) && aligned(y, 8), "packed rows must be 8-byte aligned");
     if (!complete) d.P *= 4;  // one output row per (position, gate)
-    const int64_t total = rows * words;
-    CL_ARG(ceil_div(total, 256) < (int64_t(1) << 31), "tensor too large");
-    k_tree_packed<<<unsigned(ceil_div(total, 256)), 256, 0, as_stream(stream)>>>(
-        static_cast<const uint64_t*>(x), words, gates, selection, d, static_cast<uint64_t*>(y));
+    const int64_t nchunks = ceil_div(words, kPkChunk), rblocks = ceil_div(rows, kPkRows);
+    const int64_t grid = nchunks >= 8 ? 8 * ceil_div(nchunks, 8) * rblocks : nchunks * rblocks;
+    CL_ARG(grid < (int64_t(1) << 31), "tensor too large");
+    k_tree_packed<<<unsigned(grid), 256, 0, as_stream(stream)>>>(
+        static_cast<const uint64_t*>(x), words, gates, selection, d, nchunks, rblocks,
+        static_cast<uint64_t*>(y));
     return check_launch("cl_tree_conv_eval_packed");
 }

@@ -397,6 +397,7 @@ class LogicLayer(torch.nn.Module):
             x.t = timing.timed(f"cl_dense_eval_packed[{self.in_dim}->{self.out_dim}]",
                                lambda: _dl.eval_packed(x.t, a, b, w, self.gate_sequence))
             return x
+        assert x.shape[-1] == self.in_dim, (x.shape, self.in_dim)
         return _dl.eval(to_rows(x), a, b, w, self.gate_sequence).transpose(0, 1)
 
     def extra_repr(self):

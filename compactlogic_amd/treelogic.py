@@ -24,7 +24,7 @@ import torch
 from torch import nn
 from torch.autograd import Function
 
-from . import _capi
+from . import _capi, timing
 from . import difflogic_hip as _dl
 from .layers import PackBitsTensor
 
@@ -114,10 +114,11 @@ def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_
         x2 = torch.empty((n, c_out, ho, wo, 4), dtype=x.dtype, device=x.device)
         x3 = torch.empty((n, c_out, ho, wo, 2), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_tree_conv_forward", _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
-                   selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
-                   kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2), _dl.ptr(x3), idx.data_ptr(),
-                   _dl.stream_of(x))
+        timing.timed(f"cl_tree_conv_forward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
+            "cl_tree_conv_forward", _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
+            selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
+            kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2), _dl.ptr(x3), idx.data_ptr(),
+            _dl.stream_of(x)))
     return y, x2, x3, idx
 
 
@@ -163,12 +164,12 @@ def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w
                pad_w, kernel_h, kernel_w, int(complete), ctypes.byref(need))
     ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_tree_conv_backward", code, grad_y.data_ptr(), x.data_ptr(),
-                   w_prob.data_ptr(), selection.data_ptr(),
-                   indices.data_ptr() if complete else None, _dl.ptr(ptr), _dl.ptr(ent), n, c_in,
-                   h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
-                   int(complete), _dl.ptr(gx), _dl.ptr(gw), ws.data_ptr(), need.value,
-                   _dl.stream_of(x))
+        timing.timed(f"cl_tree_conv_backward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
+            "cl_tree_conv_backward", code, grad_y.data_ptr(), x.data_ptr(), w_prob.data_ptr(),
+            selection.data_ptr(), indices.data_ptr() if complete else None, _dl.ptr(ptr),
+            _dl.ptr(ent), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
+            kernel_w, int(complete), _dl.ptr(gx), _dl.ptr(gw), ws.data_ptr(), need.value,
+            _dl.stream_of(x)))
     return gx, gw
 
 
@@ -237,10 +238,11 @@ def tree_conv_eval_packed(x_words, gates, selection, in_shape, stride, padding, 
     rows = c_out * (ho // 2) * (wo // 2) if complete else c_out * ho * wo * 4
     y = torch.empty((rows, x_words.shape[1]), dtype=x_words.dtype, device=x_words.device)
     with torch.cuda.device(x_words.device):
-        _capi.call("cl_tree_conv_eval_packed", x_words.data_ptr(),
-                   x_words.shape[1] * x_words.element_size(), gates.data_ptr(),
-                   selection.data_ptr(), c_in, h, w, c_out, sh, sw, ph, pw, kh, kw,
-                   int(complete), y.data_ptr(), _dl.stream_of(x_words))
+        timing.timed(f"cl_tree_conv_eval_packed[{c_in * h * w}->{rows}]", lambda: _capi.call(
+            "cl_tree_conv_eval_packed", x_words.data_ptr(),
+            x_words.shape[1] * x_words.element_size(), gates.data_ptr(), selection.data_ptr(),
+            c_in, h, w, c_out, sh, sw, ph, pw, kh, kw, int(complete), y.data_ptr(),
+            _dl.stream_of(x_words)))
     return y
 
 

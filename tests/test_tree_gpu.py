@@ -247,3 +247,24 @@ def test_tree_layer_module_and_errors():
         TL.channel_uses(torch.tensor([[5 << 16] * 8], dtype=torch.int32, device="cuda"), 3)
     with pytest.raises(ValueError):
         cl.ConvLogicLayer(2, 2, implementation="python")
+
+
+def test_packed_tree_network_counts_match_float_eval():
+    """A frozen tree network (two complete blocks, flatten, dense, GroupSum) evaluated on packed
+    bits gives the class counts that the float eval gives as logits * tau (the
+    counts == round(logits * tau) check of simulation/consistency.py:241)."""
+    torch.manual_seed(11)
+    blocks = [cl.ConvLogicLayer(3, 8, stride=2, padding=1, kernel=3, complete=True),
+              cl.ConvLogicLayer(8, 16, stride=1, padding=1, kernel=3, complete=True)]
+    model = torch.nn.Sequential(*blocks, torch.nn.Flatten(), cl.LogicLayer(64, 120),
+                                cl.LogicLayer(120, 100), cl.GroupSum(5, 3.0)).cuda()
+    for m in model:
+        if isinstance(m, cl.LogicLayer):
+            m.freeze()
+    model.eval()
+    n = 300
+    bits = torch.rand((n, 3, 16, 16), device="cuda") < 0.5
+    logits = model(bits.float())
+    counts = model(cl.PackBitsTensor(bits.reshape(n, -1), 64))
+    assert counts.dtype == torch.int32 and counts.shape == (n, 5)
+    assert torch.equal(counts, torch.round(logits * 3.0).to(torch.int32))
