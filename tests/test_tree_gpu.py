@@ -118,10 +118,15 @@ def test_tree_level_matches_oracle(dtype):
 
 
 @pytest.mark.parametrize("complete", [True, False])
-def test_packed_block_matches_bit_oracle(complete):
+@pytest.mark.parametrize("c_in,h,w,stride,pad,kernel,words", [
+    (9, 32, 32, (2, 2), (1, 1), (3, 3), 5),     # conv1 of the tree reading, partial chunk
+    (3, 12, 12, (2, 2), (1, 1), (3, 3), 33),    # 3 x 3 windows, two chunks
+    (2, 10, 10, (1, 1), (1, 1), (3, 3), 17),    # stride 1
+    (16, 8, 8, (2, 2), (1, 1), (3, 3), 40),     # conv2 of the tree reading
+])
+def test_packed_block_matches_bit_oracle(complete, c_in, h, w, stride, pad, kernel, words):
     rng = np.random.default_rng(6)
-    c_in, h, w, c_out, words = 9, 32, 32, 12, 5
-    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    c_out = 12
     nodes = 7 if complete else 4
     xw = rng.integers(0, 2**63, (c_in * h * w, words), dtype=np.int64).view(np.uint64)
     gates = rng.integers(0, 16, (c_out, nodes)).astype(np.uint8)
