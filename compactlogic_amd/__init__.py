@@ -2,7 +2,9 @@
 
 Same public modules as the reference package `compactlogic` (compactlogic/__init__.py:1):
 LogicLayer, ConvLayer, GroupSum and the autograd bridges LogicLayerCudaFunction and
-ConvLayerCudaFunction, plus the packed-bit inference API (PackBitsTensor).  All numerics run in libcompactlogic_hip.so, built in-tree by
+ConvLayerCudaFunction, plus the packed-bit inference API (PackBitsTensor), and the logic-tree
+conv blocks of the third-party ConvLogic package (ConvLogicLayer, TreeLogicLayer,
+PoolLogicLayer).  All numerics run in libcompactlogic_hip.so, built in-tree by
 ``python -m compactlogic_amd.build``.
 """
 from . import convlogic_hip, difflogic_hip
