@@ -31,6 +31,8 @@ namespace {
 
 constexpr int kTaps = 8;
 constexpr int kMaxNodes = 7;
+constexpr int kGatherBatch = 4;  // channel uses whose loads the input-gradient gather overlaps
+constexpr int kNodeItems = 4;    // items per thread of the backward node kernel
 
 template <typename T>
 __device__ __forceinline__ T quiet_nan() {
@@ -202,20 +204,22 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
     load_channel(w_prob, sel, c, NODES, d, sk, st, &bad);
     __syncthreads();
     if (blockIdx.x == 0 && threadIdx.x < NM) kc[int64_t(c) * NM + threadIdx.x] = sk[threadIdx.x >> 2][threadIdx.x & 3];
-    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
     T mom[NM];
 #pragma unroll
     for (int i = 0; i < NM; ++i) mom[i] = T(0);
-    if (item < int64_t(d.n) * d.P) {
+    // kNodeItems items per thread (strided by the workgroup size), so the moments of that many
+    // items are summed in registers before the wave reductions
+    for (int it = 0; it < kNodeItems; ++it) {
+        const int64_t item = (int64_t(blockIdx.x) * kNodeItems + it) * 256 + threadIdx.x;
+        if (item >= int64_t(d.n) * d.P) break;
         const int n = int(item / d.P), p = int(item % d.P);
         const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
         const int64_t cell = int64_t(n) * d.cout + c;
         T gc[4];
         Eval<T, COMPLETE> e;
-        bool live = true;
         if constexpr (COMPLETE) {
             const int win = idx[cell * d.P + p];
-            live = win >= 0 && win < d.ho * d.wo;
+            const bool live = win >= 0 && win < d.ho * d.wo;
             const int w0 = live ? win : 0;
             eval_at<T, true>(xn, d, st, sk, w0 / d.wo, w0 % d.wo, e);
             const T gy = live ? grad_y[cell * d.P + p] : T(0);
@@ -225,22 +229,21 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
             gc[1] = gt0 * fma(sk[4][3], e.g[0], sk[4][2]);
             gc[2] = gt1 * fma(sk[5][3], e.g[3], sk[5][1]);
             gc[3] = gt1 * fma(sk[5][3], e.g[2], sk[5][2]);
-            const T* gn = gc;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gn[q];
+            for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gc[q];
             const T gts[2] = {gt0, gt1};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const T a = e.g[2 * j], b = e.g[2 * j + 1], g = gts[j];
-                mom[(4 + j) * 4 + 0] = g * a * b;
-                mom[(4 + j) * 4 + 1] = g * a;
-                mom[(4 + j) * 4 + 2] = g * b;
-                mom[(4 + j) * 4 + 3] = g;
+                mom[(4 + j) * 4 + 0] += g * a * b;
+                mom[(4 + j) * 4 + 1] += g * a;
+                mom[(4 + j) * 4 + 2] += g * b;
+                mom[(4 + j) * 4 + 3] += g;
             }
-            mom[24] = gy * e.t[0] * e.t[1];
-            mom[25] = gy * e.t[0];
-            mom[26] = gy * e.t[1];
-            mom[27] = gy;
+            mom[24] += gy * e.t[0] * e.t[1];
+            mom[25] += gy * e.t[0];
+            mom[26] += gy * e.t[1];
+            mom[27] += gy;
         } else {
             const int oy = p / d.wo, ox = p % d.wo;
             eval_at<T, false>(xn, d, st, sk, oy, ox, e);
@@ -250,10 +253,10 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const T a = e.v[2 * q], b = e.v[2 * q + 1], g = gc[q];
-            mom[q * 4 + 0] = g * a * b;
-            mom[q * 4 + 1] = g * a;
-            mom[q * 4 + 2] = g * b;
-            mom[q * 4 + 3] = g;
+            mom[q * 4 + 0] += g * a * b;
+            mom[q * 4 + 1] += g * a;
+            mom[q * 4 + 2] += g * b;
+            mom[q * 4 + 3] += g;
         }
     }
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -310,25 +313,47 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
         // trip count uniform over the wave: the largest use count of its groups
         int cnt = e1 - e0;
         for (int off = 32; off > 0; off >>= 1) cnt = max(cnt, __shfl_xor(cnt, off, 64));
-        for (int j = 0; j < cnt; ++j) {
-            const bool on = j < e1 - e0;
-            const int u = on ? ent[e0 + j] : 0;
-            const int c = u >> 3, k = u & 7;
-            const TapOff tk = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
-            const TapOff tp = decode_tap(sel[c * kTaps + (k ^ 1)], d.ph, d.pw);
-            const T* kq = kc + (int64_t(c) * NODES + (k >> 1)) * 4;
-            const T kown = (k & 1) ? kq[2] : kq[1], k3 = kq[3];
-            const int64_t cell = int64_t(n) * d.cout + c;
-            for (int p = pl; on && p < d.P; p += PW) {
-                int win = p;
-                if constexpr (COMPLETE) win = idx[cell * d.P + p];
-                if (win < 0 || win >= d.ho * d.wo) continue;
-                const int oy = win / d.wo, ox = win % d.wo;
-                const int iy = oy * d.sh + tk.dy, ix = ox * d.sw + tk.dx;
-                if (iy < 0 || iy >= d.h || ix < 0 || ix >= d.w) continue;
-                const T xp = tap_value(xn, d, tp, oy, ox);
-                const T g = gsrc[(cell * d.P + p) * 4 + (k >> 1)];
-                atomicAdd(&gx[(ch - ch0) * hw + iy * d.w + ix], g * fma(k3, xp, kown));
+        // uses in batches of kGatherBatch: the records, coefficients and gradients of a batch
+        // are loaded together, then its additions are applied in use order
+        for (int j = 0; j < cnt; j += kGatherBatch) {
+            bool on[kGatherBatch];
+            TapOff tk[kGatherBatch], tp[kGatherBatch];
+            T kown[kGatherBatch], k3[kGatherBatch];
+            int64_t cell[kGatherBatch];
+            int kn[kGatherBatch];
+#pragma unroll
+            for (int i = 0; i < kGatherBatch; ++i) {
+                on[i] = j + i < e1 - e0;
+                const int u = on[i] ? ent[e0 + j + i] : 0;
+                const int c = u >> 3, k = u & 7;
+                tk[i] = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
+                tp[i] = decode_tap(sel[c * kTaps + (k ^ 1)], d.ph, d.pw);
+                const T* kq = kc + (int64_t(c) * NODES + (k >> 1)) * 4;
+                kown[i] = (k & 1) ? kq[2] : kq[1];
+                k3[i] = kq[3];
+                cell[i] = int64_t(n) * d.cout + c;
+                kn[i] = k >> 1;
+            }
+            for (int p = pl; p < d.P; p += PW) {
+                int tgt[kGatherBatch];
+                T add[kGatherBatch];
+#pragma unroll
+                for (int i = 0; i < kGatherBatch; ++i) {
+                    int win = p;
+                    if constexpr (COMPLETE) win = on[i] ? idx[cell[i] * d.P + p] : -1;
+                    const bool wok = on[i] && win >= 0 && win < d.ho * d.wo;
+                    const int w0 = wok ? win : 0;
+                    const int oy = w0 / d.wo, ox = w0 % d.wo;
+                    const int iy = oy * d.sh + tk[i].dy, ix = ox * d.sw + tk[i].dx;
+                    const bool ok = wok && iy >= 0 && iy < d.h && ix >= 0 && ix < d.w;
+                    tgt[i] = ok ? iy * d.w + ix : -1;
+                    const T xp = ok ? tap_value(xn, d, tp[i], oy, ox) : T(0);
+                    const T g = ok ? gsrc[(cell[i] * d.P + p) * 4 + kn[i]] : T(0);
+                    add[i] = g * fma(k3[i], xp, kown[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < kGatherBatch; ++i)
+                    if (tgt[i] >= 0) atomicAdd(&gx[(ch - ch0) * hw + tgt[i]], add[i]);
             }
         }
     }
@@ -586,7 +611,7 @@ constexpr int64_t kGatherLdsBytes = 64 * 1024;
 template <typename T>
 int64_t tree_workspace_bytes(const TreeDims& d) {
     const int nodes = d.complete ? 7 : 4;
-    const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256);
+    const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256 * kNodeItems);
     int64_t b = 0;
     if (d.complete) b += int64_t(d.n) * d.cout * d.P * 4 * sizeof(T);  // gconv
     b = (b + 255) / 256 * 256;
@@ -679,7 +704,7 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
         CL_ARG(workspace && workspace_bytes >= need,
                "workspace of %lld bytes needed (see cl_tree_conv_workspace)", (long long)need);
         CL_ARG(aligned(workspace, 256), "workspace must be 256-byte aligned");
-        const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256);
+        const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256 * kNodeItems);
         unsigned char* ws = static_cast<unsigned char*>(workspace);
         T* gconv = nullptr;
         int64_t off = 0;
@@ -713,17 +738,21 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
             CL_ARG(hw_bytes <= kGatherLdsBytes,
                    "input planes of more than %lld bytes are not supported by the input gradient",
                    (long long)kGatherLdsBytes);
-            const int cg = int(std::min<int64_t>(d.cin, kGatherLdsBytes / hw_bytes));
+            // one pass of the workgroup's lane groups per channel group: more workgroups
+            // (each staging only its channels) keep more waves in flight
+            const int pw_lanes = gather_lanes(d.P);
+            const int cg = int(std::min<int64_t>(std::min<int64_t>(d.cin, 4 * (64 / pw_lanes)),
+                                                 kGatherLdsBytes / hw_bytes));
             const dim3 g2(unsigned(d.n), unsigned(ceil_div(d.cin, cg)));
             const size_t lds = size_t(cg) * size_t(hw_bytes);
             const T* src = complete ? gconv : gy;
             if (complete)
                 k_tree_gather<T, true><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
-                                                            ent, kc, d, cg, gather_lanes(d.P),
+                                                            ent, kc, d, cg, pw_lanes,
                                                             static_cast<T*>(grad_x));
             else
                 k_tree_gather<T, false><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
-                                                             ent, kc, d, cg, gather_lanes(d.P),
+                                                             ent, kc, d, cg, pw_lanes,
                                                              static_cast<T*>(grad_x));
             if (int rc = check_launch("cl_tree_conv_backward(gather)")) return rc;
         }
