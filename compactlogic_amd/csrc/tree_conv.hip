@@ -58,12 +58,17 @@ __device__ __forceinline__ TapOff decode_tap(int32_t s, int ph, int pw) {
     return t;
 }
 
+// Tap value at conv position (oy, ox), zero outside the image.  Branch-free: the load always
+// goes to an address inside the sample (element 0 when the tap is outside) and the value is
+// selected afterwards, so 32 taps do not become 32 divergent branches.
 template <typename T>
 __device__ __forceinline__ T tap_value(const T* __restrict__ xn, const TreeDims& d, const TapOff& t,
                                        int oy, int ox) {
     const int iy = oy * d.sh + t.dy, ix = ox * d.sw + t.dx;
-    if (iy < 0 || iy >= d.h || ix < 0 || ix >= d.w || t.ch >= d.cin) return T(0);
-    return xn[(int64_t(t.ch) * d.h + iy) * d.w + ix];
+    const bool ok = uint32_t(iy) < uint32_t(d.h) && uint32_t(ix) < uint32_t(d.w) &&
+                    uint32_t(t.ch) < uint32_t(d.cin);
+    const T v = xn[ok ? (t.ch * d.h + iy) * d.w + ix : 0];
+    return ok ? v : T(0);
 }
 
 template <typename T>
@@ -176,6 +181,74 @@ __global__ __launch_bounds__(256) void k_tree_fwd(const T* __restrict__ x, const
         const int64_t pos = cell * d.P + p;
 #pragma unroll
         for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? nan : e.g[q];
+    }
+}
+
+// Complete block, quad form: one thread per conv position, the four positions of a pooling
+// window in the four lanes of a quad (lane order (0,0), (0,1), (1,0), (1,1)), so each thread
+// gathers 8 taps instead of 32 and the pool is two quad-DPP steps that keep the earlier lane
+// on ties (strict >, as the first-maximum rule).  Lane 0 of the quad stores y and the winner.
+template <typename T>
+__global__ __launch_bounds__(256) void k_tree_fwd_q(const T* __restrict__ x, const T* __restrict__ w_prob,
+                                                    const int32_t* __restrict__ sel, TreeDims d,
+                                                    T* __restrict__ y, T* __restrict__ x2,
+                                                    T* __restrict__ x3, int32_t* __restrict__ idx) {
+    __shared__ T sk[kMaxNodes][4];
+    __shared__ TapOff st[kTaps];
+    __shared__ int bad;
+    const int c = blockIdx.y;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    load_channel(w_prob, sel, c, 7, d, sk, st, &bad);
+    __syncthreads();
+    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (n, window) * 4 + q
+    const int64_t total = int64_t(d.n) * d.P * 4;
+    const bool live = item < total;
+    const int64_t it = live ? item : 0;
+    const int q = int(it & 3);
+    const int64_t win = it >> 2;
+    const int n = int(win / d.P), p = int(win % d.P);
+    const int wp = d.wo / 2;
+    const int oy = 2 * (p / wp) + (q >> 1), ox = 2 * (p % wp) + (q & 1);
+    const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
+    Eval<T, true> e;
+    eval_at<T, true>(xn, d, st, sk, oy, ox, e);
+    const int64_t cell = int64_t(n) * d.cout + c;
+    const T nan = quiet_nan<T>();
+    if (live) {
+        const int64_t pos = cell * d.ho * d.wo + int64_t(oy) * d.wo + ox;
+        if (x2) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x2[pos * 4 + k] = bad ? nan : e.g[k];
+        }
+        if (x3) {
+            x3[pos * 2 + 0] = bad ? nan : e.t[0];
+            x3[pos * 2 + 1] = bad ? nan : e.t[1];
+        }
+    }
+    // first maximum over the quad: (0 vs 1), (2 vs 3), then (01 vs 23); the later lane wins
+    // only when strictly greater.  A NaN never wins (it enters as -inf with winner -1), so a
+    // window of NaNs keeps the reference's -inf / -1.
+    const bool num = e.r == e.r;
+    T r = num ? e.r : -T(__builtin_inf());
+    int wi = num ? oy * d.wo + ox : -1;
+    {
+        const T ro = dpp_move<0xB1>(r);        // quad_perm [1,0,3,2]
+        const int wo_ = dpp_move<0xB1>(wi);
+        const bool take = (q & 1) ? !(r > ro) : (ro > r);  // odd lane: partner is the earlier one
+        r = take ? ro : r;
+        wi = take ? wo_ : wi;
+    }
+    {
+        const T ro = dpp_move<0x4E>(r);        // quad_perm [2,3,0,1]
+        const int wo_ = dpp_move<0x4E>(wi);
+        const bool take = (q & 2) ? !(r > ro) : (ro > r);
+        r = take ? ro : r;
+        wi = take ? wo_ : wi;
+    }
+    if (live && q == 0) {
+        y[cell * d.P + p] = bad ? nan : r;
+        if (idx) idx[cell * d.P + p] = wi;
     }
 }
 
@@ -580,6 +653,7 @@ int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t
                "pooling, but got H_out=%lld, W_out=%lld",
                (long long)ho, (long long)wo);
     const int64_t P = complete ? (ho / 2) * (wo / 2) : ho * wo;
+    CL_ARG(cin * h * w < (int64_t(1) << 31), "one sample's input must have fewer than 2^31 elements");
     CL_ARG(n * cin * h * w < (int64_t(1) << 40) && cout * P < (int64_t(1) << 31) &&
                n * P < (int64_t(1) << 40) && cout < 65536,
            "block too large");
@@ -644,10 +718,12 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
-        if (complete)
-            k_tree_fwd<T, true><<<grid, 256, 0, s>>>(
+        if (complete) {
+            const unsigned gq = unsigned(ceil_div(int64_t(d.n) * d.P * 4, 256));
+            k_tree_fwd_q<T><<<dim3(gq, unsigned(d.cout)), 256, 0, s>>>(
                 static_cast<const T*>(x), static_cast<const T*>(w_prob), selection, d,
                 static_cast<T*>(y), static_cast<T*>(x2), static_cast<T*>(x3), indices);
+        }
         else
             k_tree_fwd<T, false><<<grid, 256, 0, s>>>(
                 static_cast<const T*>(x), static_cast<const T*>(w_prob), selection, d,
