@@ -124,64 +124,29 @@ __device__ __forceinline__ void eval_at(const T* __restrict__ xn, const TreeDims
 }
 
 // ------------------------------------------------------------------------------------------
-// Forward: one thread per (sample, pooled window) (complete) or (sample, conv position), the
-// workgroup's channel in blockIdx.y.
-template <typename T, bool COMPLETE>
+// Forward of the conv gates alone: one thread per (sample, conv position) of the workgroup's
+// channel (blockIdx.y); y [N, C, Ho, Wo, 4].
+template <typename T>
 __global__ __launch_bounds__(256) void k_tree_fwd(const T* __restrict__ x, const T* __restrict__ w_prob,
                                                   const int32_t* __restrict__ sel, TreeDims d,
-                                                  T* __restrict__ y, T* __restrict__ x2,
-                                                  T* __restrict__ x3, int32_t* __restrict__ idx) {
-    constexpr int NODES = COMPLETE ? 7 : 4;
+                                                  T* __restrict__ y) {
     __shared__ T sk[kMaxNodes][4];
     __shared__ TapOff st[kTaps];
     __shared__ int bad;
     const int c = blockIdx.y;
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();
-    load_channel(w_prob, sel, c, NODES, d, sk, st, &bad);
+    load_channel(w_prob, sel, c, 4, d, sk, st, &bad);
     __syncthreads();
     const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (item >= int64_t(d.n) * d.P) return;
     const int n = int(item / d.P), p = int(item % d.P);
     const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
-    const T nan = quiet_nan<T>();
-    const int64_t cell = int64_t(n) * d.cout + c;  // (n, c)
-    if constexpr (COMPLETE) {
-        const int wp = d.wo / 2;
-        const int py = p / wp, px = p % wp;
-        T best = -T(__builtin_inf());
-        int bidx = -1;
+    Eval<T, false> e;
+    eval_at<T, false>(xn, d, st, sk, p / d.wo, p % d.wo, e);
+    const int64_t pos = (int64_t(n) * d.cout + c) * d.P + p;
 #pragma unroll
-        for (int dy2 = 0; dy2 < 2; ++dy2)
-#pragma unroll
-            for (int dx2 = 0; dx2 < 2; ++dx2) {
-                const int oy = 2 * py + dy2, ox = 2 * px + dx2;
-                Eval<T, true> e;
-                eval_at<T, true>(xn, d, st, sk, oy, ox, e);
-                const int64_t pos = cell * d.ho * d.wo + int64_t(oy) * d.wo + ox;
-                if (x2) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) x2[pos * 4 + q] = bad ? nan : e.g[q];
-                }
-                if (x3) {
-                    x3[pos * 2 + 0] = bad ? nan : e.t[0];
-                    x3[pos * 2 + 1] = bad ? nan : e.t[1];
-                }
-                if (e.r > best) {
-                    best = e.r;
-                    bidx = oy * d.wo + ox;
-                }
-            }
-        y[cell * d.P + p] = bad ? nan : best;
-        if (idx) idx[cell * d.P + p] = bidx;
-    } else {
-        const int oy = p / d.wo, ox = p % d.wo;
-        Eval<T, false> e;
-        eval_at<T, false>(xn, d, st, sk, oy, ox, e);
-        const int64_t pos = cell * d.P + p;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? nan : e.g[q];
-    }
+    for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? quiet_nan<T>() : e.g[q];
 }
 
 // Complete block, quad form: one thread per conv position, the four positions of a pooling
@@ -725,9 +690,9 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
                 static_cast<T*>(y), static_cast<T*>(x2), static_cast<T*>(x3), indices);
         }
         else
-            k_tree_fwd<T, false><<<grid, 256, 0, s>>>(
-                static_cast<const T*>(x), static_cast<const T*>(w_prob), selection, d,
-                static_cast<T*>(y), nullptr, nullptr, nullptr);
+            k_tree_fwd<T><<<grid, 256, 0, s>>>(static_cast<const T*>(x),
+                                               static_cast<const T*>(w_prob), selection, d,
+                                               static_cast<T*>(y));
     });
     return check_launch("cl_tree_conv_forward");
 }
