@@ -513,77 +513,162 @@ __global__ __launch_bounds__(256) void k_level_bwd(const T* __restrict__ grad_y,
 // the pool of {0, 1} values is the OR of the window.
 //
 // Every input pixel is read by many output rows (all taps of all output channels that name
-// its channel), so the words are cut into chunks of kPkChunk and a workgroup evaluates
-// kPkRows output rows over one chunk.  Chunk j runs only on XCD j % 8 (workgroup w runs on XCD
+// its channel), so the words are cut into chunks of kPkChunk and a workgroup evaluates a block
+// of output rows over one chunk.  Chunk j runs only on XCD j % 8 (workgroup w runs on XCD
 // w % 8), all row blocks of a chunk before the next chunk of that XCD: the chunk's slice of
 // the input (rows x 256 B) stays in the XCD's L2 while every output row reads it.
-constexpr int kPkChunk = 32;                 // words per chunk (one 256-byte row segment)
-constexpr int kPkRows = 256 / kPkChunk;      // output rows per workgroup
+//
+// A lane holds WPL consecutive words of one row (WPL = 2: 16-byte loads and stores), so a
+// row's opcodes, tap offsets and bounds are worked out once per WPL words.  Tap loads are
+// unconditional (a tap outside the image reads row 0 and is masked to zero afterwards) and the
+// row index is 32-bit (the input holds fewer than 2^31 rows), leaving one 64-bit multiply-add
+// per load.
+constexpr int kPkChunk = 32;  // words per chunk (one 256-byte row segment)
 
-__global__ __launch_bounds__(256) void k_tree_packed(const uint64_t* __restrict__ x, int64_t words,
-                                                     const uint8_t* __restrict__ gates,
-                                                     const int32_t* __restrict__ sel, TreeDims d,
-                                                     int64_t nchunks, int64_t rblocks,
-                                                     uint64_t* __restrict__ y) {
-    int64_t chunk, rb;
-    const int64_t wg = blockIdx.x;
-    if (nchunks >= 8) {
-        const int64_t xcd = wg % 8, j = wg / 8;
-        chunk = xcd + 8 * (j / rblocks);
-        rb = j % rblocks;
-    } else {
-        chunk = wg / rblocks;
-        rb = wg % rblocks;
-    }
-    if (chunk >= nchunks) return;  // uniform per workgroup
-    const int64_t r = rb * kPkRows + threadIdx.x / kPkChunk;
-    const int64_t w = chunk * kPkChunk + threadIdx.x % kPkChunk;
-    const int64_t rows = int64_t(d.cout) * d.P;
-    if (r >= rows || w >= words) return;
-    const int c = int(r / d.P), p = int(r % d.P);
-    const int nodes = d.complete ? 7 : 4;
-    int op[kMaxNodes];
+// Opcode g as four minterm masks: result bit = m[a][b] of the (a, b) bit pair.
+struct GateMask {
+    uint32_t m00, m01, m10, m11;
+};
+
+__device__ __forceinline__ GateMask gate_mask(int g) {
+    GateMask m;
+    m.m00 = 0u - uint32_t((g >> 3) & 1);
+    m.m01 = 0u - uint32_t((g >> 2) & 1);
+    m.m10 = 0u - uint32_t((g >> 1) & 1);
+    m.m11 = 0u - uint32_t(g & 1);
+    return m;
+}
+
+template <int N>
+struct Bits {
+    uint32_t v[N];
+};
+
+template <int N>
+__device__ __forceinline__ Bits<N> apply_gate(const GateMask& m, const Bits<N>& a,
+                                              const Bits<N>& b) {
+    Bits<N> o;
 #pragma unroll
-    for (int q = 0; q < kMaxNodes; ++q) op[q] = q < nodes ? (gates[c * nodes + q] & 15) : 0;
-    TapOff t[kTaps];
+    for (int i = 0; i < N; ++i) {
+        const uint32_t if_b = (a.v[i] & m.m11) | (~a.v[i] & m.m01);
+        const uint32_t if_not_b = (a.v[i] & m.m10) | (~a.v[i] & m.m00);
+        o.v[i] = (b.v[i] & if_b) | (~b.v[i] & if_not_b);
+    }
+    return o;
+}
+
+template <int WPL>
+__device__ __forceinline__ Bits<2 * WPL> load_words(const uint64_t* p, uint32_t mask) {
+    Bits<2 * WPL> r;
+    if constexpr (WPL == 2) {
+        const uint4 q = *reinterpret_cast<const uint4*>(p);
+        r.v[0] = q.x & mask, r.v[1] = q.y & mask, r.v[2] = q.z & mask, r.v[3] = q.w & mask;
+    } else {
+        const uint2 q = *reinterpret_cast<const uint2*>(p);
+        r.v[0] = q.x & mask, r.v[1] = q.y & mask;
+    }
+    return r;
+}
+
+template <int WPL>
+__device__ __forceinline__ void store_words(uint64_t* p, const Bits<2 * WPL>& r) {
+    if constexpr (WPL == 2) {
+        *reinterpret_cast<uint4*>(p) = make_uint4(r.v[0], r.v[1], r.v[2], r.v[3]);
+    } else {
+        *reinterpret_cast<uint2*>(p) = make_uint2(r.v[0], r.v[1]);
+    }
+}
+
+// At most four waves per SIMD: the tap offsets, gate masks and loaded words then fit in
+// registers without scratch.
+template <int WPL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_tree_packed(
+    const uint64_t* __restrict__ x, int64_t words, const uint8_t* __restrict__ gates,
+    const int32_t* __restrict__ sel, TreeDims d, int64_t nchunks, int64_t rblocks,
+    uint64_t* __restrict__ y) {
+    constexpr int kLanes = kPkChunk / WPL;  // lanes per row segment
+    constexpr int kRows = 256 / kLanes;     // output rows per workgroup
+    constexpr int N = 2 * WPL;              // 32-bit halves per lane
+    // Grid, row and chunk counts are below 2^31 (checked by the caller): 32-bit index math.
+    uint32_t chunk, rb;
+    const uint32_t wg = blockIdx.x, nrb = uint32_t(rblocks);
+    if (nchunks >= 8) {
+        const uint32_t j = wg / 8;
+        chunk = wg % 8 + 8 * (j / nrb);
+        rb = j % nrb;
+    } else {
+        chunk = wg / nrb;
+        rb = wg % nrb;
+    }
+    if (chunk >= uint32_t(nchunks)) return;  // uniform per workgroup
+    const uint32_t r = rb * kRows + threadIdx.x / kLanes;
+    const int64_t w = int64_t(chunk) * kPkChunk + (threadIdx.x % kLanes) * WPL;
+    if (r >= uint32_t(d.cout) * uint32_t(d.P) || w >= words) return;
+    const int c = int(r / uint32_t(d.P)), p = int(r % uint32_t(d.P));
+    const int nodes = d.complete ? 7 : 4;
     bool bad = false;
 #pragma unroll
-    for (int k = 0; k < kTaps; ++k) {
-        t[k] = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
-        bad |= t[k].ch >= d.cin;
-    }
-    auto word_at = [&](const TapOff& tk, int oy, int ox) -> uint64_t {
-        const int iy = oy * d.sh + tk.dy, ix = ox * d.sw + tk.dx;
-        if (iy < 0 || iy >= d.h || ix < 0 || ix >= d.w || tk.ch >= d.cin) return 0;
-        return x[((int64_t(tk.ch) * d.h + iy) * d.w + ix) * words + w];
+    for (int k = 0; k < kTaps; ++k) bad |= ((sel[c * kTaps + k] >> 16) & 0xFFFF) >= d.cin;
+    const char* xw = reinterpret_cast<const char*>(x + w);
+    const uint32_t row_stride = uint32_t(words) * 8u;  // bytes; words < 2^28 (caller)
+    // Tap value at conv position (oy, ox).  Row arithmetic is unsigned 32-bit: for a tap inside
+    // the image the wrapped sum equals the row (ch * H + iy) * W + ix < 2^31.
+    auto tap = [&](const TapOff& t, uint32_t base, int oy, int ox) -> Bits<N> {
+        const int iy = oy * d.sh + t.dy, ix = ox * d.sw + t.dx;
+        const bool ok = (!bad) & (unsigned(iy) < unsigned(d.h)) & (unsigned(ix) < unsigned(d.w));
+        const uint32_t row = ok ? base + uint32_t(oy * d.sh) * uint32_t(d.w) + uint32_t(ox * d.sw)
+                                : 0u;
+        return load_words<WPL>(
+            reinterpret_cast<const uint64_t*>(xw + uint64_t(row) * uint64_t(row_stride)),
+            ok ? ~0u : 0u);
     };
+    auto plane_base = [&](const TapOff& t) -> uint32_t {
+        return (uint32_t(t.ch) * uint32_t(d.h) + uint32_t(t.dy)) * uint32_t(d.w) + uint32_t(t.dx);
+    };
+    Bits<N> out;
     if (d.complete) {
+        GateMask gm[kMaxNodes];
+#pragma unroll
+        for (int q = 0; q < kMaxNodes; ++q) gm[q] = gate_mask(gates[c * nodes + q] & 15);
+        TapOff t[kTaps];
+        uint32_t base[kTaps];
+#pragma unroll
+        for (int k = 0; k < kTaps; ++k) {
+            t[k] = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
+            base[k] = plane_base(t[k]);
+        }
         const int wp = d.wo / 2;
         const int py = p / wp, px = p % wp;
-        uint64_t out = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i) out.v[i] = 0;
 #pragma unroll
         for (int dy2 = 0; dy2 < 2; ++dy2)
 #pragma unroll
             for (int dx2 = 0; dx2 < 2; ++dx2) {
                 const int oy = 2 * py + dy2, ox = 2 * px + dx2;
-                uint64_t g[4];
+                Bits<N> g[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    g[q] = bitwise_op<uint64_t>(op[q], word_at(t[2 * q], oy, ox),
-                                                word_at(t[2 * q + 1], oy, ox));
-                const uint64_t t0 = bitwise_op<uint64_t>(op[4], g[0], g[1]);
-                const uint64_t t1 = bitwise_op<uint64_t>(op[5], g[2], g[3]);
-                out |= bitwise_op<uint64_t>(op[6], t0, t1);
+                    g[q] = apply_gate(gm[q], tap(t[2 * q], base[2 * q], oy, ox),
+                                      tap(t[2 * q + 1], base[2 * q + 1], oy, ox));
+                const Bits<N> r3 = apply_gate(gm[6], apply_gate(gm[4], g[0], g[1]),
+                                              apply_gate(gm[5], g[2], g[3]));
+#pragma unroll
+                for (int i = 0; i < N; ++i) out.v[i] |= r3.v[i];
             }
-        __builtin_nontemporal_store(bad ? ~uint64_t(0) : out, &y[r * words + w]);
     } else {
         const int q = p & 3, pos = p >> 2;
         const int oy = pos / d.wo, ox = pos % d.wo;
-        const uint64_t v = bad ? ~uint64_t(0)
-                               : bitwise_op<uint64_t>(op[q], word_at(t[2 * q], oy, ox),
-                                                      word_at(t[2 * q + 1], oy, ox));
-        __builtin_nontemporal_store(v, &y[r * words + w]);
+        const TapOff ta = decode_tap(sel[c * kTaps + 2 * q], d.ph, d.pw);
+        const TapOff tb = decode_tap(sel[c * kTaps + 2 * q + 1], d.ph, d.pw);
+        out = apply_gate(gate_mask(gates[c * nodes + q] & 15), tap(ta, plane_base(ta), oy, ox),
+                         tap(tb, plane_base(tb), oy, ox));
     }
+    if (bad) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) out.v[i] = ~0u;
+    }
+    store_words<WPL>(y + int64_t(r) * words + w, out);
 }
 
 template <typename T>
@@ -886,11 +971,20 @@ extern "C" int cl_tree_conv_eval_packed(const void* x, int64_t row_bytes, const 
     CL_ARG(x && gates && selection && y, "null pointer argument");
     CL_ARG(aligned(x, 8) && aligned(y, 8), "packed rows must be 8-byte aligned");
     if (!complete) d.P *= 4;  // one output row per (position, gate)
-    const int64_t nchunks = ceil_div(words, kPkChunk), rblocks = ceil_div(rows, kPkRows);
+    CL_ARG(words < (int64_t(1) << 28) && rows < (int64_t(1) << 31), "tensor too large");
+    // Two words per lane when every lane's pair is whole and 16-byte aligned.
+    const bool pairs = words % 2 == 0 && aligned(x, 16) && aligned(y, 16);
+    const int64_t nchunks = ceil_div(words, kPkChunk);
+    const int64_t rblocks = ceil_div(rows, pairs ? 16 : 8);
     const int64_t grid = nchunks >= 8 ? 8 * ceil_div(nchunks, 8) * rblocks : nchunks * rblocks;
     CL_ARG(grid < (int64_t(1) << 31), "tensor too large");
-    k_tree_packed<<<unsigned(grid), 256, 0, as_stream(stream)>>>(
-        static_cast<const uint64_t*>(x), words, gates, selection, d, nchunks, rblocks,
-        static_cast<uint64_t*>(y));
+    const auto xs = static_cast<const uint64_t*>(x);
+    const auto ys = static_cast<uint64_t*>(y);
+    if (pairs)
+        k_tree_packed<2><<<unsigned(grid), 256, 0, as_stream(stream)>>>(
+            xs, words, gates, selection, d, nchunks, rblocks, ys);
+    else
+        k_tree_packed<1><<<unsigned(grid), 256, 0, as_stream(stream)>>>(
+            xs, words, gates, selection, d, nchunks, rblocks, ys);
     return check_launch("cl_tree_conv_eval_packed");
 }
