@@ -189,6 +189,7 @@ def packed_kernel_bytes(model, words: int, k: int) -> dict:
     """Packed eval: read the input rows once, write the output rows once (8 bytes per word);
     GroupSum reads the last rows and writes int32 counts [samples, k]."""
     import compactlogic_amd as cl
+    from compactlogic_amd.treelogic import tree_row_bytes
     out = {}
     rows = None
     for m in model:
@@ -198,6 +199,9 @@ def packed_kernel_bytes(model, words: int, k: int) -> dict:
             wo = (w + 2 * m.padding[1] - m.kernel[1]) // m.stride[1] + 1
             fin, fout = c * h * w, m.out_channels * (ho // 2) * (wo // 2)
             out[f"cl_tree_conv_eval_packed[{fin}->{fout}]"] = (fin + fout) * words * 8
+            if rows is None and tree_row_bytes(words * 8) != words * 8:
+                # the first block widens power-of-two rows once (read + write of its input)
+                out[f"widen_rows[{fin}]"] = fin * (words * 8 + tree_row_bytes(words * 8))
             rows = fout
         elif isinstance(m, cl.ConvLayer):
             fin = m.in_shape[0] * m.in_shape[1] * m.in_shape[2]

@@ -27,7 +27,8 @@ from .plan import PART_SLOTS, RunPlan, build_run_plan
 
 class PackBitsTensor:
     """Bit-packed batch: `t` is [features, ceil(batch / bit_count)] integer words, bit i of word
-    w holds sample bit_count * w + i (packbitstensor.py:11-21)."""
+    w holds sample bit_count * w + i (packbitstensor.py:11-21); the last pad_len bits of a row
+    are padding (layers may widen the rows and pad_len with them)."""
 
     def __init__(self, t: torch.Tensor, bit_count: int = 32):
         assert len(t.shape) == 2, t.shape

@@ -221,6 +221,28 @@ def treelogic_backward(grad_y, x, w_prob, need_x: bool = True, need_w: bool = Tr
     return gx, gw
 
 
+def tree_row_bytes(row_bytes: int) -> int:
+    """Row length the packed block reads best: rows of 16 KiB or more are widened to the next
+    odd multiple of 256 bytes.  The block reads one 256-byte column window of every input row
+    while it works on that window (the window's rows are reused from L2 by every output
+    channel); rows a large power of two apart put the whole window into the same few L2 sets,
+    and its reads then miss again and again.  Rows an odd number of 256-byte blocks apart
+    spread it over all sets."""
+    if row_bytes < 16384:
+        return row_bytes
+    nbytes = -(-row_bytes // 256) * 256
+    return nbytes + 256 if (nbytes // 256) % 2 == 0 else nbytes
+
+
+def widen_rows(t: torch.Tensor, row_bytes: int) -> torch.Tensor:
+    """Copy of packed rows t [rows, words] widened to row_bytes with zero words."""
+    words = row_bytes // t.element_size()
+    out = torch.empty((t.shape[0], words), dtype=t.dtype, device=t.device)
+    out[:, :t.shape[1]].copy_(t)
+    out[:, t.shape[1]:].zero_()
+    return out
+
+
 def tree_conv_eval_packed(x_words, gates, selection, in_shape, stride, padding, kernel,
                           complete: bool = True):
     """Packed discrete block: x_words [c_in * h * w, words] (rows in NCHW feature order), gates
@@ -460,7 +482,13 @@ class ConvLogicLayer(nn.Module):
                 raise ValueError("non-square input: pass in_hw=(h, w) to forward_packed")
             in_hw = (side, side)
         gates = self.weights.argmax(-1).to(torch.uint8).contiguous()
-        x.t = tree_conv_eval_packed(x.t, gates, self.selection.to(torch.int32).contiguous(),
+        t = x.t
+        nbytes = t.shape[1] * t.element_size()
+        want = tree_row_bytes(nbytes)
+        if want != nbytes:  # widen once; the output rows (and later blocks) keep the width
+            t = timing.timed(f"widen_rows[{rows}]", lambda: widen_rows(x.t, want))
+            x.pad_len += (want - nbytes) * 8
+        x.t = tree_conv_eval_packed(t, gates, self.selection.to(torch.int32).contiguous(),
                                     (self.in_channels, *in_hw), self.stride, self.padding,
                                     self.kernel, complete=self.complete)
         return x

@@ -152,6 +152,18 @@ def test_forward_rejects_host_tensors():
         cl.GroupSum(2)(torch.zeros(2, 4))
 
 
+def test_tree_row_bytes():
+    from compactlogic_amd.treelogic import tree_row_bytes
+    for nbytes in [0, 8, 4096, 16376, 16384, 16392, 16640, 131072, 131080, 1 << 21]:
+        got = tree_row_bytes(nbytes)
+        if nbytes < 16384:
+            assert got == nbytes                  # short rows are read as they are
+        else:
+            assert got % 256 == 0 and (got // 256) % 2 == 1 and 0 <= got - nbytes < 512
+    # 2^20 samples in 64-bit words: a 128 KiB row becomes 128 KiB + 256 B
+    assert tree_row_bytes(131072) == 131328 and tree_row_bytes(131328) == 131328
+
+
 def test_config_network_is_deterministic():
     cfg = configs.CONFIGS["cfg1"]
     m1 = configs.dense_network(cfg, device="cpu")

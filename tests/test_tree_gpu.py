@@ -138,6 +138,24 @@ def test_packed_block_matches_bit_oracle(complete, c_in, h, w, stride, pad, kern
     assert np.array_equal(np_(out).view(np.uint64), ref)
 
 
+def test_module_packed_path_widens_power_of_two_rows():
+    """Rows of 16 KiB are widened to an odd number of 256-byte blocks before the block reads
+    them: the sample words are those of the unwidened evaluation, num_samples is unchanged."""
+    torch.manual_seed(9)
+    layer = cl.ConvLogicLayer(3, 4, stride=2, padding=1, kernel=3, complete=True).cuda().eval()
+    words = 2048                                                   # 16 KiB rows
+    xw = torch.randint(-2**62, 2**62, (3 * 8 * 8, words), dtype=torch.int64, device="cuda")
+    gates = layer.weights.argmax(-1).to(torch.uint8).contiguous()
+    direct = TL.tree_conv_eval_packed(xw, gates, layer.selection.to(torch.int32).contiguous(),
+                                      (3, 8, 8), layer.stride, layer.padding, layer.kernel, True)
+    xp = cl.PackBitsTensor.from_packed(xw.clone(), 5)
+    n = xp.num_samples
+    out = layer(xp)
+    assert out.t.shape == (direct.shape[0], TL.tree_row_bytes(words * 8) // 8)
+    assert out.num_samples == n
+    assert torch.equal(out.t[:, :words], direct)
+
+
 def test_module_packed_path_matches_float_eval():
     torch.manual_seed(8)
     layer = cl.ConvLogicLayer(3, 6, stride=2, padding=1, kernel=3, complete=True).cuda().eval()
