@@ -149,6 +149,8 @@ __global__ __launch_bounds__(256) void k_tree_fwd(const T* __restrict__ x, const
     for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? quiet_nan<T>() : e.g[q];
 }
 
+constexpr int kFwdItems = 4;  // passes of 256 items per forward workgroup
+
 // Complete block, quad form: one thread per conv position, the four positions of a pooling
 // window in the four lanes of a quad (lane order (0,0), (0,1), (1,0), (1,1)), so each thread
 // gathers 8 taps instead of 32 and the pool is two quad-DPP steps that keep the earlier lane
@@ -166,54 +168,59 @@ __global__ __launch_bounds__(256) void k_tree_fwd_q(const T* __restrict__ x, con
     __syncthreads();
     load_channel(w_prob, sel, c, 7, d, sk, st, &bad);
     __syncthreads();
-    const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (n, window) * 4 + q
     const int64_t total = int64_t(d.n) * d.P * 4;
-    const bool live = item < total;
-    const int64_t it = live ? item : 0;
-    const int q = int(it & 3);
-    const int64_t win = it >> 2;
-    const int n = int(win / d.P), p = int(win % d.P);
     const int wp = d.wo / 2;
-    const int oy = 2 * (p / wp) + (q >> 1), ox = 2 * (p % wp) + (q & 1);
-    const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
-    Eval<T, true> e;
-    eval_at<T, true>(xn, d, st, sk, oy, ox, e);
-    const int64_t cell = int64_t(n) * d.cout + c;
     const T nan = quiet_nan<T>();
-    if (live) {
-        const int64_t pos = cell * d.ho * d.wo + int64_t(oy) * d.wo + ox;
-        if (x2) {
+    // kFwdItems passes of 256 items per workgroup: the channel's coefficients are collapsed
+    // once for all of them.
+    for (int pass = 0; pass < kFwdItems; ++pass) {
+        const int64_t item = (int64_t(blockIdx.x) * kFwdItems + pass) * 256 + threadIdx.x;
+        if ((item & ~int64_t(255)) >= total) break;  // uniform per workgroup
+        const bool live = item < total;  // (n, window) * 4 + q
+        const int64_t it = live ? item : 0;
+        const int q = int(it & 3);
+        const int64_t win = it >> 2;
+        const int n = int(win / d.P), p = int(win % d.P);
+        const int oy = 2 * (p / wp) + (q >> 1), ox = 2 * (p % wp) + (q & 1);
+        const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
+        Eval<T, true> e;
+        eval_at<T, true>(xn, d, st, sk, oy, ox, e);
+        const int64_t cell = int64_t(n) * d.cout + c;
+        if (live) {
+            const int64_t pos = cell * d.ho * d.wo + int64_t(oy) * d.wo + ox;
+            if (x2) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) x2[pos * 4 + k] = bad ? nan : e.g[k];
+                for (int k = 0; k < 4; ++k) x2[pos * 4 + k] = bad ? nan : e.g[k];
+            }
+            if (x3) {
+                x3[pos * 2 + 0] = bad ? nan : e.t[0];
+                x3[pos * 2 + 1] = bad ? nan : e.t[1];
+            }
         }
-        if (x3) {
-            x3[pos * 2 + 0] = bad ? nan : e.t[0];
-            x3[pos * 2 + 1] = bad ? nan : e.t[1];
+        // first maximum over the quad: (0 vs 1), (2 vs 3), then (01 vs 23); the later lane
+        // wins only when strictly greater.  A NaN never wins (it enters as -inf with winner
+        // -1), so a window of NaNs keeps the reference's -inf / -1.
+        const bool num = e.r == e.r;
+        T r = num ? e.r : -T(__builtin_inf());
+        int wi = num ? oy * d.wo + ox : -1;
+        {
+            const T ro = dpp_move<0xB1>(r);        // quad_perm [1,0,3,2]
+            const int wo_ = dpp_move<0xB1>(wi);
+            const bool take = (q & 1) ? !(r > ro) : (ro > r);  // odd lane: partner is earlier
+            r = take ? ro : r;
+            wi = take ? wo_ : wi;
         }
-    }
-    // first maximum over the quad: (0 vs 1), (2 vs 3), then (01 vs 23); the later lane wins
-    // only when strictly greater.  A NaN never wins (it enters as -inf with winner -1), so a
-    // window of NaNs keeps the reference's -inf / -1.
-    const bool num = e.r == e.r;
-    T r = num ? e.r : -T(__builtin_inf());
-    int wi = num ? oy * d.wo + ox : -1;
-    {
-        const T ro = dpp_move<0xB1>(r);        // quad_perm [1,0,3,2]
-        const int wo_ = dpp_move<0xB1>(wi);
-        const bool take = (q & 1) ? !(r > ro) : (ro > r);  // odd lane: partner is the earlier one
-        r = take ? ro : r;
-        wi = take ? wo_ : wi;
-    }
-    {
-        const T ro = dpp_move<0x4E>(r);        // quad_perm [2,3,0,1]
-        const int wo_ = dpp_move<0x4E>(wi);
-        const bool take = (q & 2) ? !(r > ro) : (ro > r);
-        r = take ? ro : r;
-        wi = take ? wo_ : wi;
-    }
-    if (live && q == 0) {
-        y[cell * d.P + p] = bad ? nan : r;
-        if (idx) idx[cell * d.P + p] = wi;
+        {
+            const T ro = dpp_move<0x4E>(r);        // quad_perm [2,3,0,1]
+            const int wo_ = dpp_move<0x4E>(wi);
+            const bool take = (q & 2) ? !(r > ro) : (ro > r);
+            r = take ? ro : r;
+            wi = take ? wo_ : wi;
+        }
+        if (live && q == 0) {
+            y[cell * d.P + p] = bad ? nan : r;
+            if (idx) idx[cell * d.P + p] = wi;
+        }
     }
 }
 
@@ -769,7 +776,7 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
         if (complete) {
-            const unsigned gq = unsigned(ceil_div(int64_t(d.n) * d.P * 4, 256));
+            const unsigned gq = unsigned(ceil_div(int64_t(d.n) * d.P * 4, 256 * kFwdItems));
             k_tree_fwd_q<T><<<dim3(gq, unsigned(d.cout)), 256, 0, s>>>(
                 static_cast<const T*>(x), static_cast<const T*>(w_prob), selection, d,
                 static_cast<T*>(y), static_cast<T*>(x2), static_cast<T*>(x3), indices);

@@ -38,6 +38,8 @@ SHAPES = [  # stride, pad, kernel, (n, c_in, h, w, c_out)
     ((2, 2), (1, 1), (3, 3), (4, 9, 32, 32, 16)),     # conv1 of the tree reading of cfg3
     ((2, 2), (1, 1), (3, 3), (3, 16, 8, 8, 32)),      # conv2 of the tree reading
     ((1, 1), (0, 0), (2, 2), (2, 2, 5, 5, 3)),
+    ((2, 2), (1, 1), (3, 3), (128, 9, 16, 16, 41)),   # channel groups of 2, the last one short
+    ((1, 1), (1, 1), (3, 3), (2, 5, 64, 64, 3)),      # 80 KiB (fp32) / 160 KiB (fp64) planes
 ]
 
 
