@@ -68,9 +68,13 @@ def log(msg):
 # ---------------------------------------------------------------------------------- dense cfg2
 
 def dense_step_fn(model, x, labels, torch):
+    """One training step: the network, the mean cross-entropy of GroupSum's scores (fused into
+    GroupSum's kernels: GroupSum.cross_entropy is cross_entropy(GroupSum(x), labels)), and the
+    backward into every layer's logits."""
+    body, head = model[:-1], model[-1]
+
     def step():
-        out = model(x)
-        loss = torch.nn.functional.cross_entropy(out, labels)
+        loss = head.cross_entropy(body(x), labels)
         loss.backward()
         return loss
     return step

@@ -9,7 +9,8 @@ PoolLogicLayer).  All numerics run in libcompactlogic_hip.so, built in-tree by
 """
 from . import convlogic_hip, difflogic_hip
 from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction,
-                     ConvLayerWindowFunction, GroupSum, GroupSumFunction, LogicLayer,
+                     ConvLayerWindowFunction, GroupSum, GroupSumCrossEntropyFunction,
+                     GroupSumFunction, LogicLayer,
                      LogicLayerCudaFunction, LogicLayerRunsFunction, PackBitsTensor)
 from .packed_net import PackedNetwork
 from .plan import RunPlan, build_run_plan
@@ -20,7 +21,7 @@ from .treelogic import (ConvLogicFunction, ConvLogicLayer, FullConvLogicFunction
 
 __all__ = [
     "LogicLayer", "GroupSum", "LogicLayerCudaFunction", "LogicLayerRunsFunction",
-    "GroupSumFunction", "PackBitsTensor", "RunPlan", "build_run_plan", "difflogic_hip",
+    "GroupSumCrossEntropyFunction", "GroupSumFunction", "PackBitsTensor", "RunPlan", "build_run_plan", "difflogic_hip",
     "ConvLayer", "ConvLayerCudaFunction", "ConvLayerSoftmaxFunction", "ConvLayerWindowFunction",
     "convlogic_hip", "SequentialEntropyFreezer", "FixedSequentialEntropyFreezer",
     "EntropyRowResampler", "PackedNetwork", "ConvLogicLayer", "TreeLogicLayer", "PoolLogicLayer",

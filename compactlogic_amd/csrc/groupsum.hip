@@ -165,12 +165,47 @@ __global__ __launch_bounds__(256) void k_gsum_fwd_generic(const T* __restrict__ 
     out[n * k + c] = s / tau;
 }
 
-// ---- backward: grad_x[n, j] = g[n, j / gsz] / tau.  Elements are visited in memory order
+template <typename T>
+__device__ __forceinline__ T nan_of() {
+    return T(__builtin_nan(""));
+}
+
+// ---- gradient of the class scores, as the backward kernels read it: src(n, c) is
+// d loss / d out[n, c] divided by tau (the gradient each feature of group c receives).
+template <typename T>
+struct ScoreGrad {  // a given gradient g [B, k]
+    const T* g;
+    int64_t k;
+    T tau;
+    __device__ __forceinline__ T operator()(int64_t n, int64_t c) const { return g[n * k + c] / tau; }
+};
+
+// Mean cross-entropy of the scores: g[n, c] = gl * (p[n, c] - [c == y_n]) / count for a
+// counted sample, 0 for an ignored one (y_n == ignore_index), NaN for a label outside [0, k).
+// gl (the loss's upstream gradient) and count live in device memory.
+template <typename T>
+struct CrossEntropyGrad {
+    const T* p;
+    const int64_t* y;
+    int64_t ignore;
+    const T* gl;
+    const T* count;
+    int64_t k;
+    T tau;
+    __device__ __forceinline__ T operator()(int64_t n, int64_t c) const {
+        const int64_t lab = y[n];
+        if (lab == ignore) return T(0);
+        if (lab < 0 || lab >= k) return nan_of<T>();
+        const T d = p[n * k + c] - (lab == c ? T(1) : T(0));
+        return d * (gl[0] / (count[0] * tau));
+    }
+};
+
+// ---- backward: grad_x[n, j] = src(n, j / gsz).  Elements are visited in memory order
 // of grad_x: `inner` is the unit-stride dimension (batch or feature).
-template <typename T, int VEC, bool BATCH_INNER>
-__global__ __launch_bounds__(256) void k_gsum_bwd(const T* __restrict__ g, int64_t B, int64_t F,
-                                                  int64_t so, int64_t gsz, int64_t k, T tau,
-                                                  T* __restrict__ gx) {
+template <typename T, int VEC, bool BATCH_INNER, typename Src>
+__global__ __launch_bounds__(256) void k_gsum_bwd(Src src, int64_t B, int64_t F, int64_t so,
+                                                  int64_t gsz, T* __restrict__ gx) {
     // Rows: features (BATCH_INNER) or samples; inner: samples or features.
     const int64_t rows = BATCH_INNER ? F : B;
     const int64_t inner = BATCH_INNER ? B : F;
@@ -183,7 +218,7 @@ __global__ __launch_bounds__(256) void k_gsum_bwd(const T* __restrict__ g, int64
     for (int i = 0; i < VEC; ++i) {
         const int64_t n = BATCH_INNER ? i0 + i : row;
         const int64_t j = BATCH_INNER ? row : i0 + i;
-        v.v[i] = g[n * k + j / gsz] / tau;
+        v.v[i] = src(n, j / gsz);
     }
     vstore<T, VEC>(gx + row * so + i0, v);
 }
@@ -191,10 +226,9 @@ __global__ __launch_bounds__(256) void k_gsum_bwd(const T* __restrict__ g, int64
 // ---- backward, batch-contiguous grad_x ([F, batch] in memory): block = (batch tile, class
 // c, slice of the group's rows).  Each lane computes its g[n, c] / tau once and streams it
 // down the rows of its slice with non-temporal stores.
-template <typename T, int VEC>
-__global__ __launch_bounds__(256) void k_gsum_bwd_rows(const T* __restrict__ g, int64_t B,
-                                                       int64_t F, int64_t sf, int64_t gsz,
-                                                       int64_t k, int64_t slice, T tau,
+template <typename T, int VEC, typename Src>
+__global__ __launch_bounds__(256) void k_gsum_bwd_rows(Src src, int64_t B, int64_t F, int64_t sf,
+                                                       int64_t gsz, int64_t slice,
                                                        T* __restrict__ gx) {
     const int64_t n0 = (int64_t(blockIdx.x) * 64 + (threadIdx.x & 63)) * VEC;
     if (n0 >= B) return;
@@ -203,7 +237,7 @@ __global__ __launch_bounds__(256) void k_gsum_bwd_rows(const T* __restrict__ g, 
     const int64_t j1 = std::min<int64_t>(std::min<int64_t>(j0 + slice, (c + 1) * gsz), F);
     Vec<T, VEC> v;
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) v.v[i] = g[(n0 + i) * k + c] / tau;
+    for (int i = 0; i < VEC; ++i) v.v[i] = src(n0 + i, c);
     for (int64_t j = j0 + (threadIdx.x >> 6); j < j1; j += 4) {
         T* dst = gx + j * sf + n0;
         if constexpr (VEC == 4 && sizeof(T) == 4) {
@@ -220,15 +254,103 @@ __global__ __launch_bounds__(256) void k_gsum_bwd_rows(const T* __restrict__ g, 
     }
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void k_gsum_bwd_generic(const T* __restrict__ g, int64_t B,
-                                                          int64_t F, int64_t sb, int64_t sf,
-                                                          int64_t gsz, int64_t k, T tau,
+template <typename T, typename Src>
+__global__ __launch_bounds__(256) void k_gsum_bwd_generic(Src src, int64_t B, int64_t F,
+                                                          int64_t sb, int64_t sf, int64_t gsz,
                                                           T* __restrict__ gx) {
     const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (item >= B * F) return;
     const int64_t n = item / F, j = item % F;
-    gx[n * sb + j * sf] = g[n * k + j / gsz] / tau;
+    gx[n * sb + j * sf] = src(n, j / gsz);
+}
+
+// ---- mean cross-entropy of the scores.  k_ce_rows: workgroup of kCeSamples samples; its
+// threads first add the group-sum slices of every (sample, class) pair (the split forward's
+// finish, slices in order) into out and LDS, then one thread per sample takes the softmax
+// (kept for the backward), its loss term and whether it counts.  k_ce_mean: one workgroup adds
+// the terms in a fixed order.  Both are deterministic.
+constexpr int kCeSamples = 64;
+constexpr int kCeThreads = 256;
+
+template <typename T>
+__global__ __launch_bounds__(kCeThreads) void k_ce_rows(const T* __restrict__ part,
+                                                        int64_t nslices, const int64_t* y,
+                                                        int64_t B, int64_t k, int64_t ignore,
+                                                        T tau, T* __restrict__ out,
+                                                        T* __restrict__ p,
+                                                        T* __restrict__ term) {
+    extern __shared__ __align__(16) unsigned char ce_lds[];
+    T* z = reinterpret_cast<T*>(ce_lds);  // [kCeSamples][k]
+    const int64_t n0 = int64_t(blockIdx.x) * kCeSamples;
+    const int64_t ns = std::min<int64_t>(kCeSamples, B - n0);
+    const int64_t step = k * B;
+    for (int64_t e = threadIdx.x; e < ns * k; e += kCeThreads) {
+        const int64_t c = e % k, n = n0 + e / k;
+        const T* src = part + c * B + n;
+        T t = 0;
+        int64_t sl = 0;
+        for (; sl + 8 <= nslices; sl += 8) {
+            T v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = src[(sl + i) * step];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t += v[i];
+        }
+        for (; sl < nslices; ++sl) t += src[sl * step];
+        t = t / tau;
+        out[n * k + c] = t;
+        z[e] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < ns) {
+        const int64_t n = n0 + threadIdx.x;
+        const T* zr = z + threadIdx.x * k;
+        T mx = -T(__builtin_inf());
+        for (int64_t c = 0; c < k; ++c) mx = fmax(mx, zr[c]);
+        T sum = 0;
+        for (int64_t c = 0; c < k; ++c) sum += exp(zr[c] - mx);
+        const T inv = T(1) / sum;
+        for (int64_t c = 0; c < k; ++c) p[n * k + c] = exp(zr[c] - mx) * inv;
+        const int64_t lab = y[n];
+        // term[n] = loss term, term[B + n] = 1 when the sample counts
+        const bool counted = lab != ignore;
+        term[n] = !counted ? T(0)
+                  : (lab >= 0 && lab < k) ? (mx + log(sum)) - zr[lab] : nan_of<T>();
+        term[B + n] = counted ? T(1) : T(0);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_scores_to_slices(const T* __restrict__ sc, int64_t B,
+                                                          int64_t k, T* __restrict__ part) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // n * k + c
+    if (i < B * k) part[(i % k) * B + i / k] = sc[i];
+}
+
+template <typename T>
+__global__ __launch_bounds__(kCeThreads) void k_ce_mean(const T* __restrict__ term, int64_t B,
+                                                        T* __restrict__ loss,
+                                                        T* __restrict__ count) {
+    __shared__ T sl[kCeThreads], sc[kCeThreads];
+    T l = 0, c = 0;
+    for (int64_t n = threadIdx.x; n < B; n += kCeThreads) {
+        l += term[n];
+        c += term[B + n];
+    }
+    sl[threadIdx.x] = l;
+    sc[threadIdx.x] = c;
+    __syncthreads();
+    for (int h = kCeThreads / 2; h > 0; h >>= 1) {
+        if (int(threadIdx.x) < h) {
+            sl[threadIdx.x] += sl[threadIdx.x + h];
+            sc[threadIdx.x] += sc[threadIdx.x + h];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        loss[0] = sl[0] / sc[0];  // no counted sample: 0 / 0 = NaN, the mean of nothing
+        count[0] = sc[0];
+    }
 }
 
 }  // namespace
@@ -318,6 +440,44 @@ extern "C" int cl_group_sum_forward(int dtype, const void* x, int64_t batch, int
     return check_launch("cl_group_sum_forward");
 }
 
+namespace {
+// grad_x from a gradient source, in grad_x's memory order (see the kernels above).
+template <typename T, typename Src>
+int launch_gsum_backward(const Src& src, int64_t batch, int64_t features, int64_t k,
+                         T* gxs, int64_t stride_batch, int64_t stride_feature, hipStream_t s) {
+    const int64_t gsz = ceil_div(features, k);
+    constexpr int W = wide_vec<T>();
+    if (stride_batch == 1) {
+        const bool wide = batch % W == 0 && stride_feature % W == 0 && aligned(gxs, 16);
+        const int vec = wide ? W : 1;
+        const int64_t slice = std::max<int64_t>(std::min<int64_t>(gsz, 32), ceil_div(gsz, 65535));
+        const dim3 grid(unsigned(ceil_div(batch, 64 * vec)), unsigned(k),
+                        unsigned(ceil_div(gsz, slice)));
+        if (wide)
+            k_gsum_bwd_rows<T, W><<<grid, 256, 0, s>>>(src, batch, features, stride_feature, gsz,
+                                                      slice, gxs);
+        else
+            k_gsum_bwd_rows<T, 1><<<grid, 256, 0, s>>>(src, batch, features, stride_feature, gsz,
+                                                      slice, gxs);
+    } else if (stride_feature == 1) {
+        const bool wide = features % W == 0 && stride_batch % W == 0 && aligned(gxs, 16);
+        const int vec = wide ? W : 1;
+        const dim3 grid(unsigned(ceil_div(batch, 4)), unsigned(ceil_div(features, 64 * vec)), 1);
+        if (wide)
+            k_gsum_bwd<T, W, false><<<grid, 256, 0, s>>>(src, batch, features, stride_batch, gsz,
+                                                        gxs);
+        else
+            k_gsum_bwd<T, 1, false><<<grid, 256, 0, s>>>(src, batch, features, stride_batch, gsz,
+                                                        gxs);
+    } else {
+        const dim3 grid(unsigned(ceil_div(batch * features, 256)), 1, 1);
+        k_gsum_bwd_generic<T><<<grid, 256, 0, s>>>(src, batch, features, stride_batch,
+                                                   stride_feature, gsz, gxs);
+    }
+    return CL_OK;
+}
+}  // namespace
+
 extern "C" int cl_group_sum_backward(int dtype, const void* grad_out, int64_t batch,
                                      int64_t features, int64_t k, double tau, void* grad_x,
                                      int64_t stride_batch, int64_t stride_feature, void* stream) {
@@ -327,41 +487,118 @@ extern "C" int cl_group_sum_backward(int dtype, const void* grad_out, int64_t ba
     CL_ARG(stride_batch >= 0 && stride_feature >= 0, "negative strides are not supported");
     if (batch == 0 || features == 0) return CL_OK;
     CL_ARG(grad_out && grad_x, "null pointer argument");
-    const int64_t gsz = ceil_div(features, k);
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
-        const T* gs = static_cast<const T*>(grad_out);
-        T* gxs = static_cast<T*>(grad_x);
-        const T t = T(tau);
-        constexpr int W = wide_vec<T>();
-        if (stride_batch == 1) {
-            const bool wide = batch % W == 0 && stride_feature % W == 0 && aligned(grad_x, 16);
-            const int vec = wide ? W : 1;
-            const int64_t slice = std::max<int64_t>(std::min<int64_t>(gsz, 32), ceil_div(gsz, 65535));
-            const dim3 grid(unsigned(ceil_div(batch, 64 * vec)), unsigned(k),
-                            unsigned(ceil_div(gsz, slice)));
-            if (wide)
-                k_gsum_bwd_rows<T, W><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
-                                                          gsz, k, slice, t, gxs);
-            else
-                k_gsum_bwd_rows<T, 1><<<grid, 256, 0, s>>>(gs, batch, features, stride_feature,
-                                                          gsz, k, slice, t, gxs);
-        } else if (stride_feature == 1) {
-            const bool wide = features % W == 0 && stride_batch % W == 0 && aligned(grad_x, 16);
-            const int vec = wide ? W : 1;
-            const dim3 grid(unsigned(ceil_div(batch, 4)), unsigned(ceil_div(features, 64 * vec)), 1);
-            if (wide)
-                k_gsum_bwd<T, W, false><<<grid, 256, 0, s>>>(gs, batch, features, stride_batch,
-                                                            gsz, k, t, gxs);
-            else
-                k_gsum_bwd<T, 1, false><<<grid, 256, 0, s>>>(gs, batch, features, stride_batch,
-                                                            gsz, k, t, gxs);
-        } else {
-            const dim3 grid(unsigned(ceil_div(batch * features, 256)), 1, 1);
-            k_gsum_bwd_generic<T><<<grid, 256, 0, s>>>(gs, batch, features, stride_batch,
-                                                       stride_feature, gsz, k, t, gxs);
-        }
+        const ScoreGrad<T> src{static_cast<const T*>(grad_out), k, T(tau)};
+        launch_gsum_backward<T>(src, batch, features, k, static_cast<T*>(grad_x), stride_batch,
+                                stride_feature, s);
     });
     return check_launch("cl_group_sum_backward");
+}
+
+extern "C" int cl_group_sum_cross_entropy_workspace_size(int dtype, int64_t batch,
+                                                         int64_t features, int64_t k,
+                                                         int64_t* bytes) {
+    clear_error();
+    CL_ARG(bytes, "null pointer argument");
+    CL_ARG(batch >= 0 && features >= 0 && k >= 1, "bad shape");
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        constexpr int W = wide_vec<T>();
+        const int64_t slices = gsum_slices(batch, features, k, W);
+        *bytes = (slices * k * batch + 2 * batch) * int64_t(sizeof(T));
+    });
+    return CL_OK;
+}
+
+extern "C" int cl_group_sum_cross_entropy_forward(int dtype, const void* x, int64_t batch,
+                                                  int64_t features, int64_t stride_batch,
+                                                  int64_t stride_feature, int64_t k, double tau,
+                                                  const int64_t* labels, int64_t ignore_index,
+                                                  void* out, void* probs, void* loss,
+                                                  void* count, void* workspace,
+                                                  int64_t workspace_bytes, void* stream) {
+    clear_error();
+    CL_ARG(batch >= 0 && features >= 0, "negative shape");
+    CL_ARG(k >= 1, "k must be >= 1, got %lld", (long long)k);
+    CL_ARG(stride_batch >= 0 && stride_feature >= 0, "negative strides are not supported");
+    CL_ARG(labels && probs && loss && count && out, "null pointer argument");
+    CL_ARG(features == 0 || x, "null pointer argument");
+    CL_ARG(k * kCeSamples * 8 <= 64 * 1024, "k too large for the fused cross-entropy");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        const T t = T(tau);
+        constexpr int W = wide_vec<T>();
+        const int64_t gsz = features == 0 ? 1 : ceil_div(features, k);
+        const bool split = gsum_split_applies(batch, features, stride_batch);
+        const bool wide = split && batch % W == 0 && stride_feature % W == 0 && aligned(x, 16);
+        // slices of the split forward (one slice: the plain sums, written by the same path)
+        const int64_t slices = split ? gsum_slices(batch, features, k, wide ? W : 1) : 1;
+        const int64_t need = (slices * k * batch + 2 * batch) * int64_t(sizeof(T));
+        CL_ARG(need == 0 || (workspace && workspace_bytes >= need),
+               "workspace of %lld bytes needed (cl_group_sum_cross_entropy_workspace_size)",
+               (long long)need);
+        T* part = static_cast<T*>(workspace);
+        T* term = part + slices * k * batch;
+        if (batch > 0) {
+            if (split) {
+                const int64_t slice = ceil_div(gsz, slices);
+                const dim3 grid(unsigned(ceil_div(batch, 64 * (wide ? W : 1))), unsigned(k),
+                                unsigned(slices));
+                if (wide)
+                    k_gsum_partial<T, W><<<grid, kPartWaves * 64, 0, s>>>(
+                        static_cast<const T*>(x), batch, features, stride_feature, gsz, k,
+                        slice, part);
+                else
+                    k_gsum_partial<T, 1><<<grid, kPartWaves * 64, 0, s>>>(
+                        static_cast<const T*>(x), batch, features, stride_feature, gsz, k,
+                        slice, part);
+            } else {
+                // the other layouts: their sums (tau = 1) into out, then out as one [k, batch]
+                // slice; k_ce_rows overwrites out with the scores
+                if (int rc = cl_group_sum_forward(dtype, x, batch, features, stride_batch,
+                                                  stride_feature, k, 1.0, out, nullptr, 0,
+                                                  stream))
+                    return rc;
+                k_scores_to_slices<T><<<unsigned(ceil_div(batch * k, 256)), 256, 0, s>>>(
+                    static_cast<const T*>(out), batch, k, part);
+            }
+            if (int rc = check_launch("cl_group_sum_cross_entropy_forward(sums)")) return rc;
+            k_ce_rows<T><<<unsigned(ceil_div(batch, kCeSamples)), kCeThreads,
+                           size_t(kCeSamples * k * sizeof(T)), s>>>(
+                part, slices, labels, batch, k, ignore_index, t, static_cast<T*>(out),
+                static_cast<T*>(probs), term);
+            if (int rc = check_launch("cl_group_sum_cross_entropy_forward(rows)")) return rc;
+        }
+        k_ce_mean<T><<<1, kCeThreads, 0, s>>>(term, batch, static_cast<T*>(loss),
+                                              static_cast<T*>(count));
+    });
+    return check_launch("cl_group_sum_cross_entropy_forward");
+}
+
+extern "C" int cl_group_sum_cross_entropy_backward(int dtype, const void* probs,
+                                                   const int64_t* labels, int64_t ignore_index,
+                                                   const void* grad_loss, const void* count,
+                                                   int64_t batch, int64_t features, int64_t k,
+                                                   double tau, void* grad_x,
+                                                   int64_t stride_batch, int64_t stride_feature,
+                                                   void* stream) {
+    clear_error();
+    CL_ARG(batch >= 0 && features >= 0, "negative shape");
+    CL_ARG(k >= 1, "k must be >= 1, got %lld", (long long)k);
+    CL_ARG(stride_batch >= 0 && stride_feature >= 0, "negative strides are not supported");
+    if (batch == 0 || features == 0) return CL_OK;
+    CL_ARG(probs && labels && grad_loss && count && grad_x, "null pointer argument");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        const CrossEntropyGrad<T> src{static_cast<const T*>(probs), labels, ignore_index,
+                                      static_cast<const T*>(grad_loss),
+                                      static_cast<const T*>(count), k, T(tau)};
+        launch_gsum_backward<T>(src, batch, features, k, static_cast<T*>(grad_x), stride_batch,
+                                stride_feature, s);
+    });
+    return check_launch("cl_group_sum_cross_entropy_backward");
 }

@@ -987,6 +987,71 @@ class ConvLayer(LogicLayer):
         return x_flag, y_flag
 
 
+class GroupSumCrossEntropyFunction(torch.autograd.Function):
+    """cross_entropy(GroupSum(k, tau)(x), labels) with the mean over counted samples, fused:
+    the group sums, the softmax and the loss in three launches and the input gradient in one,
+    instead of GroupSum's two plus torch's log-softmax / NLL kernels each way.  No counterpart
+    in the reference (its training loops call torch's cross_entropy on GroupSum's output,
+    compactlogic/compactlogic.py:450-468); the result is the same function.  Returns
+    (loss, scores); the scores are not differentiable through this function."""
+
+    @staticmethod
+    def forward(ctx, x, labels, k, tau, ignore_index):
+        if x.device.type != "cuda" or labels.device != x.device:
+            raise RuntimeError("GroupSum cross-entropy needs x and labels on the same HIP device")
+        if x.dim() != 2:
+            raise RuntimeError("GroupSum expects a 2-D [batch, features] input")
+        batch, feats = x.shape
+        if labels.dtype != torch.int64 or labels.shape != (batch,):
+            raise RuntimeError(f"labels must be int64 of shape ({batch},)")
+        labels = labels.contiguous()
+        sb, sf = x.stride()
+        if sb < 0 or sf < 0 or (batch > 1 and feats > 1 and (sb == 0 or sf == 0)):
+            x = x.contiguous()
+            sb, sf = x.stride()
+        out = torch.empty((batch, k), dtype=x.dtype, device=x.device)
+        probs = torch.empty((batch, k), dtype=x.dtype, device=x.device)
+        loss = torch.empty((), dtype=x.dtype, device=x.device)
+        count = torch.empty((), dtype=x.dtype, device=x.device)  # samples in the mean
+        need = ctypes.c_int64(0)
+        _capi.call("cl_group_sum_cross_entropy_workspace_size", _dl.dtype_code(x), batch, feats,
+                   k, ctypes.byref(need))
+        ws = torch.empty(need.value, dtype=torch.uint8, device=x.device) if need.value else None
+        with torch.cuda.device(x.device):
+            timing.timed("cl_group_sum_cross_entropy_forward", lambda: _capi.call(
+                "cl_group_sum_cross_entropy_forward", _dl.dtype_code(x), x.data_ptr(), batch,
+                feats, sb, sf, k, float(tau), labels.data_ptr(), int(ignore_index),
+                out.data_ptr(), probs.data_ptr(), loss.data_ptr(), count.data_ptr(),
+                _dl.ptr(ws), need.value, _dl.stream_of(x)))
+        ctx.save_for_backward(probs, labels, count)
+        ctx.k, ctx.tau, ctx.ignore_index = k, tau, int(ignore_index)
+        ctx.shape = (batch, feats)
+        ctx.batch_major = sb == 1 and sf != 1
+        ctx.mark_non_differentiable(out)
+        ctx.set_materialize_grads(False)  # the scores' gradient is never used: no zero fill
+        return loss, out
+
+    @staticmethod
+    def backward(ctx, grad_loss, _grad_out):
+        if grad_loss is None:
+            return None, None, None, None, None
+        probs, labels, count = ctx.saved_tensors
+        grad_loss = grad_loss.to(probs.dtype).contiguous()
+        batch, feats = ctx.shape
+        if ctx.batch_major:
+            grad_x = torch.empty((feats, batch), dtype=probs.dtype, device=probs.device).t()
+        else:
+            grad_x = torch.empty((batch, feats), dtype=probs.dtype, device=probs.device)
+        sb, sf = grad_x.stride()
+        with torch.cuda.device(probs.device):
+            timing.timed("cl_group_sum_cross_entropy_backward", lambda: _capi.call(
+                "cl_group_sum_cross_entropy_backward", _dl.dtype_code(probs), probs.data_ptr(),
+                labels.data_ptr(), ctx.ignore_index, grad_loss.data_ptr(), count.data_ptr(),
+                batch, feats, ctx.k, float(ctx.tau),
+                grad_x.data_ptr(), sb, sf, _dl.stream_of(probs)))
+        return grad_x, None, None, None, None
+
+
 class GroupSum(torch.nn.Module):
     """k class scores from the summed outputs of k equal feature groups, divided by tau
     (compactlogic/compactlogic.py:450-468).  A PackBitsTensor gives int32 per-class counts
@@ -1002,6 +1067,13 @@ class GroupSum(torch.nn.Module):
         if isinstance(x, PackBitsTensor):
             return x.group_sum(self.k)
         return GroupSumFunction.apply(x, self.k, self.tau)
+
+    def cross_entropy(self, x, labels, ignore_index: int = -100, return_scores: bool = False):
+        """torch.nn.functional.cross_entropy(self(x), labels, ignore_index=ignore_index) in one
+        fused op (mean over the samples whose label is not ignore_index); with return_scores,
+        also the scores self(x) (not differentiable through this call)."""
+        loss, out = GroupSumCrossEntropyFunction.apply(x, labels, self.k, self.tau, ignore_index)
+        return (loss, out) if return_scores else loss
 
     def extra_repr(self):
         return 'k={}, tau={}'.format(self.k, self.tau)

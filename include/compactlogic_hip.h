@@ -347,6 +347,35 @@ int cl_group_sum_backward(int dtype, const void* grad_out, int64_t batch, int64_
                           int64_t k, double tau, void* grad_x, int64_t stride_batch,
                           int64_t stride_feature, void* stream);
 
+/* GroupSum followed by the mean cross-entropy of its scores, fused (no counterpart in the
+ * reference, whose training loops call torch's cross_entropy on GroupSum's output,
+ * compactlogic/compactlogic.py:450-468).  For the last layer of a training step:
+ *   out [batch, k]    = the GroupSum scores (as cl_group_sum_forward, same workspace);
+ *   probs [batch, k]  = softmax of each row of out, kept for the backward;
+ *   loss[0]           = mean over counted samples of logsumexp(out[n]) - out[n, labels[n]];
+ *   count[0]          = the number of counted samples (labels[n] != ignore_index).
+ * A label outside [0, k) that is not ignore_index makes the loss NaN.  The reduction order is
+ * fixed, so the loss is bitwise repeatable.  loss and count are device scalars of dtype.
+ * workspace: at least cl_group_sum_cross_entropy_workspace_size bytes; k <= 128. */
+int cl_group_sum_cross_entropy_forward(int dtype, const void* x, int64_t batch, int64_t features,
+                                       int64_t stride_batch, int64_t stride_feature, int64_t k,
+                                       double tau, const int64_t* labels, int64_t ignore_index,
+                                       void* out, void* probs, void* loss, void* count,
+                                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of cl_group_sum_cross_entropy_forward (an upper bound for every layout). */
+int cl_group_sum_cross_entropy_workspace_size(int dtype, int64_t batch, int64_t features,
+                                              int64_t k, int64_t* bytes);
+
+/* Its backward: grad_x[n, j] = grad_loss[0] * (probs[n, c] - [c == labels[n]]) /
+ * (count[0] * tau) for c = group(j); 0 for an ignored sample, NaN for a label outside [0, k).
+ * grad_loss and count are device scalars (graph-capturable: nothing is read on the host). */
+int cl_group_sum_cross_entropy_backward(int dtype, const void* probs, const int64_t* labels,
+                                        int64_t ignore_index, const void* grad_loss,
+                                        const void* count, int64_t batch, int64_t features,
+                                        int64_t k, double tau, void* grad_x, int64_t stride_batch,
+                                        int64_t stride_feature, void* stream);
+
 /* -------------------------------------------------------------------------------------------
  * Layout change: dst [cols, rows] = transpose of src [rows, cols] (both contiguous, not
  * overlapping).  Replaces the torch transpose copy of compactlogic/compactlogic.py:100-101

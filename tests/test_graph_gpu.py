@@ -8,7 +8,8 @@ import compactlogic_amd as cl
 pytestmark = pytest.mark.gpu
 
 
-def test_graph_replays_match_eager(device):
+@pytest.mark.parametrize("fused_loss", [False, True])
+def test_graph_replays_match_eager(device, fused_loss):
     torch.manual_seed(0)
     model = torch.nn.Sequential(cl.LogicLayer(100, 200, connections="original"),
                                 cl.LogicLayer(200, 200), cl.GroupSum(10, 5.0)).to(device)
@@ -16,8 +17,10 @@ def test_graph_replays_match_eager(device):
     labels = torch.randint(0, 10, (256,), device=device)
 
     def step():
-        out = model(x)
-        loss = torch.nn.functional.cross_entropy(out, labels)
+        if fused_loss:
+            loss = model[-1].cross_entropy(model[:-1](x), labels)
+        else:
+            loss = torch.nn.functional.cross_entropy(model(x), labels)
         loss.backward()
         return loss
 
