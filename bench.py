@@ -282,6 +282,14 @@ def cpu_baseline_train(torch, which: str):
         model = configs.dense_network(cfg, device="cpu")
         x, labels = configs.dense_inputs(cfg, device="cpu", batch=batch)
         what = "cfg2 network (6x12000, G=16, fp32)"
+    elif which == "cfg3_tree":
+        cfg = configs.TREE_CONFIGS["cfg3_tree"]
+        batch, warm, steps = 32, 1, 3
+        # the blocks are built on the device (their constructor requires one), then copied
+        model = configs.tree_network(cfg, device=torch.device("cuda:0"))
+        x, labels = configs.conv_inputs(cfg, device="cpu", batch=batch)
+        what = ("cfg3_tree network (2 logic-tree conv blocks, the python-path block of "
+                "oracle/torch_cpu.py, + 2x16000 dense, fp32)")
     else:
         cfg = configs.CONV_CONFIGS["cfg3"]
         batch, warm, steps = 64, 1, 3
@@ -459,27 +467,48 @@ def cpu_baseline_packed(torch, which: str):
         model = configs.dense_network(cfg, device="cpu")
         configs.freeze_uniform_gates(model)
         in_features, log2n = cfg.in_dim, 16
+    elif which == "cfg3_tree":
+        cfg = configs.TREE_CONFIGS["cfg3_tree"]
+        model = configs.tree_network(cfg, device=torch.device("cuda:0"))
+        configs.freeze_argmax(model)
+        in_features, log2n = cfg.in_shape[0] * cfg.in_shape[1] * cfg.in_shape[2], 16
     else:
         cfg = configs.CONV_CONFIGS["cfg5"]
         model = configs.conv_network(cfg, device="cpu")
         configs.freeze_argmax(model)
         in_features, log2n = cfg.in_shape[0] * cfg.in_shape[1] * cfg.in_shape[2], 15
-    layers = []
+    layers, blocks = [], []
+    shape = getattr(cfg, "in_shape", None)
     for m in model:
-        if isinstance(m, cl.ConvLayer):
+        if isinstance(m, cl.ConvLogicLayer):
+            gates = m.weights.argmax(-1).to(torch.uint8).cpu().numpy()
+            sel = m.selection.to(torch.int32).cpu().numpy()
+            blocks.append((gates, sel, shape, m.stride, m.padding, m.kernel))
+            ho = (shape[1] + 2 * m.padding[0] - m.kernel[0]) // m.stride[0] + 1
+            wo = (shape[2] + 2 * m.padding[1] - m.kernel[1]) // m.stride[1] + 1
+            shape = (m.out_channels, ho // 2, wo // 2)
+        elif isinstance(m, cl.ConvLayer):
             layers.append(P.resolve_conv_slots(m.offsets_ch.numpy(), m.offsets_h.numpy(),
                                                m.offsets_w.numpy(), m.gate_sequence.numpy(),
                                                m.w.numpy(), m.in_shape, m.stride, m.out_shape[1:]))
         elif isinstance(m, cl.LogicLayer):
-            layers.append(P.resolve_slots(m.indices.numpy(), m.gate_sequence.numpy(), m.w.numpy()))
+            layers.append(P.resolve_slots(m.indices.cpu().numpy(), m.gate_sequence.cpu().numpy(),
+                                          m.w.cpu().numpy()))
     n = 1 << log2n
     words = n // 64
     xw = np.stack([P.fill_splitmix64(words, (1 << 40) + f * words) for f in range(in_features)])
-    P.network_counts(xw, layers, cfg.k)           # warm
+
+    def one_pass():
+        h = xw
+        for gates, sel, shp, stride, pad, kernel in blocks:
+            h = P.tree_block_bits(h, gates, sel, shp, stride, pad, kernel)
+        return P.network_counts(h, layers, cfg.k)
+
+    one_pass()                                    # warm
     t0 = time.perf_counter()
     reps = 3
     for _ in range(reps):
-        P.network_counts(xw, layers, cfg.k)
+        one_pass()
     dt = (time.perf_counter() - t0) / reps
     return {"value": n / dt / 1e9, "unit": "Gsamples/s", "cores": 1, "kind": "port",
             "sample": f"{which} network on 2^{log2n} samples, C oracle oracle/packed_ref.c, "
@@ -555,6 +584,9 @@ def main():
         log(f"tree conv cfg3_tree: warmup={args.conv_warmup} steps={args.conv_steps}")
         tree = bench_tree(args, torch)
         log(f"tree conv cfg3_tree: {tree['value']:,.0f} samples/s, {tree['ms_per_step']:.3f} ms/step")
+        if not args.no_cpu_baseline:
+            log("cpu baseline (cfg3_tree)")
+            tree["cpu_baseline"] = cpu_baseline_train(torch, "cfg3_tree")
         result["conv_tree_train"] = tree
     if not args.no_packed:
         log(f"packed cfg4: 2^{args.packed_log2_samples} samples x {args.packed_passes} passes")
@@ -612,6 +644,9 @@ def main():
                                  "word, 2 packed ConvLogic blocks + 2 dense layers + popcount "
                                  "GroupSum", CFG5_TREE_BYTES_PER_SAMPLE)
             log(f"packed cfg3_tree: {pt['value']} Gsamples/s")
+            if not args.no_cpu_baseline:
+                log("cpu baseline (packed cfg3_tree)")
+                pt["cpu_baseline"] = cpu_baseline_packed(torch, "cfg3_tree")
             result["packed_conv_tree"] = pt
     print(json.dumps(result), flush=True)
 

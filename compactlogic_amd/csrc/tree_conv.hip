@@ -274,8 +274,10 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
             gc[1] = gt0 * fma(sk[4][3], e.g[0], sk[4][2]);
             gc[2] = gt1 * fma(sk[5][3], e.g[3], sk[5][1]);
             gc[3] = gt1 * fma(sk[5][3], e.g[2], sk[5][2]);
+            if (gconv) {  // only the input gradient reads them
 #pragma unroll
-            for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gc[q];
+                for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gc[q];
+            }
             const T gts[2] = {gt0, gt1};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -855,7 +857,8 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
         const T* xs = static_cast<const T*>(x);
         const T* wp = static_cast<const T*>(w_prob);
         if (complete)
-            k_tree_nodes<T, true><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gconv,
+            k_tree_nodes<T, true><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d,
+                                                       grad_x ? gconv : nullptr,
                                                        part, kc);
         else
             k_tree_nodes<T, false><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gconv,

@@ -39,6 +39,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_pack_bits.argtypes = [p, i64, i64, ctypes.c_int, p]
         L.oracle_eval_packed.argtypes = [p, i64, i64, p, p, p, i64, p]
         L.oracle_group_bit_sum.argtypes = [p, i64, i64, i64, i64, p]
+        L.oracle_tree_block_bits.argtypes = [p, i64, p, p] + [ctypes.c_int] * 10 + [p]
         _lib = L
     return _lib
 
@@ -133,3 +134,20 @@ def network_counts(x_words: np.ndarray, layers, k: int, pad_len: int = 0) -> np.
     for ia, ib, g in layers:
         h = eval_layer(h, ia, ib, g)
     return group_bit_sum(h, pad_len, k)
+
+
+def tree_block_bits(x_words: np.ndarray, gates: np.ndarray, sel: np.ndarray, in_shape, stride,
+                    pad, kernel) -> np.ndarray:
+    """Complete packed tree block (pool = OR): uint64 rows [c_in * h * w, words] ->
+    [c_out * hp * wp, words]."""
+    xw = np.ascontiguousarray(x_words, dtype=np.uint64)
+    g = np.ascontiguousarray(gates, dtype=np.uint8)
+    s = np.ascontiguousarray(sel, dtype=np.int32)
+    c_in, h, w = in_shape
+    (sh, sw), (ph, pw), (kh, kw) = stride, pad, kernel
+    ho, wo = (h + 2 * ph - kh) // sh + 1, (w + 2 * pw - kw) // sw + 1
+    c_out = s.shape[0]
+    y = np.empty((c_out * (ho // 2) * (wo // 2), xw.shape[1]), dtype=np.uint64)
+    lib().oracle_tree_block_bits(_ptr(xw), xw.shape[1], _ptr(g), _ptr(s), c_in, h, w, c_out,
+                                 sh, sw, ph, pw, kh, kw, _ptr(y))
+    return y

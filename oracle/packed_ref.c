@@ -7,6 +7,10 @@
  *                   pad_len = (bits - n % bits) % bits)
  *   layer eval      third_party/convlogic_source_code/src/difflogic/cuda/difflogic_kernel.cu:271-293
  *   group popcount  compactlogic/cuda/difflogic_kernel.cu:500-567 (counts [N, k])
+ *   tree conv block third_party/convlogic_source_code/src/convlogic/convlogic_layer.py:236-321
+ *                   with the argmax gates: 8 taps (sel = ch << 16 | row << 8 | col, zero outside
+ *                   the image), gates on the tap pairs, on (0,1), (2,3) and their pair; 2x2
+ *                   pool of {0, 1} values = OR
  * A packed row is a little-endian bit string: bit j of the row = bit j%8 of byte j/8.
  */
 #include <stdint.h>
@@ -79,4 +83,46 @@ void oracle_group_bit_sum(const uint8_t* packed, int64_t rows, int64_t row_bytes
             const uint8_t* row = packed + r * row_bytes;
             for (int64_t s = 0; s < n_valid; ++s) counts[s * k + c] += (row[s >> 3] >> (s & 7)) & 1;
         }
+}
+
+/* Complete packed tree block: x rows (ch * h + y) * w + x of `words` 64-bit words; gates
+ * [c_out][7] opcodes; sel [c_out][8]; output rows (c * hp + py) * wp + px. */
+void oracle_tree_block_bits(const uint64_t* x, int64_t words, const uint8_t* gates,
+                            const int32_t* sel, int c_in, int h, int w, int c_out, int sh,
+                            int sw, int ph, int pw, int kh, int kw, uint64_t* y) {
+    const int ho = (h + 2 * ph - kh) / sh + 1, wo = (w + 2 * pw - kw) / sw + 1;
+    const int hp = ho / 2, wp = wo / 2;
+    for (int c = 0; c < c_out; ++c) {
+        int ch[8], dy[8], dx[8];
+        for (int k = 0; k < 8; ++k) {
+            ch[k] = (sel[c * 8 + k] >> 16) & 0xFFFF;
+            dy[k] = ((sel[c * 8 + k] >> 8) & 0xFF) - ph;
+            dx[k] = (sel[c * 8 + k] & 0xFF) - pw;
+        }
+        const uint8_t* g = gates + (int64_t)c * 7;
+        for (int py = 0; py < hp; ++py)
+            for (int px = 0; px < wp; ++px) {
+                uint64_t* out = y + (((int64_t)c * hp + py) * wp + px) * words;
+                const uint64_t* tap[4][8];  /* NULL = zero word */
+                for (int q = 0; q < 4; ++q) {
+                    const int oy = 2 * py + (q >> 1), ox = 2 * px + (q & 1);
+                    for (int k = 0; k < 8; ++k) {
+                        const int iy = oy * sh + dy[k], ix = ox * sw + dx[k];
+                        const int in = ch[k] < c_in && iy >= 0 && iy < h && ix >= 0 && ix < w;
+                        tap[q][k] = in ? x + (((int64_t)ch[k] * h + iy) * w + ix) * words : 0;
+                    }
+                }
+                for (int64_t j = 0; j < words; ++j) {
+                    uint64_t acc = 0;
+                    for (int q = 0; q < 4; ++q) {
+                        uint64_t v[8], n[4];
+                        for (int k = 0; k < 8; ++k) v[k] = tap[q][k] ? tap[q][k][j] : 0;
+                        for (int k = 0; k < 4; ++k) n[k] = oracle_gate_word(g[k] & 15, v[2 * k], v[2 * k + 1]);
+                        acc |= oracle_gate_word(g[6] & 15, oracle_gate_word(g[4] & 15, n[0], n[1]),
+                                                oracle_gate_word(g[5] & 15, n[2], n[3]));
+                    }
+                    out[j] = acc;
+                }
+            }
+    }
 }

@@ -100,6 +100,43 @@ def conv_forward(x: torch.Tensor, och: torch.Tensor, oh: torch.Tensor, ow: torch
     return (op * probs.unsqueeze(-1).unsqueeze(-1)).sum(2)
 
 
+def _gate_coefficients(dtype) -> torch.Tensor:
+    """[16, 4]: gate g(a, b) = c0 + c1 a + c2 b + c3 a b, read off _GATES at the corners."""
+    one, zero = torch.ones(()), torch.zeros(())
+    f = torch.tensor([[float(gate(zero, zero)), float(gate(one, zero)), float(gate(zero, one)),
+                       float(gate(one, one))] for gate in _GATES], dtype=dtype)
+    return torch.stack((f[:, 0], f[:, 1] - f[:, 0], f[:, 2] - f[:, 0],
+                        f[:, 3] - f[:, 1] - f[:, 2] + f[:, 0]), dim=1)
+
+
+def tree_block_forward(x: torch.Tensor, logits: torch.Tensor, selection: torch.Tensor,
+                       stride, padding, kernel) -> torch.Tensor:
+    """Complete logic-tree conv block, x [N, C, H, W] -> [N, Cout, Ho/2, Wo/2], as the
+    reference's python path (third_party/convlogic_source_code/src/convlogic/
+    convlogic_layer.py:236-321): 8 taps per output channel (selection = ch << 16 | row << 8 |
+    col, zero outside the image), relaxed gates on the tap pairs, then on (0,1), (2,3) and the
+    pair of those, mixed with softmax(logits) [Cout, 7, 16]; 2x2 max pool."""
+    coef = torch.softmax(logits, dim=-1) @ _gate_coefficients(x.dtype)     # [Cout, 7, 4]
+    sel = selection.long()
+    ch, ry, rx = (sel >> 16) & 0xFFFF, (sel >> 8) & 0xFF, sel & 0xFF       # [Cout, 8]
+    (sh, sw), (ph, pw), (kh, kw) = stride, padding, kernel
+    n, _, h, w = x.shape
+    ho, wo = (h + 2 * ph - kh) // sh + 1, (w + 2 * pw - kw) // sw + 1
+    xp = torch.nn.functional.pad(x, (pw, pw, ph, ph))
+    cout = sel.shape[0]
+    iy = (torch.arange(ho) * sh).view(1, 1, ho, 1) + ry.view(cout, 8, 1, 1)
+    ix = (torch.arange(wo) * sw).view(1, 1, 1, wo) + rx.view(cout, 8, 1, 1)
+    taps = xp[:, ch.view(cout, 8, 1, 1), iy, ix]                           # [N, Cout, 8, Ho, Wo]
+
+    def node(q, a, b):
+        c = [coef[:, q, i].view(1, cout, 1, 1) for i in range(4)]
+        return c[0] + c[1] * a + c[2] * b + c[3] * (a * b)
+
+    g = [node(j, taps[:, :, 2 * j], taps[:, :, 2 * j + 1]) for j in range(4)]
+    r = node(6, node(4, g[0], g[1]), node(5, g[2], g[3]))
+    return torch.nn.functional.max_pool2d(r, 2)
+
+
 def group_sum(x: torch.Tensor, k: int, tau: float) -> torch.Tensor:
     if x.shape[-1] % k:
         x = torch.cat([x, torch.zeros((x.shape[0], k - x.shape[1] % k), dtype=x.dtype)], dim=1)
@@ -119,9 +156,10 @@ class CpuDenseNet:
             if spec[0] == "flatten":
                 self.layers.append(spec)
                 continue
-            *bufs, lg = spec[1:-2] if spec[0] == "conv" else spec[1:]
+            ntail = {"conv": 2, "tree": 3}.get(spec[0], 0)
+            *bufs, lg = spec[1:len(spec) - ntail]
             leaf = lg.detach().cpu().to(dtype).clone().requires_grad_(True)
-            tail = tuple(spec[-2:]) if spec[0] == "conv" else ()
+            tail = tuple(spec[len(spec) - ntail:])
             self.layers.append((spec[0],) + tuple(b.cpu() for b in bufs) + (leaf,) + tail)
         self.k, self.tau, self.dtype = k, tau, dtype
 
@@ -129,7 +167,10 @@ class CpuDenseNet:
     def from_model(cls, model, dtype=torch.float32):
         from_layers, k, tau = [], None, None
         for m in model:
-            if hasattr(m, "offsets_ch"):
+            if hasattr(m, "selection") and getattr(m, "complete", False):
+                from_layers.append(("tree", m.selection, m.weights, m.stride, m.padding,
+                                    m.kernel))
+            elif hasattr(m, "offsets_ch"):
                 from_layers.append(("conv", m.offsets_ch, m.offsets_h, m.offsets_w,
                                     m.gate_sequence, m.weights, m.stride, tuple(m.out_shape[1:])))
             elif hasattr(m, "indices"):
@@ -141,8 +182,8 @@ class CpuDenseNet:
         return cls(from_layers, k, tau, dtype)
 
     def leaves(self):
-        return [spec[-3] if spec[0] == "conv" else spec[-1]
-                for spec in self.layers if spec[0] != "flatten"]
+        ntail = {"conv": 2, "tree": 3}
+        return [spec[-1 - ntail.get(spec[0], 0)] for spec in self.layers if spec[0] != "flatten"]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         h = x.cpu().to(self.dtype)
@@ -151,6 +192,8 @@ class CpuDenseNet:
                 h = layer_forward(h, *spec[1:])
             elif spec[0] == "conv":
                 h = conv_forward(h, *spec[1:])
+            elif spec[0] == "tree":
+                h = tree_block_forward(h, spec[2], spec[1], *spec[3:])
             else:
                 h = h.flatten(1)
         return group_sum(h, self.k, self.tau)

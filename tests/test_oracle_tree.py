@@ -162,3 +162,40 @@ def test_block_bits_matches_float_block_on_one_hot(complete):
     out = T.block_bits(words, gates, sel.numpy(), (c_in, h, w), stride, pad, kernel, complete)
     got = np.stack([(out[:, 0] >> np.uint64(j)) & np.uint64(1) for j in range(n)])
     assert np.array_equal(got.astype(np.float64), ref.reshape(n, -1))
+
+
+def test_cpu_baseline_tree_block_matches_oracle():
+    """The torch CPU block timed as the CPU baseline (oracle/torch_cpu.py) is the oracle's
+    function: values and input gradient."""
+    from oracle import torch_cpu as TC
+    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    x, w_prob, sel = make(11, 2, 3, 10, 10, 4)
+    logits = torch.log(w_prob)                       # softmax(log p) = p
+    xx = x.clone().requires_grad_(True)
+    y = TC.tree_block_forward(xx, logits, sel, stride, pad, kernel)
+    ry = T.block_forward(x.numpy(), w_prob.numpy(), sel.numpy(), stride, pad, kernel)[0]
+    np.testing.assert_allclose(y.detach().numpy(), ry, rtol=1e-12, atol=1e-12)
+    gy = np.random.default_rng(12).standard_normal(ry.shape)
+    y.backward(torch.as_tensor(gy))
+    gx, _ = T.block_backward(x.numpy(), w_prob.numpy(), sel.numpy(), stride, pad, kernel, gy)
+    np.testing.assert_allclose(xx.grad.numpy(), gx, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("shape,stride,pad,kernel", [((9, 16, 16), (2, 2), (1, 1), (3, 3)),
+                                                     ((3, 6, 6), (1, 1), (1, 1), (3, 3)),
+                                                     ((4, 8, 8), (2, 2), (0, 0), (2, 2))])
+def test_c_tree_block_matches_numpy_bits(shape, stride, pad, kernel):
+    """The C restatement (oracle/packed_ref.c, timed as the packed CPU baseline) equals the
+    numpy bit evaluator, which is pinned against the float block above."""
+    from oracle import packed as P
+    rng = np.random.default_rng(13)
+    c_in, h, w = shape
+    c_out = 5
+    xw = rng.integers(0, 2**63, (c_in * h * w, 3), dtype=np.int64).view(np.uint64)
+    gates = rng.integers(0, 16, (c_out, 7)).astype(np.uint8)
+    _, _, sel = make(14, 1, c_in, h, w, c_out, kernel[0])
+    sel = sel.numpy()
+    if kernel[1] != kernel[0]:
+        sel = (sel & ~0xFF) | (sel & 0xFF) % kernel[1]
+    ref = T.block_bits(xw, gates, sel, shape, stride, pad, kernel, True)
+    assert np.array_equal(P.tree_block_bits(xw, gates, sel, shape, stride, pad, kernel), ref)
