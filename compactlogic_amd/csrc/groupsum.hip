@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) void k_gsum_bwd_generic(Src src, int64_t B, in
 // finish, slices in order) into out and LDS, then one thread per sample takes the softmax
 // (kept for the backward), its loss term and whether it counts.  k_ce_mean: one workgroup adds
 // the terms in a fixed order.  Both are deterministic.
-constexpr int kCeSamples = 64;
+constexpr int kCeSamples = 16;
 constexpr int kCeThreads = 256;
 
 template <typename T>
