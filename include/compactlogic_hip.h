@@ -356,7 +356,7 @@ int cl_group_sum_backward(int dtype, const void* grad_out, int64_t batch, int64_
  *   count[0]          = the number of counted samples (labels[n] != ignore_index).
  * A label outside [0, k) that is not ignore_index makes the loss NaN.  The reduction order is
  * fixed, so the loss is bitwise repeatable.  loss and count are device scalars of dtype.
- * workspace: at least cl_group_sum_cross_entropy_workspace_size bytes; k <= 128. */
+ * workspace: at least cl_group_sum_cross_entropy_workspace_size bytes; k <= 512. */
 int cl_group_sum_cross_entropy_forward(int dtype, const void* x, int64_t batch, int64_t features,
                                        int64_t stride_batch, int64_t stride_feature, int64_t k,
                                        double tau, const int64_t* labels, int64_t ignore_index,
