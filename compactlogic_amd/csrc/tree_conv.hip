@@ -32,7 +32,7 @@ namespace {
 constexpr int kTaps = 8;
 constexpr int kMaxNodes = 7;
 constexpr int kGatherBatch = 4;  // channel uses whose loads the input-gradient gather overlaps
-constexpr int kNodeItems = 4;    // items per thread of the backward node kernel
+constexpr int kNodeItems = 16;   // items per thread of the backward node kernel
 
 template <typename T>
 __device__ __forceinline__ T quiet_nan() {
