@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void k_tree_fwd(const T* __restrict__ x, const
     for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? quiet_nan<T>() : e.g[q];
 }
 
-constexpr int kFwdItems = 4;  // passes of 256 items per forward workgroup
+constexpr int kFwdItems = 8;  // passes of 256 items per forward workgroup
 
 // Complete block, quad form: one thread per conv position, the four positions of a pooling
 // window in the four lanes of a quad (lane order (0,0), (0,1), (1,0), (1,1)), so each thread
