@@ -72,10 +72,11 @@ def dense_step_fn(model, x, labels, torch):
     GroupSum's kernels: GroupSum.cross_entropy is cross_entropy(GroupSum(x), labels)), and the
     backward into every layer's logits."""
     body, head = model[:-1], model[-1]
+    one = torch.ones((), dtype=torch.float32, device=x.device)  # d loss / d loss, made once
 
     def step():
         loss = head.cross_entropy(body(x), labels)
-        loss.backward()
+        loss.backward(one)
         return loss
     return step
 
