@@ -321,10 +321,12 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward, input gradient.  Workgroup (n, channel group); LDS holds the gradient of CG input
-// channels.  A lane group of PW lanes (PW = items per pass, a power of two <= 64) owns one input
-// channel at a time and walks its uses ent[ent_ptr[ch] ..) = c * 8 + k in order; lane pl of the
-// group handles items pl, pl + PW, ...  For use (c, k) at item p (conv position win, the pooled
+// Backward, input gradient.  Workgroup (spw samples, channel group); LDS holds the gradient of
+// CG input channels of each sample.  A lane group of PW * spw lanes (PW = items per pass, a power
+// of two <= 64; spw samples, each with PW lanes) owns one input channel at a time and walks its
+// uses ent[ent_ptr[ch] ..) = c * 8 + k in order, so one use's taps and coefficients serve all
+// spw samples; lane pl of a sample handles items pl, pl + PW, ...  Each (sample, channel) plane
+// is added to by its own lanes only, in use order.  For use (c, k) at item p (conv position win, the pooled
 // window's winner when complete) the tap reads (iy, ix) = (oy*sh + dy_k, ox*sw + dx_k) and adds
 //   gconv[n, c, p, k/2] * (k even ? K1 + K3 x_partner : K2 + K3 x_partner)
 // of node k/2, x_partner being the other tap of the node at the same position.
@@ -335,21 +337,27 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
                                                      const int32_t* __restrict__ ent_ptr,
                                                      const int32_t* __restrict__ ent,
                                                      const T* __restrict__ kc, TreeDims d, int cg,
-                                                     int pw_lanes, T* __restrict__ grad_x) {
+                                                     int pw_lanes, int spw,
+                                                     T* __restrict__ grad_x) {
     constexpr int NODES = COMPLETE ? 7 : 4;
     extern __shared__ unsigned char smem_raw[];
-    T* gx = reinterpret_cast<T*>(smem_raw);
-    const int n = blockIdx.x;
+    T* gx = reinterpret_cast<T*>(smem_raw);  // [spw][cg][h * w]
+    const int n0 = blockIdx.x * spw;
     const int ch0 = blockIdx.y * cg;
     const int nch = min(cg, d.cin - ch0);
     const int hw = d.h * d.w;
-    for (int i = threadIdx.x; i < nch * hw; i += 256) gx[i] = T(0);
+    for (int i = threadIdx.x; i < spw * nch * hw; i += 256) gx[i] = T(0);
     __syncthreads();
-    const T* xn = x + int64_t(n) * d.cin * hw;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int PW = pw_lanes;
-    const int groups_per_wave = 64 / PW;
-    const int sub = lane / PW, pl = lane % PW;
+    // a lane group of PW * spw lanes: spw samples, PW items of each
+    const int GL = PW * spw;
+    const int groups_per_wave = 64 / GL;
+    const int sub = lane / GL, gl = lane % GL, sl = gl / PW, pl = gl % PW;
+    const int n = n0 + sl;
+    const bool n_ok = n < d.n;
+    const T* xn = x + int64_t(n_ok ? n : 0) * d.cin * hw;
+    T* gxs = gx + sl * nch * hw;
     // channel slot handled by this lane group in pass `it`: wave-major so a wave's groups take
     // consecutive channels
     for (int base = 0; base < nch; base += 4 * groups_per_wave) {
@@ -370,8 +378,8 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
             int kn[kGatherBatch];
 #pragma unroll
             for (int i = 0; i < kGatherBatch; ++i) {
-                on[i] = j + i < e1 - e0;
-                const int u = on[i] ? ent[e0 + j + i] : 0;
+                on[i] = n_ok && j + i < e1 - e0;
+                const int u = j + i < e1 - e0 ? ent[e0 + j + i] : 0;
                 const int c = u >> 3, k = u & 7;
                 tk[i] = decode_tap(sel[c * kTaps + k], d.ph, d.pw);
                 tp[i] = decode_tap(sel[c * kTaps + (k ^ 1)], d.ph, d.pw);
@@ -400,13 +408,15 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
                 }
 #pragma unroll
                 for (int i = 0; i < kGatherBatch; ++i)
-                    if (tgt[i] >= 0) atomicAdd(&gx[(ch - ch0) * hw + tgt[i]], add[i]);
+                    if (tgt[i] >= 0) atomicAdd(&gxs[(ch - ch0) * hw + tgt[i]], add[i]);
             }
         }
     }
     __syncthreads();
-    T* dst = grad_x + (int64_t(n) * d.cin + ch0) * hw;
-    for (int i = threadIdx.x; i < nch * hw; i += 256) dst[i] = gx[i];
+    for (int i = threadIdx.x; i < spw * nch * hw; i += 256) {
+        const int si = i / (nch * hw), r = i % (nch * hw);
+        if (n0 + si < d.n) grad_x[(int64_t(n0 + si) * d.cin + ch0) * hw + r] = gx[i];
+    }
 }
 
 // grad_w[c][q][g] = c0(g) M3 + c1(g) M1 + c2(g) M2 + c3(g) M0 with M the node's moments summed
@@ -877,18 +887,23 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
             // one pass of the workgroup's lane groups per channel group: more workgroups
             // (each staging only its channels) keep more waves in flight
             const int pw_lanes = gather_lanes(d.P);
-            const int cg = int(std::min<int64_t>(std::min<int64_t>(d.cin, 4 * (64 / pw_lanes)),
-                                                 kGatherLdsBytes / hw_bytes));
-            const dim3 g2(unsigned(d.n), unsigned(ceil_div(d.cin, cg)));
-            const size_t lds = size_t(cg) * size_t(hw_bytes);
+            // small pooled planes: a lane group takes several samples of a channel, so the
+            // loads of a use's taps and coefficients serve PW * spw lanes
+            int spw = std::max(1, 32 / pw_lanes);
+            while (spw > 1 && int64_t(spw) * hw_bytes > kGatherLdsBytes) spw >>= 1;
+            const int cg = int(std::max<int64_t>(1, std::min<int64_t>(
+                std::min<int64_t>(d.cin, 4 * (64 / (pw_lanes * spw))),
+                kGatherLdsBytes / (hw_bytes * spw))));
+            const dim3 g2(unsigned(ceil_div(d.n, spw)), unsigned(ceil_div(d.cin, cg)));
+            const size_t lds = size_t(spw) * size_t(cg) * size_t(hw_bytes);
             const T* src = complete ? gconv : gy;
             if (complete)
                 k_tree_gather<T, true><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
-                                                            ent, kc, d, cg, pw_lanes,
+                                                            ent, kc, d, cg, pw_lanes, spw,
                                                             static_cast<T*>(grad_x));
             else
                 k_tree_gather<T, false><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
-                                                             ent, kc, d, cg, pw_lanes,
+                                                             ent, kc, d, cg, pw_lanes, spw,
                                                              static_cast<T*>(grad_x));
             if (int rc = check_launch("cl_tree_conv_backward(gather)")) return rc;
         }
