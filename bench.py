@@ -533,7 +533,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs are "
-                                   "not part of this build (see DESIGN.md, sharding)",
+                                   "not part of this build",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
