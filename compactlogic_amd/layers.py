@@ -10,6 +10,7 @@ that is not on a HIP device is rejected, never computed on the CPU.
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import numpy as np
 import torch
@@ -797,7 +798,7 @@ class ConvLayer(LogicLayer):
         assert self.is_frozen or not self.training
         w = getattr(self, "w", None)
         if w is None:
-            w = self.weights.argmax(-1).to(dtype=torch.uint8, device=self.weights.device)
+            w = self._argmax_slots()
         if isinstance(x, PackBitsTensor):
             ia, ib, gate = self.packed_tables(w)
             order = self.packed_order(w)
@@ -809,13 +810,29 @@ class ConvLayer(LogicLayer):
                         self.gate_sequence, self.stride, self.padding, self.ks)
 
     @torch.no_grad()
+    def _argmax_slots(self) -> torch.Tensor:
+        """Winner slots of an unfrozen layer (argmax of the logits, uint8), kept while the
+        logits tensor is alive and unmodified, so the packed tables derived from them stay
+        cached across eval calls."""
+        src = self.weights
+        hit = getattr(self, "_argmax_cache", None)
+        if hit is not None and hit[0]() is src and hit[1] == src._version:
+            return hit[2]
+        w = src.argmax(-1).to(dtype=torch.uint8, device=src.device)
+        self._argmax_cache = (weakref.ref(src), src._version, w)
+        return w
+
+    @torch.no_grad()
     def packed_tables(self, w: torch.Tensor):
         """(ia, ib, gate) per output feature (c, oy, ox) for the winner slots ``w``: the
         flattened NCHW input feature of each tap, -1 outside the plane (compiler/extract.py:
-        101-174), and the opcode.  Cached until the offsets, opcodes or winners change."""
-        key = (w.data_ptr(), w._version, self.offsets_ch._version, self.offsets_h._version,
-               self.offsets_w._version, self.gate_sequence._version, w.device)
-        if self._packed_key == key:
+        101-174), and the opcode.  Cached until the offsets, opcodes or winners change: the
+        cache holds weak references to those tensors and their versions, so a new tensor at a
+        recycled address never hits it."""
+        srcs = (w, self.offsets_ch, self.offsets_h, self.offsets_w, self.gate_sequence)
+        key = tuple(t._version for t in srcs)
+        hit = self._packed_key
+        if hit is not None and hit[1] == key and all(r() is t for r, t in zip(hit[0], srcs)):
             return self._packed_tables
         dev = w.device
         c_in, h, wd = self.in_shape
@@ -836,7 +853,7 @@ class ConvLayer(LogicLayer):
                 .expand(self.c_out, self.h_out * self.w_out).reshape(-1).contiguous())
         self._packed_tables = (tables[0], tables[1], gate)
         self._packed_order = None
-        self._packed_key = key
+        self._packed_key = (tuple(weakref.ref(t) for t in srcs), key)
         return self._packed_tables
 
     def packed_order(self, w: torch.Tensor) -> torch.Tensor:

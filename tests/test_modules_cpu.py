@@ -224,6 +224,42 @@ def test_conv_packed_tables_match_oracle():
     assert layer.packed_tables(layer.w)[0] is not ia
 
 
+def test_conv_packed_tables_not_hit_by_recycled_storage():
+    """A new winners tensor over the same storage (same data_ptr, version 0) must rebuild the
+    tables, not return those of the tensor it replaces."""
+    from oracle import packed as P
+    torch.manual_seed(5)
+    layer = cl.ConvLayer((2, 6, 6), padding=1, c_out=4, ks=3, stride=1, num_chn=0, num_gates=4)
+    store = torch.zeros(layer.c_out, dtype=torch.uint8)
+    w0 = store.view(layer.c_out)
+    t0 = layer.packed_tables(w0)
+    del w0
+    store.numpy()[:] = [1, 2, 3, 0]          # a write torch does not see: versions stay 0
+    w1 = store.view(layer.c_out)
+    assert w1.data_ptr() == store.data_ptr() and w1._version == 0
+    ia, ib, g = layer.packed_tables(w1)
+    assert ia is not t0[0]
+    ra, rb, rg = P.resolve_conv_slots(layer.offsets_ch.numpy(), layer.offsets_h.numpy(),
+                                      layer.offsets_w.numpy(), layer.gate_sequence.numpy(),
+                                      w1.numpy(), layer.in_shape, 1, layer.out_shape[1:])
+    assert np.array_equal(ia.numpy(), ra) and np.array_equal(ib.numpy(), rb)
+    assert np.array_equal(g.numpy(), rg)
+
+
+def test_conv_eval_winners_follow_weight_updates():
+    """An unfrozen layer in eval mode takes its winners from the logits; an in-place update of
+    the logits must change the cached winners."""
+    torch.manual_seed(6)
+    layer = cl.ConvLayer((2, 6, 6), padding=1, c_out=4, ks=3, stride=1, num_chn=0, num_gates=4)
+    w0 = layer._argmax_slots()
+    assert layer._argmax_slots() is w0
+    with torch.no_grad():
+        layer.weights.zero_()
+        layer.weights[:, 2] = 1.0
+    w1 = layer._argmax_slots()
+    assert w1 is not w0 and torch.equal(w1, torch.full((4,), 2, dtype=torch.uint8))
+
+
 def test_conv_layer_rewiring_keeps_ranges():
     torch.manual_seed(4)
     layer = cl.ConvLayer((4, 8, 8), padding=1, c_out=6, ks=3, stride=1, num_chn=0, num_gates=8)
