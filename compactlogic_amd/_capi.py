@@ -6,12 +6,10 @@ is no fallback: if the library is missing or fails to load, every call raises.
 from __future__ import annotations
 
 import ctypes
-import os
 from pathlib import Path
 
-# COMPACTLOGIC_HIP_LIB selects another build of the same library (e.g. a tuning variant).
-LIB_PATH = Path(os.environ.get("COMPACTLOGIC_HIP_LIB",
-                               Path(__file__).resolve().parent / "libcompactlogic_hip.so"))
+# The in-tree build; nothing else is loaded.
+LIB_PATH = Path(__file__).resolve().parent / "libcompactlogic_hip.so"
 
 CL_OK = 0
 CL_ERR_INVALID_ARGUMENT = 1
@@ -100,12 +98,12 @@ class CompactLogicError(RuntimeError):
     """Raised when an entry point of the HIP library reports a failure."""
 
 
-def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
-    """Load (once) and return the HIP library; raises if it is missing."""
+def load() -> ctypes.CDLL:
+    """Load (once) and return the in-tree HIP library; raises if it is missing."""
     global _lib
     if _lib is not None:
         return _lib
-    p = Path(path) if path is not None else LIB_PATH
+    p = LIB_PATH
     if not p.exists():
         raise CompactLogicError(
             f"HIP library not found at {p}; build it with `python -m compactlogic_amd.build`")

@@ -44,10 +44,6 @@ __device__ __forceinline__ V vld(const void* p) {
     return *reinterpret_cast<const V*>(p);
 }
 
-#ifndef CL_STREAM_STORES
-#define CL_STREAM_STORES 0
-#endif
-
 // Lane accesses of the forward / backward tiled kernels are this many 16-byte vectors wide
 // (two for the backward: twice the bytes per gather for the same index records).
 #ifndef CL_FWD_VEC_MULT
@@ -60,21 +56,12 @@ __device__ __forceinline__ V vld(const void* p) {
 #define CL_FUSED_VEC_MULT 1
 #endif
 
-// Inverse-index entries a backward lane group handles per step (loads kept in flight).
-#ifndef CL_BWD_UNROLL
-#define CL_BWD_UNROLL 1
-#endif
-
 // Store of an output row segment.  Regular (write-back) stores measure faster inside a
 // training step than non-temporal ones: the next kernel reads these rows right away and then
 // finds them in the Infinity Cache.
 template <typename V>
 __device__ __forceinline__ void vst_stream(void* p, V v) {
-#if CL_STREAM_STORES
-    __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
-#else
     *reinterpret_cast<V*>(p) = v;
-#endif
 }
 
 template <typename T, int N>
@@ -130,10 +117,6 @@ __host__ __device__ __forceinline__ int64_t tile_grid(const TileMap& m) {
     return m.nchunks * m.ntiles;
 }
 
-#ifndef CL_TILE_ROTATE
-#define CL_TILE_ROTATE 0
-#endif
-
 __device__ __forceinline__ bool map_tile(const TileMap& m, int64_t w, int64_t& c, int64_t& t) {
     // grids stay below 2^32 workgroups and tile counts below 2^31: 32-bit divisions
     const uint32_t nt = uint32_t(m.ntiles);
@@ -145,28 +128,7 @@ __device__ __forceinline__ bool map_tile(const TileMap& m, int64_t w, int64_t& c
         c = uint32_t(w) / nt;
         t = uint32_t(w) % nt;
     }
-#if CL_TILE_ROTATE
-    // Chunk c starts its tile sweep at a different row band, so the XCDs working on different
-    // chunks at the same moment read different rows.
-    t += (c % kXcds) * m.ntiles / kXcds;
-    if (t >= m.ntiles) t -= m.ntiles;
-#endif
     return c < m.nchunks;
-}
-
-#ifndef CL_TILE_ITERS
-#define CL_TILE_ITERS 1
-#endif
-
-// Virtual tile `it` of workgroup w: the same XCD (w % kXcds), consecutive along that XCD.
-__device__ __forceinline__ int64_t virtual_tile(int64_t w, int it) {
-    return ((w / kXcds) * CL_TILE_ITERS + it) * kXcds + w % kXcds;
-}
-
-// Grid of a kernel whose workgroups each take CL_TILE_ITERS virtual tiles.
-inline int64_t iter_grid(const TileMap& m) {
-    const int64_t v = tile_grid(m);
-    return kXcds * ceil_div(v, int64_t(kXcds) * CL_TILE_ITERS);
 }
 
 constexpr int kMaxSlotGroups = 8;  // G <= 128 = 8 groups of 16 slots
@@ -317,8 +279,6 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ x, const T* __res
     }
 }
 
-// Workgroup w handles CL_TILE_ITERS consecutive virtual tiles of its XCD (w % 8), so fewer,
-// longer-lived workgroups cover the grid.
 template <typename T, int VEC, int LPN, int NPG>
 __global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
                                                    const T* __restrict__ kc,
@@ -327,11 +287,9 @@ __global__ __launch_bounds__(256) void k_fwd_tiled(const T* __restrict__ x,
                                                    T* __restrict__ y, int64_t in_dim,
                                                    int64_t out_dim, int64_t num_runs, int64_t B,
                                                    TileMap tm) {
-    for (int it = 0; it < CL_TILE_ITERS; ++it) {
-        int64_t c, t;
-        if (map_tile(tm, virtual_tile(blockIdx.x, it), c, t))
-            fwd_tile<T, VEC, LPN, NPG>(x, kc, nab, run_ab, y, in_dim, out_dim, num_runs, B, c, t);
-    }
+    int64_t c, t;
+    if (map_tile(tm, blockIdx.x, c, t))
+        fwd_tile<T, VEC, LPN, NPG>(x, kc, nab, run_ab, y, in_dim, out_dim, num_runs, B, c, t);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -511,12 +469,10 @@ __global__ __launch_bounds__(256) void k_fwd_fused(const T* __restrict__ x, cons
                                                    T* __restrict__ y, int64_t in_dim,
                                                    int64_t out_dim, int64_t num_runs, int64_t B,
                                                    int G, TileMap tm) {
-    for (int it = 0; it < CL_TILE_ITERS; ++it) {
-        int64_t c, t;
-        if (map_tile(tm, virtual_tile(blockIdx.x, it), c, t))
-            fwd_fused_tile<T, VEC, LPN, NPG>(x, w, softmax, gs, nab, inv_pos, probs, inv_coef, y,
-                                             in_dim, out_dim, num_runs, B, G, tm, c, t);
-    }
+    int64_t c, t;
+    if (map_tile(tm, blockIdx.x, c, t))
+        fwd_fused_tile<T, VEC, LPN, NPG>(x, w, softmax, gs, nab, inv_pos, probs, inv_coef, y,
+                                         in_dim, out_dim, num_runs, B, G, tm, c, t);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -792,77 +748,68 @@ __device__ __forceinline__ void bwd_tile(
         xi[j] = V(T(0));
         if (WANT_GW && live[j] && col) xi[j] = vld<V>(x + row[j] * B + idx);
     }
-    // Entries are taken U at a time: the records of the next U entries are fetched while
-    // the gathers of the current U are in flight, so each lane group keeps 2U row segments
-    // in flight.  The accumulation order is still the entry order.
-    constexpr int U = CL_BWD_UNROLL;
-    int4 rec[NPG][U];
-    V2 kk[NPG][U];
+    // The records of the next entry are fetched while the current entry's gathers are in
+    // flight; the accumulation order is the entry order.
+    int4 rec[NPG];
+    V2 kk[NPG];
 #pragma unroll
-    for (int j = 0; j < NPG; ++j)
+    for (int j = 0; j < NPG; ++j) {
+        rec[j] = make_int4(0, 0, 0, 0);
+        kk[j] = V2(T(0));
+        if (deg[j] > 0) {
+            rec[j] = inv_rec[e0[j]];
+            kk[j] = vld<V2>(inv_coef + 2 * e0[j]);
+        }
+    }
+    for (int64_t k = 0; k < maxdeg; ++k) {
+        int4 cur[NPG];
+        V2 ck[NPG];
+        V vo[NPG], vg[NPG];
+        bool use[NPG];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            rec[j][u] = make_int4(0, 0, 0, 0);
-            kk[j][u] = V2(T(0));
-            if (u < deg[j]) {
-                rec[j][u] = inv_rec[e0[j] + u];
-                kk[j][u] = vld<V2>(inv_coef + 2 * (e0[j] + u));
+        for (int j = 0; j < NPG; ++j) {
+            cur[j] = rec[j];
+            ck[j] = kk[j];
+            if (k + 1 < deg[j]) {
+                rec[j] = inv_rec[e0[j] + k + 1];
+                kk[j] = vld<V2>(inv_coef + 2 * (e0[j] + k + 1));
+            }
+            use[j] = k < deg[j];
+            if (use[j] && (uint64_t(cur[j].x) >= uint64_t(out_dim) ||
+                           uint64_t(cur[j].y) >= uint64_t(in_dim) ||
+                           uint64_t(cur[j].z) >= uint64_t(num_runs))) {
+                bad[j] = true;
+                use[j] = false;
+            }
+            vo[j] = V(T(0));
+            vg[j] = V(T(0));
+            if (use[j] && col) {
+                vo[j] = vld<V>(x + int64_t(cur[j].y) * B + idx);
+                vg[j] = vld<V>(gy + int64_t(cur[j].x) * B + idx);
             }
         }
-    for (int64_t k = 0; k < maxdeg; k += U) {
-        int4 cur[NPG][U];
-        V2 ck[NPG][U];
-        V vo[NPG][U], vg[NPG][U];
-        bool use[NPG][U];
 #pragma unroll
-        for (int j = 0; j < NPG; ++j)
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                cur[j][u] = rec[j][u];
-                ck[j][u] = kk[j][u];
-                if (k + U + u < deg[j]) {
-                    rec[j][u] = inv_rec[e0[j] + k + U + u];
-                    kk[j][u] = vld<V2>(inv_coef + 2 * (e0[j] + k + U + u));
-                }
-                use[j][u] = k + u < deg[j];
-                if (use[j][u] && (uint64_t(cur[j][u].x) >= uint64_t(out_dim) ||
-                                  uint64_t(cur[j][u].y) >= uint64_t(in_dim) ||
-                                  uint64_t(cur[j][u].z) >= uint64_t(num_runs))) {
-                    bad[j] = true;
-                    use[j][u] = false;
-                }
-                vo[j][u] = V(T(0));
-                vg[j][u] = V(T(0));
-                if (use[j][u] && col) {
-                    vo[j][u] = vld<V>(x + int64_t(cur[j][u].y) * B + idx);
-                    vg[j][u] = vld<V>(gy + int64_t(cur[j][u].x) * B + idx);
+        for (int j = 0; j < NPG; ++j) {
+            if (!use[j]) continue;
+            if (WANT_GX) acc[j] += (ck[j][0] + ck[j][1] * vo[j]) * vg[j];
+            if (WANT_GW && cur[j].w == 0) {
+                const V ga = vg[j] * xi[j];
+                T s1 = hsum<T, VEC>(vg[j]), sa = hsum<T, VEC>(ga);
+                T sb = hsum<T, VEC>(vg[j] * vo[j]), sab = hsum<T, VEC>(ga * vo[j]);
+                s1 = group_sum<LPN>(s1);
+                sa = group_sum<LPN>(sa);
+                sb = group_sum<LPN>(sb);
+                sab = group_sum<LPN>(sab);
+                if (leader) {
+                    V4 mv;
+                    mv[0] = s1;
+                    mv[1] = sa;
+                    mv[2] = sb;
+                    mv[3] = sab;
+                    *reinterpret_cast<V4*>(part + (int64_t(cur[j].z) * tm.nchunks + c) * 4) = mv;
                 }
             }
-#pragma unroll
-        for (int j = 0; j < NPG; ++j)
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (!use[j][u]) continue;
-                const int side = cur[j][u].w;
-                if (WANT_GX) acc[j] += (ck[j][u][0] + ck[j][u][1] * vo[j][u]) * vg[j][u];
-                if (WANT_GW && side == 0) {
-                    const V ga = vg[j][u] * xi[j];
-                    T s1 = hsum<T, VEC>(vg[j][u]), sa = hsum<T, VEC>(ga);
-                    T sb = hsum<T, VEC>(vg[j][u] * vo[j][u]), sab = hsum<T, VEC>(ga * vo[j][u]);
-                    s1 = group_sum<LPN>(s1);
-                    sa = group_sum<LPN>(sa);
-                    sb = group_sum<LPN>(sb);
-                    sab = group_sum<LPN>(sab);
-                    if (leader) {
-                        V4 mv;
-                        mv[0] = s1;
-                        mv[1] = sa;
-                        mv[2] = sb;
-                        mv[3] = sab;
-                        *reinterpret_cast<V4*>(part + (int64_t(cur[j][u].z) * tm.nchunks + c) * 4) = mv;
-                    }
-                }
-            }
+        }
     }
     if (WANT_GX && col) {
 #pragma unroll
@@ -881,13 +828,10 @@ __global__ __launch_bounds__(256) void k_bwd_tiled(
     const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef, T* __restrict__ gx,
     T* __restrict__ part,
     int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, TileMap tm) {
-    for (int it = 0; it < CL_TILE_ITERS; ++it) {
-        int64_t c, t;
-        if (map_tile(tm, virtual_tile(blockIdx.x, it), c, t))
-            bwd_tile<T, VEC, LPN, NPG, WANT_GX, WANT_GW>(x, gy, slot_rec, inv_rec, inv_coef, gx,
-                                                         part, in_dim, out_dim, num_runs, B, tm,
-                                                         c, t);
-    }
+    int64_t c, t;
+    if (map_tile(tm, blockIdx.x, c, t))
+        bwd_tile<T, VEC, LPN, NPG, WANT_GX, WANT_GW>(x, gy, slot_rec, inv_rec, inv_coef, gx, part,
+                                                     in_dim, out_dim, num_runs, B, tm, c, t);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1419,7 +1363,7 @@ extern "C" int cl_dense_forward_tiled(int dtype, const void* x, const void* run_
         using T = scalar_t;
         CL_ARG(!vec_ok<T>(batch) || all_aligned({x, y}), "x and y must be 16-byte aligned");
         const Tiling tl = choose_tiling<T>(batch, out_dim, CL_FWD_VEC_MULT, CL_FWD_LPN, CL_FWD_NPG);
-        const unsigned grid = unsigned(iter_grid(tl.map));
+        const unsigned grid = unsigned(tile_grid(tl.map));
         auto* xs = static_cast<const T*>(x);
         auto* kc = static_cast<const T*>(run_coef);
         auto* nb = reinterpret_cast<const int4*>(nab);
@@ -1454,7 +1398,7 @@ extern "C" int cl_dense_forward_fused(int dtype, const void* x, const void* w, i
         using T = scalar_t;
         CL_ARG(!vec_ok<T>(batch) || all_aligned({x, y}), "x and y must be 16-byte aligned");
         const Tiling tl = choose_tiling<T>(batch, out_dim, CL_FUSED_VEC_MULT, CL_FWD_LPN, CL_FWD_NPG);
-        const unsigned grid = unsigned(iter_grid(tl.map));
+        const unsigned grid = unsigned(tile_grid(tl.map));
         auto* xs = static_cast<const T*>(x);
         auto* ws = static_cast<const T*>(w);
         auto* nb = reinterpret_cast<const int4*>(nab);
@@ -1577,7 +1521,7 @@ extern "C" int cl_dense_backward_tiled(int dtype, const void* x, const void* gra
         auto* mom = static_cast<T*>(moments);
         if (grad_x && in_dim > 0) {
             const Tiling tl = choose_tiling<T>(batch, in_dim, CL_BWD_VEC_MULT, CL_BWD_LPN, CL_BWD_NPG);
-            const unsigned grid = unsigned(iter_grid(tl.map));
+            const unsigned grid = unsigned(tile_grid(tl.map));
             if (moments) {
                 CL_ARG(nchunks == tl.map.nchunks, "moments buffer must use the backward chunk count");
                 with_tiling<T, CL_BWD_VEC_MULT>(tl, [&](auto vc, auto lc) {

@@ -56,12 +56,7 @@ __global__ __launch_bounds__(256) void k_pack_bits(const uint8_t* __restrict__ t
 // row, and the band of x they gather from stays cache resident.  The output rows are
 // written once and read by the next layer only, so 16-byte rows are stored non-temporally
 // and leave the caches to the band being gathered (7% faster per pass at cfg4).
-#ifndef CL_PACKED_NT
-#define CL_PACKED_NT 1
-#endif
-#ifndef CL_PACKED_U
-#define CL_PACKED_U 4  // 16-byte vectors per lane and row (8 measures slower)
-#endif
+constexpr int kPackedU = 4;  // 16-byte vectors per lane and row (8 measures slower)
 
 template <typename W, int VEC, int U>
 __global__ __launch_bounds__(256) void k_eval_packed(const W* __restrict__ x,
@@ -101,85 +96,15 @@ __global__ __launch_bounds__(256) void k_eval_packed(const W* __restrict__ x,
                     r.z = bitwise_op<uint32_t>(g, va.z, vb.z);
                     r.w = bitwise_op<uint32_t>(g, va.w, vb.w);
                 }
-#if CL_PACKED_NT
                 typedef unsigned int U4v __attribute__((ext_vector_type(4)));
                 const U4v rv = {r.x, r.y, r.z, r.w};
                 __builtin_nontemporal_store(rv, reinterpret_cast<U4v*>(yr + idx));
-#else
-                *reinterpret_cast<uint4*>(yr + idx) = r;
-#endif
             } else {
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     yr[idx + v] = bad ? W(0) : bitwise_op<W>(g, xa[idx + v], xb[idx + v]);
             }
         }
-    }
-}
-
-// XCD-pinned variant for 64-bit words: the words are cut into chunks of 32 (16 lanes x 16
-// bytes per row), and chunk c is evaluated only by workgroups w with w % 8 == c % 8 -- the
-// XCD that workgroup w is dispatched to -- so the chunk's band of x (rows x 256 bytes, 3 MB at
-// 12000 rows) stays in that XCD's L2 while ~two neurons gather each of its rows.  Each
-// workgroup evaluates kEvalIter tiles of 16 neurons of one chunk (one tile, so that the
-// workgroups resident on an XCD span a fraction of one chunk and its band alone occupies the
-// L2); outputs bypass the cache.
-#ifndef CL_PACKED_TILED
-#define CL_PACKED_TILED 0
-#endif
-constexpr bool kPackedTiled = CL_PACKED_TILED;  // XCD-pinned layer kernel for 16-byte rows
-constexpr int kXcds = 8;
-constexpr int kEvalLanes = 16;  // lanes per neuron row segment
-constexpr int kEvalIter = 1;    // neuron tiles per workgroup
-
-__global__ __launch_bounds__(256) void k_eval_packed_tiled(const uint64_t* __restrict__ x,
-                                                           const int64_t* __restrict__ a,
-                                                           const int64_t* __restrict__ b,
-                                                           const uint8_t* __restrict__ wslot,
-                                                           const uint8_t* __restrict__ gs,
-                                                           uint64_t* __restrict__ y,
-                                                           int64_t in_dim, int64_t out_dim,
-                                                           int64_t words, int G, int64_t nchunks,
-                                                           int64_t ntiles) {
-    typedef unsigned int U4 __attribute__((ext_vector_type(4)));
-    const int64_t w = blockIdx.x;
-    int64_t c, t;
-    if (nchunks >= kXcds) {
-        const int64_t xcd = w % kXcds, j = w / kXcds;
-        c = xcd + kXcds * (j / ntiles);
-        t = j % ntiles;
-    } else {
-        c = w / ntiles;
-        t = w % ntiles;
-    }
-    if (c >= nchunks) return;
-    const int64_t idx = c * (kEvalLanes * 2) + int64_t(threadIdx.x % kEvalLanes) * 2;
-    if (idx >= words) return;
-#pragma unroll
-    for (int it = 0; it < kEvalIter; ++it) {
-        const int64_t o = (t * kEvalIter + it) * (256 / kEvalLanes) + threadIdx.x / kEvalLanes;
-        if (o >= out_dim) break;
-        const int s = wslot[o];
-        bool bad = s >= G;
-        int64_t ia = 0, ib = 0;
-        int g = 0;
-        if (!bad) {
-            ia = a[o * G + s];
-            ib = b[o * G + s];
-            g = gs[o * G + s];
-            bad = uint64_t(ia) >= uint64_t(in_dim) || uint64_t(ib) >= uint64_t(in_dim);
-        }
-        U4 r = {0u, 0u, 0u, 0u};
-        if (!bad) {
-            const U4 va = *reinterpret_cast<const U4*>(x + ia * words + idx);
-            const U4 vb = *reinterpret_cast<const U4*>(x + ib * words + idx);
-            const U4 m00 = U4(0u - unsigned((g >> 3) & 1));
-            const U4 m01 = U4(0u - unsigned((g >> 2) & 1));
-            const U4 m10 = U4(0u - unsigned((g >> 1) & 1));
-            const U4 m11 = U4(0u - unsigned(g & 1));
-            r = (~va & ~vb & m00) | (~va & vb & m01) | (va & ~vb & m10) | (va & vb & m11);
-        }
-        __builtin_nontemporal_store(r, reinterpret_cast<U4*>(y + o * words + idx));
     }
 }
 
@@ -227,9 +152,6 @@ struct SliceCounter {
 
 // Every packed word is read once: non-temporal loads.  Column tiles of 32 words keep the LDS
 // transpose tile at 41 KB, so three workgroups fit a CU (48 columns: two).
-#ifndef CL_GBS_NT
-#define CL_GBS_NT 1
-#endif
 #ifndef CL_GBS_MAX_COLS
 #define CL_GBS_MAX_COLS 32
 #endif
@@ -264,11 +186,7 @@ __global__ __launch_bounds__(kGbsThreads) void k_group_bit_sum(const W* __restri
             W v[16];
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-#if CL_GBS_NT
                 v[q] = __builtin_nontemporal_load(p + (r + q) * words);
-#else
-                v[q] = p[(r + q) * words];
-#endif
             }
             W twosA, twosB, foursA, foursB, eightsA, eightsB, sixteens;
             csa(twosA, ones, ones, v[0], v[1]);
@@ -411,18 +329,8 @@ extern "C" int cl_dense_eval_packed(const void* x, const int64_t* a, const int64
     hipStream_t s = as_stream(stream);
     const int G = int(num_gates);
     const unsigned gx = unsigned(ceil_div(out_dim, 4));
-    if (kPackedTiled && row_bytes % 16 == 0 && aligned(x, 16) && aligned(y, 16)) {
-        const int64_t words = row_bytes / 8;
-        const int64_t nchunks = ceil_div(words, kEvalLanes * 2);
-        const int64_t ntiles = ceil_div(out_dim, int64_t(256 / kEvalLanes) * kEvalIter);
-        const int64_t blocks = nchunks >= kXcds ? kXcds * ceil_div(nchunks, kXcds) * ntiles
-                                                : nchunks * ntiles;
-        CL_ARG(blocks < (int64_t(1) << 32), "packed layer too large for one launch");
-        k_eval_packed_tiled<<<unsigned(blocks), 256, 0, s>>>(
-            static_cast<const uint64_t*>(x), a, b, w_slot, gate_seq, static_cast<uint64_t*>(y),
-            in_dim, out_dim, words, G, nchunks, ntiles);
-    } else if (row_bytes % 16 == 0 && aligned(x, 16) && aligned(y, 16)) {
-        constexpr int VEC = 2, U = CL_PACKED_U;
+    if (row_bytes % 16 == 0 && aligned(x, 16) && aligned(y, 16)) {
+        constexpr int VEC = 2, U = kPackedU;
         const int64_t words = row_bytes / 8;
         const dim3 grid(gx, unsigned(ceil_div(words, 64 * VEC * U)), 1);
         k_eval_packed<uint64_t, VEC, U><<<grid, 256, 0, s>>>(
