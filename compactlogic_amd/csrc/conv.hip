@@ -259,19 +259,28 @@ __global__ __launch_bounds__(256) void k_eval_packed_idx(const V* __restrict__ x
     const V m01 = zero - V((g >> 2) & 1);
     const V m10 = zero - V((g >> 1) & 1);
     const V m11 = zero - V(g & 1);
+    // every load unconditional (row 0 for a negative or bad index, element 0 past the row's
+    // end, masked afterwards), so the U loads of a lane are in flight together
+    const V ka = (!bad && a >= 0) ? ~zero : zero;
+    const V kb = (!bad && b >= 0) ? ~zero : zero;
+    const int64_t ra = (!bad && a >= 0) ? a : 0, rb = (!bad && b >= 0) ? b : 0;
     const int64_t e0 = int64_t(blockIdx.y) * (64 * U) + lane_id();
+    V va[U], vb[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t e = e0 + int64_t(u) * 64;
-        if (e < elems) {
-            V va = zero, vb = zero;
-            if (!bad && a >= 0) va = x[a * elems + e];
-            if (!bad && b >= 0) vb = x[b * elems + e];
-            V r = (~va & ~vb & m00) | (~va & vb & m01) | (va & ~vb & m10) | (va & vb & m11);
-            if (bad) r = zero;
-            // written once, read by the next layer only: bypass the caches
-            __builtin_nontemporal_store(r, y + o * elems + e);
-        }
+        const int64_t off = e < elems ? e : 0;
+        va[u] = x[ra * elems + off];
+        vb[u] = x[rb * elems + off];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t e = e0 + int64_t(u) * 64;
+        const V p = va[u] & ka, q = vb[u] & kb;
+        V r = (~p & ~q & m00) | (~p & q & m01) | (p & ~q & m10) | (p & q & m11);
+        if (bad) r = zero;
+        // written once, read by the next layer only: bypass the caches
+        if (e < elems) __builtin_nontemporal_store(r, y + o * elems + e);
     }
 }
 
@@ -448,6 +457,7 @@ extern "C" int cl_eval_packed_indexed(const void* x, const int32_t* ia, const in
     clear_error();
     CL_ARG(in_dim >= 0 && out_dim >= 0 && row_bytes >= 0, "negative shape");
     if (out_dim == 0 || row_bytes == 0) return CL_OK;
+    CL_ARG(in_dim > 0, "in_dim is 0 but out_dim > 0");
     CL_ARG(x && ia && ib && gate && y, "null pointer argument");
     CL_ARG(ceil_div(out_dim, 4) < (int64_t(1) << 31), "too many rows");
     typedef unsigned int U4 __attribute__((ext_vector_type(4)));

@@ -44,6 +44,13 @@ __device__ __forceinline__ V vld(const void* p) {
     return *reinterpret_cast<const V*>(p);
 }
 
+// One 16-byte load of an int4 record (the HIP struct type may be split into narrower loads).
+__device__ __forceinline__ int4 ld_rec(const int4* p) {
+    typedef int I4 __attribute__((ext_vector_type(4)));
+    const I4 v = *reinterpret_cast<const I4*>(p);
+    return make_int4(v[0], v[1], v[2], v[3]);
+}
+
 // Lane accesses of the forward / backward tiled kernels are this many 16-byte vectors wide
 // (two for the backward: twice the bytes per gather for the same index records).
 #ifndef CL_FWD_VEC_MULT
@@ -345,7 +352,7 @@ __device__ __forceinline__ T fused_rcp(T v) {
 // the last reduction (DPP reads its neighbours), partial-chunk lanes only skip their row
 // accesses.  The tile's writer chunk (t mod nchunks) stores probs and the inverse-index
 // coefficients that the backward pass reads.
-template <typename T, int VEC, int LPN, int NPG>
+template <typename T, int VEC, int LPN, int NPG, bool COEF>
 __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T* __restrict__ w,
                                                int softmax, const uint8_t* __restrict__ gs,
                                                const int4* __restrict__ nab,
@@ -362,11 +369,18 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
     const int l = threadIdx.x % LPN;
     const int64_t idx = c * (LPN * VEC) + int64_t(l) * VEC;
     const bool col = idx < B;
+    const int64_t off = col ? idx : 0;
     const bool writer = uint32_t(c) == uint32_t(t) % uint32_t(tm.nchunks);
+    // Every load is unconditional (a clamped address, the value masked after it arrives): a
+    // load under a branch makes the compiler wait there for all loads in flight, which would
+    // serialize the logits, the records and the row gathers.
+    bool live[NPG];
     int4 rec[NPG];
 #pragma unroll
-    for (int j = 0; j < NPG; ++j)
-        rec[j] = obase + j < out_dim ? nab[obase + j] : make_int4(0, 0, 0, 0);
+    for (int j = 0; j < NPG; ++j) {
+        live[j] = obase + j < out_dim;
+        rec[j] = ld_rec(nab + (live[j] ? obase + j : obase));
+    }
     T p[NPG][SPL];
     int code[NPG][SPL];
 #pragma unroll
@@ -374,29 +388,33 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
 #pragma unroll
         for (int m = 0; m < SPL; ++m) {
             const int g = l + LPN * m;
-            const bool v = obase + j < out_dim && g < G;
-            p[j][m] = v ? w[(obase + j) * G + g] : -T(__builtin_inf());
-            code[j][m] = v ? gs[(obase + j) * G + g] : 0;
+            const int64_t wi = (live[j] ? obase + j : obase) * G + (g < G ? g : 0);
+            p[j][m] = w[wi];
+            code[j][m] = gs[wi];
         }
     V va[NPG], vb[NPG];
     bool ok[NPG];
     int2 ipos[NPG];
 #pragma unroll
     for (int j = 0; j < NPG; ++j) {
-        ok[j] = obase + j < out_dim && rec[j].z >= 0 && rec[j].w == rec[j].z + 1 &&
-                rec[j].w <= num_runs && uint32_t(rec[j].x) < uint64_t(in_dim) &&
-                uint32_t(rec[j].y) < uint64_t(in_dim);
-        va[j] = V(T(0));
-        vb[j] = V(T(0));
-        if (ok[j] && col) {
-            va[j] = vld<V>(x + int64_t(rec[j].x) * B + idx);
-            vb[j] = vld<V>(x + int64_t(rec[j].y) * B + idx);
+        ok[j] = live[j] && rec[j].z >= 0 && rec[j].w == rec[j].z + 1 && rec[j].w <= num_runs &&
+                uint32_t(rec[j].x) < uint64_t(in_dim) && uint32_t(rec[j].y) < uint64_t(in_dim);
+        va[j] = vld<V>(x + int64_t(ok[j] ? rec[j].x : 0) * B + off);
+        vb[j] = vld<V>(x + int64_t(ok[j] ? rec[j].y : 0) * B + off);
+        // entry positions of the run's two sides, for the tile's writer chunk
+        if constexpr (COEF) {
+            const int64_t rz = ok[j] ? rec[j].z : 0;
+            ipos[j] = make_int2(inv_pos[2 * rz], inv_pos[2 * rz + 1]);
         }
-        // entry positions of the run's two sides, loaded with the rows by the writer chunk
-        ipos[j] = make_int2(-1, -1);
-        if (writer && inv_coef && ok[j] && l == 0)
-            ipos[j] = make_int2(inv_pos[2 * int64_t(rec[j].z)], inv_pos[2 * int64_t(rec[j].z) + 1]);
     }
+#pragma unroll
+    for (int j = 0; j < NPG; ++j)
+#pragma unroll
+        for (int m = 0; m < SPL; ++m) {
+            const bool v = live[j] && l + LPN * m < G;
+            p[j][m] = v ? p[j][m] : -T(__builtin_inf());
+            code[j][m] = v ? code[j][m] : 0;
+        }
 #pragma unroll
     for (int j = 0; j < NPG; ++j) {
         const int64_t o = obase + j;
@@ -440,15 +458,17 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
                 for (int m = 0; m < SPL; ++m)
                     if (l + LPN * m < G) probs[o * G + l + LPN * m] = p[j][m];
             }
-            if (inv_coef && ok[j] && l == 0) {
-                const int64_t pa = ipos[j].x, pb = ipos[j].y;
-                if (uint64_t(pa) < uint64_t(2 * num_runs)) {
-                    inv_coef[2 * pa + 0] = k1;
-                    inv_coef[2 * pa + 1] = k3;
-                }
-                if (uint64_t(pb) < uint64_t(2 * num_runs)) {
-                    inv_coef[2 * pb + 0] = k2;
-                    inv_coef[2 * pb + 1] = k3;
+            if constexpr (COEF) {
+                if (ok[j] && l == 0) {
+                    const int64_t pa = ipos[j].x, pb = ipos[j].y;
+                    if (uint64_t(pa) < uint64_t(2 * num_runs)) {
+                        inv_coef[2 * pa + 0] = k1;
+                        inv_coef[2 * pa + 1] = k3;
+                    }
+                    if (uint64_t(pb) < uint64_t(2 * num_runs)) {
+                        inv_coef[2 * pb + 0] = k2;
+                        inv_coef[2 * pb + 1] = k3;
+                    }
                 }
             }
         }
@@ -460,7 +480,7 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
     }
 }
 
-template <typename T, int VEC, int LPN, int NPG>
+template <typename T, int VEC, int LPN, int NPG, bool COEF>
 __global__ __launch_bounds__(256) void k_fwd_fused(const T* __restrict__ x, const T* __restrict__ w,
                                                    int softmax, const uint8_t* __restrict__ gs,
                                                    const int4* __restrict__ nab,
@@ -471,7 +491,7 @@ __global__ __launch_bounds__(256) void k_fwd_fused(const T* __restrict__ x, cons
                                                    int G, TileMap tm) {
     int64_t c, t;
     if (map_tile(tm, blockIdx.x, c, t))
-        fwd_fused_tile<T, VEC, LPN, NPG>(x, w, softmax, gs, nab, inv_pos, probs, inv_coef, y,
+        fwd_fused_tile<T, VEC, LPN, NPG, COEF>(x, w, softmax, gs, nab, inv_pos, probs, inv_coef, y,
                                          in_dim, out_dim, num_runs, B, G, tm, c, t);
 }
 
@@ -626,8 +646,11 @@ __global__ __launch_bounds__(256) void k_wgrad_full(const T* __restrict__ x, con
 // k_wgrad_rows: the same with one wave per neuron over the whole batch (lane l holds samples
 // (u * 64 + l) * VEC .. +VEC-1, u < U), for batches of at most 64 * VEC * U samples and at
 // most 64 slots (lane g owns slot g).  grad_y of the neuron is loaded once for all its runs;
-// each run's moments are wave totals, so no partial sums leave the wave.
-template <typename T, int VEC, int U>
+// each run's moments are wave totals, so no partial sums leave the wave.  Loads are
+// unconditional (clamped, masked afterwards) so they are in flight together, and run o's
+// pair is fetched with run_ptr[o]: in a layer of single-run neurons run o is neuron o's
+// only run, and its row gathers need no second round trip.
+template <typename T, int VEC, int U, bool HAS_P>
 __global__ __launch_bounds__(256) void k_wgrad_rows(const T* __restrict__ x,
                                                     const T* __restrict__ gy,
                                                     const uint8_t* __restrict__ gs,
@@ -642,57 +665,68 @@ __global__ __launch_bounds__(256) void k_wgrad_rows(const T* __restrict__ x,
     const int lane = threadIdx.x & 63;
     const int64_t o = int64_t(blockIdx.x) * 4 + wave_id();
     if (o >= out_dim) return;  // uniform per wave
-    // the run range first, so that the grad_y row and the first run's rows load together
+    int64_t off[U];
+    bool in[U];
+    V vg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t idx = int64_t(u * 64 + lane) * VEC;
+        in[u] = idx < B;
+        off[u] = in[u] ? idx : 0;
+        vg[u] = vld<V>(gy + o * B + off[u]);
+    }
+    const int gl = lane < G ? lane : 0;
+    const int code = gs[o * G + gl];
+    const T p = HAS_P ? probs[o * G + gl] : T(0);
+    const int64_t oc = o < num_runs ? o : num_runs - 1;
+    const int2 ab_o = run_ab[oc];
+    const int gl_o = run_gl[oc];
     bool bad = false;
     int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
     if (r0 < 0 || r1 < r0 || r1 > num_runs) {
         bad = true;
         r1 = r0;
     }
-    V vg[U];
+    T s1 = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int64_t idx = int64_t(u * 64 + lane) * VEC;
-        vg[u] = idx < B ? vld<V>(gy + o * B + idx) : V(T(0));
+        vg[u] = in[u] ? vg[u] : V(T(0));
+        s1 += hsum<T, VEC>(vg[u]);
     }
-    // the slot's opcode and probability are loaded with the rows, not after the moments
-    const int code = lane < G ? gs[o * G + lane] : 0;
-    const T p = (probs && lane < G) ? probs[o * G + lane] : T(0);
-    T s1 = 0;
-    T gp = T(0), m0 = T(0);
+    const T m0 = wave_total(s1);
+    T gp = T(0);
     for (int64_t r = r0; r < r1; ++r) {
-        const int2 ab = run_ab[r];
-        const int gl = run_gl[r];
-        const int g0 = gl & 0xff, g1 = g0 + (gl >> 8);
-        if (uint32_t(ab.x) >= uint64_t(in_dim) || uint32_t(ab.y) >= uint64_t(in_dim)) {
+        int2 ab = ab_o;
+        int glr = gl_o;
+        if (r != oc) {
+            ab = run_ab[r];
+            glr = run_gl[r];
+        }
+        const int g0 = glr & 0xff, g1 = g0 + (glr >> 8);
+        const bool ok = uint32_t(ab.x) < uint64_t(in_dim) && uint32_t(ab.y) < uint64_t(in_dim);
+        if (!ok) {
             bad = true;
-            continue;
+            ab = make_int2(0, 0);
         }
         T s2 = 0, s3 = 0, s4 = 0;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t idx = int64_t(u * 64 + lane) * VEC;
-            if (idx < B) {
-                const V va = vld<V>(x + int64_t(ab.x) * B + idx);
-                const V vb = vld<V>(x + int64_t(ab.y) * B + idx);
-                const V ga = vg[u] * va;
-                s2 += hsum<T, VEC>(ga);
-                s3 += hsum<T, VEC>(vg[u] * vb);
-                s4 += hsum<T, VEC>(ga * vb);
-            }
-        }
-        if (r == r0) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) s1 += hsum<T, VEC>(vg[u]);
-            m0 = wave_total(s1);
+            const V va = vld<V>(x + int64_t(ab.x) * B + off[u]);
+            const V vb = vld<V>(x + int64_t(ab.y) * B + off[u]);
+            const V ga = vg[u] * va;
+            s2 += hsum<T, VEC>(ga);
+            s3 += hsum<T, VEC>(vg[u] * vb);
+            s4 += hsum<T, VEC>(ga * vb);
         }
         const T m1 = wave_total(s2), m2 = wave_total(s3), m3 = wave_total(s4);
-        if (lane >= g0 && lane < g1 && lane < G) {
-            const Coef4<T> cf = gate_coef<T>(code);
-            gp = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
-        }
+        const Coef4<T> cf = gate_coef<T>(code);
+        const T v = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
+        if (lane >= g0 && lane < g1 && lane < G) gp = v;
     }
-    if (probs) gp = p * (gp - wave_total(p * gp));
+    if constexpr (HAS_P) {
+        const T pl = lane < G ? p : T(0);
+        gp = pl * (gp - wave_total(pl * gp));
+    }
     if (lane < G) grad_w[o * G + lane] = bad ? nan_of<T>() : gp;
 }
 
@@ -1011,7 +1045,14 @@ __global__ __launch_bounds__(256) void k_bwd_part(
 // the neuron's logits gradient: no moments buffer and no finalize launch.  Workgroup w (four
 // rows) takes slot block (w % 8) * nblk + w / 8, so XCD w % 8 walks one contiguous stretch of
 // the processing order, whose rows share neighbours.
-template <typename T, int VEC, int U, bool WANT_GW>
+//
+// The kernel is bound by memory latency (a handful of dependent round trips per wave), so
+// every load is unconditional: lanes past the batch read sample 0 and are masked afterwards,
+// and an invalid record reads row 0 and poisons the result.  A load under a branch would make
+// the compiler wait for all loads in flight at the branch's end.  Entries are taken EPI at a
+// time (the records are wave-uniform), so their row gathers are in flight together; the
+// input gradient still adds the entries in entry order.
+template <typename T, int VEC, int U, bool WANT_GW, bool HAS_P>
 __global__ __launch_bounds__(256) void k_bwd_rows(
     const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
     const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef,
@@ -1020,95 +1061,110 @@ __global__ __launch_bounds__(256) void k_bwd_rows(
     int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, int G, int64_t nblk) {
     using V = typename VT<T, VEC>::type;
     using V2 = typename VT<T, 2>::type;
+    constexpr int EPI = U <= 4 ? 2 : 1;  // entries per step (register budget)
     const int lane = threadIdx.x & 63;
     const int64_t w = blockIdx.x;
     const int64_t slot = ((w % kXcds) * nblk + w / kXcds) * 4 + wave_id();
     if (slot >= in_dim) return;  // uniform per wave
     const int4 sr = slot_rec[slot];
     const int64_t row = sr.x, e0 = sr.y;
-    int64_t deg = int64_t(sr.z) - sr.y;
+    const int64_t deg = int64_t(sr.z) - sr.y;
     if (uint64_t(row) >= uint64_t(in_dim) || sr.y < 0 || deg < 0 || sr.z > 2 * num_runs)
         return;  // corrupt slot record: nothing is read or written for it
+    int64_t off[U];
+    bool in[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t idx = int64_t(u * 64 + lane) * VEC;
+        in[u] = idx < B;
+        off[u] = in[u] ? idx : 0;
+    }
     V xi[U], acc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int64_t idx = int64_t(u * 64 + lane) * VEC;
         acc[u] = V(T(0));
         xi[u] = V(T(0));
-        if (WANT_GW && idx < B) xi[u] = vld<V>(x + row * B + idx);
+        if constexpr (WANT_GW) xi[u] = vld<V>(x + row * B + off[u]);
     }
+    const int gl = lane < G ? lane : 0;  // slot of this lane in the finalize (clamped)
     bool bad = false;
-    int4 rec = make_int4(0, 0, 0, 0);
-    V2 kk = V2(T(0));
-    if (deg > 0) {
-        rec = inv_rec[e0];
-        kk = vld<V2>(inv_coef + 2 * e0);
-    }
-    for (int64_t k = 0; k < deg; ++k) {
-        const int4 cur = rec;
-        const V2 ck = kk;
-        if (k + 1 < deg) {
-            rec = inv_rec[e0 + k + 1];
-            kk = vld<V2>(inv_coef + 2 * (e0 + k + 1));
-        }
-        if (uint64_t(cur.x) >= uint64_t(out_dim) || uint64_t(cur.y) >= uint64_t(in_dim) ||
-            uint64_t(cur.z) >= uint64_t(num_runs)) {
-            bad = true;
-            continue;
-        }
-        V vo[U], vg[U];
+    for (int64_t k = 0; k < deg; k += EPI) {
+        int4 cur[EPI];
+        V2 ck[EPI];
+        bool use[EPI];
+        V vo[EPI][U], vg[EPI][U];
+        int rp0[EPI], rp1[EPI], code[EPI];
+        T p[EPI];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t idx = int64_t(u * 64 + lane) * VEC;
-            vo[u] = V(T(0));
-            vg[u] = V(T(0));
-            if (idx < B) {
-                vo[u] = vld<V>(x + int64_t(cur.y) * B + idx);
-                vg[u] = vld<V>(gy + int64_t(cur.x) * B + idx);
-            }
-        }
-        // the finalize's per-neuron data is loaded with the rows, not after the moments
-        const bool fin = WANT_GW && cur.w == 0;
-        int rp0 = 0, rp1 = 0, code = 0;
-        T p = T(0);
-        if (fin) {
-            rp0 = run_ptr[cur.x];
-            rp1 = run_ptr[cur.x + 1];
-            if (lane < G) {
-                code = gs[int64_t(cur.x) * G + lane];
-                if (probs) p = probs[int64_t(cur.x) * G + lane];
-            }
+        for (int q = 0; q < EPI; ++q) {
+            const int64_t e = e0 + (k + q < deg ? k + q : k);
+            cur[q] = inv_rec[e];
+            ck[q] = vld<V2>(inv_coef + 2 * e);
+            use[q] = k + q < deg;
+            const bool ok = uint64_t(cur[q].x) < uint64_t(out_dim) &&
+                            uint64_t(cur[q].y) < uint64_t(in_dim) &&
+                            uint64_t(cur[q].z) < uint64_t(num_runs);
+            if (use[q] && !ok) bad = true;
+            use[q] = use[q] && ok;
+            if (!ok) cur[q] = make_int4(0, 0, 0, 1);  // reads row 0, side b: no finalize
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc[u] += (ck[0] + ck[1] * vo[u]) * vg[u];
-        if (fin) {
-            T s1 = 0, s2 = 0, s3 = 0, s4 = 0;
+        for (int q = 0; q < EPI; ++q) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const V ga = vg[u] * xi[u];
-                s1 += hsum<T, VEC>(vg[u]);
-                s2 += hsum<T, VEC>(ga);
-                s3 += hsum<T, VEC>(vg[u] * vo[u]);
-                s4 += hsum<T, VEC>(ga * vo[u]);
+                vo[q][u] = vld<V>(x + int64_t(cur[q].y) * B + off[u]);
+                vg[q][u] = vld<V>(gy + int64_t(cur[q].x) * B + off[u]);
             }
-            const T m0 = wave_total(s1), m1 = wave_total(s2);
-            const T m2 = wave_total(s3), m3 = wave_total(s4);
-            const int64_t o = cur.x;
-            const bool single = rp0 == cur.z && rp1 == cur.z + 1;
-            T gp = T(0);
-            if (lane < G) {
-                const Coef4<T> cf = gate_coef<T>(code);
-                gp = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
+            // the finalize's per-neuron data is loaded with the rows, not after the moments
+            if constexpr (WANT_GW) {
+                rp0[q] = run_ptr[cur[q].x];
+                rp1[q] = run_ptr[cur[q].x + 1];
+                code[q] = gs[int64_t(cur[q].x) * G + gl];
+                p[q] = HAS_P ? probs[int64_t(cur[q].x) * G + gl] : T(0);
             }
-            if (probs) gp = p * (gp - wave_total(p * gp));
-            if (lane < G) grad_w[o * G + lane] = single ? gp : nan_of<T>();
+        }
+        // all gathers of the step are issued before any of them is waited for
+        __builtin_amdgcn_sched_barrier(0);
+        // Everything below is computed for every entry, used or not, and only the stores
+        // are conditional: a value used under a branch would let the compiler sink its load
+        // into that branch and wait for it there.  An unused entry adds -0, which leaves every
+        // sum bitwise unchanged.
+#pragma unroll
+        for (int q = 0; q < EPI; ++q) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const V t = (ck[q][0] + ck[q][1] * vo[q][u]) * vg[q][u];
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) acc[u][i] += use[q] ? t[i] : -T(0);
+            }
+            if constexpr (WANT_GW) {
+                T s1 = 0, s2 = 0, s3 = 0, s4 = 0;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const V g = in[u] ? vg[q][u] : V(T(0));
+                    const V ga = g * xi[u];
+                    s1 += hsum<T, VEC>(g);
+                    s2 += hsum<T, VEC>(ga);
+                    s3 += hsum<T, VEC>(g * vo[q][u]);
+                    s4 += hsum<T, VEC>(ga * vo[q][u]);
+                }
+                const T m0 = wave_total(s1), m1 = wave_total(s2);
+                const T m2 = wave_total(s3), m3 = wave_total(s4);
+                const Coef4<T> cf = gate_coef<T>(code[q]);
+                T gp = lane < G ? fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0))) : T(0);
+                if constexpr (HAS_P) {
+                    const T pl = lane < G ? p[q] : T(0);
+                    gp = pl * (gp - wave_total(pl * gp));
+                }
+                const bool single = rp0[q] == cur[q].z && rp1[q] == cur[q].z + 1;
+                if (use[q] && cur[q].w == 0 && lane < G)
+                    grad_w[int64_t(cur[q].x) * G + lane] = single ? gp : nan_of<T>();
+            }
         }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int64_t idx = int64_t(u * 64 + lane) * VEC;
-        if (idx < B) vst_stream<V>(gx + row * B + idx, bad ? V(nan_of<T>()) : acc[u]);
-    }
+    for (int u = 0; u < U; ++u)
+        if (in[u]) vst_stream<V>(gx + row * B + off[u], bad ? V(nan_of<T>()) : acc[u]);
 }
 
 // k_moments: the per-chunk moments of every run, per neuron (used when grad_x is not needed).
@@ -1393,6 +1449,7 @@ extern "C" int cl_dense_forward_fused(int dtype, const void* x, const void* w, i
     CL_ARG(x && w && gate_seq && nab && y, "null pointer argument");
     CL_ARG(!inv_coef || inv_pos, "inv_coef needs inv_pos");
     CL_ARG(aligned(nab, 16), "nab misaligned");
+    CL_ARG(num_runs >= 1, "num_runs must be >= 1 when out_dim > 0");
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
@@ -1406,9 +1463,15 @@ extern "C" int cl_dense_forward_fused(int dtype, const void* x, const void* w, i
         auto* ic = static_cast<T*>(inv_coef);
         auto* ys = static_cast<T*>(y);
         with_tiling<T, CL_FUSED_VEC_MULT>(tl, [&](auto vc, auto lc) {
-            k_fwd_fused<T, decltype(vc)::value, decltype(lc)::value, CL_FWD_NPG>
-                <<<grid, 256, 0, s>>>(xs, ws, softmax, gate_seq, nb, inv_pos, pr, ic, ys, in_dim,
-                                      out_dim, num_runs, batch, int(num_gates), tl.map);
+            constexpr int VEC = decltype(vc)::value, LPN = decltype(lc)::value;
+            if (ic)
+                k_fwd_fused<T, VEC, LPN, CL_FWD_NPG, true><<<grid, 256, 0, s>>>(
+                    xs, ws, softmax, gate_seq, nb, inv_pos, pr, ic, ys, in_dim, out_dim, num_runs,
+                    batch, int(num_gates), tl.map);
+            else
+                k_fwd_fused<T, VEC, LPN, CL_FWD_NPG, false><<<grid, 256, 0, s>>>(
+                    xs, ws, softmax, gate_seq, nb, inv_pos, pr, ic, ys, in_dim, out_dim, num_runs,
+                    batch, int(num_gates), tl.map);
         });
     });
     return check_launch("cl_dense_forward_fused");
@@ -1426,6 +1489,7 @@ extern "C" int cl_dense_weight_grad(int dtype, const void* x, const void* grad_y
     CL_ARG(gate_seq && run_ptr && run_ab && run_gl && grad_w, "null pointer argument");
     CL_ARG(batch == 0 || (x && grad_y), "null pointer argument");
     CL_ARG(aligned(run_ab, 8), "run_ab misaligned");
+    CL_ARG(num_runs >= 1, "num_runs must be >= 1 when out_dim > 0");
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
@@ -1438,12 +1502,18 @@ extern "C" int cl_dense_weight_grad(int dtype, const void* x, const void* grad_y
         auto* pr = static_cast<const T*>(probs);
         auto* ab = reinterpret_cast<const int2*>(run_ab);
         auto* gw = static_cast<T*>(grad_w);
-        if (v && num_gates <= 64 && batch <= 64 * W * 8) {
+        if (v && batch > 0 && num_gates <= 64 && batch <= 64 * W * 8) {
             const unsigned wgrid = unsigned(ceil_div(out_dim, int64_t(4)));
             auto go = [&](auto uc) {
-                k_wgrad_rows<T, W, decltype(uc)::value><<<wgrid, 256, 0, s>>>(
-                    xs, gys, gate_seq, pr, run_ptr, ab, run_gl, gw, std::max<int64_t>(in_dim, 1),
-                    out_dim, num_runs, batch, int(num_gates));
+                constexpr int U = decltype(uc)::value;
+                if (pr)
+                    k_wgrad_rows<T, W, U, true><<<wgrid, 256, 0, s>>>(
+                        xs, gys, gate_seq, pr, run_ptr, ab, run_gl, gw,
+                        std::max<int64_t>(in_dim, 1), out_dim, num_runs, batch, int(num_gates));
+                else
+                    k_wgrad_rows<T, W, U, false><<<wgrid, 256, 0, s>>>(
+                        xs, gys, gate_seq, pr, run_ptr, ab, run_gl, gw,
+                        std::max<int64_t>(in_dim, 1), out_dim, num_runs, batch, int(num_gates));
             };
             const int64_t per_u = 64 * W;
             if (batch <= per_u) go(std::integral_constant<int, 1>{});
@@ -1645,16 +1715,16 @@ extern "C" int cl_dense_backward_rows(int dtype, const void* x, const void* grad
             auto* pr = static_cast<const T*>(probs);
             auto* gw = static_cast<T*>(grad_w);
             auto* gxs = static_cast<T*>(grad_x);
-            if (grad_w)
-                k_bwd_rows<T, W, U, true><<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq,
-                                                             pr, run_ptr, gw, gxs, in_dim,
-                                                             out_dim, num_runs, batch,
-                                                             int(num_gates), nblk);
-            else
-                k_bwd_rows<T, W, U, false><<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq,
-                                                              pr, run_ptr, gw, gxs, in_dim,
-                                                              out_dim, num_runs, batch,
-                                                              int(num_gates), nblk);
+            auto launch = [&](auto gwc, auto pc) {
+                k_bwd_rows<T, W, U, decltype(gwc)::value, decltype(pc)::value>
+                    <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq, pr, run_ptr, gw, gxs,
+                                          in_dim, out_dim, num_runs, batch, int(num_gates), nblk);
+            };
+            using Y = std::true_type;
+            using N = std::false_type;
+            if (grad_w && probs) launch(Y{}, Y{});
+            else if (grad_w) launch(Y{}, N{});
+            else launch(N{}, N{});
         };
         const int64_t per_u = 64 * W;
         if (batch <= per_u) go(std::integral_constant<int, 1>{});

@@ -68,43 +68,59 @@ __global__ __launch_bounds__(256) void k_eval_packed(const W* __restrict__ x,
                                                      int64_t out_dim, int64_t words, int G) {
     const int64_t o = int64_t(blockIdx.x) * 4 + wave_id();
     if (o >= out_dim) return;
+    // Every load is unconditional (clamped slot, row 0 for a bad record, word 0 past the
+    // row's end, results masked afterwards): a load under a branch makes the compiler wait
+    // for it inside the branch, which serialized the U steps of a lane.
     const int s = wslot[o];
-    bool bad = s >= G;
-    int64_t ia = 0, ib = 0;
-    int g = 0;
-    if (!bad) {
-        ia = a[o * G + s];
-        ib = b[o * G + s];
-        g = gs[o * G + s];
-        bad = uint64_t(ia) >= uint64_t(in_dim) || uint64_t(ib) >= uint64_t(in_dim);
-    }
+    const int sc = s < G ? s : 0;
+    int64_t ia = a[o * G + sc];
+    int64_t ib = b[o * G + sc];
+    const int g = gs[o * G + sc];
+    const bool bad = s >= G || uint64_t(ia) >= uint64_t(in_dim) || uint64_t(ib) >= uint64_t(in_dim);
+    if (bad) ia = ib = 0;
     const W* xa = x + ia * words;
     const W* xb = x + ib * words;
     W* yr = y + o * words;
     const int64_t w0 = int64_t(blockIdx.y) * (64 * VEC * U) + int64_t(lane_id()) * VEC;
+    if constexpr (VEC == 2 && sizeof(W) == 8) {
+        typedef unsigned int U4v __attribute__((ext_vector_type(4)));
+        U4v va[U], vb[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int64_t idx = w0 + int64_t(u) * 64 * VEC;
-        if (idx < words) {
-            if constexpr (VEC == 2 && sizeof(W) == 8) {
-                uint4 r = {0u, 0u, 0u, 0u};
-                if (!bad) {
-                    const uint4 va = *reinterpret_cast<const uint4*>(xa + idx);
-                    const uint4 vb = *reinterpret_cast<const uint4*>(xb + idx);
-                    r.x = bitwise_op<uint32_t>(g, va.x, vb.x);
-                    r.y = bitwise_op<uint32_t>(g, va.y, vb.y);
-                    r.z = bitwise_op<uint32_t>(g, va.z, vb.z);
-                    r.w = bitwise_op<uint32_t>(g, va.w, vb.w);
-                }
-                typedef unsigned int U4v __attribute__((ext_vector_type(4)));
-                const U4v rv = {r.x, r.y, r.z, r.w};
-                __builtin_nontemporal_store(rv, reinterpret_cast<U4v*>(yr + idx));
-            } else {
-#pragma unroll
-                for (int v = 0; v < VEC; ++v)
-                    yr[idx + v] = bad ? W(0) : bitwise_op<W>(g, xa[idx + v], xb[idx + v]);
-            }
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = w0 + int64_t(u) * 64 * VEC;
+            const int64_t off = idx < words ? idx : 0;
+            va[u] = *reinterpret_cast<const U4v*>(xa + off);
+            vb[u] = *reinterpret_cast<const U4v*>(xb + off);
         }
+        const U4v keep = U4v(bad ? 0u : ~0u);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = w0 + int64_t(u) * 64 * VEC;
+            U4v r;
+            r.x = bitwise_op<uint32_t>(g, va[u].x, vb[u].x);
+            r.y = bitwise_op<uint32_t>(g, va[u].y, vb[u].y);
+            r.z = bitwise_op<uint32_t>(g, va[u].z, vb[u].z);
+            r.w = bitwise_op<uint32_t>(g, va[u].w, vb[u].w);
+            if (idx < words) __builtin_nontemporal_store(r & keep, reinterpret_cast<U4v*>(yr + idx));
+        }
+    } else {
+        W va[U][VEC], vb[U][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                const int64_t idx = w0 + int64_t(u) * 64 * VEC + v;
+                const int64_t off = idx < words ? idx : 0;
+                va[u][v] = xa[off];
+                vb[u][v] = xb[off];
+            }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                const int64_t idx = w0 + int64_t(u) * 64 * VEC + v;
+                if (idx < words) yr[idx] = bad ? W(0) : bitwise_op<W>(g, va[u][v], vb[u][v]);
+            }
     }
 }
 

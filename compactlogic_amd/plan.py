@@ -8,7 +8,8 @@ with per-slot random wiring most slots are runs of length one.
 
 The plan also carries the inverse index over inputs that the input-gradient kernel walks:
 row i lists the (run, operand side) uses of input i, encoded as 2 * run + side.  Entries
-within a row are in ascending (side, run) order, so the result is deterministic.  Each entry
+within a row are ordered by the distance, in the processing order below, between the row and
+the run's other input (ties: side, then run), so the result is deterministic.  Each entry
 also has a ready record (neuron, other input, run, side) so the kernel needs no second
 lookup, `inv_pos` maps a run side to its entry (where the per-step coefficients are written),
 and `row_order` is the processing order of the inputs: a depth-first preorder over the graph
@@ -211,13 +212,23 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
     rb = b.reshape(-1)[pos]
     run_ab = torch.stack((ra, rb), dim=1)
     run_gl = g0 | (length << 8)
-    # Inverse index: side-0 entries of all runs, then side-1 entries; a stable sort by
-    # input keeps that order inside every row.
+    # Inverse index: the entries of every input row, nearest partner first: ordered by the
+    # distance between the row and the run's other input in the processing order (then by
+    # side-0 entries of all runs before side-1 entries, in run order).  Two rows joined by a
+    # run then tend to reach that run's entry at the same step, while its grad_y row and
+    # their two input rows are in cache.
     inputs = torch.cat((ra, rb))
+    others = torch.cat((rb, ra))
     ids = torch.arange(r, dtype=torch.int64, device=dev) * 2
     entry = torch.cat((ids, ids + 1))
-    order = torch.sort(inputs, stable=True).indices
     inv_counts = torch.bincount(inputs, minlength=in_dim)
+    row_order = locality_order(ra, rb, inv_counts, in_dim)
+    rpos = torch.empty(in_dim, dtype=torch.int64, device=dev)
+    rpos[row_order] = torch.arange(in_dim, dtype=torch.int64, device=dev)
+    dist = (rpos[inputs] - rpos[others]).abs()
+    nent = max(2 * r, 1)
+    key = (inputs * (in_dim + 1) + dist) * nent + torch.arange(2 * r, dtype=torch.int64, device=dev)
+    order = torch.sort(key).indices
     inv_ptr = torch.zeros(in_dim + 1, dtype=torch.int64, device=dev)
     inv_ptr[1:] = torch.cumsum(inv_counts, 0)
     i32 = torch.int32
@@ -228,7 +239,6 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
     inv_rec = torch.stack((run_y[ent_run], ent_other, ent_run, ent_side), dim=1)
     inv_pos = torch.empty_like(inv_entry)
     inv_pos[inv_entry] = torch.arange(inv_entry.numel(), dtype=torch.int64, device=dev)
-    row_order = locality_order(ra, rb, inv_counts, in_dim)
     first = run_ptr[:-1].clamp(max=max(r - 1, 0))
     has = run_ptr[1:] > run_ptr[:-1]
     nab = torch.stack((torch.where(has, ra[first] if r else first, 0),
