@@ -223,6 +223,24 @@ def conv_backward(x, och, oh, ow, w, gs, gy, stride, pad):
     return gx, gw
 
 
+def conv_backward_w(x, och, oh, ow, gs, gy, stride):
+    """grad_w of conv_forward alone (no input gradient):
+    grad_w[c, g] = sum over n, oy, ox of gy[n, c, oy, ox] * op_{gs[c,g]}(tap_a, tap_b), following
+    compactlogic/cuda/convlogic_kernel.cu:295-430; the same sum as conv_backward's second
+    result, without its per-position input-gradient scatter."""
+    x, gy = _f64(x), _f64(gy)
+    gs = np.asarray(gs).astype(np.int64)
+    c_out, g_n = gs.shape
+    h_out, w_out = gy.shape[2], gy.shape[3]
+    gw = np.zeros((c_out, g_n))
+    for c in range(c_out):
+        for g in range(g_n):
+            va = _conv_taps(x, och, oh, ow, stride, h_out, w_out, 0, c, g)[0]
+            vb = _conv_taps(x, och, oh, ow, stride, h_out, w_out, 1, c, g)[0]
+            gw[c, g] = (gy[:, c] * relaxed(gs[c, g], va, vb)).sum()
+    return gw
+
+
 def conv_eval(x, och, oh, ow, w_slot, gs, stride, pad, ks):
     """Discrete conv: output channel c uses its argmax slot s = w_slot[c] only."""
     x = _f64(x)

@@ -218,6 +218,9 @@ def test_conv_oracle_against_loops(stride, pad, ks):
     ogx, ogw = O.conv_backward(x, och, oh, ow, w, gs, gy, stride, pad)
     np.testing.assert_allclose(ogx, gx.numpy(), atol=1e-12)
     np.testing.assert_allclose(ogw, gw.numpy(), atol=1e-12)
+    # the weight-gradient-only restatement against the same scalar-loop autograd
+    np.testing.assert_allclose(O.conv_backward_w(x, och, oh, ow, gs, gy, stride), gw.numpy(),
+                               atol=1e-12)
     slot = rng.integers(0, g_n, c_out)
     xb = (x > 0.5).astype(np.float64)
     onehot = np.zeros_like(w)
