@@ -83,6 +83,9 @@ SIGNATURES: dict[str, list] = {
     "cl_group_sum_cross_entropy_workspace_size": [_int, _i64, _i64, _i64, ctypes.POINTER(_i64)],
     "cl_group_sum_cross_entropy_backward": [_int, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _f64,
                                             _p, _i64, _i64, _p],
+    "cl_group_sum_cross_entropy_scratch_limit": [ctypes.POINTER(_i64)],
+    "cl_group_sum_cross_entropy_forward_noalloc": [_int, _p, _i64, _i64, _i64, _i64, _i64, _f64,
+                                                   _p, _i64, _p, _p, _p, _p, _p],
     "cl_pack_bits": [_p, _i64, _i64, _i32, _p, ctypes.POINTER(_i64), _p],
     "cl_dense_eval_packed": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "cl_group_bit_sum": [_p, _i64, _i64, _i64, _i64, _p, _p],

@@ -602,3 +602,85 @@ extern "C" int cl_group_sum_cross_entropy_backward(int dtype, const void* probs,
     });
     return check_launch("cl_group_sum_cross_entropy_backward");
 }
+
+// ------------------------------------------------------------------------------------------
+// Allocation-free variant of cl_group_sum_cross_entropy_forward: the same kernels, with the
+// workspace taken from a file-scope device array instead of the caller.  Each GPU holds its
+// own copy of `scratch` for the life of the process.  Its device address is looked up once
+// per device (hipGetSymbolAddress, with that device current) and kept in g_scratch_ptr; the
+// array's name is never used as an address on the host.  The kernels write every workspace
+// element they later read (slice partials, loss terms), so nothing needs clearing between
+// calls.  Calls that overlap on one GPU (several streams, several host threads) race on the
+// array.
+#include <mutex>
+
+namespace {
+constexpr int64_t kCeScratchBytes = int64_t(8) << 20;  // 8 MiB per GPU
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kCeScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `dev` (looked up on the first call for that device).
+int scratch_on(int dev, void** out) {
+    CL_ARG(dev >= 0 && dev < kMaxDevices, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess) {
+            set_error("hipGetDevice failed");
+            return CL_ERR_HIP;
+        }
+        if (cur != dev && hipSetDevice(dev) != hipSuccess) {
+            set_error("hipSetDevice(%d) failed", dev);
+            return CL_ERR_HIP;
+        }
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess || !p) {
+            set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                      hipGetErrorString(e));
+            return CL_ERR_HIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return CL_OK;
+}
+}  // namespace
+
+extern "C" int cl_group_sum_cross_entropy_scratch_limit(int64_t* bytes) {
+    clear_error();
+    CL_ARG(bytes, "null pointer argument");
+    *bytes = kCeScratchBytes;
+    return CL_OK;
+}
+
+extern "C" int cl_group_sum_cross_entropy_forward_noalloc(
+    int dtype, const void* x, int64_t batch, int64_t features, int64_t stride_batch,
+    int64_t stride_feature, int64_t k, double tau, const int64_t* labels, int64_t ignore_index,
+    void* out, void* probs, void* loss, void* count, void* stream) {
+    clear_error();
+    CL_ARG(batch >= 0 && features >= 0 && k >= 1, "bad shape");
+    int64_t need = 0;
+    if (int rc = cl_group_sum_cross_entropy_workspace_size(dtype, batch, features, k, &need))
+        return rc;
+    CL_ARG(need <= kCeScratchBytes,
+           "cl_group_sum_cross_entropy_forward_noalloc: this shape needs %lld bytes of scratch, "
+           "the limit is %lld (use cl_group_sum_cross_entropy_forward with a workspace)",
+           (long long)need, (long long)kCeScratchBytes);
+    int dev = -1;
+    hipError_t e = stream ? hipStreamGetDevice(as_stream(stream), &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("cannot determine the stream's device: %s", hipGetErrorString(e));
+        return CL_ERR_HIP;
+    }
+    void* ws = nullptr;
+    if (int rc = scratch_on(dev, &ws)) return rc;
+    return cl_group_sum_cross_entropy_forward(dtype, x, batch, features, stride_batch,
+                                              stride_feature, k, tau, labels, ignore_index, out,
+                                              probs, loss, count, ws, kCeScratchBytes, stream);
+}

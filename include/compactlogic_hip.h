@@ -367,6 +367,24 @@ int cl_group_sum_cross_entropy_forward(int dtype, const void* x, int64_t batch, 
 int cl_group_sum_cross_entropy_workspace_size(int dtype, int64_t batch, int64_t features,
                                               int64_t k, int64_t* bytes);
 
+/* Allocation-free form of cl_group_sum_cross_entropy_forward (no counterpart in the
+ * reference): for callers that cannot allocate device memory -- code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc.  Same arguments without the workspace, same
+ * kernels and bitwise the same results; the workspace is a device array of the library (one
+ * per GPU, held until the process ends) of cl_group_sum_cross_entropy_scratch_limit bytes
+ * (8 MiB).  A shape whose workspace (cl_group_sum_cross_entropy_workspace_size) exceeds it
+ * returns CL_ERR_INVALID_ARGUMENT.  It allocates nothing; calls that overlap on one GPU race
+ * on the array. */
+int cl_group_sum_cross_entropy_forward_noalloc(int dtype, const void* x, int64_t batch,
+                                               int64_t features, int64_t stride_batch,
+                                               int64_t stride_feature, int64_t k, double tau,
+                                               const int64_t* labels, int64_t ignore_index,
+                                               void* out, void* probs, void* loss, void* count,
+                                               void* stream);
+
+/* Bytes of the device array behind cl_group_sum_cross_entropy_forward_noalloc. */
+int cl_group_sum_cross_entropy_scratch_limit(int64_t* bytes);
+
 /* Its backward: grad_x[n, j] = grad_loss[0] * (probs[n, c] - [c == labels[n]]) /
  * (count[0] * tau) for c = group(j); 0 for an ignored sample, NaN for a label outside [0, k).
  * grad_loss and count are device scalars (graph-capturable: nothing is read on the host). */
