@@ -10,6 +10,8 @@ Also reported on the same JSON line:
   roofline      the dominant kernel's algorithmic bytes per launch / its average duration,
                 timed live with HIP events on the stream it runs on
   cpu_baseline  the pure-PyTorch CPU step (oracle/torch_cpu.py) on a bounded sample
+  train_full    cfg2 with the optimizer half of the reference's step: clip_grad_norm_(10) and
+                Adam fused (FusedAdam), the whole step in one HIP graph
   conv_train    cfg3: conv 9x32x32 -> 256x16x16 -> 512x7x7, flatten, 2 x 16000 dense,
                 GroupSum(10, tau 30), batch 256, fp32 fwd + CE + bwd, same measurements
   conv_tree_train  the logic-tree reading of cfg3: two complete ConvLogicLayer blocks (8 taps,
@@ -142,6 +144,53 @@ def bench_dense(args, torch):
 # its input and writes its output; the dense fused backward and the conv input gradient read
 # the input and grad_y and write grad_x; a weight gradient alone reads the input and grad_y.
 # Parameters, indices and partial sums are not counted.
+def bench_train_full(args, torch):
+    """cfg2 with the optimizer half of the reference's training step
+    (experiments/experiment_script.py:280-293): forward, the fused GroupSum cross-entropy,
+    backward, clip_grad_norm_(10.0) and Adam(lr 0.01) fused (FusedAdam), the whole step
+    captured in one HIP graph."""
+    import compactlogic_amd as cl
+    from compactlogic_amd import configs
+    cfg = configs.CONFIGS["cfg2"]
+    dev = torch.device("cuda:0")
+    model = configs.dense_network(cfg, device=dev)
+    x, labels = configs.dense_inputs(cfg, device=dev)
+    opt = cl.FusedAdam(model.parameters(), lr=0.01, max_norm=10.0)
+    body, head = model[:-1], model[-1]
+
+    def step():
+        loss = head.cross_entropy(body(x), labels)
+        loss.backward()
+        opt.step()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            model.zero_grad(set_to_none=True)
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    model.zero_grad(set_to_none=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    nparams = sum(p.numel() for p in model.parameters())
+    del model, opt, graph
+    torch.cuda.empty_cache()
+    return {"workload": "cfg2 full training step: fwd + fused CE + bwd + clip_grad_norm_(10) + "
+                        "Adam(lr 0.01), one HIP graph",
+            "value": round(x.shape[0] / dt, 1), "unit": "samples/s",
+            "ms_per_step": round(dt * 1e3, 4), "steps": args.steps, "parameters": nparams}
+
+
 def train_kernel_bytes(model, batch: int) -> dict:
     import compactlogic_amd as cl
     out = {}
@@ -571,6 +620,9 @@ def main():
                                          "after the timed region"),
         "kernels": kernels_json(kernels, args.kernel_steps),
     }
+    log("dense cfg2 full step (with clip + Adam)")
+    result["train_full"] = bench_train_full(args, torch)
+    log(f"dense cfg2 full step: {result['train_full']['ms_per_step']:.3f} ms/step")
     if not args.no_cpu_baseline:
         log("cpu baseline (cfg2)")
         result["cpu_baseline"] = cpu_baseline_train(torch, "cfg2")

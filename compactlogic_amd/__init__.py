@@ -12,6 +12,7 @@ from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction,
                      ConvLayerWindowFunction, GroupSum, GroupSumCrossEntropyFunction,
                      GroupSumFunction, LogicLayer,
                      LogicLayerCudaFunction, LogicLayerRunsFunction, PackBitsTensor)
+from .optim import FusedAdam
 from .packed_net import PackedNetwork
 from .plan import RunPlan, build_run_plan
 from .schedules import (EntropyRowResampler, FixedSequentialEntropyFreezer,
@@ -25,5 +26,5 @@ __all__ = [
     "ConvLayer", "ConvLayerCudaFunction", "ConvLayerSoftmaxFunction", "ConvLayerWindowFunction",
     "convlogic_hip", "SequentialEntropyFreezer", "FixedSequentialEntropyFreezer",
     "EntropyRowResampler", "PackedNetwork", "ConvLogicLayer", "TreeLogicLayer", "PoolLogicLayer",
-    "ConvLogicFunction", "FullConvLogicFunction", "TreeLogicFunction",
+    "ConvLogicFunction", "FullConvLogicFunction", "TreeLogicFunction", "FusedAdam",
 ]

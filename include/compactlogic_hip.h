@@ -395,6 +395,26 @@ int cl_group_sum_cross_entropy_backward(int dtype, const void* probs, const int6
                                         int64_t stride_feature, void* stream);
 
 /* -------------------------------------------------------------------------------------------
+ * Optimizer step of a training iteration (experiments/experiment_script.py:280-293):
+ * torch.nn.utils.clip_grad_norm_(params, max_norm) followed by torch.optim.Adam.step() (the
+ * reference's optimizer, :362), over num_tensors parameter tensors in two launches.  params,
+ * grads, exp_avg, exp_avg_sq: host arrays of device pointers (dtype elements, contiguous);
+ * numels: host array of element counts.  The gradients are scaled in place by
+ * min(1, max_norm / (norm + 1e-6)) (no clipping when max_norm <= 0), then
+ *   m = beta1 m + (1 - beta1) g, v = beta2 v + (1 - beta2) g^2,
+ *   p -= lr / (1 - beta1^t) * m / (sqrt(v) / sqrt(1 - beta2^t) + eps),
+ * with t = step[0] + 1 written back to step (a device scalar of dtype, so a captured graph
+ * replays correct bias corrections).  workspace: cl_adam_clip_workspace elements of dtype.
+ * Sums have a fixed order: bitwise reproducible. */
+int cl_adam_clip_max_tensors(int64_t* n);
+int cl_adam_clip_workspace(int64_t num_tensors, const int64_t* numels, int64_t* elements);
+int cl_adam_clip_step(int dtype, int64_t num_tensors, void* const* params, void* const* grads,
+                      void* const* exp_avg, void* const* exp_avg_sq, const int64_t* numels,
+                      void* step, double lr, double beta1, double beta2, double eps,
+                      double max_norm, void* workspace, int64_t workspace_elements,
+                      void* stream);
+
+/* -------------------------------------------------------------------------------------------
  * Layout change: dst [cols, rows] = transpose of src [rows, cols] (both contiguous, not
  * overlapping).  Replaces the torch transpose copy of compactlogic/compactlogic.py:100-101
  * between a module's [batch, features] input and the kernels' [features, batch] rows.
