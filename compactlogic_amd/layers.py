@@ -468,11 +468,15 @@ class LogicLayer(torch.nn.Module):
         self._plan = None
 
     def run_plan(self) -> RunPlan:
-        """The connection-run plan for the current `indices`, rebuilt after any change."""
-        key = (self.indices.data_ptr(), self.indices._version, self.indices.device)
-        if self._plan is None or self._plan_key != key:
-            self._plan = build_run_plan(self.indices, self.in_dim)
-            self._plan_key = key
+        """The connection-run plan for the current `indices`, rebuilt after any change: the
+        cache holds a weak reference to the indices tensor and its version, so an in-place
+        rewiring or a new tensor (even one at a recycled address) rebuilds it."""
+        ind = self.indices
+        hit = self._plan_key
+        if (self._plan is None or hit is None or hit[0]() is not ind
+                or hit[1] != (ind._version, ind.device)):
+            self._plan = build_run_plan(ind, self.in_dim)
+            self._plan_key = (weakref.ref(ind), (ind._version, ind.device))
         return self._plan
 
     # -- rewiring, entropy, freezing ----------------------------------------------------------------------------------

@@ -28,10 +28,13 @@ internal runs (the rest stay external).
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import numpy as np
 import torch
+
+from . import _capi
 
 
 PART_ROWS = 16    # inputs per tile of the partitioned input-gradient kernel
@@ -65,81 +68,27 @@ class RunPlan:
         return int(self.run_gl.numel())
 
 
-def dfs_forest(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor, in_dim: int):
-    """Depth-first spanning forest of the graph whose edges are the runs (a, b): returns
-    (roots, parent, children) as Python lists, parent[v] = -1 for a root and -2 for an input of
-    degree 0.  Each search starts from the highest-degree unvisited input (lowest index on
-    ties) and follows the neighbours in entry order; children are listed in discovery order."""
-    a = ra.cpu().numpy().astype(np.int64)
-    b = rb.cpu().numpy().astype(np.int64)
-    deg = degree.cpu().numpy().astype(np.int64)
-    src = np.concatenate((a, b))
-    dst = np.concatenate((b, a))
-    nbr = dst[np.argsort(src, kind="stable")].tolist()
-    ptr = np.zeros(in_dim + 1, dtype=np.int64)
-    np.cumsum(np.bincount(src, minlength=in_dim), out=ptr[1:])
-    ptr = ptr.tolist()
-    parent = [-2] * in_dim
-    children = [[] for _ in range(in_dim)]
-    roots = []
-    for s in np.argsort(-deg, kind="stable").tolist():
-        if parent[s] != -2 or deg[s] == 0:
-            continue
-        parent[s] = -1
-        roots.append(s)
-        stack = [[s, ptr[s]]]
-        while stack:
-            top = stack[-1]
-            u, i = top
-            if i < ptr[u + 1]:
-                top[1] = i + 1
-                v = nbr[i]
-                if parent[v] == -2:
-                    parent[v] = u
-                    children[u].append(v)
-                    stack.append([v, ptr[v]])
-            else:
-                stack.pop()
-    return roots, parent, children
-
-
-def locality_order(ra: torch.Tensor, rb: torch.Tensor, degree: torch.Tensor,
-                   in_dim: int) -> torch.Tensor:
-    """Processing order of the inputs for the input-gradient pass: preorder of the depth-first
-    spanning forest of the run graph (dfs_forest), in which the children of every input are
-    visited in increasing order of their subtree sizes (equal sizes in discovery order);
-    inputs of degree 0 last.
+def locality_order(ra: torch.Tensor, rb: torch.Tensor, in_dim: int) -> torch.Tensor:
+    """Processing order of the inputs for the input-gradient pass (int64 [in_dim], on ra's
+    device): the preorder of a depth-first spanning forest of the graph whose edges are the
+    runs (a, b), every input's children visited in increasing order of their subtree sizes
+    (equal sizes in discovery order), inputs of degree 0 last.  Searches start from the
+    highest-degree unvisited input and scan an input's runs in run order (operand a, then
+    operand b).
 
     A subtree occupies consecutive positions, so a run between a parent and its child spans
     only the subtrees of the child's smaller siblings; visiting the small subtrees first keeps
     that span short for every child, and with it the time between the two reads of the
-    run's grad_y row and of the shared input rows.  Deterministic."""
+    run's grad_y row and of the shared input rows.  Deterministic; built on the host by the
+    library (cl_plan_locality_order), in linear time."""
     dev = ra.device
-    roots, parent, children = dfs_forest(ra, rb, degree, in_dim)
-    size = [1] * in_dim
-    # a parent is discovered before its children, so reversed discovery (preorder) order
-    # visits every child before its parent
-    pre = []
-    for r in roots:
-        stack = [r]
-        while stack:
-            u = stack.pop()
-            pre.append(u)
-            stack.extend(children[u])
-    for u in reversed(pre):
-        if parent[u] >= 0:
-            size[parent[u]] += size[u]
-    out = []
-    for r in roots:
-        stack = [r]
-        while stack:
-            u = stack.pop()
-            out.append(u)
-            ch = sorted(children[u], key=lambda v: size[v])   # stable: discovery order on ties
-            stack.extend(reversed(ch))
-    deg = degree.cpu().numpy()
-    out.extend(np.nonzero(deg == 0)[0].tolist())
-    return torch.as_tensor(np.asarray(out, dtype=np.int64), dtype=torch.int64, device=dev)
+    a = np.ascontiguousarray(ra.detach().cpu().numpy().astype(np.int32))
+    b = np.ascontiguousarray(rb.detach().cpu().numpy().astype(np.int32))
+    out = np.empty(in_dim, dtype=np.int32)
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    _capi.call("cl_plan_locality_order", a.ctypes.data_as(i32p), b.ctypes.data_as(i32p),
+               a.size, in_dim, out.ctypes.data_as(i32p))
+    return torch.as_tensor(out.astype(np.int64), device=dev)
 
 
 def partition_tiles(row_order: torch.Tensor, ra: torch.Tensor, rb: torch.Tensor,
@@ -222,7 +171,7 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
     ids = torch.arange(r, dtype=torch.int64, device=dev) * 2
     entry = torch.cat((ids, ids + 1))
     inv_counts = torch.bincount(inputs, minlength=in_dim)
-    row_order = locality_order(ra, rb, inv_counts, in_dim)
+    row_order = locality_order(ra, rb, in_dim)
     rpos = torch.empty(in_dim, dtype=torch.int64, device=dev)
     rpos[row_order] = torch.arange(in_dim, dtype=torch.int64, device=dev)
     dist = (rpos[inputs] - rpos[others]).abs()

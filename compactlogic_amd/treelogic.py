@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 
 import torch
 from torch import nn
@@ -438,11 +439,14 @@ class ConvLogicLayer(nn.Module):
         return unpack_selection(selection)
 
     def _channel_uses(self):
+        """The channel-use index of the current selection, cached with a weak reference to
+        the selection tensor and its version (a new tensor at a recycled address rebuilds)."""
         sel = self.selection
-        key = (sel.data_ptr(), sel._version, sel.device)
-        if self._uses is None or self._uses[0] != key:
-            self._uses = (key, channel_uses(sel.to(torch.int32), self.in_channels))
-        return self._uses[1]
+        hit = self._uses
+        if hit is None or hit[0]() is not sel or hit[1] != (sel._version, sel.device):
+            self._uses = (weakref.ref(sel), (sel._version, sel.device),
+                          channel_uses(sel.to(torch.int32), self.in_channels))
+        return self._uses[2]
 
     def _w_prob(self, dtype):
         if self.training:

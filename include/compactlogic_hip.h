@@ -110,6 +110,16 @@ int cl_dense_eval(int dtype, const void* x, const int64_t* a, const int64_t* b,
  * batch % (16 / sizeof(T)) == 0 the row buffers must be 16-byte aligned.
  * ----------------------------------------------------------------------------------------- */
 
+/* Host function (no device work; all pointers are host pointers).  Processing order of the
+ * input rows for the row backward: the preorder of a depth-first spanning forest of the graph
+ * with one vertex per input row and one edge (ra[r], rb[r]) per run, every vertex's children
+ * visited in increasing subtree size (ties: discovery order), rows without runs last in index
+ * order.  Searches start from the highest-degree unvisited row (ties: lowest index) and scan a
+ * row's runs in run order, operand-a uses before operand-b uses.  order: int32 [in_dim].
+ * Linear time; replaces the Python construction of the plan (no reference counterpart). */
+int cl_plan_locality_order(const int32_t* ra, const int32_t* rb, int64_t num_runs,
+                           int64_t in_dim, int32_t* order);
+
 /* Probabilities (softmax of w over the slots when `softmax` is non-zero, else w itself;
  * written to `probs` when not NULL) and the run coefficients K (run_coef, 16-byte aligned).
  * With inv_coef (T [2 * num_runs, 2], may be NULL) the coefficients of every inverse-index

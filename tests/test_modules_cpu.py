@@ -318,7 +318,8 @@ def test_run_plan_processing_order():
     """row_order is the preorder of a depth-first spanning forest of the run graph with every
     input's children visited smallest subtree first, inputs of degree 0 last; slot_rec
     follows it."""
-    from compactlogic_amd.plan import build_run_plan, dfs_forest
+    from compactlogic_amd.plan import build_run_plan
+    from plan_reference import dfs_forest
     g = torch.Generator().manual_seed(11)
     in_dim, out_dim = 3000, 1600
     pair = torch.randint(0, in_dim, (2, out_dim, 1), generator=g).expand(2, out_dim, 16)
@@ -488,3 +489,36 @@ def test_conv_packed_order_groups_channels_by_input():
     assert torch.equal(order.view(20, hw) - (chans * hw).view(-1, 1), torch.arange(hw).expand(20, hw))
     src = layer.offsets_ch[0, chans, layer.w.long()[chans]]
     assert bool((src[1:] >= src[:-1]).all())
+
+
+@pytest.mark.parametrize("case", ["shared", "per_slot", "self_pairs", "sparse"])
+def test_native_processing_order_equals_python_reference(case):
+    """The library's host-side order (cl_plan_locality_order) is the same traversal as the
+    Python statement of it in tests/plan_reference.py: identical orders."""
+    import plan_reference as ref
+    from compactlogic_amd.plan import locality_order
+    g = torch.Generator().manual_seed(21)
+    in_dim, out_dim = 2000, 1500
+    if case == "shared":
+        ind = torch.randint(0, in_dim, (2, out_dim, 1), generator=g).expand(2, out_dim, 4)
+    elif case == "per_slot":
+        ind = torch.randint(0, in_dim, (2, out_dim, 4), generator=g)
+    elif case == "self_pairs":
+        a = torch.randint(0, in_dim, (out_dim, 1), generator=g)
+        ind = torch.stack((a, torch.where(torch.rand((out_dim, 1), generator=g) < 0.3, a,
+                                          torch.randint(0, in_dim, (out_dim, 1), generator=g))))
+    else:  # few runs: many rows of degree 0, many small components
+        ind = torch.randint(0, in_dim, (2, 300, 1), generator=g)
+    ind = ind.contiguous()
+    plan = cl.build_run_plan(ind, in_dim)
+    ra, rb = plan.run_ab[:, 0].long(), plan.run_ab[:, 1].long()
+    deg = torch.bincount(torch.cat((ra, rb)), minlength=in_dim)
+    want = ref.locality_order(ra, rb, deg, in_dim)
+    assert torch.equal(locality_order(ra, rb, in_dim), want)
+    assert torch.equal(plan.row_order.long(), want)
+
+
+def test_native_processing_order_rejects_bad_runs():
+    from compactlogic_amd.plan import locality_order
+    with pytest.raises(RuntimeError, match="outside"):
+        locality_order(torch.tensor([0, 5]), torch.tensor([1, 2]), 4)
