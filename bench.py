@@ -262,7 +262,7 @@ def packed_kernel_bytes(model, words: int, k: int) -> dict:
             out[f"cl_eval_packed_indexed[{fin}->{m.out_dim}]"] = (fin + m.out_dim) * words * 8
             rows = m.out_dim
         elif isinstance(m, cl.LogicLayer):
-            out[f"cl_dense_eval_packed[{m.in_dim}->{m.out_dim}]"] = (m.in_dim + m.out_dim) * words * 8
+            out[f"cl_eval_packed_indexed[{m.in_dim}->{m.out_dim}]"] = (m.in_dim + m.out_dim) * words * 8
             rows = m.out_dim
     out[f"cl_group_bit_sum[{rows}]"] = rows * words * 8 + words * 64 * k * 4
     return out

@@ -246,8 +246,14 @@ __global__ __launch_bounds__(256) void k_eval_packed_idx(const V* __restrict__ x
                                                          const uint8_t* __restrict__ gate,
                                                          const int32_t* __restrict__ order,
                                                          V* __restrict__ y, int64_t in_dim,
-                                                         int64_t out_dim, int64_t elems) {
-    const int64_t i = int64_t(blockIdx.x) * 4 + wave_id();
+                                                         int64_t out_dim, int64_t elems,
+                                                         int64_t nblk) {
+    // Workgroup (bx, chunk) takes row block (bx % 8) * nblk + bx / 8 of the processing order:
+    // with gridDim.x a multiple of 8 it runs on XCD bx % 8, so each XCD walks one contiguous
+    // stretch of the order, and rows that read the same input row (adjacent in the order)
+    // find its words in that XCD's L2.
+    const int64_t bx = blockIdx.x, chunk = blockIdx.y;
+    const int64_t i = ((bx % 8) * nblk + bx / 8) * 4 + wave_id();
     if (i >= out_dim) return;
     const int64_t o = order ? int64_t(order[i]) : i;
     if (uint64_t(o) >= uint64_t(out_dim)) return;  // corrupt order entry: nothing is written
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(256) void k_eval_packed_idx(const V* __restrict__ x
     const V ka = (!bad && a >= 0) ? ~zero : zero;
     const V kb = (!bad && b >= 0) ? ~zero : zero;
     const int64_t ra = (!bad && a >= 0) ? a : 0, rb = (!bad && b >= 0) ? b : 0;
-    const int64_t e0 = int64_t(blockIdx.y) * (64 * U) + lane_id();
+    const int64_t e0 = chunk * (64 * U) + lane_id();
     V va[U], vb[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -290,10 +296,13 @@ int launch_eval_packed_idx(const void* x, const int32_t* ia, const int32_t* ib,
                            int64_t out_dim, int64_t row_bytes, hipStream_t s) {
     constexpr int U = 4;
     const int64_t elems = row_bytes / int64_t(sizeof(V));
-    CL_ARG(ceil_div(elems, 64 * U) < 65536, "packed rows too long for one launch");
-    const dim3 grid(unsigned(ceil_div(out_dim, 4)), unsigned(ceil_div(elems, 64 * U)), 1);
+    const int64_t nblk = ceil_div(ceil_div(out_dim, 4), 8);
+    const int64_t nchunks = ceil_div(elems, 64 * U);
+    CL_ARG(8 * nblk < (int64_t(1) << 31) && nchunks < 65536, "packed layer too large for one launch");
+    const dim3 grid(unsigned(8 * nblk), unsigned(nchunks), 1);
     k_eval_packed_idx<V, U><<<grid, 256, 0, s>>>(static_cast<const V*>(x), ia, ib, gate, order,
-                                                 static_cast<V*>(y), in_dim, out_dim, elems);
+                                                 static_cast<V*>(y), in_dim, out_dim, elems,
+                                                 nblk);
     return CL_OK;
 }
 

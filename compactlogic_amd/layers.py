@@ -19,7 +19,7 @@ from . import _capi
 from . import convlogic_hip as _cl
 from . import difflogic_hip as _dl
 from . import timing
-from .plan import PART_SLOTS, RunPlan, build_run_plan
+from .plan import PART_SLOTS, RunPlan, build_run_plan, locality_order
 
 
 ########################################################################################################################
@@ -323,6 +323,11 @@ class GroupSumFunction(torch.autograd.Function):
 # Modules
 
 
+# Average reads per input row up to which a frozen layer's packed evaluation follows the
+# chain order (above it, many consecutive neurons would read the same input row at once).
+_PACKED_CHAIN_MAX_DEGREE = 8
+
+
 class LogicLayer(torch.nn.Module):
     """Differentiable logic-gate layer (compactlogic/compactlogic.py:10-130).
 
@@ -392,15 +397,68 @@ class LogicLayer(torch.nn.Module):
         assert self.is_frozen or not self.training
         w = getattr(self, "w", None)
         if w is None:
-            w = self.weights.argmax(-1).to(dtype=torch.uint8, device=self.weights.device)
+            w = self._argmax_slots()
         a, b = self.indices[0], self.indices[1]
         if isinstance(x, PackBitsTensor):
             assert x.t.shape[0] == self.in_dim, (x.t.shape, self.in_dim)
-            x.t = timing.timed(f"cl_dense_eval_packed[{self.in_dim}->{self.out_dim}]",
-                               lambda: _dl.eval_packed(x.t, a, b, w, self.gate_sequence))
+            ia, ib, gate, order = self.packed_tables(w)
+            x.t = timing.timed(f"cl_eval_packed_indexed[{self.in_dim}->{self.out_dim}]",
+                               lambda: _cl.eval_packed_indexed(x.t, ia, ib, gate, order))
             return x
         assert x.shape[-1] == self.in_dim, (x.shape, self.in_dim)
         return _dl.eval(to_rows(x), a, b, w, self.gate_sequence).transpose(0, 1)
+
+    @torch.no_grad()
+    def _argmax_slots(self) -> torch.Tensor:
+        """Winner slots of an unfrozen layer (argmax of the logits, uint8), kept while the
+        logits tensor is alive and unmodified, so the packed tables derived from them stay
+        cached across eval calls."""
+        src = self.weights
+        hit = getattr(self, "_argmax_cache", None)
+        if hit is not None and hit[0]() is src and hit[1] == src._version:
+            return hit[2]
+        w = src.argmax(-1).to(dtype=torch.uint8, device=src.device)
+        self._argmax_cache = (weakref.ref(src), src._version, w)
+        return w
+
+    @torch.no_grad()
+    def packed_tables(self, w: torch.Tensor):
+        """(ia, ib, gate, order) of the packed layer for the winner slots ``w``: the two input
+        rows and the opcode of every neuron's winner slot (int32, int32, uint8; a winner slot
+        outside [0, num_gates) or an input outside [0, in_dim) gets row in_dim, which the kernel
+        evaluates as zero words, as the slot-indirect evaluation does), and the order in which
+        the kernel evaluates the neurons: sorted by the later of their two inputs in the
+        depth-first order of the input rows (plan.locality_order over the edges (ia, ib)), so
+        that neurons adjacent in the order mostly share an input row; None (neuron order)
+        when the input rows are read more than _PACKED_CHAIN_MAX_DEGREE times on average.  Cached until the
+        winners, the wiring or the opcodes change (weak references and versions)."""
+        srcs = (w, self.indices, self.gate_sequence)
+        key = tuple((t._version, t.device) for t in srcs)
+        hit = getattr(self, "_packed_key", None)
+        if hit is not None and hit[1] == key and all(r() is t for r, t in zip(hit[0], srcs)):
+            return self._packed_tables
+        rows = torch.arange(self.out_dim, device=w.device)
+        s = w.to(torch.long)
+        ok_s = s < self.num_gates
+        sc = torch.where(ok_s, s, torch.zeros_like(s))
+        a = self.indices[0, rows, sc]
+        b = self.indices[1, rows, sc]
+        ok = ok_s & (a >= 0) & (a < self.in_dim) & (b >= 0) & (b < self.in_dim)
+        bad = torch.full_like(a, self.in_dim)
+        ia = torch.where(ok, a, bad).to(torch.int32).contiguous()
+        ib = torch.where(ok, b, bad).to(torch.int32).contiguous()
+        gate = self.gate_sequence[rows, sc].contiguous()
+        order = None
+        if 2 * self.out_dim <= _PACKED_CHAIN_MAX_DEGREE * self.in_dim:
+            ga = torch.where(ok, a, torch.zeros_like(a))
+            gb = torch.where(ok, b, torch.zeros_like(b))
+            pos = torch.empty(self.in_dim, dtype=torch.long, device=w.device)
+            pos[locality_order(ga, gb, self.in_dim)] = torch.arange(self.in_dim, device=w.device)
+            later = torch.maximum(pos[ga], pos[gb])
+            order = torch.sort(later * self.out_dim + rows).indices.to(torch.int32).contiguous()
+        self._packed_tables = (ia, ib, gate, order)
+        self._packed_key = (tuple(weakref.ref(t) for t in srcs), key)
+        return self._packed_tables
 
     def extra_repr(self):
         return '{}, {}, {}'.format(self.in_dim, self.out_dim, 'train' if self.training else 'eval')
@@ -812,19 +870,6 @@ class ConvLayer(LogicLayer):
             return x
         return _cl.eval(x.contiguous(), self.offsets_ch, self.offsets_h, self.offsets_w, w,
                         self.gate_sequence, self.stride, self.padding, self.ks)
-
-    @torch.no_grad()
-    def _argmax_slots(self) -> torch.Tensor:
-        """Winner slots of an unfrozen layer (argmax of the logits, uint8), kept while the
-        logits tensor is alive and unmodified, so the packed tables derived from them stay
-        cached across eval calls."""
-        src = self.weights
-        hit = getattr(self, "_argmax_cache", None)
-        if hit is not None and hit[0]() is src and hit[1] == src._version:
-            return hit[2]
-        w = src.argmax(-1).to(dtype=torch.uint8, device=src.device)
-        self._argmax_cache = (weakref.ref(src), src._version, w)
-        return w
 
     @torch.no_grad()
     def packed_tables(self, w: torch.Tensor):

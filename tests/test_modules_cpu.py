@@ -522,3 +522,33 @@ def test_native_processing_order_rejects_bad_runs():
     from compactlogic_amd.plan import locality_order
     with pytest.raises(RuntimeError, match="outside"):
         locality_order(torch.tensor([0, 5]), torch.tensor([1, 2]), 4)
+
+
+def test_dense_packed_tables_and_order():
+    """A frozen LogicLayer's packed tables: the winner slot's inputs and opcode per neuron, row
+    in_dim (zero words) for a winner outside the slots, and an evaluation order that is a
+    permutation in which most neighbours share an input row."""
+    torch.manual_seed(8)
+    layer = cl.LogicLayer(300, 400, connections="original")
+    layer.freeze()
+    w = layer.w.clone()
+    w[5] = 200                                    # a slot that does not exist
+    ia, ib, gate, order = layer.packed_tables(w)
+    assert order is not None
+    o = torch.arange(400)
+    s = w.long().clamp(max=15)
+    ok = w.long() < 16
+    assert torch.equal(ia[ok].long(), layer.indices[0, o, s][ok])
+    assert torch.equal(ib[ok].long(), layer.indices[1, o, s][ok])
+    assert torch.equal(gate[ok], layer.gate_sequence[o, s][ok])
+    assert int(ia[5]) == 300 and int(ib[5]) == 300
+    assert sorted(order.tolist()) == list(range(400))
+    a, b = ia[order.long()], ib[order.long()]
+    share = ((a[1:] == a[:-1]) | (a[1:] == b[:-1]) | (b[1:] == a[:-1]) | (b[1:] == b[:-1]))
+    assert share.float().mean() > 0.5
+    assert layer.packed_tables(w)[0] is ia            # cached
+    w2 = w.clone()
+    assert layer.packed_tables(w2)[0] is not ia       # another winners tensor
+    wide = cl.LogicLayer(50, 400, connections="original")   # 16 reads per input row
+    wide.freeze()
+    assert wide.packed_tables(wide.w)[3] is None
