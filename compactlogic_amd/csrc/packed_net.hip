@@ -147,75 +147,95 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net(const uint32_t* __re
 // inputs, 16 bits each, and the opcode) in registers for the whole launch, so the gate
 // tables are read once per workgroup instead of once per column, and each workgroup walks a
 // range of columns, loading the next column's input words while it evaluates the current one.
-constexpr int kSlotCap = 80;  // gate slots per thread (registers)
+constexpr int kSlotCap = 72;  // gate slots per thread (registers)
 
-// Bit-sliced addition of the partner lane's number to this lane's: a += partner(a), W words
-// (word i holds bit i of 32 counts), the sum fitting in W bits.  Each word is fetched from
-// the partner inside the carry loop: all lanes fetch word i before any lane updates it, so
-// one temporary register suffices.
-// Only the low N words can be non-zero in either addend (N <= W).
-template <int CTRL, int N, int W>
-__device__ __forceinline__ void bs_add_dpp(uint32_t (&a)[W]) {
-    uint32_t c = 0;
+// Exchange with lane l ^ K inside each 32-lane half of the wave.
+template <int K>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (K == 1) return dpp_move<0xB1>(v);         // quad_perm [1,0,3,2]
+    else if constexpr (K == 2) return dpp_move<0x4E>(v);    // quad_perm [2,3,0,1]
+    else if constexpr (K == 8) return dpp_move<0x128>(v);   // row_ror:8
+    else return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), (K << 10) | 0x1F));  // xor mode
+}
+
+// One stage of the 32 x 32 bit transpose across a half-wave (row = lane, column = bit): lanes
+// l and l ^ K swap the off-diagonal K x K blocks of every 2K x 2K block.  The lane with bit K
+// clear keeps its columns c with c & K == 0 and takes the partner's same columns shifted up by
+// K; the other keeps c & K != 0 and takes the partner's shifted down.  A rotation by K or
+// 32 - K moves the wanted bits into place for either lane (the bits it wraps round are masked).
+template <int K>
+__device__ __forceinline__ uint32_t transpose_stage(uint32_t t, int lane) {
+    constexpr uint32_t m = K == 16 ? 0x0000FFFFu
+                           : K == 8 ? 0x00FF00FFu
+                           : K == 4 ? 0x0F0F0F0Fu
+                           : K == 2 ? 0x33333333u
+                                    : 0x55555555u;  // columns c with c & K == 0
+    const bool low = (lane & K) == 0;
+    const uint32_t p = xor_lane<K>(t);
+    const uint32_t sh = __builtin_amdgcn_alignbit(p, p, low ? 32 - K : K);  // rotate right
+    const uint32_t keep = low ? m : ~m;
+    return (t & keep) | (sh & ~keep);
+}
+
+// Adds the 1-bit numbers of x into the bit planes a[I..B) (a ripple of half adders).
+template <int I, int B>
+__device__ __forceinline__ void add_planes(uint32_t (&a)[B], uint32_t x) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const uint32_t x = a[i], y = dpp_move<CTRL>(x);
-        a[i] = x ^ y ^ c;
-        c = (x & y) | (c & (x | y));
+    for (int i = I; i < B; ++i) {
+        const uint32_t carry = a[i] & x;
+        a[i] ^= x;
+        x = carry;
     }
 }
 
-template <int N, int W>
-__device__ __forceinline__ void bs_add_xor(uint32_t (&a)[W], int d) {
-    uint32_t c = 0;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const uint32_t x = a[i], y = uint32_t(__shfl_xor(int(x), d, 64));
-        a[i] = x ^ y ^ c;
-        c = (x & y) | (c & (x | y));
-    }
+// Full adder on bit planes: a, carry = a + x + y (sum bit and carry bit per sample).
+__device__ __forceinline__ uint32_t full_add(uint32_t& a, uint32_t x, uint32_t y) {
+    const uint32_t carry = (a & x) | (a & y) | (x & y);
+    a ^= x ^ y;
+    return carry;
 }
 
-// Class counts of one column, one wave per class: lane l adds rows l, l + 64, ... of the
-// class into (W - 6)-bit vertical counters, six butterfly steps of bit-sliced addition (DPP
-// inside each 16-lane row, then lane shuffles across rows) leave the class total of all 32
-// samples in every lane as W bit planes, and lane s < 32 reads off the count of sample s.
-// Requires gs <= 2^W - 64 (per-lane counts fit W - 6 bits, the total W bits).  Integer sums:
-// exact and independent of the order.
-template <int W>
+// Class counts of one column, one wave per class.  Lane l adds rows l, l + 64, ... of the
+// class into B bit planes (bit s of plane b = bit b of its count for sample s; four rows per
+// step through three full adders); the lane's count is at most ceil(gs / 64) < 2^B.  Each
+// plane, read across a half-wave, is a 32 x 32 bit matrix (row = lane, column = sample); five
+// exchange stages transpose it, after which lane j holds column j and one popcount sums the
+// plane over the half-wave's 32 lanes for sample j.  The two half-waves' sums are added.
+// Integer sums: exact and independent of the order.
+template <int B>
 __device__ __forceinline__ void column_counts_wave(const uint32_t* last, const PackedNet& net,
                                                    int64_t col, int64_t nsamples,
                                                    int32_t* __restrict__ counts) {
-    constexpr int LW = W - 6;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int gs = net.rows[net.num_layers] / net.k;
-    for (int c = wave; c < net.k; c += kNetThreads / 64) {  // uniform per wave
-        uint32_t a[W];
+    for (int c = wave_id(); c < net.k; c += kNetThreads / 64) {  // uniform per wave
+        uint32_t a[B];
 #pragma unroll
-        for (int i = 0; i < W; ++i) a[i] = 0;
+        for (int i = 0; i < B; ++i) a[i] = 0;
+        const int end = (c + 1) * gs;
+        int r = c * gs + lane;
 #pragma unroll 1
-        for (int r = c * gs + lane; r < (c + 1) * gs; r += 64) {
-            // add one row's bits into the low LW words (per-lane counts stay below 2^LW)
-            uint32_t x = last[r];
-#pragma unroll
-            for (int i = 0; i < LW; ++i) {
-                const uint32_t carry = a[i] & x;
-                a[i] ^= x;
-                x = carry;
-            }
+        for (; r + 192 < end; r += 256) {
+            const uint32_t x0 = last[r], x1 = last[r + 64], x2 = last[r + 128], x3 = last[r + 192];
+            const uint32_t c1 = full_add(a[0], x0, x1);
+            const uint32_t c2 = full_add(a[0], x2, x3);
+            add_planes<2>(a, full_add(a[1], c1, c2));
         }
-        // after step k the sums have at most LW + k bits: each step carries one word further
-        constexpr auto n = [](int k) { return LW + k < W ? LW + k : W; };
-        bs_add_dpp<0xB1, n(1)>(a);   // quad_perm [1,0,3,2]
-        bs_add_dpp<0x4E, n(2)>(a);   // quad_perm [2,3,0,1]
-        bs_add_dpp<0x124, n(3)>(a);  // row_ror:4
-        bs_add_dpp<0x128, n(4)>(a);  // row_ror:8
-        bs_add_xor<n(5)>(a, 16);
-        bs_add_xor<n(6)>(a, 32);
-        if (lane < 32) {
-            int32_t n = 0;
+#pragma unroll 1
+        for (; r < end; r += 64) add_planes<0>(a, last[r]);
+        int32_t n = 0;
 #pragma unroll
-            for (int i = 0; i < W; ++i) n |= int32_t((a[i] >> lane) & 1u) << i;
+        for (int b = 0; b < B; ++b) {
+            uint32_t t = a[b];
+            t = transpose_stage<16>(t, lane);
+            t = transpose_stage<8>(t, lane);
+            t = transpose_stage<4>(t, lane);
+            t = transpose_stage<2>(t, lane);
+            t = transpose_stage<1>(t, lane);
+            n += int32_t(__builtin_popcount(t)) << b;
+        }
+        n += __shfl_xor(n, 32, 64);  // the other half-wave's rows
+        if (lane < 32) {
             const int64_t sample = col * 32 + lane;
             if (sample < nsamples) counts[sample * net.k + c] = n;
         }
@@ -237,29 +257,53 @@ __device__ __forceinline__ void column_counts_wave(const uint32_t* last, const P
 #endif
 constexpr int kBatch = CL_NET_BATCH;  // gates whose row reads are in flight together
 
-template <int CW, int J, int IPT>
+// With J <= 12 the opcode nibbles live in LDS after the two row buffers (word i of thread t
+// at i * 1024 + t, conflict-free), not in registers: with 1024-thread workgroups a wave has
+// at most 128 VGPRs, and the gate entries alone take up to 72 of them.  A layer loads the two
+// or three opcode words of its slots when it starts.  (Two buffers of 16 * 1024 rows leave no
+// room for them: with J = 16 they stay in registers, next to 64 entries.)
+constexpr int kOpsLdsMaxJ = 12;
+
+template <int B, int J, int IPT>
 __global__ __launch_bounds__(kNetThreads) void k_packed_net_slots(
     const uint32_t* __restrict__ x, int64_t cols, int64_t nsamples,
     const uint64_t* __restrict__ tables, PackedNet net, int32_t* __restrict__ counts,
     int buf_words) {
     constexpr int LMAX = kSlotCap / J < kNetMaxLayers ? kSlotCap / J : kNetMaxLayers;
     constexpr int TG = LMAX * J;
+    constexpr int OW = (TG + 7) / 8;
+    constexpr bool OPSL = J <= kOpsLdsMaxJ;
     extern __shared__ __align__(16) uint32_t lds[];
+    uint32_t* ops_lds = lds + 2 * buf_words;
     const int tid = threadIdx.x;
     const int L = net.num_layers;
     uint32_t ent[TG];
-    uint32_t ops[(TG + 7) / 8];
+    uint32_t ops[OW];
 #pragma unroll
-    for (int i = 0; i < (TG + 7) / 8; ++i) ops[i] = 0;
+    for (int i = 0; i < OW; ++i) ops[i] = 0;
 #pragma unroll
     for (int q = 0; q < TG; ++q) {
         const int l = q / J, o = tid + kNetThreads * (q % J);
-        ent[q] = 0;  // no gate in this slot: reads row 0, writes past the layer's rows
-        if (l < L && o < net.rows[l + 1]) {
-            const uint64_t e = tables[net.table_off[l] + o];
+        // no gate in this slot: entry 0 reads row 0 and writes past the layer's rows
+        const bool gate = l < L && o < net.rows[l + 1];
+        uint64_t e = 0;
+        if constexpr (TG <= 16) {
+            // selects, not branches: a conditionally assigned array this small becomes one
+            // vector register tuple, copied whole at every branch
+            e = tables[gate ? net.table_off[l] + o : 0];
+            e = gate ? e : 0;
+        } else {
+            if (gate) e = tables[net.table_off[l] + o];
+        }
+        ent[q] = 0;
+        if (TG <= 16 || gate) {
             ent[q] = (uint32_t(e) & 0xffffu) | (__builtin_amdgcn_ubfe(uint32_t(e >> 20), 0, 16) << 16);
             ops[q / 8] |= __builtin_amdgcn_ubfe(uint32_t(e >> 32), 8, 4) << (4 * (q % 8));
         }
+    }
+    if constexpr (OPSL) {
+#pragma unroll
+        for (int i = 0; i < OW; ++i) ops_lds[i * kNetThreads + tid] = ops[i];
     }
     const int64_t per = (cols + 7) / 8;
     const int64_t nb8 = gridDim.x / 8;
@@ -286,8 +330,10 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net_slots(
         // compiler from hoisting per-gate values derived from them (the two LDS addresses,
         // the four truth-table masks) out of the column loop, which would need up to six more
         // registers per gate.
+        if constexpr (!OPSL) {
 #pragma unroll
-        for (int i = 0; i < (TG + 7) / 8; ++i) asm volatile("" : "+v"(ops[i]));
+            for (int i = 0; i < OW; ++i) asm volatile("" : "+v"(ops[i]));
+        }
 #pragma unroll
         for (int q = 0; q < TG; ++q) asm volatile("" : "+v"(ent[q]));
 #pragma unroll
@@ -296,6 +342,15 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net_slots(
                 const unsigned char* cur =
                     reinterpret_cast<const unsigned char*>(lds + (l & 1) * buf_words);
                 uint32_t* nxt = lds + ((l + 1) & 1) * buf_words;
+                // the opcode words of this layer's slots (a constant range once unrolled)
+                constexpr int NW = (J + 7) / 8 + 1;
+                const int wlo = (l * J) / 8;
+                uint32_t lw[NW];
+#pragma unroll
+                for (int i = 0; i < NW; ++i) {
+                    const int wi = wlo + i < OW ? wlo + i : OW - 1;
+                    lw[i] = OPSL ? ops_lds[wi * kNetThreads + tid] : ops[wi];
+                }
                 // the row reads of kBatch gates are issued together, then the gates computed
 #pragma unroll
                 for (int j0 = 0; j0 < J; j0 += kBatch) {
@@ -310,14 +365,14 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net_slots(
                     for (int j = j0; j < j0 + kBatch && j < J; ++j) {
                         const int q = l * J + j;
                         nxt[tid + kNetThreads * j] = gate_word(
-                            (ops[q / 8] >> (4 * (q % 8))) & 15u, va[j - j0], vb[j - j0]);
+                            (lw[q / 8 - wlo] >> (4 * (q % 8))) & 15u, va[j - j0], vb[j - j0]);
                     }
                 }
                 __syncthreads();
             }
         }
         // the last layer's rows are in buffer L % 2
-        column_counts_wave<CW>(lds + (L & 1) * buf_words, net, col, nsamples, counts);
+        column_counts_wave<B>(lds + (L & 1) * buf_words, net, col, nsamples, counts);
         __syncthreads();  // the next column overwrites both buffers
     }
 }
@@ -364,28 +419,9 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
         set_error("in_dim (%d) has to be divisible by k (%lld) but it is not", last, (long long)k);
         return CL_ERR_VALUE;
     }
-    // slices per class: one thread each, as many as fit
     const int gs = last / int(k);
     CL_ARG(int(k) <= kNetThreads, "k must be at most %d for the fused pass", kNetThreads);
-    const int S = std::max(1, std::min(kNetThreads / int(k), gs));
-    const int per_slice = int(ceil_div(gs, S));
-    int NB = 1;
-    while ((1 << NB) <= per_slice) ++NB;
-    NB = NB <= 4 ? 4 : (NB <= 8 ? 8 : NB);
-    CL_ARG(NB <= kMaxCountBits, "class groups too large for the fused pass");
-    net.slices = S;
-    const int pairs = 32 * int(k);
-    const int P = std::max(1, kNetThreads / pairs);
-    const int count_words = int(k) * S * NB + P * pairs;
-    int buf_words = std::max(max_rows, count_words);
-    size_t lds = size_t(2) * buf_words * 4;
-    CL_ARG(lds <= 160 * 1024, "activations do not fit in LDS");
     const int64_t cols = row_bytes / 4;
-    if (nsamples == 0 || cols == 0) return CL_OK;
-    CL_ARG(x && tables && counts, "null pointer argument");
-    CL_ARG(aligned(x, 4) && aligned(tables, 8), "misaligned buffers");
-    const int64_t blocks = 8 * ceil_div(cols, 8);
-    CL_ARG(blocks < (int64_t(1) << 31), "too many columns");
     int rc = CL_OK;
     // persistent slot-table variant when it applies: J slots of 1024 rows per layer
     int J = int(ceil_div(int64_t(*std::max_element(net.rows + 1, net.rows + num_layers + 1)),
@@ -396,12 +432,20 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
             break;
         }
     }
+    // a lane of the class counts adds at most ceil(gs / 64) rows, fewer than 2^B
+    const int per_lane = int(ceil_div(gs, 64));
     const bool slots = max_rows <= 16383 && net.rows[0] <= 4 * kNetThreads && J <= 16 &&
-                       num_layers <= std::min(kSlotCap / J, kNetMaxLayers);
+                       num_layers <= std::min(kSlotCap / J, kNetMaxLayers) && per_lane < 256;
     if (slots && !kNetDisableRegs) {
         // every slot writes: a buffer spans the J * 1024 rows a thread's slots can address
-        buf_words = std::max(buf_words, J * kNetThreads);
-        lds = size_t(2) * buf_words * 4;
+        const int buf_words = std::max(max_rows, J * kNetThreads);
+        const int LMAX = std::min(kSlotCap / J, kNetMaxLayers);
+        const size_t ops_bytes = size_t((LMAX * J + 7) / 8) * kNetThreads * 4;
+        const size_t lds = size_t(2) * buf_words * 4 + (J <= kOpsLdsMaxJ ? ops_bytes : 0);
+        CL_REQUIRE(lds <= 160 * 1024, CL_ERR_VALUE, "internal error: %zu bytes of LDS", lds);
+        if (nsamples == 0 || cols == 0) return CL_OK;
+        CL_ARG(x && tables && counts, "null pointer argument");
+        CL_ARG(aligned(x, 4) && aligned(tables, 8), "misaligned buffers");
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
@@ -438,14 +482,32 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
             if (net.rows[0] <= kNetThreads) by_j(nb, std::integral_constant<int, 1>());
             else by_j(nb, std::integral_constant<int, 4>());
         };
-        // count width: gs <= 2^CW - 64
-        if (gs <= 192) by_ipt(std::integral_constant<int, 8>());
-        else if (gs <= 960) by_ipt(std::integral_constant<int, 10>());
-        else if (gs <= 4032) by_ipt(std::integral_constant<int, 12>());
-        else by_ipt(std::integral_constant<int, 15>());
+        if (per_lane < 8) by_ipt(std::integral_constant<int, 3>());
+        else if (per_lane < 32) by_ipt(std::integral_constant<int, 5>());
+        else by_ipt(std::integral_constant<int, 8>());
         if (rc) return rc;
         return check_launch("cl_packed_network");
     }
+    // one column per workgroup; the class counts use the buffers as scratch
+    // slices per class: one thread each, as many as fit
+    const int S = std::max(1, std::min(kNetThreads / int(k), gs));
+    const int per_slice = int(ceil_div(gs, S));
+    int NB = 1;
+    while ((1 << NB) <= per_slice) ++NB;
+    NB = NB <= 4 ? 4 : (NB <= 8 ? 8 : NB);
+    CL_ARG(NB <= kMaxCountBits, "class groups too large for the fused pass");
+    net.slices = S;
+    const int pairs = 32 * int(k);
+    const int P = std::max(1, kNetThreads / pairs);
+    const int count_words = int(k) * S * NB + P * pairs;
+    const int buf_words = std::max(max_rows, count_words);
+    const size_t lds = size_t(2) * buf_words * 4;
+    CL_ARG(lds <= 160 * 1024, "activations do not fit in LDS");
+    if (nsamples == 0 || cols == 0) return CL_OK;
+    CL_ARG(x && tables && counts, "null pointer argument");
+    CL_ARG(aligned(x, 4) && aligned(tables, 8), "misaligned buffers");
+    const int64_t blocks = 8 * ceil_div(cols, 8);
+    CL_ARG(blocks < (int64_t(1) << 31), "too many columns");
     auto launch = [&](auto nb) {
         auto* kern = &k_packed_net<decltype(nb)::value>;
         // more than the default 64 KiB of dynamic LDS per workgroup

@@ -42,6 +42,9 @@ def oracle_counts(model, words_np, n):
     ([(64, 2000), (2000, 1000)], 8, 16, 4096),
     ([(12, 20)] + [(20, 20)] * 14 + [(20, 30)], 3, 8, 130),
     ([(64, 17000), (17000, 8500)], 10, 4, 200),     # wider than the register-table variant
+    ([(3000, 5000), (5000, 2600)], 4, 16, 700),     # > 1024 input rows: 4 per thread
+    ([(64, 15000), (15000, 16000)], 2, 4, 300),     # 16 gates per thread, 8000-row classes
+    ([(50, 400), (400, 340)], 20, 8, 150),          # more classes than waves
 ])
 def test_packed_network_matches_oracle_and_layerwise(device, dims, k, g_n, n):
     model = frozen_net(dims, k, g_n, sum(d[1] for d in dims), device)
