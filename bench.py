@@ -71,13 +71,15 @@ def log(msg):
 
 def dense_step_fn(model, x, labels, torch):
     """One training step: the network, the mean cross-entropy of GroupSum's scores (fused into
-    GroupSum's kernels: GroupSum.cross_entropy is cross_entropy(GroupSum(x), labels)), and the
-    backward into every layer's logits."""
-    body, head = model[:-1], model[-1]
+    GroupSum's kernels: GroupSum.cross_entropy is cross_entropy(GroupSum(x), labels); when the
+    last layer is dense, fused with it too: sequential_cross_entropy), and the backward into
+    every layer's logits."""
+    import compactlogic_amd as cl
     one = torch.ones((), dtype=torch.float32, device=x.device)  # d loss / d loss, made once
 
     def step():
-        loss = head.cross_entropy(body(x), labels)
+        # the last dense layer, GroupSum and the loss through the fused classifier head
+        loss = cl.sequential_cross_entropy(model, x, labels)
         loss.backward(one)
         return loss
     return step
@@ -156,10 +158,9 @@ def bench_train_full(args, torch):
     model = configs.dense_network(cfg, device=dev)
     x, labels = configs.dense_inputs(cfg, device=dev)
     opt = cl.FusedAdam(model.parameters(), lr=0.01, max_norm=10.0)
-    body, head = model[:-1], model[-1]
 
     def step():
-        loss = head.cross_entropy(body(x), labels)
+        loss = cl.sequential_cross_entropy(model, x, labels)
         loss.backward()
         opt.step()
 
@@ -195,6 +196,8 @@ def train_kernel_bytes(model, batch: int) -> dict:
     import compactlogic_amd as cl
     out = {}
     first = True
+    prev_out = 0
+    k_out = next((mm.k for mm in model if isinstance(mm, cl.GroupSum)), 0)
     for m in model:
         if isinstance(m, cl.ConvLogicLayer):
             # complete block: forward reads x, writes the pooled y; backward reads x and
@@ -226,9 +229,20 @@ def train_kernel_bytes(model, batch: int) -> dict:
                         "cl_dense_backward_rows" + tag: 2 * xb + yb,
                         "cl_dense_backward_part" + tag: 2 * xb + yb,
                         "cl_dense_weight_grad" + tag: xb + yb})
+            # as the classifier head with GroupSum's cross-entropy: the forward reads x (and
+            # writes scores and softmax, [batch, k] each), the backward reads x, writes grad_x
+            out["cl_dense_group_sum_cross_entropy_forward" + tag] = xb + 8 * batch * k_out
+            out["cl_dense_group_sum_cross_entropy_backward" + tag] = 2 * xb
             # layout change of a [batch, in_dim] input and of its gradient: read + write
             out[f"cl_transpose[{batch}x{m.in_dim}]"] = 2 * xb
             out[f"cl_transpose[{m.in_dim}x{batch}]"] = 2 * xb
+            prev_out = m.out_dim
+        elif isinstance(m, cl.GroupSum) and prev_out:
+            # unfused cross-entropy: the forward reads the last layer's output, the backward
+            # writes its gradient (scores and softmax, [batch, k] each, besides)
+            fb = 4 * batch * prev_out
+            out["cl_group_sum_cross_entropy_forward"] = fb + 8 * batch * m.k
+            out["cl_group_sum_cross_entropy_backward"] = fb
         if not isinstance(m, torch_flatten_types()):
             first = False
     return out

@@ -10,8 +10,9 @@ PoolLogicLayer).  All numerics run in libcompactlogic_hip.so, built in-tree by
 from . import convlogic_hip, difflogic_hip
 from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction,
                      ConvLayerWindowFunction, GroupSum, GroupSumCrossEntropyFunction,
-                     GroupSumFunction, LogicLayer,
-                     LogicLayerCudaFunction, LogicLayerRunsFunction, PackBitsTensor)
+                     GroupSumFunction, LogicGroupSumCrossEntropyFunction, LogicLayer,
+                     LogicLayerCudaFunction, LogicLayerRunsFunction, PackBitsTensor,
+                     logic_group_sum_cross_entropy, sequential_cross_entropy)
 from .optim import FusedAdam
 from .packed_net import PackedNetwork
 from .plan import RunPlan, build_run_plan
@@ -27,4 +28,6 @@ __all__ = [
     "convlogic_hip", "SequentialEntropyFreezer", "FixedSequentialEntropyFreezer",
     "EntropyRowResampler", "PackedNetwork", "ConvLogicLayer", "TreeLogicLayer", "PoolLogicLayer",
     "ConvLogicFunction", "FullConvLogicFunction", "TreeLogicFunction", "FusedAdam",
+    "LogicGroupSumCrossEntropyFunction", "logic_group_sum_cross_entropy",
+    "sequential_cross_entropy",
 ]

@@ -84,6 +84,15 @@ SIGNATURES: dict[str, list] = {
     "cl_group_sum_cross_entropy_backward": [_int, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _f64,
                                             _p, _i64, _i64, _p],
     "cl_group_sum_cross_entropy_scratch_limit": [ctypes.POINTER(_i64)],
+    "cl_dense_group_sum_cross_entropy_workspace_size": [_int, _i64, _i64, _i64,
+                                                        ctypes.POINTER(_i64),
+                                                        ctypes.POINTER(_i64)],
+    "cl_dense_group_sum_cross_entropy_forward": [_int, _p, _p, _int, _p, _p, _p, _p, _p, _i64,
+                                                 _i64, _i64, _i64, _i64, _i64, _f64, _p, _i64,
+                                                 _p, _p, _p, _p, _p, _i64, _p],
+    "cl_dense_group_sum_cross_entropy_backward": [_int, _p, _p, _p, _i64, _p, _p, _i64, _f64,
+                                                  _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
+                                                  _i64, _i64, _i64, _p, _i64, _p],
     "cl_plan_locality_order": [ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i64, _i64,
                                ctypes.POINTER(_i32)],
     "cl_adam_clip_max_tensors": [ctypes.POINTER(_i64)],

@@ -219,4 +219,14 @@ constexpr int wide_vec() {
     return 16 / int(sizeof(T));
 }
 
+// Cross-entropy of GroupSum scores given as per-tile class partials of the classifier head
+// (the last dense layer's fused forward, dense_tiled.hip): part[(t * 2 + slot) * batch + n] is
+// the sum over tile t's rows (tile_rows consecutive rows) of class (t * tile_rows / gsz) + slot.
+// Adds them per (sample, class) into `nslices` slices, then the softmax, the loss terms and
+// their mean as cl_group_sum_cross_entropy_forward does (groupsum.hip).
+int ce_from_tile_partials(int dtype, const void* part, int64_t batch, int64_t features,
+                          int64_t k, int64_t tile_rows, double tau, const int64_t* labels,
+                          int64_t ignore_index, void* out, void* probs, void* loss, void* count,
+                          void* slices, int64_t nslices, void* term, hipStream_t stream);
+
 }  // namespace cl

@@ -352,7 +352,13 @@ __device__ __forceinline__ T fused_rcp(T v) {
 // the last reduction (DPP reads its neighbours), partial-chunk lanes only skip their row
 // accesses.  The tile's writer chunk (t mod nchunks) stores probs and the inverse-index
 // coefficients that the backward pass reads.
-template <typename T, int VEC, int LPN, int NPG, bool COEF>
+//
+// HEAD (the last layer of a classifier, followed by GroupSum and the cross-entropy): the
+// outputs are not stored.  Each lane adds its rows' outputs into two class sums (the class of
+// the tile's first row, and the next class), the tile's lane groups add theirs in LDS in row
+// order, and the tile writes part[(t * 2 + slot) * B + n]; a tile spans at most two classes
+// (gsz >= 256 / LPN * NPG rows, checked by the host).
+template <typename T, int VEC, int LPN, int NPG, bool COEF, bool HEAD>
 __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T* __restrict__ w,
                                                int softmax, const uint8_t* __restrict__ gs,
                                                const int4* __restrict__ nab,
@@ -360,12 +366,16 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
                                                T* __restrict__ probs, T* __restrict__ inv_coef,
                                                T* __restrict__ y, int64_t in_dim, int64_t out_dim,
                                                int64_t num_runs, int64_t B, int G,
-                                               const TileMap& tm, int64_t c, int64_t t) {
+                                               const TileMap& tm, int64_t c, int64_t t,
+                                               T* __restrict__ part, int64_t gsz,
+                                               T* __restrict__ red) {
     using V = typename VT<T, VEC>::type;
     constexpr int GROUPS = 256 / LPN;
     constexpr int SPL = 16 / LPN;
     const int64_t obase = (t * GROUPS + threadIdx.x / LPN) * NPG;
-    if (obase >= out_dim) return;  // uniform per lane group
+    // uniform per lane group; the head's lane groups past the end stay for the tile's barrier
+    if (!HEAD && obase >= out_dim) return;
+    const int64_t ob = obase < out_dim ? obase : 0;  // clamped row for the loads
     const int l = threadIdx.x % LPN;
     const int64_t idx = c * (LPN * VEC) + int64_t(l) * VEC;
     const bool col = idx < B;
@@ -379,7 +389,7 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
 #pragma unroll
     for (int j = 0; j < NPG; ++j) {
         live[j] = obase + j < out_dim;
-        rec[j] = ld_rec(nab + (live[j] ? obase + j : obase));
+        rec[j] = ld_rec(nab + (live[j] ? obase + j : ob));
     }
     T p[NPG][SPL];
     int code[NPG][SPL];
@@ -388,7 +398,7 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
 #pragma unroll
         for (int m = 0; m < SPL; ++m) {
             const int g = l + LPN * m;
-            const int64_t wi = (live[j] ? obase + j : obase) * G + (g < G ? g : 0);
+            const int64_t wi = (live[j] ? obase + j : ob) * G + (g < G ? g : 0);
             p[j][m] = w[wi];
             code[j][m] = gs[wi];
         }
@@ -415,6 +425,9 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
             p[j][m] = v ? p[j][m] : -T(__builtin_inf());
             code[j][m] = v ? code[j][m] : 0;
         }
+    // head: the first row of the tile's second class
+    const int64_t bound = HEAD ? (t * GROUPS * NPG / gsz + 1) * gsz : 0;
+    V h0 = V(T(0)), h1 = V(T(0));
 #pragma unroll
     for (int j = 0; j < NPG; ++j) {
         const int64_t o = obase + j;
@@ -475,12 +488,40 @@ __device__ __forceinline__ void fwd_fused_tile(const T* __restrict__ x, const T*
         if (col) {
             V acc = V(nan_of<T>());
             if (ok[j]) acc = k3 * (va[j] * vb[j]) + k2 * vb[j] + k1 * va[j] + k0;
-            vst_stream<V>(y + o * B + idx, acc);
+            if constexpr (HEAD) {
+                if (o < bound) h0 += acc;
+                else h1 += acc;
+            } else {
+                vst_stream<V>(y + o * B + idx, acc);
+            }
+        }
+    }
+    if constexpr (HEAD) {
+        // red[(group * 2 + slot) * LPN * VEC + column]: the lane groups' sums, added in group
+        // (= row) order by the thread of each (slot, column)
+        constexpr int CW = LPN * VEC;
+        const int grp = threadIdx.x / LPN;
+        const T* e0 = reinterpret_cast<const T*>(&h0);  // V is T itself when VEC == 1
+        const T* e1 = reinterpret_cast<const T*>(&h1);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            red[(grp * 2 + 0) * CW + l * VEC + i] = e0[i];
+            red[(grp * 2 + 1) * CW + l * VEC + i] = e1[i];
+        }
+        __syncthreads();
+        const int64_t first = t * GROUPS * NPG;
+        for (int e = threadIdx.x; e < 2 * CW; e += 256) {
+            const int slot = e / CW, cc = e % CW;
+            T sum = T(0);
+#pragma unroll 8
+            for (int g = 0; g < GROUPS; ++g) sum += red[(g * 2 + slot) * CW + cc];
+            const int64_t n = c * CW + cc;
+            if (n < B && first < out_dim) part[(t * 2 + slot) * B + n] = sum;
         }
     }
 }
 
-template <typename T, int VEC, int LPN, int NPG, bool COEF>
+template <typename T, int VEC, int LPN, int NPG, bool COEF, bool HEAD>
 __global__ __launch_bounds__(256) void k_fwd_fused(const T* __restrict__ x, const T* __restrict__ w,
                                                    int softmax, const uint8_t* __restrict__ gs,
                                                    const int4* __restrict__ nab,
@@ -488,11 +529,14 @@ __global__ __launch_bounds__(256) void k_fwd_fused(const T* __restrict__ x, cons
                                                    T* __restrict__ probs, T* __restrict__ inv_coef,
                                                    T* __restrict__ y, int64_t in_dim,
                                                    int64_t out_dim, int64_t num_runs, int64_t B,
-                                                   int G, TileMap tm) {
+                                                   int G, TileMap tm, T* __restrict__ part,
+                                                   int64_t gsz) {
+    __shared__ T red[HEAD ? 2 * 256 * VEC : 1];
     int64_t c, t;
-    if (map_tile(tm, blockIdx.x, c, t))
-        fwd_fused_tile<T, VEC, LPN, NPG, COEF>(x, w, softmax, gs, nab, inv_pos, probs, inv_coef, y,
-                                         in_dim, out_dim, num_runs, B, G, tm, c, t);
+    if (map_tile(tm, blockIdx.x, c, t))  // uniform per workgroup
+        fwd_fused_tile<T, VEC, LPN, NPG, COEF, HEAD>(x, w, softmax, gs, nab, inv_pos, probs,
+                                                     inv_coef, y, in_dim, out_dim, num_runs, B,
+                                                     G, tm, c, t, part, gsz, red);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1051,14 +1095,17 @@ __global__ __launch_bounds__(256) void k_bwd_part(
 // and an invalid record reads row 0 and poisons the result.  A load under a branch would make
 // the compiler wait for all loads in flight at the branch's end.  Entries are taken EPI at a
 // time (the records are wave-uniform), so their row gathers are in flight together; the
-// input gradient still adds the entries in entry order.
+// input gradient still adds the entries in entry order.  With gy_magic != 0 the gradient of
+// neuron o is row o / gsz of grad_y (one row per GroupSum class: the fused classifier head),
+// gy_magic = ceil(2^32 / gsz) with out_dim * gsz <= 2^32, so the multiply-high is exact.
 template <typename T, int VEC, int U, bool WANT_GW, bool HAS_P>
 __global__ __launch_bounds__(256) void k_bwd_rows(
     const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
     const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef,
     const uint8_t* __restrict__ gs, const T* __restrict__ probs,
     const int32_t* __restrict__ run_ptr, T* __restrict__ grad_w, T* __restrict__ gx,
-    int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, int G, int64_t nblk) {
+    int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, int G, int64_t nblk,
+    uint32_t gy_magic) {
     using V = typename VT<T, VEC>::type;
     using V2 = typename VT<T, 2>::type;
     constexpr int EPI = U <= 4 ? 2 : 1;  // entries per step (register budget)
@@ -1110,10 +1157,13 @@ __global__ __launch_bounds__(256) void k_bwd_rows(
         }
 #pragma unroll
         for (int q = 0; q < EPI; ++q) {
+            // grad_y row of the neuron: its own, or its class's (o / gsz as a multiply-high)
+            const int64_t gyr = gy_magic ? int64_t(__umulhi(uint32_t(cur[q].x), gy_magic))
+                                         : int64_t(cur[q].x);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 vo[q][u] = vld<V>(x + int64_t(cur[q].y) * B + off[u]);
-                vg[q][u] = vld<V>(gy + int64_t(cur[q].x) * B + off[u]);
+                vg[q][u] = vld<V>(gy + gyr * B + off[u]);
             }
             // the finalize's per-neuron data is loaded with the rows, not after the moments
             if constexpr (WANT_GW) {
@@ -1465,13 +1515,13 @@ extern "C" int cl_dense_forward_fused(int dtype, const void* x, const void* w, i
         with_tiling<T, CL_FUSED_VEC_MULT>(tl, [&](auto vc, auto lc) {
             constexpr int VEC = decltype(vc)::value, LPN = decltype(lc)::value;
             if (ic)
-                k_fwd_fused<T, VEC, LPN, CL_FWD_NPG, true><<<grid, 256, 0, s>>>(
+                k_fwd_fused<T, VEC, LPN, CL_FWD_NPG, true, false><<<grid, 256, 0, s>>>(
                     xs, ws, softmax, gate_seq, nb, inv_pos, pr, ic, ys, in_dim, out_dim, num_runs,
-                    batch, int(num_gates), tl.map);
+                    batch, int(num_gates), tl.map, nullptr, 0);
             else
-                k_fwd_fused<T, VEC, LPN, CL_FWD_NPG, false><<<grid, 256, 0, s>>>(
+                k_fwd_fused<T, VEC, LPN, CL_FWD_NPG, false, false><<<grid, 256, 0, s>>>(
                     xs, ws, softmax, gate_seq, nb, inv_pos, pr, ic, ys, in_dim, out_dim, num_runs,
-                    batch, int(num_gates), tl.map);
+                    batch, int(num_gates), tl.map, nullptr, 0);
         });
     });
     return check_launch("cl_dense_forward_fused");
@@ -1678,14 +1728,12 @@ extern "C" int cl_dense_backward_part(int dtype, const void* x, const void* grad
     return check_launch("cl_dense_backward_part");
 }
 
-extern "C" int cl_dense_backward_rows(int dtype, const void* x, const void* grad_y,
-                                      const int32_t* slot_rec, const int32_t* inv_rec,
-                                      const void* inv_coef, const uint8_t* gate_seq,
-                                      const void* probs, const int32_t* run_ptr, void* grad_w,
-                                      void* grad_x, int64_t in_dim, int64_t out_dim,
-                                      int64_t num_runs, int64_t batch, int64_t num_gates,
-                                      void* stream) {
-    clear_error();
+namespace {
+int backward_rows_impl(int dtype, const void* x, const void* grad_y, const int32_t* slot_rec,
+                       const int32_t* inv_rec, const void* inv_coef, const uint8_t* gate_seq,
+                       const void* probs, const int32_t* run_ptr, void* grad_w, void* grad_x,
+                       int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t batch,
+                       int64_t num_gates, uint32_t gy_magic, void* stream) {
     if (int rc = check_plan_dims(in_dim, out_dim, batch, num_gates, num_runs)) return rc;
     CL_ARG(num_gates <= 64, "the row backward takes at most 64 slots, got %lld",
            (long long)num_gates);
@@ -1718,7 +1766,8 @@ extern "C" int cl_dense_backward_rows(int dtype, const void* x, const void* grad
             auto launch = [&](auto gwc, auto pc) {
                 k_bwd_rows<T, W, U, decltype(gwc)::value, decltype(pc)::value>
                     <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq, pr, run_ptr, gw, gxs,
-                                          in_dim, out_dim, num_runs, batch, int(num_gates), nblk);
+                                          in_dim, out_dim, num_runs, batch, int(num_gates), nblk,
+                                          gy_magic);
             };
             using Y = std::true_type;
             using N = std::false_type;
@@ -1733,6 +1782,149 @@ extern "C" int cl_dense_backward_rows(int dtype, const void* x, const void* grad
         else go(std::integral_constant<int, 8>{});
     });
     return check_launch("cl_dense_backward_rows");
+}
+}  // namespace
+
+extern "C" int cl_dense_backward_rows(int dtype, const void* x, const void* grad_y,
+                                      const int32_t* slot_rec, const int32_t* inv_rec,
+                                      const void* inv_coef, const uint8_t* gate_seq,
+                                      const void* probs, const int32_t* run_ptr, void* grad_w,
+                                      void* grad_x, int64_t in_dim, int64_t out_dim,
+                                      int64_t num_runs, int64_t batch, int64_t num_gates,
+                                      void* stream) {
+    clear_error();
+    return backward_rows_impl(dtype, x, grad_y, slot_rec, inv_rec, inv_coef, gate_seq, probs,
+                              run_ptr, grad_w, grad_x, in_dim, out_dim, num_runs, batch,
+                              num_gates, 0, stream);
+}
+
+// ------------------------------------------------------------------------------------------
+// The classifier head: the last dense layer, GroupSum(k, tau) and the mean cross-entropy in
+// one autograd step.  The forward runs the fused forward kernel in its HEAD mode (the layer's
+// outputs are never stored: each tile writes the sums of its rows by class), adds the tiles'
+// partials per class and takes the softmax / loss as the GroupSum cross-entropy does.  The
+// backward writes the class gradients [k, batch] (every row of a class has the same one) and
+// runs the row backward with grad_y row o / gsz for neuron o.  Against the layer followed by
+// GroupSum's cross-entropy this saves writing and re-reading the layer's output and its
+// gradient (2 * 2 * out_dim * batch elements).
+namespace {
+constexpr int64_t kHeadSlices = 4;
+
+struct HeadShape {
+    Tiling tl;
+    int64_t tile_rows, gsz, part_elems, slice_elems;
+};
+
+template <typename T>
+bool head_shape(int64_t out_dim, int64_t batch, int64_t k, HeadShape& h) {
+    h.tl = choose_tiling<T>(batch, out_dim, CL_FUSED_VEC_MULT, CL_FWD_LPN, CL_FWD_NPG);
+    h.tile_rows = int64_t(256 / h.tl.lpn) * CL_FWD_NPG;
+    h.gsz = ceil_div(out_dim, k);
+    h.part_elems = h.tl.map.ntiles * 2 * batch;
+    h.slice_elems = kHeadSlices * k * batch;
+    // a tile spans at most two classes; o / gsz is an exact multiply-high for o < out_dim
+    return h.tile_rows <= h.gsz && uint64_t(out_dim) * uint64_t(h.gsz) <= (uint64_t(1) << 32);
+}
+}  // namespace
+
+extern "C" int cl_dense_group_sum_cross_entropy_workspace_size(int dtype, int64_t out_dim,
+                                                              int64_t batch, int64_t k,
+                                                              int64_t* forward_bytes,
+                                                              int64_t* backward_bytes) {
+    clear_error();
+    CL_ARG(forward_bytes && backward_bytes, "null pointer argument");
+    CL_ARG(out_dim >= 1 && batch >= 1 && k >= 1, "bad shape");
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        HeadShape h;
+        if (!head_shape<T>(out_dim, batch, k, h)) {
+            *forward_bytes = *backward_bytes = -1;  // the fused head does not apply
+        } else {
+            *forward_bytes = (h.part_elems + h.slice_elems + 2 * batch) * int64_t(sizeof(T));
+            *backward_bytes = k * batch * int64_t(sizeof(T));
+        }
+    });
+    return CL_OK;
+}
+
+extern "C" int cl_dense_group_sum_cross_entropy_forward(
+    int dtype, const void* x, const void* w, int softmax, const uint8_t* gate_seq,
+    const int32_t* nab, const int32_t* inv_pos, void* probs, void* inv_coef, int64_t in_dim,
+    int64_t out_dim, int64_t num_runs, int64_t batch, int64_t num_gates, int64_t k, double tau,
+    const int64_t* labels, int64_t ignore_index, void* scores, void* ce_probs, void* loss,
+    void* count, void* workspace, int64_t workspace_bytes, void* stream) {
+    clear_error();
+    if (int rc = check_plan_dims(in_dim, out_dim, batch, num_gates, num_runs)) return rc;
+    CL_ARG(num_gates <= 16, "the fused forward takes at most 16 slots, got %lld",
+           (long long)num_gates);
+    CL_ARG(batch >= 1 && out_dim >= 1 && in_dim >= 1 && k >= 1, "bad shape");
+    CL_ARG(num_runs >= 1, "num_runs must be >= 1 when out_dim > 0");
+    CL_ARG(x && w && gate_seq && nab && inv_pos && inv_coef && labels && scores && ce_probs &&
+               loss && count && workspace,
+           "null pointer argument");
+    CL_ARG(aligned(nab, 16), "nab misaligned");
+    hipStream_t s = as_stream(stream);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        HeadShape h;
+        CL_ARG(head_shape<T>(out_dim, batch, k, h),
+               "the fused head needs classes of at least %d rows (and out_dim * rows per "
+               "class <= 2^32)", 256 / CL_FWD_LPN * CL_FWD_NPG);
+        const int64_t need = (h.part_elems + h.slice_elems + 2 * batch) * int64_t(sizeof(T));
+        CL_ARG(workspace_bytes >= need,
+               "workspace of %lld bytes needed (cl_dense_group_sum_cross_entropy_workspace_size)",
+               (long long)need);
+        CL_ARG(!vec_ok<T>(batch) || all_aligned({x, workspace}),
+               "x and the workspace must be 16-byte aligned");
+        T* part = static_cast<T*>(workspace);
+        T* slices = part + h.part_elems;
+        T* term = slices + h.slice_elems;
+        const unsigned grid = unsigned(tile_grid(h.tl.map));
+        with_tiling<T, CL_FUSED_VEC_MULT>(h.tl, [&](auto vc, auto lc) {
+            constexpr int VEC = decltype(vc)::value, LPN = decltype(lc)::value;
+            k_fwd_fused<T, VEC, LPN, CL_FWD_NPG, true, true><<<grid, 256, 0, s>>>(
+                static_cast<const T*>(x), static_cast<const T*>(w), softmax, gate_seq,
+                reinterpret_cast<const int4*>(nab), inv_pos, static_cast<T*>(probs),
+                static_cast<T*>(inv_coef), nullptr, in_dim, out_dim, num_runs, batch,
+                int(num_gates), h.tl.map, part, h.gsz);
+        });
+        if (int rc = check_launch("cl_dense_group_sum_cross_entropy_forward(layer)")) return rc;
+        return ce_from_tile_partials(dtype, part, batch, out_dim, k, h.tile_rows, tau, labels,
+                                     ignore_index, scores, ce_probs, loss, count, slices,
+                                     kHeadSlices, term, s);
+    });
+    return CL_OK;
+}
+
+extern "C" int cl_dense_group_sum_cross_entropy_backward(
+    int dtype, const void* x, const void* ce_probs, const int64_t* labels, int64_t ignore_index,
+    const void* grad_loss, const void* count, int64_t k, double tau, const int32_t* slot_rec,
+    const int32_t* inv_rec, const void* inv_coef, const uint8_t* gate_seq, const void* probs,
+    const int32_t* run_ptr, void* grad_w, void* grad_x, int64_t in_dim, int64_t out_dim,
+    int64_t num_runs, int64_t batch, int64_t num_gates, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+    clear_error();
+    CL_ARG(out_dim >= 1 && batch >= 1 && k >= 1, "bad shape");
+    CL_ARG(workspace, "null pointer argument");
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        HeadShape h;
+        CL_ARG(head_shape<T>(out_dim, batch, k, h), "the fused head does not apply to this shape");
+        CL_ARG(workspace_bytes >= k * batch * int64_t(sizeof(T)),
+               "workspace of %lld bytes needed", (long long)(k * batch * int64_t(sizeof(T))));
+        CL_ARG(aligned(workspace, 16), "workspace must be 16-byte aligned");
+        // class gradients, [k, batch]: grad_scores[n, c] / tau of the cross-entropy
+        if (int rc = cl_group_sum_cross_entropy_backward(dtype, ce_probs, labels, ignore_index,
+                                                         grad_loss, count, batch, k, k, tau,
+                                                         workspace, 1, batch, stream))
+            return rc;
+        const uint32_t magic =
+            h.gsz == 1 ? 0u : uint32_t(((uint64_t(1) << 32) + uint64_t(h.gsz) - 1) / uint64_t(h.gsz));
+        return backward_rows_impl(dtype, x, workspace, slot_rec, inv_rec, inv_coef, gate_seq,
+                                  probs, run_ptr, grad_w, grad_x, in_dim, out_dim, num_runs, batch,
+                                  num_gates, magic, stream);
+    });
+    return CL_OK;
 }
 
 extern "C" int cl_dense_backward_finalize(int dtype, const void* moments, int64_t nchunks,

@@ -353,7 +353,60 @@ __global__ __launch_bounds__(kCeThreads) void k_ce_mean(const T* __restrict__ te
     }
 }
 
+// ---- class sums of the classifier head's tile partials: block = (256 samples, class c,
+// slice s of the tiles overlapping class c).  A tile overlapping class c starts in class c
+// (slot 0) or in class c - 1 (slot 1): tiles are at most gsz rows.  Tiles in order.
+template <typename T>
+__global__ __launch_bounds__(256) void k_head_slices(const T* __restrict__ part, int64_t B,
+                                                     int64_t F, int64_t gsz, int64_t k,
+                                                     int64_t tile_rows, int64_t nslices,
+                                                     T* __restrict__ slices) {
+    const int64_t n = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (n >= B) return;
+    const int64_t c = blockIdx.y, sl = blockIdx.z;
+    const int64_t r0 = c * gsz, r1 = std::min<int64_t>((c + 1) * gsz, F);
+    T acc = T(0);
+    if (r0 < r1) {
+        const int64_t t0 = r0 / tile_rows, t1 = (r1 - 1) / tile_rows;
+        const int64_t per = (t1 - t0 + nslices) / nslices;  // ceil((t1 - t0 + 1) / nslices)
+        const int64_t a = t0 + sl * per, b = std::min<int64_t>(a + per, t1 + 1);
+        for (int64_t t = a; t < b; ++t) {
+            const int64_t slot = (t * tile_rows) / gsz == c ? 0 : 1;
+            acc += part[(t * 2 + slot) * B + n];
+        }
+    }
+    slices[(sl * k + c) * B + n] = acc;
+}
+
 }  // namespace
+
+int ce_from_tile_partials(int dtype, const void* part, int64_t batch, int64_t features,
+                          int64_t k, int64_t tile_rows, double tau, const int64_t* labels,
+                          int64_t ignore_index, void* out, void* probs, void* loss, void* count,
+                          void* slices, int64_t nslices, void* term, hipStream_t s) {
+    CL_ARG(batch >= 1 && features >= 1 && k >= 1 && tile_rows >= 1 && nslices >= 1,
+           "bad head shape");
+    CL_ARG(k * kCeSamples * 8 <= 64 * 1024, "k too large for the fused cross-entropy");
+    const int64_t gsz = ceil_div(features, k);
+    CL_ARG(tile_rows <= gsz, "tiles of %lld rows span more than two classes of %lld",
+           (long long)tile_rows, (long long)gsz);
+    CL_DTYPE_SWITCH(dtype, {
+        using T = scalar_t;
+        const dim3 grid(unsigned(ceil_div(batch, 256)), unsigned(k), unsigned(nslices));
+        k_head_slices<T><<<grid, 256, 0, s>>>(static_cast<const T*>(part), batch, features, gsz,
+                                              k, tile_rows, nslices, static_cast<T*>(slices));
+        if (int rc = check_launch("cl_dense_group_sum_cross_entropy_forward(sums)")) return rc;
+        k_ce_rows<T><<<unsigned(ceil_div(batch, kCeSamples)), kCeThreads,
+                       size_t(kCeSamples * k * sizeof(T)), s>>>(
+            static_cast<const T*>(slices), nslices, labels, batch, k, ignore_index, T(tau),
+            static_cast<T*>(out), static_cast<T*>(probs), static_cast<T*>(term));
+        if (int rc = check_launch("cl_dense_group_sum_cross_entropy_forward(rows)")) return rc;
+        k_ce_mean<T><<<1, kCeThreads, 0, s>>>(static_cast<const T*>(term), batch,
+                                              static_cast<T*>(loss), static_cast<T*>(count));
+    });
+    return check_launch("cl_dense_group_sum_cross_entropy_forward(mean)");
+}
+
 }  // namespace cl
 
 using namespace cl;

@@ -1143,3 +1143,135 @@ class GroupSum(torch.nn.Module):
 
     def extra_repr(self):
         return 'k={}, tau={}'.format(self.k, self.tau)
+
+
+class LogicGroupSumCrossEntropyFunction(torch.autograd.Function):
+    """The classifier head of a training step, fused: a dense LogicLayer's training forward,
+    GroupSum(k, tau) and the mean cross-entropy (cl_dense_group_sum_cross_entropy_forward /
+    _backward).  The same function as GroupSumCrossEntropyFunction applied to
+    LogicLayerRunsFunction's output, but the layer's output [out_dim, batch] and its gradient
+    are never stored: the forward sums each tile of outputs by class, the backward reads one
+    gradient row per class.  No counterpart in the reference (its training loops run the layer,
+    GroupSum and torch's cross_entropy in turn: compactlogic/compactlogic.py:83-118, :450-468).
+    Returns (loss, scores); the scores are not differentiable through this function."""
+
+    @staticmethod
+    def forward(ctx, x, w, gate_sequence, plan: RunPlan, softmax, labels, k, tau, ignore_index,
+                forward_bytes, backward_bytes):
+        _dl._check(x, "x")
+        batch = x.shape[1]
+        dev, code = x.device, _dl.dtype_code(x)
+        w = w.contiguous()
+        labels = labels.contiguous()
+        probs = torch.empty_like(w) if softmax else None
+        inv_coef = torch.empty((2 * plan.num_runs, 2), dtype=x.dtype, device=dev)
+        scores = torch.empty((batch, k), dtype=x.dtype, device=dev)
+        ce_probs = torch.empty((batch, k), dtype=x.dtype, device=dev)
+        loss = torch.empty((), dtype=x.dtype, device=dev)
+        count = torch.empty((), dtype=x.dtype, device=dev)
+        ws = torch.empty(forward_bytes, dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            timing.timed(f"cl_dense_group_sum_cross_entropy_forward[{plan.in_dim}->{plan.out_dim}]",
+                         lambda: _capi.call(
+                "cl_dense_group_sum_cross_entropy_forward", code, x.data_ptr(), w.data_ptr(),
+                int(softmax), gate_sequence.data_ptr(), plan.nab.data_ptr(),
+                plan.inv_pos.data_ptr(), _dl.ptr(probs), inv_coef.data_ptr(), plan.in_dim,
+                plan.out_dim, plan.num_runs, batch, plan.num_gates, k, float(tau),
+                labels.data_ptr(), int(ignore_index), scores.data_ptr(), ce_probs.data_ptr(),
+                loss.data_ptr(), count.data_ptr(), ws.data_ptr(), forward_bytes,
+                _dl.stream_of(x)))
+        ctx.save_for_backward(x, inv_coef, gate_sequence, probs, ce_probs, labels, count)
+        ctx.plan, ctx.k, ctx.tau, ctx.ignore_index = plan, k, tau, int(ignore_index)
+        ctx.backward_bytes = backward_bytes
+        ctx.mark_non_differentiable(scores)
+        ctx.set_materialize_grads(False)
+        return loss, scores
+
+    @staticmethod
+    def backward(ctx, grad_loss, _grad_scores):
+        if grad_loss is None:
+            return (None,) * 11
+        x, inv_coef, gate_sequence, probs, ce_probs, labels, count = ctx.saved_tensors
+        plan: RunPlan = ctx.plan
+        grad_loss = grad_loss.to(x.dtype).contiguous()
+        batch = x.shape[1]
+        grad_x = torch.empty_like(x)  # the row backward always writes it
+        grad_w = (torch.empty((plan.out_dim, plan.num_gates), dtype=x.dtype, device=x.device)
+                  if ctx.needs_input_grad[1] else None)
+        ws = torch.empty(ctx.backward_bytes, dtype=torch.uint8, device=x.device)
+        with torch.cuda.device(x.device):
+            timing.timed(f"cl_dense_group_sum_cross_entropy_backward[{plan.in_dim}->{plan.out_dim}]",
+                         lambda: _capi.call(
+                "cl_dense_group_sum_cross_entropy_backward", _dl.dtype_code(x), x.data_ptr(),
+                ce_probs.data_ptr(), labels.data_ptr(), ctx.ignore_index, grad_loss.data_ptr(),
+                count.data_ptr(), ctx.k, float(ctx.tau), plan.slot_rec.data_ptr(),
+                plan.inv_rec.data_ptr(), inv_coef.data_ptr(), gate_sequence.data_ptr(),
+                _dl.ptr(probs), plan.run_ptr.data_ptr(), _dl.ptr(grad_w), grad_x.data_ptr(),
+                plan.in_dim, plan.out_dim, plan.num_runs, batch, plan.num_gates, ws.data_ptr(),
+                ctx.backward_bytes, _dl.stream_of(x)))
+        return (grad_x if ctx.needs_input_grad[0] else None, grad_w) + (None,) * 9
+
+
+def _head_workspace(layer: LogicLayer, x: torch.Tensor, k: int):
+    """(forward, backward) workspace bytes of the fused classifier head for layer on x
+    ([batch, in_dim]), or None when it does not apply."""
+    if (type(layer) is not LogicLayer or not layer.training or getattr(layer, "is_frozen", False)
+            or isinstance(x, PackBitsTensor) or x.device.type != "cuda" or x.dim() != 2
+            or x.dtype not in (torch.float32, torch.float64) or layer.weights.dtype != x.dtype):
+        return None
+    # Not under HIP graph capture: a capture of the fused head ended the process in
+    # torch's capture_end (cause not established); captured steps take the composition.
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    batch = x.shape[0]
+    wide = 16 // x.element_size()
+    if batch == 0 or batch % wide or batch > 64 * wide * 8:
+        return None
+    plan = layer.run_plan()
+    if not plan.single_run or plan.num_gates > 16:
+        return None
+    fb, bb = ctypes.c_int64(), ctypes.c_int64()
+    _capi.call("cl_dense_group_sum_cross_entropy_workspace_size", _dl.dtype_code(x),
+               layer.out_dim, batch, int(k), ctypes.byref(fb), ctypes.byref(bb))
+    return None if fb.value < 0 else (fb.value, bb.value)
+
+
+def logic_group_sum_cross_entropy(layer: LogicLayer, group_sum: GroupSum, x, labels,
+                                  ignore_index: int = -100, return_scores: bool = False):
+    """group_sum.cross_entropy(layer(x), labels, ignore_index): the loss of a classifier whose
+    last dense layer is `layer`, with the layer's output never stored (the fused head,
+    LogicGroupSumCrossEntropyFunction).  Gradients flow to x and the layer's logits exactly as
+    through the composition (equal up to the rounding of the class sums).  Where the fused
+    head does not apply (a conv or frozen layer, eval mode, classes narrower than a forward
+    tile, batches outside the row backward's range, or under HIP graph capture) this is the
+    composition itself."""
+    ws = _head_workspace(layer, x, group_sum.k) if isinstance(x, torch.Tensor) else None
+    if ws is None:
+        return group_sum.cross_entropy(layer(x), labels, ignore_index, return_scores)
+    if labels.device != x.device or labels.dtype != torch.int64 or labels.shape != (x.shape[0],):
+        raise RuntimeError(f"labels must be int64 of shape ({x.shape[0]},) on {x.device}")
+    xr = to_rows(x)
+    assert xr.shape[0] == layer.in_dim, (xr.shape, layer.in_dim)
+    loss, scores = LogicGroupSumCrossEntropyFunction.apply(
+        xr, layer.weights, layer.gate_sequence, layer.run_plan(), True, labels, group_sum.k,
+        group_sum.tau, ignore_index, ws[0], ws[1])
+    return (loss, scores) if return_scores else loss
+
+
+def sequential_cross_entropy(model, x, labels, ignore_index: int = -100,
+                             return_scores: bool = False):
+    """cross_entropy(model(x), labels) for a Sequential ending in GroupSum, the training loss of
+    experiments/experiment_script.py:280-284; when the module before the GroupSum is a dense
+    LogicLayer, through the fused head (logic_group_sum_cross_entropy)."""
+    mods = list(model)
+    if not mods or not isinstance(mods[-1], GroupSum):
+        raise ValueError("the model must end with a GroupSum")
+    h = x
+    if len(mods) >= 2 and type(mods[-2]) is LogicLayer:
+        for m in mods[:-2]:
+            h = m(h)
+        return logic_group_sum_cross_entropy(mods[-2], mods[-1], h, labels, ignore_index,
+                                             return_scores)
+    for m in mods[:-1]:
+        h = m(h)
+    return mods[-1].cross_entropy(h, labels, ignore_index, return_scores)

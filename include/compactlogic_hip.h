@@ -404,6 +404,43 @@ int cl_group_sum_cross_entropy_backward(int dtype, const void* probs, const int6
                                         int64_t k, double tau, void* grad_x, int64_t stride_batch,
                                         int64_t stride_feature, void* stream);
 
+/* The classifier head of a training step: the last dense layer, GroupSum(k, tau) and the
+ * mean cross-entropy fused (no counterpart in the reference, whose training loops run the
+ * layer, GroupSum and torch's cross_entropy one after the other: compactlogic/compactlogic.py
+ * :83-118 and :450-468, experiments/experiment_script.py:280-293).  The layer's outputs and
+ * their gradient are never stored: the forward sums each tile's outputs by class, and the
+ * backward gives every row of a class its class's gradient.
+ * Workspace sizes for the forward and the backward; both -1 when the fused head does not
+ * apply (classes of fewer than 32 rows for fp32, or out_dim * ceil(out_dim / k) > 2^32). */
+int cl_dense_group_sum_cross_entropy_workspace_size(int dtype, int64_t out_dim, int64_t batch,
+                                                    int64_t k, int64_t* forward_bytes,
+                                                    int64_t* backward_bytes);
+
+/* Forward: the layer's arguments as cl_dense_forward_fused (inv_coef required: probs and
+ * inv_coef are written for the backward) without y, then GroupSum's cross-entropy arguments
+ * as cl_group_sum_cross_entropy_forward with the layer's output as x (features = out_dim):
+ * scores [batch, k], ce_probs [batch, k], loss and count device scalars.  The class sums add
+ * the layer's outputs in a fixed order (not that of cl_group_sum_forward): bitwise repeatable,
+ * equal to the unfused composition up to rounding. */
+int cl_dense_group_sum_cross_entropy_forward(
+    int dtype, const void* x, const void* w, int softmax, const uint8_t* gate_seq,
+    const int32_t* nab, const int32_t* inv_pos, void* probs, void* inv_coef, int64_t in_dim,
+    int64_t out_dim, int64_t num_runs, int64_t batch, int64_t num_gates, int64_t k, double tau,
+    const int64_t* labels, int64_t ignore_index, void* scores, void* ce_probs, void* loss,
+    void* count, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Backward: the cross-entropy's class gradients (cl_group_sum_cross_entropy_backward's values,
+ * into the workspace as [k, batch]) and the layer's input and logits gradients as
+ * cl_dense_backward_rows with grad_y row o / ceil(out_dim / k) for neuron o (same batch and
+ * slot limits). */
+int cl_dense_group_sum_cross_entropy_backward(
+    int dtype, const void* x, const void* ce_probs, const int64_t* labels, int64_t ignore_index,
+    const void* grad_loss, const void* count, int64_t k, double tau, const int32_t* slot_rec,
+    const int32_t* inv_rec, const void* inv_coef, const uint8_t* gate_seq, const void* probs,
+    const int32_t* run_ptr, void* grad_w, void* grad_x, int64_t in_dim, int64_t out_dim,
+    int64_t num_runs, int64_t batch, int64_t num_gates, void* workspace,
+    int64_t workspace_bytes, void* stream);
+
 /* -------------------------------------------------------------------------------------------
  * Optimizer step of a training iteration (experiments/experiment_script.py:280-293):
  * torch.nn.utils.clip_grad_norm_(params, max_norm) followed by torch.optim.Adam.step() (the
