@@ -7,7 +7,7 @@ conv blocks of the third-party ConvLogic package (ConvLogicLayer, TreeLogicLayer
 PoolLogicLayer).  All numerics run in libcompactlogic_hip.so, built in-tree by
 ``python -m compactlogic_amd.build``.
 """
-from . import convlogic_hip, difflogic_hip
+from . import checkpoint, circuit, convlogic_hip, difflogic_hip
 from .layers import (ConvLayer, ConvLayerCudaFunction, ConvLayerSoftmaxFunction,
                      ConvLayerWindowFunction, GroupSum, GroupSumCrossEntropyFunction,
                      GroupSumFunction, LogicGroupSumCrossEntropyFunction, LogicLayer,
@@ -29,5 +29,5 @@ __all__ = [
     "EntropyRowResampler", "PackedNetwork", "ConvLogicLayer", "TreeLogicLayer", "PoolLogicLayer",
     "ConvLogicFunction", "FullConvLogicFunction", "TreeLogicFunction", "FusedAdam",
     "LogicGroupSumCrossEntropyFunction", "logic_group_sum_cross_entropy",
-    "sequential_cross_entropy",
+    "sequential_cross_entropy", "checkpoint", "circuit",
 ]
