@@ -95,6 +95,9 @@ SIGNATURES: dict[str, list] = {
                                                   _i64, _i64, _i64, _p, _i64, _p],
     "cl_plan_locality_order": [ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i64, _i64,
                                ctypes.POINTER(_i32)],
+    "cl_packed_bank_layout": [ctypes.POINTER(_i32), ctypes.POINTER(_i32),
+                              ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i64, _i64,
+                              ctypes.POINTER(_i32)],
     "cl_adam_clip_max_tensors": [ctypes.POINTER(_i64)],
     "cl_adam_clip_workspace": [_i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
     "cl_adam_clip_step": [_int, _i64, _p, _p, _p, _p, ctypes.POINTER(_i64), _p, _f64, _f64,

@@ -25,86 +25,53 @@ def _limits():
     return nl.value, rows.value
 
 
-# LDS geometry of gfx950 as the fused kernel uses it: rows are 32-bit words, bank = word % 64,
-# and a read instruction is served 32 lanes at a time; the lanes of one half-wave read the
-# rows of 32 consecutive positions of the layer being computed.
-_LDS_BANKS = 64
+# LDS geometry of gfx950 as the fused kernel uses it (measured with 64-lane ds_read_b32
+# patterns and SQ_LDS_BANK_CONFLICT): a read instruction is served one half-wave (32 lanes) at
+# a time, and the lanes of a half-wave conflict when their words share word % 32.  The lanes of
+# one half-wave read the rows of 32 consecutive positions of the layer being computed.
+_LDS_BANKS = 32
 _HALF_WAVE = 32
 
 
-def bank_aware_positions(pos_a: np.ndarray, pos_b: np.ndarray, rows: int) -> np.ndarray:
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _layout(ka, kb, fa, fb, rows: int, class_size: int) -> np.ndarray:
+    P = ctypes.POINTER(ctypes.c_int32)
+    ka, kb = _i32(ka), _i32(kb)
+    pos = np.empty(int(rows), dtype=np.int32)
+    fa_ = None if fa is None else _i32(fa)
+    fb_ = None if fb is None else _i32(fb)
+    _capi.call("cl_packed_bank_layout", ka.ctypes.data_as(P), kb.ctypes.data_as(P),
+               None if fa_ is None else fa_.ctypes.data_as(P),
+               None if fb_ is None else fb_.ctypes.data_as(P), int(rows), int(class_size),
+               pos.ctypes.data_as(P))
+    return pos.astype(np.int64)
+
+
+def bank_aware_positions(pos_a: np.ndarray, pos_b: np.ndarray, rows: int,
+                         fan_a: np.ndarray | None = None,
+                         fan_b: np.ndarray | None = None) -> np.ndarray:
     """Positions (LDS words, a permutation of 0..rows-1) for the gates of one layer whose
-    inputs sit at words pos_a / pos_b of the previous layer, chosen so that the gates of each
-    block of 32 consecutive positions (one half-wave of the kernel's row reads) read their a
-    rows from 32 distinct banks and their b rows from 32 distinct banks.  The gate-to-position
-    assignment is free because the next layer addresses rows through the tables; a greedy
-    first fit (gates in a fixed order, blocks in order) colours the (bank a, bank b) multigraph
-    with blocks.  A gate that fits no block conflict-free goes to the open block with the
-    fewest clashes.  Deterministic."""
-    n = int(rows)
-    blocks = (n + _HALF_WAVE - 1) // _HALF_WAVE
-    cap = np.full(blocks, _HALF_WAVE, dtype=np.int64)
-    cap[-1] = n - (blocks - 1) * _HALF_WAVE
-    fill = np.zeros(blocks, dtype=np.int64)
-    used_a = np.zeros((_LDS_BANKS, blocks), dtype=bool)
-    used_b = np.zeros((_LDS_BANKS, blocks), dtype=bool)
-    ka = (np.asarray(pos_a) % _LDS_BANKS).astype(np.int64)
-    kb = (np.asarray(pos_b) % _LDS_BANKS).astype(np.int64)
-    pos = np.empty(n, dtype=np.int64)
-    open_ = np.ones(blocks, dtype=bool)
-    for o in range(n):
-        ok = open_ & ~used_a[ka[o]] & ~used_b[kb[o]]
-        blk = int(ok.argmax())
-        if not ok[blk]:
-            clash = used_a[ka[o]].astype(np.int64) + used_b[kb[o]]
-            clash[~open_] = 3
-            blk = int(clash.argmin())
-        used_a[ka[o], blk] = True
-        used_b[kb[o], blk] = True
-        pos[o] = blk * _HALF_WAVE + fill[blk]
-        fill[blk] += 1
-        if fill[blk] == cap[blk]:
-            open_[blk] = False
-    return pos
+    inputs sit at words pos_a / pos_b of the previous layer (cl_packed_bank_layout): blocks of
+    32 consecutive positions (one half-wave of the kernel's row reads) that read their a rows
+    from 32 distinct banks and their b rows from 32 distinct banks, from an edge colouring of
+    the (bank a, bank b) multigraph with one colour per block.  Inside a block the position is
+    free for this layer; with the next layer's fan-outs of these rows (fan_a: reads as operand
+    a, fan_b: as operand b) it is chosen to level the next layer's bank degrees, which is what
+    lets that layer's colouring avoid conflicts.  Deterministic."""
+    return _layout(np.asarray(pos_a) % _LDS_BANKS, np.asarray(pos_b) % _LDS_BANKS, fan_a, fan_b,
+                   rows, 0)
 
 
 def bank_aware_positions_grouped(pos_a: np.ndarray, pos_b: np.ndarray, rows: int,
                                  group_size: int) -> np.ndarray:
     """bank_aware_positions for the last layer, whose rows must stay in their class: gate o
-    (class o // group_size) is placed inside [class * group_size, (class + 1) * group_size),
-    in the first block overlapping that range that has a free position there and both banks
-    free (else the one with the fewest clashes).  Deterministic."""
-    n, gsz = int(rows), int(group_size)
-    blocks = (n + _HALF_WAVE - 1) // _HALF_WAVE
-    used_a = np.zeros((_LDS_BANKS, blocks), dtype=bool)
-    used_b = np.zeros((_LDS_BANKS, blocks), dtype=bool)
-    ka = (np.asarray(pos_a) % _LDS_BANKS).astype(np.int64)
-    kb = (np.asarray(pos_b) % _LDS_BANKS).astype(np.int64)
-    taken = np.zeros(n, dtype=bool)
-    pos = np.empty(n, dtype=np.int64)
-    for c in range(n // gsz):
-        lo, hi = c * gsz, (c + 1) * gsz
-        blks = np.arange(lo // _HALF_WAVE, (hi - 1) // _HALF_WAVE + 1)
-        # free positions of the class inside each of its blocks
-        first = np.maximum(blks * _HALF_WAVE, lo)
-        last = np.minimum(blks * _HALF_WAVE + _HALF_WAVE, hi)
-        room = last - first
-        for o in range(lo, hi):
-            open_ = room > 0
-            ok = open_ & ~used_a[ka[o], blks] & ~used_b[kb[o], blks]
-            i = int(ok.argmax())
-            if not ok[i]:
-                clash = used_a[ka[o], blks].astype(np.int64) + used_b[kb[o], blks]
-                clash[~open_] = 3
-                i = int(clash.argmin())
-            blk = int(blks[i])
-            used_a[ka[o], blk] = True
-            used_b[kb[o], blk] = True
-            p = int(first[i]) + int(np.argmin(taken[first[i]:last[i]]))
-            taken[p] = True
-            pos[o] = p
-            room[i] -= 1
-    return pos
+    (class o // group_size) is placed inside [class * group_size, (class + 1) * group_size).
+    Deterministic."""
+    return _layout(np.asarray(pos_a) % _LDS_BANKS, np.asarray(pos_b) % _LDS_BANKS, None, None,
+                   rows, group_size)
 
 
 class PackedNetwork:
@@ -142,8 +109,8 @@ class PackedNetwork:
                              "but it is not")
         entries = []
         with torch.no_grad():
-            prev_pos = np.arange(self.rows[0], dtype=np.int64)   # input rows stay in place
-            for i, m in enumerate(layers):
+            wiring = []
+            for m in layers:
                 w = getattr(m, "w", None)
                 if w is None:
                     w = m.weights.argmax(-1)
@@ -154,17 +121,22 @@ class PackedNetwork:
                 if int(a.min()) < 0 or int(a.max()) >= m.in_dim or int(b.min()) < 0 or \
                         int(b.max()) >= m.in_dim:
                     raise IndexError("connection indices out of range")
-                pa = prev_pos[a.cpu().numpy()]
-                pb = prev_pos[b.cpu().numpy()]
+                wiring.append((a.cpu().numpy(), b.cpu().numpy(), g.cpu().numpy(), a.device))
+            prev_pos = np.arange(self.rows[0], dtype=np.int64)   # input rows stay in place
+            for i, (m, (a, b, g, dev)) in enumerate(zip(layers, wiring)):
+                pa, pb = prev_pos[a], prev_pos[b]
                 if not bank_aware:
                     pos = np.arange(m.out_dim, dtype=np.int64)
                 elif i + 1 < len(layers):
-                    pos = bank_aware_positions(pa, pb, m.out_dim)
+                    na, nb = wiring[i + 1][:2]
+                    pos = bank_aware_positions(pa, pb, m.out_dim,
+                                               np.bincount(na, minlength=m.out_dim),
+                                               np.bincount(nb, minlength=m.out_dim))
                 else:  # class groups stay contiguous
                     pos = bank_aware_positions_grouped(pa, pb, m.out_dim, m.out_dim // self.k)
                 ent = np.empty(m.out_dim, dtype=np.int64)
-                ent[pos] = (pa * 4) | ((pb * 4) << 20) | (g.cpu().numpy() << 40)
-                entries.append(torch.as_tensor(ent, device=a.device))
+                ent[pos] = (pa * 4) | ((pb * 4) << 20) | (g << 40)
+                entries.append(torch.as_tensor(ent, device=dev))
                 prev_pos = pos
         self.tables = torch.cat(entries).contiguous()
         self.device = self.tables.device

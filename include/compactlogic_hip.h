@@ -120,6 +120,19 @@ int cl_dense_eval(int dtype, const void* x, const int64_t* a, const int64_t* b,
 int cl_plan_locality_order(const int32_t* ra, const int32_t* rb, int64_t num_runs,
                            int64_t in_dim, int32_t* order);
 
+/* Host function (no device work; all pointers are host pointers).  LDS positions of one
+ * layer's gates for cl_packed_network: gate o reads rows in LDS banks ka[o] and kb[o] (word %
+ * 32, the banks a half-wave's 32 lanes conflict on); pos (int32 [n]) is a permutation of
+ * 0..n-1 such that the blocks of 32 consecutive positions read distinct banks where the bank
+ * degrees allow (an edge colouring of the bank multigraph, one colour per block, then swaps
+ * that lower the remaining conflicts).  fa / fb (int32 [n], both NULL or both given): the
+ * next layer's reads of each gate's row as operand a / b; inside a block the positions are
+ * then assigned so that the next layer's bank degrees are level.  class_size > 0 keeps gate
+ * o within positions [c * class_size, (c + 1) * class_size), c = o / class_size (the last
+ * layer, read by class).  No reference counterpart (the fused network is this build's). */
+int cl_packed_bank_layout(const int32_t* ka, const int32_t* kb, const int32_t* fa,
+                          const int32_t* fb, int64_t n, int64_t class_size, int32_t* pos);
+
 /* Probabilities (softmax of w over the slots when `softmax` is non-zero, else w itself;
  * written to `probs` when not NULL) and the run coefficients K (run_coef, 16-byte aligned).
  * With inv_coef (T [2 * num_runs, 2], may be NULL) the coefficients of every inverse-index

@@ -422,11 +422,22 @@ def test_run_plan_tiles(in_dim, out_dim, g_n, seed):
         assert int(inv_slot[inv_pos[2 * r]]) == -1 and int(inv_slot[inv_pos[2 * r + 1]]) == -1
 
 
+def _clashes(p, pa, pb, banks=32):
+    """Extra LDS cycles of a layout: per block of 32 positions, reads beyond one per bank."""
+    n = 0
+    for blk in range(int(p.max()) // 32 + 1):
+        m = p // 32 == blk
+        for k in (pa[m] % banks, pb[m] % banks):
+            n += len(k) - len(set(k.tolist()))
+    return n
+
+
 @pytest.mark.parametrize("rows,seed", [(12000, 0), (1000, 1), (47, 2), (32, 3)])
 def test_bank_aware_positions(rows, seed):
     """The fused packed layout is a permutation of the layer's rows whose blocks of 32
     consecutive positions read their a rows and their b rows from distinct LDS banks (word %
-    64) far more often than the identity layout does."""
+    32, per half-wave) more often than the identity layout; when every bank is read equally
+    often (a regular multigraph) the colouring is conflict-free."""
     from compactlogic_amd.packed_net import bank_aware_positions
     rng = np.random.default_rng(seed)
     pa = rng.integers(0, 5 * rows, rows)
@@ -434,19 +445,32 @@ def test_bank_aware_positions(rows, seed):
     pb[::5] = pa[::5]
     pos = bank_aware_positions(pa, pb, rows)
     assert sorted(pos.tolist()) == list(range(rows))
+    assert _clashes(pos, pa, pb) <= _clashes(np.arange(rows), pa, pb)
+    if rows % 32 == 0:
+        ra = rng.permutation(np.arange(rows) % 32) + 32 * rng.integers(0, 100, rows)
+        rb = rng.permutation(np.arange(rows) % 32) + 32 * rng.integers(0, 100, rows)
+        pos = bank_aware_positions(ra, rb, rows)
+        assert sorted(pos.tolist()) == list(range(rows))
+        assert _clashes(pos, ra, rb) == 0
 
-    def clashes(p):
-        n = 0
-        for blk in range(int(p.max()) // 32 + 1):
-            m = p // 32 == blk
-            for k in (pa[m] % 64, pb[m] % 64):
-                n += len(k) - len(set(k.tolist()))
-        return n
 
-    # few blocks leave the placement little choice; with many it removes nearly all clashes
-    assert clashes(pos) <= clashes(np.arange(rows))
-    if rows >= 1000:
-        assert clashes(np.arange(rows)) > 10 * max(1, clashes(pos))
+def test_bank_aware_chain_levels_the_next_layer():
+    """With the next layer's fan-outs, positions inside each block level that layer's bank
+    degrees, and its own layout is then nearly conflict-free."""
+    from compactlogic_amd.packed_net import bank_aware_positions
+    rng = np.random.default_rng(7)
+    n = 12000
+    a1, b1 = rng.integers(0, 784, n), rng.integers(0, 784, n)   # layer 1 reads the inputs
+    a2, b2 = rng.integers(0, n, n), rng.integers(0, n, n)       # layer 2 reads layer 1
+    plain = bank_aware_positions(a1, b1, n)
+    level = bank_aware_positions(a1, b1, n, np.bincount(a2, minlength=n),
+                                 np.bincount(b2, minlength=n))
+    assert _clashes(plain, a1, b1) == _clashes(level, a1, b1)  # same blocks for layer 1
+    deg = lambda p, idx: np.bincount(p[idx] % 32, minlength=32).max()
+    assert deg(level, a2) < deg(plain, a2) and deg(level, b2) < deg(plain, b2)
+    c_plain = _clashes(bank_aware_positions(plain[a2], plain[b2], n), plain[a2], plain[b2])
+    c_level = _clashes(bank_aware_positions(level[a2], level[b2], n), level[a2], level[b2])
+    assert c_level * 4 < c_plain and c_level < 0.1 * 2 * (n // 32)
 
 
 @pytest.mark.parametrize("rows,k", [(12000, 10), (1500, 10), (96, 3), (100, 4)])
@@ -463,17 +487,14 @@ def test_bank_aware_positions_grouped(rows, k):
     assert all(o // gs == p // gs for o, p in enumerate(pos.tolist()))
 
     def clashes(p):
-        n = 0
-        for blk in range(int(p.max()) // 32 + 1):
-            m = p // 32 == blk
-            for kk in (pa[m] % 64, pb[m] % 64):
-                n += len(kk) - len(set(kk.tolist()))
-        return n
+        return _clashes(p, pa, pb)
 
     # a class spans few blocks, so the choice is narrower than for hidden layers
     assert clashes(pos) <= clashes(np.arange(rows))
-    if rows >= 1000:
+    if gs >= 1000:
         assert clashes(np.arange(rows)) > 3 * max(1, clashes(pos))
+    elif rows >= 1000:
+        assert clashes(np.arange(rows)) > 1.5 * max(1, clashes(pos))
 
 
 def test_conv_packed_order_groups_channels_by_input():
