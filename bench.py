@@ -22,7 +22,8 @@ Also reported on the same JSON line:
   packed_conv   cfg5: the cfg3 network with 4 candidate gates per row, frozen, 2^20
                 bit-packed samples
   packed_conv_tree  the cfg3_tree network frozen to argmax gates (pool = OR), 2^20 bit-packed
-                samples
+                samples; its "fused" member runs the two dense layers and the counts in one
+                launch after the conv blocks
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10]
 """
@@ -476,9 +477,10 @@ def bench_packed_net(model, in_features: int, log2n: int, passes: int, k: int, t
 
 
 def bench_packed_fused(model, in_features: int, log2n: int, passes: int, checksum: int, torch):
-    """The same network through PackedNetwork (all layers and the popcount GroupSum in one
-    launch, activations in LDS).  Compulsory HBM bytes of the fused pass: the packed input and
-    the int32 counts."""
+    """The same network through PackedNetwork: its dense tail and the popcount GroupSum in one
+    launch (activations in LDS), after the modules before the tail (conv blocks) layer by layer
+    on the packed kernels.  Compulsory HBM bytes of a pass with no such prefix: the packed
+    input and the int32 counts."""
     import compactlogic_amd as cl
     from compactlogic_amd import configs
     n = 1 << log2n
@@ -497,16 +499,21 @@ def bench_packed_fused(model, in_features: int, log2n: int, passes: int, checksu
         times.append(a.elapsed_time(b) * 1e-3)
     dt = min(times)
     same = int(counts.to(torch.int64).sum().item()) == checksum
-    fused_bytes = in_features // 8 + 4 * model[-1].k
-    del xw, counts
+    fused_rows = net.rows or []
+    prefix = len(net.prefix)
+    del xw, counts, net
     torch.cuda.empty_cache()
-    return {"workload": "the same network and inputs through PackedNetwork: one launch, "
-                        "32-sample columns held in LDS through all layers",
-            "value": round(n / dt / 1e9, 4), "unit": "Gsamples/s", "ms_per_pass": round(dt * 1e3, 3),
-            "counts_match_layerwise": same,
-            "fused_compulsory_bytes_per_sample": fused_bytes,
-            "hbm_frac_of_fused_bytes": round(fused_bytes * n / dt / 1e9 / HBM_PEAK_GBS, 4),
-            "speedup_vs_layerwise": None}
+    out = {"workload": ("the same network and inputs through PackedNetwork: "
+                        + (f"{prefix} modules layer by layer, then " if prefix else "")
+                        + f"the dense layers {fused_rows} and the class counts in one launch, "
+                          "32-sample columns held in LDS through all fused layers"),
+           "value": round(n / dt / 1e9, 4), "unit": "Gsamples/s", "ms_per_pass": round(dt * 1e3, 3),
+           "counts_match_layerwise": same, "speedup_vs_layerwise": None}
+    if not prefix:
+        fused_bytes = in_features // 8 + 4 * model[-1].k
+        out["fused_compulsory_bytes_per_sample"] = fused_bytes
+        out["hbm_frac_of_fused_bytes"] = round(fused_bytes * n / dt / 1e9 / HBM_PEAK_GBS, 4)
+    return out
 
 
 def packed_json(pk: dict, workload: str, bytes_per_sample: int) -> dict:
@@ -723,7 +730,16 @@ def main():
                                  f"2^{args.conv_packed_log2_samples} samples bit-packed 64 per "
                                  "word, 2 packed ConvLogic blocks + 2 dense layers + popcount "
                                  "GroupSum", CFG5_TREE_BYTES_PER_SAMPLE)
-            log(f"packed cfg3_tree: {pt['value']} Gsamples/s")
+            model = configs.tree_network(ct, device=torch.device("cuda:0"))
+            configs.freeze_argmax(model)
+            ft = bench_packed_fused(model, ct.in_shape[0] * ct.in_shape[1] * ct.in_shape[2],
+                                    args.conv_packed_log2_samples, args.packed_passes,
+                                    pt["counts_checksum"], torch)
+            del model
+            ft["speedup_vs_layerwise"] = round(ft["value"] / pt["value"], 2)
+            pt["fused"] = ft
+            log(f"packed cfg3_tree: {pt['value']} Gsamples/s layer by layer, "
+                f"{ft['value']} Gsamples/s with the dense tail fused")
             if not args.no_cpu_baseline:
                 log("cpu baseline (packed cfg3_tree)")
                 pt["cpu_baseline"] = cpu_baseline_packed(torch, "cfg3_tree")

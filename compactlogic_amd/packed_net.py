@@ -74,36 +74,60 @@ def bank_aware_positions_grouped(pos_a: np.ndarray, pos_b: np.ndarray, rows: int
                    rows, group_size)
 
 
-class PackedNetwork:
-    """Fused packed evaluator of `model`: LogicLayers (frozen or in eval mode; each neuron uses
-    its argmax slot `w`) followed by a GroupSum.  Call it with a PackBitsTensor of the first
-    layer's input (or its [features, words] tensor) to get int32 class counts [samples, k].
+# the fused kernel stages each 32-sample column of its input in LDS: at most _LDS_INPUT_ROWS
+# input rows (four per thread).  Gathering one word of every input row per column from a wider
+# input is bound by L2 capacity (the rows' lines of 32 columns must stay resident), and a
+# kernel that did so measured 3.7-7x slower than the layer path.
+_LDS_INPUT_ROWS = 4096
 
-    Widths are limited by LDS: every layer at most cl_packed_network_limits()'s row count.  The
-    gate tables are built once here; rebuild after changing the model.  With `bank_aware`
-    (default), each hidden layer's rows are laid out in LDS by bank_aware_positions, so that
-    the row reads of the kernel's half-waves hit distinct LDS banks; the counts do not depend
-    on the layout.
+
+def _fusable(in_rows: int, outs: list, max_layers: int, max_rows: int) -> bool:
+    """Whether cl_packed_network takes dense layers of widths `outs` on `in_rows` inputs."""
+    return (bool(outs) and len(outs) <= max_layers and in_rows <= _LDS_INPUT_ROWS
+            and max(outs) <= max_rows)
+
+
+class PackedNetwork:
+    """Fused packed evaluator of `model` (frozen or in eval mode; each neuron uses its argmax
+    slot `w`), ending in a GroupSum.  Call it with a PackBitsTensor of the network's input (or
+    its [features, words] tensor) to get int32 class counts [samples, k].
+
+    The longest tail of dense LogicLayers that the fused kernel takes (an input of at most
+    4096 rows, widths within LDS) runs in one launch with every 32-sample column held in LDS;
+    the modules before it (ConvLayers, ConvLogicLayers, wider dense layers, Flatten) run layer
+    by layer on the packed kernels first.  When no tail qualifies every module runs layer by
+    layer and the counts come from the group popcount.  The gate tables are built once here;
+    rebuild after changing the model.  With `bank_aware` (default), each fused layer's rows
+    are laid out in LDS by bank_aware_positions, so that the row reads of the kernel's
+    half-waves hit distinct LDS banks; the counts do not depend on the layout.
     """
 
     def __init__(self, model, bank_aware: bool = True):
         mods = list(model)
         if not mods or not isinstance(mods[-1], GroupSum):
             raise ValueError("the network must end with a GroupSum")
-        layers = mods[:-1]
-        if not layers or not all(isinstance(m, LogicLayer) and not isinstance(m, ConvLayer)
-                                 for m in layers):
-            raise ValueError("the fused packed pass takes dense LogicLayers followed by GroupSum")
+        body = mods[:-1]
+        if not body:
+            raise ValueError("the network needs a layer before its GroupSum")
         max_layers, max_rows = _limits()
-        if len(layers) > max_layers:
-            raise ValueError(f"at most {max_layers} layers")
         self.k = int(mods[-1].k)
+        # the fused tail: the longest run of trailing dense layers that the kernel takes
+        first = len(body)
+        while first > 0 and type(body[first - 1]) is LogicLayer:
+            first -= 1
+        start = next((j for j in range(first, len(body))
+                      if _fusable(int(body[j].in_dim), [int(m.out_dim) for m in body[j:]],
+                                  max_layers, max_rows)), len(body))
+        layers = body[start:]
+        self.prefix = body[:start]
+        if not layers:
+            self.rows = None            # no fused tail: layer by layer, then the popcount
+            self.device = None
+            return
         self.rows = [int(layers[0].in_dim)] + [int(m.out_dim) for m in layers]
         for i, (prev, m) in enumerate(zip(self.rows[:-1], layers)):
             if m.in_dim != prev:
                 raise ValueError(f"layer {i} expects {m.in_dim} inputs, gets {prev}")
-        if max(self.rows) > max_rows:
-            raise ValueError(f"layer widths must be at most {max_rows} for the fused pass")
         if self.rows[-1] % self.k:
             raise ValueError(f"in_dim ({self.rows[-1]}) has to be divisible by k ({self.k}) "
                              "but it is not")
@@ -135,7 +159,7 @@ class PackedNetwork:
                 else:  # class groups stay contiguous
                     pos = bank_aware_positions_grouped(pa, pb, m.out_dim, m.out_dim // self.k)
                 ent = np.empty(m.out_dim, dtype=np.int64)
-                ent[pos] = (pa * 4) | ((pb * 4) << 20) | (g << 40)
+                ent[pos] = (pa * 4) | ((pb * 4) << 20) | (g << 40)   # LDS byte offsets
                 entries.append(torch.as_tensor(ent, device=dev))
                 prev_pos = pos
         self.tables = torch.cat(entries).contiguous()
@@ -143,6 +167,17 @@ class PackedNetwork:
         self._rows_host = (ctypes.c_int64 * len(self.rows))(*self.rows)
 
     def __call__(self, x) -> torch.Tensor:
+        if self.prefix:
+            if isinstance(x, PackBitsTensor):
+                h = PackBitsTensor.from_packed(x.t, x.pad_len)   # the caller's object stays
+            else:
+                h = PackBitsTensor.from_packed(x)
+            with torch.no_grad():
+                for m in self.prefix:
+                    h = m(h)
+            if self.rows is None:
+                return h.group_sum(self.k)
+            x = h
         if isinstance(x, PackBitsTensor):
             words, n = x.t, x.num_samples
         else:

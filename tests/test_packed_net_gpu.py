@@ -60,6 +60,62 @@ def test_packed_network_matches_oracle_and_layerwise(device, dims, k, g_n, n):
     assert torch.equal(counts, layerwise)
 
 
+def conv_oracle_counts(model, words_np, n):
+    """The C oracle through a network of ConvLayers, Flatten and LogicLayers."""
+    layers = []
+    for m in model:
+        if isinstance(m, cl.ConvLayer):
+            layers.append(P.resolve_conv_slots(np_(m.offsets_ch), np_(m.offsets_h),
+                                               np_(m.offsets_w), np_(m.gate_sequence), np_(m.w),
+                                               m.in_shape, m.stride, m.out_shape[1:]))
+        elif isinstance(m, cl.LogicLayer):
+            layers.append(P.resolve_slots(np_(m.indices), np_(m.gate_sequence), np_(m.w)))
+    pad = words_np.shape[1] * 64 - n
+    return P.network_counts(words_np, layers, model[-1].k, pad)
+
+
+def test_packed_network_cfg5_runs_layer_by_layer(device):
+    """cfg5's first dense layer reads 25088 rows, more than the fused kernel stages in LDS: no
+    tail is fused and every module runs on the packed kernels, then the group popcount."""
+    cfg = configs.CONV_CONFIGS["cfg5"]
+    model = configs.conv_network(cfg, device=device)
+    configs.freeze_argmax(model)
+    feats = int(np.prod(cfg.in_shape))
+    xw = configs.packed_input_words(feats, 64, device=device)            # 2^12 samples
+    net = cl.PackedNetwork(model)
+    assert net.rows is None and len(net.prefix) == len(model) - 1
+    x = cl.PackBitsTensor.from_packed(xw)
+    counts = net(x)
+    assert x.t is xw                                                     # input untouched
+    ref = conv_oracle_counts(model, np_(xw).view(np.uint64), 1 << 12)
+    assert np.array_equal(np_(counts), ref)
+    assert torch.equal(counts, model(cl.PackBitsTensor.from_packed(xw.clone())))
+
+
+def test_packed_network_cfg3_tree_fuses_the_dense_tail(device):
+    """cfg3_tree: two ConvLogicLayer blocks layer by layer, then 2048 -> 16000 -> 16000 and
+    the class counts in one launch; equal to the whole network layer by layer."""
+    cfg = configs.TREE_CONFIGS["cfg3_tree"]
+    model = configs.tree_network(cfg, device=device)
+    configs.freeze_argmax(model)
+    feats = int(np.prod(cfg.in_shape))
+    xw = configs.packed_input_words(feats, 64, device=device)            # 2^12 samples
+    net = cl.PackedNetwork(model)
+    assert len(net.prefix) == 3 and net.rows == [2048, 16000, 16000]
+    counts = net(cl.PackBitsTensor.from_packed(xw))
+    layerwise = model(cl.PackBitsTensor.from_packed(xw.clone()))
+    assert torch.equal(counts, layerwise)
+    # the fused tail alone against the C oracle, on the blocks' packed output
+    with torch.no_grad():
+        h = cl.PackBitsTensor.from_packed(xw.clone())
+        for m in net.prefix:
+            h = m(h)
+    dense = torch.nn.Sequential(*list(model)[3:])
+    hw = np_(h.t).view(np.uint64)
+    ref = oracle_counts(dense, hw, 1 << 12)
+    assert np.array_equal(np_(counts), ref)
+
+
 def test_packed_network_cfg4_slice(device):
     cfg = configs.CONFIGS["cfg2"]
     model = configs.dense_network(cfg, device=device)
@@ -84,8 +140,10 @@ def test_packed_network_word_widths_and_errors(device):
     with pytest.raises(ValueError):
         cl.PackedNetwork(bad)                                           # 20 % 3 != 0
     wide = frozen_net([(30, 30000)], 10, 2, 2, device)
-    with pytest.raises(ValueError):
-        cl.PackedNetwork(wide)                                          # too wide for LDS
+    net = cl.PackedNetwork(wide)                                        # too wide for LDS
+    assert net.rows is None
+    x = cl.PackBitsTensor(torch.as_tensor(bits, device=device), 64)
+    assert torch.equal(net(x), wide(cl.PackBitsTensor.from_packed(x.t.clone(), x.pad_len)))
     with pytest.raises(RuntimeError):
         cl.PackedNetwork(model)(torch.zeros((31, 4), dtype=torch.int64, device=device))
 
