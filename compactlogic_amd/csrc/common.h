@@ -55,6 +55,27 @@ inline bool aligned(const void* p, size_t bytes) {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Division of x < 2^31 by a fixed d >= 1 as a multiply and a shift (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994, round-up method at N = 31):
+// with l = ceil(log2 d) and m = ceil(2^(31 + l) / d), which is below 2^32, floor(x / d) =
+// floor(x * m / 2^(31 + l)) for every x < 2^31, since m * d - 2^(31 + l) < d <= 2^l.
+struct FastDiv {
+    uint32_t m;
+    uint32_t s;
+    uint32_t d;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((uint64_t(1) << l) < d) ++l;
+    const uint64_t num = uint64_t(1) << (31 + l);
+    return FastDiv{uint32_t((num + d - 1) / d), 31 + l, d};
+}
+
+__device__ __host__ __forceinline__ uint32_t fast_div(uint32_t x, const FastDiv& f) {
+    return uint32_t((uint64_t(x) * f.m) >> f.s);
+}
+
 // ---------------------------------------------------------------- gate algebra
 //
 // Opcode g in 0..15 stores its truth table in its four bits, MSB first over the input

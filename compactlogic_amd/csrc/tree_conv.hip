@@ -43,6 +43,7 @@ struct TreeDims {
     int n, cin, h, w, cout, ho, wo, sh, sw, ph, pw;
     int complete;
     int P;  // items per (sample, channel): pooled windows (complete) or conv positions
+    FastDiv div_p, div_wp;  // by P, and by the windows per pooled row (complete) or wo
 };
 
 // Decoded tap: channel, row and column offset relative to the output position (pad removed).
@@ -123,6 +124,30 @@ __device__ __forceinline__ void eval_at(const T* __restrict__ xn, const TreeDims
     }
 }
 
+// One item of the conv-gates-only form with global taps: (sample, conv position) of channel c.
+template <typename T>
+__device__ __forceinline__ void fwd_gates_item(const T* __restrict__ x, const TreeDims& d,
+                                               const TapOff* st, T (*sk)[4], bool bad, int c,
+                                               int64_t item, T* __restrict__ y) {
+    const int64_t total = int64_t(d.n) * d.P;
+    if (item >= total) return;
+    int n, p;
+    if (total < (int64_t(1) << 31)) {  // uniform: 32-bit multiply-shift division
+        n = int(fast_div(uint32_t(item), d.div_p));
+        p = int(item) - n * d.P;
+    } else {
+        n = int(item / d.P);
+        p = int(item % d.P);
+    }
+    const int oy = int(fast_div(uint32_t(p), d.div_wp));
+    const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
+    Eval<T, false> e;
+    eval_at<T, false>(xn, d, st, sk, oy, p - oy * d.wo, e);
+    const int64_t pos = (int64_t(n) * d.cout + c) * d.P + p;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? quiet_nan<T>() : e.g[q];
+}
+
 // ------------------------------------------------------------------------------------------
 // Forward of the conv gates alone: one thread per (sample, conv position) of the workgroup's
 // channel (blockIdx.y); y [N, C, Ho, Wo, 4].
@@ -139,49 +164,36 @@ __global__ __launch_bounds__(256) void k_tree_fwd(const T* __restrict__ x, const
     load_channel(w_prob, sel, c, 4, d, sk, st, &bad);
     __syncthreads();
     const int64_t item = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (item >= int64_t(d.n) * d.P) return;
-    const int n = int(item / d.P), p = int(item % d.P);
-    const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
-    Eval<T, false> e;
-    eval_at<T, false>(xn, d, st, sk, p / d.wo, p % d.wo, e);
-    const int64_t pos = (int64_t(n) * d.cout + c) * d.P + p;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) y[pos * 4 + q] = bad ? quiet_nan<T>() : e.g[q];
+    fwd_gates_item(x, d, st, sk, bad != 0, c, item, y);
 }
 
 constexpr int kFwdItems = 8;  // passes of 256 items per forward workgroup
 
-// Complete block, quad form: one thread per conv position, the four positions of a pooling
-// window in the four lanes of a quad (lane order (0,0), (0,1), (1,0), (1,1)), so each thread
-// gathers 8 taps instead of 32 and the pool is two quad-DPP steps that keep the earlier lane
-// on ties (strict >, as the first-maximum rule).  Lane 0 of the quad stores y and the winner.
+// One item of the complete block with global taps: (sample, window) * 4 + q of channel c,
+// the quad's four lanes together (every lane of the quad calls it).
 template <typename T>
-__global__ __launch_bounds__(256) void k_tree_fwd_q(const T* __restrict__ x, const T* __restrict__ w_prob,
-                                                    const int32_t* __restrict__ sel, TreeDims d,
-                                                    T* __restrict__ y, T* __restrict__ x2,
-                                                    T* __restrict__ x3, int32_t* __restrict__ idx) {
-    __shared__ T sk[kMaxNodes][4];
-    __shared__ TapOff st[kTaps];
-    __shared__ int bad;
-    const int c = blockIdx.y;
-    if (threadIdx.x == 0) bad = 0;
-    __syncthreads();
-    load_channel(w_prob, sel, c, 7, d, sk, st, &bad);
-    __syncthreads();
-    const int64_t total = int64_t(d.n) * d.P * 4;
+__device__ __forceinline__ void fwd_q_item(const T* __restrict__ x, const TreeDims& d,
+                                           const TapOff* st, T (*sk)[4], bool bad, int c,
+                                           int64_t item, int64_t total, T* __restrict__ y,
+                                           T* __restrict__ x2, T* __restrict__ x3,
+                                           int32_t* __restrict__ idx) {
     const int wp = d.wo / 2;
     const T nan = quiet_nan<T>();
-    // kFwdItems passes of 256 items per workgroup: the channel's coefficients are collapsed
-    // once for all of them.
-    for (int pass = 0; pass < kFwdItems; ++pass) {
-        const int64_t item = (int64_t(blockIdx.x) * kFwdItems + pass) * 256 + threadIdx.x;
-        if ((item & ~int64_t(255)) >= total) break;  // uniform per workgroup
+    {
         const bool live = item < total;  // (n, window) * 4 + q
         const int64_t it = live ? item : 0;
         const int q = int(it & 3);
         const int64_t win = it >> 2;
-        const int n = int(win / d.P), p = int(win % d.P);
-        const int oy = 2 * (p / wp) + (q >> 1), ox = 2 * (p % wp) + (q & 1);
+        int n, p, py;
+        if (total < (int64_t(1) << 31)) {  // uniform: 32-bit multiply-shift division
+            n = int(fast_div(uint32_t(win), d.div_p));
+            p = int(win) - n * d.P;
+        } else {
+            n = int(win / d.P);
+            p = int(win % d.P);
+        }
+        py = int(fast_div(uint32_t(p), d.div_wp));
+        const int oy = 2 * py + (q >> 1), ox = 2 * (p - py * wp) + (q & 1);
         const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
         Eval<T, true> e;
         eval_at<T, true>(xn, d, st, sk, oy, ox, e);
@@ -221,6 +233,317 @@ __global__ __launch_bounds__(256) void k_tree_fwd_q(const T* __restrict__ x, con
             y[cell * d.P + p] = bad ? nan : r;
             if (idx) idx[cell * d.P + p] = wi;
         }
+    }
+}
+
+// Complete block, quad form: one thread per conv position, the four positions of a pooling
+// window in the four lanes of a quad (lane order (0,0), (0,1), (1,0), (1,1)), so each thread
+// gathers 8 taps instead of 32 and the pool is two quad-DPP steps that keep the earlier lane
+// on ties (strict >, as the first-maximum rule).  Lane 0 of the quad stores y and the winner.
+template <typename T>
+__global__ __launch_bounds__(256) void k_tree_fwd_q(const T* __restrict__ x, const T* __restrict__ w_prob,
+                                                    const int32_t* __restrict__ sel, TreeDims d,
+                                                    T* __restrict__ y, T* __restrict__ x2,
+                                                    T* __restrict__ x3, int32_t* __restrict__ idx) {
+    __shared__ T sk[kMaxNodes][4];
+    __shared__ TapOff st[kTaps];
+    __shared__ int bad;
+    const int c = blockIdx.y;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    load_channel(w_prob, sel, c, 7, d, sk, st, &bad);
+    __syncthreads();
+    const int64_t total = int64_t(d.n) * d.P * 4;
+    // kFwdItems passes of 256 items per workgroup: the channel's coefficients are collapsed
+    // once for all of them.
+    for (int pass = 0; pass < kFwdItems; ++pass) {
+        const int64_t item = (int64_t(blockIdx.x) * kFwdItems + pass) * 256 + threadIdx.x;
+        if ((item & ~int64_t(255)) >= total) break;  // uniform per workgroup
+        fwd_q_item(x, d, st, sk, bad != 0, c, item, total, y, x2, x3, idx);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// LDS-staged forward (both forms).  A workgroup takes one sample (blockIdx.x) and a group of
+// cg output channels (blockIdx.y).  It stages the sample's whole input in LDS once, zero
+// padded, so a tap is one LDS read at a fixed per-lane base plus a per-channel offset: no
+// bounds test, no per-tap index arithmetic beyond one add.  Staged layout of input channel ch,
+// padded row iy (0 <= iy < H + 2 ph), padded column ix:
+//     ch * cs + iy * rp + (ix % sw) * ws + ix / sw
+// Columns are split by their phase modulo the stride, so the taps of neighbouring positions
+// (ox, ox + 1) are neighbouring words; the row pitch rp is chosen on the host so that the two
+// conv rows of a half-wave fall on distinct banks where it can be.  Tap k of channel c at
+// conv position (oy, ox) then reads word  oy * sh * rp + ox + off[c][k]  with
+//     off[c][k] = ch * cs + row * rp + (col % sw) * ws + col / sw.
+// A channel whose taps leave the kernel window (row >= kh or col >= kw; the selection sampler
+// never draws one) or read an input channel >= C is skipped here; k_tree_fwd_fix, launched
+// after this kernel, computes it with the global-memory gather and its bounds tests (NaN for
+// an out-of-range channel, as in the other forms).
+//
+// Lanes: IP items per channel (four per pooling window in the complete form, one per conv
+// position otherwise).  When IP >= 64 a wave walks one channel's items 64 at a time; when
+// IP < 64 a wave holds 64 / IP channels side by side.  The quad layout and the first-maximum
+// pool are those of k_tree_fwd_q.
+struct TreeLds {
+    int rp, ws, cs;      // row pitch, phase block width, channel stride (elements)
+    int cg;              // output channels per workgroup
+    int kh, kw;          // kernel window
+    int ip;              // items per channel
+    FastDiv div_pos;     // items -> conv rows: windows per pooled row (complete) or wo
+    FastDiv div_hw, div_w, div_sw;  // staging: element -> (channel, row, column), phase
+};
+
+constexpr int kTapFlagIrregular = 1;
+constexpr int kTapFlagBad = 2;
+
+template <typename T, bool COMPLETE, bool INTER>
+__device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* __restrict__ w_prob,
+                                             const int32_t* __restrict__ sel, const TreeDims& d,
+                                             const TreeLds& g, T* __restrict__ y,
+                                             T* __restrict__ x2, T* __restrict__ x3,
+                                             int32_t* __restrict__ idx) {
+    constexpr int NODES = COMPLETE ? 7 : 4;
+    constexpr int NK = NODES * 4;
+    extern __shared__ __align__(16) unsigned char tree_lds[];
+    const int n = blockIdx.x;
+    const int c_lo = blockIdx.y * g.cg;
+    const int c_n = min(g.cg, d.cout - c_lo);
+    const int planes = d.cin * g.cs;
+    T* plane = reinterpret_cast<T*>(tree_lds);
+    T* coef = plane + planes;                                        // [cg][NK]
+    int* toff = reinterpret_cast<int*>(coef + g.cg * NK);            // [cg][8]
+    int* tflag = toff + g.cg * kTaps;                                // [cg]
+    const int tid = threadIdx.x, nt = blockDim.x;
+
+    for (int i = tid; i < planes; i += nt) plane[i] = T(0);
+    // One thread per (channel, node): the four coefficients in the order of load_channel.
+    for (int i = tid; i < c_n * NODES; i += nt) {
+        const T* p = w_prob + (int64_t(c_lo) * NODES + i) * 16;
+        T a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+#pragma unroll
+        for (int gi = 0; gi < 16; ++gi) {
+            const Coef4<T> cf = gate_coef<T>(gi);
+            const T pg = p[gi];
+            a0 = fma(pg, cf.c0, a0);
+            a1 = fma(pg, cf.c1, a1);
+            a2 = fma(pg, cf.c2, a2);
+            a3 = fma(pg, cf.c3, a3);
+        }
+        coef[i * 4 + 0] = a0;
+        coef[i * 4 + 1] = a1;
+        coef[i * 4 + 2] = a2;
+        coef[i * 4 + 3] = a3;
+    }
+    __syncthreads();
+    for (int cc = tid; cc < c_n; cc += nt) {
+        int flag = 0;
+        for (int k = 0; k < kTaps; ++k) {
+            const int32_t s = sel[int64_t(c_lo + cc) * kTaps + k];
+            const int ch = (s >> 16) & 0xFFFF, row = (s >> 8) & 0xFF, col = s & 0xFF;
+            if (ch >= d.cin) flag |= kTapFlagBad;
+            if (row >= g.kh || col >= g.kw) flag |= kTapFlagIrregular;
+            const uint32_t cq = fast_div(uint32_t(col), g.div_sw);
+            toff[cc * kTaps + k] =  // bytes
+                (ch * g.cs + row * g.rp + (col - int(cq) * d.sw) * g.ws + int(cq)) *
+                int(sizeof(T));
+        }
+        tflag[cc] = flag;
+        if (flag) {  // skipped here (k_tree_fwd_fix): its dead lanes read word 0 instead
+#pragma unroll
+            for (int k = 0; k < kTaps; ++k) toff[cc * kTaps + k] = 0;
+        }
+    }
+    {
+        const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
+        const int e_n = d.cin * d.h * d.w;
+        for (int e = tid; e < e_n; e += nt) {
+            const int ch = int(fast_div(uint32_t(e), g.div_hw));
+            const int rem = e - ch * d.h * d.w;
+            const int iy = int(fast_div(uint32_t(rem), g.div_w));
+            const int ix = rem - iy * d.w + d.pw;
+            const int xq = int(fast_div(uint32_t(ix), g.div_sw));
+            plane[ch * g.cs + (iy + d.ph) * g.rp + (ix - xq * d.sw) * g.ws + xq] = xn[e];
+        }
+    }
+    __syncthreads();
+
+    const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+    const int cpw = g.ip >= 64 ? 1 : 64 / g.ip;
+    const int sub = g.ip >= 64 ? 0 : lane / g.ip;
+    const int r0 = lane - sub * (g.ip >= 64 ? 0 : g.ip);
+    const int row_step = d.sh * g.rp;
+    const int wp = COMPLETE ? d.wo / 2 : d.wo;
+    // Items are (window, q) with q = item & 3, and every chunk of a wave starts at a multiple
+    // of 4 items, so a lane's q is fixed: lane & 3.
+    const int q_lane = COMPLETE ? (lane & 3) : 0;
+    {
+        for (int it = wave * cpw; it < c_n; it += nw * cpw) {
+            const int cc = it + sub;
+            const int cl_ = (sub < cpw && cc < c_n) ? cc : it;
+            const int flag = tflag[cl_];
+            const bool cok = sub < cpw && cc < c_n && flag == 0;  // flagged: k_tree_fwd_fix
+            T k[NODES][4];
+#pragma unroll
+            for (int q = 0; q < NODES; ++q)
+#pragma unroll
+                for (int m = 0; m < 4; ++m) k[q][m] = coef[cl_ * NK + q * 4 + m];
+            int off[kTaps];
+#pragma unroll
+            for (int t = 0; t < kTaps; ++t) off[t] = toff[cl_ * kTaps + t];
+            const int c = c_lo + cl_;
+            const int64_t cell = int64_t(n) * d.cout + c;
+            for (int j = 0; j < g.ip; j += 64) {
+                const int r = j + r0;
+                const bool live = cok && r < g.ip;
+                const int re = live ? r : q_lane;  // a dead lane keeps its quad position
+                int oy, ox, p;
+                if constexpr (COMPLETE) {
+                    p = re >> 2;
+                    const int py = int(fast_div(uint32_t(p), g.div_pos));
+                    const int px = p - py * wp;
+                    oy = 2 * py + (q_lane >> 1);
+                    ox = 2 * px + (q_lane & 1);
+                } else {
+                    p = re;
+                    oy = int(fast_div(uint32_t(p), g.div_pos));
+                    ox = p - oy * wp;
+                }
+                // Every lane reads in bounds: a dead lane sits at a valid position of a channel
+                // whose offsets are valid (or 0 for a flagged one), and drops what it reads.
+                T v[kTaps];
+                {
+                    const int base = (oy * row_step + ox) * int(sizeof(T));
+                    const char* pl = reinterpret_cast<const char*>(plane) + base;
+#pragma unroll
+                    for (int t = 0; t < kTaps; ++t) v[t] = *reinterpret_cast<const T*>(pl + off[t]);
+                }
+                T gv[4];
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) gv[qq] = node(k[qq], v[2 * qq], v[2 * qq + 1]);
+                if constexpr (!COMPLETE) {
+                    if (live) {
+                        const int64_t pos = cell * d.P + p;
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) y[pos * 4 + qq] = gv[qq];
+                    }
+                } else {
+                    const T t0 = node(k[4], gv[0], gv[1]);
+                    const T t1 = node(k[5], gv[2], gv[3]);
+                    const T rv = node(k[6], t0, t1);
+                    if (INTER && live) {
+                        const int64_t pos = cell * d.ho * d.wo + int64_t(oy) * d.wo + ox;
+                        if (x2) {
+#pragma unroll
+                            for (int qq = 0; qq < 4; ++qq) x2[pos * 4 + qq] = gv[qq];
+                        }
+                        if (x3) {
+                            x3[pos * 2 + 0] = t0;
+                            x3[pos * 2 + 1] = t1;
+                        }
+                    }
+                    // No NaN enters the quad (one enters as -inf), so for the later lane of a
+                    // pair "not strictly greater than the earlier one" is ro >= rr.
+                    const bool num = rv == rv;
+                    T rr = num ? rv : -T(__builtin_inf());
+                    int wi = num ? oy * d.wo + ox : -1;
+                    // The comparisons are wave masks; the lane parity picks between them in
+                    // scalar code (lanes with q & 1: 0xAAAA...; with q & 2: 0xCCCC...).
+                    {
+                        const T ro = dpp_move<0xB1>(rr);
+                        const int wo_ = dpp_move<0xB1>(wi);
+                        const uint64_t gt = __ballot(ro > rr), ge = __ballot(ro >= rr);
+                        const bool take = __builtin_amdgcn_inverse_ballot_w64(
+                            (ge & 0xAAAAAAAAAAAAAAAAull) | (gt & 0x5555555555555555ull));
+                        rr = take ? ro : rr;
+                        wi = take ? wo_ : wi;
+                    }
+                    {
+                        const T ro = dpp_move<0x4E>(rr);
+                        const int wo_ = dpp_move<0x4E>(wi);
+                        const uint64_t gt = __ballot(ro > rr), ge = __ballot(ro >= rr);
+                        const bool take = __builtin_amdgcn_inverse_ballot_w64(
+                            (ge & 0xCCCCCCCCCCCCCCCCull) | (gt & 0x3333333333333333ull));
+                        rr = take ? ro : rr;
+                        wi = take ? wo_ : wi;
+                    }
+                    if (live && q_lane == 0) {
+                        y[cell * d.P + p] = rr;
+                        if (idx) idx[cell * d.P + p] = wi;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// fp32 without the intermediates fits 64 VGPRs: two workgroups of 16 waves per CU.
+template <bool COMPLETE>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void k_tree_fwd_lds_f32(
+    const float* __restrict__ x, const float* __restrict__ w_prob, const int32_t* __restrict__ sel,
+    TreeDims d, TreeLds g, float* __restrict__ y, float* __restrict__ x2, float* __restrict__ x3,
+    int32_t* __restrict__ idx) {
+    tree_fwd_lds<float, COMPLETE, false>(x, w_prob, sel, d, g, y, x2, x3, idx);
+}
+
+template <typename T, bool COMPLETE, bool INTER>
+__global__ __launch_bounds__(1024) void k_tree_fwd_lds(
+    const T* __restrict__ x, const T* __restrict__ w_prob, const int32_t* __restrict__ sel,
+    TreeDims d, TreeLds g, T* __restrict__ y, T* __restrict__ x2, T* __restrict__ x3,
+    int32_t* __restrict__ idx) {
+    tree_fwd_lds<T, COMPLETE, INTER>(x, w_prob, sel, d, g, y, x2, x3, idx);
+}
+
+// The channels k_tree_fwd_lds skips.  Each workgroup checks 256 channels, one per thread, and
+// returns when all of them are regular (the usual case: one short launch of a few
+// workgroups); each flagged one is then computed by the whole workgroup with the global
+// gather over every sample.
+constexpr int kFixChannels = 256;
+
+template <typename T, bool COMPLETE>
+__global__ __launch_bounds__(256) void k_tree_fwd_fix(const T* __restrict__ x,
+                                                      const T* __restrict__ w_prob,
+                                                      const int32_t* __restrict__ sel, TreeDims d,
+                                                      int kh, int kw, T* __restrict__ y,
+                                                      T* __restrict__ x2, T* __restrict__ x3,
+                                                      int32_t* __restrict__ idx) {
+    __shared__ int flagged[kFixChannels];
+    __shared__ int nflagged;
+    __shared__ T sk[kMaxNodes][4];
+    __shared__ TapOff st[kTaps];
+    __shared__ int bad;
+    if (threadIdx.x == 0) nflagged = 0;
+    __syncthreads();
+    {
+        const int c = blockIdx.x * kFixChannels + threadIdx.x;
+        bool f = false;
+        if (c < d.cout) {
+#pragma unroll
+            for (int k = 0; k < kTaps; ++k) {
+                const int32_t s = sel[int64_t(c) * kTaps + k];
+                f |= ((s >> 16) & 0xFFFF) >= d.cin || ((s >> 8) & 0xFF) >= kh ||
+                     (s & 0xFF) >= kw;
+            }
+        }
+        if (f) flagged[atomicAdd(&nflagged, 1)] = c;  // LDS atomic
+    }
+    __syncthreads();
+    const int nf = nflagged;
+    for (int i = 0; i < nf; ++i) {  // uniform
+        const int c = flagged[i];
+        if (threadIdx.x == 0) bad = 0;
+        __syncthreads();
+        load_channel(w_prob, sel, c, COMPLETE ? 7 : 4, d, sk, st, &bad);
+        __syncthreads();
+        if constexpr (COMPLETE) {
+            const int64_t total = int64_t(d.n) * d.P * 4;
+            for (int64_t item = threadIdx.x; (item & ~int64_t(255)) < total; item += 256)
+                fwd_q_item(x, d, st, sk, bad != 0, c, item, total, y, x2, x3, idx);
+        } else {
+            const int64_t total = int64_t(d.n) * d.P;
+            for (int64_t item = threadIdx.x; item < total; item += 256)
+                fwd_gates_item(x, d, st, sk, bad != 0, c, item, y);
+        }
+        __syncthreads();  // sk / st are rewritten for the next channel
     }
 }
 
@@ -739,6 +1062,8 @@ int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t
     d.pw = pw;
     d.complete = complete ? 1 : 0;
     d.P = int(P);
+    d.div_p = make_fastdiv(uint32_t(std::max<int64_t>(P, 1)));
+    d.div_wp = make_fastdiv(uint32_t(std::max<int64_t>(complete ? wo / 2 : wo, 1)));
     return CL_OK;
 }
 
@@ -750,6 +1075,96 @@ int gather_lanes(int P) {
 }
 
 constexpr int64_t kGatherLdsBytes = 64 * 1024;
+
+constexpr int64_t kFwdLdsLimit = 160 * 1024;  // LDS of one gfx950 CU
+constexpr int kFwdLdsThreads = 1024;
+constexpr int kMaxDevices = 64;
+
+// Geometry of the LDS-staged forward, or false when one sample's padded input does not fit.
+template <typename T>
+bool plan_tree_fwd_lds(const TreeDims& d, int kh, int kw, TreeLds& g, int& groups,
+                       int64_t& lds) {
+    const int hpad = d.h + 2 * d.ph, wpad = d.w + 2 * d.pw;
+    g.kh = kh;
+    g.kw = kw;
+    g.ws = (wpad + d.sw - 1) / d.sw;
+    g.ip = d.complete ? 4 * d.P : d.P;
+    const int base = d.sw * g.ws;
+    const int64_t tab = int64_t(d.complete ? 28 : 16) * sizeof(T) + (kTaps + 1) * 4;
+    // Staging pays when a sample's items outnumber its input elements (conv1 of the tree
+    // reading of cfg3: 7 per element); below two per element the global gather is kept.
+    const int64_t staged = int64_t(d.cin) * d.h * d.w;
+    if (int64_t(d.cout) * g.ip < 2 * staged) return false;
+    auto total = [&](int rp, int64_t cg) {
+        return int64_t(d.cin) * hpad * rp * int64_t(sizeof(T)) + cg * tab;
+    };
+    // Row pitch: conv rows oy and oy + 1 are sh * rp words apart; 16 banks apart (mod 32)
+    // puts the two rows of a half-wave on distinct banks.
+    int rp = base;
+    for (int e = 0; e <= 16; ++e)
+        if ((int64_t(d.sh) * (base + e)) % 32 == 16) {
+            rp = base + e;
+            break;
+        }
+    if (total(rp, 1) > kFwdLdsLimit) rp = base;
+    if (total(rp, 1) > kFwdLdsLimit) return false;
+    if (int64_t(d.cin) * hpad * rp >= (int64_t(1) << 30)) return false;
+    g.rp = rp;
+    g.cs = hpad * rp;
+    // Channel groups: enough workgroups to fill the chip twice while every workgroup still
+    // computes at least twice as many items as it stages input elements; then as many more
+    // as LDS needs.
+    int64_t G = 1;
+    while (int64_t(d.n) * G < 512 && 2 * G <= d.cout &&
+           ceil_div(d.cout, 2 * G) * g.ip >= 2 * staged)
+        G *= 2;
+    while (total(rp, ceil_div(d.cout, G)) > kFwdLdsLimit) ++G;
+    g.cg = int(ceil_div(d.cout, G));
+    groups = int(ceil_div(d.cout, g.cg));
+    lds = total(rp, g.cg);
+    g.div_pos = make_fastdiv(uint32_t(d.complete ? d.wo / 2 : d.wo));
+    g.div_hw = make_fastdiv(uint32_t(d.h * d.w));
+    g.div_w = make_fastdiv(uint32_t(d.w));
+    g.div_sw = make_fastdiv(uint32_t(d.sw));
+    return groups < 65536;
+}
+
+template <typename T, bool COMPLETE>
+int launch_tree_fwd_lds(const TreeDims& d, const TreeLds& g, int groups, int64_t lds,
+                        const T* x, const T* w_prob, const int32_t* sel, T* y, T* x2, T* x3,
+                        int32_t* idx, hipStream_t s) {
+    void (*kern)(const T*, const T*, const int32_t*, TreeDims, TreeLds, T*, T*, T*, int32_t*);
+    const bool inter = x2 != nullptr || x3 != nullptr;
+    if constexpr (sizeof(T) == 4) {
+        if (!inter) kern = &k_tree_fwd_lds_f32<COMPLETE>;
+        else kern = &k_tree_fwd_lds<T, COMPLETE, true>;
+    } else {
+        kern = inter ? &k_tree_fwd_lds<T, COMPLETE, true> : &k_tree_fwd_lds<T, COMPLETE, false>;
+    }
+    // Above 64 KiB the kernel needs the attribute, set once per device and instantiation.
+    static bool reserved[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("cannot query the device");
+        return CL_ERR_HIP;
+    }
+    if (lds > 64 * 1024 && !reserved[dev]) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                int(kFwdLdsLimit)) != hipSuccess) {
+            set_error("cannot reserve %lld bytes of LDS for the tree block forward",
+                      (long long)lds);
+            return CL_ERR_HIP;
+        }
+        reserved[dev] = true;
+    }
+    kern<<<dim3(unsigned(d.n), unsigned(groups)), kFwdLdsThreads, size_t(lds), s>>>(
+        x, w_prob, sel, d, g, y, x2, x3, idx);
+    if (int rc = check_launch("cl_tree_conv_forward")) return rc;
+    k_tree_fwd_fix<T, COMPLETE><<<unsigned(ceil_div(d.cout, kFixChannels)), kFixChannels, 0, s>>>(
+        x, w_prob, sel, d, g.kh, g.kw, y, x2, x3, idx);
+    return check_launch("cl_tree_conv_forward");
+}
 
 template <typename T>
 int64_t tree_workspace_bytes(const TreeDims& d) {
@@ -787,6 +1202,20 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
+        TreeLds g;
+        int groups = 0;
+        int64_t lds = 0;
+        if (plan_tree_fwd_lds<T>(d, kernel_h, kernel_w, g, groups, lds)) {
+            const T* xs = static_cast<const T*>(x);
+            const T* ws = static_cast<const T*>(w_prob);
+            if (complete)
+                return launch_tree_fwd_lds<T, true>(d, g, groups, lds, xs, ws, selection,
+                                                    static_cast<T*>(y), static_cast<T*>(x2),
+                                                    static_cast<T*>(x3), indices, s);
+            return launch_tree_fwd_lds<T, false>(d, g, groups, lds, xs, ws, selection,
+                                                 static_cast<T*>(y), nullptr, nullptr, nullptr,
+                                                 s);
+        }
         if (complete) {
             const unsigned gq = unsigned(ceil_div(int64_t(d.n) * d.P * 4, 256 * kFwdItems));
             k_tree_fwd_q<T><<<dim3(gq, unsigned(d.cout)), 256, 0, s>>>(

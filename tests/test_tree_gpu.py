@@ -40,6 +40,10 @@ SHAPES = [  # stride, pad, kernel, (n, c_in, h, w, c_out)
     ((1, 1), (0, 0), (2, 2), (2, 2, 5, 5, 3)),
     ((2, 2), (1, 1), (3, 3), (128, 9, 16, 16, 41)),   # channel groups of 2, the last one short
     ((1, 1), (1, 1), (3, 3), (2, 5, 64, 64, 3)),      # 80 KiB (fp32) / 160 KiB (fp64) planes
+    # LDS-staged forward (at least two items per staged input element):
+    ((2, 2), (1, 1), (3, 3), (2, 9, 32, 32, 96)),     # conv1 geometry, a channel per wave
+    ((2, 2), (1, 1), (3, 3), (2, 3, 8, 8, 64)),       # 16 items per channel: 4 channels a wave
+    ((1, 1), (1, 1), (3, 3), (2, 2, 10, 10, 24)),     # stride 1, 5 windows a row, 100 items
 ]
 
 
@@ -145,6 +149,10 @@ BINARY_SHAPES = [  # stride, pad, kernel, (n, c_in, h, w, c_out)
     ((2, 2), (1, 1), (3, 3), (16, 16, 8, 8, 32)),     # conv2 of the tree reading
     ((1, 1), (1, 1), (3, 3), (4, 3, 12, 12, 6)),
     ((1, 1), (0, 0), (2, 2), (6, 2, 7, 9, 5)),        # many positions share all eight taps
+    # LDS-staged forward:
+    ((2, 2), (1, 1), (3, 3), (4, 9, 32, 32, 96)),     # conv1 geometry
+    ((2, 2), (1, 1), (3, 3), (4, 3, 8, 8, 64)),       # four channels a wave
+    ((1, 1), (0, 0), (2, 2), (6, 2, 7, 9, 40)),       # 48 items per channel, 16 lanes idle
 ]
 
 
@@ -281,6 +289,39 @@ def test_range_determinism_and_irregular_channels():
     y = cl.ConvLogicLayer(1, 1, kernel=2, padding=0, complete=True).cuda().eval()(
         torch.randn(1, 1, 3, 3, device="cuda"))
     assert y.shape == (1, 1, 1, 1)
+
+
+@pytest.mark.parametrize("dtype,shape", [
+    (torch.float32, (3, 4, 12, 12, 64)),      # LDS-staged forward, flagged channels fixed up
+    (torch.float64, (3, 4, 12, 12, 64)),
+    (torch.float64, (1, 5, 64, 64, 6)),       # global gather throughout
+])
+@pytest.mark.parametrize("complete", [True, False])
+def test_forward_taps_outside_the_window_and_out_of_range_channels(dtype, shape, complete):
+    """A channel with a tap outside the kernel window (still inside the padded image) matches
+    the oracle; a channel reading an input channel >= C yields NaN; the others are unchanged."""
+    n, c_in, h, w, c_out = shape
+    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    x, w_prob, sel = make(7, n, c_in, h, w, c_out, 3, nodes=7 if complete else 4, dtype=dtype)
+    sel = sel.clone()
+    sel[1, 2] = (sel[1, 2] & ~0xFF00) | (4 << 8)          # row 4 of a 3x3 window
+    sel[3, 5] = (sel[3, 5] & ~0xFF) | 3                   # column 3
+    ok = sel.clone()
+    sel[4, 0] = (sel[4, 0] & 0xFFFF) | (c_in << 16)       # input channel C
+    ok[4, 0] = ok[4, 0] & 0xFFFF
+    live = [c for c in range(c_out) if c != 4]
+    if complete:
+        y, x2, x3, idx = TL.full_convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel)
+        ry, rx2, rx3, ridx = T.block_forward(np_(x), np_(w_prob), np_(ok), stride, pad, kernel)
+        np.testing.assert_allclose(np_(y)[:, live], ry[:, live], **tol(dtype))
+        np.testing.assert_allclose(np_(x2)[:, live], rx2[:, live], **tol(dtype))
+        np.testing.assert_allclose(np_(x3)[:, live], rx3[:, live], **tol(dtype))
+        assert torch.isnan(y[:, 4]).all() and torch.isnan(x2[:, 4]).all()
+    else:
+        y = TL.convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel)
+        ref = T.block_forward(np_(x), np_(w_prob), np_(ok), stride, pad, kernel, complete=False)
+        np.testing.assert_allclose(np_(y)[:, live], ref[:, live], **tol(dtype))
+        assert torch.isnan(y[:, 4]).all()
 
 
 def test_identity_init():
