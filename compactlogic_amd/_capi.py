@@ -18,6 +18,7 @@ CL_ERR_HIP = 3
 
 CL_DTYPE_F32 = 0
 CL_DTYPE_F64 = 1
+CL_DTYPE_F16 = 2
 
 ABI_VERSION = 1
 

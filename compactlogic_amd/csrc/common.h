@@ -5,6 +5,7 @@
 // asynchronous on the stream the caller passes.
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdarg.h>
@@ -46,6 +47,54 @@ int check_launch(const char* what);
             return CL_ERR_INVALID_ARGUMENT;                                             \
         }                                                                               \
     } while (0)
+
+// As CL_DTYPE_SWITCH, and CL_DTYPE_F16 binds scalar_t to __half (storage only: kernels
+// compute in acc_t<scalar_t>).
+#define CL_DTYPE_SWITCH_F16(dtype, ...)                                                 \
+    do {                                                                                \
+        if ((dtype) == CL_DTYPE_F32) {                                                  \
+            using scalar_t = float;                                                     \
+            __VA_ARGS__                                                                 \
+        } else if ((dtype) == CL_DTYPE_F64) {                                           \
+            using scalar_t = double;                                                    \
+            __VA_ARGS__                                                                 \
+        } else if ((dtype) == CL_DTYPE_F16) {                                           \
+            using scalar_t = __half;                                                    \
+            __VA_ARGS__                                                                 \
+        } else {                                                                        \
+            ::cl::set_error("unsupported dtype code %d (expected CL_DTYPE_F32, F64 or F16)", \
+                            int(dtype));                                                \
+            return CL_ERR_INVALID_ARGUMENT;                                             \
+        }                                                                               \
+    } while (0)
+
+// Arithmetic type of a storage type: half is loaded, summed in fp32 and rounded once on store.
+template <typename S>
+struct AccType {
+    using type = S;
+};
+template <>
+struct AccType<__half> {
+    using type = float;
+};
+template <typename S>
+using acc_t = typename AccType<S>::type;
+
+template <typename S>
+__device__ __forceinline__ acc_t<S> to_acc(S v) {
+    if constexpr (sizeof(S) == 2)
+        return __half2float(v);
+    else
+        return v;
+}
+
+template <typename S>
+__device__ __forceinline__ S from_acc(acc_t<S> v) {
+    if constexpr (sizeof(S) == 2)
+        return __float2half_rn(v);
+    else
+        return v;
+}
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -193,6 +242,10 @@ template <typename T>
 struct Vec<T, 4> {
     T v[4];
 };
+template <typename T>
+struct Vec<T, 8> {
+    T v[8];
+};
 
 template <typename T, int VEC>
 __device__ __forceinline__ Vec<T, VEC> vload(const T* p) {
@@ -207,6 +260,14 @@ __device__ __forceinline__ Vec<T, VEC> vload(const T* p) {
         const double2 t = *reinterpret_cast<const double2*>(p);
         r.v[0] = __builtin_bit_cast(T, t.x);
         r.v[1] = __builtin_bit_cast(T, t.y);
+    } else if constexpr (VEC == 8 && sizeof(T) == 2) {
+        const uint4 t = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.v[2 * i] = __builtin_bit_cast(T, uint16_t(w[i] & 0xFFFFu));
+            r.v[2 * i + 1] = __builtin_bit_cast(T, uint16_t(w[i] >> 16));
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) r.v[i] = p[i];
@@ -228,6 +289,13 @@ __device__ __forceinline__ void vstore(T* p, const Vec<T, VEC>& r) {
         t.x = __builtin_bit_cast(double, r.v[0]);
         t.y = __builtin_bit_cast(double, r.v[1]);
         *reinterpret_cast<double2*>(p) = t;
+    } else if constexpr (VEC == 8 && sizeof(T) == 2) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = uint32_t(__builtin_bit_cast(uint16_t, r.v[2 * i])) |
+                   (uint32_t(__builtin_bit_cast(uint16_t, r.v[2 * i + 1])) << 16);
+        *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) p[i] = r.v[i];

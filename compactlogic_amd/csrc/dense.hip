@@ -26,27 +26,31 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup (256 threads)
 
-template <typename T>
-__device__ __forceinline__ T qnan() {
-    return T(__builtin_nan(""));
+// Storage type S (float, double or __half) and arithmetic type A = acc_t<S>: half rows are
+// widened on load, summed in fp32 and rounded once on store.
+template <typename S>
+__device__ __forceinline__ S qnan() {
+    return from_acc<S>(acc_t<S>(__builtin_nan("")));
 }
 
 // Collapsed coefficients of the run [g0, g0+len) of one neuron: lane l takes slots
 // g0 + l, g0 + l + 64, ..., and the four partial sums are reduced across the wave.  The
 // result is wave-uniform.
-template <typename T>
-__device__ __forceinline__ Coef4<T> run_coef(const T* __restrict__ wrow,
-                                             const uint8_t* __restrict__ grow, int g0, int len) {
-    T p0 = 0, p1 = 0, p2 = 0, p3 = 0;
+template <typename S>
+__device__ __forceinline__ Coef4<acc_t<S>> run_coef(const S* __restrict__ wrow,
+                                                    const uint8_t* __restrict__ grow, int g0,
+                                                    int len) {
+    using A = acc_t<S>;
+    A p0 = 0, p1 = 0, p2 = 0, p3 = 0;
     for (int g = g0 + lane_id(); g < g0 + len; g += kWave) {
-        const T wg = wrow[g];
-        const Coef4<T> c = gate_coef<T>(grow[g]);
+        const A wg = to_acc(wrow[g]);
+        const Coef4<A> c = gate_coef<A>(grow[g]);
         p0 = fma(wg, c.c0, p0);
         p1 = fma(wg, c.c1, p1);
         p2 = fma(wg, c.c2, p2);
         p3 = fma(wg, c.c3, p3);
     }
-    Coef4<T> k;
+    Coef4<A> k;
     k.c0 = wave_total(p0);
     k.c1 = wave_total(p1);
     k.c2 = wave_total(p2);
@@ -55,63 +59,68 @@ __device__ __forceinline__ Coef4<T> run_coef(const T* __restrict__ wrow,
 }
 
 // acc += K(xa, xb) over the wave's U vectors of the batch chunk starting at b0.
-template <typename T, int VEC, int U>
-__device__ __forceinline__ void accum_run(Vec<T, VEC> (&acc)[U], const T* __restrict__ xa,
-                                          const T* __restrict__ xb, const Coef4<T>& k, int64_t b0,
-                                          int64_t B) {
+template <typename S, int VEC, int U>
+__device__ __forceinline__ void accum_run(Vec<acc_t<S>, VEC> (&acc)[U], const S* __restrict__ xa,
+                                          const S* __restrict__ xb, const Coef4<acc_t<S>>& k,
+                                          int64_t b0, int64_t B) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t idx = b0 + int64_t(u) * kWave * VEC;
         if (idx < B) {
-            const Vec<T, VEC> va = vload<T, VEC>(xa + idx);
-            const Vec<T, VEC> vb = vload<T, VEC>(xb + idx);
+            const Vec<S, VEC> va = vload<S, VEC>(xa + idx);
+            const Vec<S, VEC> vb = vload<S, VEC>(xb + idx);
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) acc[u].v[i] += relaxed_op(k, va.v[i], vb.v[i]);
+            for (int i = 0; i < VEC; ++i)
+                acc[u].v[i] += relaxed_op(k, to_acc(va.v[i]), to_acc(vb.v[i]));
         }
     }
 }
 
-template <typename T, int VEC, int U>
-__device__ __forceinline__ void store_rows(T* __restrict__ yrow, const Vec<T, VEC> (&acc)[U],
-                                           int64_t b0, int64_t B, bool poison) {
+template <typename S, int VEC, int U>
+__device__ __forceinline__ void store_rows(S* __restrict__ yrow,
+                                           const Vec<acc_t<S>, VEC> (&acc)[U], int64_t b0,
+                                           int64_t B, bool poison) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t idx = b0 + int64_t(u) * kWave * VEC;
         if (idx < B) {
-            Vec<T, VEC> r = acc[u];
-            if (poison) {
+            Vec<S, VEC> r;
 #pragma unroll
-                for (int i = 0; i < VEC; ++i) r.v[i] = qnan<T>();
-            }
-            vstore<T, VEC>(yrow + idx, r);
+            for (int i = 0; i < VEC; ++i) r.v[i] = poison ? qnan<S>() : from_acc<S>(acc[u].v[i]);
+            vstore<S, VEC>(yrow + idx, r);
         }
     }
+}
+
+template <typename A, int VEC, int U>
+__device__ __forceinline__ void zero_acc(Vec<A, VEC> (&acc)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[u].v[i] = A(0);
 }
 
 // ------------------------------------------------------------------------------------------
 // Forward over the reference's int64 indices (runs detected on the fly).
-template <typename T, int VEC, int U>
-__global__ __launch_bounds__(256) void k_dense_forward(const T* __restrict__ x,
+template <typename S, int VEC, int U>
+__global__ __launch_bounds__(256) void k_dense_forward(const S* __restrict__ x,
                                                        const int64_t* __restrict__ a,
                                                        const int64_t* __restrict__ b,
-                                                       const T* __restrict__ w,
+                                                       const S* __restrict__ w,
                                                        const uint8_t* __restrict__ gs,
-                                                       T* __restrict__ y, int64_t in_dim,
+                                                       S* __restrict__ y, int64_t in_dim,
                                                        int64_t out_dim, int64_t B, int G) {
+    using A = acc_t<S>;
     const int64_t o = int64_t(blockIdx.x) * kWaves + wave_id();
     if (o >= out_dim) return;
     const int64_t b0 = int64_t(blockIdx.y) * (kWave * VEC * U) + int64_t(lane_id()) * VEC;
     const int64_t* arow = a + o * G;
     const int64_t* brow = b + o * G;
-    const T* wrow = w + o * G;
+    const S* wrow = w + o * G;
     const uint8_t* grow = gs + o * G;
 
-    Vec<T, VEC> acc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[u].v[i] = T(0);
-
+    Vec<A, VEC> acc[U];
+    zero_acc(acc);
     bool bad = false;
     int g = 0;
     while (g < G) {
@@ -121,36 +130,38 @@ __global__ __launch_bounds__(256) void k_dense_forward(const T* __restrict__ x,
         if (uint64_t(ia) >= uint64_t(in_dim) || uint64_t(ib) >= uint64_t(in_dim)) {
             bad = true;
         } else {
-            const Coef4<T> k = run_coef(wrow, grow, g, g1 - g);
-            accum_run<T, VEC, U>(acc, x + ia * B, x + ib * B, k, b0, B);
+            const Coef4<A> k = run_coef(wrow, grow, g, g1 - g);
+            accum_run<S, VEC, U>(acc, x + ia * B, x + ib * B, k, b0, B);
         }
         g = g1;
     }
-    store_rows<T, VEC, U>(y + o * B, acc, b0, B, bad);
+    store_rows<S, VEC, U>(y + o * B, acc, b0, B, bad);
 }
 
 // ------------------------------------------------------------------------------------------
 // Batch moments of one run: S1 = sum gy, Sa = sum gy*a, Sb = sum gy*b, Sab = sum gy*a*b over
 // the whole batch, reduced across the wave (every lane returns the totals).
-template <typename T, int VEC>
-__device__ __forceinline__ Coef4<T> run_moments(const T* __restrict__ gyrow,
-                                                const T* __restrict__ xa,
-                                                const T* __restrict__ xb, int64_t B) {
-    T s1 = 0, sa = 0, sb = 0, sab = 0;
+template <typename S, int VEC>
+__device__ __forceinline__ Coef4<acc_t<S>> run_moments(const S* __restrict__ gyrow,
+                                                       const S* __restrict__ xa,
+                                                       const S* __restrict__ xb, int64_t B) {
+    using A = acc_t<S>;
+    A s1 = 0, sa = 0, sb = 0, sab = 0;
     for (int64_t idx = int64_t(lane_id()) * VEC; idx < B; idx += kWave * VEC) {
-        const Vec<T, VEC> g = vload<T, VEC>(gyrow + idx);
-        const Vec<T, VEC> va = vload<T, VEC>(xa + idx);
-        const Vec<T, VEC> vb = vload<T, VEC>(xb + idx);
+        const Vec<S, VEC> g = vload<S, VEC>(gyrow + idx);
+        const Vec<S, VEC> va = vload<S, VEC>(xa + idx);
+        const Vec<S, VEC> vb = vload<S, VEC>(xb + idx);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-            s1 += g.v[i];
-            const T ga = g.v[i] * va.v[i];
+            const A gi = to_acc(g.v[i]), ai = to_acc(va.v[i]), bi = to_acc(vb.v[i]);
+            s1 += gi;
+            const A ga = gi * ai;
             sa += ga;
-            sb = fma(g.v[i], vb.v[i], sb);
-            sab = fma(ga, vb.v[i], sab);
+            sb = fma(gi, bi, sb);
+            sab = fma(ga, bi, sab);
         }
     }
-    Coef4<T> m;
+    Coef4<A> m;
     m.c0 = wave_total(s1);
     m.c1 = wave_total(sa);
     m.c2 = wave_total(sb);
@@ -159,27 +170,28 @@ __device__ __forceinline__ Coef4<T> run_moments(const T* __restrict__ gyrow,
 }
 
 // grad_w[o, g] for g in [g0, g0+len) from the run's moments m = (S1, Sa, Sb, Sab).
-template <typename T>
-__device__ __forceinline__ void write_run_grad_w(T* __restrict__ gwrow,
+template <typename S>
+__device__ __forceinline__ void write_run_grad_w(S* __restrict__ gwrow,
                                                  const uint8_t* __restrict__ grow, int g0,
-                                                 int len, const Coef4<T>& m, bool poison) {
+                                                 int len, const Coef4<acc_t<S>>& m, bool poison) {
+    using A = acc_t<S>;
     for (int g = g0 + lane_id(); g < g0 + len; g += kWave) {
-        const Coef4<T> c = gate_coef<T>(grow[g]);
-        T v = fma(c.c3, m.c3, fma(c.c2, m.c2, fma(c.c1, m.c1, c.c0 * m.c0)));
-        if (poison) v = qnan<T>();
-        gwrow[g] = v;
+        const Coef4<A> c = gate_coef<A>(grow[g]);
+        const A v = fma(c.c3, m.c3, fma(c.c2, m.c2, fma(c.c1, m.c1, c.c0 * m.c0)));
+        gwrow[g] = poison ? qnan<S>() : from_acc<S>(v);
     }
 }
 
 // Weight gradient over the reference's int64 indices: one wave per neuron, whole batch.
-template <typename T, int VEC>
-__global__ __launch_bounds__(256) void k_dense_backward_w(const T* __restrict__ x,
+template <typename S, int VEC>
+__global__ __launch_bounds__(256) void k_dense_backward_w(const S* __restrict__ x,
                                                           const int64_t* __restrict__ a,
                                                           const int64_t* __restrict__ b,
                                                           const uint8_t* __restrict__ gs,
-                                                          const T* __restrict__ gy,
-                                                          T* __restrict__ gw, int64_t in_dim,
+                                                          const S* __restrict__ gy,
+                                                          S* __restrict__ gw, int64_t in_dim,
                                                           int64_t out_dim, int64_t B, int G) {
+    using A = acc_t<S>;
     const int64_t o = int64_t(blockIdx.x) * kWaves + wave_id();
     if (o >= out_dim) return;
     const int64_t* arow = a + o * G;
@@ -191,9 +203,9 @@ __global__ __launch_bounds__(256) void k_dense_backward_w(const T* __restrict__ 
         int g1 = g + 1;
         while (g1 < G && arow[g1] == ia && brow[g1] == ib) ++g1;
         const bool bad = uint64_t(ia) >= uint64_t(in_dim) || uint64_t(ib) >= uint64_t(in_dim);
-        Coef4<T> m{T(0), T(0), T(0), T(0)};
-        if (!bad) m = run_moments<T, VEC>(gy + o * B, x + ia * B, x + ib * B, B);
-        write_run_grad_w<T>(gw + o * G, grow, g, g1 - g, m, bad);
+        Coef4<A> m{A(0), A(0), A(0), A(0)};
+        if (!bad) m = run_moments<S, VEC>(gy + o * B, x + ia * B, x + ib * B, B);
+        write_run_grad_w<S>(gw + o * G, grow, g, g1 - g, m, bad);
         g = g1;
     }
 }
@@ -201,23 +213,20 @@ __global__ __launch_bounds__(256) void k_dense_backward_w(const T* __restrict__ 
 // ------------------------------------------------------------------------------------------
 // Input gradient through the reference's inverse index: one wave per input row i over a batch
 // chunk; every entry is one (neuron, slot, operand side) use of x_i.
-template <typename T, int VEC, int U>
+template <typename S, int VEC, int U>
 __global__ __launch_bounds__(256) void k_dense_backward_x(
-    const T* __restrict__ x, const int64_t* __restrict__ a, const int64_t* __restrict__ b,
-    const T* __restrict__ w, const uint8_t* __restrict__ gs, const T* __restrict__ gy,
+    const S* __restrict__ x, const int64_t* __restrict__ a, const int64_t* __restrict__ b,
+    const S* __restrict__ w, const uint8_t* __restrict__ gs, const S* __restrict__ gy,
     const int64_t* __restrict__ start, const int64_t* __restrict__ yidx,
-    const int8_t* __restrict__ gcode, int64_t num_entries, T* __restrict__ gx, int64_t in_dim,
+    const int8_t* __restrict__ gcode, int64_t num_entries, S* __restrict__ gx, int64_t in_dim,
     int64_t out_dim, int64_t B, int G) {
+    using A = acc_t<S>;
     const int64_t i = int64_t(blockIdx.x) * kWaves + wave_id();
     if (i >= in_dim) return;
     const int64_t b0 = int64_t(blockIdx.y) * (kWave * VEC * U) + int64_t(lane_id()) * VEC;
 
-    Vec<T, VEC> acc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[u].v[v] = T(0);
-
+    Vec<A, VEC> acc[U];
+    zero_acc(acc);
     bool bad = false;
     int64_t e0 = start[i], e1 = start[i + 1];
     if (e0 < 0 || e1 < e0 || e1 > num_entries) {
@@ -238,57 +247,55 @@ __global__ __launch_bounds__(256) void k_dense_backward_x(
             bad = true;
             continue;
         }
-        const T wg = w[yo * G + g];
-        const Coef4<T> c = gate_coef<T>(gs[yo * G + g]);
-        const T kself = side_a ? c.c1 : c.c2;
-        const T* xo = x + other * B;
-        const T* gyr = gy + yo * B;
+        const A wg = to_acc(w[yo * G + g]);
+        const Coef4<A> c = gate_coef<A>(gs[yo * G + g]);
+        const A kself = side_a ? c.c1 : c.c2;
+        const S* xo = x + other * B;
+        const S* gyr = gy + yo * B;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t idx = b0 + int64_t(u) * kWave * VEC;
             if (idx < B) {
-                const Vec<T, VEC> vo = vload<T, VEC>(xo + idx);
-                const Vec<T, VEC> vg = vload<T, VEC>(gyr + idx);
+                const Vec<S, VEC> vo = vload<S, VEC>(xo + idx);
+                const Vec<S, VEC> vg = vload<S, VEC>(gyr + idx);
 #pragma unroll
                 for (int v = 0; v < VEC; ++v) {
-                    const T dydx = wg * fma(c.c3, vo.v[v], kself);
-                    acc[u].v[v] = fma(dydx, vg.v[v], acc[u].v[v]);
+                    const A dydx = wg * fma(c.c3, to_acc(vo.v[v]), kself);
+                    acc[u].v[v] = fma(dydx, to_acc(vg.v[v]), acc[u].v[v]);
                 }
             }
         }
     }
-    store_rows<T, VEC, U>(gx + i * B, acc, b0, B, bad);
+    store_rows<S, VEC, U>(gx + i * B, acc, b0, B, bad);
 }
 
 // Discrete forward with the argmax slot, relaxed formula (exact on {0, 1} inputs).
-template <typename T, int VEC, int U>
-__global__ __launch_bounds__(256) void k_dense_eval(const T* __restrict__ x,
+template <typename S, int VEC, int U>
+__global__ __launch_bounds__(256) void k_dense_eval(const S* __restrict__ x,
                                                     const int64_t* __restrict__ a,
                                                     const int64_t* __restrict__ b,
                                                     const uint8_t* __restrict__ wslot,
                                                     const uint8_t* __restrict__ gs,
-                                                    T* __restrict__ y, int64_t in_dim,
+                                                    S* __restrict__ y, int64_t in_dim,
                                                     int64_t out_dim, int64_t B, int G) {
+    using A = acc_t<S>;
     const int64_t o = int64_t(blockIdx.x) * kWaves + wave_id();
     if (o >= out_dim) return;
     const int64_t b0 = int64_t(blockIdx.y) * (kWave * VEC * U) + int64_t(lane_id()) * VEC;
     const int s = wslot[o];
     bool bad = s >= G;
     int64_t ia = 0, ib = 0;
-    Coef4<T> c{T(0), T(0), T(0), T(0)};
+    Coef4<A> c{A(0), A(0), A(0), A(0)};
     if (!bad) {
         ia = a[o * G + s];
         ib = b[o * G + s];
-        c = gate_coef<T>(gs[o * G + s]);
+        c = gate_coef<A>(gs[o * G + s]);
         bad = uint64_t(ia) >= uint64_t(in_dim) || uint64_t(ib) >= uint64_t(in_dim);
     }
-    Vec<T, VEC> acc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[u].v[v] = T(0);
-    if (!bad) accum_run<T, VEC, U>(acc, x + ia * B, x + ib * B, c, b0, B);
-    store_rows<T, VEC, U>(y + o * B, acc, b0, B, bad);
+    Vec<A, VEC> acc[U];
+    zero_acc(acc);
+    if (!bad) accum_run<S, VEC, U>(acc, x + ia * B, x + ib * B, c, b0, B);
+    store_rows<S, VEC, U>(y + o * B, acc, b0, B, bad);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -334,7 +341,7 @@ extern "C" int cl_dense_forward(int dtype, const void* x, const int64_t* a, cons
     if (out_dim == 0 || batch == 0) return CL_OK;
     CL_ARG(in_dim > 0, "in_dim is 0 but out_dim > 0");
     CL_ARG(x && a && b && w && gate_seq && y, "null pointer argument");
-    CL_DTYPE_SWITCH(dtype, {
+    CL_DTYPE_SWITCH_F16(dtype, {
         const int vec = pick_vec<scalar_t>(batch, {x, y});
         const dim3 grid = rows_grid(out_dim, batch, vec, kChunkUnroll);
         auto* xs = static_cast<const scalar_t*>(x);
@@ -361,7 +368,7 @@ extern "C" int cl_dense_backward_w(int dtype, const void* x, const int64_t* a, c
     CL_ARG(a && b && gate_seq && grad_w, "null pointer argument");
     CL_ARG(batch == 0 || (x && grad_y), "null pointer argument");
     CL_ARG(in_dim > 0 || batch == 0, "in_dim is 0 but out_dim > 0");
-    CL_DTYPE_SWITCH(dtype, {
+    CL_DTYPE_SWITCH_F16(dtype, {
         const int vec = pick_vec<scalar_t>(batch, {x, grad_y});
         const dim3 grid(unsigned(ceil_div(out_dim, kWaves)), 1, 1);
         auto* xs = static_cast<const scalar_t*>(x);
@@ -391,7 +398,7 @@ extern "C" int cl_dense_backward_x(int dtype, const void* x, const int64_t* a, c
     CL_ARG(num_entries >= 0, "negative num_entries");
     CL_ARG(x && a && b && w && gate_seq && grad_y && start && grad_x, "null pointer argument");
     CL_ARG(num_entries == 0 || (y_index && gate_code), "null inverse-index pointer");
-    CL_DTYPE_SWITCH(dtype, {
+    CL_DTYPE_SWITCH_F16(dtype, {
         const int vec = pick_vec<scalar_t>(batch, {x, grad_y, grad_x});
         const dim3 grid = rows_grid(in_dim, batch, vec, kChunkUnroll);
         auto* xs = static_cast<const scalar_t*>(x);
@@ -420,7 +427,7 @@ extern "C" int cl_dense_eval(int dtype, const void* x, const int64_t* a, const i
     if (out_dim == 0 || batch == 0) return CL_OK;
     CL_ARG(in_dim > 0, "in_dim is 0 but out_dim > 0");
     CL_ARG(x && a && b && w_slot && gate_seq && y, "null pointer argument");
-    CL_DTYPE_SWITCH(dtype, {
+    CL_DTYPE_SWITCH_F16(dtype, {
         const int vec = pick_vec<scalar_t>(batch, {x, y});
         const dim3 grid = rows_grid(out_dim, batch, vec, kChunkUnroll);
         auto* xs = static_cast<const scalar_t*>(x);

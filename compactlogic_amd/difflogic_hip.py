@@ -39,6 +39,19 @@ def dtype_code(t: torch.Tensor) -> int:
                            "and float64") from None
 
 
+def dense_dtype_code(t: torch.Tensor) -> int:
+    """dtype code for the four reference-interface dense kernels, which also take float16
+    (half storage, fp32 sums), as the reference dispatches them over half
+    (compactlogic/cuda/difflogic_kernel.cu:222,267,315,397)."""
+    if t.dtype == torch.float16:
+        return _capi.CL_DTYPE_F16
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported floating dtype {t.dtype}; the dense kernels take "
+                           "float16, float32 and float64") from None
+
+
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -70,7 +83,7 @@ def forward(x, a, b, w, gate_seq):
         raise RuntimeError("a, b, w and gate_seq must all be [out_dim, num_gates]")
     y = torch.empty((out_dim, batch), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_dense_forward", dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(w),
+        _capi.call("cl_dense_forward", dense_dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(w),
                    ptr(gate_seq), ptr(y), in_dim, out_dim, batch, g, stream_of(x))
     return y
 
@@ -86,7 +99,7 @@ def backward_w(x, a, b, gate_seq, grad_y):
         raise RuntimeError("grad_y must be [out_dim, batch] with the dtype of x")
     grad_w = torch.empty((out_dim, g), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_dense_backward_w", dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(gate_seq),
+        _capi.call("cl_dense_backward_w", dense_dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(gate_seq),
                    ptr(grad_y), ptr(grad_w), in_dim, out_dim, batch, g, stream_of(x))
     return grad_w
 
@@ -112,7 +125,7 @@ def backward_x(x, a, b, w, gate_seq, grad_y, given_x_indices_of_y_start, given_x
         raise RuntimeError("given_x_indices_of_y and given_x_indices_of_gate differ in length")
     grad_x = torch.empty_like(x)
     with torch.cuda.device(x.device):
-        _capi.call("cl_dense_backward_x", dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(w),
+        _capi.call("cl_dense_backward_x", dense_dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(w),
                    ptr(gate_seq), ptr(grad_y), ptr(given_x_indices_of_y_start),
                    ptr(given_x_indices_of_y), ptr(given_x_indices_of_gate),
                    given_x_indices_of_y.numel(), ptr(grad_x), in_dim, out_dim, batch, g,
@@ -164,7 +177,7 @@ def eval(x, a, b, w, gate_seq):  # noqa: A001 - mirrors difflogic_cuda.eval
         raise RuntimeError("w must hold one slot per neuron")
     y = torch.empty((out_dim, batch), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_dense_eval", dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(w),
+        _capi.call("cl_dense_eval", dense_dtype_code(x), ptr(x), ptr(a), ptr(b), ptr(w),
                    ptr(gate_seq), ptr(y), in_dim, out_dim, batch, g, stream_of(x))
     return y
 

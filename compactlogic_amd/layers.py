@@ -381,6 +381,14 @@ class LogicLayer(torch.nn.Module):
         assert x.ndim == 2, x.ndim
         x = to_rows(x)
         assert x.shape[0] == self.in_dim, (x.shape, self.in_dim)
+        if x.dtype == torch.float16:
+            # half: the reference-interface kernels (half storage, fp32 sums) with the
+            # reference's own argument list and inverse index
+            w = torch.nn.functional.softmax(self.weights, dim=-1).to(x.dtype)
+            return LogicLayerCudaFunction.apply(
+                x, self.indices[0], self.indices[1], w, self.gate_sequence,
+                self.given_x_indices_of_y_start, self.given_x_indices_of_y,
+                self.given_x_indices_of_gate).transpose(0, 1)
         plan = self.run_plan()
         if self.weights.dtype == x.dtype:
             # softmax(weights) and its backward run inside the kernels
@@ -1130,15 +1138,33 @@ class GroupSum(torch.nn.Module):
         self.device = device
 
     def forward(self, x):
+        """[..., features] -> [..., k] (any leading dims, as the reference's reshape-and-sum);
+        features not divisible by k are summed as if zero-padded to the next multiple."""
         if isinstance(x, PackBitsTensor):
             return x.group_sum(self.k)
-        return GroupSumFunction.apply(x, self.k, self.tau)
+        if x.dtype == torch.float16:
+            # half scores from fp32 sums (torch's half sum in the reference accumulates in
+            # fp32 as well); the gradient is cast back by autograd
+            return self(x.float()).to(torch.float16)
+        if x.dim() == 2:
+            return GroupSumFunction.apply(x, self.k, self.tau)
+        if x.dim() == 0:
+            raise RuntimeError("GroupSum needs an input with a feature dimension")
+        lead = x.shape[:-1]
+        out = GroupSumFunction.apply(x.reshape(-1, x.shape[-1]), self.k, self.tau)
+        return out.reshape(*lead, self.k)
 
     def cross_entropy(self, x, labels, ignore_index: int = -100, return_scores: bool = False):
         """torch.nn.functional.cross_entropy(self(x), labels, ignore_index=ignore_index) in one
         fused op (mean over the samples whose label is not ignore_index); with return_scores,
         also the scores self(x) (not differentiable through this call)."""
-        loss, out = GroupSumCrossEntropyFunction.apply(x, labels, self.k, self.tau, ignore_index)
+        if isinstance(x, torch.Tensor) and x.dtype == torch.float16:
+            loss, out = GroupSumCrossEntropyFunction.apply(x.float(), labels, self.k, self.tau,
+                                                           ignore_index)
+            loss, out = loss.to(torch.float16), out.to(torch.float16)
+        else:
+            loss, out = GroupSumCrossEntropyFunction.apply(x, labels, self.k, self.tau,
+                                                           ignore_index)
         return (loss, out) if return_scores else loss
 
     def extra_repr(self):

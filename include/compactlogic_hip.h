@@ -11,7 +11,10 @@
  *   - The return value is CL_OK (0) or one of the CL_ERR_* codes; cl_last_error() then
  *     describes the failure for the calling thread.  No entry point exits the process.
  *   - `dtype` selects the floating-point element type of the float buffers: CL_DTYPE_F32 or
- *     CL_DTYPE_F64.
+ *     CL_DTYPE_F64; the four reference-interface dense entry points (cl_dense_forward,
+ *     cl_dense_backward_w, cl_dense_backward_x, cl_dense_eval) also take CL_DTYPE_F16
+ *     (IEEE half storage, sums in fp32), as the reference dispatches them over half
+ *     (difflogic_kernel.cu:222,267,315,397).
  *   - Index buffers keep the reference's types: connection indices int64, gate opcodes
  *     uint8, argmax slots uint8, backward-index starts / neuron ids int64, gate codes int8.
  *   - Out-of-range indices never cause an out-of-bounds access: the affected outputs are
@@ -39,6 +42,7 @@ extern "C" {
 
 #define CL_DTYPE_F32 0
 #define CL_DTYPE_F64 1
+#define CL_DTYPE_F16 2
 
 /* ABI version of this header; bumped on any incompatible change. */
 int cl_abi_version(void);

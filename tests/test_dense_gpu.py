@@ -87,6 +87,66 @@ def test_dropin_kernels_match_oracle(device, dtype, shape):
     np.testing.assert_allclose(np_(gx2), np_(gx), **TOL[dtype])
 
 
+@pytest.mark.parametrize("shape", SHAPES)
+def test_dropin_kernels_half_match_oracle(device, shape):
+    """float16 storage, as the reference dispatches these kernels over half
+    (difflogic_kernel.cu:222,267,315,397): the oracle runs in float64 on the half-rounded
+    inputs; the kernels sum in fp32 and round once, so the results stay within a few half
+    ulps (rtol 2e-3) of it."""
+    in_dim, out_dim, g_n, batch, shared = shape
+    L = make_layer(hash(shape) % 1000 + 7, in_dim, out_dim, g_n, batch, shared)
+    half = {k: torch.as_tensor(L[k]).half() for k in ("x", "w", "gy")}
+    R = dict(L, **{k: v.double().numpy() for k, v in half.items()})
+    D = to_dev(L, device, torch.float16)
+    for k, v in half.items():
+        D[k] = v.to(device).contiguous()
+    y = dl.forward(D["x"], D["a"], D["b"], D["w"], D["gs"])
+    assert y.dtype == torch.float16
+    np.testing.assert_allclose(np_(y).astype(np.float64),
+                               O.dense_forward(R["x"], R["a"], R["b"], R["w"], R["gs"]),
+                               rtol=2e-3, atol=1e-3)
+    gw = dl.backward_w(D["x"], D["a"], D["b"], D["gs"], D["gy"])
+    rgw = O.dense_backward_w(R["x"], R["a"], R["b"], R["gs"], R["gy"])
+    np.testing.assert_allclose(np_(gw).astype(np.float64), rgw, rtol=2e-3,
+                               atol=2e-3 * max(1e-3, float(np.abs(rgw).max())))
+    start, yidx, code = O.backward_index(np.stack([L["a"], L["b"]]), in_dim)
+    gx = dl.backward_x(D["x"], D["a"], D["b"], D["w"], D["gs"], D["gy"],
+                       torch.as_tensor(start, device=device), torch.as_tensor(yidx, device=device),
+                       torch.as_tensor(code, device=device))
+    rgx = O.dense_backward_x_direct(R["x"], R["a"], R["b"], R["w"], R["gs"], R["gy"])
+    np.testing.assert_allclose(np_(gx).astype(np.float64), rgx, rtol=2e-3,
+                               atol=2e-3 * max(1e-4, float(np.abs(rgx).max())))
+    # the discrete eval on {0, 1} inputs is exact in half
+    xb = (D["x"] > 0.5).half()
+    slot = torch.as_tensor(np.random.default_rng(1).integers(0, g_n, out_dim).astype(np.uint8),
+                           device=device)
+    assert torch.equal(dl.eval(xb, D["a"], D["b"], slot, D["gs"]).float(),
+                       dl.eval(xb.float(), D["a"], D["b"], slot, D["gs"]))
+
+
+def test_half_logic_layer_trains_through_the_reference_kernels(device):
+    """A LogicLayer fed float16 (fp32 logits, as the reference's forward_cuda casts its softmax
+    to the input dtype) runs the half kernels forward and backward; a float32 copy of the same
+    network gives the same loss and gradients within half rounding."""
+    torch.manual_seed(4)
+    net = torch.nn.Sequential(cl.LogicLayer(96, 300), cl.LogicLayer(300, 200),
+                              cl.GroupSum(10, 4.0)).to(device)
+    x = (torch.rand((256, 96), device=device) < 0.5).float()
+    y = torch.randint(0, 10, (256,), device=device)
+    loss32 = torch.nn.functional.cross_entropy(net(x), y)
+    loss32.backward()
+    g32 = [m.weights.grad.clone() for m in net[:2]]
+    net.zero_grad(set_to_none=True)
+    out16 = net(x.half())
+    assert out16.dtype == torch.float16
+    loss16 = torch.nn.functional.cross_entropy(out16.float(), y)
+    loss16.backward()
+    np.testing.assert_allclose(float(loss16.detach()), float(loss32.detach()), rtol=2e-3)
+    for m, ref in zip(net[:2], g32):
+        scale = float(ref.abs().max())
+        np.testing.assert_allclose(np_(m.weights.grad), np_(ref), rtol=2e-2, atol=2e-2 * scale)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_run_plan_kernels_match_oracle(device, dtype, shape):

@@ -39,6 +39,24 @@ def test_group_sum_forward_backward(device, batch, feats, k, layout, dtype):
         assert gx.t().is_contiguous(), "gradient should keep the [features, batch] layout"
 
 
+@pytest.mark.parametrize("shape,k", [((4, 3, 60), 10), ((2, 5, 7, 33), 4), ((90,), 9)])
+def test_group_sum_any_leading_dims(device, shape, k):
+    """[..., features] -> [..., k], as the reference's reshape-and-sum
+    (compactlogic/compactlogic.py:460-465), with its gradient."""
+    rng = np.random.default_rng(len(shape) + k)
+    xn = rng.random(shape)
+    x = torch.as_tensor(xn, device=device).requires_grad_(True)
+    out = cl.GroupSum(k, 3.0)(x)
+    assert out.shape == shape[:-1] + (k,)
+    flat = xn.reshape(-1, shape[-1])
+    np.testing.assert_allclose(out.detach().cpu().numpy().reshape(-1, k),
+                               O.group_sum(flat, k, 3.0), rtol=1e-12, atol=1e-12)
+    g = rng.standard_normal(out.shape)
+    (gx,) = torch.autograd.grad(out, x, torch.as_tensor(g, device=device))
+    ref = O.group_sum_backward(g.reshape(-1, k), shape[-1], k, 3.0).reshape(shape)
+    np.testing.assert_allclose(gx.cpu().numpy(), ref, rtol=1e-12, atol=1e-12)
+
+
 def test_group_sum_network_head(device):
     torch.manual_seed(0)
     model = torch.nn.Sequential(cl.LogicLayer(50, 60), cl.GroupSum(10, 2.0)).to(device)
