@@ -44,6 +44,7 @@ struct TreeDims {
     int complete;
     int P;  // items per (sample, channel): pooled windows (complete) or conv positions
     FastDiv div_p, div_wp;  // by P, and by the windows per pooled row (complete) or wo
+    FastDiv div_wo;         // by wo (conv positions -> rows)
 };
 
 // Decoded tap: channel, row and column offset relative to the output position (pad removed).
@@ -296,26 +297,38 @@ struct TreeLds {
 constexpr int kTapFlagIrregular = 1;
 constexpr int kTapFlagBad = 2;
 
-template <typename T, bool COMPLETE, bool INTER>
-__device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* __restrict__ w_prob,
-                                             const int32_t* __restrict__ sel, const TreeDims& d,
-                                             const TreeLds& g, T* __restrict__ y,
-                                             T* __restrict__ x2, T* __restrict__ x3,
-                                             int32_t* __restrict__ idx) {
-    constexpr int NODES = COMPLETE ? 7 : 4;
-    constexpr int NK = NODES * 4;
-    extern __shared__ __align__(16) unsigned char tree_lds[];
-    const int n = blockIdx.x;
-    const int c_lo = blockIdx.y * g.cg;
-    const int c_n = min(g.cg, d.cout - c_lo);
-    const int planes = d.cin * g.cs;
-    T* plane = reinterpret_cast<T*>(tree_lds);
-    T* coef = plane + planes;                                        // [cg][NK]
-    int* toff = reinterpret_cast<int*>(coef + g.cg * NK);            // [cg][8]
-    int* tflag = toff + g.cg * kTaps;                                // [cg]
-    const int tid = threadIdx.x, nt = blockDim.x;
+// LDS of a staged workgroup: the sample's planes, then per channel of the group its NK
+// collapsed coefficients, its 8 tap offsets (bytes) and its flag.
+template <typename T, int NK>
+struct StagedLds {
+    T* plane;
+    T* coef;
+    int* toff;
+    int* tflag;
+};
 
-    for (int i = tid; i < planes; i += nt) plane[i] = T(0);
+template <typename T, int NK>
+__device__ __forceinline__ StagedLds<T, NK> staged_lds(unsigned char* raw, const TreeDims& d,
+                                                       const TreeLds& g) {
+    StagedLds<T, NK> L;
+    L.plane = reinterpret_cast<T*>(raw);
+    L.coef = L.plane + d.cin * g.cs;                             // [cg][NK]
+    L.toff = reinterpret_cast<int*>(L.coef + g.cg * NK);         // [cg][8]
+    L.tflag = L.toff + g.cg * kTaps;                             // [cg]
+    return L;
+}
+
+// Prologue of the staged kernels (whole workgroup, ends with a barrier): the channel group's
+// collapsed coefficients (the order of load_channel), tap offsets and flags, and sample n's
+// zero-padded input.
+template <typename T, int NODES>
+__device__ __forceinline__ void stage_sample(const T* __restrict__ x, const T* __restrict__ w_prob,
+                                             const int32_t* __restrict__ sel, const TreeDims& d,
+                                             const TreeLds& g, int n, int c_lo, int c_n,
+                                             const StagedLds<T, NODES * 4>& L) {
+    const int planes = d.cin * g.cs;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int i = tid; i < planes; i += nt) L.plane[i] = T(0);
     // One thread per (channel, node): the four coefficients in the order of load_channel.
     for (int i = tid; i < c_n * NODES; i += nt) {
         const T* p = w_prob + (int64_t(c_lo) * NODES + i) * 16;
@@ -329,10 +342,10 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
             a2 = fma(pg, cf.c2, a2);
             a3 = fma(pg, cf.c3, a3);
         }
-        coef[i * 4 + 0] = a0;
-        coef[i * 4 + 1] = a1;
-        coef[i * 4 + 2] = a2;
-        coef[i * 4 + 3] = a3;
+        L.coef[i * 4 + 0] = a0;
+        L.coef[i * 4 + 1] = a1;
+        L.coef[i * 4 + 2] = a2;
+        L.coef[i * 4 + 3] = a3;
     }
     __syncthreads();
     for (int cc = tid; cc < c_n; cc += nt) {
@@ -343,14 +356,14 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
             if (ch >= d.cin) flag |= kTapFlagBad;
             if (row >= g.kh || col >= g.kw) flag |= kTapFlagIrregular;
             const uint32_t cq = fast_div(uint32_t(col), g.div_sw);
-            toff[cc * kTaps + k] =  // bytes
+            L.toff[cc * kTaps + k] =  // bytes
                 (ch * g.cs + row * g.rp + (col - int(cq) * d.sw) * g.ws + int(cq)) *
                 int(sizeof(T));
         }
-        tflag[cc] = flag;
-        if (flag) {  // skipped here (k_tree_fwd_fix): its dead lanes read word 0 instead
+        L.tflag[cc] = flag;
+        if (flag) {  // skipped by the staged kernels (a fix-up kernel takes it)
 #pragma unroll
-            for (int k = 0; k < kTaps; ++k) toff[cc * kTaps + k] = 0;
+            for (int k = 0; k < kTaps; ++k) L.toff[cc * kTaps + k] = 0;  // in-bounds reads
         }
     }
     {
@@ -362,10 +375,31 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
             const int iy = int(fast_div(uint32_t(rem), g.div_w));
             const int ix = rem - iy * d.w + d.pw;
             const int xq = int(fast_div(uint32_t(ix), g.div_sw));
-            plane[ch * g.cs + (iy + d.ph) * g.rp + (ix - xq * d.sw) * g.ws + xq] = xn[e];
+            L.plane[ch * g.cs + (iy + d.ph) * g.rp + (ix - xq * d.sw) * g.ws + xq] = xn[e];
         }
     }
     __syncthreads();
+}
+
+template <typename T, bool COMPLETE, bool INTER>
+__device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* __restrict__ w_prob,
+                                             const int32_t* __restrict__ sel, const TreeDims& d,
+                                             const TreeLds& g, T* __restrict__ y,
+                                             T* __restrict__ x2, T* __restrict__ x3,
+                                             int32_t* __restrict__ idx) {
+    constexpr int NODES = COMPLETE ? 7 : 4;
+    constexpr int NK = NODES * 4;
+    extern __shared__ __align__(16) unsigned char tree_lds[];
+    const int n = blockIdx.x;
+    const int c_lo = blockIdx.y * g.cg;
+    const int c_n = min(g.cg, d.cout - c_lo);
+    const StagedLds<T, NK> L = staged_lds<T, NK>(tree_lds, d, g);
+    T* plane = L.plane;
+    const T* coef = L.coef;
+    const int* toff = L.toff;
+    const int* tflag = L.tflag;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    stage_sample<T, NODES>(x, w_prob, sel, d, g, n, c_lo, c_n, L);
 
     const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
     const int cpw = g.ip >= 64 ? 1 : 64 / g.ip;
@@ -547,6 +581,87 @@ __global__ __launch_bounds__(256) void k_tree_fwd_fix(const T* __restrict__ x,
     }
 }
 
+// Backward through nodes 6, 4 and 5 of the complete block at one position: the upstream
+// gradients gc of the four conv gates, and the moments of nodes 4, 5 and 6.
+template <typename T, typename K>
+__device__ __forceinline__ void node_grads(const K& k, const T* g, const T* t, T gy, T* gc,
+                                           T* mom) {
+    const T gt0 = gy * fma(k[6][3], t[1], k[6][1]);
+    const T gt1 = gy * fma(k[6][3], t[0], k[6][2]);
+    gc[0] = gt0 * fma(k[4][3], g[1], k[4][1]);
+    gc[1] = gt0 * fma(k[4][3], g[0], k[4][2]);
+    gc[2] = gt1 * fma(k[5][3], g[3], k[5][1]);
+    gc[3] = gt1 * fma(k[5][3], g[2], k[5][2]);
+    const T gts[2] = {gt0, gt1};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const T a = g[2 * j], b = g[2 * j + 1], gg = gts[j];
+        mom[(4 + j) * 4 + 0] += gg * a * b;
+        mom[(4 + j) * 4 + 1] += gg * a;
+        mom[(4 + j) * 4 + 2] += gg * b;
+        mom[(4 + j) * 4 + 3] += gg;
+    }
+    mom[24] += gy * t[0] * t[1];
+    mom[25] += gy * t[0];
+    mom[26] += gy * t[1];
+    mom[27] += gy;
+}
+
+// Moments of the four conv gates (nodes 0..3) at one position: taps v, upstream gradients gc.
+template <typename T>
+__device__ __forceinline__ void gate_moments(const T* v, const T* gc, T* mom) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const T a = v[2 * q], b = v[2 * q + 1], g = gc[q];
+        mom[q * 4 + 0] += g * a * b;
+        mom[q * 4 + 1] += g * a;
+        mom[q * 4 + 2] += g * b;
+        mom[q * 4 + 3] += g;
+    }
+}
+
+// One item of the backward node pass with global taps: (sample, window) of channel c for the
+// complete block (recomputed at the window's winner), (sample, position) otherwise; adds its
+// node moments to mom[node * 4 + (gab, ga, gb, g)] and stores the four conv-gate gradients
+// when gconv is given (complete block).
+template <typename T, bool COMPLETE>
+__device__ __forceinline__ void nodes_item(const T* __restrict__ grad_y, const T* __restrict__ x,
+                                           const int32_t* __restrict__ idx, const TreeDims& d,
+                                           const TapOff* st, T (*sk)[4], int c, int64_t item,
+                                           int64_t total, T* __restrict__ gconv, T* mom) {
+    int n, p;
+    if (total < (int64_t(1) << 31)) {  // uniform: 32-bit multiply-shift division
+        n = int(fast_div(uint32_t(item), d.div_p));
+        p = int(item) - n * d.P;
+    } else {
+        n = int(item / d.P);
+        p = int(item % d.P);
+    }
+    const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
+    const int64_t cell = int64_t(n) * d.cout + c;
+    T gc[4];
+    Eval<T, COMPLETE> e;
+    if constexpr (COMPLETE) {
+        const int win = idx[cell * d.P + p];
+        const bool live = win >= 0 && win < d.ho * d.wo;
+        const int w0 = live ? win : 0;
+        const int wy = int(fast_div(uint32_t(w0), d.div_wo));
+        eval_at<T, true>(xn, d, st, sk, wy, w0 - wy * d.wo, e);
+        const T gy = live ? grad_y[cell * d.P + p] : T(0);
+        node_grads<T>(sk, e.g, e.t, gy, gc, mom);
+        if (gconv) {  // only the input gradient reads them
+#pragma unroll
+            for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gc[q];
+        }
+    } else {
+        const int oy = int(fast_div(uint32_t(p), d.div_wo));
+        eval_at<T, false>(xn, d, st, sk, oy, p - oy * d.wo, e);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) gc[q] = grad_y[(cell * d.P + p) * 4 + q];
+    }
+    gate_moments<T>(e.v, gc, mom);
+}
+
 // ------------------------------------------------------------------------------------------
 // Backward, node part: per item the upstream gradients of the four conv gates (gconv, complete
 // only; the conv-only block reads them from grad_y) and the node moments, reduced over the
@@ -577,57 +692,11 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
     for (int i = 0; i < NM; ++i) mom[i] = T(0);
     // kNodeItems items per thread (strided by the workgroup size), so the moments of that many
     // items are summed in registers before the wave reductions
+    const int64_t total = int64_t(d.n) * d.P;
     for (int it = 0; it < kNodeItems; ++it) {
         const int64_t item = (int64_t(blockIdx.x) * kNodeItems + it) * 256 + threadIdx.x;
-        if (item >= int64_t(d.n) * d.P) break;
-        const int n = int(item / d.P), p = int(item % d.P);
-        const T* xn = x + int64_t(n) * d.cin * d.h * d.w;
-        const int64_t cell = int64_t(n) * d.cout + c;
-        T gc[4];
-        Eval<T, COMPLETE> e;
-        if constexpr (COMPLETE) {
-            const int win = idx[cell * d.P + p];
-            const bool live = win >= 0 && win < d.ho * d.wo;
-            const int w0 = live ? win : 0;
-            eval_at<T, true>(xn, d, st, sk, w0 / d.wo, w0 % d.wo, e);
-            const T gy = live ? grad_y[cell * d.P + p] : T(0);
-            const T gt0 = gy * fma(sk[6][3], e.t[1], sk[6][1]);
-            const T gt1 = gy * fma(sk[6][3], e.t[0], sk[6][2]);
-            gc[0] = gt0 * fma(sk[4][3], e.g[1], sk[4][1]);
-            gc[1] = gt0 * fma(sk[4][3], e.g[0], sk[4][2]);
-            gc[2] = gt1 * fma(sk[5][3], e.g[3], sk[5][1]);
-            gc[3] = gt1 * fma(sk[5][3], e.g[2], sk[5][2]);
-            if (gconv) {  // only the input gradient reads them
-#pragma unroll
-                for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gc[q];
-            }
-            const T gts[2] = {gt0, gt1};
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const T a = e.g[2 * j], b = e.g[2 * j + 1], g = gts[j];
-                mom[(4 + j) * 4 + 0] += g * a * b;
-                mom[(4 + j) * 4 + 1] += g * a;
-                mom[(4 + j) * 4 + 2] += g * b;
-                mom[(4 + j) * 4 + 3] += g;
-            }
-            mom[24] += gy * e.t[0] * e.t[1];
-            mom[25] += gy * e.t[0];
-            mom[26] += gy * e.t[1];
-            mom[27] += gy;
-        } else {
-            const int oy = p / d.wo, ox = p % d.wo;
-            eval_at<T, false>(xn, d, st, sk, oy, ox, e);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) gc[q] = grad_y[(cell * d.P + p) * 4 + q];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const T a = e.v[2 * q], b = e.v[2 * q + 1], g = gc[q];
-            mom[q * 4 + 0] += g * a * b;
-            mom[q * 4 + 1] += g * a;
-            mom[q * 4 + 2] += g * b;
-            mom[q * 4 + 3] += g;
-        }
+        if (item >= total) break;
+        nodes_item<T, COMPLETE>(grad_y, x, idx, d, st, sk, c, item, total, gconv, mom);
     }
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
@@ -721,7 +790,7 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
                     if constexpr (COMPLETE) win = on[i] ? idx[cell[i] * d.P + p] : -1;
                     const bool wok = on[i] && win >= 0 && win < d.ho * d.wo;
                     const int w0 = wok ? win : 0;
-                    const int oy = w0 / d.wo, ox = w0 % d.wo;
+                    const int oy = int(fast_div(uint32_t(w0), d.div_wo)), ox = w0 - oy * d.wo;
                     const int iy = oy * d.sh + tk[i].dy, ix = ox * d.sw + tk[i].dx;
                     const bool ok = wok && iy >= 0 && iy < d.h && ix >= 0 && ix < d.w;
                     tgt[i] = ok ? iy * d.w + ix : -1;
@@ -1064,6 +1133,7 @@ int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t
     d.P = int(P);
     d.div_p = make_fastdiv(uint32_t(std::max<int64_t>(P, 1)));
     d.div_wp = make_fastdiv(uint32_t(std::max<int64_t>(complete ? wo / 2 : wo, 1)));
+    d.div_wo = make_fastdiv(uint32_t(std::max<int64_t>(wo, 1)));
     return CL_OK;
 }
 
@@ -1080,21 +1150,22 @@ constexpr int64_t kFwdLdsLimit = 160 * 1024;  // LDS of one gfx950 CU
 constexpr int kFwdLdsThreads = 1024;
 constexpr int kMaxDevices = 64;
 
-// Geometry of the LDS-staged forward, or false when one sample's padded input does not fit.
+// Geometry of an LDS-staged kernel with `ip` items per (sample, channel), or false when one
+// sample's padded input does not fit or staging does not pay: a sample's items must number
+// at least `ratio` times its input elements (the forward asks 2; conv1 of the tree reading of
+// cfg3 has 7).
 template <typename T>
-bool plan_tree_fwd_lds(const TreeDims& d, int kh, int kw, TreeLds& g, int& groups,
-                       int64_t& lds) {
+bool plan_tree_lds(const TreeDims& d, int kh, int kw, int ip, int ratio, TreeLds& g,
+                   int& groups, int64_t& lds) {
     const int hpad = d.h + 2 * d.ph, wpad = d.w + 2 * d.pw;
     g.kh = kh;
     g.kw = kw;
     g.ws = (wpad + d.sw - 1) / d.sw;
-    g.ip = d.complete ? 4 * d.P : d.P;
+    g.ip = ip;
     const int base = d.sw * g.ws;
     const int64_t tab = int64_t(d.complete ? 28 : 16) * sizeof(T) + (kTaps + 1) * 4;
-    // Staging pays when a sample's items outnumber its input elements (conv1 of the tree
-    // reading of cfg3: 7 per element); below two per element the global gather is kept.
     const int64_t staged = int64_t(d.cin) * d.h * d.w;
-    if (int64_t(d.cout) * g.ip < 2 * staged) return false;
+    if (int64_t(d.cout) * g.ip < ratio * staged) return false;
     auto total = [&](int rp, int64_t cg) {
         return int64_t(d.cin) * hpad * rp * int64_t(sizeof(T)) + cg * tab;
     };
@@ -1116,7 +1187,7 @@ bool plan_tree_fwd_lds(const TreeDims& d, int kh, int kw, TreeLds& g, int& group
     // as LDS needs.
     int64_t G = 1;
     while (int64_t(d.n) * G < 512 && 2 * G <= d.cout &&
-           ceil_div(d.cout, 2 * G) * g.ip >= 2 * staged)
+           ceil_div(d.cout, 2 * G) * g.ip >= staged)
         G *= 2;
     while (total(rp, ceil_div(d.cout, G)) > kFwdLdsLimit) ++G;
     g.cg = int(ceil_div(d.cout, G));
@@ -1127,6 +1198,26 @@ bool plan_tree_fwd_lds(const TreeDims& d, int kh, int kw, TreeLds& g, int& group
     g.div_w = make_fastdiv(uint32_t(d.w));
     g.div_sw = make_fastdiv(uint32_t(d.sw));
     return groups < 65536;
+}
+
+// Above 64 KiB of LDS a kernel needs the attribute, set once per device and kernel.
+template <typename K>
+int reserve_lds(K* kern, int64_t lds, bool* reserved, const char* what) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("cannot query the device");
+        return CL_ERR_HIP;
+    }
+    if (lds > 64 * 1024 && !reserved[dev]) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                int(kFwdLdsLimit)) != hipSuccess) {
+            set_error("cannot reserve %lld bytes of LDS for %s", (long long)lds, what);
+            return CL_ERR_HIP;
+        }
+        reserved[dev] = true;
+    }
+    return CL_OK;
 }
 
 template <typename T, bool COMPLETE>
@@ -1141,23 +1232,9 @@ int launch_tree_fwd_lds(const TreeDims& d, const TreeLds& g, int groups, int64_t
     } else {
         kern = inter ? &k_tree_fwd_lds<T, COMPLETE, true> : &k_tree_fwd_lds<T, COMPLETE, false>;
     }
-    // Above 64 KiB the kernel needs the attribute, set once per device and instantiation.
-    static bool reserved[kMaxDevices] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        set_error("cannot query the device");
-        return CL_ERR_HIP;
-    }
-    if (lds > 64 * 1024 && !reserved[dev]) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                int(kFwdLdsLimit)) != hipSuccess) {
-            set_error("cannot reserve %lld bytes of LDS for the tree block forward",
-                      (long long)lds);
-            return CL_ERR_HIP;
-        }
-        reserved[dev] = true;
-    }
+    static bool reserved[2][kMaxDevices] = {};  // per kernel chosen below
+    if (int rc = reserve_lds(kern, lds, reserved[inter ? 1 : 0], "the tree block forward"))
+        return rc;
     kern<<<dim3(unsigned(d.n), unsigned(groups)), kFwdLdsThreads, size_t(lds), s>>>(
         x, w_prob, sel, d, g, y, x2, x3, idx);
     if (int rc = check_launch("cl_tree_conv_forward")) return rc;
@@ -1166,10 +1243,15 @@ int launch_tree_fwd_lds(const TreeDims& d, const TreeLds& g, int groups, int64_t
     return check_launch("cl_tree_conv_forward");
 }
 
+// Partial moment blocks per channel of the backward node pass: one per kNodeItems * 256 items.
+inline int64_t node_blocks(const TreeDims& d) {
+    return ceil_div(int64_t(d.n) * d.P, 256 * kNodeItems);
+}
+
 template <typename T>
 int64_t tree_workspace_bytes(const TreeDims& d) {
     const int nodes = d.complete ? 7 : 4;
-    const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256 * kNodeItems);
+    const int64_t nblk = node_blocks(d);
     int64_t b = 0;
     if (d.complete) b += int64_t(d.n) * d.cout * d.P * 4 * sizeof(T);  // gconv
     b = (b + 255) / 256 * 256;
@@ -1205,7 +1287,8 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
         TreeLds g;
         int groups = 0;
         int64_t lds = 0;
-        if (plan_tree_fwd_lds<T>(d, kernel_h, kernel_w, g, groups, lds)) {
+        if (plan_tree_lds<T>(d, kernel_h, kernel_w, complete ? 4 * d.P : d.P, 2, g, groups,
+                             lds)) {
             const T* xs = static_cast<const T*>(x);
             const T* ws = static_cast<const T*>(w_prob);
             if (complete)
@@ -1278,7 +1361,7 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
         CL_ARG(workspace && workspace_bytes >= need,
                "workspace of %lld bytes needed (see cl_tree_conv_workspace)", (long long)need);
         CL_ARG(aligned(workspace, 256), "workspace must be 256-byte aligned");
-        const int64_t nblk = ceil_div(int64_t(d.n) * d.P, 256 * kNodeItems);
+        const int64_t nblk = node_blocks(d);
         unsigned char* ws = static_cast<unsigned char*>(workspace);
         T* gconv = nullptr;
         int64_t off = 0;
@@ -1295,9 +1378,9 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
         const T* gy = static_cast<const T*>(grad_y);
         const T* xs = static_cast<const T*>(x);
         const T* wp = static_cast<const T*>(w_prob);
+        T* gcv = (complete && grad_x) ? gconv : nullptr;
         if (complete)
-            k_tree_nodes<T, true><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d,
-                                                       grad_x ? gconv : nullptr,
+            k_tree_nodes<T, true><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gcv,
                                                        part, kc);
         else
             k_tree_nodes<T, false><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gconv,

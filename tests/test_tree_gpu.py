@@ -41,7 +41,7 @@ SHAPES = [  # stride, pad, kernel, (n, c_in, h, w, c_out)
     ((2, 2), (1, 1), (3, 3), (128, 9, 16, 16, 41)),   # channel groups of 2, the last one short
     ((1, 1), (1, 1), (3, 3), (2, 5, 64, 64, 3)),      # 80 KiB (fp32) / 160 KiB (fp64) planes
     # LDS-staged forward (at least two items per staged input element):
-    ((2, 2), (1, 1), (3, 3), (2, 9, 32, 32, 96)),     # conv1 geometry, a channel per wave
+    ((2, 2), (1, 1), (3, 3), (2, 9, 32, 32, 160)),    # conv1 geometry, a channel per wave
     ((2, 2), (1, 1), (3, 3), (2, 3, 8, 8, 64)),       # 16 items per channel: 4 channels a wave
     ((1, 1), (1, 1), (3, 3), (2, 2, 10, 10, 24)),     # stride 1, 5 windows a row, 100 items
 ]
@@ -150,7 +150,7 @@ BINARY_SHAPES = [  # stride, pad, kernel, (n, c_in, h, w, c_out)
     ((1, 1), (1, 1), (3, 3), (4, 3, 12, 12, 6)),
     ((1, 1), (0, 0), (2, 2), (6, 2, 7, 9, 5)),        # many positions share all eight taps
     # LDS-staged forward:
-    ((2, 2), (1, 1), (3, 3), (4, 9, 32, 32, 96)),     # conv1 geometry
+    ((2, 2), (1, 1), (3, 3), (4, 9, 32, 32, 160)),    # conv1 geometry (staged node pass)
     ((2, 2), (1, 1), (3, 3), (4, 3, 8, 8, 64)),       # four channels a wave
     ((1, 1), (0, 0), (2, 2), (6, 2, 7, 9, 40)),       # 48 items per channel, 16 lanes idle
 ]
@@ -217,6 +217,7 @@ def test_tree_level_matches_oracle(dtype):
 @pytest.mark.parametrize("complete", [True, False])
 @pytest.mark.parametrize("c_in,h,w,stride,pad,kernel,words", [
     (9, 32, 32, (2, 2), (1, 1), (3, 3), 5),     # conv1 of the tree reading, partial chunk
+    (9, 32, 32, (2, 2), (1, 1), (3, 3), 200),   # staged patches over seven chunks
     (3, 12, 12, (2, 2), (1, 1), (3, 3), 33),    # 3 x 3 windows, two chunks
     (2, 10, 10, (1, 1), (1, 1), (3, 3), 17),    # stride 1
     (16, 8, 8, (2, 2), (1, 1), (3, 3), 40),     # conv2 of the tree reading
@@ -233,6 +234,32 @@ def test_packed_block_matches_bit_oracle(complete, c_in, h, w, stride, pad, kern
                                    kernel, complete)
     ref = T.block_bits(xw, gates, np_(sel), (c_in, h, w), stride, pad, kernel, complete)
     assert np.array_equal(np_(out).view(np.uint64), ref)
+
+
+@pytest.mark.parametrize("c_in,h,w,words", [(4, 12, 12, 40), (16, 8, 8, 40)])
+def test_packed_block_taps_outside_the_window_and_out_of_range_channels(c_in, h, w, words):
+    """Staged (4 input channels) and global-gather (16) packed blocks: a channel with a tap
+    outside the kernel window matches the bit oracle, one reading an input channel >= C
+    gives all-ones rows."""
+    rng = np.random.default_rng(8)
+    c_out, stride, pad, kernel = 12, (2, 2), (1, 1), (3, 3)
+    xw = rng.integers(0, 2**63, (c_in * h * w, words), dtype=np.int64).view(np.uint64)
+    gates = rng.integers(0, 16, (c_out, 7)).astype(np.uint8)
+    _, _, sel = make(9, 1, c_in, h, w, c_out, nodes=7)
+    sel = sel.clone()
+    sel[1, 2] = (sel[1, 2] & ~0xFF00) | (4 << 8)
+    sel[3, 5] = (sel[3, 5] & ~0xFF) | 3
+    ok = sel.clone()
+    sel[4, 0] = (sel[4, 0] & 0xFFFF) | (c_in << 16)
+    ok[4, 0] = ok[4, 0] & 0xFFFF
+    out = np_(TL.tree_conv_eval_packed(torch.as_tensor(xw.view(np.int64)).cuda(),
+                                       torch.as_tensor(gates).cuda(), sel, (c_in, h, w), stride,
+                                       pad, kernel, True)).view(np.uint64)
+    ref = T.block_bits(xw, gates, np_(ok), (c_in, h, w), stride, pad, kernel, True)
+    P = out.shape[0] // c_out
+    rows = np.arange(out.shape[0]) // P
+    assert np.array_equal(out[rows != 4], ref[rows != 4])
+    assert (out[rows == 4] == np.uint64(2**64 - 1)).all()
 
 
 def test_module_packed_path_widens_power_of_two_rows():
@@ -317,6 +344,18 @@ def test_forward_taps_outside_the_window_and_out_of_range_channels(dtype, shape,
         np.testing.assert_allclose(np_(x2)[:, live], rx2[:, live], **tol(dtype))
         np.testing.assert_allclose(np_(x3)[:, live], rx3[:, live], **tol(dtype))
         assert torch.isnan(y[:, 4]).all() and torch.isnan(x2[:, 4]).all()
+        # backward with the out-of-window taps only (the staged node pass leaves those
+        # channels to its fix-up kernel), through the oracle's winners
+        _, _, _, idx_ok = TL.full_convlogic_forward(x, w_prob, ok, *stride, *pad, *kernel)
+        gy = torch.randn(ry.shape, generator=torch.Generator().manual_seed(3),
+                         dtype=torch.float64)
+        gx, gw = TL.tree_conv_backward(gy.to(x.device, x.dtype), x, w_prob, ok, idx_ok, *stride,
+                                       *pad, *kernel, True)
+        rgx, rgw = T.block_backward(np_(x), np_(w_prob), np_(ok), stride, pad, kernel,
+                                    np_(gy.to(x.dtype)), True, idx=np_(idx_ok))
+        scale = max(1.0, float(np.abs(rgw).max()))
+        np.testing.assert_allclose(np_(gx), rgx, **tol(dtype))
+        np.testing.assert_allclose(np_(gw) / scale, rgw / scale, **tol(dtype))
     else:
         y = TL.convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel)
         ref = T.block_forward(np_(x), np_(w_prob), np_(ok), stride, pad, kernel, complete=False)
