@@ -12,6 +12,8 @@ Also reported on the same JSON line:
   cpu_baseline  the pure-PyTorch CPU step (oracle/torch_cpu.py) on a bounded sample
   train_full    cfg2 with the optimizer half of the reference's step: clip_grad_norm_(10) and
                 Adam fused (FusedAdam), the whole step in one HIP graph
+  train_random_wiring  cfg2 with the reference's default connections='random' (a pair per
+                slot: the multi-run kernels)
   conv_train    cfg3: conv 9x32x32 -> 256x16x16 -> 512x7x7, flatten, 2 x 16000 dense,
                 GroupSum(10, tau 30), batch 256, fp32 fwd + CE + bwd, same measurements
   conv_tree_train  the logic-tree reading of cfg3: two complete ConvLogicLayer blocks (8 taps,
@@ -141,6 +143,27 @@ def bench_dense(args, torch):
     del model
     torch.cuda.empty_cache()
     return cfg, samples_s, dt, kernels, matches
+
+
+def bench_dense_random(args, torch):
+    """cfg2 with the reference's default wiring (connections='random', compactlogic/
+    compactlogic.py:160-182): every slot of a neuron reads its own input pair, so a neuron is
+    16 runs and the layer takes the multi-run kernels (prep, tiled forward, chunked backward
+    with its finalize) instead of the single-run fused forward and row backward."""
+    from compactlogic_amd import configs
+    cfg = configs.CONFIGS["cfg2"]
+    dev = torch.device("cuda:0")
+    model = configs.dense_network(cfg, device=dev, wiring="random")
+    x, labels = configs.dense_inputs(cfg, device=dev)
+    samples_s, dt, kernels, matches = bench_train(model, x, labels, args.steps, args.warmup,
+                                                  args.mode, args.kernel_steps, torch)
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": "cfg2 (6x12000, G=16, B=1024, fp32 fwd+CE+bwd) with connections='random': "
+                        "16 input pairs per neuron, the multi-run kernels",
+            "value": round(samples_s, 1), "unit": "samples/s", "ms_per_step": round(dt * 1e3, 4),
+            "steps": args.steps, "timed_path_matches_eager": matches,
+            "kernels": kernels_json(kernels, args.kernel_steps)}
 
 
 # Algorithmic bytes per launch (activations read once + written once, fp32): a forward reads
@@ -657,6 +680,9 @@ def main():
     log("dense cfg2 full step (with clip + Adam)")
     result["train_full"] = bench_train_full(args, torch)
     log(f"dense cfg2 full step: {result['train_full']['ms_per_step']:.3f} ms/step")
+    log("dense cfg2 with the reference's default wiring (connections='random')")
+    result["train_random_wiring"] = bench_dense_random(args, torch)
+    log(f"dense cfg2 random wiring: {result['train_random_wiring']['ms_per_step']:.3f} ms/step")
     if not args.no_cpu_baseline:
         log("cpu baseline (cfg2)")
         result["cpu_baseline"] = cpu_baseline_train(torch, "cfg2")

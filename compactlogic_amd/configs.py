@@ -91,9 +91,31 @@ def _seeded_layer(in_dim: int, out_dim: int, gen: torch.Generator, num_gates: in
     return layer
 
 
-def dense_network(cfg: DenseConfig, device="cuda", seed: int = NET_SEED) -> torch.nn.Sequential:
+def _seeded_random_layer(in_dim: int, out_dim: int, gen: torch.Generator,
+                         num_gates: int) -> LogicLayer:
+    """The reference's default wiring, connections='random' (compactlogic/compactlogic.py:
+    160-182): every slot its own input pair, drawn by the layer's own sampler under a seeded
+    RNG; logits from `gen`; gate_sequence = arange(16)."""
+    layer_seed = int(torch.randint(0, 2**31 - 1, (1,), generator=gen))
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(layer_seed)
+        layer = LogicLayer(in_dim, out_dim, connections="random", num_gates=num_gates)
+    logits = torch.randn((out_dim, num_gates), generator=gen)
+    with torch.no_grad():
+        layer.weights.copy_(logits)
+        layer.gate_sequence.copy_(
+            (torch.arange(num_gates, dtype=torch.int64) & 15).to(torch.uint8).expand(out_dim, num_gates))
+    layer.refresh_backward_index()
+    return layer
+
+
+def dense_network(cfg: DenseConfig, device="cuda", seed: int = NET_SEED,
+                  wiring: str = "original") -> torch.nn.Sequential:
+    """cfg's network.  wiring 'original': one seeded input pair per neuron shared by its
+    slots (the benched configs); 'random': the reference's default, a pair per slot."""
     gen = torch.Generator().manual_seed(seed)
-    layers = [_seeded_layer(i, o, gen, cfg.num_gates) for i, o in cfg.dims]
+    make = _seeded_random_layer if wiring == "random" else _seeded_layer
+    layers = [make(i, o, gen, cfg.num_gates) for i, o in cfg.dims]
     model = torch.nn.Sequential(*layers, GroupSum(cfg.k, cfg.tau))
     return model.to(device)
 
