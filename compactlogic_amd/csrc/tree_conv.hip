@@ -729,15 +729,18 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
                                                      const int32_t* __restrict__ ent_ptr,
                                                      const int32_t* __restrict__ ent,
                                                      const T* __restrict__ kc, TreeDims d, int cg,
-                                                     int pw_lanes, int spw,
+                                                     int pw_lanes, int spw, int band_rows,
                                                      T* __restrict__ grad_x) {
     constexpr int NODES = COMPLETE ? 7 : 4;
     extern __shared__ unsigned char smem_raw[];
-    T* gx = reinterpret_cast<T*>(smem_raw);  // [spw][cg][h * w]
+    T* gx = reinterpret_cast<T*>(smem_raw);  // [spw][cg][band rows * w]
     const int n0 = blockIdx.x * spw;
     const int ch0 = blockIdx.y * cg;
     const int nch = min(cg, d.cin - ch0);
-    const int hw = d.h * d.w;
+    // the workgroup's band of input rows [y0, y1) (the whole plane when it fits LDS); every
+    // use is walked by every band and adds only to its own rows, in the same order
+    const int y0 = blockIdx.z * band_rows, y1 = min(d.h, y0 + band_rows);
+    const int hw = (y1 - y0) * d.w;
     for (int i = threadIdx.x; i < spw * nch * hw; i += 256) gx[i] = T(0);
     __syncthreads();
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -748,7 +751,7 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
     const int sub = lane / GL, gl = lane % GL, sl = gl / PW, pl = gl % PW;
     const int n = n0 + sl;
     const bool n_ok = n < d.n;
-    const T* xn = x + int64_t(n_ok ? n : 0) * d.cin * hw;
+    const T* xn = x + int64_t(n_ok ? n : 0) * d.cin * d.h * d.w;  // the whole sample
     T* gxs = gx + sl * nch * hw;
     // channel slot handled by this lane group in pass `it`: wave-major so a wave's groups take
     // consecutive channels
@@ -792,8 +795,8 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
                     const int w0 = wok ? win : 0;
                     const int oy = int(fast_div(uint32_t(w0), d.div_wo)), ox = w0 - oy * d.wo;
                     const int iy = oy * d.sh + tk[i].dy, ix = ox * d.sw + tk[i].dx;
-                    const bool ok = wok && iy >= 0 && iy < d.h && ix >= 0 && ix < d.w;
-                    tgt[i] = ok ? iy * d.w + ix : -1;
+                    const bool ok = wok && iy >= y0 && iy < y1 && ix >= 0 && ix < d.w;
+                    tgt[i] = ok ? (iy - y0) * d.w + ix : -1;
                     const T xp = ok ? tap_value(xn, d, tp[i], oy, ox) : T(0);
                     const T g = ok ? gsrc[(cell[i] * d.P + p) * 4 + kn[i]] : T(0);
                     add[i] = g * fma(k3[i], xp, kown[i]);
@@ -805,9 +808,12 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
         }
     }
     __syncthreads();
+    const int64_t plane = int64_t(d.h) * d.w;
     for (int i = threadIdx.x; i < spw * nch * hw; i += 256) {
         const int si = i / (nch * hw), r = i % (nch * hw);
-        if (n0 + si < d.n) grad_x[(int64_t(n0 + si) * d.cin + ch0) * hw + r] = gx[i];
+        const int chl = r / hw, rr = r - chl * hw;
+        if (n0 + si < d.n)
+            grad_x[(int64_t(n0 + si) * d.cin + ch0 + chl) * plane + int64_t(y0) * d.w + rr] = gx[i];
     }
 }
 
@@ -1392,10 +1398,14 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
             if (int rc = check_launch("cl_tree_conv_backward(finalize)")) return rc;
         }
         if (grad_x) {
-            const int64_t hw_bytes = int64_t(d.h) * d.w * int64_t(sizeof(T));
-            CL_ARG(hw_bytes <= kGatherLdsBytes,
-                   "input planes of more than %lld bytes are not supported by the input gradient",
+            const int64_t row_bytes = int64_t(d.w) * int64_t(sizeof(T));
+            CL_ARG(row_bytes <= kGatherLdsBytes,
+                   "input rows of more than %lld bytes are not supported by the input gradient",
                    (long long)kGatherLdsBytes);
+            // planes beyond LDS: bands of rows, one workgroup per band
+            const int band_rows = int(std::min<int64_t>(d.h, kGatherLdsBytes / row_bytes));
+            const int nbands = int(ceil_div(d.h, band_rows));
+            const int64_t hw_bytes = int64_t(band_rows) * row_bytes;
             // one pass of the workgroup's lane groups per channel group: more workgroups
             // (each staging only its channels) keep more waves in flight
             const int pw_lanes = gather_lanes(d.P);
@@ -1406,17 +1416,19 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
             const int cg = int(std::max<int64_t>(1, std::min<int64_t>(
                 std::min<int64_t>(d.cin, 4 * (64 / (pw_lanes * spw))),
                 kGatherLdsBytes / (hw_bytes * spw))));
-            const dim3 g2(unsigned(ceil_div(d.n, spw)), unsigned(ceil_div(d.cin, cg)));
+            const dim3 g2(unsigned(ceil_div(d.n, spw)), unsigned(ceil_div(d.cin, cg)),
+                          unsigned(nbands));
+            CL_ARG(nbands < 65536, "input planes too tall for the input gradient");
             const size_t lds = size_t(spw) * size_t(cg) * size_t(hw_bytes);
             const T* src = complete ? gconv : gy;
             if (complete)
                 k_tree_gather<T, true><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
                                                             ent, kc, d, cg, pw_lanes, spw,
-                                                            static_cast<T*>(grad_x));
+                                                            band_rows, static_cast<T*>(grad_x));
             else
                 k_tree_gather<T, false><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
                                                              ent, kc, d, cg, pw_lanes, spw,
-                                                             static_cast<T*>(grad_x));
+                                                             band_rows, static_cast<T*>(grad_x));
             if (int rc = check_launch("cl_tree_conv_backward(gather)")) return rc;
         }
     });

@@ -571,9 +571,9 @@ int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_
  * the forward's y; indices are the forward's (complete only).  ent_ptr (int32 [c_in + 1]) and
  * ent (int32 [8 * c_out], c * 8 + k) list the taps reading each input channel in ascending
  * order (the input gradient's gather order).  grad_x [n, c_in, h, w] (may be NULL) is exact
- * and reproducible: a sum over the taps in that order, no float atomics; it needs
- * h * w * sizeof(element) <= 65536.  grad_w [c_out, nodes, 16] (may be NULL) is the gradient of
- * the probabilities. */
+ * and reproducible: a sum over the taps in that order, no float atomics; planes above 64 KiB
+ * are gathered in bands of rows (one row must fit: w * sizeof(element) <= 65536).  grad_w
+ * [c_out, nodes, 16] (may be NULL) is the gradient of the probabilities. */
 int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x, const void* w_prob,
                           const int32_t* selection, const int32_t* indices,
                           const int32_t* ent_ptr, const int32_t* ent, int64_t n, int64_t c_in,

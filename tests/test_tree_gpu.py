@@ -117,6 +117,32 @@ def test_block_backward_matches_oracle_and_is_reproducible(complete, dtype, stri
     assert gx3 is None and torch.equal(gw3, gw)
 
 
+@pytest.mark.parametrize("complete", [True, False])
+@pytest.mark.parametrize("dtype,hw", [(torch.float32, 136), (torch.float64, 96)])
+def test_backward_of_planes_beyond_lds_in_row_bands(complete, dtype, hw):
+    """Input planes above 64 KiB (fp32 136 x 136, fp64 96 x 96) are gathered in bands of
+    rows; the input gradient matches the oracle and repeats bitwise."""
+    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    n, c_in, c_out = 2, 2, 3
+    nodes = 7 if complete else 4
+    x, w_prob, sel = make(13, n, c_in, hw, hw, c_out, kernel[0], nodes=nodes, dtype=dtype)
+    if complete:
+        y, _, _, idx = TL.full_convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel,
+                                                 intermediate=False)
+    else:
+        y, idx = TL.convlogic_forward(x, w_prob, sel, *stride, *pad, *kernel), None
+    gy = torch.randn(y.shape, generator=torch.Generator().manual_seed(14),
+                     dtype=torch.float64).to(y.device, dtype)
+    gx, gw = TL.tree_conv_backward(gy, x, w_prob, sel, idx, *stride, *pad, *kernel, complete)
+    rgx, rgw = T.block_backward(np_(x), np_(w_prob), np_(sel), stride, pad, kernel, np_(gy),
+                                complete, idx=np_(idx) if complete else None)
+    scale = max(1.0, float(np.abs(rgw).max()))
+    np.testing.assert_allclose(np_(gx), rgx, **tol(dtype))
+    np.testing.assert_allclose(np_(gw) / scale, rgw / scale, **tol(dtype))
+    gx2, _ = TL.tree_conv_backward(gy, x, w_prob, sel, idx, *stride, *pad, *kernel, complete)
+    assert torch.equal(gx, gx2)
+
+
 def _window_scores(x, w_prob, sel, stride, pad, kernel):
     """Oracle block outputs at every conv position [N, C, Ho, Wo] (node 6 of the tree), from
     the oracle's own node values."""
