@@ -11,7 +11,9 @@
 //
 // Every node's 16 probabilities w_prob[c][q][:] collapse to the four coefficients of
 // K0 + K1 a + K2 b + K3 a b (the multilinear form of the gate mixture), so a node costs one
-// evaluation whatever the mixture.
+// evaluation whatever the mixture.  With TreeDims::softmax set, the 16 values are the node's
+// logits and the probabilities are their softmax, taken where the coefficients are collapsed
+// (once per workgroup and channel), and the finalize returns the gradient of the logits.
 //
 // Backward (all deterministic, no float atomics in global memory):
 //   k_tree_nodes   per (sample, channel, pooled window): recompute the winner position's
@@ -23,7 +25,8 @@
 //                  a fixed order; within one use the positions are distinct (a tap offset maps
 //                  positions one to one), so every LDS word receives its additions in a fixed
 //                  order and the result is bitwise reproducible;
-//   k_tree_finalize  partials summed in block order, moments -> gradient of every probability.
+//   k_tree_finalize  partials summed in block order, moments -> gradient of every probability
+//                  (or, from logits, of every logit: the softmax backward p (g - sum p g)).
 #include "common.h"
 
 namespace cl {
@@ -42,6 +45,7 @@ __device__ __forceinline__ T quiet_nan() {
 struct TreeDims {
     int n, cin, h, w, cout, ho, wo, sh, sw, ph, pw;
     int complete;
+    int softmax;  // the weights are logits: softmax over each node's 16 values on load
     int P;  // items per (sample, channel): pooled windows (complete) or conv positions
     FastDiv div_p, div_wp;  // by P, and by the windows per pooled row (complete) or wo
     FastDiv div_wo;         // by wo (conv positions -> rows)
@@ -78,6 +82,31 @@ __device__ __forceinline__ T node(const T* k, T a, T b) {
     return fma(k[3], a * b, fma(k[2], b, fma(k[1], a, k[0])));
 }
 
+// The 16 probabilities of a node from its weights: the weights themselves, or with `softmax`
+// their softmax exp(w - max) * (1 / sum), one division per node (every workgroup of a forward
+// recomputes the softmax of its channels).  The exponential is the accurate library one: the
+// hardware exp2 form is off by a few 1e-7 relative, which the input gradient's cancelling sums
+// turn into absolute errors above 1e-6.
+template <typename T>
+__device__ __forceinline__ void node_probs(const T* __restrict__ w, bool softmax, T (&p)[16]) {
+#pragma unroll
+    for (int g = 0; g < 16; ++g) p[g] = w[g];
+    if (softmax) {
+        T mx = p[0];
+#pragma unroll
+        for (int g = 1; g < 16; ++g) mx = fmax(mx, p[g]);
+        T sum = 0;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            p[g] = exp(p[g] - mx);
+            sum += p[g];
+        }
+        const T inv = T(1) / sum;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) p[g] = p[g] * inv;
+    }
+}
+
 // Collapse w_prob[c][q][:] for q < nodes into sk[q][0..3]; taps of channel c into st.  Called by
 // the whole workgroup, followed by a barrier.
 template <typename T>
@@ -88,8 +117,10 @@ __device__ __forceinline__ void load_channel(const T* __restrict__ w_prob,
     const int t = threadIdx.x;
     if (t < nodes * 4) {
         const int q = t >> 2, m = t & 3;
-        const T* p = w_prob + (int64_t(c) * nodes + q) * 16;
+        T p[16];
+        node_probs(w_prob + (int64_t(c) * nodes + q) * 16, d.softmax != 0, p);
         T acc = 0;
+#pragma unroll
         for (int g = 0; g < 16; ++g) {
             const Coef4<T> cf = gate_coef<T>(g);
             const T cm = m == 0 ? cf.c0 : m == 1 ? cf.c1 : m == 2 ? cf.c2 : cf.c3;
@@ -331,7 +362,8 @@ __device__ __forceinline__ void stage_sample(const T* __restrict__ x, const T* _
     for (int i = tid; i < planes; i += nt) L.plane[i] = T(0);
     // One thread per (channel, node): the four coefficients in the order of load_channel.
     for (int i = tid; i < c_n * NODES; i += nt) {
-        const T* p = w_prob + (int64_t(c_lo) * NODES + i) * 16;
+        T p[16];
+        node_probs(w_prob + (int64_t(c_lo) * NODES + i) * 16, d.softmax != 0, p);
         T a0 = 0, a1 = 0, a2 = 0, a3 = 0;
 #pragma unroll
         for (int gi = 0; gi < 16; ++gi) {
@@ -822,6 +854,7 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
 template <typename T>
 __global__ __launch_bounds__(256) void k_tree_finalize(const T* __restrict__ part, int64_t cout,
                                                        int nodes, int64_t nblk,
+                                                       const T* __restrict__ logits,
                                                        T* __restrict__ grad_w) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= cout * nodes * 16) return;
@@ -834,8 +867,25 @@ __global__ __launch_bounds__(256) void k_tree_finalize(const T* __restrict__ par
 #pragma unroll
         for (int j = 0; j < 4; ++j) m[j] += src[j];
     }
-    const Coef4<T> cf = gate_coef<T>(g);
-    grad_w[i] = fma(cf.c3, m[0], fma(cf.c2, m[2], fma(cf.c1, m[1], cf.c0 * m[3])));
+    auto prob_grad = [&](int h) {
+        const Coef4<T> cf = gate_coef<T>(h);
+        return fma(cf.c3, m[0], fma(cf.c2, m[2], fma(cf.c1, m[1], cf.c0 * m[3])));
+    };
+    if (!logits) {
+        grad_w[i] = prob_grad(g);
+        return;
+    }
+    // softmax backward: every lane of the node forms all 16 probabilities and their
+    // gradients itself, so the sum over the node is taken in one fixed order
+    T p[16];
+    node_probs(logits + cq * 16, true, p);
+    T dot = 0, pg = 0;
+#pragma unroll
+    for (int h = 0; h < 16; ++h) {
+        dot = fma(p[h], prob_grad(h), dot);
+        pg = h == g ? p[h] : pg;  // a select per slot: no dynamic index into registers
+    }
+    grad_w[i] = pg * (prob_grad(g) - dot);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1136,6 +1186,7 @@ int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t
     d.ph = ph;
     d.pw = pw;
     d.complete = complete ? 1 : 0;
+    d.softmax = 0;
     d.P = int(P);
     d.div_p = make_fastdiv(uint32_t(std::max<int64_t>(P, 1)));
     d.div_wp = make_fastdiv(uint32_t(std::max<int64_t>(complete ? wo / 2 : wo, 1)));
@@ -1272,17 +1323,17 @@ int64_t tree_workspace_bytes(const TreeDims& d) {
 
 using namespace cl;
 
-extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob,
-                                    const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
-                                    int64_t w, int64_t c_out, int stride_h, int stride_w,
-                                    int pad_h, int pad_w, int kernel_h, int kernel_w,
-                                    int complete, void* y, void* x2, void* x3, int32_t* indices,
-                                    void* stream) {
-    clear_error();
+namespace {
+int tree_conv_forward_impl(int dtype, const void* x, const void* w_prob,
+                           const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
+                           int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
+                           int pad_w, int kernel_h, int kernel_w, int complete, void* y, void* x2,
+                           void* x3, int32_t* indices, int softmax, void* stream) {
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
+    d.softmax = softmax ? 1 : 0;
     if (n == 0 || c_out == 0) return CL_OK;
     CL_ARG(x && w_prob && selection && y, "null pointer argument");
     const unsigned gx = unsigned(ceil_div(int64_t(d.n) * d.P, 256));
@@ -1318,6 +1369,31 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
     });
     return check_launch("cl_tree_conv_forward");
 }
+}  // namespace
+
+extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob,
+                                    const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
+                                    int64_t w, int64_t c_out, int stride_h, int stride_w,
+                                    int pad_h, int pad_w, int kernel_h, int kernel_w,
+                                    int complete, void* y, void* x2, void* x3, int32_t* indices,
+                                    void* stream) {
+    clear_error();
+    return tree_conv_forward_impl(dtype, x, w_prob, selection, n, c_in, h, w, c_out, stride_h,
+                                  stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
+                                  indices, 0, stream);
+}
+
+extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void* w_logits,
+                                            const int32_t* selection, int64_t n, int64_t c_in,
+                                            int64_t h, int64_t w, int64_t c_out, int stride_h,
+                                            int stride_w, int pad_h, int pad_w, int kernel_h,
+                                            int kernel_w, int complete, void* y, void* x2,
+                                            void* x3, int32_t* indices, void* stream) {
+    clear_error();
+    return tree_conv_forward_impl(dtype, x, w_logits, selection, n, c_in, h, w, c_out, stride_h,
+                                  stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
+                                  indices, 1, stream);
+}
 
 extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,
                                       int64_t c_out, int stride_h, int stride_w, int pad_h,
@@ -1333,19 +1409,19 @@ extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_
     return CL_OK;
 }
 
-extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x,
-                                     const void* w_prob, const int32_t* selection,
-                                     const int32_t* indices, const int32_t* ent_ptr,
-                                     const int32_t* ent, int64_t n, int64_t c_in, int64_t h,
-                                     int64_t w, int64_t c_out, int stride_h, int stride_w,
-                                     int pad_h, int pad_w, int kernel_h, int kernel_w,
-                                     int complete, void* grad_x, void* grad_w, void* workspace,
-                                     int64_t workspace_bytes, void* stream) {
-    clear_error();
+namespace {
+int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const void* w_prob,
+                            const int32_t* selection, const int32_t* indices,
+                            const int32_t* ent_ptr, const int32_t* ent, int64_t n, int64_t c_in,
+                            int64_t h, int64_t w, int64_t c_out, int stride_h, int stride_w,
+                            int pad_h, int pad_w, int kernel_h, int kernel_w, int complete,
+                            void* grad_x, void* grad_w, void* workspace, int64_t workspace_bytes,
+                            int softmax, void* stream) {
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
+    d.softmax = softmax ? 1 : 0;
     if (!grad_x && !grad_w) return CL_OK;
     const int nodes = complete ? 7 : 4;
     hipStream_t s = as_stream(stream);
@@ -1394,7 +1470,7 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
         if (int rc = check_launch("cl_tree_conv_backward(nodes)")) return rc;
         if (grad_w) {
             k_tree_finalize<T><<<unsigned(ceil_div(int64_t(d.cout) * nodes * 16, 256)), 256, 0, s>>>(
-                part, d.cout, nodes, nblk, static_cast<T*>(grad_w));
+                part, d.cout, nodes, nblk, softmax ? wp : nullptr, static_cast<T*>(grad_w));
             if (int rc = check_launch("cl_tree_conv_backward(finalize)")) return rc;
         }
         if (grad_x) {
@@ -1433,6 +1509,38 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
         }
     });
     return CL_OK;
+}
+}  // namespace
+
+extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x,
+                                     const void* w_prob, const int32_t* selection,
+                                     const int32_t* indices, const int32_t* ent_ptr,
+                                     const int32_t* ent, int64_t n, int64_t c_in, int64_t h,
+                                     int64_t w, int64_t c_out, int stride_h, int stride_w,
+                                     int pad_h, int pad_w, int kernel_h, int kernel_w,
+                                     int complete, void* grad_x, void* grad_w, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+    clear_error();
+    return tree_conv_backward_impl(dtype, grad_y, x, w_prob, selection, indices, ent_ptr, ent, n,
+                                   c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
+                                   kernel_w, complete, grad_x, grad_w, workspace,
+                                   workspace_bytes, 0, stream);
+}
+
+extern "C" int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
+                                             const void* w_logits, const int32_t* selection,
+                                             const int32_t* indices, const int32_t* ent_ptr,
+                                             const int32_t* ent, int64_t n, int64_t c_in,
+                                             int64_t h, int64_t w, int64_t c_out, int stride_h,
+                                             int stride_w, int pad_h, int pad_w, int kernel_h,
+                                             int kernel_w, int complete, void* grad_x,
+                                             void* grad_w, void* workspace,
+                                             int64_t workspace_bytes, void* stream) {
+    clear_error();
+    return tree_conv_backward_impl(dtype, grad_y, x, w_logits, selection, indices, ent_ptr, ent,
+                                   n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
+                                   kernel_h, kernel_w, complete, grad_x, grad_w, workspace,
+                                   workspace_bytes, 1, stream);
 }
 
 extern "C" int cl_tree_level_forward(int dtype, const void* x, const void* w_prob, int64_t n,
@@ -1497,7 +1605,7 @@ extern "C" int cl_tree_level_backward(int dtype, const void* grad_y, const void*
         if (int rc = check_launch("cl_tree_level_backward")) return rc;
         if (grad_w) {
             k_tree_finalize<T><<<unsigned(ceil_div(channels * out_bits * 16, 256)), 256, 0, s>>>(
-                part, channels, int(out_bits), nblk, static_cast<T*>(grad_w));
+                part, channels, int(out_bits), nblk, nullptr, static_cast<T*>(grad_w));
         }
     });
     return check_launch("cl_tree_level_backward");

@@ -95,11 +95,12 @@ def _check_block(x, w_prob, selection, nodes):
 
 
 def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h,
-                           kernel_w, intermediate: bool = True):
+                           kernel_w, intermediate: bool = True, softmax: bool = False):
     """Complete block forward (replaces convlogic_cuda.full_convlogic_forward,
     full_convlogic_kernel.cu:156-231): (y [N, C, Ho/2, Wo/2], x2 [N, C, Ho, Wo, 4],
     x3 [N, C, Ho, Wo, 2], indices int32 [N, C, Ho/2 * Wo/2]); x2 and x3 are None unless
-    `intermediate`."""
+    `intermediate`.  With `softmax`, w_prob holds the node logits and the kernels take their
+    softmax (cl_tree_conv_forward_softmax)."""
     c_out = _check_block(x, w_prob, selection, 7)
     n, c_in, h, w = x.shape
     ho, wo = _out_hw(h, w, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
@@ -116,16 +117,18 @@ def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_
         x3 = torch.empty((n, c_out, ho, wo, 2), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
         timing.timed(f"cl_tree_conv_forward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
-            "cl_tree_conv_forward", _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
+            "cl_tree_conv_forward_softmax" if softmax else "cl_tree_conv_forward",
+            _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
             selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
             kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2), _dl.ptr(x3), idx.data_ptr(),
             _dl.stream_of(x)))
     return y, x2, x3, idx
 
 
-def convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w):
+def convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
+                      softmax: bool = False):
     """Conv gates only (replaces convlogic_cuda.convlogic_forward, convlogic_kernel.cu:67-107):
-    y [N, C, Ho, Wo, 4]."""
+    y [N, C, Ho, Wo, 4].  With `softmax`, w_prob holds the node logits."""
     c_out = _check_block(x, w_prob, selection, 4)
     n, c_in, h, w = x.shape
     ho, wo = _out_hw(h, w, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
@@ -133,7 +136,8 @@ def convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, ke
         raise RuntimeError(f"Invalid output shape: H_out={ho}, W_out={wo}")
     y = torch.empty((n, c_out, ho, wo, 4), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_tree_conv_forward", _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
+        _capi.call("cl_tree_conv_forward_softmax" if softmax else "cl_tree_conv_forward",
+                   _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
                    selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
                    kernel_h, kernel_w, 0, y.data_ptr(), None, None, None, _dl.stream_of(x))
     return y
@@ -141,10 +145,11 @@ def convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, ke
 
 def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w, pad_h, pad_w,
                        kernel_h, kernel_w, complete: bool, need_x: bool = True,
-                       need_w: bool = True, uses=None):
+                       need_w: bool = True, uses=None, softmax: bool = False):
     """(grad_x or None, grad_w_prob or None) of the complete block or of the conv gates
     (replaces full_convlogic_backward_x / _weight and convlogic_backward_x / _weight).  `uses`
-    is channel_uses(selection, C_in), computed when not given."""
+    is channel_uses(selection, C_in), computed when not given.  With `softmax`, w_prob holds
+    the node logits and the second result is the gradient of the logits."""
     nodes = 7 if complete else 4
     c_out = _check_block(x, w_prob, selection, nodes)
     n, c_in, h, w = x.shape
@@ -166,7 +171,8 @@ def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w
     ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
     with torch.cuda.device(x.device):
         timing.timed(f"cl_tree_conv_backward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
-            "cl_tree_conv_backward", code, grad_y.data_ptr(), x.data_ptr(), w_prob.data_ptr(),
+            "cl_tree_conv_backward_softmax" if softmax else "cl_tree_conv_backward", code,
+            grad_y.data_ptr(), x.data_ptr(), w_prob.data_ptr(),
             selection.data_ptr(), indices.data_ptr() if complete else None, _dl.ptr(ptr),
             _dl.ptr(ent), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
             kernel_w, int(complete), _dl.ptr(gx), _dl.ptr(gw), ws.data_ptr(), need.value,
@@ -464,14 +470,18 @@ class ConvLogicLayer(nn.Module):
 
     def forward_cuda(self, x):
         x = x.contiguous()
-        w_prob = self._w_prob(x.dtype)
+        # Training with logits of x's dtype: the kernels take the softmax of the logits
+        # themselves (and its backward), so no probability tensor or softmax launch is needed.
+        softmax = self.training and self.weights.dtype == x.dtype
+        w = self.weights.contiguous() if softmax else self._w_prob(x.dtype)
         sel = self.selection.to(torch.int32).contiguous()
-        args = (x, w_prob, sel, self.stride[0], self.stride[1], self.padding[0], self.padding[1],
+        args = (x, w, sel, self.stride[0], self.stride[1], self.padding[0], self.padding[1],
                 self.kernel[0], self.kernel[1])
         if self.complete:
             return _FullConvLogicWithUses.apply(*args, self.return_intermediate,
-                                                self.return_indices, self._channel_uses())
-        return _ConvLogicWithUses.apply(*args, self._channel_uses())
+                                                self.return_indices, self._channel_uses(),
+                                                softmax)
+        return _ConvLogicWithUses.apply(*args, self._channel_uses(), softmax)
 
     def forward_packed(self, x: PackBitsTensor, in_hw=None) -> PackBitsTensor:
         """Bitwise block on packed rows (eval mode): rows = in_channels * h * w features in NCHW
@@ -502,39 +512,45 @@ class ConvLogicLayer(nn.Module):
 
 
 class _ConvLogicWithUses(Function):
-    """ConvLogicFunction with the layer's cached channel-use index."""
+    """ConvLogicFunction with the layer's cached channel-use index; with `softmax`, w holds
+    the node logits (the kernels' softmax and its backward)."""
 
     @staticmethod
-    def forward(ctx, x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
-                uses):
-        y = convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h,
-                              kernel_w)
-        ctx.save_for_backward(x, w_prob, selection)
+    def forward(ctx, x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
+                uses, softmax=False):
+        y = convlogic_forward(x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h,
+                              kernel_w, softmax=softmax)
+        ctx.save_for_backward(x, w, selection)
         ctx.geom = (stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
         ctx.uses = uses
+        ctx.softmax = softmax
         return y
 
     @staticmethod
     def backward(ctx, grad_y):
-        x, w_prob, selection = ctx.saved_tensors
-        gx, gw = tree_conv_backward(grad_y, x, w_prob, selection, None, *ctx.geom, complete=False,
+        x, w, selection = ctx.saved_tensors
+        gx, gw = tree_conv_backward(grad_y, x, w, selection, None, *ctx.geom, complete=False,
                                     need_x=ctx.needs_input_grad[0],
-                                    need_w=ctx.needs_input_grad[1], uses=ctx.uses)
-        return gx, gw, None, None, None, None, None, None, None, None
+                                    need_w=ctx.needs_input_grad[1], uses=ctx.uses,
+                                    softmax=ctx.softmax)
+        return gx, gw, None, None, None, None, None, None, None, None, None
 
 
 class _FullConvLogicWithUses(Function):
-    """FullConvLogicFunction with the layer's cached channel-use index."""
+    """FullConvLogicFunction with the layer's cached channel-use index; with `softmax`, w
+    holds the node logits."""
 
     @staticmethod
-    def forward(ctx, x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
-                return_intermediate, return_indices, uses):
-        y, x2, x3, idx = full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h,
+    def forward(ctx, x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
+                return_intermediate, return_indices, uses, softmax=False):
+        y, x2, x3, idx = full_convlogic_forward(x, w, selection, stride_h, stride_w, pad_h,
                                                 pad_w, kernel_h, kernel_w,
-                                                intermediate=return_intermediate)
-        ctx.save_for_backward(x, w_prob, selection, idx)
+                                                intermediate=return_intermediate,
+                                                softmax=softmax)
+        ctx.save_for_backward(x, w, selection, idx)
         ctx.geom = (stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
         ctx.uses = uses
+        ctx.softmax = softmax
         extra = []
         if return_intermediate:
             extra += [x2, x3]
@@ -547,11 +563,12 @@ class _FullConvLogicWithUses(Function):
 
     @staticmethod
     def backward(ctx, grad_y, *unused):
-        x, w_prob, selection, idx = ctx.saved_tensors
-        gx, gw = tree_conv_backward(grad_y, x, w_prob, selection, idx, *ctx.geom, complete=True,
+        x, w, selection, idx = ctx.saved_tensors
+        gx, gw = tree_conv_backward(grad_y, x, w, selection, idx, *ctx.geom, complete=True,
                                     need_x=ctx.needs_input_grad[0],
-                                    need_w=ctx.needs_input_grad[1], uses=ctx.uses)
-        return gx, gw, None, None, None, None, None, None, None, None, None, None
+                                    need_w=ctx.needs_input_grad[1], uses=ctx.uses,
+                                    softmax=ctx.softmax)
+        return gx, gw, None, None, None, None, None, None, None, None, None, None, None
 
 
 class TreeLogicLayer(nn.Module):

@@ -582,6 +582,28 @@ int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x, const vo
                           void* grad_x, void* grad_w, void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/* The same block from the node logits (no reference counterpart: the module path, where the
+ * reference's ConvLogicLayer takes torch.softmax of its weights before the extension,
+ * third_party/convlogic_source_code/src/convlogic/convlogic_layer.py:236-321).  w_logits:
+ * [c_out, nodes, 16]; each node's probabilities are the softmax of its 16 logits, taken in the
+ * kernels where the coefficients are collapsed, so no probability tensor is formed.  The
+ * backward's grad_w is the gradient of the logits (softmax backward included).  Other
+ * arguments, outputs and errors as cl_tree_conv_forward / cl_tree_conv_backward. */
+int cl_tree_conv_forward_softmax(int dtype, const void* x, const void* w_logits,
+                                 const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
+                                 int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
+                                 int pad_w, int kernel_h, int kernel_w, int complete, void* y,
+                                 void* x2, void* x3, int32_t* indices, void* stream);
+
+int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
+                                  const void* w_logits, const int32_t* selection,
+                                  const int32_t* indices, const int32_t* ent_ptr,
+                                  const int32_t* ent, int64_t n, int64_t c_in, int64_t h,
+                                  int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
+                                  int pad_w, int kernel_h, int kernel_w, int complete,
+                                  void* grad_x, void* grad_w, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
 /* One tree level (TreeLogicLayer).  Replaces treelogic_forward (treelogic_kernel.cu:46-86):
  * x [n, channels, positions, 2*out_bits] -> y [n, channels, positions, out_bits], node j of the
  * channel on inputs (2j, 2j+1); w_prob [channels, out_bits, 16]; out_bits <= 4. */

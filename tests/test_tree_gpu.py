@@ -117,6 +117,55 @@ def test_block_backward_matches_oracle_and_is_reproducible(complete, dtype, stri
     assert gx3 is None and torch.equal(gw3, gw)
 
 
+# global gather, conv1 / conv2 of the tree reading, and the two LDS-staged shapes
+SOFTMAX_SHAPES = [SHAPES[0], SHAPES[2], SHAPES[3], SHAPES[7], SHAPES[8]]
+
+
+@pytest.mark.parametrize("complete", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("stride,pad,kernel,shape", SOFTMAX_SHAPES)
+def test_logit_entry_points_match_oracle_on_the_softmax(complete, dtype, stride, pad, kernel,
+                                                        shape):
+    """cl_tree_conv_forward_softmax / _backward_softmax take node logits: the outputs equal the
+    oracle's on softmax(logits) (float64), the weight gradient equals the oracle's probability
+    gradient through the softmax Jacobian p (g - sum p g), the input gradient the oracle's; the
+    winners are compared away from near ties, as for the probability entry points."""
+    n, c_in, h, w, c_out = shape
+    nodes = 7 if complete else 4
+    x, _, sel = make(11, n, c_in, h, w, c_out, kernel[0], nodes=nodes, dtype=dtype)
+    g = torch.Generator().manual_seed(12)
+    logits64 = 3.0 * torch.randn((c_out, nodes, 16), generator=g, dtype=torch.float64)
+    p64 = np_(torch.softmax(logits64, -1))
+    logits = logits64.to(x.device, dtype)
+    xs, ss = np_(x).astype(np.float64), np_(sel)
+    idx = oidx = None
+    if complete:
+        y, _, _, idx = TL.full_convlogic_forward(x, logits, sel, *stride, *pad, *kernel,
+                                                 intermediate=False, softmax=True)
+        ry, _, _, ridx = T.block_forward(xs, p64, ss, stride, pad, kernel)
+        eps = float(np.finfo(np.float32 if dtype == torch.float32 else np.float64).eps)
+        free = _near_ties(_window_scores(xs, p64, ss, stride, pad, kernel), eps)
+        assert np.array_equal(np_(idx)[~free], ridx[~free])
+        oidx = np.where(free, np_(idx), ridx)
+    else:
+        y = TL.convlogic_forward(x, logits, sel, *stride, *pad, *kernel, softmax=True)
+        ry = T.block_forward(xs, p64, ss, stride, pad, kernel, complete=False)
+    np.testing.assert_allclose(np_(y), ry, **tol(dtype))
+    gy = torch.randn(y.shape, generator=g, dtype=torch.float64).to(y.device, dtype)
+    gx, gl = TL.tree_conv_backward(gy, x, logits, sel, idx, *stride, *pad, *kernel, complete,
+                                   softmax=True)
+    rgx, rgw = T.block_backward(xs, p64, ss, stride, pad, kernel, np_(gy).astype(np.float64),
+                                complete, idx=oidx)
+    rgl = p64 * (rgw - (rgw * p64).sum(-1, keepdims=True))
+    np.testing.assert_allclose(np_(gx), rgx, **tol(dtype))
+    # p (g - sum p g) loses the absolute precision of g in the difference: scale by max |g|
+    scale = max(1.0, float(np.abs(rgw).max()))
+    np.testing.assert_allclose(np_(gl) / scale, rgl / scale, **tol(dtype))
+    gx2, gl2 = TL.tree_conv_backward(gy, x, logits, sel, idx, *stride, *pad, *kernel, complete,
+                                     softmax=True)
+    assert torch.equal(gx, gx2) and torch.equal(gl, gl2)
+
+
 @pytest.mark.parametrize("complete", [True, False])
 @pytest.mark.parametrize("dtype,hw", [(torch.float32, 136), (torch.float64, 96)])
 def test_backward_of_planes_beyond_lds_in_row_bands(complete, dtype, hw):
@@ -429,9 +478,9 @@ def test_split_layers_vs_complete(stride, pad):
 
 
 def test_module_gradients_match_oracle():
-    """Training mode through the module: softmax of the logits (torch), the block's kernels,
-    and the gradients of the logits and the input against the oracle chained with the softmax
-    Jacobian."""
+    """Training mode through the module: the block's kernels on the logits (softmax and its
+    backward in the kernels), and the gradients of the logits and the input against the oracle
+    chained with the softmax Jacobian."""
     torch.manual_seed(9)
     layer = cl.ConvLogicLayer(4, 6, stride=2, padding=1, kernel=3, complete=True).cuda().double()
     x = torch.rand(3, 4, 12, 12, device="cuda", dtype=torch.float64, requires_grad=True)
