@@ -51,7 +51,7 @@ SIGNATURES: dict[str, list] = {
     "cl_tree_conv_backward": [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                               _int, _int, _int, _int, _int, _int, _int, _p, _p, _p, _i64, _p],
     "cl_tree_conv_forward_softmax": [_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int,
-                                     _int, _int, _int, _int, _int, _p, _p, _p, _p, _p],
+                                     _int, _int, _int, _int, _int, _p, _p, _p, _p, _int, _p],
     "cl_tree_conv_backward_softmax": [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                       _i64, _int, _int, _int, _int, _int, _int, _int, _p, _p, _p,
                                       _i64, _p],

@@ -46,6 +46,7 @@ struct TreeDims {
     int n, cin, h, w, cout, ho, wo, sh, sw, ph, pw;
     int complete;
     int softmax;  // the weights are logits: softmax over each node's 16 values on load
+    int regular;  // the caller guarantees every tap lies in the window and reads a channel < cin
     int P;  // items per (sample, channel): pooled windows (complete) or conv positions
     FastDiv div_p, div_wp;  // by P, and by the windows per pooled row (complete) or wo
     FastDiv div_wo;         // by wo (conv positions -> rows)
@@ -447,7 +448,10 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
             const int cc = it + sub;
             const int cl_ = (sub < cpw && cc < c_n) ? cc : it;
             const int flag = tflag[cl_];
-            const bool cok = sub < cpw && cc < c_n && flag == 0;  // flagged: k_tree_fwd_fix
+            // flagged: k_tree_fwd_fix, or, when the caller guaranteed regular taps (no fix-up
+            // launch), NaN outputs that make the broken guarantee visible
+            const bool cok = sub < cpw && cc < c_n && (flag == 0 || d.regular != 0);
+            const bool poison = flag != 0;
             T k[NODES][4];
 #pragma unroll
             for (int q = 0; q < NODES; ++q)
@@ -490,7 +494,7 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
                     if (live) {
                         const int64_t pos = cell * d.P + p;
 #pragma unroll
-                        for (int qq = 0; qq < 4; ++qq) y[pos * 4 + qq] = gv[qq];
+                        for (int qq = 0; qq < 4; ++qq) y[pos * 4 + qq] = poison ? quiet_nan<T>() : gv[qq];
                     }
                 } else {
                     const T t0 = node(k[4], gv[0], gv[1]);
@@ -500,11 +504,12 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
                         const int64_t pos = cell * d.ho * d.wo + int64_t(oy) * d.wo + ox;
                         if (x2) {
 #pragma unroll
-                            for (int qq = 0; qq < 4; ++qq) x2[pos * 4 + qq] = gv[qq];
+                            for (int qq = 0; qq < 4; ++qq)
+                                x2[pos * 4 + qq] = poison ? quiet_nan<T>() : gv[qq];
                         }
                         if (x3) {
-                            x3[pos * 2 + 0] = t0;
-                            x3[pos * 2 + 1] = t1;
+                            x3[pos * 2 + 0] = poison ? quiet_nan<T>() : t0;
+                            x3[pos * 2 + 1] = poison ? quiet_nan<T>() : t1;
                         }
                     }
                     // No NaN enters the quad (one enters as -inf), so for the later lane of a
@@ -533,8 +538,8 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
                         wi = take ? wo_ : wi;
                     }
                     if (live && q_lane == 0) {
-                        y[cell * d.P + p] = rr;
-                        if (idx) idx[cell * d.P + p] = wi;
+                        y[cell * d.P + p] = poison ? quiet_nan<T>() : rr;
+                        if (idx) idx[cell * d.P + p] = poison ? -1 : wi;
                     }
                 }
             }
@@ -1187,6 +1192,7 @@ int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t
     d.pw = pw;
     d.complete = complete ? 1 : 0;
     d.softmax = 0;
+    d.regular = 0;
     d.P = int(P);
     d.div_p = make_fastdiv(uint32_t(std::max<int64_t>(P, 1)));
     d.div_wp = make_fastdiv(uint32_t(std::max<int64_t>(complete ? wo / 2 : wo, 1)));
@@ -1295,6 +1301,7 @@ int launch_tree_fwd_lds(const TreeDims& d, const TreeLds& g, int groups, int64_t
     kern<<<dim3(unsigned(d.n), unsigned(groups)), kFwdLdsThreads, size_t(lds), s>>>(
         x, w_prob, sel, d, g, y, x2, x3, idx);
     if (int rc = check_launch("cl_tree_conv_forward")) return rc;
+    if (d.regular) return CL_OK;  // no channel for the fix-up pass, by the caller's guarantee
     k_tree_fwd_fix<T, COMPLETE><<<unsigned(ceil_div(d.cout, kFixChannels)), kFixChannels, 0, s>>>(
         x, w_prob, sel, d, g.kh, g.kw, y, x2, x3, idx);
     return check_launch("cl_tree_conv_forward");
@@ -1328,12 +1335,13 @@ int tree_conv_forward_impl(int dtype, const void* x, const void* w_prob,
                            const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
                            int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
                            int pad_w, int kernel_h, int kernel_w, int complete, void* y, void* x2,
-                           void* x3, int32_t* indices, int softmax, void* stream) {
+                           void* x3, int32_t* indices, int softmax, int regular, void* stream) {
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
     d.softmax = softmax ? 1 : 0;
+    d.regular = regular ? 1 : 0;
     if (n == 0 || c_out == 0) return CL_OK;
     CL_ARG(x && w_prob && selection && y, "null pointer argument");
     const unsigned gx = unsigned(ceil_div(int64_t(d.n) * d.P, 256));
@@ -1380,7 +1388,7 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
     clear_error();
     return tree_conv_forward_impl(dtype, x, w_prob, selection, n, c_in, h, w, c_out, stride_h,
                                   stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
-                                  indices, 0, stream);
+                                  indices, 0, 0, stream);
 }
 
 extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void* w_logits,
@@ -1388,11 +1396,12 @@ extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void
                                             int64_t h, int64_t w, int64_t c_out, int stride_h,
                                             int stride_w, int pad_h, int pad_w, int kernel_h,
                                             int kernel_w, int complete, void* y, void* x2,
-                                            void* x3, int32_t* indices, void* stream) {
+                                            void* x3, int32_t* indices, int regular_taps,
+                                            void* stream) {
     clear_error();
     return tree_conv_forward_impl(dtype, x, w_logits, selection, n, c_in, h, w, c_out, stride_h,
                                   stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
-                                  indices, 1, stream);
+                                  indices, 1, regular_taps, stream);
 }
 
 extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,

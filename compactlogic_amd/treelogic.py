@@ -94,13 +94,25 @@ def _check_block(x, w_prob, selection, nodes):
     return c_out
 
 
+def _forward_call(softmax: bool, regular: bool):
+    if regular and not softmax:
+        raise ValueError("the regular-taps guarantee is taken by the logits forward only")
+    return ("cl_tree_conv_forward_softmax",) if softmax else ("cl_tree_conv_forward",)
+
+
+def _forward_tail(softmax: bool, regular: bool):
+    return (int(regular),) if softmax else ()
+
+
 def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h,
-                           kernel_w, intermediate: bool = True, softmax: bool = False):
+                           kernel_w, intermediate: bool = True, softmax: bool = False,
+                           regular: bool = False):
     """Complete block forward (replaces convlogic_cuda.full_convlogic_forward,
     full_convlogic_kernel.cu:156-231): (y [N, C, Ho/2, Wo/2], x2 [N, C, Ho, Wo, 4],
     x3 [N, C, Ho, Wo, 2], indices int32 [N, C, Ho/2 * Wo/2]); x2 and x3 are None unless
     `intermediate`.  With `softmax`, w_prob holds the node logits and the kernels take their
-    softmax (cl_tree_conv_forward_softmax)."""
+    softmax (cl_tree_conv_forward_softmax); `regular` then passes that call the guarantee that
+    every tap lies in the kernel window and reads an input channel."""
     c_out = _check_block(x, w_prob, selection, 7)
     n, c_in, h, w = x.shape
     ho, wo = _out_hw(h, w, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
@@ -117,16 +129,15 @@ def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_
         x3 = torch.empty((n, c_out, ho, wo, 2), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
         timing.timed(f"cl_tree_conv_forward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
-            "cl_tree_conv_forward_softmax" if softmax else "cl_tree_conv_forward",
-            _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
+            *_forward_call(softmax, regular), _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
             selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
             kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2), _dl.ptr(x3), idx.data_ptr(),
-            _dl.stream_of(x)))
+            *_forward_tail(softmax, regular), _dl.stream_of(x)))
     return y, x2, x3, idx
 
 
 def convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
-                      softmax: bool = False):
+                      softmax: bool = False, regular: bool = False):
     """Conv gates only (replaces convlogic_cuda.convlogic_forward, convlogic_kernel.cu:67-107):
     y [N, C, Ho, Wo, 4].  With `softmax`, w_prob holds the node logits."""
     c_out = _check_block(x, w_prob, selection, 4)
@@ -136,10 +147,10 @@ def convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, ke
         raise RuntimeError(f"Invalid output shape: H_out={ho}, W_out={wo}")
     y = torch.empty((n, c_out, ho, wo, 4), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _capi.call("cl_tree_conv_forward_softmax" if softmax else "cl_tree_conv_forward",
-                   _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
-                   selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
-                   kernel_h, kernel_w, 0, y.data_ptr(), None, None, None, _dl.stream_of(x))
+        _capi.call(*_forward_call(softmax, regular), _dl.dtype_code(x), x.data_ptr(),
+                   w_prob.data_ptr(), selection.data_ptr(), n, c_in, h, w, c_out, stride_h,
+                   stride_w, pad_h, pad_w, kernel_h, kernel_w, 0, y.data_ptr(), None, None, None,
+                   *_forward_tail(softmax, regular), _dl.stream_of(x))
     return y
 
 
@@ -436,6 +447,7 @@ class ConvLogicLayer(nn.Module):
         assert selection.shape == (out_channels, 8)
         assert self.weights.shape[-1] == 16, f"Expected 16 logic functions, got {self.weights.shape[-1]}"
         self._uses = None
+        self._regular = None
 
     def generate_selection(self, num_chn: int = 2) -> torch.Tensor:
         return generate_selection(self.in_channels, self.out_channels, self.kernel, self.groups,
@@ -453,6 +465,25 @@ class ConvLogicLayer(nn.Module):
             self._uses = (weakref.ref(sel), (sel._version, sel.device),
                           channel_uses(sel.to(torch.int32), self.in_channels))
         return self._uses[2]
+
+    def _regular_taps(self) -> bool:
+        """Whether every tap of the selection lies in the kernel window and reads an input
+        channel (what the selection sampler draws), cached with a weak reference to the
+        selection and its version.  A cold cache under HIP graph capture answers False (no host
+        read is possible there), which only costs the forward its fix-up launch."""
+        sel = self.selection
+        key = (sel._version, sel.device)
+        hit = self._regular
+        if hit is not None and hit[0]() is sel and hit[1] == key:
+            return hit[2]
+        if sel.is_cuda and torch.cuda.is_current_stream_capturing():
+            return False
+        s = sel.to(torch.int64).cpu()
+        ok = bool((((s >> 16) & 0xFFFF) < self.in_channels).all()
+                  and (((s >> 8) & 0xFF) < self.kernel[0]).all()
+                  and ((s & 0xFF) < self.kernel[1]).all())
+        self._regular = (weakref.ref(sel), key, ok)
+        return ok
 
     def _w_prob(self, dtype):
         if self.training:
@@ -477,11 +508,12 @@ class ConvLogicLayer(nn.Module):
         sel = self.selection.to(torch.int32).contiguous()
         args = (x, w, sel, self.stride[0], self.stride[1], self.padding[0], self.padding[1],
                 self.kernel[0], self.kernel[1])
+        regular = softmax and self._regular_taps()
         if self.complete:
             return _FullConvLogicWithUses.apply(*args, self.return_intermediate,
                                                 self.return_indices, self._channel_uses(),
-                                                softmax)
-        return _ConvLogicWithUses.apply(*args, self._channel_uses(), softmax)
+                                                softmax, regular)
+        return _ConvLogicWithUses.apply(*args, self._channel_uses(), softmax, regular)
 
     def forward_packed(self, x: PackBitsTensor, in_hw=None) -> PackBitsTensor:
         """Bitwise block on packed rows (eval mode): rows = in_channels * h * w features in NCHW
@@ -517,9 +549,9 @@ class _ConvLogicWithUses(Function):
 
     @staticmethod
     def forward(ctx, x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
-                uses, softmax=False):
+                uses, softmax=False, regular=False):
         y = convlogic_forward(x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h,
-                              kernel_w, softmax=softmax)
+                              kernel_w, softmax=softmax, regular=regular)
         ctx.save_for_backward(x, w, selection)
         ctx.geom = (stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
         ctx.uses = uses
@@ -533,7 +565,7 @@ class _ConvLogicWithUses(Function):
                                     need_x=ctx.needs_input_grad[0],
                                     need_w=ctx.needs_input_grad[1], uses=ctx.uses,
                                     softmax=ctx.softmax)
-        return gx, gw, None, None, None, None, None, None, None, None, None
+        return gx, gw, None, None, None, None, None, None, None, None, None, None
 
 
 class _FullConvLogicWithUses(Function):
@@ -542,11 +574,11 @@ class _FullConvLogicWithUses(Function):
 
     @staticmethod
     def forward(ctx, x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
-                return_intermediate, return_indices, uses, softmax=False):
+                return_intermediate, return_indices, uses, softmax=False, regular=False):
         y, x2, x3, idx = full_convlogic_forward(x, w, selection, stride_h, stride_w, pad_h,
                                                 pad_w, kernel_h, kernel_w,
                                                 intermediate=return_intermediate,
-                                                softmax=softmax)
+                                                softmax=softmax, regular=regular)
         ctx.save_for_backward(x, w, selection, idx)
         ctx.geom = (stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
         ctx.uses = uses
@@ -568,7 +600,7 @@ class _FullConvLogicWithUses(Function):
                                     need_x=ctx.needs_input_grad[0],
                                     need_w=ctx.needs_input_grad[1], uses=ctx.uses,
                                     softmax=ctx.softmax)
-        return gx, gw, None, None, None, None, None, None, None, None, None, None, None
+        return gx, gw, None, None, None, None, None, None, None, None, None, None, None, None
 
 
 class TreeLogicLayer(nn.Module):

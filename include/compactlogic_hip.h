@@ -587,13 +587,18 @@ int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x, const vo
  * third_party/convlogic_source_code/src/convlogic/convlogic_layer.py:236-321).  w_logits:
  * [c_out, nodes, 16]; each node's probabilities are the softmax of its 16 logits, taken in the
  * kernels where the coefficients are collapsed, so no probability tensor is formed.  The
- * backward's grad_w is the gradient of the logits (softmax backward included).  Other
- * arguments, outputs and errors as cl_tree_conv_forward / cl_tree_conv_backward. */
+ * backward's grad_w is the gradient of the logits (softmax backward included).
+ * regular_taps = 1 is the caller's guarantee that every tap lies in the kernel window (row <
+ * kernel_h, col < kernel_w) and reads a channel < c_in, as the module's selection sampler
+ * draws them: the forward then skips the launch that computes irregular channels, and a
+ * channel that breaks the guarantee may get NaN outputs (and winner -1) instead of its values.
+ * Other arguments, outputs and errors as cl_tree_conv_forward / cl_tree_conv_backward. */
 int cl_tree_conv_forward_softmax(int dtype, const void* x, const void* w_logits,
                                  const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
                                  int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
                                  int pad_w, int kernel_h, int kernel_w, int complete, void* y,
-                                 void* x2, void* x3, int32_t* indices, void* stream);
+                                 void* x2, void* x3, int32_t* indices, int regular_taps,
+                                 void* stream);
 
 int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
                                   const void* w_logits, const int32_t* selection,

@@ -438,6 +438,60 @@ def test_forward_taps_outside_the_window_and_out_of_range_channels(dtype, shape,
         assert torch.isnan(y[:, 4]).all()
 
 
+@pytest.mark.parametrize("complete", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_regular_taps_guarantee_skips_the_fix_up_and_poisons_a_broken_one(complete, dtype):
+    """cl_tree_conv_forward_softmax with regular_taps = 1: on a sampled (regular) selection the
+    outputs are bitwise those of the call without the guarantee; a channel that breaks it on
+    the LDS-staged path (a tap outside the window, another channel reading input C) gets NaN
+    outputs and winner -1, and every other channel is unchanged."""
+    n, c_in, h, w, c_out = 3, 4, 12, 12, 64   # LDS-staged
+    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    nodes = 7 if complete else 4
+    x, _, sel = make(21, n, c_in, h, w, c_out, 3, nodes=nodes, dtype=dtype)
+    logits = torch.randn((c_out, nodes, 16), generator=torch.Generator().manual_seed(22),
+                         dtype=torch.float64).to(x.device, dtype)
+
+    def fwd(s, regular):
+        if complete:
+            y, x2, x3, idx = TL.full_convlogic_forward(x, logits, s, *stride, *pad, *kernel,
+                                                       softmax=True, regular=regular)
+            return y, x2, x3, idx
+        return (TL.convlogic_forward(x, logits, s, *stride, *pad, *kernel, softmax=True,
+                                     regular=regular),)
+
+    for a, b in zip(fwd(sel, False), fwd(sel, True)):
+        assert torch.equal(a, b)
+    bad = sel.clone()
+    bad[1, 2] = (bad[1, 2] & ~0xFF00) | (4 << 8)        # row 4 of a 3x3 window
+    bad[4, 0] = (bad[4, 0] & 0xFFFF) | (c_in << 16)     # input channel C
+    ref, got = fwd(bad, False), fwd(bad, True)
+    live = [c for c in range(c_out) if c not in (1, 4)]
+    for a, b in zip(ref, got):
+        assert torch.equal(a[:, live], b[:, live])
+    assert torch.isnan(got[0][:, [1, 4]]).all()
+    if complete:
+        assert torch.isnan(got[1][:, [1, 4]]).all() and torch.isnan(got[2][:, [1, 4]]).all()
+        assert (got[3][:, [1, 4]] == -1).all()
+
+
+def test_module_regular_taps_cache_follows_the_selection():
+    """ConvLogicLayer passes the guarantee only for a selection whose taps it has checked on
+    the host; an in-place change of the selection is seen through its version."""
+    torch.manual_seed(5)
+    layer = cl.ConvLogicLayer(4, 8, stride=2, padding=1, kernel=3, complete=True).cuda()
+    assert layer._regular_taps()
+    with torch.no_grad():
+        layer.selection[0, 0] = (layer.selection[0, 0] & ~0xFF00) | (3 << 8)
+    assert not layer._regular_taps()
+    x = torch.rand(2, 4, 12, 12, device="cuda")
+    y = layer(x)   # the fix-up kernel computes the out-of-window channel
+    ref = T.block_forward(np_(x).astype(np.float64),
+                          np_(torch.softmax(layer.weights.detach().double(), -1)),
+                          np_(layer.selection), (2, 2), (1, 1), (3, 3))[0]
+    np.testing.assert_allclose(np_(y), ref, rtol=1e-5, atol=1e-6)
+
+
 def test_identity_init():
     layer = cl.ConvLogicLayer(2, 2, residual_init=True, complete=True).cuda().eval()
     assert bool((layer.weights.argmax(-1) == 3).all())
