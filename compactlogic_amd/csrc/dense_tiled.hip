@@ -51,13 +51,15 @@ __device__ __forceinline__ int4 ld_rec(const int4* p) {
     return make_int4(v[0], v[1], v[2], v[3]);
 }
 
-// Lane accesses of the forward / backward tiled kernels are this many 16-byte vectors wide
-// (two for the backward: twice the bytes per gather for the same index records).
+// Lane accesses of the forward / backward tiled kernels are this many 16-byte vectors wide.
+// One for both: with connections='random' (16 runs per neuron) two-vector backward lanes
+// measured 0.346 ms per 12000 -> 12000 layer against 0.335 ms with one (2.78 -> 2.69 ms per
+// step); 8-lane chunks were far slower (0.58 ms: the per-chunk run work doubles).
 #ifndef CL_FWD_VEC_MULT
 #define CL_FWD_VEC_MULT 1
 #endif
 #ifndef CL_BWD_VEC_MULT
-#define CL_BWD_VEC_MULT 2
+#define CL_BWD_VEC_MULT 1
 #endif
 #ifndef CL_FUSED_VEC_MULT
 #define CL_FUSED_VEC_MULT 1
