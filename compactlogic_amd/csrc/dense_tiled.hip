@@ -55,6 +55,12 @@ __device__ __forceinline__ int4 ld_rec(const int4* p) {
 // One for both: with connections='random' (16 runs per neuron) two-vector backward lanes
 // measured 0.346 ms per 12000 -> 12000 layer against 0.335 ms with one (2.78 -> 2.69 ms per
 // step); 8-lane chunks were far slower (0.58 ms: the per-chunk run work doubles).
+// Runs of a neuron the tiled forward gathers together (connections='random': 0.134 -> 0.111 ms
+// per 12000 -> 12000 layer against one at a time; eight measured 0.124 ms).
+constexpr int kFwdRunBatch = 4;
+// Inverse-index entries the tiled backward gathers together (connections='random': 0.367 ->
+// 0.314 ms per 12000 -> 12000 layer against one at a time; two 0.342, eight 0.339 ms).
+constexpr int kBwdEntryBatch = 4;
 #ifndef CL_FWD_VEC_MULT
 #define CL_FWD_VEC_MULT 1
 #endif
@@ -272,7 +278,37 @@ __device__ __forceinline__ void fwd_tile(const T* __restrict__ x, const T* __res
         V acc = V(nan_of<T>());
         if (ok[j]) {
             acc = k[j][3] * (va[j] * vb[j]) + k[j][2] * vb[j] + k[j][1] * va[j] + k[j][0];
-            for (int64_t r = int64_t(rec[j].z) + 1; r < rec[j].w; ++r) {
+            int64_t r = int64_t(rec[j].z) + 1;
+            // the further runs kFwdRunBatch at a time: their records and rows are in flight
+            // together, the additions stay in run order
+            bool badr = false;
+            for (; r + kFwdRunBatch <= rec[j].w; r += kFwdRunBatch) {
+                int2 ab[kFwdRunBatch];
+                V4 kr[kFwdRunBatch];
+#pragma unroll
+                for (int q = 0; q < kFwdRunBatch; ++q) {
+                    ab[q] = run_ab[r + q];
+                    kr[q] = vld<V4>(kc + 4 * (r + q));
+                }
+                V a[kFwdRunBatch], b[kFwdRunBatch];
+#pragma unroll
+                for (int q = 0; q < kFwdRunBatch; ++q) {
+                    const bool v = uint32_t(ab[q].x) < uint64_t(in_dim) &&
+                                   uint32_t(ab[q].y) < uint64_t(in_dim);
+                    badr = badr || !v;
+                    a[q] = vld<V>(x + int64_t(v ? ab[q].x : 0) * B + idx);
+                    b[q] = vld<V>(x + int64_t(v ? ab[q].y : 0) * B + idx);
+                }
+                if (badr) break;
+#pragma unroll
+                for (int q = 0; q < kFwdRunBatch; ++q)
+                    acc += kr[q][3] * (a[q] * b[q]) + kr[q][2] * b[q] + kr[q][1] * a[q] + kr[q][0];
+            }
+            if (badr) {
+                r = rec[j].w;
+                acc = V(nan_of<T>());
+            }
+            for (; r < rec[j].w; ++r) {
                 const int2 ab = run_ab[r];
                 if (uint32_t(ab.x) >= uint64_t(in_dim) || uint32_t(ab.y) >= uint64_t(in_dim)) {
                     acc = V(nan_of<T>());
@@ -828,68 +864,69 @@ __device__ __forceinline__ void bwd_tile(
         xi[j] = V(T(0));
         if (WANT_GW && live[j] && col) xi[j] = vld<V>(x + row[j] * B + idx);
     }
-    // The records of the next entry are fetched while the current entry's gathers are in
-    // flight; the accumulation order is the entry order.
-    int4 rec[NPG];
-    V2 kk[NPG];
+    // Entries are taken kBwdEntryBatch at a time: the batch's records and coefficients, then
+    // all of its row gathers, are in flight together (every load unconditional: an unused
+    // entry reads entry e0 and row 0, lanes past the batch read sample 0, and both are masked
+    // afterwards); the accumulation order is the entry order.
+    constexpr int EB = kBwdEntryBatch;
+    const int64_t off = col ? idx : 0;
 #pragma unroll
-    for (int j = 0; j < NPG; ++j) {
-        rec[j] = make_int4(0, 0, 0, 0);
-        kk[j] = V2(T(0));
-        if (deg[j] > 0) {
-            rec[j] = inv_rec[e0[j]];
-            kk[j] = vld<V2>(inv_coef + 2 * e0[j]);
-        }
-    }
-    for (int64_t k = 0; k < maxdeg; ++k) {
-        int4 cur[NPG];
-        V2 ck[NPG];
-        V vo[NPG], vg[NPG];
-        bool use[NPG];
+    for (int j = 0; j < NPG; ++j)
+        if (!live[j]) e0[j] = 0;  // a dead or corrupt slot's unused loads read entry 0
+    for (int64_t k = 0; k < maxdeg; k += EB) {
+        int4 cur[NPG][EB];
+        V2 ck[NPG][EB];
+        bool use[NPG][EB];
 #pragma unroll
-        for (int j = 0; j < NPG; ++j) {
-            cur[j] = rec[j];
-            ck[j] = kk[j];
-            if (k + 1 < deg[j]) {
-                rec[j] = inv_rec[e0[j] + k + 1];
-                kk[j] = vld<V2>(inv_coef + 2 * (e0[j] + k + 1));
-            }
-            use[j] = k < deg[j];
-            if (use[j] && (uint64_t(cur[j].x) >= uint64_t(out_dim) ||
-                           uint64_t(cur[j].y) >= uint64_t(in_dim) ||
-                           uint64_t(cur[j].z) >= uint64_t(num_runs))) {
-                bad[j] = true;
-                use[j] = false;
-            }
-            vo[j] = V(T(0));
-            vg[j] = V(T(0));
-            if (use[j] && col) {
-                vo[j] = vld<V>(x + int64_t(cur[j].y) * B + idx);
-                vg[j] = vld<V>(gy + int64_t(cur[j].x) * B + idx);
-            }
-        }
+        for (int j = 0; j < NPG; ++j)
 #pragma unroll
-        for (int j = 0; j < NPG; ++j) {
-            if (!use[j]) continue;
-            if (WANT_GX) acc[j] += (ck[j][0] + ck[j][1] * vo[j]) * vg[j];
-            if (WANT_GW && cur[j].w == 0) {
-                const V ga = vg[j] * xi[j];
-                T s1 = hsum<T, VEC>(vg[j]), sa = hsum<T, VEC>(ga);
-                T sb = hsum<T, VEC>(vg[j] * vo[j]), sab = hsum<T, VEC>(ga * vo[j]);
-                s1 = group_sum<LPN>(s1);
-                sa = group_sum<LPN>(sa);
-                sb = group_sum<LPN>(sb);
-                sab = group_sum<LPN>(sab);
-                if (leader) {
-                    V4 mv;
-                    mv[0] = s1;
-                    mv[1] = sa;
-                    mv[2] = sb;
-                    mv[3] = sab;
-                    *reinterpret_cast<V4*>(part + (int64_t(cur[j].z) * tm.nchunks + c) * 4) = mv;
+            for (int q = 0; q < EB; ++q) {
+                use[j][q] = k + q < deg[j];
+                const int64_t e = e0[j] + (use[j][q] ? k + q : 0);
+                cur[j][q] = inv_rec[e];
+                ck[j][q] = vld<V2>(inv_coef + 2 * e);
+            }
+        V vo[NPG][EB], vg[NPG][EB];
+#pragma unroll
+        for (int j = 0; j < NPG; ++j)
+#pragma unroll
+            for (int q = 0; q < EB; ++q) {
+                if (use[j][q] && (uint64_t(cur[j][q].x) >= uint64_t(out_dim) ||
+                                  uint64_t(cur[j][q].y) >= uint64_t(in_dim) ||
+                                  uint64_t(cur[j][q].z) >= uint64_t(num_runs))) {
+                    bad[j] = true;
+                    use[j][q] = false;
+                }
+                const bool u = use[j][q];
+                vo[j][q] = vld<V>(x + int64_t(u ? cur[j][q].y : 0) * B + off);
+                vg[j][q] = vld<V>(gy + int64_t(u ? cur[j][q].x : 0) * B + off);
+            }
+#pragma unroll
+        for (int j = 0; j < NPG; ++j)
+#pragma unroll
+            for (int q = 0; q < EB; ++q) {
+                if (!use[j][q]) continue;
+                const V o = col ? vo[j][q] : V(T(0));
+                const V g = col ? vg[j][q] : V(T(0));
+                if (WANT_GX) acc[j] += (ck[j][q][0] + ck[j][q][1] * o) * g;
+                if (WANT_GW && cur[j][q].w == 0) {
+                    const V ga = g * xi[j];
+                    T s1 = hsum<T, VEC>(g), sa = hsum<T, VEC>(ga);
+                    T sb = hsum<T, VEC>(g * o), sab = hsum<T, VEC>(ga * o);
+                    s1 = group_sum<LPN>(s1);
+                    sa = group_sum<LPN>(sa);
+                    sb = group_sum<LPN>(sb);
+                    sab = group_sum<LPN>(sab);
+                    if (leader) {
+                        V4 mv;
+                        mv[0] = s1;
+                        mv[1] = sa;
+                        mv[2] = sb;
+                        mv[3] = sab;
+                        *reinterpret_cast<V4*>(part + (int64_t(cur[j][q].z) * tm.nchunks + c) * 4) = mv;
+                    }
                 }
             }
-        }
     }
     if (WANT_GX && col) {
 #pragma unroll
