@@ -817,8 +817,8 @@ __global__ __launch_bounds__(256) void k_wgrad_rows(const T* __restrict__ x,
 // processing-slot order (descending entry count, so the rows of a group and the groups of a
 // wave have nearly equal work), and slot_rec[slot] = (input row, first entry, end entry) is
 // one load.  Entry e of the inverse index carries a record (neuron, other input, run, side)
-// and the coefficients (own-operand K, K3) written by k_prep; the records of the group's NPG
-// rows for the next step are fetched while the current step's row loads are in flight.
+// and the coefficients (own-operand K, K3) written by k_prep; entries are taken
+// kBwdEntryBatch at a time, their records and row gathers in flight together.
 // part[(r * nchunks + c) * 4 + j] receives the chunk-c moments of run r (WANT_GW) at the
 // run's operand-a entry.
 template <typename T, int VEC, int LPN, int NPG, bool WANT_GX, bool WANT_GW>
