@@ -195,15 +195,33 @@ __global__ __launch_bounds__(256) void k_prep(const T* __restrict__ w, int softm
     }
     int64_t r0 = run_ptr[o], r1 = run_ptr[o + 1];
     if (r0 < 0 || r1 < r0 || r1 > num_runs) return;
-    for (int64_t r = r0; r < r1; ++r) {
-        const int gl = run_gl[r];
+    // The row's gate codes, and the records of its runs 16 at a time (one per lane, handed
+    // round by lane shuffles), are loaded before the runs are walked: no load waits inside.
+    int code[kMaxSlotGroups];
+#pragma unroll
+    for (int m = 0; m < kMaxSlotGroups; ++m) {
+        const int g = l + 16 * m;
+        code[m] = (m < ng && g < G) ? int(gs[o * G + g]) : 0;
+    }
+    const int row_lane0 = int(threadIdx.x) & ~15;
+    for (int64_t rb = r0; rb < r1; rb += 16) {
+    const int64_t rl = rb + l;
+    const bool have = rl < r1;
+    const int gl_l = have ? run_gl[rl] : 0;
+    const int pa_l = (have && inv_coef) ? inv_pos[2 * rl] : -1;
+    const int pb_l = (have && inv_coef) ? inv_pos[2 * rl + 1] : -1;
+    const int nb = int(r1 - rb < 16 ? r1 - rb : 16);
+    for (int q = 0; q < nb; ++q) {
+        const int64_t r = rb + q;
+        const int gl = __shfl(gl_l, row_lane0 + q);
+        const int64_t pa = __shfl(pa_l, row_lane0 + q), pb = __shfl(pb_l, row_lane0 + q);
         const int g0 = gl & 0xff, g1 = g0 + (gl >> 8);
         T k0 = 0, k1 = 0, k2 = 0, k3 = 0;
 #pragma unroll
         for (int m = 0; m < kMaxSlotGroups; ++m) {
             const int g = l + 16 * m;
             if (m < ng && g >= g0 && g < g1 && g < G) {
-                const Coef4<T> c = gate_coef<T>(gs[o * G + g]);
+                const Coef4<T> c = gate_coef<T>(code[m]);
                 k0 = fma(p[m], c.c0, k0);
                 k1 = fma(p[m], c.c1, k1);
                 k2 = fma(p[m], c.c2, k2);
@@ -222,7 +240,6 @@ __global__ __launch_bounds__(256) void k_prep(const T* __restrict__ w, int softm
             kc[4 * r + 3] = k3;
             if (inv_coef) {
                 // (own-operand coefficient, c3) of the run's two inverse-index entries
-                const int64_t pa = inv_pos[2 * r], pb = inv_pos[2 * r + 1];
                 if (uint64_t(pa) < uint64_t(2 * num_runs)) {
                     inv_coef[2 * pa + 0] = k1;
                     inv_coef[2 * pa + 1] = k3;
@@ -233,6 +250,7 @@ __global__ __launch_bounds__(256) void k_prep(const T* __restrict__ w, int softm
                 }
             }
         }
+    }
     }
 }
 
