@@ -194,6 +194,8 @@ def tree_network(cfg: TreeConfig, device="cuda", seed: int = NET_SEED) -> torch.
         layers.append(layer)
         ho, wo = (h + 2 * pad - ks) // stride + 1, (w + 2 * pad - ks) // stride + 1
         c, h, w = c_out, ho // 2, wo // 2
+    # the last block feeds the flattened dense layers: its training output feature-major
+    layers[-1].rows_output = True
     layers.append(torch.nn.Flatten())
     in_dim = c * h * w
     for out_dim in cfg.widths:

@@ -47,10 +47,17 @@ struct TreeDims {
     int complete;
     int softmax;  // the weights are logits: softmax over each node's 16 values on load
     int regular;  // the caller guarantees every tap lies in the window and reads a channel < cin
+    int y_rows;   // complete form: y / grad_y element (n, c, p) at (c * P + p) * n_total + n
     int P;  // items per (sample, channel): pooled windows (complete) or conv positions
     FastDiv div_p, div_wp;  // by P, and by the windows per pooled row (complete) or wo
     FastDiv div_wo;         // by wo (conv positions -> rows)
 };
+
+// Pooled output / its gradient of (sample n, channel c, window p): NCHW, or with y_rows the
+// feature-major [c * P + p][n] rows a following dense layer reads without a transpose.
+__device__ __forceinline__ int64_t y_at(const TreeDims& d, int n, int c, int p) {
+    return d.y_rows ? (int64_t(c) * d.P + p) * d.n + n : (int64_t(n) * d.cout + c) * d.P + p;
+}
 
 // Decoded tap: channel, row and column offset relative to the output position (pad removed).
 struct TapOff {
@@ -263,7 +270,7 @@ __device__ __forceinline__ void fwd_q_item(const T* __restrict__ x, const TreeDi
             wi = take ? wo_ : wi;
         }
         if (live && q == 0) {
-            y[cell * d.P + p] = bad ? nan : r;
+            y[y_at(d, n, c, p)] = bad ? nan : r;
             if (idx) idx[cell * d.P + p] = wi;
         }
     }
@@ -538,7 +545,7 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
                         wi = take ? wo_ : wi;
                     }
                     if (live && q_lane == 0) {
-                        y[cell * d.P + p] = poison ? quiet_nan<T>() : rr;
+                        y[y_at(d, n, c, p)] = poison ? quiet_nan<T>() : rr;
                         if (idx) idx[cell * d.P + p] = poison ? -1 : wi;
                     }
                 }
@@ -684,7 +691,7 @@ __device__ __forceinline__ void nodes_item(const T* __restrict__ grad_y, const T
         const int w0 = live ? win : 0;
         const int wy = int(fast_div(uint32_t(w0), d.div_wo));
         eval_at<T, true>(xn, d, st, sk, wy, w0 - wy * d.wo, e);
-        const T gy = live ? grad_y[cell * d.P + p] : T(0);
+        const T gy = live ? grad_y[y_at(d, n, c, p)] : T(0);
         node_grads<T>(sk, e.g, e.t, gy, gc, mom);
         if (gconv) {  // only the input gradient reads them
 #pragma unroll
@@ -1193,6 +1200,7 @@ int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t
     d.complete = complete ? 1 : 0;
     d.softmax = 0;
     d.regular = 0;
+    d.y_rows = 0;
     d.P = int(P);
     d.div_p = make_fastdiv(uint32_t(std::max<int64_t>(P, 1)));
     d.div_wp = make_fastdiv(uint32_t(std::max<int64_t>(complete ? wo / 2 : wo, 1)));
@@ -1335,13 +1343,16 @@ int tree_conv_forward_impl(int dtype, const void* x, const void* w_prob,
                            const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
                            int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
                            int pad_w, int kernel_h, int kernel_w, int complete, void* y, void* x2,
-                           void* x3, int32_t* indices, int softmax, int regular, void* stream) {
+                           void* x3, int32_t* indices, int softmax, int regular, int y_rows,
+                           void* stream) {
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
+    CL_ARG(!y_rows || complete, "the feature-major output is for the complete block");
     d.softmax = softmax ? 1 : 0;
     d.regular = regular ? 1 : 0;
+    d.y_rows = y_rows ? 1 : 0;
     if (n == 0 || c_out == 0) return CL_OK;
     CL_ARG(x && w_prob && selection && y, "null pointer argument");
     const unsigned gx = unsigned(ceil_div(int64_t(d.n) * d.P, 256));
@@ -1388,7 +1399,7 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
     clear_error();
     return tree_conv_forward_impl(dtype, x, w_prob, selection, n, c_in, h, w, c_out, stride_h,
                                   stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
-                                  indices, 0, 0, stream);
+                                  indices, 0, 0, 0, stream);
 }
 
 extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void* w_logits,
@@ -1397,11 +1408,11 @@ extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void
                                             int stride_w, int pad_h, int pad_w, int kernel_h,
                                             int kernel_w, int complete, void* y, void* x2,
                                             void* x3, int32_t* indices, int regular_taps,
-                                            void* stream) {
+                                            int y_rows, void* stream) {
     clear_error();
     return tree_conv_forward_impl(dtype, x, w_logits, selection, n, c_in, h, w, c_out, stride_h,
                                   stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
-                                  indices, 1, regular_taps, stream);
+                                  indices, 1, regular_taps, y_rows, stream);
 }
 
 extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,
@@ -1425,12 +1436,14 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
                             int64_t h, int64_t w, int64_t c_out, int stride_h, int stride_w,
                             int pad_h, int pad_w, int kernel_h, int kernel_w, int complete,
                             void* grad_x, void* grad_w, void* workspace, int64_t workspace_bytes,
-                            int softmax, void* stream) {
+                            int softmax, int y_rows, void* stream) {
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
+    CL_ARG(!y_rows || complete, "the feature-major gradient is for the complete block");
     d.softmax = softmax ? 1 : 0;
+    d.y_rows = y_rows ? 1 : 0;
     if (!grad_x && !grad_w) return CL_OK;
     const int nodes = complete ? 7 : 4;
     hipStream_t s = as_stream(stream);
@@ -1533,7 +1546,7 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
     return tree_conv_backward_impl(dtype, grad_y, x, w_prob, selection, indices, ent_ptr, ent, n,
                                    c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                                    kernel_w, complete, grad_x, grad_w, workspace,
-                                   workspace_bytes, 0, stream);
+                                   workspace_bytes, 0, 0, stream);
 }
 
 extern "C" int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
@@ -1544,12 +1557,13 @@ extern "C" int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, cons
                                              int stride_w, int pad_h, int pad_w, int kernel_h,
                                              int kernel_w, int complete, void* grad_x,
                                              void* grad_w, void* workspace,
-                                             int64_t workspace_bytes, void* stream) {
+                                             int64_t workspace_bytes, int y_rows,
+                                             void* stream) {
     clear_error();
     return tree_conv_backward_impl(dtype, grad_y, x, w_logits, selection, indices, ent_ptr, ent,
                                    n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
                                    kernel_h, kernel_w, complete, grad_x, grad_w, workspace,
-                                   workspace_bytes, 1, stream);
+                                   workspace_bytes, 1, y_rows, stream);
 }
 
 extern "C" int cl_tree_level_forward(int dtype, const void* x, const void* w_prob, int64_t n,

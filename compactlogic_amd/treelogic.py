@@ -94,25 +94,28 @@ def _check_block(x, w_prob, selection, nodes):
     return c_out
 
 
-def _forward_call(softmax: bool, regular: bool):
-    if regular and not softmax:
-        raise ValueError("the regular-taps guarantee is taken by the logits forward only")
+def _forward_call(softmax: bool, regular: bool, y_rows: bool = False):
+    if (regular or y_rows) and not softmax:
+        raise ValueError("the regular-taps guarantee and the feature-major output are taken by "
+                         "the logits forward only")
     return ("cl_tree_conv_forward_softmax",) if softmax else ("cl_tree_conv_forward",)
 
 
-def _forward_tail(softmax: bool, regular: bool):
-    return (int(regular),) if softmax else ()
+def _forward_tail(softmax: bool, regular: bool, y_rows: bool = False):
+    return (int(regular), int(y_rows)) if softmax else ()
 
 
 def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, intermediate: bool = True, softmax: bool = False,
-                           regular: bool = False):
+                           regular: bool = False, y_rows: bool = False):
     """Complete block forward (replaces convlogic_cuda.full_convlogic_forward,
     full_convlogic_kernel.cu:156-231): (y [N, C, Ho/2, Wo/2], x2 [N, C, Ho, Wo, 4],
     x3 [N, C, Ho, Wo, 2], indices int32 [N, C, Ho/2 * Wo/2]); x2 and x3 are None unless
     `intermediate`.  With `softmax`, w_prob holds the node logits and the kernels take their
     softmax (cl_tree_conv_forward_softmax); `regular` then passes that call the guarantee that
-    every tap lies in the kernel window and reads an input channel."""
+    every tap lies in the kernel window and reads an input channel, and `y_rows` has it write y
+    feature-major: y is then the [N, C, Ho/2, Wo/2] view of a contiguous [C*Ho/2*Wo/2, N]
+    buffer, which flattens to the transpose a following dense layer reads as its rows."""
     c_out = _check_block(x, w_prob, selection, 7)
     n, c_in, h, w = x.shape
     ho, wo = _out_hw(h, w, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
@@ -121,7 +124,11 @@ def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_
     if ho % 2 or wo % 2:
         raise RuntimeError("Output height and width after convolution must be divisible by 2 for "
                            f"2x2 max pooling, but got H_out={ho}, W_out={wo}")
-    y = torch.empty((n, c_out, ho // 2, wo // 2), dtype=x.dtype, device=x.device)
+    if y_rows:
+        y = torch.empty((c_out, ho // 2, wo // 2, n), dtype=x.dtype,
+                        device=x.device).permute(3, 0, 1, 2)
+    else:
+        y = torch.empty((n, c_out, ho // 2, wo // 2), dtype=x.dtype, device=x.device)
     idx = torch.empty((n, c_out, (ho // 2) * (wo // 2)), dtype=torch.int32, device=x.device)
     x2 = x3 = None
     if intermediate:
@@ -129,10 +136,10 @@ def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_
         x3 = torch.empty((n, c_out, ho, wo, 2), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
         timing.timed(f"cl_tree_conv_forward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
-            *_forward_call(softmax, regular), _dl.dtype_code(x), x.data_ptr(), w_prob.data_ptr(),
-            selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
-            kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2), _dl.ptr(x3), idx.data_ptr(),
-            *_forward_tail(softmax, regular), _dl.stream_of(x)))
+            *_forward_call(softmax, regular, y_rows), _dl.dtype_code(x), x.data_ptr(),
+            w_prob.data_ptr(), selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w,
+            pad_h, pad_w, kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2), _dl.ptr(x3),
+            idx.data_ptr(), *_forward_tail(softmax, regular, y_rows), _dl.stream_of(x)))
     return y, x2, x3, idx
 
 
@@ -164,8 +171,13 @@ def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w
     nodes = 7 if complete else 4
     c_out = _check_block(x, w_prob, selection, nodes)
     n, c_in, h, w = x.shape
-    grad_y = grad_y.contiguous()
-    _dl._check(grad_y, "grad_y")
+    # the logits path reads a complete block's grad_y feature-major as it comes from a
+    # flattened dense layer (the transpose of a contiguous [C*Hp*Wp, N]), NCHW otherwise
+    y_rows = (softmax and complete and grad_y.dim() == 4 and not grad_y.is_contiguous()
+              and grad_y.permute(1, 2, 3, 0).is_contiguous())
+    if not y_rows:
+        grad_y = grad_y.contiguous()
+    _dl._check(grad_y.permute(1, 2, 3, 0) if y_rows else grad_y, "grad_y")
     if complete:
         _dl._check_dtype(indices, torch.int32, "indices")
     gx = torch.empty_like(x) if need_x else None
@@ -187,7 +199,7 @@ def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w
             selection.data_ptr(), indices.data_ptr() if complete else None, _dl.ptr(ptr),
             _dl.ptr(ent), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
             kernel_w, int(complete), _dl.ptr(gx), _dl.ptr(gw), ws.data_ptr(), need.value,
-            _dl.stream_of(x)))
+            *((int(y_rows),) if softmax else ()), _dl.stream_of(x)))
     return gx, gw
 
 
@@ -448,6 +460,9 @@ class ConvLogicLayer(nn.Module):
         assert self.weights.shape[-1] == 16, f"Expected 16 logic functions, got {self.weights.shape[-1]}"
         self._uses = None
         self._regular = None
+        # training output feature-major (the view of a [C*Hp*Wp, N] buffer) for a block whose
+        # output is flattened into a dense layer: no transposes either way (complete only)
+        self.rows_output = False
 
     def generate_selection(self, num_chn: int = 2) -> torch.Tensor:
         return generate_selection(self.in_channels, self.out_channels, self.kernel, self.groups,
@@ -510,9 +525,10 @@ class ConvLogicLayer(nn.Module):
                 self.kernel[0], self.kernel[1])
         regular = softmax and self._regular_taps()
         if self.complete:
+            rows = softmax and getattr(self, "rows_output", False)
             return _FullConvLogicWithUses.apply(*args, self.return_intermediate,
                                                 self.return_indices, self._channel_uses(),
-                                                softmax, regular)
+                                                softmax, regular, rows)
         return _ConvLogicWithUses.apply(*args, self._channel_uses(), softmax, regular)
 
     def forward_packed(self, x: PackBitsTensor, in_hw=None) -> PackBitsTensor:
@@ -574,11 +590,12 @@ class _FullConvLogicWithUses(Function):
 
     @staticmethod
     def forward(ctx, x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
-                return_intermediate, return_indices, uses, softmax=False, regular=False):
+                return_intermediate, return_indices, uses, softmax=False, regular=False,
+                y_rows=False):
         y, x2, x3, idx = full_convlogic_forward(x, w, selection, stride_h, stride_w, pad_h,
                                                 pad_w, kernel_h, kernel_w,
                                                 intermediate=return_intermediate,
-                                                softmax=softmax, regular=regular)
+                                                softmax=softmax, regular=regular, y_rows=y_rows)
         ctx.save_for_backward(x, w, selection, idx)
         ctx.geom = (stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
         ctx.uses = uses
@@ -600,7 +617,7 @@ class _FullConvLogicWithUses(Function):
                                     need_x=ctx.needs_input_grad[0],
                                     need_w=ctx.needs_input_grad[1], uses=ctx.uses,
                                     softmax=ctx.softmax)
-        return gx, gw, None, None, None, None, None, None, None, None, None, None, None, None
+        return gx, gw, None, None, None, None, None, None, None, None, None, None, None, None, None
 
 
 class TreeLogicLayer(nn.Module):

@@ -592,13 +592,16 @@ int cl_tree_conv_backward(int dtype, const void* grad_y, const void* x, const vo
  * kernel_h, col < kernel_w) and reads a channel < c_in, as the module's selection sampler
  * draws them: the forward then skips the launch that computes irregular channels, and a
  * channel that breaks the guarantee may get NaN outputs (and winner -1) instead of its values.
+ * y_rows = 1 (complete block only) lays y, and the backward's grad_y, out feature-major:
+ * element (n, c, p) of the pooled output at (c * Hp*Wp + p) * n_samples + n, the [features,
+ * batch] rows a following flattened dense layer reads without a transpose.
  * Other arguments, outputs and errors as cl_tree_conv_forward / cl_tree_conv_backward. */
 int cl_tree_conv_forward_softmax(int dtype, const void* x, const void* w_logits,
                                  const int32_t* selection, int64_t n, int64_t c_in, int64_t h,
                                  int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
                                  int pad_w, int kernel_h, int kernel_w, int complete, void* y,
                                  void* x2, void* x3, int32_t* indices, int regular_taps,
-                                 void* stream);
+                                 int y_rows, void* stream);
 
 int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
                                   const void* w_logits, const int32_t* selection,
@@ -607,7 +610,7 @@ int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
                                   int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
                                   int pad_w, int kernel_h, int kernel_w, int complete,
                                   void* grad_x, void* grad_w, void* workspace,
-                                  int64_t workspace_bytes, void* stream);
+                                  int64_t workspace_bytes, int y_rows, void* stream);
 
 /* One tree level (TreeLogicLayer).  Replaces treelogic_forward (treelogic_kernel.cu:46-86):
  * x [n, channels, positions, 2*out_bits] -> y [n, channels, positions, out_bits], node j of the

@@ -589,3 +589,52 @@ def test_packed_tree_network_counts_match_float_eval():
     counts = model(cl.PackBitsTensor(bits.reshape(n, -1), 64))
     assert counts.dtype == torch.int32 and counts.shape == (n, 5)
     assert torch.equal(counts, torch.round(logits * 3.0).to(torch.int32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_feature_major_output_and_gradient_equal_the_nchw_ones(dtype):
+    """cl_tree_conv_forward_softmax / _backward_softmax with y_rows: y is the [N, C, Hp, Wp] view
+    of a [C*Hp*Wp, N] buffer holding bitwise the NCHW values, and a gradient in that layout
+    gives bitwise the NCHW call's gradients (LDS-staged and global-gather shapes)."""
+    for (n, c_in, h, w, c_out) in [(3, 4, 12, 12, 64), (5, 16, 8, 8, 24)]:
+        stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+        x, _, sel = make(31, n, c_in, h, w, c_out, 3, dtype=dtype)
+        logits = torch.randn((c_out, 7, 16), generator=torch.Generator().manual_seed(32),
+                             dtype=torch.float64).to(x.device, dtype)
+        y0, _, _, i0 = TL.full_convlogic_forward(x, logits, sel, *stride, *pad, *kernel,
+                                                 intermediate=False, softmax=True)
+        y1, _, _, i1 = TL.full_convlogic_forward(x, logits, sel, *stride, *pad, *kernel,
+                                                 intermediate=False, softmax=True, y_rows=True)
+        assert not y1.is_contiguous() and y1.permute(1, 2, 3, 0).is_contiguous()
+        assert torch.equal(y0, y1) and torch.equal(i0, i1)
+        gy = torch.randn(y0.shape, generator=torch.Generator().manual_seed(33),
+                         dtype=torch.float64).to(x.device, dtype)
+        gy_rows = gy.permute(1, 2, 3, 0).contiguous().permute(3, 0, 1, 2)
+        g0 = TL.tree_conv_backward(gy, x, logits, sel, i0, *stride, *pad, *kernel, True,
+                                   softmax=True)
+        g1 = TL.tree_conv_backward(gy_rows, x, logits, sel, i1, *stride, *pad, *kernel, True,
+                                   softmax=True)
+        assert torch.equal(g0[0], g1[0]) and torch.equal(g0[1], g1[1])
+
+
+def test_tree_network_with_feature_major_block_output_trains_identically():
+    """The cfg3_tree-shaped network (blocks, Flatten, dense layers, GroupSum) with its last
+    block's output feature-major gives bitwise the loss and gradients of the NCHW network: the
+    flattened output reaches the dense layer as its rows, and the dense layer's input gradient
+    reaches the block without a transpose."""
+    from compactlogic_amd import configs
+    cfg = configs.TreeConfig("small_tree", (3, 16, 16), [(32, 3, 2, 1), (48, 3, 2, 1)],
+                             [400, 400], 64)
+    net = configs.tree_network(cfg, device="cuda")
+    assert net[1].rows_output
+    x, labels = configs.conv_inputs(cfg, device="cuda")
+    losses, grads = [], []
+    for rows in (True, False):
+        net[1].rows_output = rows
+        net.zero_grad(set_to_none=True)
+        loss = net[-1].cross_entropy(net[:-1](x), labels)
+        loss.backward()
+        losses.append(loss.detach())
+        grads.append([p.grad.clone() for p in net.parameters()])
+    assert torch.equal(losses[0], losses[1])
+    assert all(torch.equal(a, b) for a, b in zip(*grads))
