@@ -229,8 +229,10 @@ __global__ __launch_bounds__(256) void k_gsum_bwd(Src src, int64_t B, int64_t F,
 }
 
 // ---- backward, batch-contiguous grad_x ([F, batch] in memory): block = (batch tile, class
-// c, slice of the group's rows).  Each lane computes its g[n, c] / tau once and streams it
-// down the rows of its slice with non-temporal stores.
+// c, slice of the group's rows).  Each lane computes its g[n, c] / tau once and writes it
+// down the rows of its slice.  The stores are ordinary write-back ones: the next kernel (the
+// last layer's backward) reads these rows at once and finds them in the Infinity Cache;
+// non-temporal stores measured 5 us slower per cfg2 step.
 template <typename T, int VEC, typename Src>
 __global__ __launch_bounds__(256) void k_gsum_bwd_rows(Src src, int64_t B, int64_t F, int64_t sf,
                                                        int64_t gsz, int64_t slice,
@@ -243,20 +245,7 @@ __global__ __launch_bounds__(256) void k_gsum_bwd_rows(Src src, int64_t B, int64
     Vec<T, VEC> v;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) v.v[i] = src(n0 + i, c);
-    for (int64_t j = j0 + (threadIdx.x >> 6); j < j1; j += 4) {
-        T* dst = gx + j * sf + n0;
-        if constexpr (VEC == 4 && sizeof(T) == 4) {
-            typedef float F4 __attribute__((ext_vector_type(4)));
-            F4 t = {v.v[0], v.v[1], v.v[2], v.v[3]};
-            __builtin_nontemporal_store(t, reinterpret_cast<F4*>(dst));
-        } else if constexpr (VEC == 2 && sizeof(T) == 8) {
-            typedef double D2 __attribute__((ext_vector_type(2)));
-            D2 t = {v.v[0], v.v[1]};
-            __builtin_nontemporal_store(t, reinterpret_cast<D2*>(dst));
-        } else {
-            vstore<T, VEC>(dst, v);
-        }
-    }
+    for (int64_t j = j0 + (threadIdx.x >> 6); j < j1; j += 4) vstore<T, VEC>(gx + j * sf + n0, v);
 }
 
 template <typename T, typename Src>
