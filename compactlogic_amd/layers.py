@@ -367,6 +367,16 @@ class LogicLayer(torch.nn.Module):
         self.num_weights = out_dim
         self.is_frozen = False
 
+    # caches keyed by weak references, which do not pickle; they rebuild on the next call
+    _weak_caches = ("_argmax_cache", "_plan_key", "_plan", "_packed_key", "_packed_tables")
+
+    def __getstate__(self):
+        state = super().__getstate__()
+        for name in self._weak_caches:
+            if name in state:
+                state[name] = None
+        return state
+
     # -- forward ------------------------------------------------------------------------------------------------------
 
     def forward(self, x):
@@ -832,6 +842,8 @@ class ConvLayer(LogicLayer):
         self._packed_key = None
         self._packed_tables = None
         self._packed_order = None
+
+    _weak_caches = LogicLayer._weak_caches + ("_packed_order",)
 
     def forward_cuda(self, x):
         """x [N, c_in, h, w] -> [N, c_out, h_out, w_out] (:598-626)."""

@@ -464,6 +464,13 @@ class ConvLogicLayer(nn.Module):
         # output is flattened into a dense layer: no transposes either way (complete only)
         self.rows_output = False
 
+    def __getstate__(self):
+        # the caches hold weak references, which do not pickle; they rebuild on the next call
+        state = super().__getstate__()
+        state["_uses"] = None
+        state["_regular"] = None
+        return state
+
     def generate_selection(self, num_chn: int = 2) -> torch.Tensor:
         return generate_selection(self.in_channels, self.out_channels, self.kernel, self.groups,
                                   num_chn, self.input_bits, self.weights.device)

@@ -573,3 +573,29 @@ def test_dense_packed_tables_and_order():
     wide = cl.LogicLayer(50, 400, connections="original")   # 16 reads per input row
     wide.freeze()
     assert wide.packed_tables(wide.w)[3] is None
+
+
+def test_layers_with_warm_caches_pickle_and_rebuild():
+    """torch.save of a whole module pickles it: the weak-reference caches are left out and
+    rebuilt on the next call, and the loaded layer's plans equal the original's."""
+    import io
+    torch.manual_seed(5)
+    dense = cl.LogicLayer(12, 20, num_gates=16)
+    plan = dense.run_plan()
+    dense._argmax_slots()
+    conv = cl.ConvLayer((3, 7, 9), padding=1, c_out=5, ks=3, stride=2, num_chn=0, num_gates=4)
+    conv.freeze()
+    ia, ib, g = conv.packed_tables(conv.w)
+    buf = io.BytesIO()
+    torch.save(torch.nn.Sequential(dense, conv), buf)
+    buf.seek(0)
+    loaded = torch.load(buf, weights_only=False)  # written by this test
+    d2, c2 = loaded[0], loaded[1]
+    assert d2._plan is None and d2._plan_key is None and c2._packed_key is None
+    p2 = d2.run_plan()
+    assert p2.num_runs == plan.num_runs
+    assert torch.equal(d2._argmax_slots(), dense._argmax_slots())
+    for a, b in zip(c2.packed_tables(c2.w), (ia, ib, g)):
+        assert torch.equal(a, b)
+    # the original keeps its caches
+    assert dense.run_plan() is plan and conv.packed_tables(conv.w)[0] is ia

@@ -492,6 +492,28 @@ def test_module_regular_taps_cache_follows_the_selection():
     np.testing.assert_allclose(np_(y), ref, rtol=1e-5, atol=1e-6)
 
 
+def test_module_with_warm_caches_pickles():
+    """torch.save of a whole trained layer: the channel-use and regular-taps caches (weak
+    references) are left out and rebuilt, and the loaded layer computes the same output."""
+    import io
+    torch.manual_seed(6)
+    layer = cl.ConvLogicLayer(4, 8, stride=2, padding=1, kernel=3, complete=True).cuda()
+    x = torch.rand(2, 4, 12, 12, device="cuda", requires_grad=True)
+    layer(x).sum().backward()
+    assert layer._uses is not None and layer._regular is not None
+    buf = io.BytesIO()
+    torch.save(layer, buf)
+    buf.seek(0)
+    other = torch.load(buf, weights_only=False)  # written by this test
+    assert other._uses is None and other._regular is None
+    with torch.no_grad():
+        assert torch.equal(other(x), layer(x))
+    other.eval()
+    layer.eval()
+    with torch.no_grad():
+        assert torch.equal(other(x), layer(x))
+
+
 def test_identity_init():
     layer = cl.ConvLogicLayer(2, 2, residual_init=True, complete=True).cuda().eval()
     assert bool((layer.weights.argmax(-1) == 3).all())
