@@ -92,16 +92,51 @@ def filtered_model_state_dict(model: torch.nn.Module) -> dict:
     return {k: v for k, v in model.state_dict().items() if not k.endswith(".w")}
 
 
-def save_checkpoint(path, step, model, optimizer=None, freezer_info=None) -> None:
-    """A checkpoint in the reference's layout (experiments/experiment_script.py:527-541)."""
+def save_checkpoint(path, step, model, optimizer, freezer_info=None) -> None:
+    """A checkpoint in the reference's layout (experiments/experiment_script.py:527-541): the
+    optimizer is required, as there, since the reference's loader restores it; the host RNG
+    and, with a GPU, every device's RNG state are saved."""
+    if optimizer is None or not hasattr(optimizer, "state_dict"):
+        raise TypeError("save_checkpoint needs the optimizer (its state is part of the layout)")
     os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
     torch.save({
         "step": step,
         "model_state": {k: v.detach().cpu() for k, v in filtered_model_state_dict(model).items()},
-        "optim_state": optimizer.state_dict() if optimizer is not None else {},
-        "rng_state": {"torch": torch.get_rng_state(), "cuda": None},
+        "optim_state": optimizer.state_dict(),
+        "rng_state": {
+            "torch": torch.get_rng_state(),
+            "cuda": torch.cuda.get_rng_state_all() if torch.cuda.is_available() else None,
+        },
         "freezer_info": freezer_info if freezer_info is not None else "",
     }, path)
+
+
+def resume_checkpoint(path, model, optimizer, map_location="cpu", strict=False):
+    """Restore a training run from a checkpoint, as the reference's training loader does
+    (experiments/experiment_script.py:543-569): the model state (non-strict: frozen layers'
+    ``.w`` buffers are not saved), layers that hold a ``w`` buffer marked frozen, the
+    optimizer state moved to the parameters' device, and the RNG states.  Loads with
+    ``weights_only=True``.  Returns (step, freezer_info)."""
+    ckpt = torch.load(path, map_location=map_location, weights_only=True)
+    model.load_state_dict(ckpt["model_state"], strict=strict)
+    for layer in model:
+        if getattr(layer, "w", None) is not None:
+            layer.is_frozen = True
+    optimizer.load_state_dict(ckpt["optim_state"])
+    params = list(model.parameters())
+    if params:
+        device = params[0].device
+        for state in optimizer.state.values():
+            for key, v in state.items():
+                if torch.is_tensor(v) and key != "step":
+                    state[key] = v.to(device)
+    rng = ckpt.get("rng_state")
+    if rng is not None:
+        if rng.get("torch") is not None:
+            torch.set_rng_state(rng["torch"])
+        if torch.cuda.is_available() and rng.get("cuda") is not None:
+            torch.cuda.set_rng_state_all(rng["cuda"])
+    return ckpt.get("step"), ckpt.get("freezer_info")
 
 
 def save_meta_data(directory, args: dict) -> None:

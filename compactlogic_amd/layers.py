@@ -428,15 +428,21 @@ class LogicLayer(torch.nn.Module):
 
     @torch.no_grad()
     def _argmax_slots(self) -> torch.Tensor:
-        """Winner slots of an unfrozen layer (argmax of the logits, uint8), kept while the
-        logits tensor is alive and unmodified, so the packed tables derived from them stay
-        cached across eval calls."""
+        """Winner slots of an unfrozen layer (argmax of the logits, uint8), recomputed on every
+        call: the logits change without a version bump when an optimizer writes them through
+        raw pointers (FusedAdam) or a captured training step is replayed.  When the winners
+        equal the previous call's, that tensor object is returned, so the packed tables keyed
+        on it stay cached across eval calls (one device comparison, which synchronises; under
+        graph capture the fresh winners are returned as they are)."""
         src = self.weights
-        hit = getattr(self, "_argmax_cache", None)
-        if hit is not None and hit[0]() is src and hit[1] == src._version:
-            return hit[2]
         w = src.argmax(-1).to(dtype=torch.uint8, device=src.device)
-        self._argmax_cache = (weakref.ref(src), src._version, w)
+        if src.device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            return w
+        prev = getattr(self, "_argmax_cache", None)
+        if prev is not None and prev.shape == w.shape and prev.device == w.device \
+                and torch.equal(prev, w):
+            return prev
+        self._argmax_cache = w
         return w
 
     @torch.no_grad()

@@ -14,7 +14,10 @@ update is bitwise reproducible.
 
 Differences from torch.optim.Adam: every parameter of the optimizer shares one step count,
 which advances on every call (torch advances a parameter's count only when it has a
-gradient); weight decay, amsgrad and maximize are not supported.
+gradient); weight decay, amsgrad and maximize are not supported.  State dicts interchange
+with torch.optim.Adam's: ``state_dict()`` gives each parameter its step as a float32 host
+scalar, as Adam keeps it, and after ``load_state_dict`` the shared count resumes from the
+loaded steps (which must agree), so the bias corrections continue where they stopped.
 """
 from __future__ import annotations
 
@@ -42,6 +45,38 @@ class FusedAdam(torch.optim.Optimizer):
         self.max_norm = max_norm
         self._step_t = None     # shared device step count
         self._workspace = None
+
+    def _loaded_step(self) -> float:
+        """The step count held in the state (after load_state_dict, a torch.optim.Adam or a
+        FusedAdam state dict): equal for every parameter that has one, else an error; 0 when
+        no parameter has one yet."""
+        steps = set()
+        for p, _ in self._params():
+            st = self.state.get(p, {})
+            if "step" in st:
+                v = st["step"]
+                steps.add(float(v.item() if torch.is_tensor(v) else v))
+        if len(steps) > 1:
+            raise RuntimeError(f"FusedAdam shares one step count, but the loaded state holds "
+                               f"several: {sorted(steps)}")
+        return steps.pop() if steps else 0.0
+
+    def load_state_dict(self, state_dict):
+        super().load_state_dict(state_dict)
+        # the shared count is taken from the loaded per-parameter steps at the next step()
+        self._step_t = None
+
+    def state_dict(self):
+        """torch.optim.Adam's layout: per-parameter step as a float32 host scalar."""
+        sd = super().state_dict()
+        state = {}
+        for k, st in sd["state"].items():
+            st = dict(st)
+            if "step" in st and torch.is_tensor(st["step"]):
+                st["step"] = torch.tensor(float(st["step"].item()), dtype=torch.float32)
+            state[k] = st
+        sd["state"] = state
+        return sd
 
     def _params(self):
         out = []
@@ -77,12 +112,20 @@ class FusedAdam(torch.optim.Optimizer):
                                "use one optimizer per parameter group setting")
         lr, (beta1, beta2), eps = next(iter(hp))
         if self._step_t is None or self._step_t.device != dev or self._step_t.dtype != dtype:
-            self._step_t = torch.zeros((), dtype=dtype, device=dev)
+            start = self._loaded_step() if self._step_t is None else float(self._step_t)
+            self._step_t = torch.full((), start, dtype=dtype, device=dev)
         for p, _ in items:
             st = self.state[p]
             if "exp_avg" not in st:
                 st["exp_avg"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
                 st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+            for key in ("exp_avg", "exp_avg_sq"):   # loaded moments: the kernel's layout
+                t = st[key]
+                if t.shape != p.shape:
+                    raise RuntimeError(f"FusedAdam state {key} has shape {tuple(t.shape)}, "
+                                       f"the parameter {tuple(p.shape)}")
+                if not t.is_contiguous() or t.device != dev or t.dtype != dtype:
+                    st[key] = t.to(device=dev, dtype=dtype).contiguous()
             st["step"] = self._step_t
         max_t = ctypes.c_int64()
         _capi.call("cl_adam_clip_max_tensors", ctypes.byref(max_t))

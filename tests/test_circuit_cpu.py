@@ -191,6 +191,19 @@ def test_checkpoint_round_trip_in_the_reference_format(tmp_path, struct):
     got = loaded.state_dict()
     for k, v in ref.items():
         assert torch.equal(got[k], v), k
+    assert set(raw["rng_state"]) == {"torch", "cuda"}
+    # the reference's training loader sequence (experiments/experiment_script.py:543-569)
+    # restores model, frozen flags, optimizer state and RNG from it
+    fresh = ck.build_model(args)
+    [m for m in fresh if isinstance(m, LogicLayer)][0].freeze()   # as the freezer left it
+    fopt = torch.optim.Adam([p for p in fresh.parameters() if p.requires_grad], lr=0.01)
+    torch.manual_seed(12345)
+    step, info = ck.resume_checkpoint(path, fresh, fopt)
+    assert step == 100 and info == {"frozen": 1}
+    assert torch.equal(torch.get_rng_state(), raw["rng_state"]["torch"])
+    assert [getattr(m, "is_frozen", False) for m in fresh] == \
+        [getattr(m, "w", None) is not None for m in fresh]
+    assert fopt.state_dict()["param_groups"] == opt.state_dict()["param_groups"]
     # the loaded network's circuit is the saved network's (argmax of the saved logits)
     model.eval()
     a, b = C.extract_circuit(model), C.extract_circuit(loaded)

@@ -75,7 +75,7 @@ def test_checkpoint_to_pruned_packed_evaluator(device, tmp_path):
     torch.manual_seed(11)
     trained = ck.build_model(args)
     path = tmp_path / "exp" / "ckpt_best_7.pt"
-    ck.save_checkpoint(path, 7, trained)
+    ck.save_checkpoint(path, 7, trained, torch.optim.Adam(trained.parameters(), lr=0.01))
     ck.save_meta_data(path.parent, args)
     model, _, step = ck.load_checkpoint(path, device=device)
     assert step == 7

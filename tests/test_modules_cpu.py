@@ -258,6 +258,45 @@ def test_conv_eval_winners_follow_weight_updates():
         layer.weights[:, 2] = 1.0
     w1 = layer._argmax_slots()
     assert w1 is not w0 and torch.equal(w1, torch.full((4,), 2, dtype=torch.uint8))
+    # a write that leaves the version unchanged (an optimizer's raw-pointer update, a graph
+    # replay) must change the winners as well: they are recomputed on every call
+    v = layer.weights._version
+    layer.weights.data[:, 3] = 5.0                   # .data writes do not bump the version
+    assert layer.weights._version == v
+    w2 = layer._argmax_slots()
+    assert torch.equal(w2, torch.full((4,), 3, dtype=torch.uint8))
+    assert layer._argmax_slots() is w2               # unchanged winners: the same tensor
+
+
+def test_fused_adam_state_dict_interchanges_with_torch_adam():
+    """FusedAdam resumes its shared step count from a loaded torch.optim.Adam state dict and
+    writes Adam's layout (float32 host step per parameter); disagreeing steps are refused."""
+    torch.manual_seed(2)
+    params = [torch.randn(5, 4, requires_grad=True), torch.randn(3, requires_grad=True)]
+    adam = torch.optim.Adam(params, lr=0.01)
+    for _ in range(3):
+        for p in params:
+            p.grad = torch.randn_like(p)
+        adam.step()
+    fused = cl.FusedAdam([p.detach().clone().requires_grad_(True) for p in params], lr=0.01)
+    assert fused._loaded_step() == 0.0
+    fused.load_state_dict(adam.state_dict())
+    assert fused._step_t is None and fused._loaded_step() == 3.0
+    sd = fused.state_dict()
+    assert all(v["step"].dtype == torch.float32 and v["step"].device.type == "cpu"
+               and float(v["step"]) == 3.0 for v in sd["state"].values())
+    bad = adam.state_dict()
+    bad["state"][1]["step"] = torch.tensor(7.0)
+    fused.load_state_dict(bad)
+    with pytest.raises(RuntimeError, match="several"):
+        fused._loaded_step()
+
+
+def test_checkpoint_needs_the_optimizer(tmp_path):
+    from compactlogic_amd import checkpoint as ck
+    model = torch.nn.Sequential(torch.nn.Flatten(), cl.LogicLayer(16, 20))
+    with pytest.raises(TypeError):
+        ck.save_checkpoint(tmp_path / "c.pt", 1, model, None)
 
 
 def test_conv_layer_rewiring_keeps_ranges():

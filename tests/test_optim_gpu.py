@@ -116,3 +116,72 @@ def test_whole_training_step_in_a_graph_replays_like_eager(device):
         for pe, pg in zip(eager.parameters(), graphed.parameters()):
             assert torch.equal(pe, pg)
         assert float(opt_g.state[next(iter(graphed.parameters()))]["step"]) == 3 + k
+
+
+def test_eval_after_fused_adam_uses_the_updated_winners(device):
+    """FusedAdam writes the logits through raw pointers (no version bump): an eval after a
+    training step must evaluate the winners of the updated logits, not the first eval's."""
+    model = make_model(device, seed=4)
+    x, y = batch(device, seed=4)
+    opt = cl.FusedAdam(model.parameters(), lr=0.5, max_norm=None)
+    model.eval()
+    with torch.no_grad():
+        model[:-1](x)                                     # the first eval caches its winners
+    model.train()
+    changed = False
+    for _ in range(4):
+        before = [m.weights.argmax(-1).clone() for m in model[:-1]]
+        model.zero_grad(set_to_none=True)
+        loss_of(model, x, y).backward()
+        opt.step()
+        changed |= any(not torch.equal(b, m.weights.argmax(-1)) for b, m in zip(before, model[:-1]))
+    assert changed, "the steps moved no winner; the check would be vacuous"
+    model.eval()
+    for m in model[:-1]:
+        assert torch.equal(m._argmax_slots().long(), m.weights.argmax(-1))
+    with torch.no_grad():
+        got = model[:-1](x)
+        h = x
+        for m in model[:-1]:
+            w = m.weights.argmax(-1).to(torch.uint8)
+            h = cl.difflogic_hip.eval(h.t().contiguous(), m.indices[0], m.indices[1], w,
+                                      m.gate_sequence).t()
+    assert torch.equal(got, h)
+
+
+def test_fused_adam_resumes_from_a_checkpoint(device, tmp_path):
+    """Two steps, save, two more; against: two steps, save, resume into a fresh model and a
+    fresh FusedAdam (the reference's loader sequence), two more.  Bitwise equal, including the
+    bias corrections (the restored step count)."""
+    from compactlogic_amd import checkpoint as ck
+    x, y = batch(device, seed=6)
+
+    def run(resume_at=None):
+        model = make_model(device, seed=6)
+        opt = cl.FusedAdam(model.parameters(), lr=0.01, max_norm=10.0)
+        for i in range(4):
+            if i == resume_at:
+                path = tmp_path / f"ckpt_{resume_at}.pt"
+                ck.save_checkpoint(path, i, model, opt)
+                model = make_model(device, seed=99)       # different initial weights
+                opt = cl.FusedAdam(model.parameters(), lr=0.01, max_norm=10.0)
+                step, _ = ck.resume_checkpoint(path, model, opt)
+                assert step == i
+            model.zero_grad(set_to_none=True)
+            loss_of(model, x, y).backward()
+            opt.step()
+        torch.cuda.synchronize()
+        return [p.detach().clone() for p in model.parameters()], opt
+
+    ref, ropt = run()
+    got, gopt = run(resume_at=2)
+    assert all(torch.equal(a, b) for a, b in zip(ref, got))
+    assert float(gopt._step_t) == 4.0
+    # the saved optimizer state is torch.optim.Adam's layout: it loads into Adam as well
+    sd = gopt.state_dict()
+    assert all(v["step"].device.type == "cpu" and v["step"].dtype == torch.float32
+               for v in sd["state"].values())
+    params = [p.detach().clone().requires_grad_(True) for p in ref]
+    adam = torch.optim.Adam(params, lr=0.01)
+    adam.load_state_dict(sd)
+    assert all(float(adam.state[p]["step"]) == 4.0 for p in params)
