@@ -292,8 +292,206 @@ __global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
     }
 }
 
-// One wave per channel: moments summed over the chunks in order (lane j: moment j), then
-// slot g (lane g) takes c0 S0 + c1 S_a + c2 S_b + c3 S_ab; with probs the softmax backward.
+// ------------------------------------------------------------------------------------------
+// Moments of input channels read by many output channels (cfg3's first layer: about 28 per
+// input channel), as a register-tiled product on the VALU.  For input channel ch the moments
+// of its output channels c are M[c][m] = sum_e gy_c(e) f_m(e) over the elements e = (sample,
+// position), with the 64 features f_m(e) = [1, v_k, v_k v_l (k <= l), 0 ...] of e's window in
+// the coefficient-block order (padded with zeros past NM).  One wave per (ch, tile of 32 of its
+// channels, element chunk q): the elements are taken 32 at a time; the wave stages the 32 x 32
+// grad_y values and the 32 x 64 features in LDS, then lane (cq, fg) adds gy * f for channels
+// 4 cq .. 4 cq + 3 and features 8 fg .. 8 fg + 7 of every staged element, in element order.
+// The window is loaded once per element for all the tile's channels (the per-channel-pair
+// kernel above loads it once per pair).  Feature group fg sits at LDS offsets off0(fg) and
+// off0(fg) ^ 4 (floats) of an element's row, so the eight groups' 16-byte reads of a half
+// fall on distinct banks.
+constexpr int kMmTile = 32;     // output channels per wave
+constexpr int kMmSlab = 32;     // elements staged at a time
+constexpr int kMmFeat = 64;     // features per element (>= NM, padded)
+#ifndef CL_WIN_MM_NWAVES
+#define CL_WIN_MM_NWAVES 4
+#endif
+constexpr int kMmWaves = CL_WIN_MM_NWAVES;  // waves per workgroup, each taking every kMmWaves-th slab
+
+// LDS position of feature m in an element's row: group fg = m / 8 owns floats 8 fg .. 8 fg + 7;
+// its first half (features 8 fg .. + 3) sits in the upper four of them when fg >= 4.
+__host__ __device__ constexpr int mm_first(int fg) { return 8 * fg + 4 * (fg >> 2); }
+__host__ __device__ constexpr int mm_second(int fg) { return 8 * fg + 4 * (1 - (fg >> 2)); }
+__host__ __device__ constexpr int mm_pos(int m) {
+    return ((m & 7) < 4 ? mm_first(m >> 3) : mm_second(m >> 3)) + (m & 3);
+}
+
+// (k, l) of the quadratic moments in coefficient-block order (row-major upper triangle)
+template <int P>
+struct BetaPairs {
+    int k[P * (P + 1) / 2], l[P * (P + 1) / 2];
+    constexpr BetaPairs() : k(), l() {
+        int r = 0;
+        for (int a = 0; a < P; ++a)
+            for (int b = a; b < P; ++b) {
+                k[r] = a;
+                l[r] = b;
+                ++r;
+            }
+    }
+};
+
+template <typename T, int KW>
+__global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mm(
+    const T* __restrict__ x, const T* __restrict__ gy, const int32_t* __restrict__ grp_ptr,
+    const int32_t* __restrict__ chan_order, T* __restrict__ part, int ntile, int nq,
+    WinDims d) {
+    constexpr int P = Win<KW>::P, NM = 1 + P + Win<KW>::NP, CW = Win<KW>::CW;
+    static_assert(NM <= kMmFeat, "too many features");
+    typedef T V4 __attribute__((ext_vector_type(4)));
+    // per wave: rows padded by 4 floats, so the staging writes of 32 elements spread over
+    // 8 banks; the closing reduction reuses the feature buffers
+    // (declared as 16-byte vectors, so the compiler knows the reads below are aligned)
+    constexpr int GW = (kMmTile + 4) / 4, FW = (kMmFeat + 4) / 4;
+    __shared__ V4 gs4[kMmWaves][kMmSlab][GW];    // [element][channel / 4]
+    __shared__ V4 fs4[kMmWaves][kMmSlab][FW];    // [element][feature position / 4]
+    static_assert(kMmWaves == 1 || sizeof(fs4) >= (kMmWaves - 1) * 64 * 32 * sizeof(T),
+                  "reduction space");
+    T* const gsw = reinterpret_cast<T*>(&gs4[0][0][0]);
+    T* const fsw = reinterpret_cast<T*>(&fs4[0][0][0]);
+    const int wv = wave_id(), lane = threadIdx.x & 63;
+    const int q = blockIdx.y;
+    const int ch = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+    const int g0 = grp_ptr[ch] + tile * kMmTile, g1 = std::min(grp_ptr[ch + 1], g0 + kMmTile);
+    if (g0 >= g1) return;  // uniform per workgroup
+    const int hw = d.Ho * d.Wo, HW = d.H * d.W;
+    const int E = int(d.N) * hw;  // < 2^31 (checked by the host)
+    const int e0 = int(int64_t(q) * E / nq), e1 = int(int64_t(q + 1) * E / nq);
+    const int nslab = (e1 - e0 + kMmSlab - 1) / kMmSlab;
+    const int rounds = (nslab + kMmWaves - 1) / kMmWaves;  // equal for every wave
+    // staging roles: element se = lane % 32; grad_y channels (lane / 32) * 16 .. + 15 of the
+    // tile (clamped to a valid channel, masked after the load); features: lanes < 32 write
+    // feature positions of features 0 .. 31, the others of 32 .. 63
+    const int se = lane % kMmSlab, half = lane / kMmSlab;
+    int coff[kMmTile / 2];
+    bool cok[kMmTile / 2];
+#pragma unroll
+    for (int j = 0; j < kMmTile / 2; ++j) {
+        const int gi = g0 + half * (kMmTile / 2) + j;
+        cok[j] = gi < g1;
+        coff[j] = chan_order[cok[j] ? gi : g0] * hw;
+    }
+    const int cq = lane / 8, fg = lane % 8;
+    const int o0 = mm_first(fg) / 4, o1 = mm_second(fg) / 4;   // in 16-byte vectors
+    T acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = T(0);
+    constexpr BetaPairs<P> bp{};
+    // The global loads of a slab (its window values and grad_y) are issued one slab ahead,
+    // before the wave computes on the previous one, so the wave itself hides their latency.
+    // Every load is unconditional (clamped address, value masked when used).
+    auto issue = [&](int r, T (&vr)[P], T (&gr)[kMmTile / 2], bool& live, bool (&tin)[P]) {
+        const int e = e0 + (r * kMmWaves + wv) * kMmSlab + se;
+        live = r < rounds && e < e1;
+        const int ec = live ? e : e0;
+        const int n = ec / hw, pos = ec - n * hw;
+        const int oy = pos / d.Wo, ox = pos - oy * d.Wo;
+        const int by = oy * d.stride + d.oy0, bx = ox * d.stride + d.ox0;
+        const T* plane = x + (int64_t(n) * d.Cin + ch) * HW;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const int yy = by + k / KW, xx = bx + k % KW;
+            tin[k] = live && unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W);
+            vr[k] = plane[tin[k] ? yy * d.W + xx : 0];
+        }
+        const T* gyn = gy + int64_t(n) * d.Cout * hw + pos;
+#pragma unroll
+        for (int j = 0; j < kMmTile / 2; ++j) gr[j] = gyn[coff[j]];
+    };
+    T vn[P], gn[kMmTile / 2];
+    bool liven, tinn[P];
+    issue(0, vn, gn, liven, tinn);
+    for (int r = 0; r < rounds; ++r) {
+        T v[P], gv[kMmTile / 2];
+#pragma unroll
+        for (int k = 0; k < P; ++k) v[k] = tinn[k] ? vn[k] : T(0);
+#pragma unroll
+        for (int j = 0; j < kMmTile / 2; ++j) gv[j] = (liven && cok[j]) ? gn[j] : T(0);
+        // features of the element: f_0 = 1, f_{1+k} = v_k, f_{beta(k,l)} = v_k v_l, zeros
+        // past NM (a masked element has v = 0 and gy = 0)
+        T f[kMmFeat / 2];
+#pragma unroll
+        for (int i = 0; i < kMmFeat / 2; ++i) {
+            T lo = T(0), hi = T(0);  // features i and kMmFeat / 2 + i
+            const int m0 = i, m1 = kMmFeat / 2 + i;
+            if (m0 == 0) lo = T(1);
+            else if (m0 <= P) lo = v[m0 - 1];
+            else if (m0 < NM) lo = v[bp.k[m0 - 1 - P]] * v[bp.l[m0 - 1 - P]];
+            if (m1 <= P) hi = v[m1 - 1];
+            else if (m1 < NM) hi = v[bp.k[m1 - 1 - P]] * v[bp.l[m1 - 1 - P]];
+            f[i] = half == 0 ? lo : hi;
+        }
+        // this wave's buffers only: a wave-level barrier orders its reads of the previous
+        // slab before the writes, and the writes before the reads below
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        T* const frow = fsw + (wv * kMmSlab + se) * (FW * 4);
+        T* const grow = gsw + (wv * kMmSlab + se) * (GW * 4);
+#pragma unroll
+        for (int m = 0; m < kMmFeat / 2; ++m) frow[mm_pos(half * (kMmFeat / 2) + m)] = f[m];
+#pragma unroll
+        for (int j = 0; j < kMmTile / 2; ++j) grow[half * (kMmTile / 2) + j] = gv[j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        issue(r + 1, vn, gn, liven, tinn);   // the next slab's loads, in flight meanwhile
+#pragma unroll 4
+        for (int k = 0; k < kMmSlab; ++k) {
+            const V4 gq = gs4[wv][k][cq];
+            const V4 fa = fs4[wv][k][o0];
+            const V4 fb = fs4[wv][k][o1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = fma(gq[i], fa[j], acc[i][j]);
+                    acc[i][4 + j] = fma(gq[i], fb[j], acc[i][4 + j]);
+                }
+            }
+        }
+    }
+    // the waves' sums added in wave order by wave 0
+    if constexpr (kMmWaves > 1) __syncthreads();
+    T* red = fsw;
+    if (kMmWaves > 1 && wv > 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) red[((wv - 1) * 32 + i * 8 + j) * 64 + lane] = acc[i][j];
+    }
+    if constexpr (kMmWaves > 1) __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int w = 1; w < kMmWaves; ++w)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] += red[((w - 1) * 32 + i * 8 + j) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int gi = g0 + cq * 4 + i;
+        if (gi >= g1) continue;
+        const int c = chan_order[gi];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int m = fg * 8 + j;
+            if (m < CW) part[(int64_t(q) * d.Cout + c) * CW + m] = acc[i][j];
+        }
+    }
+}
+
+// One workgroup of four waves per channel: wave w sums the moments of chunks w, w + 4, ...
+// (lane j: moment j, eight chunks' loads in flight at a time, additions in chunk order), the
+// four partial sums are added in wave order, then slot g (lane g of the first wave) takes
+// c0 S0 + c1 S_a + c2 S_b + c3 S_ab; with probs the softmax backward.
 template <typename T, int KW>
 __global__ __launch_bounds__(256) void k_win_finalize(const T* __restrict__ part, int nq,
                                                       const uint8_t* __restrict__ gs,
@@ -302,12 +500,25 @@ __global__ __launch_bounds__(256) void k_win_finalize(const T* __restrict__ part
                                                       T* __restrict__ grad_w, int64_t Cout,
                                                       int G) {
     constexpr int P = Win<KW>::P, CW = Win<KW>::CW;
-    const int64_t c = int64_t(blockIdx.x) * 4 + wave_id();
-    if (c >= Cout) return;  // uniform per wave
-    const int l = lane_id();
+    __shared__ T sums[4][64];
+    const int64_t c = blockIdx.x;
+    const int w = wave_id(), l = lane_id();
     T s = 0;
-    if (l < CW)
-        for (int q = 0; q < nq; ++q) s += part[(int64_t(q) * Cout + c) * CW + l];
+    if (l < CW) {
+        int q = w;
+        for (; q + 7 * 4 < nq; q += 8 * 4) {
+            T t[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t[i] = part[(int64_t(q + 4 * i) * Cout + c) * CW + l];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s += t[i];
+        }
+        for (; q < nq; q += 4) s += part[(int64_t(q) * Cout + c) * CW + l];
+    }
+    sums[w][l] = s;
+    __syncthreads();
+    if (w != 0) return;
+    s = ((sums[0][l] + sums[1][l]) + sums[2][l]) + sums[3][l];
     T gw = 0;
     int ia = 0, ib = 0, iab = 0;
     Coef4<T> cf = gate_coef<T>(0);
@@ -465,10 +676,35 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
 #define CL_WIN_MIN_ITERS 8
 #endif
 
+// Input channels read by at least this many output channels take the tiled moments kernel.
+#ifndef CL_WIN_MM_MIN_GROUP
+#define CL_WIN_MM_MIN_GROUP 8
+#endif
+#ifndef CL_WIN_MM_BLOCKS
+#define CL_WIN_MM_BLOCKS 768  // workgroups of the tiled moments kernel (three per CU)
+#endif
+
+namespace {
+bool use_mm(int64_t max_group) { return max_group >= CL_WIN_MM_MIN_GROUP; }
+
+// element chunks of the tiled moments kernel: about CL_WIN_MM_BLOCKS workgroups, at least
+// two staged slabs of elements per wave
+int64_t mm_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t hw) {
+    const int64_t ntile = ceil_div(max_group, kMmTile);
+    const int64_t want = ceil_div(CL_WIN_MM_BLOCKS, Cin * ntile);
+    const int64_t most = std::max<int64_t>(1, N * hw / (2 * kMmWaves * kMmSlab));
+    return std::max<int64_t>(1, std::min(want, most));
+}
+}  // namespace
+
 extern "C" int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t hw,
                                      int64_t* nq) {
     clear_error();
     CL_ARG(nq && N >= 0 && Cin >= 1 && max_group >= 0 && hw >= 1, "bad argument");
+    if (use_mm(max_group)) {
+        *nq = std::min<int64_t>(mm_chunks(N, Cin, max_group, hw), 65535);
+        return CL_OK;
+    }
     // about 1536 blocks (two rounds of resident blocks), but at least 8 (sample, position)
     // elements per thread so that the closing reduction stays small against the loop
     const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
@@ -491,6 +727,24 @@ extern "C" int cl_conv_window_moments(int dtype, const void* x, const void* grad
     CL_ARG(grp_ptr && chan_order && moments, "null pointer argument");
     CL_ARG(N == 0 || (x && grad_y), "null pointer argument");
     CL_ARG(nq >= 1 && nq < 65536 && max_group >= 0, "bad chunk count");
+    if (use_mm(max_group)) {
+        const int64_t ntile = ceil_div(max_group, kMmTile);
+        const int64_t bx = Cin * ntile;
+        CL_ARG(bx < (int64_t(1) << 31), "conv layer too large for one launch");
+        CL_ARG(N * h_out * w_out < (int64_t(1) << 31), "too many (sample, position) elements");
+        const dim3 grid(unsigned(bx), unsigned(nq), 1);
+        CL_DTYPE_SWITCH(dtype, {
+            int rc = with_kw(kw, [&](auto K) {
+                k_win_moments_mm<scalar_t, decltype(K)::value>
+                    <<<grid, kMmWaves * 64, 0, as_stream(stream)>>>(
+                    static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(grad_y),
+                    grp_ptr, chan_order, static_cast<scalar_t*>(moments), int(ntile), int(nq), d);
+                return CL_OK;
+            });
+            if (rc) return rc;
+        });
+        return check_launch("cl_conv_window_moments");
+    }
     const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
     const int64_t bx = Cin * nsub;
     CL_ARG(bx < (int64_t(1) << 31), "conv layer too large for one launch");
@@ -517,7 +771,8 @@ extern "C" int cl_conv_window_finalize(int dtype, const void* moments, int64_t n
     if (Cout == 0) return CL_OK;
     CL_ARG(moments && gate_seq && slot_win && grad_w, "null pointer argument");
     CL_ARG(nq >= 1, "bad chunk count");
-    const unsigned blocks = unsigned(ceil_div(Cout, 4));
+    CL_ARG(Cout < (int64_t(1) << 31), "too many output channels");
+    const unsigned blocks = unsigned(Cout);
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
             k_win_finalize<scalar_t, decltype(K)::value><<<blocks, 256, 0, as_stream(stream)>>>(

@@ -15,6 +15,7 @@ import numpy as np
 import torch
 
 from . import _capi
+from . import timing
 from . import difflogic_hip as _dl
 from .layers import ConvLayer, GroupSum, LogicLayer, PackBitsTensor
 
@@ -190,7 +191,8 @@ class PackedNetwork:
         row_bytes = words.shape[1] * words.element_size()
         counts = torch.empty((n, self.k), dtype=torch.int32, device=words.device)
         with torch.cuda.device(words.device):
-            _capi.call("cl_packed_network", words.data_ptr(), row_bytes, n,
-                       self.tables.data_ptr(), self._rows_host, len(self.rows) - 1, self.k,
-                       counts.data_ptr(), _dl.stream_of(words))
+            timing.timed(f"cl_packed_network[{self.rows[0]}->{self.rows[-1]}]", lambda: _capi.call(
+                "cl_packed_network", words.data_ptr(), row_bytes, n, self.tables.data_ptr(),
+                self._rows_host, len(self.rows) - 1, self.k, counts.data_ptr(),
+                _dl.stream_of(words)))
         return counts

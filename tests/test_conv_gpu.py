@@ -375,6 +375,11 @@ WINDOW_SHAPES = [
     (4, 11, 13, 9, 64, 3, 3, 1, 2),      # stride 3, 64 slots
     (5, 6, 6, 5, 1, 3, 1, 2, 70),        # one slot, wide padding, several sample chunks
     (2, 40, 24, 3, 8, 3, 1, 1, 2),       # 960 output positions in one block
+    # at least 8 output channels per input channel: the tiled moments kernel
+    (9, 32, 32, 256, 16, 3, 2, 1, 6),    # cfg3 conv1 itself (28-29 channels per input channel)
+    (3, 12, 12, 100, 8, 2, 1, 0, 9),     # 2 x 2 windows, 33-34 channels: two channel tiles
+    (2, 9, 7, 40, 4, 2, 2, 1, 3),        # 2 x 2 windows, stride 2, 20 channels per input
+    (4, 10, 10, 40, 16, 3, 1, 1, 70),    # element chunks not multiples of the staged slab
 ]
 
 
