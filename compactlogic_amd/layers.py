@@ -19,7 +19,7 @@ from . import _capi
 from . import convlogic_hip as _cl
 from . import difflogic_hip as _dl
 from . import timing
-from .plan import PART_SLOTS, RunPlan, build_run_plan, locality_order
+from .plan import PART_SLOTS, REORDER_FRACTION, RunPlan, build_run_plan, locality_order
 
 
 ########################################################################################################################
@@ -552,12 +552,23 @@ class LogicLayer(torch.nn.Module):
     def run_plan(self) -> RunPlan:
         """The connection-run plan for the current `indices`, rebuilt after any change: the
         cache holds a weak reference to the indices tensor and its version, so an in-place
-        rewiring or a new tensor (even one at a recycled address) rebuilds it."""
+        rewiring or a new tensor (even one at a recycled address) rebuilds it.  An in-place
+        rewiring of few neurons (plan.REORDER_FRACTION of them since the last full build)
+        keeps the previous processing order of the inputs, which skips the plan's host round
+        trip; the rest of the plan is rebuilt from the new wiring."""
         ind = self.indices
         hit = self._plan_key
         if (self._plan is None or hit is None or hit[0]() is not ind
                 or hit[1] != (ind._version, ind.device)):
-            self._plan = build_run_plan(ind, self.in_dim)
+            old, order, stale = self._plan, None, 0
+            if (old is not None and hit is not None and hit[0]() is ind
+                    and old.src_indices is not None and old.src_indices.shape == ind.shape
+                    and old.src_indices.device == ind.device):
+                changed = int((old.src_indices != ind).any(0).any(-1).sum())
+                if old.stale + changed <= REORDER_FRACTION * ind.shape[1]:
+                    order, stale = old.row_order, old.stale + changed
+            self._plan = build_run_plan(ind, self.in_dim, row_order=order)
+            self._plan.stale = stale
             self._plan_key = (weakref.ref(ind), (ind._version, ind.device))
         return self._plan
 

@@ -62,6 +62,8 @@ class RunPlan:
     tile_ptr: torch.Tensor = None   # int32 [ntiles + 1] internal runs of tile t
     tile_run: torch.Tensor = None   # int32 [N, 4] (neuron, run, entry of a, entry of b)
     tile_loc: torch.Tensor = None   # int32 [N] a_local | b_local << 8 | slot_a << 16 | slot_b << 24
+    src_indices: torch.Tensor = None  # the indices the plan was built from (a copy)
+    stale: int = 0                    # neurons rewired since row_order was last computed
 
     @property
     def num_runs(self) -> int:
@@ -128,8 +130,18 @@ def partition_tiles(row_order: torch.Tensor, ra: torch.Tensor, rb: torch.Tensor,
             tile_run.reshape(-1, 4).to(i32).contiguous(), loc.to(i32).contiguous())
 
 
-def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
-    """Derive the run plan from `indices` [2, out_dim, G] (int64) on its device."""
+# A rewiring that changes at most this fraction of a layer's neurons (counted since the last
+# full order) keeps the previous processing order of the inputs: the order only sets memory
+# locality, and recomputing it is the plan's one host round trip.
+REORDER_FRACTION = 0.1
+
+
+def build_run_plan(indices: torch.Tensor, in_dim: int,
+                   row_order: torch.Tensor | None = None) -> RunPlan:
+    """Derive the run plan from `indices` [2, out_dim, G] (int64) on its device.  With
+    `row_order` (a permutation of the inputs, e.g. a previous plan's) the inputs' processing
+    order is taken from it instead of being recomputed (locality_order): every result is the
+    same up to the order of additions within a row."""
     if indices.dim() != 3 or indices.shape[0] != 2:
         raise ValueError(f"indices must be [2, out_dim, num_gates], got {tuple(indices.shape)}")
     _, out_dim, g = indices.shape
@@ -171,7 +183,12 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
     ids = torch.arange(r, dtype=torch.int64, device=dev) * 2
     entry = torch.cat((ids, ids + 1))
     inv_counts = torch.bincount(inputs, minlength=in_dim)
-    row_order = locality_order(ra, rb, in_dim)
+    if row_order is None:
+        row_order = locality_order(ra, rb, in_dim)
+    else:
+        row_order = row_order.to(device=dev, dtype=torch.int64)
+        if row_order.shape != (in_dim,):
+            raise ValueError(f"row_order must have {in_dim} entries")
     rpos = torch.empty(in_dim, dtype=torch.int64, device=dev)
     rpos[row_order] = torch.arange(in_dim, dtype=torch.int64, device=dev)
     dist = (rpos[inputs] - rpos[others]).abs()
@@ -212,4 +229,5 @@ def build_run_plan(indices: torch.Tensor, in_dim: int) -> RunPlan:
         slot_rec=slot_rec.to(i32).contiguous(),
         single_run=bool(out_dim > 0 and r == out_dim),
         inv_slot=inv_slot, tile_ptr=tile_ptr, tile_run=tile_run, tile_loc=tile_loc,
+        src_indices=indices.detach().clone(),
     )

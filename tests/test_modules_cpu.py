@@ -114,6 +114,59 @@ def test_plan_rebuilds_after_in_place_rewiring():
     assert p2 is not p1 and p2.num_runs == p1.num_runs + 2
 
 
+def _plan_fields(plan):
+    return {k: getattr(plan, k) for k in ("run_ptr", "run_ab", "run_gl", "run_y", "inv_ptr",
+                                          "inv_entry", "inv_rec", "inv_pos", "row_order", "nab",
+                                          "slot_rec", "inv_slot", "tile_ptr", "tile_run",
+                                          "tile_loc")}
+
+
+def test_small_rewiring_keeps_the_input_order():
+    """An in-place rewiring of at most REORDER_FRACTION of the neurons (counted since the last
+    full order) keeps the previous plan's input order and rebuilds everything else from the new
+    wiring: the plan equals build_run_plan with that order given.  Past the fraction, or for a
+    new indices tensor, the order is recomputed (locality_order of the new runs)."""
+    from compactlogic_amd.plan import REORDER_FRACTION, build_run_plan, locality_order
+    torch.manual_seed(11)
+    layer = cl.LogicLayer(64, 100, connections="random")
+    p1 = layer.run_plan()
+    assert p1.stale == 0
+    n1 = int(REORDER_FRACTION * 100) // 2                   # 5 neurons
+    with torch.no_grad():
+        layer.indices[:, :n1] = torch.randint(0, 64, (2, n1, layer.num_gates))
+    p2 = layer.run_plan()
+    assert p2 is not p1 and p2.stale == n1
+    assert torch.equal(p2.row_order, p1.row_order)
+    want = build_run_plan(layer.indices, 64, row_order=p1.row_order)
+    for k, v in _plan_fields(want).items():
+        assert torch.equal(getattr(p2, k), v), k
+    # the runs themselves are those of a fresh build: only the input order is carried over
+    fresh = build_run_plan(layer.indices, 64)
+    for k in ("run_ptr", "run_ab", "run_gl", "run_y", "inv_ptr", "nab"):
+        assert torch.equal(getattr(p2, k), getattr(fresh, k)), k
+    # rewirings accumulate (each counts the neurons it changed) until the fraction is passed
+    with torch.no_grad():
+        layer.indices[:, :n1] = torch.randint(0, 64, (2, n1, layer.num_gates))
+    p3 = layer.run_plan()
+    assert p3.stale == 2 * n1 and torch.equal(p3.row_order, p1.row_order)
+    with torch.no_grad():
+        layer.indices[:, n1:n1 + 1] = torch.randint(0, 64, (2, 1, layer.num_gates))
+    p4 = layer.run_plan()
+    assert p4.stale == 0
+    ab = p4.run_ab.long()
+    assert torch.equal(p4.row_order.long(), locality_order(ab[:, 0], ab[:, 1], 64))
+    # a new tensor is a full build
+    layer.indices = layer.indices.clone()
+    p5 = layer.run_plan()
+    assert p5.stale == 0 and torch.equal(p5.row_order, p4.row_order)
+
+
+def test_run_plan_rejects_a_bad_row_order():
+    ind = torch.randint(0, 6, (2, 4, 3))
+    with pytest.raises(ValueError):
+        cl.build_run_plan(ind, 6, row_order=torch.arange(5))
+
+
 def test_resample_connections_updates_index():
     torch.manual_seed(4)
     layer = cl.LogicLayer(10, 16)

@@ -108,6 +108,29 @@ def test_resample_then_train_step_matches_oracle(device, connections):
         opt.step()
 
 
+@pytest.mark.parametrize("connections", ["random", "original"])
+def test_small_rewiring_keeps_order_and_matches_oracle(device, connections):
+    """Rewiring a few neurons in place keeps the inputs' processing order of the previous
+    plan (only the runs and the inverse index are rebuilt): the step still matches the
+    oracle on the new wiring."""
+    model = make_model(device, connections, seed=4)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.rand((64, 64), generator=g) < 0.4).float().to(device)
+    y = torch.randint(0, 10, (64,), generator=g).to(device)
+    train_step(model, x, y)
+    layer = model[1]
+    order = layer.run_plan().row_order.clone()
+    with torch.no_grad():
+        layer.indices[:, 3:7] = torch.randint(0, layer.in_dim, (2, 4, layer.num_gates),
+                                              device=device)
+    plan = layer.run_plan()
+    assert plan.stale == 4 and torch.equal(plan.row_order, order)
+    model.zero_grad(set_to_none=True)
+    acts = train_step(model, x, y)
+    for i, l in enumerate(model[:3]):
+        check_layer(l, acts[i], acts[i + 1])
+
+
 def test_freezer_on_partly_frozen_network(device):
     model = make_model(device, "original", seed=2)
     g = torch.Generator().manual_seed(3)
