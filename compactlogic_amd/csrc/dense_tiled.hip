@@ -1155,8 +1155,18 @@ __global__ __launch_bounds__(256) void k_bwd_part(
 // input gradient still adds the entries in entry order.  With gy_magic != 0 the gradient of
 // neuron o is row o / gsz of grad_y (one row per GroupSum class: the fused classifier head),
 // gy_magic = ceil(2^32 / gsz) with out_dim * gsz <= 2^32, so the multiply-high is exact.
+// Waves per SIMD the row backward asks the register allocator for: four (at most 128 VGPRs)
+// where the fp32 kernel fits them without spilling (rows of up to 1024 samples); more waves
+// per SIMD keep more rows' gathers in flight, which is what bounds this kernel.
+template <typename T, int U>
+constexpr int bwd_rows_waves() { return sizeof(T) == 4 && U <= 4 ? 4 : 1; }
+
+#ifndef CL_BWD_ROWS_EPI4
+#define CL_BWD_ROWS_EPI4 2
+#endif
 template <typename T, int VEC, int U, bool WANT_GW, bool HAS_P>
-__global__ __launch_bounds__(256) void k_bwd_rows(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_rows_waves<T, U>())))
+void k_bwd_rows(
     const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
     const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef,
     const uint8_t* __restrict__ gs, const T* __restrict__ probs,
@@ -1165,7 +1175,7 @@ __global__ __launch_bounds__(256) void k_bwd_rows(
     uint32_t gy_magic) {
     using V = typename VT<T, VEC>::type;
     using V2 = typename VT<T, 2>::type;
-    constexpr int EPI = U <= 4 ? 2 : 1;  // entries per step (register budget)
+    constexpr int EPI = U <= 2 ? 2 : U <= 4 ? CL_BWD_ROWS_EPI4 : 1;  // entries per step
     const int lane = threadIdx.x & 63;
     const int64_t w = blockIdx.x;
     const int64_t slot = ((w % kXcds) * nblk + w / kXcds) * 4 + wave_id();
