@@ -405,9 +405,9 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mm(
 #pragma unroll
         for (int j = 0; j < kMmTile / 2; ++j) gr[j] = gyn[coff[j]];
     };
-    T vn[P], gn[kMmTile / 2];
-    bool liven, tinn[P];
-    issue(0, vn, gn, liven, tinn);
+    T vn[P] = {}, gn[kMmTile / 2] = {};
+    bool liven = false, tinn[P] = {};
+    if (rounds > 0) issue(0, vn, gn, liven, tinn);  // an empty chunk reads nothing
     for (int r = 0; r < rounds; ++r) {
         T v[P], gv[kMmTile / 2];
 #pragma unroll
@@ -486,6 +486,245 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mm(
             if (m < CW) part[(int64_t(q) * d.Cout + c) * CW + m] = acc[i][j];
         }
     }
+}
+
+// k_win_moments_mx: the fp32 form of k_win_moments_mm on the matrix cores.  Per slab of
+// kMmSlab elements a wave stages grad_y and the window row (1, v_0 .. v_{P-1}, 0, ...) of each
+// element (pitch kMxWP) in its own LDS buffers, then runs the product
+//     M[c][m] += sum_e grad_y[c][e] f_m(e)
+// as 16x16x4 fp32 MFMA tiles: A = grad_y (16 channels x 4 elements: lane i + 16 k holds
+// channel i of element k), B = features (4 elements x 16 features: lane j + 16 k holds feature
+// j of element k, formed as the product of the two window-row entries that define it, read
+// from LDS), D = 16 x 16 moments (register r of lane l: channel 4 (l / 16) + r, feature
+// l % 16).  A wave holds 2 x 4 tiles (32 channels x 64 features).  grad_y is fetched as
+// 16-byte vectors of four consecutive elements of one channel when the plane size is a
+// multiple of 4 (G4: chunks then start at multiples of 4, so a vector never spans two samples
+// or two chunks) and staged [channel][element] (pitch kMxEP: the A reads of a half-wave fall
+// in distinct banks); otherwise one element per lane, staged [element][channel] (pitch
+// kMxGP).  The slab's global loads are issued one slab ahead; the waves' sums are added in
+// wave order as in k_win_moments_mm.
+constexpr int kMxGP = 48;  // [element][channel]: 32 channels + 16
+constexpr int kMxEP = 34;  // [channel][element]: 32 elements + 2
+constexpr int kMxWP = 12;  // 1, v_0 .. v_8, then zeros
+
+template <int KW, bool G4>
+__global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
+    const float* __restrict__ x, const float* __restrict__ gy, const int32_t* __restrict__ grp_ptr,
+    const int32_t* __restrict__ chan_order, float* __restrict__ part, int ntile, int nq,
+    WinDims d) {
+    constexpr int P = Win<KW>::P, NM = 1 + P + Win<KW>::NP, CW = Win<KW>::CW;
+    static_assert(P + 2 <= kMxWP && NM <= kMmFeat && kMmTile == 32 && kMmSlab == 32, "layout");
+    static_assert(kMmSlab * kMxEP <= kMmSlab * kMxGP, "staging space");
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    typedef float F2 __attribute__((ext_vector_type(2)));
+    __shared__ F4 gs4[kMmWaves][kMmSlab * kMxGP / 4];
+    __shared__ F4 ws4[kMmWaves][kMmSlab * kMxWP / 4];
+    static_assert(kMmWaves == 1 || sizeof(gs4) >= (kMmWaves - 1) * 64 * 32 * sizeof(float),
+                  "reduction space");
+    const int wv = wave_id(), lane = threadIdx.x & 63;
+    float* const gsw = reinterpret_cast<float*>(&gs4[wv][0]);
+    float* const wsw = reinterpret_cast<float*>(&ws4[wv][0]);
+    const int q = blockIdx.y;
+    const int ch = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+    const int g0 = grp_ptr[ch] + tile * kMmTile, g1 = std::min(grp_ptr[ch + 1], g0 + kMmTile);
+    if (g0 >= g1) return;  // uniform per workgroup
+    const int hw = d.Ho * d.Wo, HW = d.H * d.W;
+    const int E = int(d.N) * hw;  // < 2^31 (checked by the host)
+    int e0, e1;
+    if constexpr (G4) {
+        e0 = 4 * int(int64_t(q) * (E / 4) / nq);
+        e1 = 4 * int(int64_t(q + 1) * (E / 4) / nq);
+    } else {
+        e0 = int(int64_t(q) * E / nq);
+        e1 = int(int64_t(q + 1) * E / nq);
+    }
+    const int nslab = (e1 - e0 + kMmSlab - 1) / kMmSlab;
+    const int rounds = (nslab + kMmWaves - 1) / kMmWaves;  // equal for every wave
+    // window staging: element se = lane % 32 (both halves load it, half 0 stores it)
+    const int se = lane % kMmSlab, half = lane / kMmSlab;
+    // grad_y staging: G4: four elements 4 quad .. + 3 of channels cg + 8 u (u < 4);
+    // otherwise element se of channels 16 half .. + 15
+    constexpr int NG = G4 ? 4 : kMmTile / 2;  // loads per lane
+    const int quad = lane & 7, cg = lane >> 3;
+    int coff[NG];
+    bool cok[NG];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        const int gi = G4 ? g0 + cg + 8 * j : g0 + half * (kMmTile / 2) + j;
+        cok[j] = gi < g1;
+        coff[j] = chan_order[cok[j] ? gi : g0] * hw;
+    }
+    // MFMA roles: element row ek = lane / 16 of each group of four; feature 16 t + lane % 16
+    // of tile t is w[fa[t]] * w[fb[t]] of the element's window row
+    const int ek = lane / 16, li = lane % 16;
+    constexpr BetaPairs<P> bp{};
+    const float* pwa[4];
+    const float* pwb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int m = 16 * t + li;
+        int a = P + 1, b = P + 1;  // a zero entry: features past NM
+        if (m == 0) a = b = 0;
+        else if (m <= P) a = 0, b = m;
+        else if (m < NM) a = bp.k[m - 1 - P] + 1, b = bp.l[m - 1 - P] + 1;
+        pwa[t] = wsw + ek * kMxWP + a;
+        pwb[t] = wsw + ek * kMxWP + b;
+    }
+    // A operand of step kk, channel tile mi: pga[kk * dA + mi * dM]
+    const float* const pga = G4 ? gsw + li * kMxEP + ek : gsw + ek * kMxGP + li;
+    constexpr int dA = G4 ? 4 : 4 * kMxGP, dM = G4 ? 16 * kMxEP : 16;
+    F4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[i][t] = F4{0.f, 0.f, 0.f, 0.f};
+    auto issue = [&](int r, float (&vr)[P], float (&gr)[kMmTile / 2], bool& live, bool& gl,
+                     bool (&tin)[P]) {
+        const int sb = e0 + (r * kMmWaves + wv) * kMmSlab;
+        {
+            const int e = sb + se;
+            live = r < rounds && e < e1;
+            const int ec = live ? e : e0;
+            const int n = ec / hw, pos = ec - n * hw;
+            const int oy = pos / d.Wo, ox = pos - oy * d.Wo;
+            const int by = oy * d.stride + d.oy0, bx = ox * d.stride + d.ox0;
+            const float* plane = x + (int64_t(n) * d.Cin + ch) * HW;
+#pragma unroll
+            for (int k = 0; k < P; ++k) {
+                const int yy = by + k / KW, xx = bx + k % KW;
+                tin[k] = live && unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W);
+                vr[k] = plane[tin[k] ? yy * d.W + xx : 0];
+            }
+            if constexpr (!G4) {
+                gl = live;
+                const float* gyn = gy + int64_t(n) * d.Cout * hw + pos;
+#pragma unroll
+                for (int j = 0; j < NG; ++j) gr[j] = gyn[coff[j]];
+            }
+        }
+        if constexpr (G4) {
+            const int e = sb + 4 * quad;
+            gl = r < rounds && e < e1;  // e1 is a multiple of 4: the whole vector is live
+            const int ec = gl ? e : e0;
+            const int n = ec / hw, pos = ec - n * hw;
+            const float* gyn = gy + int64_t(n) * d.Cout * hw + pos;
+#pragma unroll
+            for (int j = 0; j < NG; ++j) {
+                const F4 v = *reinterpret_cast<const F4*>(gyn + coff[j]);
+                gr[4 * j] = v[0];
+                gr[4 * j + 1] = v[1];
+                gr[4 * j + 2] = v[2];
+                gr[4 * j + 3] = v[3];
+            }
+        }
+    };
+    float vn[P] = {}, gn[kMmTile / 2] = {};
+    bool liven = false, gln = false, tinn[P] = {};
+    if (rounds > 0) issue(0, vn, gn, liven, gln, tinn);  // an empty chunk reads nothing
+    for (int r = 0; r < rounds; ++r) {
+        float wrow[kMxWP];
+        wrow[0] = 1.f;
+#pragma unroll
+        for (int k = 0; k < P; ++k) wrow[1 + k] = tinn[k] ? vn[k] : 0.f;
+#pragma unroll
+        for (int k = P + 1; k < kMxWP; ++k) wrow[k] = 0.f;
+        // a masked element or channel: grad_y 0 (its window row may hold anything finite)
+        float gv[kMmTile / 2];
+#pragma unroll
+        for (int j = 0; j < kMmTile / 2; ++j) gv[j] = (gln && cok[G4 ? j / 4 : j]) ? gn[j] : 0.f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if constexpr (G4) {
+#pragma unroll
+            for (int j = 0; j < NG; ++j) {
+                F2* gdst = reinterpret_cast<F2*>(gsw + (cg + 8 * j) * kMxEP + 4 * quad);
+                gdst[0] = F2{gv[4 * j], gv[4 * j + 1]};
+                gdst[1] = F2{gv[4 * j + 2], gv[4 * j + 3]};
+            }
+        } else {
+            F4* gdst = reinterpret_cast<F4*>(gsw + se * kMxGP + half * (kMmTile / 2));
+#pragma unroll
+            for (int j = 0; j < kMmTile / 8; ++j)
+                gdst[j] = F4{gv[4 * j], gv[4 * j + 1], gv[4 * j + 2], gv[4 * j + 3]};
+        }
+        if (half == 0) {
+            F4* wdst = reinterpret_cast<F4*>(wsw + se * kMxWP);
+#pragma unroll
+            for (int j = 0; j < kMxWP / 4; ++j)
+                wdst[j] = F4{wrow[4 * j], wrow[4 * j + 1], wrow[4 * j + 2], wrow[4 * j + 3]};
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        issue(r + 1, vn, gn, liven, gln, tinn);   // the next slab's loads, in flight meanwhile
+        // operands of step kk + 1 are read from LDS while the MFMAs of step kk run; every
+        // read is a lane base plus a compile-time offset
+        float a0 = pga[0], a1 = pga[dM], wa[4], wb[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            wa[t] = pwa[t][0];
+            wb[t] = pwb[t][0];
+        }
+#pragma unroll
+        for (int kk = 0; kk < kMmSlab / 4; ++kk) {
+            float b[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) b[t] = wa[t] * wb[t];
+            const float c0 = a0, c1 = a1;
+            if (kk + 1 < kMmSlab / 4) {
+                constexpr int dw = 4 * kMxWP;
+                a0 = pga[(kk + 1) * dA];
+                a1 = pga[(kk + 1) * dA + dM];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    wa[t] = pwa[t][(kk + 1) * dw];
+                    wb[t] = pwb[t][(kk + 1) * dw];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(c0, b[t], acc[0][t], 0, 0, 0);
+                acc[1][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(c1, b[t], acc[1][t], 0, 0, 0);
+            }
+        }
+    }
+    // the waves' sums added in wave order by wave 0
+    if constexpr (kMmWaves > 1) __syncthreads();
+    float* red = reinterpret_cast<float*>(&gs4[0][0]);
+    if (kMmWaves > 1 && wv > 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    red[((wv - 1) * 32 + (i * 4 + t) * 4 + r) * 64 + lane] = acc[i][t][r];
+    }
+    if constexpr (kMmWaves > 1) __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int w = 1; w < kMmWaves; ++w)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[i][t][r] += red[((w - 1) * 32 + (i * 4 + t) * 4 + r) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int gi = g0 + 16 * i + 4 * ek + r;
+            if (gi >= g1) continue;
+            const int c = chan_order[gi];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int m = 16 * t + li;
+                if (m < CW) part[(int64_t(q) * d.Cout + c) * CW + m] = acc[i][t][r];
+            }
+        }
 }
 
 // One workgroup of four waves per channel: wave w sums the moments of chunks w, w + 4, ...
@@ -677,11 +916,14 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
 #endif
 
 // Input channels read by at least this many output channels take the tiled moments kernel.
+#ifndef CL_WIN_MX
+#define CL_WIN_MX 1
+#endif
 #ifndef CL_WIN_MM_MIN_GROUP
 #define CL_WIN_MM_MIN_GROUP 8
 #endif
 #ifndef CL_WIN_MM_BLOCKS
-#define CL_WIN_MM_BLOCKS 768  // workgroups of the tiled moments kernel (three per CU)
+#define CL_WIN_MM_BLOCKS 768  // resident workgroups of the tiled moments kernels (three per CU)
 #endif
 
 namespace {
@@ -691,7 +933,8 @@ bool use_mm(int64_t max_group) { return max_group >= CL_WIN_MM_MIN_GROUP; }
 // two staged slabs of elements per wave
 int64_t mm_chunks(int64_t N, int64_t Cin, int64_t max_group, int64_t hw) {
     const int64_t ntile = ceil_div(max_group, kMmTile);
-    const int64_t want = ceil_div(CL_WIN_MM_BLOCKS, Cin * ntile);
+    // at most one round of resident workgroups: a few left over would run as a second round
+    const int64_t want = std::max<int64_t>(1, CL_WIN_MM_BLOCKS / (Cin * ntile));
     const int64_t most = std::max<int64_t>(1, N * hw / (2 * kMmWaves * kMmSlab));
     return std::max<int64_t>(1, std::min(want, most));
 }
@@ -733,6 +976,25 @@ extern "C" int cl_conv_window_moments(int dtype, const void* x, const void* grad
         CL_ARG(bx < (int64_t(1) << 31), "conv layer too large for one launch");
         CL_ARG(N * h_out * w_out < (int64_t(1) << 31), "too many (sample, position) elements");
         const dim3 grid(unsigned(bx), unsigned(nq), 1);
+#if CL_WIN_MX
+        if (dtype == CL_DTYPE_F32) {
+            // 16-byte grad_y vectors: planes of a multiple of 4 elements, an aligned tensor
+            const bool g4 = (h_out * w_out) % 4 == 0 && aligned(grad_y, 16);
+            int rc = with_kw(kw, [&](auto K) {
+                auto go = [&](auto gc) {
+                    k_win_moments_mx<decltype(K)::value, decltype(gc)::value>
+                        <<<grid, kMmWaves * 64, 0, as_stream(stream)>>>(
+                        static_cast<const float*>(x), static_cast<const float*>(grad_y), grp_ptr,
+                        chan_order, static_cast<float*>(moments), int(ntile), int(nq), d);
+                };
+                if (g4) go(std::true_type{});
+                else go(std::false_type{});
+                return CL_OK;
+            });
+            if (rc) return rc;
+            return check_launch("cl_conv_window_moments");
+        }
+#endif
         CL_DTYPE_SWITCH(dtype, {
             int rc = with_kw(kw, [&](auto K) {
                 k_win_moments_mm<scalar_t, decltype(K)::value>

@@ -398,6 +398,24 @@ def test_window_path_matches_oracle(device, shape, dtype):
     _layer_vs_oracle(layer, x, gy, dtype)
 
 
+@pytest.mark.parametrize("c_out", [20, 256])
+def test_window_path_empty_batch(device, c_out):
+    """A batch of 0 samples: empty outputs and input gradient, zero logits gradient, no read of
+    the (empty) inputs, on the chunked moments kernel (20 channels over 9 inputs) and on the
+    tiled one (28-29 channels per input channel)."""
+    torch.manual_seed(2)
+    layer = cl.ConvLayer((9, 32, 32), padding=1, c_out=c_out, ks=3, stride=2, num_chn=1,
+                         num_gates=16).to(device)
+    x = torch.rand((0, 9, 32, 32), device=device, requires_grad=True)
+    assert layer.window_plan(x) is not None
+    y = layer(x)
+    assert y.shape == (0, c_out, 16, 16)
+    y.sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad.shape == x.shape
+    assert torch.equal(layer.weights.grad, torch.zeros_like(layer.weights))
+
+
 def test_window_path_self_pairs_and_rewiring(device):
     """Slots whose two operands are the same tap (reachable through rewiring, which does not
     re-resolve conflicts) give square terms; in-place offset changes rebuild the plan."""
