@@ -519,8 +519,7 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
     typedef float F2 __attribute__((ext_vector_type(2)));
     __shared__ F4 gs4[kMmWaves][kMmSlab * kMxGP / 4];
     __shared__ F4 ws4[kMmWaves][kMmSlab * kMxWP / 4];
-    static_assert(kMmWaves == 1 || sizeof(gs4) >= (kMmWaves - 1) * 64 * 32 * sizeof(float),
-                  "reduction space");
+    static_assert(sizeof(gs4) >= kMmWaves * 64 * 16 * sizeof(float), "reduction space");
     const int wv = wave_id(), lane = threadIdx.x & 63;
     float* const gsw = reinterpret_cast<float*>(&gs4[wv][0]);
     float* const wsw = reinterpret_cast<float*>(&ws4[wv][0]);
@@ -540,8 +539,15 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
     }
     const int nslab = (e1 - e0 + kMmSlab - 1) / kMmSlab;
     const int rounds = (nslab + kMmWaves - 1) / kMmWaves;  // equal for every wave
-    // window staging: element se = lane % 32 (both halves load it, half 0 stores it)
+    // window staging: element se = lane % 32, taps KH * half .. + KH - 1 (the window row's
+    // constant entries, 1 and the zeros past P, are stored once here)
+    constexpr int KH = (P + 1) / 2;
     const int se = lane % kMmSlab, half = lane / kMmSlab;
+    if (half == 0) {
+        wsw[se * kMxWP] = 1.f;
+#pragma unroll
+        for (int k = P + 1; k < kMxWP; ++k) wsw[se * kMxWP + k] = 0.f;
+    }
     // grad_y staging: G4: four elements 4 quad .. + 3 of channels cg + 8 u (u < 4);
     // otherwise element se of channels 16 half .. + 15
     constexpr int NG = G4 ? 4 : kMmTile / 2;  // loads per lane
@@ -557,16 +563,29 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
     // MFMA roles: element row ek = lane / 16 of each group of four; feature 16 t + lane % 16
     // of tile t is w[fa[t]] * w[fb[t]] of the element's window row
     const int ek = lane / 16, li = lane % 16;
-    constexpr BetaPairs<P> bp{};
     const float* pwa[4];
     const float* pwb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const int m = 16 * t + li;
         int a = P + 1, b = P + 1;  // a zero entry: features past NM
-        if (m == 0) a = b = 0;
-        else if (m <= P) a = 0, b = m;
-        else if (m < NM) a = bp.k[m - 1 - P] + 1, b = bp.l[m - 1 - P] + 1;
+        if (m == 0) {
+            a = b = 0;
+        } else if (m <= P) {
+            a = 0;
+            b = m;
+        } else if (m < NM) {
+            // pair r of the upper triangle by rows: (k, l) = (row, row + offset in the row)
+            // (a lane-indexed table would be held in registers)
+            int r = m - 1 - P, row = 0, len = P;
+            while (r >= len) {
+                r -= len;
+                ++row;
+                --len;
+            }
+            a = row + 1;
+            b = row + r + 1;
+        }
         pwa[t] = wsw + ek * kMxWP + a;
         pwb[t] = wsw + ek * kMxWP + b;
     }
@@ -578,8 +597,8 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[i][t] = F4{0.f, 0.f, 0.f, 0.f};
-    auto issue = [&](int r, float (&vr)[P], float (&gr)[kMmTile / 2], bool& live, bool& gl,
-                     bool (&tin)[P]) {
+    auto issue = [&](int r, float (&vr)[KH], float (&gr)[kMmTile / 2], bool& live, bool& gl,
+                     bool (&tin)[KH]) {
         const int sb = e0 + (r * kMmWaves + wv) * kMmSlab;
         {
             const int e = sb + se;
@@ -590,10 +609,13 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
             const int by = oy * d.stride + d.oy0, bx = ox * d.stride + d.ox0;
             const float* plane = x + (int64_t(n) * d.Cin + ch) * HW;
 #pragma unroll
-            for (int k = 0; k < P; ++k) {
-                const int yy = by + k / KW, xx = bx + k % KW;
-                tin[k] = live && unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W);
-                vr[k] = plane[tin[k] ? yy * d.W + xx : 0];
+            for (int j = 0; j < KH; ++j) {
+                // tap j of half 0, tap KH + j of half 1 (P itself: the zero entry)
+                const int dy = half ? (KH + j) / KW : j / KW, dx = half ? (KH + j) % KW : j % KW;
+                const bool tap = !half || KH + j < P;
+                const int yy = by + dy, xx = bx + dx;
+                tin[j] = live && tap && unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W);
+                vr[j] = plane[tin[j] ? yy * d.W + xx : 0];
             }
             if constexpr (!G4) {
                 gl = live;
@@ -618,16 +640,13 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
             }
         }
     };
-    float vn[P] = {}, gn[kMmTile / 2] = {};
-    bool liven = false, gln = false, tinn[P] = {};
+    float vn[KH] = {}, gn[kMmTile / 2] = {};
+    bool liven = false, gln = false, tinn[KH] = {};
     if (rounds > 0) issue(0, vn, gn, liven, gln, tinn);  // an empty chunk reads nothing
     for (int r = 0; r < rounds; ++r) {
-        float wrow[kMxWP];
-        wrow[0] = 1.f;
+        float wv_[KH];
 #pragma unroll
-        for (int k = 0; k < P; ++k) wrow[1 + k] = tinn[k] ? vn[k] : 0.f;
-#pragma unroll
-        for (int k = P + 1; k < kMxWP; ++k) wrow[k] = 0.f;
+        for (int j = 0; j < KH; ++j) wv_[j] = tinn[j] ? vn[j] : 0.f;
         // a masked element or channel: grad_y 0 (its window row may hold anything finite)
         float gv[kMmTile / 2];
 #pragma unroll
@@ -648,11 +667,10 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
             for (int j = 0; j < kMmTile / 8; ++j)
                 gdst[j] = F4{gv[4 * j], gv[4 * j + 1], gv[4 * j + 2], gv[4 * j + 3]};
         }
-        if (half == 0) {
-            F4* wdst = reinterpret_cast<F4*>(wsw + se * kMxWP);
+        {
+            float* wdst = wsw + se * kMxWP + 1 + half * KH;
 #pragma unroll
-            for (int j = 0; j < kMxWP / 4; ++j)
-                wdst[j] = F4{wrow[4 * j], wrow[4 * j + 1], wrow[4 * j + 2], wrow[4 * j + 3]};
+            for (int j = 0; j < KH; ++j) wdst[j] = wv_[j];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -689,42 +707,28 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_win_moments_mx(
             }
         }
     }
-    // the waves' sums added in wave order by wave 0
-    if constexpr (kMmWaves > 1) __syncthreads();
+    // the waves' sums added in wave order, one channel tile at a time: every wave stores its
+    // 16 sums of the tile, then wave w adds feature tile w of all four waves and stores it
+    static_assert(kMmWaves == 4, "one feature tile per wave in the closing reduction");
     float* red = reinterpret_cast<float*>(&gs4[0][0]);
-    if (kMmWaves > 1 && wv > 0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+        __syncthreads();
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    red[((wv - 1) * 32 + (i * 4 + t) * 4 + r) * 64 + lane] = acc[i][t][r];
-    }
-    if constexpr (kMmWaves > 1) __syncthreads();
-    if (wv != 0) return;
-#pragma unroll
-    for (int w = 1; w < kMmWaves; ++w)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc[i][t][r] += red[((w - 1) * 32 + (i * 4 + t) * 4 + r) * 64 + lane];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
+            for (int r = 0; r < 4; ++r) red[(wv * 16 + t * 4 + r) * 64 + lane] = acc[i][t][r];
+        __syncthreads();
+        const int m = 16 * wv + li;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int gi = g0 + 16 * i + 4 * ek + r;
-            if (gi >= g1) continue;
-            const int c = chan_order[gi];
+            float sum = red[(wv * 4 + r) * 64 + lane];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int m = 16 * t + li;
-                if (m < CW) part[(int64_t(q) * d.Cout + c) * CW + m] = acc[i][t][r];
-            }
+            for (int w = 1; w < kMmWaves; ++w) sum += red[(w * 16 + wv * 4 + r) * 64 + lane];
+            const int gi = g0 + 16 * i + 4 * ek + r;
+            if (gi < g1 && m < CW) part[(int64_t(q) * d.Cout + chan_order[gi]) * CW + m] = sum;
         }
+    }
 }
 
 // One workgroup of four waves per channel: wave w sums the moments of chunks w, w + 4, ...
@@ -923,7 +927,7 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
 #define CL_WIN_MM_MIN_GROUP 8
 #endif
 #ifndef CL_WIN_MM_BLOCKS
-#define CL_WIN_MM_BLOCKS 768  // resident workgroups of the tiled moments kernels (three per CU)
+#define CL_WIN_MM_BLOCKS 1024  // resident workgroups of the fp32 tiled moments kernel (four per CU)
 #endif
 
 namespace {
