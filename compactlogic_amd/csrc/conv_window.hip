@@ -913,7 +913,7 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
 }
 
 #ifndef CL_WIN_BLOCKS
-#define CL_WIN_BLOCKS 1536
+#define CL_WIN_BLOCKS 768  // resident workgroups of the chunked moments kernel (three per CU)
 #endif
 #ifndef CL_WIN_MIN_ITERS
 #define CL_WIN_MIN_ITERS 8
@@ -952,10 +952,11 @@ extern "C" int cl_conv_window_chunks(int64_t N, int64_t Cin, int64_t max_group, 
         *nq = std::min<int64_t>(mm_chunks(N, Cin, max_group, hw), 65535);
         return CL_OK;
     }
-    // about 1536 blocks (two rounds of resident blocks), but at least 8 (sample, position)
-    // elements per thread so that the closing reduction stays small against the loop
+    // one round of resident blocks (a few left over would run as a second round), but at
+    // least 8 (sample, position) elements per thread so that the closing reduction stays
+    // small against the loop
     const int64_t nsub = std::max<int64_t>(1, ceil_div(max_group, kWinCB));
-    const int64_t want = ceil_div(CL_WIN_BLOCKS, Cin * nsub);
+    const int64_t want = std::max<int64_t>(1, CL_WIN_BLOCKS / (Cin * nsub));
     const int64_t most = N * hw / (256 * CL_WIN_MIN_ITERS);
     *nq = std::max<int64_t>(1, std::min<int64_t>(std::min(want, most), std::max<int64_t>(N, 1)));
     return CL_OK;
