@@ -35,7 +35,10 @@ namespace {
 constexpr int kTaps = 8;
 constexpr int kMaxNodes = 7;
 constexpr int kGatherBatch = 4;  // channel uses whose loads the input-gradient gather overlaps
-constexpr int kNodeItems = 16;   // items per thread of the backward node kernel
+constexpr int kNodeItems = 16;   // most items per thread of the backward node kernel
+#ifndef CL_TREE_NODE_WGS
+#define CL_TREE_NODE_WGS 1024     // workgroups the backward node kernel aims for
+#endif
 
 template <typename T>
 __device__ __forceinline__ T quiet_nan() {
@@ -49,6 +52,7 @@ struct TreeDims {
     int regular;  // the caller guarantees every tap lies in the window and reads a channel < cin
     int y_rows;   // complete form: y / grad_y element (n, c, p) at (c * P + p) * n_total + n
     int P;  // items per (sample, channel): pooled windows (complete) or conv positions
+    int node_items;  // items per thread of the backward node kernel (set by node_blocks)
     FastDiv div_p, div_wp;  // by P, and by the windows per pooled row (complete) or wo
     FastDiv div_wo;         // by wo (conv positions -> rows)
 };
@@ -734,11 +738,11 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
     T mom[NM];
 #pragma unroll
     for (int i = 0; i < NM; ++i) mom[i] = T(0);
-    // kNodeItems items per thread (strided by the workgroup size), so the moments of that many
-    // items are summed in registers before the wave reductions
+    // d.node_items items per thread (strided by the workgroup size), so the moments of that
+    // many items are summed in registers before the wave reductions
     const int64_t total = int64_t(d.n) * d.P;
-    for (int it = 0; it < kNodeItems; ++it) {
-        const int64_t item = (int64_t(blockIdx.x) * kNodeItems + it) * 256 + threadIdx.x;
+    for (int it = 0; it < d.node_items; ++it) {
+        const int64_t item = (int64_t(blockIdx.x) * d.node_items + it) * 256 + threadIdx.x;
         if (item >= total) break;
         nodes_item<T, COMPLETE>(grad_y, x, idx, d, st, sk, c, item, total, gconv, mom);
     }
@@ -1315,9 +1319,21 @@ int launch_tree_fwd_lds(const TreeDims& d, const TreeLds& g, int groups, int64_t
     return check_launch("cl_tree_conv_forward");
 }
 
-// Partial moment blocks per channel of the backward node pass: one per kNodeItems * 256 items.
-inline int64_t node_blocks(const TreeDims& d) {
-    return ceil_div(int64_t(d.n) * d.P, 256 * kNodeItems);
+// Partial moment blocks per channel of the backward node pass, and the items per thread: about
+// CL_TREE_NODE_WGS workgroups in all (more waves in flight than one block per channel gives
+// small planes), at most kNodeItems items per thread.
+inline int64_t node_blocks(const TreeDims& d, int* node_items = nullptr) {
+    const int64_t total = int64_t(d.n) * d.P;
+    const int64_t per_item_round = 256;
+    int64_t nblk = std::max<int64_t>(1, ceil_div(int64_t(CL_TREE_NODE_WGS), int64_t(d.cout)));
+    nblk = std::min(nblk, std::max<int64_t>(1, ceil_div(total, per_item_round)));
+    int64_t items = ceil_div(total, nblk * per_item_round);
+    if (items > kNodeItems) {
+        items = kNodeItems;
+        nblk = ceil_div(total, per_item_round * kNodeItems);
+    }
+    if (node_items) *node_items = int(std::max<int64_t>(1, items));
+    return nblk;
 }
 
 template <typename T>
@@ -1465,7 +1481,7 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
         CL_ARG(workspace && workspace_bytes >= need,
                "workspace of %lld bytes needed (see cl_tree_conv_workspace)", (long long)need);
         CL_ARG(aligned(workspace, 256), "workspace must be 256-byte aligned");
-        const int64_t nblk = node_blocks(d);
+        const int64_t nblk = node_blocks(d, &d.node_items);
         unsigned char* ws = static_cast<unsigned char*>(workspace);
         T* gconv = nullptr;
         int64_t off = 0;
