@@ -47,7 +47,7 @@ SIGNATURES: dict[str, list] = {
     "cl_tree_conv_forward": [_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int, _int,
                              _int, _int, _int, _int, _p, _p, _p, _p, _p],
     "cl_tree_conv_workspace": [_int, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int,
-                               _int, _int, _p],
+                               _int, _int, _int, _p],
     "cl_tree_conv_backward": [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                               _int, _int, _int, _int, _int, _int, _int, _p, _p, _p, _i64, _p],
     "cl_tree_conv_forward_softmax": [_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int,

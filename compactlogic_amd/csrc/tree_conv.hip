@@ -37,7 +37,7 @@ constexpr int kMaxNodes = 7;
 constexpr int kGatherBatch = 4;  // channel uses whose loads the input-gradient gather overlaps
 constexpr int kNodeItems = 16;   // most items per thread of the backward node kernel
 #ifndef CL_TREE_NODE_WGS
-#define CL_TREE_NODE_WGS 1024     // workgroups the backward node kernel aims for
+#define CL_TREE_NODE_WGS 512      // workgroups the backward node kernel aims for
 #endif
 
 template <typename T>
@@ -672,11 +672,12 @@ __device__ __forceinline__ void gate_moments(const T* v, const T* gc, T* mom) {
 // complete block (recomputed at the window's winner), (sample, position) otherwise; adds its
 // node moments to mom[node * 4 + (gab, ga, gb, g)] and stores the four conv-gate gradients
 // when gconv is given (complete block).
-template <typename T, bool COMPLETE>
+template <typename T, bool COMPLETE, bool REC>
 __device__ __forceinline__ void nodes_item(const T* __restrict__ grad_y, const T* __restrict__ x,
                                            const int32_t* __restrict__ idx, const TreeDims& d,
                                            const TapOff* st, T (*sk)[4], int c, int64_t item,
-                                           int64_t total, T* __restrict__ gconv, T* mom) {
+                                           int64_t total, T* __restrict__ radd,
+                                           int32_t* __restrict__ rtgt, T* mom) {
     int n, p;
     if (total < (int64_t(1) << 31)) {  // uniform: 32-bit multiply-shift division
         n = int(fast_div(uint32_t(item), d.div_p));
@@ -697,9 +698,18 @@ __device__ __forceinline__ void nodes_item(const T* __restrict__ grad_y, const T
         eval_at<T, true>(xn, d, st, sk, wy, w0 - wy * d.wo, e);
         const T gy = live ? grad_y[y_at(d, n, c, p)] : T(0);
         node_grads<T>(sk, e.g, e.t, gy, gc, mom);
-        if (gconv) {  // only the input gradient reads them
+        if constexpr (REC) {  // the input gradient's contribution of every tap: use (c, k), item
+            const int wx = w0 - wy * d.wo;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) gconv[(cell * d.P + p) * 4 + q] = gc[q];
+            for (int k = 0; k < kTaps; ++k) {
+                const int q = k >> 1;
+                const int iy = wy * d.sh + st[k].dy, ix = wx * d.sw + st[k].dx;
+                const bool ok = live && uint32_t(iy) < uint32_t(d.h) &&
+                                uint32_t(ix) < uint32_t(d.w) && uint32_t(st[k].ch) < uint32_t(d.cin);
+                const int64_t at = (int64_t(c) * kTaps + k) * total + item;
+                radd[at] = gc[q] * fma(sk[q][3], e.v[k ^ 1], (k & 1) ? sk[q][2] : sk[q][1]);
+                rtgt[at] = ok ? iy * d.w + ix : -1;
+            }
         }
     } else {
         const int oy = int(fast_div(uint32_t(p), d.div_wo));
@@ -711,18 +721,22 @@ __device__ __forceinline__ void nodes_item(const T* __restrict__ grad_y, const T
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward, node part: per item the upstream gradients of the four conv gates (gconv, complete
-// only; the conv-only block reads them from grad_y) and the node moments, reduced over the
-// workgroup's items into part[(c * nblk + blk) * NODES * 4 + q * 4 + m] with
-// m = (sum gy a b, sum gy a, sum gy b, sum gy).  The blk == 0 workgroup of each channel also
-// stores the collapsed coefficients kc[c][q][:] for the gather kernel.
-template <typename T, bool COMPLETE>
+// Backward, node part: per item the upstream gradients of the four conv gates (complete; the
+// conv-only block reads them from grad_y) and the node moments, reduced over the workgroup's
+// items into part[(c * nblk + blk) * NODES * 4 + q * 4 + m] with
+// m = (sum gy a b, sum gy a, sum gy b, sum gy).  With REC (complete, input gradient wanted)
+// it also stores, per tap k of the channel and item, the tap's input-gradient contribution
+//     radd = gconv[q] * (k even ? K1 + K3 x_partner : K2 + K3 x_partner),  q = k / 2,
+// and the input-plane position it adds to (rtgt, -1 for none), both at (c * 8 + k) * items +
+// item, for k_tree_gather_rec.  The blk == 0 workgroup of each channel also stores the
+// collapsed coefficients kc[c][q][:] for the conv-only gather.
+template <typename T, bool COMPLETE, bool REC>
 __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y, const T* __restrict__ x,
                                                     const T* __restrict__ w_prob,
                                                     const int32_t* __restrict__ sel,
                                                     const int32_t* __restrict__ idx, TreeDims d,
-                                                    T* __restrict__ gconv, T* __restrict__ part,
-                                                    T* __restrict__ kc) {
+                                                    T* __restrict__ radd, int32_t* __restrict__ rtgt,
+                                                    T* __restrict__ part, T* __restrict__ kc) {
     constexpr int NODES = COMPLETE ? 7 : 4;
     constexpr int NM = NODES * 4;
     __shared__ T sk[kMaxNodes][4];
@@ -744,7 +758,7 @@ __global__ __launch_bounds__(256) void k_tree_nodes(const T* __restrict__ grad_y
     for (int it = 0; it < d.node_items; ++it) {
         const int64_t item = (int64_t(blockIdx.x) * d.node_items + it) * 256 + threadIdx.x;
         if (item >= total) break;
-        nodes_item<T, COMPLETE>(grad_y, x, idx, d, st, sk, c, item, total, gconv, mom);
+        nodes_item<T, COMPLETE, REC>(grad_y, x, idx, d, st, sk, c, item, total, radd, rtgt, mom);
     }
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
@@ -852,6 +866,81 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
 #pragma unroll
                 for (int i = 0; i < kGatherBatch; ++i)
                     if (tgt[i] >= 0) atomicAdd(&gxs[(ch - ch0) * hw + tgt[i]], add[i]);
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t plane = int64_t(d.h) * d.w;
+    for (int i = threadIdx.x; i < spw * nch * hw; i += 256) {
+        const int si = i / (nch * hw), r = i % (nch * hw);
+        const int chl = r / hw, rr = r - chl * hw;
+        if (n0 + si < d.n)
+            grad_x[(int64_t(n0 + si) * d.cin + ch0 + chl) * plane + int64_t(y0) * d.w + rr] = gx[i];
+    }
+}
+
+// Backward, input gradient of the complete block from the node pass's contributions: the
+// workgroup and lane-group layout of k_tree_gather, but a use (c, k) at item (n, p) needs only
+// its contribution and target (radd / rtgt at (c * 8 + k) * items + n * P + p), loaded for a
+// batch of kRecBatch uses at once; the additions are applied in use order, as there.
+constexpr int kRecBatch = 8;
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_tree_gather_rec(const T* __restrict__ radd,
+                                                         const int32_t* __restrict__ rtgt,
+                                                         const int32_t* __restrict__ ent_ptr,
+                                                         const int32_t* __restrict__ ent,
+                                                         TreeDims d, int cg, int pw_lanes,
+                                                         int spw, int band_rows,
+                                                         T* __restrict__ grad_x) {
+    extern __shared__ unsigned char smem_raw[];
+    T* gx = reinterpret_cast<T*>(smem_raw);  // [spw][cg][band rows * w]
+    const int n0 = blockIdx.x * spw;
+    const int ch0 = blockIdx.y * cg;
+    const int nch = min(cg, d.cin - ch0);
+    const int y0 = blockIdx.z * band_rows, y1 = min(d.h, y0 + band_rows);
+    const int hw = (y1 - y0) * d.w, base_pos = y0 * d.w;
+    for (int i = threadIdx.x; i < spw * nch * hw; i += 256) gx[i] = T(0);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int PW = pw_lanes;
+    const int GL = PW * spw;
+    const int groups_per_wave = 64 / GL;
+    const int sub = lane / GL, gl = lane % GL, sl = gl / PW, pl = gl % PW;
+    const int n = n0 + sl;
+    const bool n_ok = n < d.n;
+    const int64_t total = int64_t(d.n) * d.P;
+    const int64_t nrow = int64_t(n_ok ? n : 0) * d.P;
+    T* gxs = gx + sl * nch * hw;
+    for (int base = 0; base < nch; base += 4 * groups_per_wave) {
+        const int chl = base + wv * groups_per_wave + sub;
+        const bool have = chl < nch;
+        const int ch = ch0 + chl;
+        const int e0 = have ? ent_ptr[ch] : 0, e1 = have ? ent_ptr[ch + 1] : 0;
+        int cnt = e1 - e0;
+        for (int off = 32; off > 0; off >>= 1) cnt = max(cnt, __shfl_xor(cnt, off, 64));
+        for (int j = 0; j < cnt; j += kRecBatch) {
+            bool on[kRecBatch];
+            int64_t urow[kRecBatch];
+#pragma unroll
+            for (int i = 0; i < kRecBatch; ++i) {
+                on[i] = n_ok && j + i < e1 - e0;
+                urow[i] = int64_t(on[i] ? ent[e0 + j + i] : 0) * total + nrow;
+            }
+            for (int p = pl; p < d.P; p += PW) {
+                int32_t tg[kRecBatch];
+                T ad[kRecBatch];
+#pragma unroll
+                for (int i = 0; i < kRecBatch; ++i) {
+                    tg[i] = rtgt[urow[i] + p];
+                    ad[i] = radd[urow[i] + p];
+                }
+#pragma unroll
+                for (int i = 0; i < kRecBatch; ++i) {
+                    const int rel = tg[i] - base_pos;
+                    if (on[i] && tg[i] >= 0 && rel >= 0 && rel < hw)
+                        atomicAdd(&gxs[(ch - ch0) * hw + rel], ad[i]);
+                }
             }
         }
     }
@@ -1336,12 +1425,20 @@ inline int64_t node_blocks(const TreeDims& d, int* node_items = nullptr) {
     return nblk;
 }
 
+// The complete block's input-gradient contributions: radd (T) then rtgt (int32), one of each
+// per (channel, tap, item).
+inline int64_t tree_records(const TreeDims& d) { return int64_t(d.cout) * kTaps * d.n * d.P; }
+
 template <typename T>
-int64_t tree_workspace_bytes(const TreeDims& d) {
+int64_t tree_workspace_bytes(const TreeDims& d, bool grad_x) {
     const int nodes = d.complete ? 7 : 4;
     const int64_t nblk = node_blocks(d);
     int64_t b = 0;
-    if (d.complete) b += int64_t(d.n) * d.cout * d.P * 4 * sizeof(T);  // gconv
+    if (d.complete && grad_x) {
+        b += tree_records(d) * int64_t(sizeof(T));
+        b = (b + 255) / 256 * 256;
+        b += tree_records(d) * 4;
+    }
     b = (b + 255) / 256 * 256;
     b += int64_t(d.cout) * nblk * nodes * 4 * sizeof(T);  // partial moments
     b = (b + 255) / 256 * 256;
@@ -1434,14 +1531,14 @@ extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void
 extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,
                                       int64_t c_out, int stride_h, int stride_w, int pad_h,
                                       int pad_w, int kernel_h, int kernel_w, int complete,
-                                      int64_t* bytes) {
+                                      int grad_x, int64_t* bytes) {
     clear_error();
     CL_ARG(bytes, "null pointer argument");
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
-    CL_DTYPE_SWITCH(dtype, { *bytes = tree_workspace_bytes<scalar_t>(d); });
+    CL_DTYPE_SWITCH(dtype, { *bytes = tree_workspace_bytes<scalar_t>(d, grad_x != 0); });
     return CL_OK;
 }
 
@@ -1477,17 +1574,20 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
         CL_ARG(grad_y && x && w_prob && selection, "null pointer argument");
         CL_ARG(!complete || indices, "the complete block's backward needs the pooling indices");
         CL_ARG(!grad_x || (ent_ptr && ent), "the input gradient needs the channel use index");
-        const int64_t need = tree_workspace_bytes<T>(d);
+        const int64_t need = tree_workspace_bytes<T>(d, grad_x != nullptr);
         CL_ARG(workspace && workspace_bytes >= need,
                "workspace of %lld bytes needed (see cl_tree_conv_workspace)", (long long)need);
         CL_ARG(aligned(workspace, 256), "workspace must be 256-byte aligned");
         const int64_t nblk = node_blocks(d, &d.node_items);
         unsigned char* ws = static_cast<unsigned char*>(workspace);
-        T* gconv = nullptr;
+        T* radd = nullptr;
+        int32_t* rtgt = nullptr;
         int64_t off = 0;
-        if (complete) {
-            gconv = reinterpret_cast<T*>(ws);
-            off = int64_t(d.n) * d.cout * d.P * 4 * sizeof(T);
+        if (complete && grad_x) {
+            radd = reinterpret_cast<T*>(ws);
+            off = (tree_records(d) * int64_t(sizeof(T)) + 255) / 256 * 256;
+            rtgt = reinterpret_cast<int32_t*>(ws + off);
+            off += tree_records(d) * 4;
         }
         off = (off + 255) / 256 * 256;
         T* part = reinterpret_cast<T*>(ws + off);
@@ -1498,13 +1598,15 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
         const T* gy = static_cast<const T*>(grad_y);
         const T* xs = static_cast<const T*>(x);
         const T* wp = static_cast<const T*>(w_prob);
-        T* gcv = (complete && grad_x) ? gconv : nullptr;
-        if (complete)
-            k_tree_nodes<T, true><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gcv,
-                                                       part, kc);
+        if (complete && radd)
+            k_tree_nodes<T, true, true><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d,
+                                                             radd, rtgt, part, kc);
+        else if (complete)
+            k_tree_nodes<T, true, false><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d,
+                                                              nullptr, nullptr, part, kc);
         else
-            k_tree_nodes<T, false><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d, gconv,
-                                                        part, kc);
+            k_tree_nodes<T, false, false><<<grid, 256, 0, s>>>(gy, xs, wp, selection, indices, d,
+                                                               nullptr, nullptr, part, kc);
         if (int rc = check_launch("cl_tree_conv_backward(nodes)")) return rc;
         if (grad_w) {
             k_tree_finalize<T><<<unsigned(ceil_div(int64_t(d.cout) * nodes * 16, 256)), 256, 0, s>>>(
@@ -1534,13 +1636,12 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
                           unsigned(nbands));
             CL_ARG(nbands < 65536, "input planes too tall for the input gradient");
             const size_t lds = size_t(spw) * size_t(cg) * size_t(hw_bytes);
-            const T* src = complete ? gconv : gy;
             if (complete)
-                k_tree_gather<T, true><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
-                                                            ent, kc, d, cg, pw_lanes, spw,
-                                                            band_rows, static_cast<T*>(grad_x));
+                k_tree_gather_rec<T><<<g2, 256, lds, s>>>(radd, rtgt, ent_ptr, ent, d, cg,
+                                                          pw_lanes, spw, band_rows,
+                                                          static_cast<T*>(grad_x));
             else
-                k_tree_gather<T, false><<<g2, 256, lds, s>>>(src, xs, selection, indices, ent_ptr,
+                k_tree_gather<T, false><<<g2, 256, lds, s>>>(gy, xs, selection, indices, ent_ptr,
                                                              ent, kc, d, cg, pw_lanes, spw,
                                                              band_rows, static_cast<T*>(grad_x));
             if (int rc = check_launch("cl_tree_conv_backward(gather)")) return rc;

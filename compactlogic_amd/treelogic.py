@@ -190,7 +190,7 @@ def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w
     code = _dl.dtype_code(x)
     need = ctypes.c_int64(0)
     _capi.call("cl_tree_conv_workspace", code, n, c_in, h, w, c_out, stride_h, stride_w, pad_h,
-               pad_w, kernel_h, kernel_w, int(complete), ctypes.byref(need))
+               pad_w, kernel_h, kernel_w, int(complete), int(gx is not None), ctypes.byref(need))
     ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
     with torch.cuda.device(x.device):
         timing.timed(f"cl_tree_conv_backward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(

@@ -560,10 +560,12 @@ int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob, const int
                          int kernel_w, int complete, void* y, void* x2, void* x3,
                          int32_t* indices, void* stream);
 
-/* Workspace bytes of cl_tree_conv_backward for this shape. */
+/* Workspace bytes of cl_tree_conv_backward for this shape; grad_x != 0 when the backward will
+ * be asked for the input gradient (the complete block then keeps every tap's contribution,
+ * (element size + 4) * c_out * 8 * n * pooled windows bytes more). */
 int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,
                            int64_t c_out, int stride_h, int stride_w, int pad_h, int pad_w,
-                           int kernel_h, int kernel_w, int complete, int64_t* bytes);
+                           int kernel_h, int kernel_w, int complete, int grad_x, int64_t* bytes);
 
 /* Replaces full_convlogic_backward_x + full_convlogic_backward_weight
  * (full_convlogic_kernel.cu:332-430, :580-701) and convlogic_backward_x +
