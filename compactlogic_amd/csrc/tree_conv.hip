@@ -883,7 +883,10 @@ __global__ __launch_bounds__(256) void k_tree_gather(const T* __restrict__ gsrc,
 // workgroup and lane-group layout of k_tree_gather, but a use (c, k) at item (n, p) needs only
 // its contribution and target (radd / rtgt at (c * 8 + k) * items + n * P + p), loaded for a
 // batch of kRecBatch uses at once; the additions are applied in use order, as there.
-constexpr int kRecBatch = 8;
+#ifndef CL_TREE_REC_BATCH
+#define CL_TREE_REC_BATCH 8
+#endif
+constexpr int kRecBatch = CL_TREE_REC_BATCH;
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_tree_gather_rec(const T* __restrict__ radd,
@@ -909,8 +912,9 @@ __global__ __launch_bounds__(256) void k_tree_gather_rec(const T* __restrict__ r
     const int sub = lane / GL, gl = lane % GL, sl = gl / PW, pl = gl % PW;
     const int n = n0 + sl;
     const bool n_ok = n < d.n;
-    const int64_t total = int64_t(d.n) * d.P;
-    const int64_t nrow = int64_t(n_ok ? n : 0) * d.P;
+    // record indices fit 32 bits (checked by the host)
+    const uint32_t total = uint32_t(d.n) * uint32_t(d.P);
+    const uint32_t nrow = uint32_t(n_ok ? n : 0) * uint32_t(d.P);
     T* gxs = gx + sl * nch * hw;
     for (int base = 0; base < nch; base += 4 * groups_per_wave) {
         const int chl = base + wv * groups_per_wave + sub;
@@ -921,11 +925,11 @@ __global__ __launch_bounds__(256) void k_tree_gather_rec(const T* __restrict__ r
         for (int off = 32; off > 0; off >>= 1) cnt = max(cnt, __shfl_xor(cnt, off, 64));
         for (int j = 0; j < cnt; j += kRecBatch) {
             bool on[kRecBatch];
-            int64_t urow[kRecBatch];
+            uint32_t urow[kRecBatch];
 #pragma unroll
             for (int i = 0; i < kRecBatch; ++i) {
                 on[i] = n_ok && j + i < e1 - e0;
-                urow[i] = int64_t(on[i] ? ent[e0 + j + i] : 0) * total + nrow;
+                urow[i] = uint32_t(on[i] ? ent[e0 + j + i] : 0) * total + nrow;
             }
             for (int p = pl; p < d.P; p += PW) {
                 int32_t tg[kRecBatch];
@@ -1636,6 +1640,8 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
                           unsigned(nbands));
             CL_ARG(nbands < 65536, "input planes too tall for the input gradient");
             const size_t lds = size_t(spw) * size_t(cg) * size_t(hw_bytes);
+            CL_ARG(!complete || tree_records(d) < (int64_t(1) << 32),
+                   "too many tap contributions for the input gradient");
             if (complete)
                 k_tree_gather_rec<T><<<g2, 256, lds, s>>>(radd, rtgt, ent_ptr, ent, d, cg,
                                                           pw_lanes, spw, band_rows,
