@@ -389,6 +389,16 @@ def roofline_of(kernels: dict, how: str) -> dict:
         out["in_step_event_ms"] = round(d["seconds"] * 1e3, 4)
         out["in_step_note"] = ("events around each single launch inside the eager steps; "
                                "they include the two event packets")
+    # the same launch against the VALU issue rate, where the counter profile has it (the conv
+    # and tree kernels are VALU-bound, not HBM-bound)
+    prof = valu_profile().get(name)
+    if prof:
+        valu = prof["valu_wave_instructions"] / sec / 1e9
+        out["valu"] = {"achieved": round(valu, 1), "peak": VALU_PEAK_G,
+                       "unit": "G wave64 VALU instructions/s", "frac": round(valu / VALU_PEAK_G, 4),
+                       "valu_wave_instructions_per_launch": prof["valu_wave_instructions"],
+                       "valu_busy_counter": prof.get("valu_busy"),
+                       "kernels": prof["kernel"]}
     return out
 
 
