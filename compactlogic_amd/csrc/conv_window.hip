@@ -108,21 +108,25 @@ struct WinDims {
 };
 
 // ------------------------------------------------------------------------------------------
-// Block = BS threads over the output positions of sample n and input channel ch
-// (blockIdx.x = (n * Cin + ch) * pchunks + chunk).
-template <typename T, int KW>
+// Block = BS threads over the output positions of sample n and input channel ch, and part
+// `part` of split equal parts of the channel's output channels
+// (blockIdx.x = ((n * Cin + ch) * pchunks + chunk) * split + part).
+template <typename T, int KW, int SPLIT>
 __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const T* __restrict__ coef,
                                                  const int32_t* __restrict__ grp_ptr,
                                                  const int32_t* __restrict__ chan_order,
                                                  T* __restrict__ y, int pchunks, WinDims d) {
     constexpr int P = Win<KW>::P, CW = Win<KW>::CW;
-    const int64_t blk = blockIdx.x;
+    const int64_t blk = blockIdx.x / SPLIT;
+    const int part = int(blockIdx.x % SPLIT);
     const int chunk = int(blk % pchunks);
     const int64_t nc = blk / pchunks;
     const int64_t ch = nc % d.Cin, n = nc / d.Cin;
     const int hw = d.Ho * d.Wo;
     const int pos = chunk * int(blockDim.x) + int(threadIdx.x);
-    const int c0 = grp_ptr[ch], c1 = grp_ptr[ch + 1];
+    const int g0 = grp_ptr[ch], g1 = grp_ptr[ch + 1];
+    const int c0 = g0 + (g1 - g0) * part / SPLIT;
+    const int c1 = g0 + (g1 - g0) * (part + 1) / SPLIT;
     if (c0 == c1 || pos >= hw) return;
     const int oy = pos / d.Wo, ox = pos - oy * d.Wo;
     T v[P];
@@ -865,13 +869,21 @@ extern "C" int cl_conv_window_forward(int dtype, const void* x, const void* coef
     const int hw = d.Ho * d.Wo;
     const int bs = block_for(hw, 256);
     const int64_t pchunks = ceil_div(hw, bs);
-    const int64_t blocks = N * Cin * pchunks;
+    // wide channel groups (many output channels per input channel on average) are split over
+    // two blocks of threads: twice the waves for the same window loads per channel
+    const int split = Cout >= 8 * Cin ? 2 : 1;
+    const int64_t blocks = N * Cin * pchunks * split;
     CL_ARG(blocks < (int64_t(1) << 32), "conv layer too large for one launch");
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
-            k_win_fwd<scalar_t, decltype(K)::value><<<unsigned(blocks), bs, 0, as_stream(stream)>>>(
-                static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(coef), grp_ptr,
-                chan_order, static_cast<scalar_t*>(y), int(pchunks), d);
+            auto go = [&](auto sc) {
+                k_win_fwd<scalar_t, decltype(K)::value, decltype(sc)::value>
+                    <<<unsigned(blocks), bs, 0, as_stream(stream)>>>(
+                    static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(coef), grp_ptr,
+                    chan_order, static_cast<scalar_t*>(y), int(pchunks), d);
+            };
+            if (split == 2) go(std::integral_constant<int, 2>{});
+            else go(std::integral_constant<int, 1>{});
             return CL_OK;
         });
         if (rc) return rc;
