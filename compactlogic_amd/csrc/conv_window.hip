@@ -111,7 +111,11 @@ struct WinDims {
 // Block = BS threads over the output positions of sample n and input channel ch, and part
 // `part` of split equal parts of the channel's output channels
 // (blockIdx.x = ((n * Cin + ch) * pchunks + chunk) * split + part).
-template <typename T, int KW, int SPLIT>
+//
+// PACK (small planes): a block of 256 threads takes spb = 256 / hw samples of input channel ch
+// instead (blockIdx.x = ((n / spb) * Cin + ch) * split + part; thread t: sample t / hw, position
+// t % hw), so that few lanes idle; pchunks is then spb.
+template <typename T, int KW, int SPLIT, bool PACK>
 __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const T* __restrict__ coef,
                                                  const int32_t* __restrict__ grp_ptr,
                                                  const int32_t* __restrict__ chan_order,
@@ -119,11 +123,22 @@ __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const 
     constexpr int P = Win<KW>::P, CW = Win<KW>::CW;
     const int64_t blk = blockIdx.x / SPLIT;
     const int part = int(blockIdx.x % SPLIT);
-    const int chunk = int(blk % pchunks);
-    const int64_t nc = blk / pchunks;
-    const int64_t ch = nc % d.Cin, n = nc / d.Cin;
     const int hw = d.Ho * d.Wo;
-    const int pos = chunk * int(blockDim.x) + int(threadIdx.x);
+    int64_t ch, n;
+    int pos;
+    if constexpr (PACK) {
+        ch = blk % d.Cin;
+        const int s = int(threadIdx.x) / hw;
+        pos = int(threadIdx.x) - s * hw;
+        n = (blk / d.Cin) * pchunks + s;
+        if (s >= pchunks || n >= d.N) return;
+    } else {
+        const int chunk = int(blk % pchunks);
+        const int64_t nc = blk / pchunks;
+        ch = nc % d.Cin;
+        n = nc / d.Cin;
+        pos = chunk * int(blockDim.x) + int(threadIdx.x);
+    }
     const int g0 = grp_ptr[ch], g1 = grp_ptr[ch + 1];
     const int c0 = g0 + (g1 - g0) * part / SPLIT;
     const int c1 = g0 + (g1 - g0) * (part + 1) / SPLIT;
@@ -868,22 +883,32 @@ extern "C" int cl_conv_window_forward(int dtype, const void* x, const void* coef
     CL_ARG(x && coef && grp_ptr && chan_order && y, "null pointer argument");
     const int hw = d.Ho * d.Wo;
     const int bs = block_for(hw, 256);
-    const int64_t pchunks = ceil_div(hw, bs);
+    // planes of at most 128 positions that would leave more than a tenth of a block idle take
+    // several samples per 256-thread block
+    const bool pack = hw <= 128 && (bs - hw) * 10 > bs;
+    const int64_t pchunks = pack ? 256 / hw : ceil_div(hw, bs);
     // wide channel groups (many output channels per input channel on average) are split over
     // two blocks of threads: twice the waves for the same window loads per channel
     const int split = Cout >= 8 * Cin ? 2 : 1;
-    const int64_t blocks = N * Cin * pchunks * split;
+    const int64_t blocks = (pack ? ceil_div(N, pchunks) : N * pchunks) * Cin * split;
     CL_ARG(blocks < (int64_t(1) << 32), "conv layer too large for one launch");
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
-            auto go = [&](auto sc) {
-                k_win_fwd<scalar_t, decltype(K)::value, decltype(sc)::value>
-                    <<<unsigned(blocks), bs, 0, as_stream(stream)>>>(
+            auto go = [&](auto sc, auto pc) {
+                k_win_fwd<scalar_t, decltype(K)::value, decltype(sc)::value, decltype(pc)::value>
+                    <<<unsigned(blocks), pack ? 256 : bs, 0, as_stream(stream)>>>(
                     static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(coef), grp_ptr,
                     chan_order, static_cast<scalar_t*>(y), int(pchunks), d);
             };
-            if (split == 2) go(std::integral_constant<int, 2>{});
-            else go(std::integral_constant<int, 1>{});
+            using S1 = std::integral_constant<int, 1>;
+            using S2 = std::integral_constant<int, 2>;
+            if (pack) {
+                if (split == 2) go(S2{}, std::true_type{});
+                else go(S1{}, std::true_type{});
+            } else {
+                if (split == 2) go(S2{}, std::false_type{});
+                else go(S1{}, std::false_type{});
+            }
             return CL_OK;
         });
         if (rc) return rc;
