@@ -389,16 +389,20 @@ def roofline_of(kernels: dict, how: str) -> dict:
         out["in_step_event_ms"] = round(d["seconds"] * 1e3, 4)
         out["in_step_note"] = ("events around each single launch inside the eager steps; "
                                "they include the two event packets")
-    # the same launch against the VALU issue rate, where the counter profile has it (the conv
-    # and tree kernels are VALU-bound, not HBM-bound)
+    # the same launch against the VALU, where the counter profile has it (the conv and tree
+    # kernels are VALU-bound, not HBM-bound): frac is the counters' VALU busy (issue cycles
+    # over elapsed cycles); the instruction rate over the nominal four-cycles-per-instruction
+    # peak is beside it, and it can pass 1 where instructions take fewer cycles
     prof = valu_profile().get(name)
     if prof:
         valu = prof["valu_wave_instructions"] / sec / 1e9
-        out["valu"] = {"achieved": round(valu, 1), "peak": VALU_PEAK_G,
-                       "unit": "G wave64 VALU instructions/s", "frac": round(valu / VALU_PEAK_G, 4),
+        out["valu"] = {"frac": prof.get("valu_busy"), "achieved": round(valu, 1),
+                       "peak": VALU_PEAK_G, "unit": "G wave64 VALU instructions/s",
+                       "issue_frac": round(valu / VALU_PEAK_G, 4),
                        "valu_wave_instructions_per_launch": prof["valu_wave_instructions"],
-                       "valu_busy_counter": prof.get("valu_busy"),
-                       "kernels": prof["kernel"]}
+                       "kernels": prof["kernel"],
+                       "source": "profiles/valu_per_launch.json (rocprofv3 --pmc SQ_INSTS_VALU "
+                                 "SQ_ACTIVE_INST_VALU GRBM_GUI_ACTIVE of this command)"}
     return out
 
 
