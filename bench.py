@@ -22,7 +22,8 @@ Also reported on the same JSON line:
                 layer-by-layer bitwise evaluation + popcount GroupSum, with its own roofline
                 and CPU (C oracle) baseline
   packed_conv   cfg5: the cfg3 network with 4 candidate gates per row, frozen, 2^20
-                bit-packed samples
+                bit-packed samples; its "fused" member writes conv2's output column-major and
+                runs the two dense layers and the counts in one launch
   packed_conv_tree  the cfg3_tree network frozen to argmax gates (pool = OR), 2^20 bit-packed
                 samples; its "fused" member runs the two dense layers and the counts in one
                 launch after the conv blocks
@@ -613,18 +614,23 @@ def bench_packed_fused(model, in_features: int, log2n: int, passes: int, checksu
     from compactlogic_amd import timing
     with timing.record() as rec:
         net(x)
-    fused_call = next((v for k, v in rec.summary().items() if k.startswith("cl_packed_network")),
-                      None)
+    calls = rec.summary()
+    fused_call = next((v for k, v in calls.items() if k.startswith("cl_packed_network")), None)
     fused_rows = net.rows or []
     prefix = len(net.prefix)
+    producer = net.producer is not None
     del xw, counts, net
     torch.cuda.empty_cache()
     out = {"workload": ("the same network and inputs through PackedNetwork: "
                         + (f"{prefix} modules layer by layer, then " if prefix else "")
+                        + ("the layer before the dense tail written column-major, then "
+                           if producer else "")
                         + f"the dense layers {fused_rows} and the class counts in one launch, "
                           "32-sample columns held in LDS through all fused layers"),
            "value": round(n / dt / 1e9, 4), "unit": "Gsamples/s", "ms_per_pass": round(dt * 1e3, 3),
-           "counts_match_layerwise": same, "speedup_vs_layerwise": None}
+           "counts_match_layerwise": same, "speedup_vs_layerwise": None,
+           "kernels": {k: {"ms": round(v["mean_ms"], 4), "calls_per_step": v["calls"]}
+                       for k, v in calls.items()}}
     if not prefix:
         fused_bytes = in_features // 8 + 4 * model[-1].k
         out["fused_compulsory_bytes_per_sample"] = fused_bytes
@@ -830,14 +836,23 @@ def main():
             c5 = configs.CONV_CONFIGS["cfg5"]
             model = configs.conv_network(c5, device=torch.device("cuda:0"))
             configs.freeze_argmax(model)
-            pk = bench_packed_net(model, c5.in_shape[0] * c5.in_shape[1] * c5.in_shape[2],
-                                  args.conv_packed_log2_samples, args.packed_passes, c5.k, torch)
+            feats5 = c5.in_shape[0] * c5.in_shape[1] * c5.in_shape[2]
+            pk = bench_packed_net(model, feats5, args.conv_packed_log2_samples,
+                                  args.packed_passes, c5.k, torch)
             del model
             pc = packed_json(pk, f"cfg5: cfg3 network with 4 candidate gates per row, frozen "
                                  f"to argmax, 2^{args.conv_packed_log2_samples} samples bit-packed "
                                  "64 per word, 2 packed conv + 2 dense layers + popcount GroupSum",
                              CFG5_BYTES_PER_SAMPLE)
-            log(f"packed cfg5: {pc['value']} Gsamples/s")
+            model = configs.conv_network(c5, device=torch.device("cuda:0"))
+            configs.freeze_argmax(model)
+            fc = bench_packed_fused(model, feats5, args.conv_packed_log2_samples,
+                                    args.packed_passes, pc["counts_checksum"], torch, key="cfg5")
+            del model
+            fc["speedup_vs_layerwise"] = round(fc["value"] / pc["value"], 2)
+            pc["fused"] = fc
+            log(f"packed cfg5: {pc['value']} Gsamples/s layer by layer, "
+                f"{fc['value']} Gsamples/s with the dense tail fused")
             if not args.no_cpu_baseline:
                 log("cpu baseline (cfg5)")
                 pc["cpu_baseline"] = cpu_baseline_packed(torch, "cfg5")

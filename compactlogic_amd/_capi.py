@@ -117,6 +117,12 @@ SIGNATURES: dict[str, list] = {
     "cl_fill_splitmix64": [_p, _i64, _u64, _p],
     "cl_packed_network_limits": [ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
     "cl_packed_network": [_p, _i64, _i64, _p, ctypes.POINTER(_i64), _i64, _i64, _p, _p],
+    "cl_packed_network_columns_layout": [ctypes.POINTER(_i64), _i64, ctypes.POINTER(_i64),
+                                         ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                         ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
+    "cl_eval_packed_indexed_columns": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "cl_packed_network_columns": [_p, _i64, _i64, _i64, _p, ctypes.POINTER(_i64), _i64, _i64,
+                                  _p, _p],
 }
 
 _lib = None

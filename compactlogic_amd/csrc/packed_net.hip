@@ -203,12 +203,11 @@ __device__ __forceinline__ uint32_t full_add(uint32_t& a, uint32_t x, uint32_t y
 // plane over the half-wave's 32 lanes for sample j.  The two half-waves' sums are added.
 // Integer sums: exact and independent of the order.
 template <int B>
-__device__ __forceinline__ void column_counts_wave(const uint32_t* last, const PackedNet& net,
+__device__ __forceinline__ void column_counts_wave(const uint32_t* last, int gs, int k,
                                                    int64_t col, int64_t nsamples,
                                                    int32_t* __restrict__ counts) {
     const int lane = threadIdx.x & 63;
-    const int gs = net.rows[net.num_layers] / net.k;
-    for (int c = wave_id(); c < net.k; c += kNetThreads / 64) {  // uniform per wave
+    for (int c = wave_id(); c < k; c += kNetThreads / 64) {  // uniform per wave
         uint32_t a[B];
 #pragma unroll
         for (int i = 0; i < B; ++i) a[i] = 0;
@@ -237,7 +236,7 @@ __device__ __forceinline__ void column_counts_wave(const uint32_t* last, const P
         n += __shfl_xor(n, 32, 64);  // the other half-wave's rows
         if (lane < 32) {
             const int64_t sample = col * 32 + lane;
-            if (sample < nsamples) counts[sample * net.k + c] = n;
+            if (sample < nsamples) counts[sample * k + c] = n;
         }
     }
 }
@@ -372,9 +371,279 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net_slots(
             }
         }
         // the last layer's rows are in buffer L % 2
-        column_counts_wave<B>(lds + (L & 1) * buf_words, net, col, nsamples, counts);
+        column_counts_wave<B>(lds + (L & 1) * buf_words, net.rows[L] / net.k, net.k, col,
+                              nsamples, counts);
         __syncthreads();  // the next column overwrites both buffers
     }
+}
+
+// ------------------------------------------------------------------------------------------
+// Wide-input fused pass.  An input wider than four rows per thread comes column-major: the
+// words of column c are x[c * in_words + r] for rows r < in_words (k_eval_packed_cols writes
+// this layout), so a workgroup loads its column with coalesced 16-byte loads however many
+// rows the input has, where the row-major layout would pull a cache line per row for 4 bytes.
+// LDS holds the column at words [0, in_words).  The first layer writes its slots
+// j < J - HOLD to base[0] + tid + 1024 j, after the input, and keeps its last HOLD slots in
+// registers until every thread has read the input; they then go to hold_base + 1024 h + tid,
+// over the input.  Later layers write to base[l] + tid + 1024 j.  Gate entries hold absolute
+// LDS word addresses (16 bits each), so the host can place each layer's rows anywhere in the
+// 160 KiB (cols_plan) and builds the entries to match; the input's LDS words cannot hold
+// both it and a full first layer when the input passes 24576 rows.
+constexpr int kLdsWords = 40960;  // 160 KiB of LDS per workgroup
+
+// Layers the gate-entry registers hold: 2 of 16 slots or 3 of 8 (with the input loads in
+// flight beside them, more entries spill).
+constexpr int cols_max_layers(int J) { return J == 16 ? 2 : 3; }
+
+struct PackedNetCols {
+    int num_layers;
+    int k;
+    int rows[kNetMaxLayers + 1];
+    int64_t table_off[kNetMaxLayers];
+    int base[kNetMaxLayers];  // LDS word of layer l's slot 0 (layer 0: its unheld slots)
+    int hold_base;            // LDS word of layer 0's first held slot
+    int in_words;             // words per input column, a multiple of 64
+};
+
+// 16-byte loads per thread that stage the widest input a plan with J - HOLD unheld
+// first-layer slots admits
+template <int J, int HOLD>
+constexpr int cols_in_loads() {
+    return (kLdsWords - kNetThreads * (J - HOLD) + 4 * kNetThreads - 1) / (4 * kNetThreads);
+}
+
+// Persistent like k_packed_net_slots (columns of one XCD contiguous, gate entries and opcodes
+// in registers, the next column's input loaded while the current one is evaluated).  Entry
+// register: LDS word of row a | that of row b << 16; opcodes as nibbles.
+template <int B, int J, int HOLD>
+__global__ __launch_bounds__(kNetThreads) void k_packed_net_cols(
+    const uint4* __restrict__ x, int64_t cols, int64_t nsamples,
+    const uint64_t* __restrict__ tables, PackedNetCols net, int32_t* __restrict__ counts) {
+    constexpr int LMAX = cols_max_layers(J);
+    constexpr int TG = LMAX * J;
+    constexpr int OW = (TG + 7) / 8;
+    constexpr int JB = J - HOLD;
+    constexpr int IPT = cols_in_loads<J, HOLD>();
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int tid = threadIdx.x;
+    const int L = net.num_layers;
+    uint32_t ent[TG];
+    uint32_t ops[OW];
+#pragma unroll
+    for (int i = 0; i < OW; ++i) ops[i] = 0;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) {
+        // no gate in this slot: entry 0 reads word 0 and writes a row no later step reads
+        const int l = q / J, o = tid + kNetThreads * (q % J);
+        uint64_t e = 0;
+        if (l < L && o < net.rows[l + 1]) e = tables[net.table_off[l] + o];
+        ent[q] = uint32_t(e);
+        ops[q / 8] |= (uint32_t(e >> 32) & 15u) << (4 * (q % 8));
+    }
+    const int in4 = net.in_words / 4;
+    const int64_t per = (cols + 7) / 8;
+    const int64_t nb8 = gridDim.x / 8;
+    const int64_t c_first = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    const int64_t c_end = std::min(cols, (blockIdx.x % 8 + 1) * per);
+    uint4 in[IPT];
+    auto fetch = [&](int64_t c) {
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int i = tid + kNetThreads * j;
+            in[j] = (c < c_end && i < in4) ? x[c * in4 + i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    fetch(c_first);
+    for (int64_t col = c_first; col < c_end; col += nb8) {
+        uint4* l4 = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int i = tid + kNetThreads * j;
+            if (i < in4) l4[i] = in[j];
+        }
+        fetch(col + nb8);
+        __syncthreads();
+        // opaque per column, as in k_packed_net_slots: no per-gate values hoisted out of the
+        // column loop
+#pragma unroll
+        for (int i = 0; i < OW; ++i) asm volatile("" : "+v"(ops[i]));
+#pragma unroll
+        for (int q = 0; q < TG; ++q) asm volatile("" : "+v"(ent[q]));
+#pragma unroll
+        for (int l = 0; l < LMAX; ++l) {
+            if (l < L) {  // uniform
+                uint32_t* nxt = lds + net.base[l];
+                constexpr int NW = (J + 7) / 8 + 1;
+                const int wlo = (l * J) / 8;
+                uint32_t lw[NW];
+#pragma unroll
+                for (int i = 0; i < NW; ++i) lw[i] = ops[wlo + i < OW ? wlo + i : OW - 1];
+                uint32_t held[HOLD > 0 ? HOLD : 1];
+#pragma unroll
+                for (int j0 = 0; j0 < J; j0 += kBatch) {
+                    uint32_t va[kBatch], vb[kBatch];
+#pragma unroll
+                    for (int j = j0; j < j0 + kBatch && j < J; ++j) {
+                        const uint32_t e = ent[l * J + j];
+                        va[j - j0] = lds[e & 0xffffu];
+                        vb[j - j0] = lds[e >> 16];
+                    }
+#pragma unroll
+                    for (int j = j0; j < j0 + kBatch && j < J; ++j) {
+                        const int q = l * J + j;
+                        const uint32_t r = gate_word((lw[q / 8 - wlo] >> (4 * (q % 8))) & 15u,
+                                                     va[j - j0], vb[j - j0]);
+                        if (HOLD > 0 && l == 0 && j >= JB) held[HOLD > 0 ? j - JB : 0] = r;
+                        else nxt[tid + kNetThreads * j] = r;
+                    }
+                }
+                __syncthreads();
+                if constexpr (HOLD > 0) {
+                    if (l == 0) {  // every thread has read the input: its words are free
+#pragma unroll
+                        for (int h = 0; h < HOLD; ++h)
+                            lds[net.hold_base + kNetThreads * h + tid] = held[h];
+                        __syncthreads();
+                    }
+                }
+            }
+        }
+        column_counts_wave<B>(lds + net.base[L - 1], net.rows[L] / net.k, net.k, col,
+                              nsamples, counts);
+        __syncthreads();  // the next column overwrites the input words
+    }
+}
+
+// Packed layer from resolved index tables with column-major output (the input layout of
+// k_packed_net_cols): y[c * out_words + o] = word c of op_{g[o]}(x[ia[o], :], x[ib[o], :]),
+// a negative index reading zeros, 0 for an index past in_dim and for rows
+// out_dim <= o < out_words.  A workgroup takes 64 rows x 128 words: a wave evaluates 16 rows
+// (per operand and row two coalesced 4-byte loads of 64 words), the tile is transposed
+// through LDS (row stride 129 words: the column reads of a half-wave hit 32 banks), and each
+// wave then writes the 64-row runs of 32 words, 256 contiguous bytes each.
+constexpr int kColRows = 64;
+constexpr int kColWords = 128;
+
+__global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __restrict__ x,
+                                                          const int32_t* __restrict__ ia,
+                                                          const int32_t* __restrict__ ib,
+                                                          const uint8_t* __restrict__ gate,
+                                                          uint32_t* __restrict__ y,
+                                                          int64_t in_dim, int64_t out_dim,
+                                                          int64_t cols, int64_t out_words) {
+    __shared__ uint32_t tile[kColRows][kColWords + 1];
+    constexpr int R = kColRows / 4;  // rows per wave
+    constexpr int RB = 8;            // rows whose loads are in flight together
+    const int64_t o0 = int64_t(blockIdx.x) * kColRows, c0 = int64_t(blockIdx.y) * kColWords;
+    const int w = wave_id(), lane = lane_id();
+    const int64_t ca = c0 + lane, cb = c0 + 64 + lane;
+    const int64_t la = ca < cols ? ca : 0, lb = cb < cols ? cb : 0;  // in bounds, unused
+#pragma unroll
+    for (int i0 = 0; i0 < R; i0 += RB) {
+        uint32_t a0[RB], a1[RB], b0[RB], b1[RB], ma[RB], mb[RB], g[RB];
+        bool live[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const int64_t o = o0 + w * R + i0 + i;  // uniform per wave
+            int64_t a = -1, b = -1;
+            if (o < out_dim) {
+                a = ia[o];
+                b = ib[o];
+            }
+            live[i] = o < out_dim && a < in_dim && b < in_dim;
+            g[i] = live[i] ? uint32_t(gate[o] & 15) : 0u;
+            const bool ua = live[i] && a >= 0, ub = live[i] && b >= 0;
+            ma[i] = ua ? ~0u : 0u;
+            mb[i] = ub ? ~0u : 0u;
+            const int64_t ra = ua ? a : 0, rb = ub ? b : 0;
+            a0[i] = x[ra * cols + la];
+            a1[i] = x[ra * cols + lb];
+            b0[i] = x[rb * cols + la];
+            b1[i] = x[rb * cols + lb];
+        }
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            uint32_t r0 = gate_word(g[i], a0[i] & ma[i], b0[i] & mb[i]);
+            uint32_t r1 = gate_word(g[i], a1[i] & ma[i], b1[i] & mb[i]);
+            if (!live[i]) r0 = r1 = 0u;
+            tile[w * R + i0 + i][lane] = r0;
+            tile[w * R + i0 + i][64 + lane] = r1;
+        }
+    }
+    __syncthreads();
+    const int64_t o = o0 + lane;
+    if (o < out_words) {
+#pragma unroll 4
+        for (int j = 0; j < kColWords / 4; ++j) {
+            const int cw = w * (kColWords / 4) + j;
+            const int64_t c = c0 + cw;
+            // read once, by the fused pass: bypass the caches
+            if (c < cols) __builtin_nontemporal_store(tile[lane][cw], y + c * out_words + o);
+        }
+    }
+}
+
+// LDS placement of the wide-input fused pass's layers (see k_packed_net_cols).
+struct ColsPlan {
+    int J = 0, hold = 0, in_words = 0, hold_base = 0, lds_words = 0;
+    int base[kNetMaxLayers] = {};
+};
+
+bool spans_overlap(int a0, int a1, int b0, int b1) { return a0 < b1 && b0 < a1; }
+
+// False when the network does not fit: a layer wider than 16 * 1024 rows, more layers than
+// the entry registers hold (cols_max_layers), or an input whose column leaves no room for the first layer
+// (holding at most two of its slots in registers).  Each later layer goes to the lowest of
+// two places (after the held slots or word 0, else the top of LDS) that does not overlap the
+// rows it reads.  Deterministic.
+bool cols_plan(const int64_t* rows, int64_t L, ColsPlan& p) {
+    if (L < 1 || L > kNetMaxLayers || rows[0] < 1) return false;
+    int64_t maxw = 0;
+    for (int64_t l = 1; l <= L; ++l) {
+        if (rows[l] < 1) return false;
+        maxw = std::max(maxw, rows[l]);
+    }
+    if (maxw > 16 * kNetThreads) return false;
+    const int J = maxw <= 8 * kNetThreads ? 8 : 16;
+    if (L > cols_max_layers(J)) return false;
+    const int64_t in_words = ceil_div(rows[0], 64) * 64;
+    if (in_words > kLdsWords) return false;
+    const int span = J * kNetThreads;
+    for (int hold : {0, 2}) {
+        if (hold > 0 && L < 2) continue;  // the class counts read one contiguous layer
+        const int split = (J - hold) * kNetThreads;
+        if (in_words + split > kLdsWords || int64_t(hold) * kNetThreads > in_words) continue;
+        ColsPlan q;
+        q.J = J;
+        q.hold = hold;
+        q.in_words = int(in_words);
+        q.hold_base = 0;
+        q.base[0] = int(in_words);
+        int end = int(in_words) + split;
+        // the runs of LDS the layer being placed reads (layer 0's output is two)
+        int r0a = q.base[0], r0b = q.base[0] + split, r1a = 0, r1b = hold * kNetThreads;
+        bool ok = true;
+        for (int64_t l = 1; l < L && ok; ++l) {
+            ok = false;
+            for (int c : {l == 1 ? hold * kNetThreads : 0, kLdsWords - span}) {
+                if (c < 0 || c + span > kLdsWords || spans_overlap(c, c + span, r0a, r0b) ||
+                    spans_overlap(c, c + span, r1a, r1b))
+                    continue;
+                q.base[l] = c;
+                end = std::max(end, c + span);
+                r0a = c;
+                r0b = c + span;
+                r1a = r1b = 0;
+                ok = true;
+                break;
+            }
+        }
+        if (!ok) continue;
+        q.lds_words = end;
+        p = q;
+        return true;
+    }
+    return false;
 }
 
 }  // namespace
@@ -525,4 +794,119 @@ extern "C" int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamp
     else launch(std::integral_constant<int, kMaxCountBits>());
     if (rc) return rc;
     return check_launch("cl_packed_network");
+}
+
+extern "C" int cl_packed_network_columns_layout(const int64_t* rows_host, int64_t num_layers,
+                                                int64_t* applies, int64_t* in_words,
+                                                int64_t* split, int64_t* hold_base,
+                                                int64_t* base) {
+    clear_error();
+    CL_ARG(rows_host && applies && in_words && split && hold_base && base,
+           "null pointer argument");
+    CL_ARG(num_layers >= 1 && num_layers <= kNetMaxLayers, "1 to %d layers", kNetMaxLayers);
+    ColsPlan p;
+    *applies = cols_plan(rows_host, num_layers, p) ? 1 : 0;
+    *in_words = p.in_words;
+    *split = int64_t(p.J - p.hold) * kNetThreads;
+    *hold_base = p.hold_base;
+    for (int64_t l = 0; l < num_layers; ++l) base[l] = p.base[l];
+    return CL_OK;
+}
+
+extern "C" int cl_eval_packed_indexed_columns(const void* x, const int32_t* ia,
+                                              const int32_t* ib, const uint8_t* gate, void* y,
+                                              int64_t in_dim, int64_t out_dim, int64_t row_bytes,
+                                              int64_t out_words, void* stream) {
+    clear_error();
+    CL_ARG(in_dim >= 0 && out_dim >= 0 && row_bytes >= 0, "negative shape");
+    CL_ARG(row_bytes % 4 == 0, "packed rows must be a multiple of 4 bytes");
+    CL_ARG(out_words >= out_dim, "out_words (%lld) must be at least out_dim (%lld)",
+           (long long)out_words, (long long)out_dim);
+    const int64_t cols = row_bytes / 4;
+    if (out_words == 0 || cols == 0) return CL_OK;
+    CL_ARG(out_dim == 0 || in_dim > 0, "in_dim is 0 but out_dim > 0");
+    CL_ARG(y && (out_dim == 0 || (x && ia && ib && gate)), "null pointer argument");
+    CL_ARG(aligned(x, 4) && aligned(y, 4), "misaligned buffers");
+    const int64_t gx = ceil_div(out_words, kColRows), gy = ceil_div(cols, kColWords);
+    CL_ARG(gx < (int64_t(1) << 31) && gy < 65536, "packed layer too large for one launch");
+    k_eval_packed_cols<<<dim3(unsigned(gx), unsigned(gy), 1), 256, 0, as_stream(stream)>>>(
+        static_cast<const uint32_t*>(x), ia, ib, gate, static_cast<uint32_t*>(y), in_dim,
+        out_dim, cols, out_words);
+    return check_launch("cl_eval_packed_indexed_columns");
+}
+
+extern "C" int cl_packed_network_columns(const void* x, int64_t cols, int64_t in_words,
+                                         int64_t nsamples, const uint64_t* tables,
+                                         const int64_t* rows_host, int64_t num_layers, int64_t k,
+                                         int32_t* counts, void* stream) {
+    clear_error();
+    CL_ARG(num_layers >= 1 && num_layers <= kNetMaxLayers, "1 to %d layers", kNetMaxLayers);
+    CL_ARG(rows_host && k >= 1 && cols >= 0, "bad arguments");
+    CL_ARG(nsamples >= 0 && nsamples <= cols * 32, "more samples than packed bits");
+    ColsPlan p;
+    CL_ARG(cols_plan(rows_host, num_layers, p),
+           "the network does not fit the wide-input fused pass "
+           "(cl_packed_network_columns_layout)");
+    CL_ARG(in_words == p.in_words, "in_words must be %d for this network, got %lld",
+           p.in_words, (long long)in_words);
+    PackedNetCols net{};
+    net.num_layers = int(num_layers);
+    net.k = int(k);
+    int64_t off = 0;
+    for (int l = 0; l <= num_layers; ++l) {
+        net.rows[l] = int(rows_host[l]);
+        if (l < num_layers) {
+            net.table_off[l] = off;
+            off += rows_host[l + 1];
+            net.base[l] = p.base[l];
+        }
+    }
+    net.hold_base = p.hold_base;
+    net.in_words = p.in_words;
+    const int last = net.rows[num_layers];
+    if (last % k != 0) {
+        set_error("in_dim (%d) has to be divisible by k (%lld) but it is not", last, (long long)k);
+        return CL_ERR_VALUE;
+    }
+    CL_ARG(k <= last, "k must be at most the last layer's width");
+    const int per_lane = int(ceil_div(last / k, 64));
+    CL_ARG(per_lane < 256, "class groups too large for the fused pass");
+    if (nsamples == 0 || cols == 0) return CL_OK;
+    CL_ARG(x && tables && counts, "null pointer argument");
+    CL_ARG(aligned(x, 16) && aligned(tables, 8), "misaligned buffers");
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        set_error("cannot query the device");
+        return CL_ERR_HIP;
+    }
+    const int64_t want = std::max<int64_t>(8, (int64_t(cus) / 8) * 8);
+    const int64_t pblocks = std::min<int64_t>(want, 8 * ceil_div(cols, 8));
+    const size_t lds = size_t(p.lds_words) * 4;
+    int rc = CL_OK;
+    auto go = [&](auto nb, auto jc, auto hc) {
+        auto* kern = &k_packed_net_cols<decltype(nb)::value, decltype(jc)::value,
+                                        decltype(hc)::value>;
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) !=
+            hipSuccess) {
+            set_error("cannot reserve %zu bytes of LDS for the fused pass", lds);
+            rc = CL_ERR_HIP;
+            return;
+        }
+        kern<<<unsigned(pblocks), kNetThreads, lds, as_stream(stream)>>>(
+            static_cast<const uint4*>(x), cols, nsamples, tables, net, counts);
+    };
+    using std::integral_constant;
+    auto by_shape = [&](auto nb) {
+        if (p.J == 8 && p.hold == 0) go(nb, integral_constant<int, 8>(), integral_constant<int, 0>());
+        else if (p.J == 8) go(nb, integral_constant<int, 8>(), integral_constant<int, 2>());
+        else if (p.hold == 0) go(nb, integral_constant<int, 16>(), integral_constant<int, 0>());
+        else go(nb, integral_constant<int, 16>(), integral_constant<int, 2>());
+    };
+    if (per_lane < 8) by_shape(integral_constant<int, 3>());
+    else if (per_lane < 32) by_shape(integral_constant<int, 5>());
+    else by_shape(integral_constant<int, 8>());
+    if (rc) return rc;
+    return check_launch("cl_packed_network_columns");
 }

@@ -88,6 +88,38 @@ def _fusable(in_rows: int, outs: list, max_layers: int, max_rows: int) -> bool:
             and max(outs) <= max_rows)
 
 
+def columns_layout(rows: list) -> dict | None:
+    """LDS placement of the wide-input fused pass for layer widths `rows` (input first), or
+    None when it does not apply (cl_packed_network_columns_layout): in_words (LDS words per
+    input column), split and hold_base (row p of the first layer is word base[0] + p below
+    split, else hold_base + p - split) and base (row p of layer l >= 1 is word base[l] + p)."""
+    n = len(rows) - 1
+    if n < 1 or n > _limits()[0]:
+        return None
+    arr = (ctypes.c_int64 * len(rows))(*[int(r) for r in rows])
+    applies, in_words, split, hold = (ctypes.c_int64() for _ in range(4))
+    base = (ctypes.c_int64 * n)()
+    _capi.call("cl_packed_network_columns_layout", arr, n, ctypes.byref(applies),
+               ctypes.byref(in_words), ctypes.byref(split), ctypes.byref(hold), base)
+    if not applies.value:
+        return None
+    return {"in_words": in_words.value, "split": split.value, "hold_base": hold.value,
+            "base": list(base)}
+
+
+def _column_producer(body: list, first: int):
+    """Index of the module whose packed output feeds the dense tail body[first:] (Flatten
+    modules in between pass a PackBitsTensor through unchanged), when it is a packed layer from
+    index tables (ConvLayer or LogicLayer) that can write the column-major input of the
+    wide-input fused pass; else None."""
+    j = first - 1
+    while j >= 0 and type(body[j]) is torch.nn.Flatten:
+        j -= 1
+    if j < 0 or type(body[j]) not in (ConvLayer, LogicLayer):
+        return None
+    return j
+
+
 class PackedNetwork:
     """Fused packed evaluator of `model` (frozen or in eval mode; each neuron uses its argmax
     slot `w`), ending in a GroupSum.  Call it with a PackBitsTensor of the network's input (or
@@ -96,7 +128,11 @@ class PackedNetwork:
     The longest tail of dense LogicLayers that the fused kernel takes (an input of at most
     4096 rows, widths within LDS) runs in one launch with every 32-sample column held in LDS;
     the modules before it (ConvLayers, ConvLogicLayers, wider dense layers, Flatten) run layer
-    by layer on the packed kernels first.  When no tail qualifies every module runs layer by
+    by layer on the packed kernels first.  A tail whose input is wider (cfg5's 25088 conv
+    outputs) is fused when a ConvLayer or dense LogicLayer feeds it and its layers fit
+    (columns_layout): that layer writes its output column-major
+    (cl_eval_packed_indexed_columns) and the tail runs on those columns
+    (cl_packed_network_columns).  When no tail qualifies every module runs layer by
     layer and the counts come from the group popcount.  The gate tables are built once here;
     rebuild after changing the model.  With `bank_aware` (default), each fused layer's rows
     are laid out in LDS by bank_aware_positions, so that the row reads of the kernel's
@@ -119,8 +155,20 @@ class PackedNetwork:
         start = next((j for j in range(first, len(body))
                       if _fusable(int(body[j].in_dim), [int(m.out_dim) for m in body[j:]],
                                   max_layers, max_rows)), len(body))
+        # a tail whose input is too wide to stage row by row: its input comes column-major
+        # from the packed layer before it (cl_eval_packed_indexed_columns)
+        self.producer = None
+        self.layout = None
+        if start != first and first < len(body):
+            prod = _column_producer(body, first)
+            rows = [int(body[first].in_dim)] + [int(m.out_dim) for m in body[first:]]
+            layout = columns_layout(rows) if prod is not None else None
+            if layout is not None:
+                start, self.producer, self.layout = first, body[prod], layout
+                self.prefix = body[:prod]
         layers = body[start:]
-        self.prefix = body[:start]
+        if self.producer is None:
+            self.prefix = body[:start]
         if not layers:
             self.rows = None            # no fused tail: layer by layer, then the popcount
             self.device = None
@@ -148,6 +196,7 @@ class PackedNetwork:
                     raise IndexError("connection indices out of range")
                 wiring.append((a.cpu().numpy(), b.cpu().numpy(), g.cpu().numpy(), a.device))
             prev_pos = np.arange(self.rows[0], dtype=np.int64)   # input rows stay in place
+            lay = self.layout
             for i, (m, (a, b, g, dev)) in enumerate(zip(layers, wiring)):
                 pa, pb = prev_pos[a], prev_pos[b]
                 if not bank_aware:
@@ -160,14 +209,26 @@ class PackedNetwork:
                 else:  # class groups stay contiguous
                     pos = bank_aware_positions_grouped(pa, pb, m.out_dim, m.out_dim // self.k)
                 ent = np.empty(m.out_dim, dtype=np.int64)
-                ent[pos] = (pa * 4) | ((pb * 4) << 20) | (g << 40)   # LDS byte offsets
+                if lay is None:
+                    ent[pos] = (pa * 4) | ((pb * 4) << 20) | (g << 40)   # LDS byte offsets
+                    prev_pos = pos
+                else:
+                    ent[pos] = pa | (pb << 16) | (g << 32)               # LDS words
+                    # the LDS word of each row (banks as the positions': every base is a
+                    # multiple of 32 words)
+                    if i == 0:
+                        prev_pos = np.where(pos < lay["split"], lay["base"][0] + pos,
+                                            lay["hold_base"] + pos - lay["split"])
+                    else:
+                        prev_pos = lay["base"][i] + pos
                 entries.append(torch.as_tensor(ent, device=dev))
-                prev_pos = pos
         self.tables = torch.cat(entries).contiguous()
         self.device = self.tables.device
         self._rows_host = (ctypes.c_int64 * len(self.rows))(*self.rows)
 
     def __call__(self, x) -> torch.Tensor:
+        if self.producer is not None:
+            return self._call_columns(x)
         if self.prefix:
             if isinstance(x, PackBitsTensor):
                 h = PackBitsTensor.from_packed(x.t, x.pad_len)   # the caller's object stays
@@ -195,4 +256,51 @@ class PackedNetwork:
                 "cl_packed_network", words.data_ptr(), row_bytes, n, self.tables.data_ptr(),
                 self._rows_host, len(self.rows) - 1, self.k, counts.data_ptr(),
                 _dl.stream_of(words)))
+        return counts
+
+    def _call_columns(self, x) -> torch.Tensor:
+        """The wide-input path: the prefix layer by layer, the producer layer written
+        column-major, then the fused tail on that input."""
+        if isinstance(x, PackBitsTensor):
+            h = PackBitsTensor.from_packed(x.t, x.pad_len)   # the caller's object stays
+        else:
+            h = PackBitsTensor.from_packed(x)
+        with torch.no_grad():
+            for m in self.prefix:
+                h = m(h)
+            m = self.producer
+            w = getattr(m, "w", None)
+            if w is None:
+                w = m._argmax_slots()
+            ia, ib, gate = m.packed_tables(w)[:3]
+        words, n = h.t, h.num_samples
+        _dl._check(words, "x")
+        if words.device != self.device:
+            raise RuntimeError(f"x is on {words.device}, the network on {self.device}")
+        in_rows = words.shape[0]
+        expect = m.in_dim if type(m) is LogicLayer else int(np.prod(m.in_shape))
+        if in_rows != expect:
+            raise RuntimeError(f"the layer before the fused tail gets {in_rows} rows, "
+                               f"expects {expect}")
+        if ia.numel() != self.rows[0]:
+            raise RuntimeError(f"the layer before the fused tail has {ia.numel()} outputs, "
+                               f"the tail reads {self.rows[0]}")
+        row_bytes = words.shape[1] * words.element_size()
+        if row_bytes % 4:
+            raise RuntimeError("packed rows must be a multiple of 4 bytes")
+        cols, in_words = row_bytes // 4, self.layout["in_words"]
+        colmaj = torch.empty((cols, in_words), dtype=torch.int32, device=words.device)
+        counts = torch.empty((n, self.k), dtype=torch.int32, device=words.device)
+        stream = _dl.stream_of(words)
+        with torch.cuda.device(words.device):
+            timing.timed(f"cl_eval_packed_indexed_columns[{in_rows}->{self.rows[0]}]",
+                         lambda: _capi.call(
+                "cl_eval_packed_indexed_columns", words.data_ptr(), ia.data_ptr(),
+                ib.data_ptr(), gate.data_ptr(), colmaj.data_ptr(), in_rows, self.rows[0],
+                row_bytes, in_words, stream))
+            timing.timed(f"cl_packed_network_columns[{self.rows[0]}->{self.rows[-1]}]",
+                         lambda: _capi.call(
+                "cl_packed_network_columns", colmaj.data_ptr(), cols, in_words, n,
+                self.tables.data_ptr(), self._rows_host, len(self.rows) - 1, self.k,
+                counts.data_ptr(), stream))
         return counts

@@ -537,6 +537,36 @@ int cl_packed_network(const void* x, int64_t row_bytes, int64_t nsamples, const 
                       const int64_t* rows_host, int64_t num_layers, int64_t k, int32_t* counts,
                       void* stream);
 
+/* Wide-input fused pass (no reference counterpart; the same fusion for dense tails whose input
+ * is wider than cl_packed_network stages, e.g. a conv block's 25088 output rows).  The input
+ * comes column-major: x[c * in_words + r] is the 32-bit word of 32-sample column c of input
+ * row r (cl_eval_packed_indexed_columns writes it), so a column is one contiguous run.  The
+ * layers' rows are placed in LDS by cl_packed_network_columns_layout; tables: for layer l,
+ * rows[l+1] entries (uint64) of wa | wb << 16 | opcode << 32, where wa, wb are the LDS words of
+ * the gate's inputs: input row r is word r; row p of layer 0 is word base[0] + p for
+ * p < split, else hold_base + p - split; row p of layer l >= 1 is word base[l] + p.  Entry p
+ * of a layer is the gate that writes its row p.  counts: int32 [nsamples, k].
+ *
+ * cl_packed_network_columns_layout: *applies = 1 and the placement when the network fits
+ * (layers at most 16384 rows, at most 2 layers when one is wider than 8192 rows, else 3,
+ * an input column and the first layer within 160 KiB less two held slots), else 0.
+ * base: num_layers entries. */
+int cl_packed_network_columns_layout(const int64_t* rows_host, int64_t num_layers,
+                                     int64_t* applies, int64_t* in_words, int64_t* split,
+                                     int64_t* hold_base, int64_t* base);
+
+/* Packed layer from resolved index tables, as cl_eval_packed_indexed (without the order), with
+ * column-major output: y[c * out_words + o] for the row_bytes / 4 32-bit columns c and rows
+ * o < out_words; rows out_dim <= o < out_words are zero.  The producer of the wide-input fused
+ * pass's input (out_words = its in_words). */
+int cl_eval_packed_indexed_columns(const void* x, const int32_t* ia, const int32_t* ib,
+                                   const uint8_t* gate, void* y, int64_t in_dim, int64_t out_dim,
+                                   int64_t row_bytes, int64_t out_words, void* stream);
+
+int cl_packed_network_columns(const void* x, int64_t cols, int64_t in_words, int64_t nsamples,
+                              const uint64_t* tables, const int64_t* rows_host,
+                              int64_t num_layers, int64_t k, int32_t* counts, void* stream);
+
 /* -------------------------------------------------------------------------------------------
  * Logic-tree convolution block (third-party ConvLogic, convlogic_cuda extension,
  * third_party/convlogic_source_code/src/convlogic/cuda/convlogic.cpp:31-43).

@@ -589,6 +589,68 @@ def test_bank_aware_positions_grouped(rows, k):
         assert clashes(np.arange(rows)) > 1.5 * max(1, clashes(pos))
 
 
+def _spans_overlap(a, b):
+    return a[0] < b[1] and b[0] < a[1]
+
+
+@pytest.mark.parametrize("rows", [
+    [25088, 16000, 16000],       # cfg5's tail: two first-layer slots held over the input
+    [8192, 3000, 2000],          # 8-slot layers, the second over the dead input
+    [9000, 12000, 10000],        # held slots, the second layer at the top of LDS
+    [5760, 12000, 10000],        # 16 slots, nothing held
+    [30000, 8000, 6000, 4000],   # three 8-slot layers, held slots
+    [32768, 100],                # one 8-slot layer after the widest input that leaves room
+    [34000, 100, 100],           # wider: two slots held
+])
+def test_columns_layout_places_every_layer_apart_from_what_it_reads(rows):
+    """The wide-input fused pass's LDS placement (a restatement of what its kernel does with
+    it): every step's slot writes, junk slots included, stay inside 160 KiB and off the words
+    that step and later ones still read; rows keep their LDS bank (bases are multiples of 32
+    words)."""
+    from compactlogic_amd.packed_net import columns_layout
+    lay = columns_layout(rows)
+    assert lay is not None
+    J = 8 if max(rows[1:]) <= 8192 else 16
+    span, split, words = J * 1024, lay["split"], 40960
+    held = span - split
+    assert lay["in_words"] >= rows[0] and lay["in_words"] % 64 == 0
+    assert split % 1024 == 0 and 0 <= held <= 2048
+    assert all(b % 32 == 0 for b in lay["base"]) and lay["hold_base"] % 32 == 0
+    inp = (0, lay["in_words"])
+    unheld = (lay["base"][0], lay["base"][0] + split)
+    hold = (lay["hold_base"], lay["hold_base"] + held)
+    assert unheld[1] <= words and not _spans_overlap(unheld, inp)      # written while read
+    if held:
+        assert len(rows) >= 3                                              # counts read one run
+        assert hold[1] <= lay["in_words"] and not _spans_overlap(hold, unheld)
+    live = [unheld, hold] if held else [unheld]
+    for l in range(1, len(rows) - 1):
+        out = (lay["base"][l], lay["base"][l] + span)
+        assert out[1] <= words and not any(_spans_overlap(out, r) for r in live if r[1] > r[0])
+        live = [out]
+
+
+@pytest.mark.parametrize("rows", [
+    [25088, 16385],              # a layer wider than 16 slots
+    [30000, 16000],              # one wide layer: no room without holding, nothing to hold for
+    [30000, 16000, 16000, 100],  # three 16-slot layers
+    [41000, 100, 100],           # the input column alone exceeds LDS
+    [38000, 8000, 100],          # the first layer does not fit even with two slots held
+])
+def test_columns_layout_rejects_what_does_not_fit(rows):
+    from compactlogic_amd.packed_net import columns_layout
+    assert columns_layout(rows) is None
+
+
+def test_columns_layout_cfg5():
+    """cfg5's tail: the input column takes words [0, 25088), the first layer's slots 0-13 the
+    next 14336 words, its slots 14-15 are held and written over the input's first 2048 words,
+    and the second layer goes after them."""
+    from compactlogic_amd.packed_net import columns_layout
+    assert columns_layout([25088, 16000, 16000]) == {
+        "in_words": 25088, "split": 14336, "hold_base": 0, "base": [25088, 2048]}
+
+
 def test_conv_packed_order_groups_channels_by_input():
     """The packed evaluation order is a permutation of the output features that visits the
     output channels in order of the input channel their winner slot reads."""

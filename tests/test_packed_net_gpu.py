@@ -74,22 +74,112 @@ def conv_oracle_counts(model, words_np, n):
     return P.network_counts(words_np, layers, model[-1].k, pad)
 
 
-def test_packed_network_cfg5_runs_layer_by_layer(device):
-    """cfg5's first dense layer reads 25088 rows, more than the fused kernel stages in LDS: no
-    tail is fused and every module runs on the packed kernels, then the group popcount."""
+def test_packed_network_cfg5_fuses_the_wide_tail(device):
+    """cfg5: conv1 layer by layer, conv2 written column-major, then 25088 -> 16000 -> 16000
+    and the class counts in one launch (two first-layer slots held over the input column);
+    equal to the C oracle and to the whole network layer by layer."""
     cfg = configs.CONV_CONFIGS["cfg5"]
     model = configs.conv_network(cfg, device=device)
     configs.freeze_argmax(model)
     feats = int(np.prod(cfg.in_shape))
     xw = configs.packed_input_words(feats, 64, device=device)            # 2^12 samples
     net = cl.PackedNetwork(model)
-    assert net.rows is None and len(net.prefix) == len(model) - 1
+    assert net.producer is model[1] and len(net.prefix) == 1
+    assert net.rows == [25088, 16000, 16000] and net.layout["split"] == 14336
     x = cl.PackBitsTensor.from_packed(xw)
     counts = net(x)
     assert x.t is xw                                                     # input untouched
     ref = conv_oracle_counts(model, np_(xw).view(np.uint64), 1 << 12)
     assert np.array_equal(np_(counts), ref)
     assert torch.equal(counts, model(cl.PackBitsTensor.from_packed(xw.clone())))
+
+
+def small_conv_net(device, in_shape, c_out, widths, k, seed):
+    torch.manual_seed(seed)
+    conv = cl.ConvLayer(in_shape, padding=1, c_out=c_out, ks=3, stride=1, num_chn=1,
+                        num_gates=4)
+    g = torch.Generator().manual_seed(seed)
+    dims = [int(np.prod(conv.out_shape))] + list(widths)
+    dense = [cl.LogicLayer(i, o, num_gates=4) for i, o in zip(dims[:-1], dims[1:])]
+    for m in [conv] + dense:
+        with torch.no_grad():
+            m.weights.copy_(torch.randn(m.weights.shape, generator=g))
+            m.gate_sequence.copy_(torch.randint(0, 16, m.gate_sequence.shape,
+                                                generator=g).to(torch.uint8))
+    model = torch.nn.Sequential(conv, torch.nn.Flatten(), *dense, cl.GroupSum(k, 1.0)).to(device)
+    configs.freeze_argmax(model)
+    return model
+
+
+@pytest.mark.parametrize("in_shape,c_out,widths,k,n,bits", [
+    ((4, 16, 16), 32, [4200, 2100], 10, 1000, 64),     # 8 slots, second layer over the input
+    ((2, 12, 12), 40, [12000, 10000], 10, 333, 64),    # 16 slots, nothing held
+    ((5, 15, 15), 40, [12000, 10000], 20, 100, 32),    # 9000 rows: held slots; odd words
+    ((3, 16, 16), 24, [5000, 4000, 2100], 3, 4096, 64),  # three layers
+])
+def test_packed_network_wide_tail_matches_oracle(device, in_shape, c_out, widths, k, n, bits):
+    model = small_conv_net(device, in_shape, c_out, widths, k, seed=n)
+    rng = np.random.default_rng(n)
+    feats = int(np.prod(in_shape))
+    x = cl.PackBitsTensor(torch.as_tensor(rng.integers(0, 2, (n, feats)).astype(bool),
+                                          device=device), bits)
+    net = cl.PackedNetwork(model)
+    assert net.producer is model[0] and net.layout is not None
+    counts = net(x)
+    assert counts.shape == (n, k)
+    words = np_(x.t)
+    if words.dtype != np.int64:                  # 32-bit words: pad to whole 64-bit words
+        words = np.concatenate([words, np.zeros((words.shape[0], words.shape[1] % 2),
+                                                words.dtype)], 1)
+    ref = conv_oracle_counts(model, np.ascontiguousarray(words).view(np.uint64), n)
+    assert np.array_equal(np_(counts), ref)
+    layerwise = model(cl.PackBitsTensor.from_packed(x.t.clone(), x.pad_len))
+    assert torch.equal(counts, layerwise)
+
+
+def test_packed_network_wide_tail_after_a_dense_producer(device):
+    """A dense LogicLayer feeds the tail through a Flatten: it writes the columns."""
+    model = frozen_net([(64, 6000), (6000, 3000), (3000, 2000)], 10, 8, 11, device)
+    model = torch.nn.Sequential(model[0], torch.nn.Flatten(), model[1], model[2], model[3])
+    net = cl.PackedNetwork(model)
+    assert net.producer is model[0] and net.prefix == [] and net.rows == [6000, 3000, 2000]
+    rng = np.random.default_rng(3)
+    x = cl.PackBitsTensor(torch.as_tensor(rng.integers(0, 2, (777, 64)).astype(bool),
+                                          device=device), 64)
+    counts = net(x)
+    ref = oracle_counts(model, np_(x.t).view(np.uint64), 777)
+    assert np.array_equal(np_(counts), ref)
+
+
+@pytest.mark.parametrize("out_dim,out_words,words,bits", [
+    (1000, 1024, 130, 32), (4096, 4096, 256, 32), (70, 128, 3, 32), (25, 64, 2, 64)])
+def test_eval_packed_indexed_columns_is_the_transposed_layer(device, out_dim, out_words, words,
+                                                             bits):
+    """cl_eval_packed_indexed_columns equals cl_eval_packed_indexed transposed to 32-bit words,
+    with zero rows past out_dim; negative and out-of-range indices as there."""
+    from compactlogic_amd import _capi
+    from compactlogic_amd import difflogic_hip as _dl
+    rng = np.random.default_rng(out_dim)
+    in_dim = 300
+    xw = torch.as_tensor(rng.integers(-2**31, 2**31, (in_dim, words * bits // 32)),
+                         dtype=torch.int32, device=device)
+    ia = rng.integers(-1, in_dim, out_dim).astype(np.int32)
+    ib = rng.integers(-1, in_dim, out_dim).astype(np.int32)
+    ia[::17] = in_dim                                   # out of range: a zero row
+    ia_t, ib_t = torch.as_tensor(ia, device=device), torch.as_tensor(ib, device=device)
+    gate = torch.as_tensor(rng.integers(0, 16, out_dim).astype(np.uint8), device=device)
+    row_bytes = xw.shape[1] * 4
+    ref = torch.empty((out_dim, xw.shape[1]), dtype=torch.int32, device=device)
+    _capi.call("cl_eval_packed_indexed", xw.data_ptr(), ia_t.data_ptr(), ib_t.data_ptr(),
+               gate.data_ptr(), None, ref.data_ptr(), in_dim, out_dim, row_bytes,
+               _dl.stream_of(xw))
+    out = torch.full((xw.shape[1], out_words), 7, dtype=torch.int32, device=device)
+    _capi.call("cl_eval_packed_indexed_columns", xw.data_ptr(), ia_t.data_ptr(),
+               ib_t.data_ptr(), gate.data_ptr(), out.data_ptr(), in_dim, out_dim, row_bytes,
+               out_words, _dl.stream_of(xw))
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :out_dim], ref.T)
+    assert int(out[:, out_dim:].abs().sum()) == 0
 
 
 def test_packed_network_cfg3_tree_fuses_the_dense_tail(device):
