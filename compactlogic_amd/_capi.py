@@ -121,6 +121,8 @@ SIGNATURES: dict[str, list] = {
                                          ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                          ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
     "cl_eval_packed_indexed_columns": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "cl_eval_packed_indexed_pair_columns": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                                            _i64, _i64, _p],
     "cl_packed_network_columns": [_p, _i64, _i64, _i64, _p, ctypes.POINTER(_i64), _i64, _i64,
                                   _p, _p],
 }

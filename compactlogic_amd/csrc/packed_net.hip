@@ -514,74 +514,163 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net_cols(
     }
 }
 
-// Packed layer from resolved index tables with column-major output (the input layout of
-// k_packed_net_cols): y[c * out_words + o] = word c of op_{g[o]}(x[ia[o], :], x[ib[o], :]),
-// a negative index reading zeros, 0 for an index past in_dim and for rows
-// out_dim <= o < out_words.  A workgroup takes 64 rows x 128 words: a wave evaluates 16 rows
-// (per operand and row two coalesced 4-byte loads of 64 words), the tile is transposed
-// through LDS (row stride 129 words: the column reads of a half-wave hit 32 banks), and each
-// wave then writes the 64-row runs of 32 words, 256 contiguous bytes each.
-constexpr int kColRows = 64;
-constexpr int kColWords = 128;
+// Packed layers from resolved index tables with column-major output (the input layout of
+// k_packed_net_cols): y[c * out_words + o] = word c of row o of the last layer, 0 for rows
+// out_dim <= o < out_words.  A layer's row o is op_{g[o]}(row ia[o], row ib[o]) of its input,
+// a negative index reading a zero row and an index past the input's rows making row o zero
+// (as k_eval_packed_idx).  With PAIR the kernel evaluates two layers composed, the first
+// (t1) on x and the second (t2) on the first's rows, computing each first-layer row the
+// second reads in place of storing the first layer: four input rows per output row instead
+// of a full intermediate written and read back.
+// Workgroups are mapped XCD-aware: XCD x (= blockIdx % 8) takes a contiguous range of column
+// tiles and walks every row tile of one column tile before the next, so the input words of a
+// column tile are read from HBM once, by one XCD, and the (up to four) reads of each input
+// row by the rows of that tile hit its L2.
+// A workgroup takes 64 rows x W words: a wave evaluates 16 rows, the indices of a row being
+// uniform (scalar loads), and lane l takes words l, l + 64, ... (coalesced 4-byte loads of
+// 64 words per input row); the tile is transposed through LDS (row stride W + 1: the column
+// reads of a half-wave hit 32 banks) and each wave then writes the 64-row runs of W / 4
+// words, 256 contiguous bytes each.
+struct PackedTabs {
+    const int32_t* ia;
+    const int32_t* ib;
+    const uint8_t* gate;
+    int64_t in;  // rows of the layer's input
+};
 
+constexpr int kColRows = 64;
+#ifndef CL_COLS_PAIR_RB
+#define CL_COLS_PAIR_RB 8
+#endif
+
+// Truth table of a gate whose input a (tt_a0) or b (tt_b0) is held at zero: the opcode
+// that gives the same words without masking the operand (bits MSB first over AB = 00, 01,
+// 10, 11, as gate_word reads them).
+__device__ __forceinline__ uint32_t tt_a0(uint32_t g) {
+    const uint32_t f00 = (g >> 3) & 1u, f01 = (g >> 2) & 1u;
+    return (f00 << 3) | (f01 << 2) | (f00 << 1) | f01;
+}
+__device__ __forceinline__ uint32_t tt_b0(uint32_t g) {
+    const uint32_t f00 = (g >> 3) & 1u, f10 = (g >> 1) & 1u;
+    return (f00 << 3) | (f00 << 2) | (f10 << 1) | f10;
+}
+
+template <int W, bool PAIR>
 __global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __restrict__ x,
-                                                          const int32_t* __restrict__ ia,
-                                                          const int32_t* __restrict__ ib,
-                                                          const uint8_t* __restrict__ gate,
+                                                          PackedTabs t1, PackedTabs t2,
                                                           uint32_t* __restrict__ y,
-                                                          int64_t in_dim, int64_t out_dim,
-                                                          int64_t cols, int64_t out_words) {
-    __shared__ uint32_t tile[kColRows][kColWords + 1];
-    constexpr int R = kColRows / 4;  // rows per wave
-    constexpr int RB = 8;            // rows whose loads are in flight together
-    const int64_t o0 = int64_t(blockIdx.x) * kColRows, c0 = int64_t(blockIdx.y) * kColWords;
+                                                          int64_t out_dim, int64_t cols,
+                                                          int64_t out_words, int64_t row_tiles,
+                                                          int64_t tiles_per_xcd) {
+    __shared__ uint32_t tile[kColRows][W + 1];
+    constexpr int K = W / 64;          // words per lane
+    constexpr int R = kColRows / 4;    // rows per wave
+    constexpr int RB = PAIR ? CL_COLS_PAIR_RB : 8;  // rows whose loads are in flight together
+    constexpr int NR = PAIR ? 4 : 2;   // input rows per output row
+    const PackedTabs& tl = PAIR ? t2 : t1;  // the layer whose rows are written
+    const int64_t i = blockIdx.x / 8;       // position in this XCD's walk
+    const int64_t ct = (blockIdx.x % 8) * tiles_per_xcd + i / row_tiles;
+    const int64_t o0 = (i % row_tiles) * kColRows, c0 = ct * W;
+    if (c0 >= cols) return;  // past the last column tile (uniform per workgroup)
     const int w = wave_id(), lane = lane_id();
-    const int64_t ca = c0 + lane, cb = c0 + 64 + lane;
-    const int64_t la = ca < cols ? ca : 0, lb = cb < cols ? cb : 0;  // in bounds, unused
+    // Lane r < R resolves row o0 + w * R + r: the input rows it reads (0 for one it does not)
+    // and its opcodes, rewritten so that an operand read as zero (a negative index, a
+    // first-layer row that is zero, a row written as zero) needs no mask: opcode 0 writes
+    // zeros, tt_a0 / tt_b0 ignore the operand.  The wave's rows then take these values by
+    // readlane, so no row waits on a chain of dependent scalar loads.
+    int32_t src[NR];
+    uint32_t ops = 0;  // output opcode | first-layer opcodes << 4, << 8
+    {
+        const int64_t o = o0 + w * R + lane;
+        int64_t a = -1, b = -1;
+        const bool row = lane < R && o < out_dim;
+        if (row) {
+            a = tl.ia[o];
+            b = tl.ib[o];
+        }
+        const bool live = row && a < tl.in && b < tl.in;
+        uint32_t g = live ? uint32_t(tl.gate[o] & 15) : 0u;
+        if constexpr (PAIR) {
+            // the two first-layer rows this row reads, each from two input rows
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int64_t p = s2 ? b : a;
+                int64_t pa = -1, pb = -1;
+                const bool has = live && p >= 0;
+                if (has) {
+                    pa = t1.ia[p];
+                    pb = t1.ib[p];
+                }
+                const bool live1 = has && pa < t1.in && pb < t1.in;
+                uint32_t g1 = live1 ? uint32_t(t1.gate[p] & 15) : 0u;
+                if (pa < 0) g1 = tt_a0(g1);
+                if (pb < 0) g1 = tt_b0(g1);
+                if (!live1) g = s2 ? tt_b0(g) : tt_a0(g);
+                ops |= g1 << (4 + 4 * s2);
+                src[2 * s2] = live1 && pa >= 0 ? int32_t(pa) : 0;
+                src[2 * s2 + 1] = live1 && pb >= 0 ? int32_t(pb) : 0;
+            }
+        } else {
+            if (a < 0) g = tt_a0(g);
+            if (b < 0) g = tt_b0(g);
+            src[0] = live && a >= 0 ? int32_t(a) : 0;
+            src[1] = live && b >= 0 ? int32_t(b) : 0;
+        }
+        ops |= g;
+    }
+    uint32_t lc[K];  // this lane's word offsets in a row (the row base is uniform)
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int64_t c = c0 + 64 * k + lane;
+        lc[k] = uint32_t(c < cols ? c : 0);  // in bounds; the word is not stored
+    }
 #pragma unroll
     for (int i0 = 0; i0 < R; i0 += RB) {
-        uint32_t a0[RB], a1[RB], b0[RB], b1[RB], ma[RB], mb[RB], g[RB];
-        bool live[RB];
+        uint32_t v[RB][NR][K], f[RB];
 #pragma unroll
-        for (int i = 0; i < RB; ++i) {
-            const int64_t o = o0 + w * R + i0 + i;  // uniform per wave
-            int64_t a = -1, b = -1;
-            if (o < out_dim) {
-                a = ia[o];
-                b = ib[o];
+        for (int ii = 0; ii < RB; ++ii) {
+            f[ii] = __builtin_amdgcn_readlane(ops, i0 + ii);
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const uint32_t* rp = x + int64_t(__builtin_amdgcn_readlane(src[r], i0 + ii)) * cols;
+#pragma unroll
+                for (int k = 0; k < K; ++k) v[ii][r][k] = rp[lc[k]];
             }
-            live[i] = o < out_dim && a < in_dim && b < in_dim;
-            g[i] = live[i] ? uint32_t(gate[o] & 15) : 0u;
-            const bool ua = live[i] && a >= 0, ub = live[i] && b >= 0;
-            ma[i] = ua ? ~0u : 0u;
-            mb[i] = ub ? ~0u : 0u;
-            const int64_t ra = ua ? a : 0, rb = ub ? b : 0;
-            a0[i] = x[ra * cols + la];
-            a1[i] = x[ra * cols + lb];
-            b0[i] = x[rb * cols + la];
-            b1[i] = x[rb * cols + lb];
         }
 #pragma unroll
-        for (int i = 0; i < RB; ++i) {
-            uint32_t r0 = gate_word(g[i], a0[i] & ma[i], b0[i] & mb[i]);
-            uint32_t r1 = gate_word(g[i], a1[i] & ma[i], b1[i] & mb[i]);
-            if (!live[i]) r0 = r1 = 0u;
-            tile[w * R + i0 + i][lane] = r0;
-            tile[w * R + i0 + i][64 + lane] = r1;
+        for (int ii = 0; ii < RB; ++ii) {
+            const uint32_t fl = f[ii];
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                uint32_t res;
+                if constexpr (PAIR) {
+                    const uint32_t u = gate_word((fl >> 4) & 15u, v[ii][0][k], v[ii][1][k]);
+                    const uint32_t q = gate_word((fl >> 8) & 15u, v[ii][2][k], v[ii][3][k]);
+                    res = gate_word(fl & 15u, u, q);
+                } else {
+                    res = gate_word(fl & 15u, v[ii][0][k], v[ii][1][k]);
+                }
+                tile[w * R + i0 + ii][64 * k + lane] = res;
+            }
         }
     }
     __syncthreads();
     const int64_t o = o0 + lane;
     if (o < out_words) {
 #pragma unroll 4
-        for (int j = 0; j < kColWords / 4; ++j) {
-            const int cw = w * (kColWords / 4) + j;
+        for (int j = 0; j < W / 4; ++j) {
+            const int cw = w * (W / 4) + j;
             const int64_t c = c0 + cw;
             // read once, by the fused pass: bypass the caches
             if (c < cols) __builtin_nontemporal_store(tile[lane][cw], y + c * out_words + o);
         }
     }
 }
+
+#ifndef CL_COLS_WORDS
+#define CL_COLS_WORDS 128
+#endif
+constexpr int kColWords = CL_COLS_WORDS;  // words (32-sample columns) per workgroup
 
 // LDS placement of the wide-input fused pass's layers (see k_packed_net_cols).
 struct ColsPlan {
@@ -813,26 +902,59 @@ extern "C" int cl_packed_network_columns_layout(const int64_t* rows_host, int64_
     return CL_OK;
 }
 
+namespace {
+int launch_packed_cols(const void* x, const PackedTabs& t1, const PackedTabs* t2, void* y,
+                       int64_t out_dim, int64_t row_bytes, int64_t out_words, void* stream) {
+    CL_ARG(row_bytes % 4 == 0, "packed rows must be a multiple of 4 bytes");
+    CL_ARG(out_words >= out_dim, "out_words (%lld) must be at least out_dim (%lld)",
+           (long long)out_words, (long long)out_dim);
+    const int64_t cols = row_bytes / 4;
+    if (out_words == 0 || cols == 0) return CL_OK;
+    CL_ARG(y && (out_dim == 0 || x), "null pointer argument");
+    CL_ARG(aligned(x, 4) && aligned(y, 4), "misaligned buffers");
+    const int64_t row_tiles = ceil_div(out_words, kColRows);
+    const int64_t per_xcd = ceil_div(ceil_div(cols, kColWords), 8);
+    CL_ARG(8 * per_xcd * row_tiles < (int64_t(1) << 31), "packed layer too large for one launch");
+    const unsigned grid = unsigned(8 * per_xcd * row_tiles);
+    auto* xs = static_cast<const uint32_t*>(x);
+    auto* ys = static_cast<uint32_t*>(y);
+    if (t2)
+        k_eval_packed_cols<kColWords, true><<<grid, 256, 0, as_stream(stream)>>>(
+            xs, t1, *t2, ys, out_dim, cols, out_words, row_tiles, per_xcd);
+    else
+        k_eval_packed_cols<kColWords, false><<<grid, 256, 0, as_stream(stream)>>>(
+            xs, t1, t1, ys, out_dim, cols, out_words, row_tiles, per_xcd);
+    return CL_OK;
+}
+}  // namespace
+
 extern "C" int cl_eval_packed_indexed_columns(const void* x, const int32_t* ia,
                                               const int32_t* ib, const uint8_t* gate, void* y,
                                               int64_t in_dim, int64_t out_dim, int64_t row_bytes,
                                               int64_t out_words, void* stream) {
     clear_error();
     CL_ARG(in_dim >= 0 && out_dim >= 0 && row_bytes >= 0, "negative shape");
-    CL_ARG(row_bytes % 4 == 0, "packed rows must be a multiple of 4 bytes");
-    CL_ARG(out_words >= out_dim, "out_words (%lld) must be at least out_dim (%lld)",
-           (long long)out_words, (long long)out_dim);
-    const int64_t cols = row_bytes / 4;
-    if (out_words == 0 || cols == 0) return CL_OK;
     CL_ARG(out_dim == 0 || in_dim > 0, "in_dim is 0 but out_dim > 0");
-    CL_ARG(y && (out_dim == 0 || (x && ia && ib && gate)), "null pointer argument");
-    CL_ARG(aligned(x, 4) && aligned(y, 4), "misaligned buffers");
-    const int64_t gx = ceil_div(out_words, kColRows), gy = ceil_div(cols, kColWords);
-    CL_ARG(gx < (int64_t(1) << 31) && gy < 65536, "packed layer too large for one launch");
-    k_eval_packed_cols<<<dim3(unsigned(gx), unsigned(gy), 1), 256, 0, as_stream(stream)>>>(
-        static_cast<const uint32_t*>(x), ia, ib, gate, static_cast<uint32_t*>(y), in_dim,
-        out_dim, cols, out_words);
+    CL_ARG(out_dim == 0 || (ia && ib && gate), "null pointer argument");
+    const PackedTabs t{ia, ib, gate, in_dim};
+    if (int rc = launch_packed_cols(x, t, nullptr, y, out_dim, row_bytes, out_words, stream))
+        return rc;
     return check_launch("cl_eval_packed_indexed_columns");
+}
+
+extern "C" int cl_eval_packed_indexed_pair_columns(
+    const void* x, const int32_t* ia1, const int32_t* ib1, const uint8_t* gate1,
+    const int32_t* ia2, const int32_t* ib2, const uint8_t* gate2, void* y, int64_t in_dim,
+    int64_t mid_dim, int64_t out_dim, int64_t row_bytes, int64_t out_words, void* stream) {
+    clear_error();
+    CL_ARG(in_dim >= 0 && mid_dim >= 0 && out_dim >= 0 && row_bytes >= 0, "negative shape");
+    CL_ARG(out_dim == 0 || (mid_dim > 0 && in_dim > 0), "an empty layer feeds out_dim > 0 rows");
+    CL_ARG(out_dim == 0 || (ia1 && ib1 && gate1 && ia2 && ib2 && gate2),
+           "null pointer argument");
+    const PackedTabs t1{ia1, ib1, gate1, in_dim}, t2{ia2, ib2, gate2, mid_dim};
+    if (int rc = launch_packed_cols(x, t1, &t2, y, out_dim, row_bytes, out_words, stream))
+        return rc;
+    return check_launch("cl_eval_packed_indexed_pair_columns");
 }
 
 extern "C" int cl_packed_network_columns(const void* x, int64_t cols, int64_t in_words,

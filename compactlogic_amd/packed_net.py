@@ -107,12 +107,11 @@ def columns_layout(rows: list) -> dict | None:
             "base": list(base)}
 
 
-def _column_producer(body: list, first: int):
-    """Index of the module whose packed output feeds the dense tail body[first:] (Flatten
-    modules in between pass a PackBitsTensor through unchanged), when it is a packed layer from
-    index tables (ConvLayer or LogicLayer) that can write the column-major input of the
-    wide-input fused pass; else None."""
-    j = first - 1
+def _table_layer_before(body: list, j: int):
+    """Index of the module before body[j] (Flatten modules pass a PackBitsTensor through
+    unchanged) when it is a packed layer from index tables (ConvLayer or LogicLayer); else
+    None."""
+    j -= 1
     while j >= 0 and type(body[j]) is torch.nn.Flatten:
         j -= 1
     if j < 0 or type(body[j]) not in (ConvLayer, LogicLayer):
@@ -157,15 +156,21 @@ class PackedNetwork:
                                   max_layers, max_rows)), len(body))
         # a tail whose input is too wide to stage row by row: its input comes column-major
         # from the packed layer before it (cl_eval_packed_indexed_columns)
-        self.producer = None
+        self.producer = None     # the layer (or pair of layers) writing the tail's columns
         self.layout = None
         if start != first and first < len(body):
-            prod = _column_producer(body, first)
+            prod = _table_layer_before(body, first)
             rows = [int(body[first].in_dim)] + [int(m.out_dim) for m in body[first:]]
             layout = columns_layout(rows) if prod is not None else None
             if layout is not None:
-                start, self.producer, self.layout = first, body[prod], layout
-                self.prefix = body[:prod]
+                start, self.layout = first, layout
+                # a table layer before the producer is composed into it: its rows are
+                # computed where the producer reads them, never stored
+                pre = _table_layer_before(body, prod)
+                if pre is not None:
+                    self.producer, self.prefix = (body[pre], body[prod]), body[:pre]
+                else:
+                    self.producer, self.prefix = (body[prod],), body[:prod]
         layers = body[start:]
         if self.producer is None:
             self.prefix = body[:start]
@@ -259,32 +264,34 @@ class PackedNetwork:
         return counts
 
     def _call_columns(self, x) -> torch.Tensor:
-        """The wide-input path: the prefix layer by layer, the producer layer written
-        column-major, then the fused tail on that input."""
+        """The wide-input path: the prefix layer by layer, the producer layer (or pair of
+        layers) written column-major, then the fused tail on those columns."""
         if isinstance(x, PackBitsTensor):
             h = PackBitsTensor.from_packed(x.t, x.pad_len)   # the caller's object stays
         else:
             h = PackBitsTensor.from_packed(x)
+        tabs = []
         with torch.no_grad():
             for m in self.prefix:
                 h = m(h)
-            m = self.producer
-            w = getattr(m, "w", None)
-            if w is None:
-                w = m._argmax_slots()
-            ia, ib, gate = m.packed_tables(w)[:3]
+            for m in self.producer:
+                w = getattr(m, "w", None)
+                if w is None:
+                    w = m._argmax_slots()
+                tabs.append(m.packed_tables(w)[:3])
         words, n = h.t, h.num_samples
         _dl._check(words, "x")
         if words.device != self.device:
             raise RuntimeError(f"x is on {words.device}, the network on {self.device}")
         in_rows = words.shape[0]
+        m = self.producer[0]
         expect = m.in_dim if type(m) is LogicLayer else int(np.prod(m.in_shape))
         if in_rows != expect:
             raise RuntimeError(f"the layer before the fused tail gets {in_rows} rows, "
                                f"expects {expect}")
-        if ia.numel() != self.rows[0]:
-            raise RuntimeError(f"the layer before the fused tail has {ia.numel()} outputs, "
-                               f"the tail reads {self.rows[0]}")
+        if tabs[-1][0].numel() != self.rows[0]:
+            raise RuntimeError(f"the layer before the fused tail has {tabs[-1][0].numel()} "
+                               f"outputs, the tail reads {self.rows[0]}")
         row_bytes = words.shape[1] * words.element_size()
         if row_bytes % 4:
             raise RuntimeError("packed rows must be a multiple of 4 bytes")
@@ -292,12 +299,19 @@ class PackedNetwork:
         colmaj = torch.empty((cols, in_words), dtype=torch.int32, device=words.device)
         counts = torch.empty((n, self.k), dtype=torch.int32, device=words.device)
         stream = _dl.stream_of(words)
+        ptrs = [t.data_ptr() for tab in tabs for t in tab]
         with torch.cuda.device(words.device):
-            timing.timed(f"cl_eval_packed_indexed_columns[{in_rows}->{self.rows[0]}]",
-                         lambda: _capi.call(
-                "cl_eval_packed_indexed_columns", words.data_ptr(), ia.data_ptr(),
-                ib.data_ptr(), gate.data_ptr(), colmaj.data_ptr(), in_rows, self.rows[0],
-                row_bytes, in_words, stream))
+            if len(tabs) == 2:
+                mid = tabs[0][0].numel()
+                timing.timed(f"cl_eval_packed_indexed_pair_columns[{in_rows}->{mid}->"
+                             f"{self.rows[0]}]", lambda: _capi.call(
+                    "cl_eval_packed_indexed_pair_columns", words.data_ptr(), *ptrs,
+                    colmaj.data_ptr(), in_rows, mid, self.rows[0], row_bytes, in_words, stream))
+            else:
+                timing.timed(f"cl_eval_packed_indexed_columns[{in_rows}->{self.rows[0]}]",
+                             lambda: _capi.call(
+                    "cl_eval_packed_indexed_columns", words.data_ptr(), *ptrs,
+                    colmaj.data_ptr(), in_rows, self.rows[0], row_bytes, in_words, stream))
             timing.timed(f"cl_packed_network_columns[{self.rows[0]}->{self.rows[-1]}]",
                          lambda: _capi.call(
                 "cl_packed_network_columns", colmaj.data_ptr(), cols, in_words, n,

@@ -563,6 +563,17 @@ int cl_eval_packed_indexed_columns(const void* x, const int32_t* ia, const int32
                                    const uint8_t* gate, void* y, int64_t in_dim, int64_t out_dim,
                                    int64_t row_bytes, int64_t out_words, void* stream);
 
+/* Two packed layers composed, with column-major output: layer 1 (ia1, ib1, gate1: mid_dim
+ * rows from the in_dim rows of x) and layer 2 (ia2, ib2, gate2: out_dim rows from layer 1's)
+ * as cl_eval_packed_indexed twice, layer 1's rows computed where layer 2 reads them instead of
+ * being stored.  Same output as cl_eval_packed_indexed of layer 1 followed by
+ * cl_eval_packed_indexed_columns of layer 2. */
+int cl_eval_packed_indexed_pair_columns(const void* x, const int32_t* ia1, const int32_t* ib1,
+                                        const uint8_t* gate1, const int32_t* ia2,
+                                        const int32_t* ib2, const uint8_t* gate2, void* y,
+                                        int64_t in_dim, int64_t mid_dim, int64_t out_dim,
+                                        int64_t row_bytes, int64_t out_words, void* stream);
+
 int cl_packed_network_columns(const void* x, int64_t cols, int64_t in_words, int64_t nsamples,
                               const uint64_t* tables, const int64_t* rows_host,
                               int64_t num_layers, int64_t k, int32_t* counts, void* stream);

@@ -75,16 +75,17 @@ def conv_oracle_counts(model, words_np, n):
 
 
 def test_packed_network_cfg5_fuses_the_wide_tail(device):
-    """cfg5: conv1 layer by layer, conv2 written column-major, then 25088 -> 16000 -> 16000
-    and the class counts in one launch (two first-layer slots held over the input column);
-    equal to the C oracle and to the whole network layer by layer."""
+    """cfg5: conv1 and conv2 composed into one launch that writes conv2's rows column-major
+    (conv1's rows computed where conv2 reads them), then 25088 -> 16000 -> 16000 and the class
+    counts in one launch (two first-layer slots held over the input column); equal to the C
+    oracle and to the whole network layer by layer."""
     cfg = configs.CONV_CONFIGS["cfg5"]
     model = configs.conv_network(cfg, device=device)
     configs.freeze_argmax(model)
     feats = int(np.prod(cfg.in_shape))
     xw = configs.packed_input_words(feats, 64, device=device)            # 2^12 samples
     net = cl.PackedNetwork(model)
-    assert net.producer is model[1] and len(net.prefix) == 1
+    assert net.producer == (model[0], model[1]) and net.prefix == []
     assert net.rows == [25088, 16000, 16000] and net.layout["split"] == 14336
     x = cl.PackBitsTensor.from_packed(xw)
     counts = net(x)
@@ -94,19 +95,23 @@ def test_packed_network_cfg5_fuses_the_wide_tail(device):
     assert torch.equal(counts, model(cl.PackBitsTensor.from_packed(xw.clone())))
 
 
-def small_conv_net(device, in_shape, c_out, widths, k, seed):
+def small_conv_net(device, in_shape, c_out, widths, k, seed, convs=1, stride=1):
     torch.manual_seed(seed)
-    conv = cl.ConvLayer(in_shape, padding=1, c_out=c_out, ks=3, stride=1, num_chn=1,
-                        num_gates=4)
+    conv, shape = [], in_shape
+    for i in range(convs):
+        conv.append(cl.ConvLayer(shape, padding=1, c_out=c_out, ks=3, stride=stride,
+                                 num_chn=1, num_gates=4))
+        shape = conv[-1].out_shape
     g = torch.Generator().manual_seed(seed)
-    dims = [int(np.prod(conv.out_shape))] + list(widths)
+    dims = [int(np.prod(shape))] + list(widths)
     dense = [cl.LogicLayer(i, o, num_gates=4) for i, o in zip(dims[:-1], dims[1:])]
-    for m in [conv] + dense:
+    for m in conv + dense:
         with torch.no_grad():
             m.weights.copy_(torch.randn(m.weights.shape, generator=g))
             m.gate_sequence.copy_(torch.randint(0, 16, m.gate_sequence.shape,
                                                 generator=g).to(torch.uint8))
-    model = torch.nn.Sequential(conv, torch.nn.Flatten(), *dense, cl.GroupSum(k, 1.0)).to(device)
+    model = torch.nn.Sequential(*conv, torch.nn.Flatten(), *dense,
+                                cl.GroupSum(k, 1.0)).to(device)
     configs.freeze_argmax(model)
     return model
 
@@ -124,7 +129,7 @@ def test_packed_network_wide_tail_matches_oracle(device, in_shape, c_out, widths
     x = cl.PackBitsTensor(torch.as_tensor(rng.integers(0, 2, (n, feats)).astype(bool),
                                           device=device), bits)
     net = cl.PackedNetwork(model)
-    assert net.producer is model[0] and net.layout is not None
+    assert net.producer == (model[0],) and net.layout is not None
     counts = net(x)
     assert counts.shape == (n, k)
     words = np_(x.t)
@@ -142,13 +147,71 @@ def test_packed_network_wide_tail_after_a_dense_producer(device):
     model = frozen_net([(64, 6000), (6000, 3000), (3000, 2000)], 10, 8, 11, device)
     model = torch.nn.Sequential(model[0], torch.nn.Flatten(), model[1], model[2], model[3])
     net = cl.PackedNetwork(model)
-    assert net.producer is model[0] and net.prefix == [] and net.rows == [6000, 3000, 2000]
+    assert net.producer == (model[0],) and net.prefix == [] and net.rows == [6000, 3000, 2000]
     rng = np.random.default_rng(3)
     x = cl.PackBitsTensor(torch.as_tensor(rng.integers(0, 2, (777, 64)).astype(bool),
                                           device=device), 64)
     counts = net(x)
     ref = oracle_counts(model, np_(x.t).view(np.uint64), 777)
     assert np.array_equal(np_(counts), ref)
+
+
+@pytest.mark.parametrize("in_shape,c_out,convs,stride,widths,k,n", [
+    ((3, 16, 16), 32, 2, 1, [4200, 2100], 10, 1000),   # conv, conv composed, 8192 rows
+    ((4, 16, 16), 24, 3, 1, [3100, 1550], 5, 333),     # conv layer by layer, then a pair
+])
+def test_packed_network_composes_two_convs(device, in_shape, c_out, convs, stride, widths, k,
+                                           n):
+    model = small_conv_net(device, in_shape, c_out, widths, k, seed=n, convs=convs,
+                           stride=stride)
+    net = cl.PackedNetwork(model)
+    assert net.producer == (model[convs - 2], model[convs - 1])
+    assert net.prefix == list(model)[:convs - 2]
+    rng = np.random.default_rng(n)
+    feats = int(np.prod(in_shape))
+    x = cl.PackBitsTensor(torch.as_tensor(rng.integers(0, 2, (n, feats)).astype(bool),
+                                          device=device), 64)
+    counts = net(x)
+    ref = conv_oracle_counts(model, np_(x.t).view(np.uint64), n)
+    assert np.array_equal(np_(counts), ref)
+    assert torch.equal(counts, model(cl.PackBitsTensor.from_packed(x.t.clone(), x.pad_len)))
+
+
+@pytest.mark.parametrize("mid,out_dim,out_words,words", [
+    (500, 1000, 1024, 130), (300, 64, 64, 64), (40, 70, 128, 3)])
+def test_eval_packed_indexed_pair_columns_is_two_layers(device, mid, out_dim, out_words, words):
+    """The composed pair equals layer 1 by cl_eval_packed_indexed, then layer 2 written
+    column-major; negative and out-of-range indices in both layers."""
+    from compactlogic_amd import _capi
+    from compactlogic_amd import difflogic_hip as _dl
+    rng = np.random.default_rng(mid + out_dim)
+    in_dim = 200
+    xw = torch.as_tensor(rng.integers(-2**31, 2**31, (in_dim, words)), dtype=torch.int32,
+                         device=device)
+
+    def tables(n_in, n_out):
+        ia = rng.integers(-1, n_in, n_out).astype(np.int32)
+        ib = rng.integers(-1, n_in, n_out).astype(np.int32)
+        ib[::13] = n_in                                   # out of range: a zero row
+        g = rng.integers(0, 16, n_out).astype(np.uint8)
+        return [torch.as_tensor(t, device=device) for t in (ia, ib, g)]
+
+    t1, t2 = tables(in_dim, mid), tables(mid, out_dim)
+    row_bytes = words * 4
+    s = _dl.stream_of(xw)
+    h = torch.empty((mid, words), dtype=torch.int32, device=device)
+    _capi.call("cl_eval_packed_indexed", xw.data_ptr(), *[t.data_ptr() for t in t1], None,
+               h.data_ptr(), in_dim, mid, row_bytes, s)
+    ref = torch.full((words, out_words), 5, dtype=torch.int32, device=device)
+    _capi.call("cl_eval_packed_indexed_columns", h.data_ptr(), *[t.data_ptr() for t in t2],
+               ref.data_ptr(), mid, out_dim, row_bytes, out_words, s)
+    out = torch.full((words, out_words), 7, dtype=torch.int32, device=device)
+    _capi.call("cl_eval_packed_indexed_pair_columns", xw.data_ptr(),
+               *[t.data_ptr() for t in t1 + t2], out.data_ptr(), in_dim, mid, out_dim,
+               row_bytes, out_words, s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert int(out[:, out_dim:].abs().sum()) == 0
 
 
 @pytest.mark.parametrize("out_dim,out_words,words,bits", [
