@@ -100,6 +100,8 @@ SIGNATURES: dict[str, list] = {
     "cl_dense_group_sum_cross_entropy_backward": [_int, _p, _p, _p, _i64, _p, _p, _i64, _f64,
                                                   _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
                                                   _i64, _i64, _i64, _p, _i64, _p],
+    "cl_dense_backward_rows_first": [_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                                     _i64, _i64, _p, _i64, _p, _i64, _p, _p, _p, _i64, _p],
     "cl_plan_locality_order": [ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i64, _i64,
                                ctypes.POINTER(_i32)],
     "cl_packed_bank_layout": [ctypes.POINTER(_i32), ctypes.POINTER(_i32),

@@ -92,6 +92,40 @@ __device__ __forceinline__ T hsum(typename VT<T, N>::type v) {
     }
 }
 
+// The product moments of one run over a lane's U vectors of a whole-batch row, summed over
+// the wave: m1 = sum g*a, m2 = sum g*b, m3 = sum g*a*b.  Every product is rounded before it is
+// added (no contraction into fused multiply-adds), so the kernels that compute a neuron's
+// moments from the same rows (k_wgrad_rows from the stored gradient, k_bwd_rows' first-layer
+// mode from the gradient it holds) produce the same bits.
+template <typename T, int VEC, int U>
+__device__ __forceinline__ void run_moments(const typename VT<T, VEC>::type (&g)[U],
+                                            const typename VT<T, VEC>::type (&a)[U],
+                                            const typename VT<T, VEC>::type (&b)[U], T& m1,
+                                            T& m2, T& m3) {
+#pragma clang fp contract(off)
+    using V = typename VT<T, VEC>::type;
+    T s2 = 0, s3 = 0, s4 = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const V ga = g[u] * a[u];
+        s2 += hsum<T, VEC>(ga);
+        s3 += hsum<T, VEC>(g[u] * b[u]);
+        s4 += hsum<T, VEC>(ga * b[u]);
+    }
+    m1 = wave_total(s2);
+    m2 = wave_total(s3);
+    m3 = wave_total(s4);
+}
+
+// Softmax backward of a slot gradient gp with probability p (0 on lanes past the slots):
+// p * (gp - sum_h p_h gp_h), without contraction (see run_moments).
+template <typename T>
+__device__ __forceinline__ T softmax_back(T p, T gp) {
+#pragma clang fp contract(off)
+    const T pg = p * gp;
+    return p * (gp - wave_total(pg));
+}
+
 template <typename T>
 __device__ __forceinline__ T nan_of() {
     return T(__builtin_nan(""));
@@ -808,25 +842,19 @@ __global__ __launch_bounds__(256) void k_wgrad_rows(const T* __restrict__ x,
             bad = true;
             ab = make_int2(0, 0);
         }
-        T s2 = 0, s3 = 0, s4 = 0;
+        V va[U], vb[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const V va = vld<V>(x + int64_t(ab.x) * B + off[u]);
-            const V vb = vld<V>(x + int64_t(ab.y) * B + off[u]);
-            const V ga = vg[u] * va;
-            s2 += hsum<T, VEC>(ga);
-            s3 += hsum<T, VEC>(vg[u] * vb);
-            s4 += hsum<T, VEC>(ga * vb);
+            va[u] = vld<V>(x + int64_t(ab.x) * B + off[u]);
+            vb[u] = vld<V>(x + int64_t(ab.y) * B + off[u]);
         }
-        const T m1 = wave_total(s2), m2 = wave_total(s3), m3 = wave_total(s4);
+        T m1, m2, m3;
+        run_moments<T, VEC, U>(vg, va, vb, m1, m2, m3);
         const Coef4<T> cf = gate_coef<T>(code);
         const T v = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
         if (lane >= g0 && lane < g1 && lane < G) gp = v;
     }
-    if constexpr (HAS_P) {
-        const T pl = lane < G ? p : T(0);
-        gp = pl * (gp - wave_total(pl * gp));
-    }
+    if constexpr (HAS_P) gp = softmax_back(lane < G ? p : T(0), gp);
     if (lane < G) grad_w[o * G + lane] = bad ? nan_of<T>() : gp;
 }
 
@@ -1158,24 +1186,49 @@ __global__ __launch_bounds__(256) void k_bwd_part(
 // Waves per SIMD the row backward asks the register allocator for: four (at most 128 VGPRs)
 // where the fp32 kernel fits them without spilling (rows of up to 1024 samples); more waves
 // per SIMD keep more rows' gathers in flight, which is what bounds this kernel.
-template <typename T, int U>
-constexpr int bwd_rows_waves() { return sizeof(T) == 4 && U <= 4 ? 4 : 1; }
+#ifndef CL_FIRST_WAVES
+#define CL_FIRST_WAVES 4
+#endif
+#ifndef CL_FIRST_EPI4
+#define CL_FIRST_EPI4 1
+#endif
+template <typename T, int U, bool FIRST = false>
+constexpr int bwd_rows_waves() { return sizeof(T) == 4 && U <= 4 ? (FIRST ? CL_FIRST_WAVES : 4) : 1; }
 
 #ifndef CL_BWD_ROWS_EPI4
 #define CL_BWD_ROWS_EPI4 2
 #endif
-template <typename T, int VEC, int U, bool WANT_GW, bool HAS_P>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_rows_waves<T, U>())))
+
+// The layer before, when its input needs no gradient (the first layer of a network): its
+// logits gradient is a function of the gradient of its output, which is the input gradient
+// the row backward computes, so the row backward finishes it for the neuron of each row
+// instead of storing that gradient (k_bwd_rows with FIRST).  Single-run neurons with the
+// softmax inside; x0 [in_dim, B] is the layer's input, nab its plan's (a, b, run_ptr[o],
+// run_ptr[o + 1]) per neuron.
+template <typename T>
+struct FirstLayer {
+    const T* x0;
+    const int4* nab;
+    const uint8_t* gs;
+    const T* probs;
+    T* grad_w;
+    int64_t in_dim;
+    int64_t num_runs;
+    int G;
+};
+
+template <typename T, int VEC, int U, bool WANT_GW, bool HAS_P, bool FIRST = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_rows_waves<T, U, FIRST>())))
 void k_bwd_rows(
     const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
     const int4* __restrict__ inv_rec, const T* __restrict__ inv_coef,
     const uint8_t* __restrict__ gs, const T* __restrict__ probs,
     const int32_t* __restrict__ run_ptr, T* __restrict__ grad_w, T* __restrict__ gx,
     int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, int G, int64_t nblk,
-    uint32_t gy_magic) {
+    uint32_t gy_magic, FirstLayer<T> first = {}) {
     using V = typename VT<T, VEC>::type;
     using V2 = typename VT<T, 2>::type;
-    constexpr int EPI = U <= 2 ? 2 : U <= 4 ? CL_BWD_ROWS_EPI4 : 1;  // entries per step
+    constexpr int EPI = U <= 2 ? 2 : U <= 4 ? (FIRST ? CL_FIRST_EPI4 : CL_BWD_ROWS_EPI4) : 1;
     const int lane = threadIdx.x & 63;
     const int64_t w = blockIdx.x;
     const int64_t slot = ((w % kXcds) * nblk + w / kXcds) * 4 + wave_id();
@@ -1185,7 +1238,7 @@ void k_bwd_rows(
     const int64_t deg = int64_t(sr.z) - sr.y;
     if (uint64_t(row) >= uint64_t(in_dim) || sr.y < 0 || deg < 0 || sr.z > 2 * num_runs)
         return;  // corrupt slot record: nothing is read or written for it
-    int64_t off[U];
+    int32_t off[U];  // batch offsets (rows of at most 64 * 8 * VEC samples)
     bool in[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1202,6 +1255,14 @@ void k_bwd_rows(
     }
     const int gl = lane < G ? lane : 0;  // slot of this lane in the finalize (clamped)
     bool bad = false;
+    // the first layer's wiring of this neuron, loaded with the rows rather than after them
+    // (uniform: kept in scalar registers through the entry loop)
+    int4 nab1 = make_int4(0, 0, 0, 0);
+    if constexpr (FIRST) {
+        const int4 t = first.nab[row];
+        nab1 = make_int4(__builtin_amdgcn_readfirstlane(t.x), __builtin_amdgcn_readfirstlane(t.y),
+                         __builtin_amdgcn_readfirstlane(t.z), __builtin_amdgcn_readfirstlane(t.w));
+    }
     for (int64_t k = 0; k < deg; k += EPI) {
         int4 cur[EPI];
         V2 ck[EPI];
@@ -1279,9 +1340,42 @@ void k_bwd_rows(
             }
         }
     }
+    if constexpr (FIRST) {
+        // acc is the gradient of the first layer's neuron `row` (what the input-gradient store
+        // below would write); its moments against the neuron's two inputs, in the order of
+        // k_wgrad_rows, give bitwise the logits gradient that kernel computes from the stored
+        // gradient.
+        const bool single = nab1.z >= 0 && nab1.w == nab1.z + 1 && nab1.w <= first.num_runs;
+        const bool ok = single && uint32_t(nab1.x) < uint64_t(first.in_dim) &&
+                        uint32_t(nab1.y) < uint64_t(first.in_dim);
+        const int64_t ra = ok ? nab1.x : 0, rb = ok ? nab1.y : 0;
+        const int gl1 = lane < first.G ? lane : 0;
+        const int code1 = first.gs[row * first.G + gl1];
+        const T p1 = first.probs[row * first.G + gl1];
+        V va[U], vb[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-        if (in[u]) vst_stream<V>(gx + row * B + off[u], bad ? V(nan_of<T>()) : acc[u]);
+        for (int u = 0; u < U; ++u) {
+            va[u] = vld<V>(first.x0 + ra * B + off[u]);
+            vb[u] = vld<V>(first.x0 + rb * B + off[u]);
+        }
+        T s1 = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            acc[u] = in[u] ? acc[u] : V(T(0));
+            s1 += hsum<T, VEC>(acc[u]);
+        }
+        const T m0 = wave_total(s1);
+        T m1, m2, m3;
+        run_moments<T, VEC, U>(acc, va, vb, m1, m2, m3);
+        const Coef4<T> cf = gate_coef<T>(code1);
+        const T v = fma(cf.c3, m3, fma(cf.c2, m2, fma(cf.c1, m1, cf.c0 * m0)));
+        const T gp = softmax_back(lane < first.G ? p1 : T(0), lane < first.G ? v : T(0));
+        if (lane < first.G) first.grad_w[row * first.G + lane] = (bad || !ok) ? nan_of<T>() : gp;
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (in[u]) vst_stream<V>(gx + row * B + off[u], bad ? V(nan_of<T>()) : acc[u]);
+    }
 }
 
 // k_moments: the per-chunk moments of every run, per neuron (used when grad_x is not needed).
@@ -1796,27 +1890,54 @@ extern "C" int cl_dense_backward_part(int dtype, const void* x, const void* grad
 }
 
 namespace {
+// The first layer for k_bwd_rows' FIRST mode, untyped (see FirstLayer).
+struct FirstArgs {
+    const void* x0;
+    const int32_t* nab;
+    const uint8_t* gs;
+    const void* probs;
+    void* grad_w;
+    int64_t in_dim, num_runs, G;
+};
+
 int backward_rows_impl(int dtype, const void* x, const void* grad_y, const int32_t* slot_rec,
                        const int32_t* inv_rec, const void* inv_coef, const uint8_t* gate_seq,
                        const void* probs, const int32_t* run_ptr, void* grad_w, void* grad_x,
                        int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t batch,
-                       int64_t num_gates, uint32_t gy_magic, void* stream) {
+                       int64_t num_gates, uint32_t gy_magic, void* stream,
+                       const FirstArgs* fa = nullptr) {
     if (int rc = check_plan_dims(in_dim, out_dim, batch, num_gates, num_runs)) return rc;
     CL_ARG(num_gates <= 64, "the row backward takes at most 64 slots, got %lld",
            (long long)num_gates);
-    CL_ARG(grad_x, "grad_x is required");
+    CL_ARG(grad_x || fa, "grad_x is required");
     if (in_dim == 0 || batch == 0) return CL_OK;
     CL_ARG(x && grad_y && slot_rec && inv_rec && inv_coef, "null pointer argument");
     CL_ARG(!grad_w || (gate_seq && run_ptr), "grad_w needs gate_seq and run_ptr");
     CL_ARG(aligned(slot_rec, 16) && aligned(inv_rec, 16) && aligned(inv_coef, 8),
            "slot_rec / inv_rec must be 16-byte aligned, inv_coef 8-byte aligned");
+    if (fa) {
+        CL_ARG(!grad_x, "the first layer's logits gradient replaces the input gradient");
+        CL_ARG(grad_w && probs, "the first-layer mode needs grad_w and the softmax");
+        CL_ARG(fa->x0 && fa->nab && fa->gs && fa->probs && fa->grad_w, "null pointer argument");
+        CL_ARG(fa->G >= 1 && fa->G <= 64, "the first layer has 1 to 64 slots, got %lld",
+               (long long)fa->G);
+        CL_ARG(fa->in_dim >= 1 && fa->num_runs >= 0, "bad first-layer shape");
+        CL_ARG(aligned(fa->nab, 16) && aligned(fa->x0, 16), "nab and x0 must be 16-byte aligned");
+    }
     hipStream_t s = as_stream(stream);
     CL_DTYPE_SWITCH(dtype, {
         using T = scalar_t;
         constexpr int W = wide_vec<T>();
         CL_ARG(batch % W == 0 && batch <= 64 * W * 8,
                "the row backward needs batch %% %d == 0 and batch <= %d", W, 64 * W * 8);
-        CL_ARG(all_aligned({x, grad_y, grad_x}), "row buffers must be 16-byte aligned");
+        CL_ARG(all_aligned({x, grad_y}) && (!grad_x || aligned(grad_x, 16)),
+               "row buffers must be 16-byte aligned");
+        FirstLayer<T> first{};
+        if (fa)
+            first = FirstLayer<T>{static_cast<const T*>(fa->x0),
+                                  reinterpret_cast<const int4*>(fa->nab), fa->gs,
+                                  static_cast<const T*>(fa->probs), static_cast<T*>(fa->grad_w),
+                                  fa->in_dim, fa->num_runs, int(fa->G)};
         const int64_t nblk = ceil_div(ceil_div(in_dim, int64_t(4)), int64_t(kXcds));
         CL_ARG(kXcds * nblk < (int64_t(1) << 31), "too many rows");
         const unsigned grid = unsigned(kXcds * nblk);
@@ -1838,7 +1959,12 @@ int backward_rows_impl(int dtype, const void* x, const void* grad_y, const int32
             };
             using Y = std::true_type;
             using N = std::false_type;
-            if (grad_w && probs) launch(Y{}, Y{});
+            if (fa)
+                k_bwd_rows<T, W, U, true, true, true>
+                    <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq, pr, run_ptr, gw,
+                                          nullptr, in_dim, out_dim, num_runs, batch,
+                                          int(num_gates), nblk, gy_magic, first);
+            else if (grad_w && probs) launch(Y{}, Y{});
             else if (grad_w) launch(Y{}, N{});
             else launch(N{}, N{});
         };
@@ -1851,6 +1977,20 @@ int backward_rows_impl(int dtype, const void* x, const void* grad_y, const int32
     return check_launch("cl_dense_backward_rows");
 }
 }  // namespace
+
+extern "C" int cl_dense_backward_rows_first(
+    int dtype, const void* x, const void* grad_y, const int32_t* slot_rec,
+    const int32_t* inv_rec, const void* inv_coef, const uint8_t* gate_seq, const void* probs,
+    const int32_t* run_ptr, void* grad_w, int64_t in_dim, int64_t out_dim, int64_t num_runs,
+    int64_t batch, int64_t num_gates, const void* x0, int64_t in0_dim, const int32_t* nab0,
+    int64_t num_runs0, const uint8_t* gate_seq0, const void* probs0, void* grad_w0,
+    int64_t num_gates0, void* stream) {
+    clear_error();
+    const FirstArgs fa{x0, nab0, gate_seq0, probs0, grad_w0, in0_dim, num_runs0, num_gates0};
+    return backward_rows_impl(dtype, x, grad_y, slot_rec, inv_rec, inv_coef, gate_seq, probs,
+                              run_ptr, grad_w, nullptr, in_dim, out_dim, num_runs, batch,
+                              num_gates, 0, stream, &fa);
+}
 
 extern "C" int cl_dense_backward_rows(int dtype, const void* x, const void* grad_y,
                                       const int32_t* slot_rec, const int32_t* inv_rec,

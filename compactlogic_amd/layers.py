@@ -139,7 +139,8 @@ class LogicLayerRunsFunction(torch.autograd.Function):
     row_backward = True
 
     @staticmethod
-    def forward(ctx, x, w, gate_sequence, plan: RunPlan, softmax: bool = False):
+    def forward(ctx, x, w, gate_sequence, plan: RunPlan, softmax: bool = False,
+                side: dict | None = None):
         _dl._check(x, "x")
         if w.dtype != x.dtype:
             raise RuntimeError("w must have the dtype of x")
@@ -163,6 +164,8 @@ class LogicLayerRunsFunction(torch.autograd.Function):
                     plan.num_runs, batch, plan.num_gates, stream))
             ctx.save_for_backward(x, inv_coef, gate_sequence, probs)
             ctx.plan = plan
+            if side is not None:
+                side["probs"] = probs
             return y
         coef = torch.empty((plan.num_runs, 4), dtype=x.dtype, device=dev)
         with torch.cuda.device(dev):
@@ -177,6 +180,8 @@ class LogicLayerRunsFunction(torch.autograd.Function):
                 batch, stream))
         ctx.save_for_backward(x, inv_coef, gate_sequence, probs)
         ctx.plan = plan
+        if side is not None:
+            side["probs"] = probs
         return y
 
     @staticmethod
@@ -236,7 +241,62 @@ class LogicLayerRunsFunction(torch.autograd.Function):
                     gate_sequence.data_ptr(), _dl.ptr(probs), plan.run_ptr.data_ptr(),
                     plan.run_ab.data_ptr(), plan.run_gl.data_ptr(), grad_w.data_ptr(),
                     plan.in_dim, plan.out_dim, plan.num_runs, batch, plan.num_gates, stream))
-        return grad_x, grad_w, None, None, None
+        return grad_x, grad_w, None, None, None, None
+
+
+def _row_backward_fits(plan: RunPlan, x: torch.Tensor) -> bool:
+    """Whether cl_dense_backward_rows takes this layer at this batch (x: [in_dim, batch])."""
+    wide = 16 // x.element_size()
+    batch = x.shape[1]
+    return (plan.single_run and plan.num_gates <= 64 and 0 < batch <= 64 * wide * 8
+            and batch % wide == 0)
+
+
+class LogicLayerFirstPairFunction(torch.autograd.Function):
+    """The second dense layer of a network together with the logits gradient of the first,
+    whose input needs no gradient (compactlogic/compactlogic.py:83-118 applied to two layers in
+    turn).  The forward is the second layer's (its input, the first layer's output y1, is
+    taken as data); the backward is the second layer's row backward, which also finishes the
+    first layer's logits gradient from the gradient of y1 as it computes it
+    (cl_dense_backward_rows_first), so that gradient [out_dim1, batch] is never stored and
+    the first layer's weight-gradient pass never runs.  Gradients are bitwise those of the two
+    layers' own autograd steps.  No counterpart in the reference."""
+
+    @staticmethod
+    def forward(ctx, y1, w2, gate_sequence2, plan2: RunPlan, w1, x0, probs1, gate_sequence1,
+                plan1: RunPlan):
+        y = torch.empty((plan2.out_dim, y1.shape[1]), dtype=y1.dtype, device=y1.device)
+        inv_coef = torch.empty((2 * plan2.num_runs, 2), dtype=y1.dtype, device=y1.device)
+        probs2 = torch.empty_like(w2)
+        w2 = w2.contiguous()
+        with torch.cuda.device(y1.device):
+            timing.timed(f"cl_dense_forward_fused[{plan2.in_dim}->{plan2.out_dim}]", lambda: _capi.call(
+                "cl_dense_forward_fused", _dl.dtype_code(y1), y1.data_ptr(), w2.data_ptr(), 1,
+                gate_sequence2.data_ptr(), plan2.nab.data_ptr(), plan2.inv_pos.data_ptr(),
+                probs2.data_ptr(), inv_coef.data_ptr(), y.data_ptr(), plan2.in_dim,
+                plan2.out_dim, plan2.num_runs, y1.shape[1], plan2.num_gates, _dl.stream_of(y1)))
+        ctx.save_for_backward(y1, inv_coef, gate_sequence2, probs2, x0, probs1, gate_sequence1)
+        ctx.plan2, ctx.plan1 = plan2, plan1
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        y1, inv_coef, gs2, probs2, x0, probs1, gs1 = ctx.saved_tensors
+        plan2, plan1 = ctx.plan2, ctx.plan1
+        grad_y = grad_y.contiguous()
+        dev = y1.device
+        grad_w2 = torch.empty((plan2.out_dim, plan2.num_gates), dtype=y1.dtype, device=dev)
+        grad_w1 = torch.empty((plan1.out_dim, plan1.num_gates), dtype=y1.dtype, device=dev)
+        with torch.cuda.device(dev):
+            timing.timed(f"cl_dense_backward_rows_first[{plan2.in_dim}->{plan2.out_dim}]", lambda: _capi.call(
+                "cl_dense_backward_rows_first", _dl.dtype_code(y1), y1.data_ptr(),
+                grad_y.data_ptr(), plan2.slot_rec.data_ptr(), plan2.inv_rec.data_ptr(),
+                inv_coef.data_ptr(), gs2.data_ptr(), probs2.data_ptr(), plan2.run_ptr.data_ptr(),
+                grad_w2.data_ptr(), plan2.in_dim, plan2.out_dim, plan2.num_runs, y1.shape[1],
+                plan2.num_gates, x0.data_ptr(), plan1.in_dim, plan1.nab.data_ptr(),
+                plan1.num_runs, gs1.data_ptr(), probs1.data_ptr(), grad_w1.data_ptr(),
+                plan1.num_gates, _dl.stream_of(y1)))
+        return None, grad_w2, None, None, grad_w1, None, None, None, None
 
 
 def _transpose_rows(x: torch.Tensor) -> torch.Tensor:
@@ -389,6 +449,7 @@ class LogicLayer(torch.nn.Module):
         """Training forward: x [batch, in_dim] -> [batch, out_dim] (a transposed view of the
         kernel's [out_dim, batch] output, as in the reference, :83-118)."""
         assert x.ndim == 2, x.ndim
+        x_in = x
         x = to_rows(x)
         assert x.shape[0] == self.in_dim, (x.shape, self.in_dim)
         if x.dtype == torch.float16:
@@ -402,11 +463,50 @@ class LogicLayer(torch.nn.Module):
         plan = self.run_plan()
         if self.weights.dtype == x.dtype:
             # softmax(weights) and its backward run inside the kernels
-            y = LogicLayerRunsFunction.apply(x, self.weights, self.gate_sequence, plan, True)
+            pair = self._first_pair(x_in, x, plan)
+            if pair is not None:
+                return pair.transpose(0, 1)
+            side = {} if self._may_lead_pair(x, plan) else None
+            y = LogicLayerRunsFunction.apply(x, self.weights, self.gate_sequence, plan, True, side)
+            out = y.transpose(0, 1)
+            if side is not None and side.get("probs") is not None:
+                # the next dense layer may finish this layer's logits gradient
+                out._cl_first = (self, x, side["probs"], plan, out._version)
+            return out
         else:
             w = torch.nn.functional.softmax(self.weights, dim=-1).to(x.dtype)
             y = LogicLayerRunsFunction.apply(x, w, self.gate_sequence, plan, False)
         return y.transpose(0, 1)
+
+    # Whether the first-layer pairing applies (LogicLayerFirstPairFunction); a class switch.
+    first_pair = True
+
+    def _may_lead_pair(self, x: torch.Tensor, plan: RunPlan) -> bool:
+        """This layer's output may feed the next layer's pair step: its input needs no
+        gradient, its logits do, and its neurons are single runs of at most 64 slots."""
+        return (LogicLayer.first_pair and type(self) is LogicLayer and torch.is_grad_enabled()
+                and not x.requires_grad and self.weights.requires_grad
+                and x.dtype in (torch.float32, torch.float64) and _row_backward_fits(plan, x))
+
+    def _first_pair(self, x_in: torch.Tensor, x: torch.Tensor, plan: RunPlan):
+        """This layer's output through LogicLayerFirstPairFunction when x_in is the output of
+        a first layer (tagged by its forward, unmodified since) and this layer's row backward
+        applies; else None."""
+        tag = getattr(x_in, "_cl_first", None)
+        if tag is None or not LogicLayer.first_pair or type(self) is not LogicLayer:
+            return None
+        first, x0, probs1, plan1, version = tag
+        # the pair gives y1 no gradient of its own: not when the caller retains or hooks it
+        if x_in.retains_grad or getattr(x_in, "_backward_hooks", None):
+            return None
+        if (x_in._version != version or not torch.is_grad_enabled()
+                or not self.weights.requires_grad or not first.weights.requires_grad
+                or first.weights.dtype != x.dtype or x.data_ptr() != x_in.data_ptr()
+                or plan1.out_dim != plan.in_dim or not _row_backward_fits(plan, x)):
+            return None
+        return LogicLayerFirstPairFunction.apply(
+            x.detach(), self.weights, self.gate_sequence, plan, first.weights, x0, probs1,
+            first.gate_sequence, plan1)
 
     @torch.no_grad()
     def forward_cuda_eval(self, x):

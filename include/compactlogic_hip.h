@@ -224,6 +224,25 @@ int cl_dense_backward_rows(int dtype, const void* x, const void* grad_y, const i
                            void* grad_x, int64_t in_dim, int64_t out_dim, int64_t num_runs,
                            int64_t batch, int64_t num_gates, void* stream);
 
+/* cl_dense_backward_rows with the softmax (probs given) and grad_w, for a layer whose input x
+ * is the output of a first dense layer whose own input needs no gradient (no counterpart in
+ * the reference: the weight-gradient pass of that first layer, cl_dense_weight_grad, folded
+ * into this one).  The input gradient is not stored: each row's wave turns it into the
+ * first layer's logits gradient for the neuron of that row, grad_w0 (T [in_dim, num_gates0]),
+ * bitwise what cl_dense_weight_grad computes from the stored input gradient.  x0: the first
+ * layer's input rows (T [in0_dim, batch]); nab0, gate_seq0, probs0: its plan's
+ * (a, b, run_ptr[o], run_ptr[o + 1]) per neuron (int32 [in_dim, 4]), its opcodes and its
+ * softmax; every neuron of the first layer a single run of at most 64 slots (else NaN). */
+int cl_dense_backward_rows_first(int dtype, const void* x, const void* grad_y,
+                                 const int32_t* slot_rec, const int32_t* inv_rec,
+                                 const void* inv_coef, const uint8_t* gate_seq,
+                                 const void* probs, const int32_t* run_ptr, void* grad_w,
+                                 int64_t in_dim, int64_t out_dim, int64_t num_runs,
+                                 int64_t batch, int64_t num_gates, const void* x0,
+                                 int64_t in0_dim, const int32_t* nab0, int64_t num_runs0,
+                                 const uint8_t* gate_seq0, const void* probs0, void* grad_w0,
+                                 int64_t num_gates0, void* stream);
+
 /* Weight gradient from the moments: grad_w[o, g] = (c0, c1, c2, c3)[gate_seq[o,g]] . (moments
  * of g's run summed over the chunks in chunk order); with `probs` (not NULL) followed by the
  * softmax backward, giving the gradient of the logits. */
