@@ -122,9 +122,9 @@ SIGNATURES: dict[str, list] = {
     "cl_packed_network_columns_layout": [ctypes.POINTER(_i64), _i64, ctypes.POINTER(_i64),
                                          ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                          ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
-    "cl_eval_packed_indexed_columns": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
-    "cl_eval_packed_indexed_pair_columns": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
-                                            _i64, _i64, _p],
+    "cl_eval_packed_indexed_columns": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "cl_eval_packed_indexed_pair_columns": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
+                                            _i64, _i64, _i64, _p],
     "cl_packed_network_columns": [_p, _i64, _i64, _i64, _p, ctypes.POINTER(_i64), _i64, _i64,
                                   _p, _p],
 }

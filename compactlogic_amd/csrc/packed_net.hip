@@ -515,8 +515,10 @@ __global__ __launch_bounds__(kNetThreads) void k_packed_net_cols(
 }
 
 // Packed layers from resolved index tables with column-major output (the input layout of
-// k_packed_net_cols): y[c * out_words + o] = word c of row o of the last layer, 0 for rows
-// out_dim <= o < out_words.  A layer's row o is op_{g[o]}(row ia[o], row ib[o]) of its input,
+// k_packed_net_cols): y[c * out_words + p] = word c of row order[p] (row p without an order)
+// of the last layer, 0 for positions out_dim <= p < out_words.  The order only changes which
+// rows run together: rows that read the same blocks of input rows, placed next to each other,
+// keep the input words a column tile needs within one XCD's L2.  A layer's row o is op_{g[o]}(row ia[o], row ib[o]) of its input,
 // a negative index reading a zero row and an index past the input's rows making row o zero
 // (as k_eval_packed_idx).  With PAIR the kernel evaluates two layers composed, the first
 // (t1) on x and the second (t2) on the first's rows, computing each first-layer row the
@@ -542,6 +544,9 @@ constexpr int kColRows = 64;
 #ifndef CL_COLS_PAIR_RB
 #define CL_COLS_PAIR_RB 8
 #endif
+#ifndef CL_COLS_NT_STORE
+#define CL_COLS_NT_STORE 1
+#endif
 
 // Truth table of a gate whose input a (tt_a0) or b (tt_b0) is held at zero: the opcode
 // that gives the same words without masking the operand (bits MSB first over AB = 00, 01,
@@ -558,6 +563,7 @@ __device__ __forceinline__ uint32_t tt_b0(uint32_t g) {
 template <int W, bool PAIR>
 __global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __restrict__ x,
                                                           PackedTabs t1, PackedTabs t2,
+                                                          const int32_t* __restrict__ order,
                                                           uint32_t* __restrict__ y,
                                                           int64_t out_dim, int64_t cols,
                                                           int64_t out_words, int64_t row_tiles,
@@ -581,9 +587,13 @@ __global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __rest
     int32_t src[NR];
     uint32_t ops = 0;  // output opcode | first-layer opcodes << 4, << 8
     {
-        const int64_t o = o0 + w * R + lane;
-        int64_t a = -1, b = -1;
-        const bool row = lane < R && o < out_dim;
+        const int64_t p = o0 + w * R + lane;  // output position; the layer row order[p]
+        int64_t o = p, a = -1, b = -1;
+        bool row = lane < R && p < out_dim;
+        if (row && order) {
+            o = order[p];
+            row = uint64_t(o) < uint64_t(out_dim);  // a corrupt entry writes zeros
+        }
         if (row) {
             a = tl.ia[o];
             b = tl.ib[o];
@@ -661,8 +671,14 @@ __global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __rest
         for (int j = 0; j < W / 4; ++j) {
             const int cw = w * (W / 4) + j;
             const int64_t c = c0 + cw;
-            // read once, by the fused pass: bypass the caches
-            if (c < cols) __builtin_nontemporal_store(tile[lane][cw], y + c * out_words + o);
+            if (c < cols) {
+#if CL_COLS_NT_STORE
+                // read once, by the fused pass: bypass the caches
+                __builtin_nontemporal_store(tile[lane][cw], y + c * out_words + o);
+#else
+                y[c * out_words + o] = tile[lane][cw];
+#endif
+            }
         }
     }
 }
@@ -903,8 +919,9 @@ extern "C" int cl_packed_network_columns_layout(const int64_t* rows_host, int64_
 }
 
 namespace {
-int launch_packed_cols(const void* x, const PackedTabs& t1, const PackedTabs* t2, void* y,
-                       int64_t out_dim, int64_t row_bytes, int64_t out_words, void* stream) {
+int launch_packed_cols(const void* x, const PackedTabs& t1, const PackedTabs* t2,
+                       const int32_t* order, void* y, int64_t out_dim, int64_t row_bytes,
+                       int64_t out_words, void* stream) {
     CL_ARG(row_bytes % 4 == 0, "packed rows must be a multiple of 4 bytes");
     CL_ARG(out_words >= out_dim, "out_words (%lld) must be at least out_dim (%lld)",
            (long long)out_words, (long long)out_dim);
@@ -920,39 +937,42 @@ int launch_packed_cols(const void* x, const PackedTabs& t1, const PackedTabs* t2
     auto* ys = static_cast<uint32_t*>(y);
     if (t2)
         k_eval_packed_cols<kColWords, true><<<grid, 256, 0, as_stream(stream)>>>(
-            xs, t1, *t2, ys, out_dim, cols, out_words, row_tiles, per_xcd);
+            xs, t1, *t2, order, ys, out_dim, cols, out_words, row_tiles, per_xcd);
     else
         k_eval_packed_cols<kColWords, false><<<grid, 256, 0, as_stream(stream)>>>(
-            xs, t1, t1, ys, out_dim, cols, out_words, row_tiles, per_xcd);
+            xs, t1, t1, order, ys, out_dim, cols, out_words, row_tiles, per_xcd);
     return CL_OK;
 }
 }  // namespace
 
 extern "C" int cl_eval_packed_indexed_columns(const void* x, const int32_t* ia,
-                                              const int32_t* ib, const uint8_t* gate, void* y,
-                                              int64_t in_dim, int64_t out_dim, int64_t row_bytes,
+                                              const int32_t* ib, const uint8_t* gate,
+                                              const int32_t* order, void* y, int64_t in_dim,
+                                              int64_t out_dim, int64_t row_bytes,
                                               int64_t out_words, void* stream) {
     clear_error();
     CL_ARG(in_dim >= 0 && out_dim >= 0 && row_bytes >= 0, "negative shape");
     CL_ARG(out_dim == 0 || in_dim > 0, "in_dim is 0 but out_dim > 0");
     CL_ARG(out_dim == 0 || (ia && ib && gate), "null pointer argument");
     const PackedTabs t{ia, ib, gate, in_dim};
-    if (int rc = launch_packed_cols(x, t, nullptr, y, out_dim, row_bytes, out_words, stream))
+    if (int rc = launch_packed_cols(x, t, nullptr, order, y, out_dim, row_bytes, out_words,
+                                    stream))
         return rc;
     return check_launch("cl_eval_packed_indexed_columns");
 }
 
 extern "C" int cl_eval_packed_indexed_pair_columns(
     const void* x, const int32_t* ia1, const int32_t* ib1, const uint8_t* gate1,
-    const int32_t* ia2, const int32_t* ib2, const uint8_t* gate2, void* y, int64_t in_dim,
-    int64_t mid_dim, int64_t out_dim, int64_t row_bytes, int64_t out_words, void* stream) {
+    const int32_t* ia2, const int32_t* ib2, const uint8_t* gate2, const int32_t* order, void* y,
+    int64_t in_dim, int64_t mid_dim, int64_t out_dim, int64_t row_bytes, int64_t out_words,
+    void* stream) {
     clear_error();
     CL_ARG(in_dim >= 0 && mid_dim >= 0 && out_dim >= 0 && row_bytes >= 0, "negative shape");
     CL_ARG(out_dim == 0 || (mid_dim > 0 && in_dim > 0), "an empty layer feeds out_dim > 0 rows");
     CL_ARG(out_dim == 0 || (ia1 && ib1 && gate1 && ia2 && ib2 && gate2),
            "null pointer argument");
     const PackedTabs t1{ia1, ib1, gate1, in_dim}, t2{ia2, ib2, gate2, mid_dim};
-    if (int rc = launch_packed_cols(x, t1, &t2, y, out_dim, row_bytes, out_words, stream))
+    if (int rc = launch_packed_cols(x, t1, &t2, order, y, out_dim, row_bytes, out_words, stream))
         return rc;
     return check_launch("cl_eval_packed_indexed_pair_columns");
 }

@@ -107,6 +107,41 @@ def columns_layout(rows: list) -> dict | None:
             "base": list(base)}
 
 
+def producer_order(tabs: list, in_rows: int) -> np.ndarray:
+    """Order in which the column producer evaluates its rows (int32, a permutation): rows
+    sorted by the sorted tuple of the blocks (in_rows // 16 rows each) of the input rows they
+    read, ties in row order.  Rows reading the same input blocks then run together, so the
+    input words of a column tile they need stay in one XCD's L2.  tabs: the (ia, ib) index
+    arrays of the producer's layers (one, or two composed, the second reading the first's
+    rows); a negative or out-of-range index reads nothing."""
+    blk = max(1, in_rows // 16)
+    none = in_rows // blk + 1
+
+    def blocks(rows, n):
+        ok = (rows >= 0) & (rows < n)
+        return ok, np.where(ok, rows, 0)
+
+    if len(tabs) == 1:
+        ia, ib = tabs[0]
+        cols = []
+        for r in (ia, ib):
+            ok, rr = blocks(r, in_rows)
+            cols.append(np.where(ok, rr // blk, none))
+    else:
+        (ia1, ib1), (ia2, ib2) = tabs
+        mid = ia1.size
+        cols = []
+        for r2 in (ia2, ib2):
+            ok2, p = blocks(r2, mid)
+            for r1 in (ia1, ib1):
+                ok1, rr = blocks(r1[p], in_rows)
+                cols.append(np.where(ok2 & ok1, rr // blk, none))
+    key = np.sort(np.stack(cols, 1), axis=1)
+    n = key.shape[0]
+    return np.lexsort((np.arange(n),) + tuple(key[:, j] for j in reversed(range(key.shape[1])))
+                      ).astype(np.int32)
+
+
 def _table_layer_before(body: list, j: int):
     """Index of the module before body[j] (Flatten modules pass a PackBitsTensor through
     unchanged) when it is a packed layer from index tables (ConvLayer or LogicLayer); else
@@ -202,6 +237,24 @@ class PackedNetwork:
                 wiring.append((a.cpu().numpy(), b.cpu().numpy(), g.cpu().numpy(), a.device))
             prev_pos = np.arange(self.rows[0], dtype=np.int64)   # input rows stay in place
             lay = self.layout
+            self.col_order = None
+            if self.producer is not None:
+                # the producer writes its rows in producer_order; input row r of the tail is
+                # then at position inv[r] of a column
+                tabs = []
+                for m in self.producer:
+                    w = getattr(m, "w", None)
+                    if w is None:
+                        w = m._argmax_slots()
+                    ia, ib = m.packed_tables(w)[:2]
+                    tabs.append((ia.cpu().numpy().astype(np.int64),
+                                 ib.cpu().numpy().astype(np.int64)))
+                m0 = self.producer[0]
+                in_rows = m0.in_dim if type(m0) is LogicLayer else int(np.prod(m0.in_shape))
+                order = producer_order(tabs, in_rows)
+                prev_pos = np.empty(self.rows[0], dtype=np.int64)
+                prev_pos[order] = np.arange(self.rows[0], dtype=np.int64)
+                self.col_order = torch.as_tensor(order, device=layers[0].weights.device)
             for i, (m, (a, b, g, dev)) in enumerate(zip(layers, wiring)):
                 pa, pb = prev_pos[a], prev_pos[b]
                 if not bank_aware:
@@ -301,16 +354,17 @@ class PackedNetwork:
         stream = _dl.stream_of(words)
         ptrs = [t.data_ptr() for tab in tabs for t in tab]
         with torch.cuda.device(words.device):
+            order = self.col_order.data_ptr()
             if len(tabs) == 2:
                 mid = tabs[0][0].numel()
                 timing.timed(f"cl_eval_packed_indexed_pair_columns[{in_rows}->{mid}->"
                              f"{self.rows[0]}]", lambda: _capi.call(
-                    "cl_eval_packed_indexed_pair_columns", words.data_ptr(), *ptrs,
+                    "cl_eval_packed_indexed_pair_columns", words.data_ptr(), *ptrs, order,
                     colmaj.data_ptr(), in_rows, mid, self.rows[0], row_bytes, in_words, stream))
             else:
                 timing.timed(f"cl_eval_packed_indexed_columns[{in_rows}->{self.rows[0]}]",
                              lambda: _capi.call(
-                    "cl_eval_packed_indexed_columns", words.data_ptr(), *ptrs,
+                    "cl_eval_packed_indexed_columns", words.data_ptr(), *ptrs, order,
                     colmaj.data_ptr(), in_rows, self.rows[0], row_bytes, in_words, stream))
             timing.timed(f"cl_packed_network_columns[{self.rows[0]}->{self.rows[-1]}]",
                          lambda: _capi.call(

@@ -574,13 +574,17 @@ int cl_packed_network_columns_layout(const int64_t* rows_host, int64_t num_layer
                                      int64_t* applies, int64_t* in_words, int64_t* split,
                                      int64_t* hold_base, int64_t* base);
 
-/* Packed layer from resolved index tables, as cl_eval_packed_indexed (without the order), with
- * column-major output: y[c * out_words + o] for the row_bytes / 4 32-bit columns c and rows
- * o < out_words; rows out_dim <= o < out_words are zero.  The producer of the wide-input fused
- * pass's input (out_words = its in_words). */
+/* Packed layer from resolved index tables, as cl_eval_packed_indexed, with column-major
+ * output: y[c * out_words + p] is word c (of the row_bytes / 4 32-bit columns) of row order[p]
+ * (row p when order is NULL) for positions p < out_dim, zero for out_dim <= p < out_words.
+ * order: a permutation of the out_dim rows (an entry out of range writes zeros); rows that
+ * read the same input rows placed together keep those rows in one XCD's L2.  The producer of
+ * the wide-input fused pass's input (out_words = its in_words; the pass's tables address
+ * input positions p). */
 int cl_eval_packed_indexed_columns(const void* x, const int32_t* ia, const int32_t* ib,
-                                   const uint8_t* gate, void* y, int64_t in_dim, int64_t out_dim,
-                                   int64_t row_bytes, int64_t out_words, void* stream);
+                                   const uint8_t* gate, const int32_t* order, void* y,
+                                   int64_t in_dim, int64_t out_dim, int64_t row_bytes,
+                                   int64_t out_words, void* stream);
 
 /* Two packed layers composed, with column-major output: layer 1 (ia1, ib1, gate1: mid_dim
  * rows from the in_dim rows of x) and layer 2 (ia2, ib2, gate2: out_dim rows from layer 1's)
@@ -589,9 +593,10 @@ int cl_eval_packed_indexed_columns(const void* x, const int32_t* ia, const int32
  * cl_eval_packed_indexed_columns of layer 2. */
 int cl_eval_packed_indexed_pair_columns(const void* x, const int32_t* ia1, const int32_t* ib1,
                                         const uint8_t* gate1, const int32_t* ia2,
-                                        const int32_t* ib2, const uint8_t* gate2, void* y,
-                                        int64_t in_dim, int64_t mid_dim, int64_t out_dim,
-                                        int64_t row_bytes, int64_t out_words, void* stream);
+                                        const int32_t* ib2, const uint8_t* gate2,
+                                        const int32_t* order, void* y, int64_t in_dim,
+                                        int64_t mid_dim, int64_t out_dim, int64_t row_bytes,
+                                        int64_t out_words, void* stream);
 
 int cl_packed_network_columns(const void* x, int64_t cols, int64_t in_words, int64_t nsamples,
                               const uint64_t* tables, const int64_t* rows_host,

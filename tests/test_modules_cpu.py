@@ -642,6 +642,36 @@ def test_columns_layout_rejects_what_does_not_fit(rows):
     assert columns_layout(rows) is None
 
 
+@pytest.mark.parametrize("pair", [False, True])
+def test_producer_order_groups_rows_by_input_blocks(pair):
+    """The column producer's row order is a permutation along which the sorted input-block
+    tuples of the rows never decrease (a reading rows from the same blocks run together), ties
+    kept in row order; negative and out-of-range indices count as no input."""
+    from compactlogic_amd.packed_net import producer_order
+    rng = np.random.default_rng(int(pair))
+    in_rows, mid, out = 1600, 900, 700
+    ia1, ib1 = rng.integers(-1, in_rows + 1, mid), rng.integers(-1, in_rows + 1, mid)
+    ia2, ib2 = rng.integers(-1, mid + 1, out), rng.integers(-1, mid + 1, out)
+    tabs = [(ia1, ib1), (ia2, ib2)] if pair else [(ia2 % in_rows, ib1[:out])]
+    order = producer_order(tabs, in_rows)
+    assert sorted(order.tolist()) == list(range(out))
+    blk, none = in_rows // 16, in_rows // (in_rows // 16) + 1
+
+    def key(o):
+        if not pair:
+            rows = [tabs[0][0][o], tabs[0][1][o]]
+        else:
+            rows = []
+            for p in (ia2[o], ib2[o]):
+                for r1 in (ia1, ib1):
+                    rows.append(r1[p] if 0 <= p < mid else -1)
+        return tuple(sorted(r // blk if 0 <= r < in_rows else none for r in rows))
+
+    keys = [key(o) for o in order.tolist()]
+    assert all(keys[i] < keys[i + 1] or (keys[i] == keys[i + 1] and order[i] < order[i + 1])
+               for i in range(out - 1))
+
+
 def test_columns_layout_cfg5():
     """cfg5's tail: the input column takes words [0, 25088), the first layer's slots 0-13 the
     next 14336 words, its slots 14-15 are held and written over the input's first 2048 words,

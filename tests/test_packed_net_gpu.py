@@ -203,12 +203,13 @@ def test_eval_packed_indexed_pair_columns_is_two_layers(device, mid, out_dim, ou
     _capi.call("cl_eval_packed_indexed", xw.data_ptr(), *[t.data_ptr() for t in t1], None,
                h.data_ptr(), in_dim, mid, row_bytes, s)
     ref = torch.full((words, out_words), 5, dtype=torch.int32, device=device)
+    order = torch.as_tensor(rng.permutation(out_dim).astype(np.int32), device=device)
     _capi.call("cl_eval_packed_indexed_columns", h.data_ptr(), *[t.data_ptr() for t in t2],
-               ref.data_ptr(), mid, out_dim, row_bytes, out_words, s)
+               order.data_ptr(), ref.data_ptr(), mid, out_dim, row_bytes, out_words, s)
     out = torch.full((words, out_words), 7, dtype=torch.int32, device=device)
     _capi.call("cl_eval_packed_indexed_pair_columns", xw.data_ptr(),
-               *[t.data_ptr() for t in t1 + t2], out.data_ptr(), in_dim, mid, out_dim,
-               row_bytes, out_words, s)
+               *[t.data_ptr() for t in t1 + t2], order.data_ptr(), out.data_ptr(), in_dim, mid,
+               out_dim, row_bytes, out_words, s)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
     assert int(out[:, out_dim:].abs().sum()) == 0
@@ -238,10 +239,18 @@ def test_eval_packed_indexed_columns_is_the_transposed_layer(device, out_dim, ou
                _dl.stream_of(xw))
     out = torch.full((xw.shape[1], out_words), 7, dtype=torch.int32, device=device)
     _capi.call("cl_eval_packed_indexed_columns", xw.data_ptr(), ia_t.data_ptr(),
-               ib_t.data_ptr(), gate.data_ptr(), out.data_ptr(), in_dim, out_dim, row_bytes,
-               out_words, _dl.stream_of(xw))
+               ib_t.data_ptr(), gate.data_ptr(), None, out.data_ptr(), in_dim, out_dim,
+               row_bytes, out_words, _dl.stream_of(xw))
     torch.cuda.synchronize()
     assert torch.equal(out[:, :out_dim], ref.T)
+    assert int(out[:, out_dim:].abs().sum()) == 0
+    # with a row order: position p holds row order[p]
+    order = torch.as_tensor(rng.permutation(out_dim).astype(np.int32), device=device)
+    _capi.call("cl_eval_packed_indexed_columns", xw.data_ptr(), ia_t.data_ptr(),
+               ib_t.data_ptr(), gate.data_ptr(), order.data_ptr(), out.data_ptr(), in_dim,
+               out_dim, row_bytes, out_words, _dl.stream_of(xw))
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :out_dim], ref.T[:, order.long()])
     assert int(out[:, out_dim:].abs().sum()) == 0
 
 
