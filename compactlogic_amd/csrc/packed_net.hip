@@ -540,7 +540,11 @@ struct PackedTabs {
     int64_t in;  // rows of the layer's input
 };
 
-constexpr int kColRows = 64;
+#ifndef CL_COLS_ROWS
+#define CL_COLS_ROWS 64
+#endif
+constexpr int kColRows = CL_COLS_ROWS;  // rows per workgroup (16 per wave)
+constexpr int kColThreads = kColRows * 4;
 #ifndef CL_COLS_PAIR_RB
 #define CL_COLS_PAIR_RB 8
 #endif
@@ -561,7 +565,7 @@ __device__ __forceinline__ uint32_t tt_b0(uint32_t g) {
 }
 
 template <int W, bool PAIR>
-__global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __restrict__ x,
+__global__ __launch_bounds__(kColThreads) void k_eval_packed_cols(const uint32_t* __restrict__ x,
                                                           PackedTabs t1, PackedTabs t2,
                                                           const int32_t* __restrict__ order,
                                                           uint32_t* __restrict__ y,
@@ -570,7 +574,8 @@ __global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __rest
                                                           int64_t tiles_per_xcd) {
     __shared__ uint32_t tile[kColRows][W + 1];
     constexpr int K = W / 64;          // words per lane
-    constexpr int R = kColRows / 4;    // rows per wave
+    constexpr int R = 16;              // rows per wave
+    constexpr int NWV = kColRows / R;  // waves per workgroup
     constexpr int RB = PAIR ? CL_COLS_PAIR_RB : 8;  // rows whose loads are in flight together
     constexpr int NR = PAIR ? 4 : 2;   // input rows per output row
     const PackedTabs& tl = PAIR ? t2 : t1;  // the layer whose rows are written
@@ -665,20 +670,20 @@ __global__ __launch_bounds__(256) void k_eval_packed_cols(const uint32_t* __rest
         }
     }
     __syncthreads();
-    const int64_t o = o0 + lane;
-    if (o < out_words) {
+    // store: wave w takes columns w, w + NWV, ...; a column's kColRows rows in 64-row pieces,
+    // so each column is written as one contiguous run of kColRows words
+    constexpr int PIECES = kColRows / 64;
 #pragma unroll 4
-        for (int j = 0; j < W / 4; ++j) {
-            const int cw = w * (W / 4) + j;
-            const int64_t c = c0 + cw;
-            if (c < cols) {
+    for (int j = w; j < W * PIECES; j += NWV) {
+        const int cw = j / PIECES, rr = (j % PIECES) * 64 + lane;
+        const int64_t c = c0 + cw, o = o0 + rr;
+        if (c < cols && o < out_words) {
 #if CL_COLS_NT_STORE
-                // read once, by the fused pass: bypass the caches
-                __builtin_nontemporal_store(tile[lane][cw], y + c * out_words + o);
+            // read once, by the fused pass: bypass the caches
+            __builtin_nontemporal_store(tile[rr][cw], y + c * out_words + o);
 #else
-                y[c * out_words + o] = tile[lane][cw];
+            y[c * out_words + o] = tile[rr][cw];
 #endif
-            }
         }
     }
 }
@@ -936,10 +941,10 @@ int launch_packed_cols(const void* x, const PackedTabs& t1, const PackedTabs* t2
     auto* xs = static_cast<const uint32_t*>(x);
     auto* ys = static_cast<uint32_t*>(y);
     if (t2)
-        k_eval_packed_cols<kColWords, true><<<grid, 256, 0, as_stream(stream)>>>(
+        k_eval_packed_cols<kColWords, true><<<grid, kColThreads, 0, as_stream(stream)>>>(
             xs, t1, *t2, order, ys, out_dim, cols, out_words, row_tiles, per_xcd);
     else
-        k_eval_packed_cols<kColWords, false><<<grid, 256, 0, as_stream(stream)>>>(
+        k_eval_packed_cols<kColWords, false><<<grid, kColThreads, 0, as_stream(stream)>>>(
             xs, t1, t1, order, ys, out_dim, cols, out_words, row_tiles, per_xcd);
     return CL_OK;
 }
