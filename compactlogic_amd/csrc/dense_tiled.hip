@@ -1189,6 +1189,12 @@ __global__ __launch_bounds__(256) void k_bwd_part(
 #ifndef CL_FIRST_WAVES
 #define CL_FIRST_WAVES 4
 #endif
+#ifndef CL_BWD_ROWS_S4
+#define CL_BWD_ROWS_S4 12  // entries per row from which four waves share a row
+#endif
+#ifndef CL_BWD_ROWS_S2
+#define CL_BWD_ROWS_S2 6   // ... two waves
+#endif
 #ifndef CL_FIRST_EPI4
 #define CL_FIRST_EPI4 1
 #endif
@@ -1217,7 +1223,11 @@ struct FirstLayer {
     int G;
 };
 
-template <typename T, int VEC, int U, bool WANT_GW, bool HAS_P, bool FIRST = false>
+// S > 1 (rows with many entries, e.g. a narrow input feeding a wide layer): S waves of a
+// workgroup share a row, wave `part` taking the contiguous part of its entries
+// [deg * part / S, deg * (part + 1) / S); the parts' input-gradient sums meet in LDS and are
+// added in part order (deterministic; the association differs from S = 1 by rounding).
+template <typename T, int VEC, int U, bool WANT_GW, bool HAS_P, bool FIRST = false, int S = 1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_rows_waves<T, U, FIRST>())))
 void k_bwd_rows(
     const T* __restrict__ x, const T* __restrict__ gy, const int4* __restrict__ slot_rec,
@@ -1226,18 +1236,30 @@ void k_bwd_rows(
     const int32_t* __restrict__ run_ptr, T* __restrict__ grad_w, T* __restrict__ gx,
     int64_t in_dim, int64_t out_dim, int64_t num_runs, int64_t B, int G, int64_t nblk,
     uint32_t gy_magic, FirstLayer<T> first = {}) {
+    static_assert(S == 1 || S == 2 || S == 4, "1, 2 or 4 waves per row");
+    static_assert(S == 1 || !FIRST, "the first-layer mode takes one wave per row");
     using V = typename VT<T, VEC>::type;
     using V2 = typename VT<T, 2>::type;
     constexpr int EPI = U <= 2 ? 2 : U <= 4 ? (FIRST ? CL_FIRST_EPI4 : CL_BWD_ROWS_EPI4) : 1;
     const int lane = threadIdx.x & 63;
     const int64_t w = blockIdx.x;
-    const int64_t slot = ((w % kXcds) * nblk + w / kXcds) * 4 + wave_id();
-    if (slot >= in_dim) return;  // uniform per wave
-    const int4 sr = slot_rec[slot];
+    const int wv = wave_id();
+    const int64_t slot = ((w % kXcds) * nblk + w / kXcds) * (4 / S) + wv / S;
+    const int part = wv % S;
+    if constexpr (S == 1) {
+        if (slot >= in_dim) return;  // uniform per wave
+    }
+    // with S > 1 every wave reaches the closing barrier: an idle one only skips its work
+    bool active = slot < in_dim;
+    int4 sr = active ? slot_rec[slot] : make_int4(0, 0, 0, 0);
+    if (uint64_t(sr.x) >= uint64_t(in_dim) || sr.y < 0 || sr.z < sr.y || sr.z > 2 * num_runs) {
+        if constexpr (S == 1) return;  // corrupt slot record: nothing is read or written for it
+        active = false;
+        sr = make_int4(0, 0, 0, 0);
+    }
     const int64_t row = sr.x, e0 = sr.y;
     const int64_t deg = int64_t(sr.z) - sr.y;
-    if (uint64_t(row) >= uint64_t(in_dim) || sr.y < 0 || deg < 0 || sr.z > 2 * num_runs)
-        return;  // corrupt slot record: nothing is read or written for it
+    const int64_t klo = active ? deg * part / S : 0, khi = active ? deg * (part + 1) / S : 0;
     int32_t off[U];  // batch offsets (rows of at most 64 * 8 * VEC samples)
     bool in[U];
 #pragma unroll
@@ -1263,7 +1285,7 @@ void k_bwd_rows(
         nab1 = make_int4(__builtin_amdgcn_readfirstlane(t.x), __builtin_amdgcn_readfirstlane(t.y),
                          __builtin_amdgcn_readfirstlane(t.z), __builtin_amdgcn_readfirstlane(t.w));
     }
-    for (int64_t k = 0; k < deg; k += EPI) {
+    for (int64_t k = klo; k < khi; k += EPI) {
         int4 cur[EPI];
         V2 ck[EPI];
         bool use[EPI];
@@ -1272,10 +1294,10 @@ void k_bwd_rows(
         T p[EPI];
 #pragma unroll
         for (int q = 0; q < EPI; ++q) {
-            const int64_t e = e0 + (k + q < deg ? k + q : k);
+            const int64_t e = e0 + (k + q < khi ? k + q : k);
             cur[q] = inv_rec[e];
             ck[q] = vld<V2>(inv_coef + 2 * e);
-            use[q] = k + q < deg;
+            use[q] = k + q < khi;
             const bool ok = uint64_t(cur[q].x) < uint64_t(out_dim) &&
                             uint64_t(cur[q].y) < uint64_t(in_dim) &&
                             uint64_t(cur[q].z) < uint64_t(num_runs);
@@ -1372,6 +1394,23 @@ void k_bwd_rows(
         const T gp = softmax_back(lane < first.G ? p1 : T(0), lane < first.G ? v : T(0));
         if (lane < first.G) first.grad_w[row * first.G + lane] = (bad || !ok) ? nan_of<T>() : gp;
     } else {
+        if constexpr (S > 1) {
+            __shared__ V red[4][U][64];
+            __shared__ int red_bad[4];
+            if (part > 0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) red[wv][u][lane] = acc[u];
+                if (lane == 0) red_bad[wv] = bad ? 1 : 0;
+            }
+            __syncthreads();
+            if (part > 0 || !active) return;
+#pragma unroll
+            for (int q = 1; q < S; ++q) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc[u] += red[wv + q][u][lane];
+                bad = bad || red_bad[wv + q] != 0;
+            }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u)
             if (in[u]) vst_stream<V>(gx + row * B + off[u], bad ? V(nan_of<T>()) : acc[u]);
@@ -1938,7 +1977,11 @@ int backward_rows_impl(int dtype, const void* x, const void* grad_y, const int32
                                   reinterpret_cast<const int4*>(fa->nab), fa->gs,
                                   static_cast<const T*>(fa->probs), static_cast<T*>(fa->grad_w),
                                   fa->in_dim, fa->num_runs, int(fa->G)};
-        const int64_t nblk = ceil_div(ceil_div(in_dim, int64_t(4)), int64_t(kXcds));
+        // waves per row: rows with many entries (a narrow input feeding a wide layer) share
+        // their entries among 2 or 4 waves
+        const int64_t avg = in_dim > 0 ? 2 * num_runs / in_dim : 0;
+        const int S = fa ? 1 : avg >= CL_BWD_ROWS_S4 ? 4 : avg >= CL_BWD_ROWS_S2 ? 2 : 1;
+        const int64_t nblk = ceil_div(ceil_div(in_dim, int64_t(4 / S)), int64_t(kXcds));
         CL_ARG(kXcds * nblk < (int64_t(1) << 31), "too many rows");
         const unsigned grid = unsigned(kXcds * nblk);
         auto go = [&](auto uc) {
@@ -1952,10 +1995,19 @@ int backward_rows_impl(int dtype, const void* x, const void* grad_y, const int32
             auto* gw = static_cast<T*>(grad_w);
             auto* gxs = static_cast<T*>(grad_x);
             auto launch = [&](auto gwc, auto pc) {
-                k_bwd_rows<T, W, U, decltype(gwc)::value, decltype(pc)::value>
-                    <<<grid, 256, 0, s>>>(xs, gys, srec, rec, ic, gate_seq, pr, run_ptr, gw, gxs,
-                                          in_dim, out_dim, num_runs, batch, int(num_gates), nblk,
-                                          gy_magic);
+                constexpr bool GW = decltype(gwc)::value, HP = decltype(pc)::value;
+                if (S == 4)
+                    k_bwd_rows<T, W, U, GW, HP, false, 4><<<grid, 256, 0, s>>>(
+                        xs, gys, srec, rec, ic, gate_seq, pr, run_ptr, gw, gxs, in_dim, out_dim,
+                        num_runs, batch, int(num_gates), nblk, gy_magic);
+                else if (S == 2)
+                    k_bwd_rows<T, W, U, GW, HP, false, 2><<<grid, 256, 0, s>>>(
+                        xs, gys, srec, rec, ic, gate_seq, pr, run_ptr, gw, gxs, in_dim, out_dim,
+                        num_runs, batch, int(num_gates), nblk, gy_magic);
+                else
+                    k_bwd_rows<T, W, U, GW, HP><<<grid, 256, 0, s>>>(
+                        xs, gys, srec, rec, ic, gate_seq, pr, run_ptr, gw, gxs, in_dim, out_dim,
+                        num_runs, batch, int(num_gates), nblk, gy_magic);
             };
             using Y = std::true_type;
             using N = std::false_type;

@@ -244,6 +244,12 @@ class LogicLayerRunsFunction(torch.autograd.Function):
         return grad_x, grad_w, None, None, None, None
 
 
+# Entries per input row (2 * num_runs / in_dim, rounded down) from which
+# cl_dense_backward_rows shares a row among several waves (CL_BWD_ROWS_S2 in
+# dense_tiled.hip); its first-layer mode keeps one wave per row.
+_ROWS_SHARED_FROM = 6
+
+
 def _row_backward_fits(plan: RunPlan, x: torch.Tensor) -> bool:
     """Whether cl_dense_backward_rows takes this layer at this batch (x: [in_dim, batch])."""
     wide = 16 // x.element_size()
@@ -503,6 +509,9 @@ class LogicLayer(torch.nn.Module):
                 or not self.weights.requires_grad or not first.weights.requires_grad
                 or first.weights.dtype != x.dtype or x.data_ptr() != x_in.data_ptr()
                 or plan1.out_dim != plan.in_dim or not _row_backward_fits(plan, x)):
+            return None
+        # bitwise equal to the unpaired steps only where those take one wave per input row
+        if 2 * plan.num_runs // max(plan.in_dim, 1) >= _ROWS_SHARED_FROM:
             return None
         return LogicLayerFirstPairFunction.apply(
             x.detach(), self.weights, self.gate_sequence, plan, first.weights, x0, probs1,

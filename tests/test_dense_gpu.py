@@ -441,13 +441,17 @@ def test_partitioned_backward_matches_untiled(device, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-@pytest.mark.parametrize("batch,g_n,softmax", [(4, 16, True), (256, 16, True), (1024, 16, True),
-                                               (2048, 5, False), (100, 40, True), (1024, 1, False)])
-def test_row_backward_matches_chunked(device, dtype, batch, g_n, softmax):
-    """cl_dense_backward_rows (one wave per input row, finalize inside) against the chunked
-    backward + finalize: the same input and logits gradients to rounding, both against the
-    oracle, bitwise reproducible.  Batches above the row kernel's limit fall back."""
-    in_dim, out_dim = 700, 900
+@pytest.mark.parametrize("batch,g_n,softmax,in_dim,out_dim", [
+    (4, 16, True, 700, 900), (256, 16, True, 700, 900), (1024, 16, True, 700, 900),
+    (2048, 5, False, 700, 900), (100, 40, True, 700, 900), (1024, 1, False, 700, 900),
+    # many entries per input row: two (about 8 per row) or four (about 27) waves share a row
+    (256, 16, True, 500, 2000), (1000, 16, True, 300, 4000), (4, 5, False, 300, 4000),
+    (1024, 1, False, 37, 3000)])
+def test_row_backward_matches_chunked(device, dtype, batch, g_n, softmax, in_dim, out_dim):
+    """cl_dense_backward_rows (one wave per input row, or several sharing a row with many
+    entries; finalize inside) against the chunked backward + finalize: the same input and
+    logits gradients to rounding, both against the oracle, bitwise reproducible.  Batches above
+    the row kernel's limit fall back."""
     g = torch.Generator().manual_seed(batch + g_n)
     pair = torch.randint(0, in_dim, (2, out_dim, 1), generator=g)
     pair[1, ::9] = pair[0, ::9]                       # self-pairs

@@ -57,6 +57,24 @@ def test_pair_gradients_are_bitwise_the_unpaired_ones(device, dims, k, batch, dt
         assert torch.equal(a, b)
 
 
+def test_pair_stays_off_where_waves_share_a_row(device):
+    """A second layer with many entries per input row (here 16) takes several waves per row in
+    its row backward, a different summation order than the first-layer mode's one wave: the
+    pair stays off and both runs are the unpaired steps."""
+    dims = [(64, 128), (128, 1024)]
+    model = net(device, dims, 8, torch.float32, seed=5)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.rand((512, 64), generator=g) < 0.4).float().to(device)
+    labels = torch.randint(0, 8, (512,), generator=g).to(device)
+    l0, g0, _ = grads(model, x, labels, pair=False)
+    l1, g1, c1 = grads(model, x, labels, pair=True)
+    assert not any(n.startswith("cl_dense_backward_rows_first") for n in c1)
+    assert any(n.startswith("cl_dense_backward_rows[") for n in c1)
+    assert torch.equal(l0, l1)
+    for a, b in zip(g0, g1):
+        assert torch.equal(a, b)
+
+
 def test_pair_cfg2_step(device):
     cfg = configs.CONFIGS["cfg2"]
     model = configs.dense_network(cfg, device=device)
