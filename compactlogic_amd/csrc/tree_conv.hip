@@ -960,6 +960,28 @@ __global__ __launch_bounds__(256) void k_tree_gather_rec(const T* __restrict__ r
 
 // grad_w[c][q][g] = c0(g) M3 + c1(g) M1 + c2(g) M2 + c3(g) M0 with M the node's moments summed
 // over the nblk partials in block order.  One thread per (c, q, g).
+// Gradient of gate g of one node from its moments m = (sum gy a b, sum gy a, sum gy b,
+// sum gy): of the probability, or with the node's logits of the logit.
+template <typename T>
+__device__ __forceinline__ T finalize_one(const T (&m)[4], const T* __restrict__ logits, int g) {
+    auto prob_grad = [&](int h) {
+        const Coef4<T> cf = gate_coef<T>(h);
+        return fma(cf.c3, m[0], fma(cf.c2, m[2], fma(cf.c1, m[1], cf.c0 * m[3])));
+    };
+    if (!logits) return prob_grad(g);
+    // softmax backward: every lane of the node forms all 16 probabilities and their
+    // gradients itself, so the sum over the node is taken in one fixed order
+    T p[16];
+    node_probs(logits, true, p);
+    T dot = 0, pg = 0;
+#pragma unroll
+    for (int h = 0; h < 16; ++h) {
+        dot = fma(p[h], prob_grad(h), dot);
+        pg = h == g ? p[h] : pg;  // a select per slot: no dynamic index into registers
+    }
+    return pg * (prob_grad(g) - dot);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_tree_finalize(const T* __restrict__ part, int64_t cout,
                                                        int nodes, int64_t nblk,
@@ -976,25 +998,390 @@ __global__ __launch_bounds__(256) void k_tree_finalize(const T* __restrict__ par
 #pragma unroll
         for (int j = 0; j < 4; ++j) m[j] += src[j];
     }
-    auto prob_grad = [&](int h) {
-        const Coef4<T> cf = gate_coef<T>(h);
-        return fma(cf.c3, m[0], fma(cf.c2, m[2], fma(cf.c1, m[1], cf.c0 * m[3])));
-    };
-    if (!logits) {
-        grad_w[i] = prob_grad(g);
-        return;
-    }
-    // softmax backward: every lane of the node forms all 16 probabilities and their
-    // gradients itself, so the sum over the node is taken in one fixed order
-    T p[16];
-    node_probs(logits + cq * 16, true, p);
-    T dot = 0, pg = 0;
+    grad_w[i] = finalize_one<T>(m, logits ? logits + cq * 16 : nullptr, g);
+}
+
+// ------------------------------------------------------------------------------------------
+// Staged backward of the complete block (float or double, when a sample's input fits LDS).
+// A workgroup takes one sample and a group of cg output channels, stages the sample's input in
+// LDS once (rows [-ph, hs - ph) and columns [-pw, ws - pw) of every input channel, zero outside
+// the image, hs = (ho - 1) sh + kh, ws = (wo - 1) sw + kw: every tap inside the kernel window
+// reads it without a bounds test), and computes per (channel, window) item what k_tree_nodes
+// computes: the node values at the window's winner, the conv-gate gradients and the 28 node
+// moments.  Lane group of L lanes per channel (L from P alone, so the summation order of a
+// channel's moments is the same in every mode): lane l takes windows l, l + L, ... in order,
+// then the L lanes are combined by an xor tree; the channel's sums for the sample go to
+// part[(c * n + sample) * 32 + (node * 4 + m)] (28 of 32 words), summed over the samples in
+// order by k_tree_moments.
+//   MODE 0  moments only;
+//   MODE 1  with the input gradient: every tap's contribution (the radd of k_tree_nodes) stays
+//           in LDS, then lane groups of PL lanes per input channel walk its uses in use order
+//           (the order of k_tree_gather_rec, so every plane word takes its additions in the
+//           same order) into the sample's input gradient in LDS, stored once; cg = cout;
+//   MODE 2  with the conv-gate gradients stored for k_tree_gather (contributions that do not
+//           fit LDS).
+// A tap outside the kernel window (never drawn by the sampler) is read from global memory with
+// bounds tests; a channel with a tap channel >= C gets NaN moments and that tap adds nothing.
+struct TreeStage {
+    int hs, ws, plane;  // staged rows, columns, words per input channel
+    int kh, kw;
+    int cg, groups;     // channels per workgroup, workgroups per sample
+    int lanes;          // L: lanes per channel in the node phase (power of two)
+    int glanes;         // PL: lanes per input channel in the gather (power of two, <= 64)
+    int vec;            // rows of x (and grad_x) are whole 16-byte vectors, aligned
+    int ul_words;       // MODE 1: room for the packed use list after the gradient planes
+    int x_words;        // staged input (MODE 1: also the input gradient, after the node phase)
+    int c_words;        // contributions (MODE 1)
+    int64_t per_xcd;    // workgroups per XCD
+    FastDiv div_hw, div_w, div_h, div_rv;  // by h * w, w, h, and the vectors per row
+};
+
+constexpr int kMomStride = 32;  // words per (channel, sample) moment record (28 used)
+
+template <typename T, int MODE, int NT>
+__global__ __launch_bounds__(NT) void k_tree_bwd_staged(
+    const T* __restrict__ grad_y, const T* __restrict__ x, const T* __restrict__ kc,
+    const int32_t* __restrict__ sel, const int32_t* __restrict__ idx,
+    const int32_t* __restrict__ ent_ptr, const int32_t* __restrict__ ent, TreeDims d,
+    TreeStage g, T* __restrict__ part, T* __restrict__ gconv, T* __restrict__ grad_x) {
+    constexpr int VEC = 16 / sizeof(T);  // elements per 16-byte load or store
+    typedef T V __attribute__((ext_vector_type(VEC)));
+    constexpr int SB = 8;                 // staging loads in flight per thread
+    constexpr int UB = 8;                 // channel uses whose records load together (global)
+    extern __shared__ unsigned char smem_raw[];
+    T* xs = reinterpret_cast<T*>(smem_raw);
+    // MODE 1: contributions cb[p * cs + cl * 8 + ((k + (cl >> 2)) & 7)] (the rotation by cl / 4
+    // spreads a wave's stores of one tap over all banks; cs = cg * 8 + 1) and the winners'
+    // input positions wins[p * (cg + 1) + cl] = (wy sh) << 16 | (wx sw), or -1 for none
+    T* cb = xs + g.x_words;
+    int* wins = reinterpret_cast<int*>(cb + g.c_words);
+    // workgroups of one XCD take consecutive (sample, group) pairs: a sample's groups share
+    // its staged input through that XCD's L2
+    const int64_t bx = blockIdx.x;
+    const int64_t j = (bx % 8) * g.per_xcd + bx / 8;
+    if (j >= int64_t(d.n) * g.groups) return;  // whole workgroup, before any barrier
+    const int n = int(j / g.groups), grp = int(j - int64_t(n) * g.groups);
+    const int c0 = grp * g.cg, cg = min(g.cg, d.cout - c0);
+    const int hw = d.h * d.w, nx = d.cin * hw;
+    const T* xn = x + int64_t(n) * nx;
+    const int t = threadIdx.x;
+    const int cs = g.cg * kTaps + 1, wsd = g.cg + 1;
+
+    // Node phase state.  Lane group of L lanes per channel; every lane walks cpl windows per
+    // channel (those past P only keep the group in step for the xor tree).  The channel's
+    // coefficients and taps and the first window's records are loaded before the staging,
+    // and each window's records one window ahead of its use.
+    const int L = g.lanes;
+    const int l = t & (L - 1);
+    const int cpl = (d.P + L - 1) / L;
+    const int slots = NT / L;
+    int cl = t / L;
+    T sk[kMaxNodes][4];
+    // staged word offsets of the taps (below 2^16: the LDS holds 40960 words), two 16-bit
+    // halves a register; flags: bit k tap k staged, bit 8 a tap channel >= C
+    uint32_t soff[kTaps / 2];
+    uint32_t flags = 0;
+    auto load_channel_regs = [&](int cc) {
+        const int c = c0 + cc;
 #pragma unroll
-    for (int h = 0; h < 16; ++h) {
-        dot = fma(p[h], prob_grad(h), dot);
-        pg = h == g ? p[h] : pg;  // a select per slot: no dynamic index into registers
+        for (int q = 0; q < kMaxNodes; ++q)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) sk[q][m] = kc[(int64_t(c) * kMaxNodes + q) * 4 + m];
+        flags = 0;
+#pragma unroll
+        for (int k = 0; k < kTaps; ++k) {
+            const int32_t sv = sel[c * kTaps + k];
+            const int ch = (sv >> 16) & 0xFFFF, row = (sv >> 8) & 0xFF, col = sv & 0xFF;
+            const bool in = ch < d.cin && row < g.kh && col < g.kw;
+            const uint32_t o = in ? uint32_t(ch * g.plane + row * g.ws + col) : 0u;
+            if (k & 1) soff[k >> 1] |= o << 16;
+            else soff[k >> 1] = o;
+            flags |= uint32_t(in) << k | uint32_t(ch >= d.cin) << 8;
+        }
+    };
+    int wn = -1;
+    T gn = T(0);
+    // item indices in 32 bits: the host checks n * cout * P < 2^31
+    auto load_item = [&](int cc, int p) {
+        const bool ok = cc < cg && p < d.P;
+        const uint32_t c = uint32_t(c0 + (ok ? cc : 0)), pp = ok ? uint32_t(p) : 0u;
+        const uint32_t at = (uint32_t(n) * uint32_t(d.cout) + c) * uint32_t(d.P) + pp;
+        wn = ok ? idx[at] : -1;
+        gn = ok ? grad_y[d.y_rows ? (c * uint32_t(d.P) + pp) * uint32_t(d.n) + uint32_t(n) : at]
+                : T(0);
+    };
+    if (cl < cg) load_channel_regs(cl);
+    load_item(cl, l);
+
+    // staging: zero the region, then the sample with 16-byte loads (rows of whole vectors)
+    // or element by element
+    {
+        V* xv = reinterpret_cast<V*>(xs);
+        for (int i = t; i < g.x_words / VEC; i += NT) xv[i] = V(T(0));
+        for (int i = (g.x_words / VEC) * VEC + t; i < g.x_words; i += NT) xs[i] = T(0);
     }
-    grad_w[i] = pg * (prob_grad(g) - dot);
+    __syncthreads();
+    if (g.vec) {
+        const V* src = reinterpret_cast<const V*>(xn);
+        const int rv = d.w / VEC;  // vectors per input row
+        const int nv = nx / VEC;
+        for (int i0 = 0; i0 < nv; i0 += SB * NT) {
+            V v[SB];
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const int i = i0 + u * NT + t;
+                if (i < nv) v[u] = src[i];
+            }
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const int i = i0 + u * NT + t;
+                if (i >= nv) continue;
+                const int r = int(fast_div(uint32_t(i), g.div_rv)), cv = i - r * rv;
+                const int ch = int(fast_div(uint32_t(r), g.div_h)), iy = r - ch * d.h;
+                const int sy = iy + d.ph;
+                if (sy >= g.hs) continue;
+                const int sx0 = cv * VEC + d.pw;
+                T* dst = xs + ch * g.plane + sy * g.ws;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e)
+                    if (sx0 + e < g.ws) dst[sx0 + e] = v[u][e];
+            }
+        }
+    } else {
+        for (int i0 = 0; i0 < nx; i0 += SB * NT) {
+            T v[SB];
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const int i = i0 + u * NT + t;
+                v[u] = i < nx ? xn[i] : T(0);
+            }
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const int i = i0 + u * NT + t;
+                if (i >= nx) continue;
+                const int ch = int(fast_div(uint32_t(i), g.div_hw)), r = i - ch * hw;
+                const int iy = int(fast_div(uint32_t(r), g.div_w)), ix = r - iy * d.w;
+                const int sy = iy + d.ph, sx = ix + d.pw;
+                if (sy < g.hs && sx < g.ws) xs[ch * g.plane + sy * g.ws + sx] = v[u];
+            }
+        }
+    }
+    __syncthreads();
+
+    // node phase
+    for (; cl < cg; cl += slots) {
+        const int c = c0 + cl;
+        const uint32_t cell = uint32_t(n) * uint32_t(d.cout) + uint32_t(c);
+        T mom[28];
+#pragma unroll
+        for (int i = 0; i < 28; ++i) mom[i] = T(0);
+        for (int i = 0; i < cpl; ++i) {
+            const int p = l + i * L;
+            const int win = wn;
+            const T gyv = gn;
+            if (i + 1 < cpl) load_item(cl, p + L);
+            else load_item(cl + slots, l);
+            if (p >= d.P) continue;
+            const bool live = win >= 0 && win < d.ho * d.wo;
+            const int w0 = live ? win : 0;
+            const int wy = int(fast_div(uint32_t(w0), d.div_wo)), wx = w0 - wy * d.wo;
+            const int pos = wy * d.sh * g.ws + wx * d.sw;
+            T v[kTaps];
+#pragma unroll
+            for (int k = 0; k < kTaps; ++k)
+                v[k] = xs[((k & 1) ? soff[k >> 1] >> 16 : soff[k >> 1] & 0xFFFFu) + pos];
+            if ((flags & 0xFFu) != 0xFFu) {
+#pragma unroll
+                for (int k = 0; k < kTaps; ++k)
+                    if (!((flags >> k) & 1))
+                        v[k] = tap_value(xn, d, decode_tap(sel[c * kTaps + k], d.ph, d.pw),
+                                         wy, wx);
+            }
+            T gg[4], tt[2], gc[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) gg[q] = node(sk[q], v[2 * q], v[2 * q + 1]);
+            tt[0] = node(sk[4], gg[0], gg[1]);
+            tt[1] = node(sk[5], gg[2], gg[3]);
+            const T gy = live ? gyv : T(0);
+            node_grads<T>(sk, gg, tt, gy, gc, mom);
+            gate_moments<T>(v, gc, mom);
+            if constexpr (MODE == 1) {
+                const int rot = cl >> 2;
+#pragma unroll
+                for (int k = 0; k < kTaps; ++k) {
+                    const int q = k >> 1;
+                    cb[p * cs + cl * kTaps + ((k + rot) & 7)] =
+                        gc[q] * fma(sk[q][3], v[k ^ 1], (k & 1) ? sk[q][2] : sk[q][1]);
+                }
+                wins[p * wsd + cl] = live ? ((wy * d.sh) << 16 | (wx * d.sw)) : -1;
+            }
+            if constexpr (MODE == 2) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) gconv[(cell * uint32_t(d.P) + p) * 4 + q] = gc[q];
+            }
+        }
+        // the channel's lanes combined in a fixed xor tree (the whole group is active)
+        for (int o = 1; o < L; o <<= 1) {
+#pragma unroll
+            for (int i = 0; i < 28; ++i) mom[i] += __shfl_xor(mom[i], o, 64);
+        }
+        if (l == 0 && part) {
+            T* dst = part + (uint32_t(c) * uint32_t(d.n) + uint32_t(n)) * kMomStride;
+#pragma unroll
+            for (int i = 0; i < 28; ++i) dst[i] = (flags >> 8) ? quiet_nan<T>() : mom[i];
+        }
+        if (cl + slots < cg) load_channel_regs(cl + slots);
+    }
+    if constexpr (MODE == 1) {
+        __syncthreads();  // the staged input is dead: its words take the input gradient
+        for (int i = t; i < nx; i += NT) xs[i] = T(0);
+        // the use list with its taps, packed u | row << 16 | col << 24 (u = c * 8 + k), into
+        // the words after the gradient planes when it fits there (g.ul_words), loaded by all
+        // threads at once
+        const int ea = ent_ptr[0], eb = ent_ptr[d.cin];
+        const bool in_lds = ea >= 0 && eb >= ea && eb - ea <= g.ul_words;
+        uint32_t* ul = reinterpret_cast<uint32_t*>(xs + nx);
+        if (in_lds) {
+            for (int e0 = ea; e0 < eb; e0 += 4 * NT) {
+                int u4[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int e = e0 + q * NT + t;
+                    u4[q] = e < eb ? ent[e] : -1;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int e = e0 + q * NT + t;
+                    const bool ok = uint32_t(u4[q]) < uint32_t(cg * kTaps);
+                    const int32_t sv = sel[ok ? u4[q] : 0];
+                    if (e < eb)
+                        ul[e - ea] = ok ? (uint32_t(u4[q]) | (uint32_t(sv & 0xFFFF) << 16))
+                                        : 0xFFFFFFFFu;
+                }
+            }
+        }
+        __syncthreads();
+        const int PL = g.glanes;
+        const int pl = t & (PL - 1);
+        for (int ch = t / PL; ch < d.cin; ch += NT / PL) {
+            const int e0 = ent_ptr[ch], e1 = ent_ptr[ch + 1];
+            T* gp = xs + ch * hw;
+            for (int e = e0; e < e1; e += UB) {
+                uint32_t rb[UB];
+                if (in_lds) {
+#pragma unroll
+                    for (int i = 0; i < UB; ++i) {
+                        const int ee = e + i - ea;
+                        rb[i] = e + i < e1 && uint32_t(ee) < uint32_t(eb - ea) ? ul[ee]
+                                                                                 : 0xFFFFFFFFu;
+                    }
+                } else {
+                    int ub[UB];
+#pragma unroll
+                    for (int i = 0; i < UB; ++i) ub[i] = e + i < e1 ? ent[e + i] : -1;
+#pragma unroll
+                    for (int i = 0; i < UB; ++i) {
+                        const bool ok = uint32_t(ub[i]) < uint32_t(cg * kTaps);
+                        const int32_t sv = sel[ok ? ub[i] : 0];
+                        rb[i] = ok ? (uint32_t(ub[i]) | (uint32_t(sv & 0xFFFF) << 16))
+                                   : 0xFFFFFFFFu;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < UB; ++i) {
+                    if (rb[i] == 0xFFFFFFFFu) continue;
+                    const int u = int(rb[i] & 0xFFFF);
+                    const int c = u >> 3, k = u & 7;
+                    const int dy = int((rb[i] >> 24) & 0xFF) - d.ph;
+                    const int dx = int((rb[i] >> 16) & 0xFF) - d.pw;
+                    const int slot = c * kTaps + ((k + (c >> 2)) & 7);
+                    for (int p = pl; p < d.P; p += PL) {
+                        const int pk = wins[p * wsd + c];
+                        if (pk < 0) continue;
+                        const int iy = (pk >> 16) + dy, ix = (pk & 0xFFFF) + dx;
+                        if (uint32_t(iy) < uint32_t(d.h) && uint32_t(ix) < uint32_t(d.w))
+                            gp[iy * d.w + ix] += cb[p * cs + slot];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        T* gxn = grad_x + int64_t(n) * nx;
+        if (g.vec) {
+            V* gv = reinterpret_cast<V*>(gxn);
+            const V* lv = reinterpret_cast<const V*>(xs);
+            for (int i = t; i < nx / VEC; i += NT) gv[i] = lv[i];
+        } else {
+            for (int i = t; i < nx; i += NT) gxn[i] = xs[i];
+        }
+    }
+}
+
+// Collapsed coefficients kc[c][q][:] of every node (from the logits with d.softmax).
+template <typename T>
+__global__ __launch_bounds__(64) void k_tree_coefs(const T* __restrict__ w_prob,
+                                                   const int32_t* __restrict__ sel, TreeDims d,
+                                                   T* __restrict__ kc) {
+    __shared__ T sk[kMaxNodes][4];
+    __shared__ TapOff st[kTaps];
+    __shared__ int bad;
+    const int c = blockIdx.x;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    load_channel(w_prob, sel, c, kMaxNodes, d, sk, st, &bad);
+    __syncthreads();
+    if (threadIdx.x < kMaxNodes * 4)
+        kc[int64_t(c) * kMaxNodes * 4 + threadIdx.x] = sk[threadIdx.x >> 2][threadIdx.x & 3];
+}
+
+// The staged pass's moment records summed over the samples, then the weight gradient as in
+// k_tree_finalize.  Workgroup per channel: thread (s, i) sums moment i over the s-th of 32
+// contiguous runs of samples in order, the 32 run sums are added in a fixed tree, and threads
+// (q, g) finish node q's gate g.
+template <typename T>
+__global__ __launch_bounds__(1024) void k_tree_moments(const T* __restrict__ part, int n,
+                                                       const T* __restrict__ logits,
+                                                       T* __restrict__ grad_w) {
+    __shared__ T run[32][28];
+    __shared__ T mom[28];
+    const int c = blockIdx.x, t = threadIdx.x;
+    const int s = t >> 5, i = t & 31;
+    const int per = (n + 31) / 32;
+    if (i < 28) {
+        const T* src = part + int64_t(c) * n * kMomStride + i;
+        const int lo = min(n, s * per), hi = min(n, lo + per);
+        T a = 0;
+        int k = lo;
+        for (; k + 4 <= hi; k += 4) {
+            const T v0 = src[int64_t(k) * kMomStride], v1 = src[int64_t(k + 1) * kMomStride];
+            const T v2 = src[int64_t(k + 2) * kMomStride], v3 = src[int64_t(k + 3) * kMomStride];
+            a += v0;
+            a += v1;
+            a += v2;
+            a += v3;
+        }
+        for (; k < hi; ++k) a += src[int64_t(k) * kMomStride];
+        run[s][i] = a;
+    }
+    __syncthreads();
+    if (t < 28) {
+        T r[32];
+#pragma unroll
+        for (int k = 0; k < 32; ++k) r[k] = run[k][t];
+#pragma unroll
+        for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+            for (int k = 0; k < w; ++k) r[k] = r[k] + r[k + w];
+        mom[t] = r[0];
+    }
+    __syncthreads();
+    if (t < kMaxNodes * 16) {
+        const int q = t >> 4, gg = t & 15;
+        const T m[4] = {mom[q * 4 + 0], mom[q * 4 + 1], mom[q * 4 + 2], mom[q * 4 + 3]};
+        const int64_t at = (int64_t(c) * kMaxNodes + q) * 16 + gg;
+        grad_w[at] = finalize_one<T>(m, logits ? logits + (int64_t(c) * kMaxNodes + q) * 16
+                                               : nullptr, gg);
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1433,9 +1820,97 @@ inline int64_t node_blocks(const TreeDims& d, int* node_items = nullptr) {
 // per (channel, tap, item).
 inline int64_t tree_records(const TreeDims& d) { return int64_t(d.cout) * kTaps * d.n * d.P; }
 
+#ifndef CL_TREE_STAGED_BWD
+#define CL_TREE_STAGED_BWD 1  // the staged backward of the complete block where it fits
+#endif
+#ifndef CL_TREE_STAGED_NT1
+#define CL_TREE_STAGED_NT1 1024  // threads of the float form with the input gradient
+#endif
+
+// Plan of k_tree_bwd_staged, or false when it does not apply (then the node pass with global
+// taps runs).  The decision and the lane count L depend on the shape and type alone, not on
+// whether the input gradient is wanted, so the weight gradient is the same either way.
+struct StagePlan {
+    TreeStage g;
+    int mode, threads;
+    int64_t lds;
+    unsigned grid;
+};
+
+bool plan_tree_stage(const TreeDims& d, int kh, int kw, bool want_gx, size_t tsize,
+                     StagePlan& sp) {
+    if (!CL_TREE_STAGED_BWD || !d.complete || d.P < 1 || kh < 1 || kw < 1) return false;
+    TreeStage& g = sp.g;
+    g.kh = kh;
+    g.kw = kw;
+    g.hs = (d.ho - 1) * d.sh + kh;
+    g.ws = (d.wo - 1) * d.sw + kw;
+    g.plane = g.hs * g.ws;
+    int L = 1;  // min(4, largest power of two <= P / 2), at least 1
+    while (2 * L <= 4 && 4 * L <= d.P) L *= 2;
+    g.lanes = L;
+    g.glanes = gather_lanes(d.P);
+    // float: 1024 threads (16 waves, one workgroup per CU); double: 512 (its registers)
+    sp.threads = tsize == 4 ? CL_TREE_STAGED_NT1 : 512;
+    const int64_t xw = int64_t(d.cin) * g.plane, nx = int64_t(d.cin) * d.h * d.w;
+    if (xw * int64_t(tsize) > kFwdLdsLimit || nx >= (int64_t(1) << 31)) return false;
+    // MODE 1: staged input / input gradient (+ the packed use list when it fits), the
+    // contributions and the winners, for all channels in one workgroup
+    const int64_t c1 = int64_t(d.P) * (int64_t(d.cout) * kTaps + 1);
+    const int64_t w1 = int64_t(d.P) * (d.cout + 1);
+    auto lds_of = [&](int64_t xwords) { return (xwords + c1) * int64_t(tsize) + w1 * 4; };
+    int64_t x1 = std::max(xw, nx + int64_t(d.cout) * kTaps);
+    if (lds_of(x1) > kFwdLdsLimit) x1 = std::max(xw, nx);
+    if (want_gx && lds_of(x1) <= kFwdLdsLimit && int64_t(d.cout) * kTaps < 65535) {
+        sp.mode = 1;
+        g.cg = d.cout;
+        g.x_words = int(x1);
+        g.c_words = int(c1);
+        g.ul_words = int(x1 - nx);
+        sp.lds = lds_of(x1);
+    } else {
+        sp.mode = want_gx ? 2 : 0;
+        // channel groups only where the samples alone leave CUs idle
+        const int slots = sp.threads / L;
+        const int64_t groups = std::min<int64_t>(ceil_div(d.cout, slots),
+                                                 std::max<int64_t>(1, ceil_div(256, d.n)));
+        g.cg = int(ceil_div(d.cout, groups));
+        g.x_words = int(xw);
+        g.c_words = 0;
+        g.ul_words = 0;
+        sp.lds = xw * int64_t(tsize);
+    }
+    g.groups = int(ceil_div(d.cout, g.cg));
+    g.per_xcd = ceil_div(int64_t(d.n) * g.groups, int64_t(8));
+    if (8 * g.per_xcd >= (int64_t(1) << 31)) return false;
+    // 32-bit item, moment-record and conv-gate-gradient indices
+    const int64_t items = int64_t(d.n) * d.cout * d.P;
+    if (items * 4 >= (int64_t(1) << 31) || int64_t(d.cout) * d.n * kMomStride >= (int64_t(1) << 31))
+        return false;
+    sp.grid = unsigned(8 * g.per_xcd);
+    g.div_hw = make_fastdiv(uint32_t(d.h * d.w));
+    g.div_w = make_fastdiv(uint32_t(d.w));
+    g.div_h = make_fastdiv(uint32_t(d.h));
+    g.div_rv = make_fastdiv(uint32_t(std::max(1, d.w / int(16 / tsize))));
+    g.vec = 0;  // set by the caller, which sees the pointers
+    return true;
+}
+
 template <typename T>
-int64_t tree_workspace_bytes(const TreeDims& d, bool grad_x) {
+int64_t tree_workspace_bytes(const TreeDims& d, bool grad_x, int kh, int kw) {
     const int nodes = d.complete ? 7 : 4;
+    StagePlan sp;
+    if (plan_tree_stage(d, kh, kw, grad_x, sizeof(T), sp)) {
+        // moment records [cout][n][32], coefficients [cout][7][4], conv-gate gradients
+        int64_t b = int64_t(d.cout) * d.n * kMomStride * sizeof(T);
+        b = (b + 255) / 256 * 256;
+        b += int64_t(d.cout) * nodes * 4 * sizeof(T);
+        if (sp.mode == 2) {
+            b = (b + 255) / 256 * 256;
+            b += int64_t(d.n) * d.cout * d.P * 4 * sizeof(T);
+        }
+        return b;
+    }
     const int64_t nblk = node_blocks(d);
     int64_t b = 0;
     if (d.complete && grad_x) {
@@ -1542,11 +2017,75 @@ extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
-    CL_DTYPE_SWITCH(dtype, { *bytes = tree_workspace_bytes<scalar_t>(d, grad_x != 0); });
+    CL_DTYPE_SWITCH(dtype, {
+        *bytes = tree_workspace_bytes<scalar_t>(d, grad_x != 0, kernel_h, kernel_w);
+    });
     return CL_OK;
 }
 
 namespace {
+template <typename T>
+int tree_backward_staged(const TreeDims& d, const StagePlan& sp, const T* gy, const T* xs,
+                         const T* wp, const int32_t* sel, const int32_t* idx,
+                         const int32_t* ent_ptr, const int32_t* ent, T* grad_x, T* grad_w,
+                         void* workspace, hipStream_t s) {
+    unsigned char* ws = static_cast<unsigned char*>(workspace);
+    T* part = reinterpret_cast<T*>(ws);
+    int64_t off = (int64_t(d.cout) * d.n * kMomStride * sizeof(T) + 255) / 256 * 256;
+    T* kc = reinterpret_cast<T*>(ws + off);
+    off += int64_t(d.cout) * kMaxNodes * 4 * sizeof(T);
+    off = (off + 255) / 256 * 256;
+    T* gconv = sp.mode == 2 ? reinterpret_cast<T*>(ws + off) : nullptr;
+    TreeStage g = sp.g;
+    g.vec = (d.w % (16 / int(sizeof(T))) == 0 && aligned(xs, 16) &&
+             (!grad_x || aligned(grad_x, 16))) ? 1 : 0;
+    k_tree_coefs<T><<<unsigned(d.cout), 64, 0, s>>>(wp, sel, d, kc);
+    if (int rc = check_launch("cl_tree_conv_backward(coefficients)")) return rc;
+    T* pw = grad_w ? part : nullptr;
+    static bool reserved[3][2][kMaxDevices] = {};
+    const int ti = sizeof(T) == 4 ? 0 : 1;
+    auto go = [&](auto kern) -> int {
+        if (int rc = reserve_lds(kern, sp.lds, reserved[sp.mode][ti], "the tree block backward"))
+            return rc;
+        kern<<<sp.grid, unsigned(sp.threads), size_t(sp.lds), s>>>(
+            gy, xs, kc, sel, idx, ent_ptr, ent, d, g, pw, gconv, grad_x);
+        return check_launch("cl_tree_conv_backward(staged)");
+    };
+    constexpr int NT = sizeof(T) == 4 ? CL_TREE_STAGED_NT1 : 512;
+    int rc = sp.mode == 1 ? go(&k_tree_bwd_staged<T, 1, NT>)
+             : sp.mode == 2 ? go(&k_tree_bwd_staged<T, 2, NT>)
+                            : go(&k_tree_bwd_staged<T, 0, NT>);
+    if (rc) return rc;
+    if (grad_w) {
+        k_tree_moments<T><<<unsigned(d.cout), 1024, 0, s>>>(part, d.n, d.softmax ? wp : nullptr,
+                                                            grad_w);
+        if (int rc2 = check_launch("cl_tree_conv_backward(moments)")) return rc2;
+    }
+    if (sp.mode == 2) {
+        const int64_t row_bytes = int64_t(d.w) * int64_t(sizeof(T));
+        CL_ARG(row_bytes <= kGatherLdsBytes,
+               "input rows of more than %lld bytes are not supported by the input gradient",
+               (long long)kGatherLdsBytes);
+        const int band_rows = int(std::min<int64_t>(d.h, kGatherLdsBytes / row_bytes));
+        const int nbands = int(ceil_div(d.h, band_rows));
+        const int64_t hw_bytes = int64_t(band_rows) * row_bytes;
+        const int pw_lanes = gather_lanes(d.P);
+        int spw = std::max(1, 32 / pw_lanes);
+        while (spw > 1 && int64_t(spw) * hw_bytes > kGatherLdsBytes) spw >>= 1;
+        const int cg = int(std::max<int64_t>(1, std::min<int64_t>(
+            std::min<int64_t>(d.cin, 4 * (64 / (pw_lanes * spw))),
+            kGatherLdsBytes / (hw_bytes * spw))));
+        CL_ARG(nbands < 65536, "input planes too tall for the input gradient");
+        const dim3 g2(unsigned(ceil_div(d.n, spw)), unsigned(ceil_div(d.cin, cg)),
+                      unsigned(nbands));
+        const size_t lds = size_t(spw) * size_t(cg) * size_t(hw_bytes);
+        k_tree_gather<T, true><<<g2, 256, lds, s>>>(gconv, xs, sel, idx, ent_ptr, ent, kc, d,
+                                                    cg, pw_lanes, spw, band_rows, grad_x);
+        if (int rc2 = check_launch("cl_tree_conv_backward(gather)")) return rc2;
+    }
+    return CL_OK;
+}
+
 int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const void* w_prob,
                             const int32_t* selection, const int32_t* indices,
                             const int32_t* ent_ptr, const int32_t* ent, int64_t n, int64_t c_in,
@@ -1578,10 +2117,17 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
         CL_ARG(grad_y && x && w_prob && selection, "null pointer argument");
         CL_ARG(!complete || indices, "the complete block's backward needs the pooling indices");
         CL_ARG(!grad_x || (ent_ptr && ent), "the input gradient needs the channel use index");
-        const int64_t need = tree_workspace_bytes<T>(d, grad_x != nullptr);
+        const int64_t need = tree_workspace_bytes<T>(d, grad_x != nullptr, kernel_h, kernel_w);
         CL_ARG(workspace && workspace_bytes >= need,
                "workspace of %lld bytes needed (see cl_tree_conv_workspace)", (long long)need);
         CL_ARG(aligned(workspace, 256), "workspace must be 256-byte aligned");
+        StagePlan sp;
+        if (plan_tree_stage(d, kernel_h, kernel_w, grad_x != nullptr, sizeof(T), sp))
+            return tree_backward_staged<T>(d, sp, static_cast<const T*>(grad_y),
+                                           static_cast<const T*>(x),
+                                           static_cast<const T*>(w_prob), selection, indices,
+                                           ent_ptr, ent, static_cast<T*>(grad_x),
+                                           static_cast<T*>(grad_w), workspace, s);
         const int64_t nblk = node_blocks(d, &d.node_items);
         unsigned char* ws = static_cast<unsigned char*>(workspace);
         T* radd = nullptr;
