@@ -56,6 +56,12 @@ SIGNATURES: dict[str, list] = {
     "cl_tree_conv_backward_softmax": [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                       _i64, _int, _int, _int, _int, _int, _int, _int, _p, _p, _p,
                                       _i64, _int, _p],
+    "cl_tree_conv_forward_softmax_coefs": [_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                           _int, _int, _int, _int, _int, _int, _p, _p, _p, _p,
+                                           _int, _int, _p, _p],
+    "cl_tree_conv_backward_softmax_coefs": [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                                            _i64, _i64, _int, _int, _int, _int, _int, _int, _p,
+                                            _p, _p, _i64, _int, _p, _p],
     "cl_tree_level_forward": [_int, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
     "cl_tree_level_workspace": [_int, _i64, _i64, _i64, _i64, _p],
     "cl_tree_level_backward": [_int, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],

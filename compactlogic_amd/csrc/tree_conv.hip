@@ -53,6 +53,10 @@ struct TreeDims {
     int y_rows;   // complete form: y / grad_y element (n, c, p) at (c * P + p) * n_total + n
     int P;  // items per (sample, channel): pooled windows (complete) or conv positions
     int node_items;  // items per thread of the backward node kernel (set by node_blocks)
+    // complete block forward: when set, the collapsed coefficients [cout][7][4] (of the
+    // probabilities, or of the logits' softmax) written by the workgroups of sample 0, in the
+    // order k_tree_coefs forms them, for the backward to take instead of forming them again
+    void* coefs;
     FastDiv div_p, div_wp;  // by P, and by the windows per pooled row (complete) or wo
     FastDiv div_wo;         // by wo (conv positions -> rows)
 };
@@ -297,6 +301,9 @@ __global__ __launch_bounds__(256) void k_tree_fwd_q(const T* __restrict__ x, con
     __syncthreads();
     load_channel(w_prob, sel, c, 7, d, sk, st, &bad);
     __syncthreads();
+    if (d.coefs && blockIdx.x == 0 && threadIdx.x < kMaxNodes * 4)
+        static_cast<T*>(d.coefs)[int64_t(c) * kMaxNodes * 4 + threadIdx.x] =
+            sk[threadIdx.x >> 2][threadIdx.x & 3];
     const int64_t total = int64_t(d.n) * d.P * 4;
     // kFwdItems passes of 256 items per workgroup: the channel's coefficients are collapsed
     // once for all of them.
@@ -444,6 +451,10 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
     const int* tflag = L.tflag;
     const int tid = threadIdx.x, nt = blockDim.x;
     stage_sample<T, NODES>(x, w_prob, sel, d, g, n, c_lo, c_n, L);
+    if (COMPLETE && d.coefs && n == 0) {
+        T* kco = static_cast<T*>(d.coefs) + int64_t(c_lo) * NK;
+        for (int i = threadIdx.x; i < c_n * NK; i += blockDim.x) kco[i] = coef[i];
+    }
 
     const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
     const int cpw = g.ip >= 64 ? 1 : 64 / g.ip;
@@ -1686,6 +1697,7 @@ int tree_dims(TreeDims& d, int64_t n, int64_t cin, int64_t h, int64_t w, int64_t
                n * P < (int64_t(1) << 40) && cout < 65536,
            "block too large");
     d.n = int(n);
+    d.coefs = nullptr;
     d.cin = int(cin);
     d.h = int(h);
     d.w = int(w);
@@ -1951,12 +1963,15 @@ int tree_conv_forward_impl(int dtype, const void* x, const void* w_prob,
                            int64_t w, int64_t c_out, int stride_h, int stride_w, int pad_h,
                            int pad_w, int kernel_h, int kernel_w, int complete, void* y, void* x2,
                            void* x3, int32_t* indices, int softmax, int regular, int y_rows,
-                           void* stream) {
+                           void* coefs, void* stream) {
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
         return rc;
     CL_ARG(!y_rows || complete, "the feature-major output is for the complete block");
+    CL_ARG(!coefs || complete, "the coefficient output is for the complete block");
+    CL_ARG(!coefs || aligned(coefs, 16), "coefs must be 16-byte aligned");
+    d.coefs = coefs;
     d.softmax = softmax ? 1 : 0;
     d.regular = regular ? 1 : 0;
     d.y_rows = y_rows ? 1 : 0;
@@ -2006,7 +2021,7 @@ extern "C" int cl_tree_conv_forward(int dtype, const void* x, const void* w_prob
     clear_error();
     return tree_conv_forward_impl(dtype, x, w_prob, selection, n, c_in, h, w, c_out, stride_h,
                                   stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
-                                  indices, 0, 0, 0, stream);
+                                  indices, 0, 0, 0, nullptr, stream);
 }
 
 extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void* w_logits,
@@ -2019,7 +2034,22 @@ extern "C" int cl_tree_conv_forward_softmax(int dtype, const void* x, const void
     clear_error();
     return tree_conv_forward_impl(dtype, x, w_logits, selection, n, c_in, h, w, c_out, stride_h,
                                   stride_w, pad_h, pad_w, kernel_h, kernel_w, complete, y, x2, x3,
-                                  indices, 1, regular_taps, y_rows, stream);
+                                  indices, 1, regular_taps, y_rows, nullptr, stream);
+}
+
+extern "C" int cl_tree_conv_forward_softmax_coefs(int dtype, const void* x, const void* w_logits,
+                                                  const int32_t* selection, int64_t n,
+                                                  int64_t c_in, int64_t h, int64_t w,
+                                                  int64_t c_out, int stride_h, int stride_w,
+                                                  int pad_h, int pad_w, int kernel_h,
+                                                  int kernel_w, void* y, void* x2, void* x3,
+                                                  int32_t* indices, int regular_taps, int y_rows,
+                                                  void* coefs, void* stream) {
+    clear_error();
+    CL_ARG(coefs, "null pointer argument");
+    return tree_conv_forward_impl(dtype, x, w_logits, selection, n, c_in, h, w, c_out, stride_h,
+                                  stride_w, pad_h, pad_w, kernel_h, kernel_w, 1, y, x2, x3,
+                                  indices, 1, regular_taps, y_rows, coefs, stream);
 }
 
 extern "C" int cl_tree_conv_workspace(int dtype, int64_t n, int64_t c_in, int64_t h, int64_t w,
@@ -2043,7 +2073,7 @@ template <typename T>
 int tree_backward_staged(const TreeDims& d, const StagePlan& sp, const T* gy, const T* xs,
                          const T* wp, const int32_t* sel, const int32_t* idx,
                          const int32_t* ent_ptr, const int32_t* ent, T* grad_x, T* grad_w,
-                         void* workspace, hipStream_t s) {
+                         void* workspace, const T* coefs_in, hipStream_t s) {
     unsigned char* ws = static_cast<unsigned char*>(workspace);
     T* part = reinterpret_cast<T*>(ws);
     int64_t off = (int64_t(d.cout) * d.n * kMomStride * sizeof(T) + 255) / 256 * 256;
@@ -2054,8 +2084,12 @@ int tree_backward_staged(const TreeDims& d, const StagePlan& sp, const T* gy, co
     TreeStage g = sp.g;
     g.vec = (d.w % (16 / int(sizeof(T))) == 0 && aligned(xs, 16) &&
              (!grad_x || aligned(grad_x, 16))) ? 1 : 0;
-    k_tree_coefs<T><<<unsigned(d.cout), 64, 0, s>>>(wp, sel, d, kc);
-    if (int rc = check_launch("cl_tree_conv_backward(coefficients)")) return rc;
+    if (coefs_in) {
+        kc = const_cast<T*>(coefs_in);  // read only
+    } else {
+        k_tree_coefs<T><<<unsigned(d.cout), 64, 0, s>>>(wp, sel, d, kc);
+        if (int rc = check_launch("cl_tree_conv_backward(coefficients)")) return rc;
+    }
     T* pw = grad_w ? part : nullptr;
     static bool reserved[3][2][kMaxDevices] = {};
     const int ti = sizeof(T) == 4 ? 0 : 1;
@@ -2107,7 +2141,7 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
                             int64_t h, int64_t w, int64_t c_out, int stride_h, int stride_w,
                             int pad_h, int pad_w, int kernel_h, int kernel_w, int complete,
                             void* grad_x, void* grad_w, void* workspace, int64_t workspace_bytes,
-                            int softmax, int y_rows, void* stream) {
+                            int softmax, int y_rows, const void* coefs, void* stream) {
     TreeDims d;
     if (int rc = tree_dims(d, n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, complete))
@@ -2142,7 +2176,8 @@ int tree_conv_backward_impl(int dtype, const void* grad_y, const void* x, const 
                                            static_cast<const T*>(x),
                                            static_cast<const T*>(w_prob), selection, indices,
                                            ent_ptr, ent, static_cast<T*>(grad_x),
-                                           static_cast<T*>(grad_w), workspace, s);
+                                           static_cast<T*>(grad_w), workspace,
+                                           static_cast<const T*>(coefs), s);
         const int64_t nblk = node_blocks(d, &d.node_items);
         unsigned char* ws = static_cast<unsigned char*>(workspace);
         T* radd = nullptr;
@@ -2230,7 +2265,7 @@ extern "C" int cl_tree_conv_backward(int dtype, const void* grad_y, const void* 
     return tree_conv_backward_impl(dtype, grad_y, x, w_prob, selection, indices, ent_ptr, ent, n,
                                    c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
                                    kernel_w, complete, grad_x, grad_w, workspace,
-                                   workspace_bytes, 0, 0, stream);
+                                   workspace_bytes, 0, 0, nullptr, stream);
 }
 
 extern "C" int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
@@ -2247,7 +2282,26 @@ extern "C" int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, cons
     return tree_conv_backward_impl(dtype, grad_y, x, w_logits, selection, indices, ent_ptr, ent,
                                    n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
                                    kernel_h, kernel_w, complete, grad_x, grad_w, workspace,
-                                   workspace_bytes, 1, y_rows, stream);
+                                   workspace_bytes, 1, y_rows, nullptr, stream);
+}
+
+extern "C" int cl_tree_conv_backward_softmax_coefs(int dtype, const void* grad_y, const void* x,
+                                                   const void* w_logits,
+                                                   const int32_t* selection,
+                                                   const int32_t* indices,
+                                                   const int32_t* ent_ptr, const int32_t* ent,
+                                                   int64_t n, int64_t c_in, int64_t h, int64_t w,
+                                                   int64_t c_out, int stride_h, int stride_w,
+                                                   int pad_h, int pad_w, int kernel_h,
+                                                   int kernel_w, void* grad_x, void* grad_w,
+                                                   void* workspace, int64_t workspace_bytes,
+                                                   int y_rows, const void* coefs, void* stream) {
+    clear_error();
+    CL_ARG(coefs, "null pointer argument");
+    return tree_conv_backward_impl(dtype, grad_y, x, w_logits, selection, indices, ent_ptr, ent,
+                                   n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
+                                   kernel_h, kernel_w, 1, grad_x, grad_w, workspace,
+                                   workspace_bytes, 1, y_rows, coefs, stream);
 }
 
 extern "C" int cl_tree_level_forward(int dtype, const void* x, const void* w_prob, int64_t n,

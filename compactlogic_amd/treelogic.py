@@ -107,7 +107,7 @@ def _forward_tail(softmax: bool, regular: bool, y_rows: bool = False):
 
 def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, kernel_h,
                            kernel_w, intermediate: bool = True, softmax: bool = False,
-                           regular: bool = False, y_rows: bool = False):
+                           regular: bool = False, y_rows: bool = False, coefs=None):
     """Complete block forward (replaces convlogic_cuda.full_convlogic_forward,
     full_convlogic_kernel.cu:156-231): (y [N, C, Ho/2, Wo/2], x2 [N, C, Ho, Wo, 4],
     x3 [N, C, Ho, Wo, 2], indices int32 [N, C, Ho/2 * Wo/2]); x2 and x3 are None unless
@@ -115,8 +115,17 @@ def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_
     softmax (cl_tree_conv_forward_softmax); `regular` then passes that call the guarantee that
     every tap lies in the kernel window and reads an input channel, and `y_rows` has it write y
     feature-major: y is then the [N, C, Ho/2, Wo/2] view of a contiguous [C*Ho/2*Wo/2, N]
-    buffer, which flattens to the transpose a following dense layer reads as its rows."""
+    buffer, which flattens to the transpose a following dense layer reads as its rows.
+    `coefs` (logits only): a [C, 7, 4] tensor the call fills with the collapsed node
+    coefficients for tree_conv_backward(..., coefs=) on the same logits
+    (cl_tree_conv_forward_softmax_coefs)."""
     c_out = _check_block(x, w_prob, selection, 7)
+    if coefs is not None:
+        if not softmax:
+            raise ValueError("the coefficient hand-over is for the logits forward")
+        _dl._check(coefs, "coefs")
+        if tuple(coefs.shape) != (c_out, 7, 4) or coefs.dtype != x.dtype:
+            raise RuntimeError(f"coefs must be [{c_out}, 7, 4] of the dtype of x")
     n, c_in, h, w = x.shape
     ho, wo = _out_hw(h, w, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
     if ho <= 0 or wo <= 0:
@@ -135,11 +144,20 @@ def full_convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_
         x2 = torch.empty((n, c_out, ho, wo, 4), dtype=x.dtype, device=x.device)
         x3 = torch.empty((n, c_out, ho, wo, 2), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        timing.timed(f"cl_tree_conv_forward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
-            *_forward_call(softmax, regular, y_rows), _dl.dtype_code(x), x.data_ptr(),
-            w_prob.data_ptr(), selection.data_ptr(), n, c_in, h, w, c_out, stride_h, stride_w,
-            pad_h, pad_w, kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2), _dl.ptr(x3),
-            idx.data_ptr(), *_forward_tail(softmax, regular, y_rows), _dl.stream_of(x)))
+        if coefs is not None:
+            timing.timed(f"cl_tree_conv_forward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
+                "cl_tree_conv_forward_softmax_coefs", _dl.dtype_code(x), x.data_ptr(),
+                w_prob.data_ptr(), selection.data_ptr(), n, c_in, h, w, c_out, stride_h,
+                stride_w, pad_h, pad_w, kernel_h, kernel_w, y.data_ptr(), _dl.ptr(x2),
+                _dl.ptr(x3), idx.data_ptr(), int(regular), int(y_rows), coefs.data_ptr(),
+                _dl.stream_of(x)))
+        else:
+            timing.timed(f"cl_tree_conv_forward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
+                *_forward_call(softmax, regular, y_rows), _dl.dtype_code(x), x.data_ptr(),
+                w_prob.data_ptr(), selection.data_ptr(), n, c_in, h, w, c_out, stride_h,
+                stride_w, pad_h, pad_w, kernel_h, kernel_w, 1, y.data_ptr(), _dl.ptr(x2),
+                _dl.ptr(x3), idx.data_ptr(), *_forward_tail(softmax, regular, y_rows),
+                _dl.stream_of(x)))
     return y, x2, x3, idx
 
 
@@ -163,11 +181,15 @@ def convlogic_forward(x, w_prob, selection, stride_h, stride_w, pad_h, pad_w, ke
 
 def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w, pad_h, pad_w,
                        kernel_h, kernel_w, complete: bool, need_x: bool = True,
-                       need_w: bool = True, uses=None, softmax: bool = False):
+                       need_w: bool = True, uses=None, softmax: bool = False, coefs=None):
     """(grad_x or None, grad_w_prob or None) of the complete block or of the conv gates
     (replaces full_convlogic_backward_x / _weight and convlogic_backward_x / _weight).  `uses`
     is channel_uses(selection, C_in), computed when not given.  With `softmax`, w_prob holds
-    the node logits and the second result is the gradient of the logits."""
+    the node logits and the second result is the gradient of the logits; `coefs` (complete
+    block, logits) are those full_convlogic_forward(..., coefs=) filled for these logits
+    (cl_tree_conv_backward_softmax_coefs)."""
+    if coefs is not None and not (softmax and complete):
+        raise ValueError("the coefficient hand-over is for the complete block's logits")
     nodes = 7 if complete else 4
     c_out = _check_block(x, w_prob, selection, nodes)
     n, c_in, h, w = x.shape
@@ -193,13 +215,24 @@ def tree_conv_backward(grad_y, x, w_prob, selection, indices, stride_h, stride_w
                pad_w, kernel_h, kernel_w, int(complete), int(gx is not None), ctypes.byref(need))
     ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=x.device)
     with torch.cuda.device(x.device):
-        timing.timed(f"cl_tree_conv_backward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
-            "cl_tree_conv_backward_softmax" if softmax else "cl_tree_conv_backward", code,
-            grad_y.data_ptr(), x.data_ptr(), w_prob.data_ptr(),
-            selection.data_ptr(), indices.data_ptr() if complete else None, _dl.ptr(ptr),
-            _dl.ptr(ent), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w, kernel_h,
-            kernel_w, int(complete), _dl.ptr(gx), _dl.ptr(gw), ws.data_ptr(), need.value,
-            *((int(y_rows),) if softmax else ()), _dl.stream_of(x)))
+        if coefs is not None:
+            _dl._check(coefs, "coefs")
+            if tuple(coefs.shape) != (c_out, 7, 4) or coefs.dtype != x.dtype:
+                raise RuntimeError(f"coefs must be [{c_out}, 7, 4] of the dtype of x")
+            timing.timed(f"cl_tree_conv_backward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
+                "cl_tree_conv_backward_softmax_coefs", code, grad_y.data_ptr(), x.data_ptr(),
+                w_prob.data_ptr(), selection.data_ptr(), indices.data_ptr(), _dl.ptr(ptr),
+                _dl.ptr(ent), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
+                kernel_h, kernel_w, _dl.ptr(gx), _dl.ptr(gw), ws.data_ptr(), need.value,
+                int(y_rows), coefs.data_ptr(), _dl.stream_of(x)))
+        else:
+            timing.timed(f"cl_tree_conv_backward[{c_in}x{h}x{w}->{c_out}]", lambda: _capi.call(
+                "cl_tree_conv_backward_softmax" if softmax else "cl_tree_conv_backward", code,
+                grad_y.data_ptr(), x.data_ptr(), w_prob.data_ptr(),
+                selection.data_ptr(), indices.data_ptr() if complete else None, _dl.ptr(ptr),
+                _dl.ptr(ent), n, c_in, h, w, c_out, stride_h, stride_w, pad_h, pad_w,
+                kernel_h, kernel_w, int(complete), _dl.ptr(gx), _dl.ptr(gw), ws.data_ptr(),
+                need.value, *((int(y_rows),) if softmax else ()), _dl.stream_of(x)))
     return gx, gw
 
 
@@ -599,11 +632,16 @@ class _FullConvLogicWithUses(Function):
     def forward(ctx, x, w, selection, stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w,
                 return_intermediate, return_indices, uses, softmax=False, regular=False,
                 y_rows=False):
+        # the logits path hands the collapsed coefficients from the forward to the backward
+        # (autograd's version check on the saved w guards that both see the same logits)
+        coefs = (torch.empty((selection.shape[0], 7, 4), dtype=x.dtype, device=x.device)
+                 if softmax else None)
         y, x2, x3, idx = full_convlogic_forward(x, w, selection, stride_h, stride_w, pad_h,
                                                 pad_w, kernel_h, kernel_w,
                                                 intermediate=return_intermediate,
-                                                softmax=softmax, regular=regular, y_rows=y_rows)
-        ctx.save_for_backward(x, w, selection, idx)
+                                                softmax=softmax, regular=regular, y_rows=y_rows,
+                                                coefs=coefs)
+        ctx.save_for_backward(x, w, selection, idx, coefs)
         ctx.geom = (stride_h, stride_w, pad_h, pad_w, kernel_h, kernel_w)
         ctx.uses = uses
         ctx.softmax = softmax
@@ -619,11 +657,11 @@ class _FullConvLogicWithUses(Function):
 
     @staticmethod
     def backward(ctx, grad_y, *unused):
-        x, w, selection, idx = ctx.saved_tensors
+        x, w, selection, idx, coefs = ctx.saved_tensors
         gx, gw = tree_conv_backward(grad_y, x, w, selection, idx, *ctx.geom, complete=True,
                                     need_x=ctx.needs_input_grad[0],
                                     need_w=ctx.needs_input_grad[1], uses=ctx.uses,
-                                    softmax=ctx.softmax)
+                                    softmax=ctx.softmax, coefs=coefs)
         return gx, gw, None, None, None, None, None, None, None, None, None, None, None, None, None
 
 

@@ -679,6 +679,32 @@ int cl_tree_conv_backward_softmax(int dtype, const void* grad_y, const void* x,
                                   void* grad_x, void* grad_w, void* workspace,
                                   int64_t workspace_bytes, int y_rows, void* stream);
 
+/* The complete block's logits forward and backward with the collapsed node coefficients
+ * handed from one to the other (no reference counterpart: the reference's backward collapses
+ * the probabilities again, full_convlogic_kernel.cu:233-701).  The forward also writes coefs
+ * [c_out, 7, 4] (16-byte aligned): per node the four coefficients of K0 + K1 a + K2 b + K3 a b
+ * collapsed from the softmax of its logits, exactly as the backward forms them; the backward
+ * takes them instead of forming them again (one launch fewer), so the pair must see the same
+ * logits.  Results are those of cl_tree_conv_forward_softmax / cl_tree_conv_backward_softmax
+ * with complete = 1; coefs NULL is an error. */
+int cl_tree_conv_forward_softmax_coefs(int dtype, const void* x, const void* w_logits,
+                                       const int32_t* selection, int64_t n, int64_t c_in,
+                                       int64_t h, int64_t w, int64_t c_out, int stride_h,
+                                       int stride_w, int pad_h, int pad_w, int kernel_h,
+                                       int kernel_w, void* y, void* x2, void* x3,
+                                       int32_t* indices, int regular_taps, int y_rows,
+                                       void* coefs, void* stream);
+
+int cl_tree_conv_backward_softmax_coefs(int dtype, const void* grad_y, const void* x,
+                                        const void* w_logits, const int32_t* selection,
+                                        const int32_t* indices, const int32_t* ent_ptr,
+                                        const int32_t* ent, int64_t n, int64_t c_in, int64_t h,
+                                        int64_t w, int64_t c_out, int stride_h, int stride_w,
+                                        int pad_h, int pad_w, int kernel_h, int kernel_w,
+                                        void* grad_x, void* grad_w, void* workspace,
+                                        int64_t workspace_bytes, int y_rows, const void* coefs,
+                                        void* stream);
+
 /* One tree level (TreeLogicLayer).  Replaces treelogic_forward (treelogic_kernel.cu:46-86):
  * x [n, channels, positions, 2*out_bits] -> y [n, channels, positions, out_bits], node j of the
  * channel on inputs (2j, 2j+1); w_prob [channels, out_bits, 16]; out_bits <= 4. */

@@ -660,3 +660,41 @@ def test_tree_network_with_feature_major_block_output_trains_identically():
         grads.append([p.grad.clone() for p in net.parameters()])
     assert torch.equal(losses[0], losses[1])
     assert all(torch.equal(a, b) for a, b in zip(*grads))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("stride,pad,kernel,shape,rows", [
+    ((2, 2), (1, 1), (3, 3), (3, 16, 8, 8, 32), True),      # conv2 geometry, staged forward
+    ((2, 2), (1, 1), (3, 3), (4, 9, 32, 32, 160), False),   # conv1 geometry, staged forward
+    ((1, 1), (1, 1), (3, 3), (2, 5, 64, 64, 3), False),     # global-gather forward, big planes
+])
+def test_coefficient_handover_matches_the_separate_calls(dtype, stride, pad, kernel, shape, rows):
+    """cl_tree_conv_forward_softmax_coefs writes each node's collapsed coefficients (checked
+    against the oracle's collapse of softmax(logits)) and leaves the forward's outputs bitwise
+    unchanged; cl_tree_conv_backward_softmax_coefs on them gives bitwise the gradients of the
+    backward that forms them itself."""
+    n, c_in, h, w, c_out = shape
+    x, _, sel = make(21, n, c_in, h, w, c_out, kernel[0], dtype=dtype)
+    g = torch.Generator().manual_seed(22)
+    logits64 = 2.0 * torch.randn((c_out, 7, 16), generator=g, dtype=torch.float64)
+    logits = logits64.to(x.device, dtype)
+    y0, _, _, idx0 = TL.full_convlogic_forward(x, logits, sel, *stride, *pad, *kernel,
+                                               intermediate=False, softmax=True, y_rows=rows)
+    coefs = torch.full((c_out, 7, 4), float("nan"), dtype=dtype, device=x.device)
+    y1, _, _, idx1 = TL.full_convlogic_forward(x, logits, sel, *stride, *pad, *kernel,
+                                               intermediate=False, softmax=True, y_rows=rows,
+                                               coefs=coefs)
+    assert torch.equal(y0, y1) and torch.equal(idx0, idx1)
+    want = T.collapse(np_(torch.softmax(logits64, -1)))
+    np.testing.assert_allclose(np_(coefs), want, **tol(dtype))
+    gy = torch.randn(y0.shape, generator=g, dtype=torch.float64).to(x.device, dtype)
+    if rows:  # the feature-major gradient a flattened dense layer hands back
+        gy = gy.permute(1, 2, 3, 0).contiguous().permute(3, 0, 1, 2)
+    gx0, gw0 = TL.tree_conv_backward(gy, x, logits, sel, idx0, *stride, *pad, *kernel, True,
+                                     softmax=True)
+    gx1, gw1 = TL.tree_conv_backward(gy, x, logits, sel, idx0, *stride, *pad, *kernel, True,
+                                     softmax=True, coefs=coefs)
+    assert torch.equal(gx0, gx1) and torch.equal(gw0, gw1)
+    with pytest.raises(ValueError):
+        TL.tree_conv_backward(gy, x, logits, sel, idx0, *stride, *pad, *kernel, True,
+                              softmax=False, coefs=coefs)
