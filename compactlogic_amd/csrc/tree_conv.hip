@@ -1027,8 +1027,9 @@ __global__ __launch_bounds__(256) void k_tree_finalize(const T* __restrict__ par
 //   MODE 0  moments only;
 //   MODE 1  with the input gradient: every tap's contribution (the radd of k_tree_nodes) stays
 //           in LDS, then lane groups of PL lanes per input channel walk its uses in use order
-//           (the order of k_tree_gather_rec, so every plane word takes its additions in the
-//           same order) into the sample's input gradient in LDS, stored once; cg = cout;
+//           (for P <= PL the order of k_tree_gather_rec, so every plane word takes its
+//           additions in the same order) into the sample's input gradient in LDS, stored once;
+//           cg = cout;
 //   MODE 2  with the conv-gate gradients stored for k_tree_gather (contributions that do not
 //           fit LDS).
 // A tap outside the kernel window (never drawn by the sampler) is read from global memory with
@@ -1041,6 +1042,7 @@ struct TreeStage {
     int glanes;         // PL: lanes per input channel in the gather (power of two, <= 64)
     int vec;            // rows of x (and grad_x) are whole 16-byte vectors, aligned
     int ul_words;       // MODE 1: room for the packed use list after the gradient planes
+    int balance;        // MODE 1: input channels gathered in an order by use count
     int x_words;        // staged input (MODE 1: also the input gradient, after the node phase)
     int c_words;        // contributions (MODE 1)
     int64_t per_xcd;    // workgroups per XCD
@@ -1049,8 +1051,19 @@ struct TreeStage {
 
 constexpr int kMomStride = 32;  // words per (channel, sample) moment record (28 used)
 
+// A channel use u = c * 8 + k for the staged gather: its contribution slot
+// c * 8 + ((k + c / 4) & 7) (the bank rotation of the contribution array) in the low 16 bits,
+// the tap's column and row (selection bits 0..15) in the high 16.
+__device__ __forceinline__ uint32_t pack_use(int u, int32_t sv) {
+    const int c = u >> 3, k = u & 7;
+    return uint32_t(c * 8 + ((k + (c >> 2)) & 7)) | (uint32_t(sv & 0xFFFF) << 16);
+}
+
 #ifndef CL_TREE_NT
 #define CL_TREE_NT 1     // moment records stored non-temporally
+#endif
+#ifndef CL_TREE_UB
+#define CL_TREE_UB 8     // channel uses a gather batch reads before its additions
 #endif
 #ifndef CL_TREE_NT_GX
 #define CL_TREE_NT_GX 0  // the staged input gradient stored non-temporally (slower: 47 vs 38 us)
@@ -1071,7 +1084,7 @@ __global__ __launch_bounds__(NT) void k_tree_bwd_staged(
     constexpr int VEC = 16 / sizeof(T);  // elements per 16-byte load or store
     typedef T V __attribute__((ext_vector_type(VEC)));
     constexpr int SB = 8;                 // staging loads in flight per thread
-    constexpr int UB = 8;                 // channel uses whose records load together (global)
+    constexpr int UB = CL_TREE_UB;        // channel uses whose records load together
     extern __shared__ unsigned char smem_raw[];
     T* xs = reinterpret_cast<T*>(smem_raw);
     // MODE 1: contributions cb[p * cs + cl * 8 + ((k + (cl >> 2)) & 7)] (the rotation by cl / 4
@@ -1280,16 +1293,43 @@ __global__ __launch_bounds__(NT) void k_tree_bwd_staged(
                     const int e = e0 + q * NT + t;
                     const bool ok = uint32_t(u4[q]) < uint32_t(cg * kTaps);
                     const int32_t sv = sel[ok ? u4[q] : 0];
-                    if (e < eb)
-                        ul[e - ea] = ok ? (uint32_t(u4[q]) | (uint32_t(sv & 0xFFFF) << 16))
-                                        : 0xFFFFFFFFu;
+                    if (e < eb) ul[e - ea] = ok ? pack_use(u4[q], sv) : 0xFFFFFFFFu;
                 }
             }
+        }
+        // Channels dealt to the lane groups in an order by use count (a counting sort by
+        // LDS atomics): a wave's groups then walk about as many uses each, where in channel
+        // order the wave waits for its busiest channel.  Each channel's additions keep their
+        // order, so the order of the channels changes no result.
+        int* perm = wins + d.P * (g.cg + 1);  // after the winners: [cin], then [64]
+        int* hist = perm + d.cin;
+        int bin = 0, pos = 0;
+        if (g.balance) {
+            if (t < 64) hist[t] = 0;
+            __syncthreads();
+            if (t < d.cin) {
+                const int cnt = ent_ptr[t + 1] - ent_ptr[t];
+                bin = 63 - min(max(cnt, 0), 63);  // busiest first
+                pos = atomicAdd(&hist[bin], 1);
+            }
+            __syncthreads();
+            if (t < 64) {  // exclusive scan of the 64 bins by the first wave
+                const int h = hist[t];
+                int incl = h;
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int v = __shfl_up(incl, o, 64);
+                    if (t >= o) incl += v;
+                }
+                hist[t] = incl - h;
+            }
+            __syncthreads();
+            if (t < d.cin) perm[hist[bin] + pos] = t;
         }
         __syncthreads();
         const int PL = g.glanes;
         const int pl = t & (PL - 1);
-        for (int ch = t / PL; ch < d.cin; ch += NT / PL) {
+        for (int chs = t / PL; chs < d.cin; chs += NT / PL) {
+            const int ch = g.balance ? perm[chs] : chs;
             const int e0 = ent_ptr[ch], e1 = ent_ptr[ch + 1];
             T* gp = xs + ch * hw;
             for (int e = e0; e < e1; e += UB) {
@@ -1309,25 +1349,32 @@ __global__ __launch_bounds__(NT) void k_tree_bwd_staged(
                     for (int i = 0; i < UB; ++i) {
                         const bool ok = uint32_t(ub[i]) < uint32_t(cg * kTaps);
                         const int32_t sv = sel[ok ? ub[i] : 0];
-                        rb[i] = ok ? (uint32_t(ub[i]) | (uint32_t(sv & 0xFFFF) << 16))
-                                   : 0xFFFFFFFFu;
+                        rb[i] = ok ? pack_use(ub[i], sv) : 0xFFFFFFFFu;
                     }
                 }
+                // per window pass: the batch's winners and contributions read first, then
+                // its additions in use order (within one use the windows add to distinct
+                // pixels, so each plane word takes its additions in a fixed order: by window
+                // pass, then by use)
+                for (int p = pl; p < d.P; p += PL) {
+                    int tg[UB];
+                    T cv[UB];
 #pragma unroll
-                for (int i = 0; i < UB; ++i) {
-                    if (rb[i] == 0xFFFFFFFFu) continue;
-                    const int u = int(rb[i] & 0xFFFF);
-                    const int c = u >> 3, k = u & 7;
-                    const int dy = int((rb[i] >> 24) & 0xFF) - d.ph;
-                    const int dx = int((rb[i] >> 16) & 0xFF) - d.pw;
-                    const int slot = c * kTaps + ((k + (c >> 2)) & 7);
-                    for (int p = pl; p < d.P; p += PL) {
+                    for (int i = 0; i < UB; ++i) {
+                        const bool on = rb[i] != 0xFFFFFFFFu;
+                        const int slot = on ? int(rb[i] & 0xFFFF) : 0, c = slot >> 3;
                         const int pk = wins[p * wsd + c];
-                        if (pk < 0) continue;
-                        const int iy = (pk >> 16) + dy, ix = (pk & 0xFFFF) + dx;
-                        if (uint32_t(iy) < uint32_t(d.h) && uint32_t(ix) < uint32_t(d.w))
-                            gp[iy * d.w + ix] += cb[p * cs + slot];
+                        cv[i] = cb[p * cs + slot];
+                        const int iy = (pk >> 16) + int(rb[i] >> 24) - d.ph;
+                        const int ix = (pk & 0xFFFF) + int((rb[i] >> 16) & 0xFF) - d.pw;
+                        tg[i] = on && pk >= 0 && uint32_t(iy) < uint32_t(d.h) &&
+                                        uint32_t(ix) < uint32_t(d.w)
+                                    ? iy * d.w + ix
+                                    : -1;
                     }
+#pragma unroll
+                    for (int i = 0; i < UB; ++i)
+                        if (tg[i] >= 0) gp[tg[i]] += cv[i];
                 }
             }
         }
@@ -1895,6 +1942,10 @@ bool plan_tree_stage(const TreeDims& d, int kh, int kw, bool want_gx, size_t tsi
         g.c_words = int(c1);
         g.ul_words = int(x1 - nx);
         sp.lds = lds_of(x1);
+        // the gather's channel order by use count (after the winners), when it fits
+        g.balance = (d.cin <= sp.threads &&
+                     sp.lds + (int64_t(d.cin) + 64) * 4 <= kFwdLdsLimit) ? 1 : 0;
+        if (g.balance) sp.lds += (int64_t(d.cin) + 64) * 4;
     } else {
         sp.mode = want_gx ? 2 : 0;
         // channel groups only where the samples alone leave CUs idle
@@ -1905,6 +1956,7 @@ bool plan_tree_stage(const TreeDims& d, int kh, int kw, bool want_gx, size_t tsi
         g.x_words = int(xw);
         g.c_words = 0;
         g.ul_words = 0;
+        g.balance = 0;
         sp.lds = xw * int64_t(tsize);
     }
     g.groups = int(ceil_div(d.cout, g.cg));
