@@ -1118,12 +1118,17 @@ __global__ __launch_bounds__(NT) void k_tree_bwd_staged(
     // halves a register; flags: bit k tap k staged, bit 8 a tap channel >= C
     uint32_t soff[kTaps / 2];
     uint32_t flags = 0;
+    typedef T V4 __attribute__((ext_vector_type(4)));
     auto load_channel_regs = [&](int cc) {
         const int c = c0 + cc;
+        // one vector load per node (the host checks kc's 16-byte alignment)
+        const V4* kv = reinterpret_cast<const V4*>(kc) + int64_t(c) * kMaxNodes;
 #pragma unroll
-        for (int q = 0; q < kMaxNodes; ++q)
+        for (int q = 0; q < kMaxNodes; ++q) {
+            const V4 v = kv[q];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) sk[q][m] = kc[(int64_t(c) * kMaxNodes + q) * 4 + m];
+            for (int m = 0; m < 4; ++m) sk[q][m] = v[m];
+        }
         flags = 0;
 #pragma unroll
         for (int k = 0; k < kTaps; ++k) {
@@ -2137,6 +2142,7 @@ int tree_backward_staged(const TreeDims& d, const StagePlan& sp, const T* gy, co
     g.vec = (d.w % (16 / int(sizeof(T))) == 0 && aligned(xs, 16) &&
              (!grad_x || aligned(grad_x, 16))) ? 1 : 0;
     if (coefs_in) {
+        CL_ARG(aligned(coefs_in, 16), "coefs must be 16-byte aligned");
         kc = const_cast<T*>(coefs_in);  // read only
     } else {
         k_tree_coefs<T><<<unsigned(d.cout), 64, 0, s>>>(wp, sel, d, kc);
