@@ -342,6 +342,7 @@ struct TreeLds {
     int ip;              // items per channel
     FastDiv div_pos;     // items -> conv rows: windows per pooled row (complete) or wo
     FastDiv div_hw, div_w, div_sw;  // staging: element -> (channel, row, column), phase
+    int idx32;           // n * cout * P < 2^31: output and winner indices in 32 bits
 };
 
 constexpr int kTapFlagIrregular = 1;
@@ -484,6 +485,11 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
             for (int t = 0; t < kTaps; ++t) off[t] = toff[cl_ * kTaps + t];
             const int c = c_lo + cl_;
             const int64_t cell = int64_t(n) * d.cout + c;
+            // 32-bit output / winner index of window p: base + p * step (when g.idx32)
+            const uint32_t ybase = d.y_rows ? uint32_t(c) * uint32_t(d.P) * uint32_t(d.n) + n
+                                            : uint32_t(cell) * uint32_t(d.P);
+            const uint32_t ystep = d.y_rows ? uint32_t(d.n) : 1u;
+            const uint32_t ibase = uint32_t(cell) * uint32_t(d.P);
             for (int j = 0; j < g.ip; j += 64) {
                 const int r = j + r0;
                 const bool live = cok && r < g.ip;
@@ -560,8 +566,13 @@ __device__ __forceinline__ void tree_fwd_lds(const T* __restrict__ x, const T* _
                         wi = take ? wo_ : wi;
                     }
                     if (live && q_lane == 0) {
-                        y[y_at(d, n, c, p)] = poison ? quiet_nan<T>() : rr;
-                        if (idx) idx[cell * d.P + p] = poison ? -1 : wi;
+                        if (g.idx32) {
+                            y[ybase + uint32_t(p) * ystep] = poison ? quiet_nan<T>() : rr;
+                            if (idx) idx[ibase + uint32_t(p)] = poison ? -1 : wi;
+                        } else {
+                            y[y_at(d, n, c, p)] = poison ? quiet_nan<T>() : rr;
+                            if (idx) idx[cell * d.P + p] = poison ? -1 : wi;
+                        }
                     }
                 }
             }
@@ -1828,6 +1839,7 @@ bool plan_tree_lds(const TreeDims& d, int kh, int kw, int ip, int ratio, TreeLds
     groups = int(ceil_div(d.cout, g.cg));
     lds = total(rp, g.cg);
     g.div_pos = make_fastdiv(uint32_t(d.complete ? d.wo / 2 : d.wo));
+    g.idx32 = int64_t(d.n) * d.cout * d.P < (int64_t(1) << 31) ? 1 : 0;
     g.div_hw = make_fastdiv(uint32_t(d.h * d.w));
     g.div_w = make_fastdiv(uint32_t(d.w));
     g.div_sw = make_fastdiv(uint32_t(d.sw));
