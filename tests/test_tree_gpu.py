@@ -698,3 +698,35 @@ def test_coefficient_handover_matches_the_separate_calls(dtype, stride, pad, ker
     with pytest.raises(ValueError):
         TL.tree_conv_backward(gy, x, logits, sel, idx0, *stride, *pad, *kernel, True,
                               softmax=False, coefs=coefs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", [(3, 16, 8, 8, 32), (2, 9, 32, 32, 24)])
+def test_staged_backward_poisons_a_channel_reading_past_the_input(dtype, shape):
+    """Weight gradient only (the network's first block): a channel with a tap on input channel
+    C gets NaN logit gradients from the staged backward, as from the node pass; every other
+    channel matches the oracle."""
+    n, c_in, h, w, c_out = shape
+    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    x, _, ok = make(41, n, c_in, h, w, c_out, 3, dtype=dtype)
+    sel = ok.clone()
+    sel[4, 3] = (sel[4, 3] & 0xFFFF) | (c_in << 16)
+    logits64 = torch.randn((c_out, 7, 16), generator=torch.Generator().manual_seed(42),
+                           dtype=torch.float64)
+    logits = logits64.to(x.device, dtype)
+    y, _, _, idx = TL.full_convlogic_forward(x, logits, sel, *stride, *pad, *kernel,
+                                             intermediate=False, softmax=True)
+    assert bool(torch.isnan(y[:, 4]).all())
+    gy = torch.randn(y.shape, generator=torch.Generator().manual_seed(43),
+                     dtype=torch.float64).to(x.device, dtype)
+    gx, gl = TL.tree_conv_backward(gy, x, logits, sel, idx, *stride, *pad, *kernel, True,
+                                   need_x=False, softmax=True)
+    assert gx is None and bool(torch.isnan(gl[4]).all())
+    live = [c for c in range(c_out) if c != 4]
+    assert not bool(torch.isnan(gl[live]).any())
+    p64 = np_(torch.softmax(logits64, -1))
+    _, rgw = T.block_backward(np_(x).astype(np.float64), p64, np_(ok), stride, pad, kernel,
+                              np_(gy).astype(np.float64), True, idx=np_(idx))
+    rgl = p64 * (rgw - (rgw * p64).sum(-1, keepdims=True))
+    scale = max(1.0, float(np.abs(rgw).max()))
+    np.testing.assert_allclose(np_(gl)[live] / scale, rgl[live] / scale, **tol(dtype))
