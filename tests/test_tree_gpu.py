@@ -44,6 +44,7 @@ SHAPES = [  # stride, pad, kernel, (n, c_in, h, w, c_out)
     ((2, 2), (1, 1), (3, 3), (2, 9, 32, 32, 160)),    # conv1 geometry, a channel per wave
     ((2, 2), (1, 1), (3, 3), (2, 3, 8, 8, 64)),       # 16 items per channel: 4 channels a wave
     ((1, 1), (1, 1), (3, 3), (2, 2, 10, 10, 24)),     # stride 1, 5 windows a row, 100 items
+    ((2, 2), (1, 1), (3, 3), (2, 9, 32, 32, 600)),    # staged backward in three channel groups
 ]
 
 
@@ -730,3 +731,45 @@ def test_staged_backward_poisons_a_channel_reading_past_the_input(dtype, shape):
     rgl = p64 * (rgw - (rgw * p64).sum(-1, keepdims=True))
     scale = max(1.0, float(np.abs(rgw).max()))
     np.testing.assert_allclose(np_(gl)[live] / scale, rgl[live] / scale, **tol(dtype))
+
+
+def test_cfg3_tree_blocks_at_full_size_match_oracle():
+    """The cfg3_tree network's own blocks (logits, sampled taps) on Bernoulli inputs: conv2 at
+    the benched batch of 256 through the staged backward with the input gradient, conv1 (the
+    network's input: logits gradient only) on 32 of its samples, forward outputs and both
+    gradients against the float64 oracle (winners compared away from near ties)."""
+    from compactlogic_amd import configs
+    cfg = configs.TREE_CONFIGS["cfg3_tree"]
+    net = configs.tree_network(cfg, device="cuda")
+    x, _ = configs.conv_inputs(cfg, device="cuda")
+    stride, pad, kernel = (2, 2), (1, 1), (3, 3)
+    with torch.no_grad():
+        h1, _, _, _ = TL.full_convlogic_forward(x, net[0].weights, net[0].selection.int(),
+                                                *stride, *pad, *kernel, intermediate=False,
+                                                softmax=True)
+    for blk, xin in ((net[0], x[:32].contiguous()), (net[2 if isinstance(net[1], torch.nn.Flatten) else 1], h1)):
+        sel = blk.selection.int().contiguous()
+        logits = blk.weights.detach().contiguous()
+        first = blk is net[0]
+        y, _, _, idx = TL.full_convlogic_forward(xin, logits, sel, *stride, *pad, *kernel,
+                                                 intermediate=False, softmax=True)
+        xs = np_(xin).astype(np.float64)
+        p64 = np_(torch.softmax(logits.double(), -1))
+        ss = np_(sel)
+        ry, _, _, ridx = T.block_forward(xs, p64, ss, stride, pad, kernel)
+        eps = float(np.finfo(np.float32).eps)
+        free = _near_ties(_window_scores(xs, p64, ss, stride, pad, kernel), eps)
+        assert np.array_equal(np_(idx)[~free], ridx[~free])
+        np.testing.assert_allclose(np_(y), ry, rtol=1e-5, atol=1e-6)
+        oidx = np.where(free, np_(idx), ridx)
+        gy = torch.randn(y.shape, generator=torch.Generator().manual_seed(51),
+                         dtype=torch.float64).to(xin.device, torch.float32)
+        gx, gl = TL.tree_conv_backward(gy, xin, logits, sel, idx, *stride, *pad, *kernel, True,
+                                       need_x=not first, softmax=True)
+        rgx, rgw = T.block_backward(xs, p64, ss, stride, pad, kernel,
+                                    np_(gy).astype(np.float64), True, idx=oidx)
+        rgl = p64 * (rgw - (rgw * p64).sum(-1, keepdims=True))
+        scale = max(1.0, float(np.abs(rgw).max()))
+        np.testing.assert_allclose(np_(gl) / scale, rgl / scale, rtol=1e-5, atol=1e-6)
+        if not first:
+            np.testing.assert_allclose(np_(gx), rgx, rtol=1e-5, atol=1e-6)
