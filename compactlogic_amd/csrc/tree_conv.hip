@@ -1914,6 +1914,9 @@ inline int64_t tree_records(const TreeDims& d) { return int64_t(d.cout) * kTaps 
 #ifndef CL_TREE_STAGED_BWD
 #define CL_TREE_STAGED_BWD 1  // the staged backward of the complete block where it fits
 #endif
+#ifndef CL_TREE_LMAX
+#define CL_TREE_LMAX 4  // most lanes per channel in the staged backward's node phase
+#endif
 #ifndef CL_TREE_STAGED_NT1
 #define CL_TREE_STAGED_NT1 1024  // threads of the float form with the input gradient
 #endif
@@ -1937,8 +1940,8 @@ bool plan_tree_stage(const TreeDims& d, int kh, int kw, bool want_gx, size_t tsi
     g.hs = (d.ho - 1) * d.sh + kh;
     g.ws = (d.wo - 1) * d.sw + kw;
     g.plane = g.hs * g.ws;
-    int L = 1;  // min(4, largest power of two <= P / 2), at least 1
-    while (2 * L <= 4 && 4 * L <= d.P) L *= 2;
+    int L = 1;  // min(CL_TREE_LMAX, largest power of two <= P / 2), at least 1
+    while (2 * L <= CL_TREE_LMAX && 4 * L <= d.P) L *= 2;
     g.lanes = L;
     g.glanes = gather_lanes(d.P);
     // float: 1024 threads (16 waves, one workgroup per CU); double: 512 (its registers)
