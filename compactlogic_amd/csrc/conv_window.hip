@@ -167,23 +167,64 @@ __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const 
 // ------------------------------------------------------------------------------------------
 // Block (sample n, input channel ch): BS >= Ho * Wo threads, one per output position; the
 // input-gradient plane of (n, ch) is built in LDS and written out whole.
+//
+// LDS layout of the plane (WinPlane): rows and columns split by their phase modulo ps (the
+// stride, or 1 when the split plane does not fit), pixel (yy, xx) at
+// ((yy % ps) * hs + yy / ps) * pitch + (xx % ps) * ws + xx / ps, with hs, ws the rows / columns
+// of one phase.  Tap k of output position (oy, ox) then lands at base + tap[k], base =
+// oy * pitch + ox when ps is the stride (> 1), else base = by * pitch + bx for the window's
+// corner (by, bx); with pitch congruent to Wo modulo 32 the 32 lanes of a half-wave
+// (consecutive positions) add to 32 distinct banks.  With pos = oy * Wo + ox both bases are
+// oy * la + pos * lb + lc for uniform la, lb, lc, taken modulo 2^32 (exact for every lane
+// that adds, whose index lies in the plane).
+//
+// The plane is written out in row-major order; when the block size is a multiple of ps * W a
+// thread keeps one column and its LDS index moves by st_step per pass (else st_step = 0 and
+// every pixel's index is computed).
+struct WinPlane {
+    int ps, hs, ws, pitch, st_step, la, lb, lc;
+    int tap[9];
+    float inv_w, inv_ps, inv_wo;  // 1 / W, 1 / ps and 1 / Wo rounded to float
+    FastDiv div_cin;
+};
+
+// floor(x / d) from inv = 1 / d rounded to float, for 0 <= x < 2^22: (x + 0.5) inv carries a
+// relative error below 2^-23, less than the distance 0.5 / d of (x + 0.5) / d to the nearest
+// integer.  Full-rate float instructions in place of 32-bit integer products.
+__device__ __forceinline__ int small_div(int x, float inv) {
+    return int(fmaf(float(x), inv, 0.5f * inv));
+}
+
+// LDS index of pixel i of the H x W plane in the WinPlane layout (i < 2^22, so every product
+// below fits 24 bits).
+__device__ __forceinline__ int win_plane_at(int i, int W, const WinPlane& lp) {
+    const int yy = small_div(i, lp.inv_w), xx = i - __mul24(yy, W);
+    const int qy = small_div(yy, lp.inv_ps), qx = small_div(xx, lp.inv_ps);
+    return __mul24(__mul24(yy - __mul24(qy, lp.ps), lp.hs) + qy, lp.pitch) +
+           __mul24(xx - __mul24(qx, lp.ps), lp.ws) + qx;
+}
+
 template <typename T, int KW>
 __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
                                                     const T* __restrict__ gy,
                                                     const T* __restrict__ coef,
                                                     const int32_t* __restrict__ grp_ptr,
                                                     const int32_t* __restrict__ chan_order,
-                                                    T* __restrict__ gx, WinDims d) {
+                                                    T* __restrict__ gx, WinDims d, WinPlane lp) {
     constexpr int P = Win<KW>::P, NP = Win<KW>::NP, CW = Win<KW>::CW;
     extern __shared__ __align__(16) unsigned char smem[];
     T* plane = reinterpret_cast<T*>(smem);
-    const int64_t ch = blockIdx.x % d.Cin, n = blockIdx.x / d.Cin;
+    // block = plane n * Cin + ch (fewer than 2^31 blocks)
+    const uint32_t n = fast_div(blockIdx.x, lp.div_cin), ch = blockIdx.x - n * uint32_t(d.Cin);
     const int hw = d.Ho * d.Wo, HW = d.H * d.W;
+    const int words = lp.ps * lp.hs * lp.pitch;
     const int pos = threadIdx.x;
     const bool active = pos < hw;
-    const int oy = active ? pos / d.Wo : 0, ox = active ? pos - oy * d.Wo : 0;
+    const int oy = active ? small_div(pos, lp.inv_wo) : 0, ox = active ? pos - oy * d.Wo : 0;
     const int by = oy * d.stride + d.oy0, bx = ox * d.stride + d.ox0;
-    const T* xplane = x + (n * d.Cin + ch) * int64_t(HW);
+    const int lane_base =
+        int(uint32_t(oy) * uint32_t(lp.la) + uint32_t(pos) * uint32_t(lp.lb) + uint32_t(lp.lc));
+    const T* xplane = x + int64_t(blockIdx.x) * HW;
     T v[P];
     load_window<T, KW>(v, xplane, d.H, d.W, by, bx, active);
     // A_k = sum_c gy_c alpha_kc, B_kl = sum_c gy_c beta_klc over the channels reading ch
@@ -193,7 +234,7 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
 #pragma unroll
     for (int q = 0; q < NP; ++q) B[q] = 0;
     const int c0 = grp_ptr[ch], c1 = grp_ptr[ch + 1];
-    const T* gyn = gy + n * d.Cout * hw + pos;
+    const T* gyn = gy + int64_t(n) * d.Cout * hw + pos;
     for (int i = c0; i < c1; ++i) {
         const int c = chan_order[i];
         const T g = active ? gyn[int64_t(c) * hw] : T(0);
@@ -203,7 +244,10 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
 #pragma unroll
         for (int q = 0; q < NP; ++q) B[q] = fma(g, cf[1 + P + q], B[q]);
     }
-    for (int i = threadIdx.x; i < HW; i += blockDim.x) plane[i] = T(0);
+    // +0 in 16-byte stores (the allocation is rounded up to 16 bytes)
+    const int zvec = (words * int(sizeof(T)) + 15) / 16;
+    uint4* zero = reinterpret_cast<uint4*>(smem);
+    for (int i = threadIdx.x; i < zvec; i += blockDim.x) zero[i] = uint4{0, 0, 0, 0};
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < P; ++k) {
@@ -216,11 +260,18 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
         }
         const int yy = by + k / KW, xx = bx + k % KW;
         if (active && unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W))
-            plane[yy * d.W + xx] += dk;
+            plane[lane_base + lp.tap[k]] += dk;
         __syncthreads();
     }
-    T* gplane = gx + (n * d.Cin + ch) * int64_t(HW);
-    for (int i = threadIdx.x; i < HW; i += blockDim.x) gplane[i] = plane[i];
+    T* gplane = gx + int64_t(blockIdx.x) * HW;
+    if (lp.st_step) {
+        int i = threadIdx.x;
+        for (int at = i < HW ? win_plane_at(i, d.W, lp) : 0; i < HW; i += blockDim.x)
+            gplane[i] = plane[at], at += lp.st_step;
+    } else {
+        for (int i = threadIdx.x; i < HW; i += blockDim.x)
+            gplane[i] = plane[win_plane_at(i, d.W, lp)];
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -265,7 +316,7 @@ __global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
         T v[P];
         load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(HW), d.H, d.W,
                            oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
-        const T* gyn = gy + n * d.Cout * hw + pos;
+        const T* gyn = gy + int64_t(n) * d.Cout * hw + pos;
         n += dn;
         oy += dy;
         ox += dx;
@@ -930,18 +981,55 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
     const int64_t hw = h_out * w_out;
     CL_ARG(hw <= 1024, "the window input gradient needs h_out * w_out <= 1024");
     const size_t tsize = dtype == CL_DTYPE_F64 ? 8 : 4;
-    const size_t lds = size_t(H * W) * tsize;
+    // the plane's LDS layout (see WinPlane): split by the stride's phases with the pitch padded
+    // to Wo modulo 32 when that fits, else split unpadded, else the plain rows
+    auto plane_words = [&](int64_t ps, int64_t pitch) { return ps * ceil_div(H, ps) * pitch; };
+    const int64_t cap = 65536 / int64_t(tsize);
+    WinPlane lp;
+    int64_t ps = stride, pitch = stride * ceil_div(W, stride);
+    while (pitch % 32 != w_out % 32) ++pitch;
+    if (plane_words(ps, pitch) > cap) pitch = stride * ceil_div(W, stride);
+    if (plane_words(ps, pitch) > cap) ps = 1, pitch = W;
+    lp.ps = int(ps);
+    lp.hs = int(ceil_div(H, ps));
+    lp.ws = int(ceil_div(W, ps));
+    lp.pitch = int(pitch);
+    // lane bases (see WinPlane), reduced modulo 2^32
+    const int64_t la = ps > 1 ? pitch - w_out : stride * (pitch - w_out);
+    const int64_t lb = ps > 1 ? 1 : stride, lc = ps > 1 ? 0 : oy0 * pitch + ox0;
+    lp.la = int(uint32_t(uint64_t(la)));
+    lp.lb = int(uint32_t(uint64_t(lb)));
+    lp.lc = int(uint32_t(uint64_t(lc)));
+    for (int k = 0; k < 9; ++k) {
+        if (ps == 1) {  // relative to the window's corner
+            lp.tap[k] = int(k / kw * pitch + k % kw);
+            continue;
+        }
+        // row / column of tap k relative to the position's phase origin (floor division)
+        const int64_t r = oy0 + k / kw, c = ox0 + k % kw;
+        const int64_t qr = r >= 0 ? r / ps : -((-r + ps - 1) / ps);
+        const int64_t qc = c >= 0 ? c / ps : -((-c + ps - 1) / ps);
+        lp.tap[k] = int(((r - qr * ps) * lp.hs + qr) * pitch + (c - qc * ps) * lp.ws + qc);
+    }
+    lp.inv_w = 1.0f / float(W);
+    lp.inv_ps = 1.0f / float(ps);
+    lp.inv_wo = 1.0f / float(w_out);
+    lp.div_cin = make_fastdiv(uint32_t(Cin));
+    const size_t lds = size_t(ceil_div(plane_words(ps, pitch) * int64_t(tsize), 16) * 16);
     CL_ARG(lds <= 65536, "the window input gradient needs the input plane in 64 KiB of LDS");
     const int bs = block_for(hw, 1024);
+    // a pass of bs pixels moves whole rows; with bs / W rows a multiple of ps, every thread's
+    // phase stays fixed and its index moves by bs / (W ps) phase rows
+    lp.st_step = bs % (W * ps) == 0 ? int(bs / (W * ps) * pitch) : 0;
     const int64_t blocks = N * Cin;
-    CL_ARG(blocks < (int64_t(1) << 32), "conv layer too large for one launch");
+    CL_ARG(blocks < (int64_t(1) << 31), "conv layer too large for one launch");
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
             k_win_bwd_x<scalar_t, decltype(K)::value>
                 <<<unsigned(blocks), bs, lds, as_stream(stream)>>>(
                     static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(grad_y),
                     static_cast<const scalar_t*>(coef), grp_ptr, chan_order,
-                    static_cast<scalar_t*>(grad_x), d);
+                    static_cast<scalar_t*>(grad_x), d, lp);
             return CL_OK;
         });
         if (rc) return rc;

@@ -398,6 +398,33 @@ def test_window_path_matches_oracle(device, shape, dtype):
     _layer_vs_oracle(layer, x, gy, dtype)
 
 
+# The input-gradient plane sits in LDS split by the stride's phases with its row pitch padded
+# so that the lanes of a half-wave add to distinct banks, split unpadded when the padding does
+# not fit in 64 KiB, or in plain rows when neither split fits; each layout against the oracle.
+LAYOUT_CASES = [
+    # (c_in, h, w, c_out, G, ks, stride, pad, n), dtype
+    ((3, 16, 20, 6, 8, 3, 4, 1, 3), torch.float32),    # stride 4, window origin -1: padded
+    ((4, 16, 16, 8, 16, 3, 4, 1, 3), torch.float64),   # stride 4, whole rows per store pass
+    ((2, 127, 126, 3, 8, 3, 4, 0, 2), torch.float32),  # padded split too large: unpadded
+    ((2, 63, 130, 3, 8, 3, 4, 0, 2), torch.float32),   # padded split
+    ((2, 63, 130, 3, 8, 3, 4, 0, 2), torch.float64),   # neither split fits: plain rows
+    ((2, 125, 64, 3, 8, 3, 3, 0, 2), torch.float64),   # plain rows, whole rows per store pass
+]
+
+
+@pytest.mark.parametrize("shape,dtype", LAYOUT_CASES,
+                         ids=lambda s: "x".join(map(str, s)) if isinstance(s, tuple) else str(s))
+def test_window_input_gradient_layouts(device, shape, dtype):
+    c_in, h, wd, c_out, g_n, ks, stride, pad, n = shape
+    torch.manual_seed(sum(shape))
+    layer = cl.ConvLayer((c_in, h, wd), padding=pad, c_out=c_out, ks=ks, stride=stride,
+                         num_chn=1, num_gates=g_n).to(device).to(dtype)
+    x = torch.rand((n, c_in, h, wd), device=device, dtype=dtype)
+    assert layer.window_plan(x) is not None
+    gy = torch.empty((n,) + layer.out_shape, device=device, dtype=dtype).uniform_(-1, 1) / n
+    _layer_vs_oracle(layer, x, gy, dtype)
+
+
 @pytest.mark.parametrize("c_out", [20, 256])
 def test_window_path_empty_batch(device, c_out):
     """A batch of 0 samples: empty outputs and input gradient, zero logits gradient, no read of
