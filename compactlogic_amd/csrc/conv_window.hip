@@ -170,8 +170,8 @@ __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const 
 //
 // LDS layout of the plane (WinPlane): rows and columns split by their phase modulo ps (the
 // stride, or 1 when the split plane does not fit), pixel (yy, xx) at
-// ((yy % ps) * hs + yy / ps) * pitch + (xx % ps) * ws + xx / ps, with hs, ws the rows / columns
-// of one phase.  Tap k of output position (oy, ox) then lands at base + tap[k], base =
+// ((yy % ps) * hs + yy / ps) * pitch + (yy % ps) * rgap + (xx % ps) * ws + xx / ps, with hs, ws
+// the rows / columns of one phase.  Tap k of output position (oy, ox) then lands at base + tap[k], base =
 // oy * pitch + ox when ps is the stride (> 1), else base = by * pitch + bx for the window's
 // corner (by, bx); with pitch congruent to Wo modulo 32 the 32 lanes of a half-wave
 // (consecutive positions) add to 32 distinct banks.  With pos = oy * Wo + ox both bases are
@@ -180,9 +180,11 @@ __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const 
 //
 // The plane is written out in row-major order; when the block size is a multiple of ps * W a
 // thread keeps one column and its LDS index moves by st_step per pass (else st_step = 0 and
-// every pixel's index is computed).
+// every pixel's index is computed).  The gap rgap between the phases' row blocks makes row
+// yy + 1 start W banks after row yy when yy % ps < ps - 1, so that a half-wave reading ps
+// rows of ps * W <= 32 pixels meets each bank once.
 struct WinPlane {
-    int ps, hs, ws, pitch, st_step, la, lb, lc;
+    int ps, hs, ws, pitch, rgap, words, st_step, la, lb, lc;
     int tap[9];
     float inv_w, inv_ps, inv_wo;  // 1 / W, 1 / ps and 1 / Wo rounded to float
     FastDiv div_cin;
@@ -200,7 +202,8 @@ __device__ __forceinline__ int small_div(int x, float inv) {
 __device__ __forceinline__ int win_plane_at(int i, int W, const WinPlane& lp) {
     const int yy = small_div(i, lp.inv_w), xx = i - __mul24(yy, W);
     const int qy = small_div(yy, lp.inv_ps), qx = small_div(xx, lp.inv_ps);
-    return __mul24(__mul24(yy - __mul24(qy, lp.ps), lp.hs) + qy, lp.pitch) +
+    const int py = yy - __mul24(qy, lp.ps);
+    return __mul24(__mul24(py, lp.hs) + qy, lp.pitch) + __mul24(py, lp.rgap) +
            __mul24(xx - __mul24(qx, lp.ps), lp.ws) + qx;
 }
 
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
     // block = plane n * Cin + ch (fewer than 2^31 blocks)
     const uint32_t n = fast_div(blockIdx.x, lp.div_cin), ch = blockIdx.x - n * uint32_t(d.Cin);
     const int hw = d.Ho * d.Wo, HW = d.H * d.W;
-    const int words = lp.ps * lp.hs * lp.pitch;
+    const int words = lp.words;
     const int pos = threadIdx.x;
     const bool active = pos < hw;
     const int oy = active ? small_div(pos, lp.inv_wo) : 0, ox = active ? pos - oy * d.Wo : 0;
@@ -983,17 +986,26 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
     const size_t tsize = dtype == CL_DTYPE_F64 ? 8 : 4;
     // the plane's LDS layout (see WinPlane): split by the stride's phases with the pitch padded
     // to Wo modulo 32 when that fits, else split unpadded, else the plain rows
-    auto plane_words = [&](int64_t ps, int64_t pitch) { return ps * ceil_div(H, ps) * pitch; };
+    // words of the layout with the gap between phase row blocks (taken modulo 32)
+    auto gap = [&](int64_t ps, int64_t pitch) {
+        return ps > 1 ? ((W - ceil_div(H, ps) * pitch) % 32 + 32) % 32 : int64_t(0);
+    };
+    auto plane_words = [&](int64_t ps, int64_t pitch, int64_t rgap) {
+        return ps * ceil_div(H, ps) * pitch + (ps - 1) * rgap;
+    };
     const int64_t cap = 65536 / int64_t(tsize);
     WinPlane lp;
-    int64_t ps = stride, pitch = stride * ceil_div(W, stride);
+    int64_t ps = stride, pitch = stride * ceil_div(W, stride), rgap = 0;
     while (pitch % 32 != w_out % 32) ++pitch;
-    if (plane_words(ps, pitch) > cap) pitch = stride * ceil_div(W, stride);
-    if (plane_words(ps, pitch) > cap) ps = 1, pitch = W;
+    rgap = gap(ps, pitch);
+    if (plane_words(ps, pitch, rgap) > cap) pitch = stride * ceil_div(W, stride), rgap = 0;
+    if (plane_words(ps, pitch, rgap) > cap) ps = 1, pitch = W;
     lp.ps = int(ps);
     lp.hs = int(ceil_div(H, ps));
     lp.ws = int(ceil_div(W, ps));
     lp.pitch = int(pitch);
+    lp.rgap = int(rgap);
+    lp.words = int(plane_words(ps, pitch, rgap));
     // lane bases (see WinPlane), reduced modulo 2^32
     const int64_t la = ps > 1 ? pitch - w_out : stride * (pitch - w_out);
     const int64_t lb = ps > 1 ? 1 : stride, lc = ps > 1 ? 0 : oy0 * pitch + ox0;
@@ -1009,13 +1021,14 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
         const int64_t r = oy0 + k / kw, c = ox0 + k % kw;
         const int64_t qr = r >= 0 ? r / ps : -((-r + ps - 1) / ps);
         const int64_t qc = c >= 0 ? c / ps : -((-c + ps - 1) / ps);
-        lp.tap[k] = int(((r - qr * ps) * lp.hs + qr) * pitch + (c - qc * ps) * lp.ws + qc);
+        lp.tap[k] = int(((r - qr * ps) * lp.hs + qr) * pitch + (r - qr * ps) * rgap +
+                        (c - qc * ps) * lp.ws + qc);
     }
     lp.inv_w = 1.0f / float(W);
     lp.inv_ps = 1.0f / float(ps);
     lp.inv_wo = 1.0f / float(w_out);
     lp.div_cin = make_fastdiv(uint32_t(Cin));
-    const size_t lds = size_t(ceil_div(plane_words(ps, pitch) * int64_t(tsize), 16) * 16);
+    const size_t lds = size_t(ceil_div(int64_t(lp.words) * int64_t(tsize), 16) * 16);
     CL_ARG(lds <= 65536, "the window input gradient needs the input plane in 64 KiB of LDS");
     const int bs = block_for(hw, 1024);
     // a pass of bs pixels moves whole rows; with bs / W rows a multiple of ps, every thread's
