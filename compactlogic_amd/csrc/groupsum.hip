@@ -80,7 +80,19 @@ __global__ __launch_bounds__(kPartWaves * 64) void k_gsum_partial(const T* __res
 #pragma unroll
     for (int i = 0; i < VEC; ++i) acc.v[i] = T(0);
     if (n0 < B) {
-        for (int64_t j = j0 + wv; j < j1; j += kPartWaves) {
+        // the wave's rows eight at a time: the loads are issued together, the additions stay
+        // in row order
+        int64_t j = j0 + wv;
+        for (; j + 7 * kPartWaves < j1; j += 8 * kPartWaves) {
+            Vec<T, VEC> v[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) v[r] = vload<T, VEC>(x + (j + r * kPartWaves) * sf + n0);
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) acc.v[i] += v[r].v[i];
+        }
+        for (; j < j1; j += kPartWaves) {
             const Vec<T, VEC> v = vload<T, VEC>(x + j * sf + n0);
 #pragma unroll
             for (int i = 0; i < VEC; ++i) acc.v[i] += v.v[i];
@@ -198,11 +210,13 @@ struct CrossEntropyGrad {
     int64_t k;
     T tau;
     __device__ __forceinline__ T operator()(int64_t n, int64_t c) const {
+        // every load first (one round trip), then the selection
         const int64_t lab = y[n];
+        const T pn = p[n * k + c], g = gl[0], cnt = count[0];
         if (lab == ignore) return T(0);
         if (lab < 0 || lab >= k) return nan_of<T>();
-        const T d = p[n * k + c] - (lab == c ? T(1) : T(0));
-        return d * (gl[0] / (count[0] * tau));
+        const T d = pn - (lab == c ? T(1) : T(0));
+        return d * (g / (cnt * tau));
     }
 };
 
@@ -283,14 +297,23 @@ __global__ __launch_bounds__(kCeThreads) void k_ce_rows(const T* __restrict__ pa
         const T* src = part + c * B + n;
         T t = 0;
         int64_t sl = 0;
-        for (; sl + 8 <= nslices; sl += 8) {
-            T v[8];
+        // up to 32 slices per round of loads (one round for the usual slice counts); the
+        // additions stay in slice order
+        for (; sl + 32 <= nslices; sl += 32) {
+            T v[32];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = src[(sl + i) * step];
+            for (int i = 0; i < 32; ++i) v[i] = src[(sl + i) * step];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) t += v[i];
+            for (int i = 0; i < 32; ++i) t += v[i];
         }
-        for (; sl < nslices; ++sl) t += src[sl * step];
+        if (sl < nslices) {
+            T v[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[i] = sl + i < nslices ? src[(sl + i) * step] : T(0);
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (sl + i < nslices) t += v[i];
+        }
         t = t / tau;
         out[n * k + c] = t;
         z[e] = t;
