@@ -61,7 +61,10 @@ __global__ __launch_bounds__(256) void k_win_prep(const T* __restrict__ w, int s
     const int64_t c = int64_t(blockIdx.x) * 4 + wave_id();
     if (c >= Cout) return;  // uniform per wave
     const int l = lane_id();
+    // every load of the channel first (lane g holds gate g's logit, opcode and taps)
     T p = l < G ? w[c * G + l] : T(0);
+    const int op = l < G ? int(gs[c * G + l]) : 0;
+    const int rec_l = l < G ? slot_win[c * G + l] : 0;
     if (softmax) {
         T m = l < G ? p : -__builtin_inf();
 #pragma unroll
@@ -73,8 +76,8 @@ __global__ __launch_bounds__(256) void k_win_prep(const T* __restrict__ w, int s
     T acc = 0;
     for (int g = 0; g < G; ++g) {
         const T pg = read_lane(p, g);
-        const Coef4<T> cf = gate_coef<T>(gs[c * G + g]);
-        const int rec = slot_win[c * G + g];
+        const Coef4<T> cf = gate_coef<T>(uint8_t(read_lane(op, g)));
+        const int rec = read_lane(rec_l, g);
         const int ka = rec & 0xff, kb = (rec >> 8) & 0xff;
         const int lo = std::min(ka, kb), hi = std::max(ka, kb);
         T add = 0;
@@ -819,6 +822,14 @@ __global__ __launch_bounds__(256) void k_win_finalize(const T* __restrict__ part
     __shared__ T sums[4][64];
     const int64_t c = blockIdx.x;
     const int w = wave_id(), l = lane_id();
+    // the slot's taps, opcode and probability loaded with the moments (wave 0 uses them)
+    int rec = 0, op = 0;
+    T pl = T(0);
+    if (w == 0 && l < G) {
+        rec = slot_win[c * G + l];
+        op = gs[c * G + l];
+        if (probs) pl = probs[c * G + l];
+    }
     T s = 0;
     if (l < CW) {
         int q = w;
@@ -839,18 +850,17 @@ __global__ __launch_bounds__(256) void k_win_finalize(const T* __restrict__ part
     int ia = 0, ib = 0, iab = 0;
     Coef4<T> cf = gate_coef<T>(0);
     if (l < G) {
-        const int rec = slot_win[c * G + l];
         const int ka = rec & 0xff, kb = (rec >> 8) & 0xff;
         ia = 1 + ka;
         ib = 1 + kb;
         iab = beta_at(P, std::min(ka, kb), std::max(ka, kb));
-        cf = gate_coef<T>(gs[c * G + l]);
+        cf = gate_coef<T>(uint8_t(op));
     }
     const T s0 = read_lane(s, 0);
     const T sa = __shfl(s, ia, kWave), sb = __shfl(s, ib, kWave), sab = __shfl(s, iab, kWave);
     if (l < G) gw = fma(cf.c3, sab, fma(cf.c2, sb, fma(cf.c1, sa, cf.c0 * s0)));
     if (probs) {
-        const T p = l < G ? probs[c * G + l] : T(0);
+        const T p = pl;
         const T dot = wave_total(p * gw);
         gw = p * (gw - dot);
     }
