@@ -52,7 +52,7 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--mode", choices=["graph", "eager"], default="graph")
     p.add_argument("--packed-log2-samples", type=int, default=24)
     p.add_argument("--packed-passes", type=int, default=3)
@@ -61,8 +61,8 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=20)
     p.add_argument("--kernel-steps", type=int, default=5)
     p.add_argument("--no-conv", action="store_true")
-    p.add_argument("--conv-steps", type=int, default=50)
-    p.add_argument("--conv-warmup", type=int, default=5)
+    p.add_argument("--conv-steps", type=int, default=100)
+    p.add_argument("--conv-warmup", type=int, default=50)
     p.add_argument("--conv-packed-log2-samples", type=int, default=20)
     return p.parse_args()
 
