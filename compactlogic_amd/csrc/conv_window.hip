@@ -91,7 +91,9 @@ __global__ __launch_bounds__(256) void k_win_prep(const T* __restrict__ w, int s
 }
 
 // Window values of the thread's output position; zero outside the plane or past the end.
-template <typename T, int KW>
+// INTERIOR: every window of every active position lies inside the plane (checked on the host),
+// so only `active` is tested.
+template <typename T, int KW, bool INTERIOR = false>
 __device__ __forceinline__ void load_window(T (&v)[KW * KW], const T* __restrict__ plane, int H,
                                             int W, int by, int bx, bool active) {
 #pragma unroll
@@ -99,7 +101,8 @@ __device__ __forceinline__ void load_window(T (&v)[KW * KW], const T* __restrict
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw) {
             const int yy = by + kh, xx = bx + kw;
-            const bool ok = active && unsigned(yy) < unsigned(H) && unsigned(xx) < unsigned(W);
+            const bool ok = active && (INTERIOR || (unsigned(yy) < unsigned(H) &&
+                                                    unsigned(xx) < unsigned(W)));
             v[kh * KW + kw] = ok ? plane[yy * W + xx] : T(0);
         }
     }
@@ -210,7 +213,7 @@ __device__ __forceinline__ int win_plane_at(int i, int W, const WinPlane& lp) {
            __mul24(xx - __mul24(qx, lp.ps), lp.ws) + qx;
 }
 
-template <typename T, int KW>
+template <typename T, int KW, bool INTERIOR>
 __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
                                                     const T* __restrict__ gy,
                                                     const T* __restrict__ coef,
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
         int(uint32_t(oy) * uint32_t(lp.la) + uint32_t(pos) * uint32_t(lp.lb) + uint32_t(lp.lc));
     const T* xplane = x + int64_t(blockIdx.x) * HW;
     T v[P];
-    load_window<T, KW>(v, xplane, d.H, d.W, by, bx, active);
+    load_window<T, KW, INTERIOR>(v, xplane, d.H, d.W, by, bx, active);
     // A_k = sum_c gy_c alpha_kc, B_kl = sum_c gy_c beta_klc over the channels reading ch
     T A[P], B[NP];
 #pragma unroll
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
             dk = fma(l == k ? T(2) * B[q] : B[q], v[l], dk);
         }
         const int yy = by + k / KW, xx = bx + k % KW;
-        if (active && unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W))
+        if (active && (INTERIOR || (unsigned(yy) < unsigned(d.H) && unsigned(xx) < unsigned(d.W))))
             plane[lane_base + lp.tap[k]] += dk;
         __syncthreads();
     }
@@ -1046,13 +1049,18 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
     lp.st_step = bs % (W * ps) == 0 ? int(bs / (W * ps) * pitch) : 0;
     const int64_t blocks = N * Cin;
     CL_ARG(blocks < (int64_t(1) << 31), "conv layer too large for one launch");
+    // every window of every output position inside the plane: no bounds tests
+    const bool interior = oy0 >= 0 && ox0 >= 0 && (h_out - 1) * stride + oy0 + kw <= H &&
+                          (w_out - 1) * stride + ox0 + kw <= W;
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
-            k_win_bwd_x<scalar_t, decltype(K)::value>
-                <<<unsigned(blocks), bs, lds, as_stream(stream)>>>(
-                    static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(grad_y),
-                    static_cast<const scalar_t*>(coef), grp_ptr, chan_order,
-                    static_cast<scalar_t*>(grad_x), d, lp);
+            constexpr int KWV = decltype(K)::value;
+            auto kern = interior ? k_win_bwd_x<scalar_t, KWV, true>
+                                 : k_win_bwd_x<scalar_t, KWV, false>;
+            kern<<<unsigned(blocks), bs, lds, as_stream(stream)>>>(
+                static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(grad_y),
+                static_cast<const scalar_t*>(coef), grp_ptr, chan_order,
+                static_cast<scalar_t*>(grad_x), d, lp);
             return CL_OK;
         });
         if (rc) return rc;
