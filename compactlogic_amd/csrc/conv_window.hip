@@ -121,7 +121,7 @@ struct WinDims {
 // PACK (small planes): a block of 256 threads takes spb = 256 / hw samples of input channel ch
 // instead (blockIdx.x = ((n / spb) * Cin + ch) * split + part; thread t: sample t / hw, position
 // t % hw), so that few lanes idle; pchunks is then spb.
-template <typename T, int KW, int SPLIT, bool PACK>
+template <typename T, int KW, int SPLIT, bool PACK, bool INTERIOR>
 __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const T* __restrict__ coef,
                                                  const int32_t* __restrict__ grp_ptr,
                                                  const int32_t* __restrict__ chan_order,
@@ -151,8 +151,8 @@ __global__ __launch_bounds__(256) void k_win_fwd(const T* __restrict__ x, const 
     if (c0 == c1 || pos >= hw) return;
     const int oy = pos / d.Wo, ox = pos - oy * d.Wo;
     T v[P];
-    load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(d.H) * d.W, d.H, d.W,
-                       oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
+    load_window<T, KW, INTERIOR>(v, x + (n * d.Cin + ch) * int64_t(d.H) * d.W, d.H, d.W,
+                                 oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
     T* yn = y + n * d.Cout * hw + pos;
 #pragma unroll 2
     for (int i = c0; i < c1; ++i) {
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(1024) void k_win_bwd_x(const T* __restrict__ x,
 // threads stride over the chunk's (sample, position) elements.  part[q, c, j] for j < CW.
 // The closing reduction adds quads with DPP, then the 16 quad sums of each of the 4 waves in
 // a fixed order through LDS.
-template <typename T, int KW, int CB>
+template <typename T, int KW, int CB, bool INTERIOR>
 __global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
                                                      const T* __restrict__ gy,
                                                      const int32_t* __restrict__ grp_ptr,
@@ -323,8 +323,8 @@ __global__ __launch_bounds__(256) void k_win_moments(const T* __restrict__ x,
     for (int64_t e = threadIdx.x; e < cnt; e += BS) {
         const int pos = oy * d.Wo + ox;
         T v[P];
-        load_window<T, KW>(v, x + (n * d.Cin + ch) * int64_t(HW), d.H, d.W,
-                           oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
+        load_window<T, KW, INTERIOR>(v, x + (n * d.Cin + ch) * int64_t(HW), d.H, d.W,
+                                     oy * d.stride + d.oy0, ox * d.stride + d.ox0, true);
         const T* gyn = gy + int64_t(n) * d.Cout * hw + pos;
         n += dn;
         oy += dy;
@@ -893,6 +893,13 @@ int with_kw(int64_t kw, F&& f) {
     }
 }
 
+// Every kw x kw window of every output position lies inside the H x W plane.
+bool win_interior(int64_t H, int64_t W, int64_t stride, int64_t h_out, int64_t w_out,
+                  int64_t oy0, int64_t ox0, int64_t kw) {
+    return oy0 >= 0 && ox0 >= 0 && (h_out - 1) * stride + oy0 + kw <= H &&
+           (w_out - 1) * stride + ox0 + kw <= W;
+}
+
 int block_for(int64_t hw, int cap) {
     int64_t b = ceil_div(hw, 64) * 64;
     return int(std::min<int64_t>(b, cap));
@@ -959,11 +966,15 @@ extern "C" int cl_conv_window_forward(int dtype, const void* x, const void* coef
     const int split = Cout >= 8 * Cin ? 2 : 1;
     const int64_t blocks = (pack ? ceil_div(N, pchunks) : N * pchunks) * Cin * split;
     CL_ARG(blocks < (int64_t(1) << 32), "conv layer too large for one launch");
+    const bool interior = win_interior(H, W, stride, h_out, w_out, oy0, ox0, kw);
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
             auto go = [&](auto sc, auto pc) {
-                k_win_fwd<scalar_t, decltype(K)::value, decltype(sc)::value, decltype(pc)::value>
-                    <<<unsigned(blocks), pack ? 256 : bs, 0, as_stream(stream)>>>(
+                constexpr int KWV = decltype(K)::value, SCV = decltype(sc)::value;
+                constexpr bool PCV = decltype(pc)::value;
+                auto kern = interior ? k_win_fwd<scalar_t, KWV, SCV, PCV, true>
+                                     : k_win_fwd<scalar_t, KWV, SCV, PCV, false>;
+                kern<<<unsigned(blocks), pack ? 256 : bs, 0, as_stream(stream)>>>(
                     static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(coef), grp_ptr,
                     chan_order, static_cast<scalar_t*>(y), int(pchunks), d);
             };
@@ -1050,8 +1061,7 @@ extern "C" int cl_conv_window_backward_x(int dtype, const void* x, const void* g
     const int64_t blocks = N * Cin;
     CL_ARG(blocks < (int64_t(1) << 31), "conv layer too large for one launch");
     // every window of every output position inside the plane: no bounds tests
-    const bool interior = oy0 >= 0 && ox0 >= 0 && (h_out - 1) * stride + oy0 + kw <= H &&
-                          (w_out - 1) * stride + ox0 + kw <= W;
+    const bool interior = win_interior(H, W, stride, h_out, w_out, oy0, ox0, kw);
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
             constexpr int KWV = decltype(K)::value;
@@ -1173,9 +1183,13 @@ extern "C" int cl_conv_window_moments(int dtype, const void* x, const void* grad
     CL_ARG(bx < (int64_t(1) << 31), "conv layer too large for one launch");
     const int bs = 256;
     const dim3 grid(unsigned(bx), unsigned(nq), 1);
+    const bool interior = win_interior(H, W, stride, h_out, w_out, oy0, ox0, kw);
     CL_DTYPE_SWITCH(dtype, {
         int rc = with_kw(kw, [&](auto K) {
-            k_win_moments<scalar_t, decltype(K)::value, kWinCB><<<grid, bs, 0, as_stream(stream)>>>(
+            constexpr int KWV = decltype(K)::value;
+            auto kern = interior ? k_win_moments<scalar_t, KWV, kWinCB, true>
+                                 : k_win_moments<scalar_t, KWV, kWinCB, false>;
+            kern<<<grid, bs, 0, as_stream(stream)>>>(
                 static_cast<const scalar_t*>(x), static_cast<const scalar_t*>(grad_y), grp_ptr,
                 chan_order, static_cast<scalar_t*>(moments), int(nsub), int(nq), d);
             return CL_OK;
